@@ -1,0 +1,155 @@
+/*
+ * C ABI of the MI355X (gfx950) Qwen3 decode library, libqwen_megakernel_amd.so.
+ *
+ * Plain pointers, sizes and a HIP stream; no torch types.  The first three
+ * entry points are the reference's launchers with the same names, argument
+ * order and meaning, with hipStream_t in place of cudaStream_t:
+ *
+ *   launch_ldg_decode_direct      <- reference csrc/kernel.cu:1477-1505
+ *                                    (declared csrc/torch_bindings.cpp:45-53)
+ *   launch_ldg_decode_persistent  <- reference csrc/kernel.cu:1507-1543
+ *                                    (declared csrc/torch_bindings.cpp:35-43)
+ *   launch_ldg_generate_nosync    <- reference csrc/kernel.cu:1547-1605
+ *                                    (declared csrc/torch_bindings.cpp:83-91)
+ *
+ * All tensors are device pointers.  Layout (as in the reference):
+ *   embed_weight / lm_head_weight  bf16 [vocab][hidden] (tied in Qwen3-0.6B)
+ *   layer_weights                  device array of num_layers LDGLayerWeights
+ *   cos_table / sin_table          bf16 [max_seq_len][head_dim]
+ *   k_cache / v_cache              bf16 [num_layers][num_kv_heads][max_seq_len][head_dim]
+ *   hidden_buffer                  bf16 [hidden]   receives the final hidden state
+ *   g_normalized                   f32  [hidden]   receives the final-norm output
+ * The other scratch pointers of the reference signature (g_activations,
+ * g_residual, g_q, g_k, g_v, g_attn_out, g_mlp_intermediate, block_max_vals,
+ * block_max_idxs) are accepted and not used: activations move between
+ * workgroups through the library's own per-stream exchange buffers.
+ *
+ * Errors: the reference reports none.  Here every entry point validates its
+ * arguments before launching (nothing is launched on error), and records a
+ * status readable with qmk_last_status() on the calling thread.  Errors
+ * found on the device (bounded waits that expired, a position outside the
+ * cache in persistent mode) are latched per stream: later launches on that
+ * stream do nothing until qmk_reset(); qmk_device_error() reports them.
+ */
+#ifndef QWEN_MEGAKERNEL_AMD_H
+#define QWEN_MEGAKERNEL_AMD_H
+
+#include <hip/hip_runtime_api.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Per-layer weight table, same field order as the reference's
+ * LDGLayerWeights (csrc/torch_bindings.cpp:21-33, csrc/kernel.cu:76-88). */
+typedef struct LDGLayerWeights {
+  const void *input_layernorm_weight;
+  const void *q_proj_weight;
+  const void *k_proj_weight;
+  const void *v_proj_weight;
+  const void *q_norm_weight;
+  const void *k_norm_weight;
+  const void *o_proj_weight;
+  const void *post_attn_layernorm_weight;
+  const void *gate_proj_weight;
+  const void *up_proj_weight;
+  const void *down_proj_weight;
+} LDGLayerWeights;
+
+/* Status codes (qmk_last_status). */
+enum {
+  QMK_OK = 0,
+  QMK_ERR_ARG = 1,        /* invalid argument (null pointer, range) */
+  QMK_ERR_POSITION = 2,   /* position outside [0, max_seq_len) */
+  QMK_ERR_DEVICE = 3,     /* device unsuitable (needs 256 CUs, gfx950) */
+  QMK_ERR_HIP = 4,        /* a HIP runtime call failed */
+  QMK_ERR_POISONED = 5,   /* a previous launch on this stream failed; call qmk_reset */
+};
+
+/* Device error bits (qmk_device_error). */
+enum {
+  QMK_DEV_TIMEOUT = 1,    /* a bounded wait expired */
+  QMK_DEV_POSITION = 2,   /* persistent-mode position outside the cache */
+  QMK_DEV_TOKEN = 4,      /* token id outside the vocabulary */
+};
+
+/* One decode step at `position` for `input_token_id`; writes the greedy next
+ * token to output_token_id (device int).  Asynchronous on `stream`.
+ * Replaces reference csrc/kernel.cu:1477-1505. */
+void launch_ldg_decode_direct(
+    int input_token_id, int *output_token_id, const void *embed_weight,
+    const LDGLayerWeights *layer_weights, const void *final_norm_weight,
+    const void *lm_head_weight, const void *cos_table, const void *sin_table,
+    void *k_cache, void *v_cache, void *hidden_buffer, void *g_activations,
+    void *g_residual, void *g_q, void *g_k, void *g_v, void *g_attn_out,
+    void *g_mlp_intermediate, void *g_normalized, void *block_max_vals,
+    void *block_max_idxs, int num_layers, int position, int max_seq_len,
+    float attn_scale, hipStream_t stream);
+
+/* Same step, but the kernel reads position/token from the stream's device
+ * state (set here), the form that a captured graph can replay.  `cache_len`
+ * must equal position + 1, as in the reference's only caller convention.
+ * Replaces reference csrc/kernel.cu:1507-1543. */
+void launch_ldg_decode_persistent(
+    int input_token_id, int *output_token_id, const void *embed_weight,
+    const LDGLayerWeights *layer_weights, const void *final_norm_weight,
+    const void *lm_head_weight, const void *cos_table, const void *sin_table,
+    void *k_cache, void *v_cache, void *hidden_buffer, void *g_activations,
+    void *g_residual, void *g_q, void *g_k, void *g_v, void *g_attn_out,
+    void *g_mlp_intermediate, void *g_normalized, void *block_max_vals,
+    void *block_max_idxs, int num_layers, int position, int cache_len,
+    int max_seq_len, float attn_scale, hipStream_t stream);
+
+/* num_steps greedy steps starting at start_position with first_token_id,
+ * with no host synchronisation between steps: each launch feeds its argmax
+ * to the next through device state.  output_log (device int[num_steps])
+ * receives the generated tokens.  Asynchronous; the caller synchronises.
+ * Replaces reference csrc/kernel.cu:1547-1605. */
+void launch_ldg_generate_nosync(
+    int first_token_id, int num_steps, const void *embed_weight,
+    const LDGLayerWeights *layer_weights, const void *final_norm_weight,
+    const void *lm_head_weight, const void *cos_table, const void *sin_table,
+    void *k_cache, void *v_cache, void *hidden_buffer, void *g_activations,
+    void *g_residual, void *g_q, void *g_k, void *g_v, void *g_attn_out,
+    void *g_mlp_intermediate, void *g_normalized, void *block_max_vals,
+    void *block_max_idxs, int *output_log, int num_layers, int start_position,
+    int max_seq_len, float attn_scale, hipStream_t stream);
+
+/* ---- additions with no counterpart in the reference ---- */
+
+/* Decode step that also writes the fp32 copy of the bf16 logits
+ * (float[vocab]) when logits_out is not NULL; used by parity tests.
+ * Returns a status code. */
+int qmk_decode_logits(
+    int input_token_id, int *output_token_id, float *logits_out,
+    const void *embed_weight, const LDGLayerWeights *layer_weights,
+    const void *final_norm_weight, const void *lm_head_weight,
+    const void *cos_table, const void *sin_table, void *k_cache, void *v_cache,
+    void *hidden_buffer, void *g_normalized, int num_layers, int position,
+    int max_seq_len, float attn_scale, hipStream_t stream);
+
+/* Status of the last call made on this thread. */
+int qmk_last_status(void);
+const char *qmk_status_string(int status);
+
+/* Synchronises `stream` and returns its latched device error bits (0 = ok). */
+uint32_t qmk_device_error(hipStream_t stream);
+
+/* Clears the stream's device state (error bits, exchange buffers).
+ * Synchronous.  Returns a status code. */
+int qmk_reset(hipStream_t stream);
+
+/* Sets the bound of every device-side wait for launches on `stream`, in
+ * wall-clock ticks (0 restores the default of one second).  Tests use a tiny
+ * bound to drive the failure path without any risk of a hang. */
+int qmk_set_wait_limit(hipStream_t stream, uint32_t ticks);
+
+/* Kernel launch geometry, for tools: workgroups and threads per workgroup. */
+void qmk_launch_geometry(int *workgroups, int *threads);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QWEN_MEGAKERNEL_AMD_H */

@@ -1,0 +1,349 @@
+// Host side of libqwen_megakernel_amd.so: the C ABI declared in
+// include/qwen_megakernel.h.
+//
+// The reference keeps barrier counters, flags and pinned ints in file-static
+// singletons allocated on first use with unchecked cudaMalloc
+// (csrc/kernel.cu:1446-1473), so two decoders on two streams corrupt each
+// other.  Here each (device, stream) pair owns a DecodeState plus exchange
+// buffers, created on first use and checked; launches on one stream are
+// ordered by the stream, launches on different streams use different state.
+
+#include <hip/hip_runtime.h>
+
+#include <map>
+#include <mutex>
+#include <utility>
+
+#include "../../include/qwen_megakernel.h"
+#include "qmk_decode_kernel.h"
+
+namespace qmk {
+namespace {
+
+using Model = Qwen3_0_6B;
+using Dm = Dims<Model>;
+
+thread_local int t_status = QMK_OK;
+
+struct Ctx {
+  int device = -1;
+  DecodeState* st = nullptr;
+  uint32_t* x = nullptr;
+  uint32_t* host_err = nullptr;
+  int xcd_local = 0;
+  uint32_t timeout = kTimeoutDefault;
+};
+
+struct DevInfo {
+  bool checked = false;
+  bool ok = false;
+  int xcd_local = 0;
+  uint32_t ticks_per_s = 100000000u;
+};
+
+std::mutex g_mu;
+std::map<std::pair<int, hipStream_t>, Ctx*> g_ctx;
+std::map<int, DevInfo> g_dev;
+
+__global__ void xcd_probe_kernel(int* ok) {
+  if (threadIdx.x == 0) {
+    unsigned v;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
+    ok[blockIdx.x] = ((v & 0xfu) == (blockIdx.x & 7u)) ? 1 : 0;
+  }
+}
+
+__global__ void set_step_kernel(DecodeState* st, int pos, int tok) {
+  st->pos = pos;
+  st->tok = tok;
+  st->step = 0;
+}
+
+int fail(int s) {
+  t_status = s;
+  return s;
+}
+
+// Checks the current device once: gfx950-class with >= 256 CUs, the decode
+// kernel fits one workgroup per CU, and whether workgroup b runs on XCD b%8.
+int check_device(int dev, DevInfo** out) {
+  DevInfo& di = g_dev[dev];
+  *out = &di;
+  if (di.checked) return di.ok ? QMK_OK : QMK_ERR_DEVICE;
+  di.checked = true;
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, dev) != hipSuccess) return QMK_ERR_HIP;
+  int occ = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, reinterpret_cast<const void*>(decode_kernel<Model>), kBlock, 0) !=
+      hipSuccess)
+    return QMK_ERR_HIP;
+  if (prop.multiProcessorCount < kNumWG || occ < 1) return QMK_ERR_DEVICE;
+  int khz = 0;
+  if (hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev) == hipSuccess && khz > 0)
+    di.ticks_per_s = (uint32_t)khz * 1000u;
+  int* d_ok = nullptr;
+  if (hipMalloc(&d_ok, kNumWG * sizeof(int)) != hipSuccess) return QMK_ERR_HIP;
+  hipLaunchKernelGGL(xcd_probe_kernel, dim3(kNumWG), dim3(64), 0, 0, d_ok);
+  int h_ok[kNumWG];
+  bool good = hipGetLastError() == hipSuccess &&
+              hipMemcpy(h_ok, d_ok, sizeof(h_ok), hipMemcpyDeviceToHost) == hipSuccess;
+  hipFree(d_ok);
+  if (!good) return QMK_ERR_HIP;
+  int all = 1;
+  for (int i = 0; i < kNumWG; i++) all &= h_ok[i];
+  di.xcd_local = all;
+  di.ok = true;
+  return QMK_OK;
+}
+
+int get_ctx(hipStream_t stream, Ctx** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess) return QMK_ERR_HIP;
+  std::lock_guard<std::mutex> lk(g_mu);
+  auto key = std::make_pair(dev, stream);
+  auto it = g_ctx.find(key);
+  if (it != g_ctx.end()) {
+    *out = it->second;
+    return QMK_OK;
+  }
+  DevInfo* di = nullptr;
+  int s = check_device(dev, &di);
+  if (s != QMK_OK) return s;
+  Ctx* c = new Ctx();
+  c->device = dev;
+  c->xcd_local = di->xcd_local;
+  c->timeout = di->ticks_per_s;  // 1 second
+  const size_t bytes = sizeof(DecodeState) + (size_t)Dm::X_WORDS * 4;
+  void* mem = nullptr;
+  if (hipMalloc(&mem, bytes) != hipSuccess) {
+    delete c;
+    return QMK_ERR_HIP;
+  }
+  if (hipMemset(mem, 0, bytes) != hipSuccess || hipHostMalloc(&c->host_err, sizeof(uint32_t), hipHostMallocDefault) != hipSuccess) {
+    hipFree(mem);
+    delete c;
+    return QMK_ERR_HIP;
+  }
+  *c->host_err = 0;
+  c->st = reinterpret_cast<DecodeState*>(mem);
+  c->x = reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(mem) + sizeof(DecodeState));
+  g_ctx[key] = c;
+  *out = c;
+  return QMK_OK;
+}
+
+struct Common {
+  const void* embed;
+  const LDGLayerWeights* layers;
+  const void* final_norm;
+  const void* lm_head;
+  const void* cos_t;
+  const void* sin_t;
+  void* k_cache;
+  void* v_cache;
+  void* hidden_out;
+  void* normalized_out;
+  int num_layers;
+  int max_seq_len;
+  float attn_scale;
+};
+
+int validate(const Common& c) {
+  if (!c.embed || !c.layers || !c.final_norm || !c.lm_head || !c.cos_t || !c.sin_t || !c.k_cache || !c.v_cache)
+    return QMK_ERR_ARG;
+  if (c.num_layers < 1 || c.num_layers > 28 || c.max_seq_len < 1) return QMK_ERR_ARG;
+  if (!(c.attn_scale > 0.f)) return QMK_ERR_ARG;
+  return QMK_OK;
+}
+
+KArgs make_args(const Common& c, Ctx* ctx) {
+  KArgs a{};
+  a.embed = static_cast<const uint16_t*>(c.embed);
+  a.layers = reinterpret_cast<const LayerPtrs*>(c.layers);
+  a.final_norm = static_cast<const uint16_t*>(c.final_norm);
+  a.lm_head = static_cast<const uint16_t*>(c.lm_head);
+  a.cos_t = static_cast<const uint16_t*>(c.cos_t);
+  a.sin_t = static_cast<const uint16_t*>(c.sin_t);
+  a.k_cache = static_cast<uint16_t*>(c.k_cache);
+  a.v_cache = static_cast<uint16_t*>(c.v_cache);
+  a.hidden_out = static_cast<uint16_t*>(c.hidden_out);
+  a.normalized_out = static_cast<float*>(c.normalized_out);
+  a.st = ctx->st;
+  a.x = ctx->x;
+  a.host_err = ctx->host_err;
+  a.num_layers = c.num_layers;
+  a.max_seq_len = c.max_seq_len;
+  a.attn_scale = c.attn_scale;
+  a.rms_eps = 1e-6f;
+  a.timeout = ctx->timeout;
+  a.xcd_local = ctx->xcd_local;
+  return a;
+}
+
+int launch(const KArgs& a, hipStream_t stream) {
+  hipLaunchKernelGGL(decode_kernel<Model>, dim3(kNumWG), dim3(kBlock), 0, stream, a);
+  return hipGetLastError() == hipSuccess ? QMK_OK : QMK_ERR_HIP;
+}
+
+int poisoned(Ctx* ctx) { return (*ctx->host_err != 0) ? QMK_ERR_POISONED : QMK_OK; }
+
+int decode_impl(const Common& c, int token, int position, int* out_token, float* logits, hipStream_t stream,
+                bool persistent) {
+  int s = validate(c);
+  if (s != QMK_OK) return fail(s);
+  if (position < 0 || position >= c.max_seq_len) return fail(QMK_ERR_POSITION);
+  if (token < 0 || token >= Dm::V) return fail(QMK_ERR_ARG);
+  Ctx* ctx = nullptr;
+  if ((s = get_ctx(stream, &ctx)) != QMK_OK) return fail(s);
+  if ((s = poisoned(ctx)) != QMK_OK) return fail(s);
+  KArgs a = make_args(c, ctx);
+  a.out_token = out_token;
+  a.logits = logits;
+  if (persistent) {
+    hipLaunchKernelGGL(set_step_kernel, dim3(1), dim3(1), 0, stream, ctx->st, position, token);
+    a.position = -1;
+  } else {
+    a.position = position;
+    a.token = token;
+  }
+  return fail(launch(a, stream));
+}
+
+}  // namespace
+}  // namespace qmk
+
+using namespace qmk;
+
+extern "C" {
+
+void launch_ldg_decode_direct(int input_token_id, int* output_token_id, const void* embed_weight,
+                              const LDGLayerWeights* layer_weights, const void* final_norm_weight,
+                              const void* lm_head_weight, const void* cos_table, const void* sin_table, void* k_cache,
+                              void* v_cache, void* hidden_buffer, void* g_activations, void* g_residual, void* g_q,
+                              void* g_k, void* g_v, void* g_attn_out, void* g_mlp_intermediate, void* g_normalized,
+                              void* block_max_vals, void* block_max_idxs, int num_layers, int position,
+                              int max_seq_len, float attn_scale, hipStream_t stream) {
+  (void)g_activations; (void)g_residual; (void)g_q; (void)g_k; (void)g_v; (void)g_attn_out;
+  (void)g_mlp_intermediate; (void)block_max_vals; (void)block_max_idxs;
+  Common c{embed_weight, layer_weights, final_norm_weight, lm_head_weight, cos_table, sin_table, k_cache, v_cache,
+           hidden_buffer, g_normalized, num_layers, max_seq_len, attn_scale};
+  decode_impl(c, input_token_id, position, output_token_id, nullptr, stream, false);
+}
+
+void launch_ldg_decode_persistent(int input_token_id, int* output_token_id, const void* embed_weight,
+                                  const LDGLayerWeights* layer_weights, const void* final_norm_weight,
+                                  const void* lm_head_weight, const void* cos_table, const void* sin_table,
+                                  void* k_cache, void* v_cache, void* hidden_buffer, void* g_activations,
+                                  void* g_residual, void* g_q, void* g_k, void* g_v, void* g_attn_out,
+                                  void* g_mlp_intermediate, void* g_normalized, void* block_max_vals,
+                                  void* block_max_idxs, int num_layers, int position, int cache_len,
+                                  int max_seq_len, float attn_scale, hipStream_t stream) {
+  (void)g_activations; (void)g_residual; (void)g_q; (void)g_k; (void)g_v; (void)g_attn_out;
+  (void)g_mlp_intermediate; (void)block_max_vals; (void)block_max_idxs;
+  if (cache_len != position + 1) {
+    fail(QMK_ERR_ARG);
+    return;
+  }
+  Common c{embed_weight, layer_weights, final_norm_weight, lm_head_weight, cos_table, sin_table, k_cache, v_cache,
+           hidden_buffer, g_normalized, num_layers, max_seq_len, attn_scale};
+  decode_impl(c, input_token_id, position, output_token_id, nullptr, stream, true);
+}
+
+void launch_ldg_generate_nosync(int first_token_id, int num_steps, const void* embed_weight,
+                                const LDGLayerWeights* layer_weights, const void* final_norm_weight,
+                                const void* lm_head_weight, const void* cos_table, const void* sin_table,
+                                void* k_cache, void* v_cache, void* hidden_buffer, void* g_activations,
+                                void* g_residual, void* g_q, void* g_k, void* g_v, void* g_attn_out,
+                                void* g_mlp_intermediate, void* g_normalized, void* block_max_vals,
+                                void* block_max_idxs, int* output_log, int num_layers, int start_position,
+                                int max_seq_len, float attn_scale, hipStream_t stream) {
+  (void)g_activations; (void)g_residual; (void)g_q; (void)g_k; (void)g_v; (void)g_attn_out;
+  (void)g_mlp_intermediate; (void)block_max_vals; (void)block_max_idxs;
+  Common c{embed_weight, layer_weights, final_norm_weight, lm_head_weight, cos_table, sin_table, k_cache, v_cache,
+           hidden_buffer, g_normalized, num_layers, max_seq_len, attn_scale};
+  int s = validate(c);
+  if (s != QMK_OK) { fail(s); return; }
+  if (num_steps < 0 || !output_log) { fail(QMK_ERR_ARG); return; }
+  if (num_steps == 0) { fail(QMK_OK); return; }
+  // every step must stay inside the cache: the last one runs at start+num_steps-1
+  if (start_position < 0 || (long long)start_position + num_steps > (long long)max_seq_len) {
+    fail(QMK_ERR_POSITION);
+    return;
+  }
+  if (first_token_id < 0 || first_token_id >= Dm::V) { fail(QMK_ERR_ARG); return; }
+  Ctx* ctx = nullptr;
+  if ((s = get_ctx(stream, &ctx)) != QMK_OK) { fail(s); return; }
+  if ((s = poisoned(ctx)) != QMK_OK) { fail(s); return; }
+  KArgs a = make_args(c, ctx);
+  a.position = -1;
+  a.out_log = output_log;
+  hipLaunchKernelGGL(set_step_kernel, dim3(1), dim3(1), 0, stream, ctx->st, start_position, first_token_id);
+  for (int i = 0; i < num_steps; i++) {
+    if ((s = launch(a, stream)) != QMK_OK) { fail(s); return; }
+  }
+  fail(QMK_OK);
+}
+
+int qmk_decode_logits(int input_token_id, int* output_token_id, float* logits_out, const void* embed_weight,
+                      const LDGLayerWeights* layer_weights, const void* final_norm_weight, const void* lm_head_weight,
+                      const void* cos_table, const void* sin_table, void* k_cache, void* v_cache, void* hidden_buffer,
+                      void* g_normalized, int num_layers, int position, int max_seq_len, float attn_scale,
+                      hipStream_t stream) {
+  Common c{embed_weight, layer_weights, final_norm_weight, lm_head_weight, cos_table, sin_table, k_cache, v_cache,
+           hidden_buffer, g_normalized, num_layers, max_seq_len, attn_scale};
+  return decode_impl(c, input_token_id, position, output_token_id, logits_out, stream, false);
+}
+
+int qmk_last_status(void) { return t_status; }
+
+const char* qmk_status_string(int status) {
+  switch (status) {
+    case QMK_OK: return "ok";
+    case QMK_ERR_ARG: return "invalid argument";
+    case QMK_ERR_POSITION: return "position outside [0, max_seq_len)";
+    case QMK_ERR_DEVICE: return "device unsuitable: needs a gfx950 GPU with 256 CUs";
+    case QMK_ERR_HIP: return "HIP runtime call failed";
+    case QMK_ERR_POISONED: return "an earlier launch on this stream failed on the device; call qmk_reset";
+    default: return "unknown status";
+  }
+}
+
+uint32_t qmk_device_error(hipStream_t stream) {
+  Ctx* ctx = nullptr;
+  if (get_ctx(stream, &ctx) != QMK_OK) return 0xffffffffu;
+  if (hipStreamSynchronize(stream) != hipSuccess) return 0xffffffffu;
+  uint32_t v = 0;
+  if (hipMemcpy(&v, &ctx->st->err, sizeof(v), hipMemcpyDeviceToHost) != hipSuccess) return 0xffffffffu;
+  return v | *ctx->host_err;
+}
+
+int qmk_reset(hipStream_t stream) {
+  Ctx* ctx = nullptr;
+  int s = get_ctx(stream, &ctx);
+  if (s != QMK_OK) return fail(s);
+  if (hipStreamSynchronize(stream) != hipSuccess) return fail(QMK_ERR_HIP);
+  const size_t bytes = sizeof(DecodeState) + (size_t)Dm::X_WORDS * 4;
+  if (hipMemset(ctx->st, 0, bytes) != hipSuccess) return fail(QMK_ERR_HIP);
+  *ctx->host_err = 0;
+  return fail(QMK_OK);
+}
+
+int qmk_set_wait_limit(hipStream_t stream, uint32_t ticks) {
+  Ctx* ctx = nullptr;
+  int s = get_ctx(stream, &ctx);
+  if (s != QMK_OK) return fail(s);
+  if (ticks == 0) {
+    DevInfo* di = nullptr;
+    check_device(ctx->device, &di);
+    ticks = di->ticks_per_s;
+  }
+  ctx->timeout = ticks;
+  return fail(QMK_OK);
+}
+
+void qmk_launch_geometry(int* workgroups, int* threads) {
+  if (workgroups) *workgroups = kNumWG;
+  if (threads) *threads = kBlock;
+}
+
+}  // extern "C"

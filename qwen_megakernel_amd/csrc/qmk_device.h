@@ -1,0 +1,154 @@
+// Device-side building blocks of the gfx950 decode kernel: bf16 rounding,
+// wave64 reductions, weight streaming, and the tagged-word exchange that
+// replaces grid barriers.
+//
+// Exchange protocol.  Every value that crosses workgroups travels as a 32-bit
+// word (payload16 << 16 | tag16).  The tag is derived from a per-launch epoch
+// and the exchange's index within the launch, and is never 0, so zeroed memory
+// and data left over from any earlier exchange are never mistaken for the
+// current one.  A consumer polls the words themselves and re-reads only the
+// 16-byte chunks whose tags are stale; one exchange therefore costs one
+// store-to-load latency instead of a barrier round trip, and only 4-byte
+// single-copy atomicity is relied upon.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace qmk {
+
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kWave = 64;
+constexpr int kNumWG = 256;       // one workgroup per CU of an MI355X
+constexpr int kComputeWaves = 8;  // waves 1..8 stream weights; wave 0 moves activations
+constexpr int kBlock = (kComputeWaves + 1) * kWave;
+constexpr int kGroups = 8;        // workgroup b runs on XCD b % 8
+constexpr int kGroupSize = kNumWG / kGroups;
+
+// ---------------------------------------------------------------- bf16
+
+__device__ __forceinline__ float bf16_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
+
+// fp32 -> bf16 bits, round to nearest even; NaN -> 0x7FC0 (as c10::BFloat16).
+__device__ __forceinline__ uint32_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+// Value of ``f`` rounded to bf16, as fp32.
+__device__ __forceinline__ float bf16r(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+
+__device__ __forceinline__ float lo_bf16(uint32_t packed) { return __uint_as_float(packed << 16); }
+__device__ __forceinline__ float hi_bf16(uint32_t packed) { return __uint_as_float(packed & 0xffff0000u); }
+
+__device__ __forceinline__ bf16x2 as_bf2(uint32_t u) { return __builtin_bit_cast(bf16x2, u); }
+
+// acc + dot(w[0..7], x[0..7]) for eight bf16 pairs held as two 16-byte chunks.
+__device__ __forceinline__ float dot8(u32x4 w, u32x4 x, float acc) {
+  uint32_t w0 = w.x, w1 = w.y, w2 = w.z, w3 = w.w;
+  uint32_t x0 = x.x, x1 = x.y, x2 = x.z, x3 = x.w;
+  acc = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(w0), as_bf2(x0), acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(w1), as_bf2(x1), acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(w2), as_bf2(x2), acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(w3), as_bf2(x3), acc, false);
+  return acc;
+}
+
+// ------------------------------------------------------------ reductions
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_add(float v) {
+  int s = __builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false);
+  return v + __int_as_float(s);
+}
+
+// Sum over each row of 16 lanes; every lane of the row receives the row sum.
+__device__ __forceinline__ float row16_sum(float v) {
+  v = dpp_add<0xB1>(v);   // quad_perm [1,0,3,2]
+  v = dpp_add<0x4E>(v);   // quad_perm [2,3,0,1]
+  v = dpp_add<0x141>(v);  // row_half_mirror
+  v = dpp_add<0x140>(v);  // row_mirror
+  return v;
+}
+
+// Sum over the wave; uniform result.
+__device__ __forceinline__ float wave_sum(float v) {
+  v = row16_sum(v);
+  float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return (a + b) + (c + d);
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  return v;
+}
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+  for (int o = 32; o >= 1; o >>= 1) {
+    uint64_t w = __shfl_xor(v, o);
+    v = w > v ? w : v;
+  }
+  return v;
+}
+
+// ------------------------------------------------------------ memory
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, bytes, 0x00020000);
+}
+
+// Streaming 16-byte weight load (non-temporal: weights are read once per token).
+__device__ __forceinline__ u32x4 ld_stream(const void* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+
+__device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+
+// ------------------------------------------------------- tagged exchange
+
+constexpr uint32_t kTimeoutDefault = 100u * 1000u * 1000u;  // 1 s of the 100 MHz wall clock
+
+// Error bits written to the state word (and mirrored to the host word).
+enum : uint32_t {
+  kErrTimeout = 1u,
+  kErrPosition = 2u,
+  kErrToken = 4u,
+  kErrPoisoned = 8u,
+};
+
+__device__ __forceinline__ uint32_t make_tag(uint32_t epoch, uint32_t k) { return ((epoch + k) % 65535u) + 1u; }
+
+__device__ __forceinline__ uint32_t word(uint32_t payload16, uint32_t tag) { return (payload16 << 16) | tag; }
+
+__device__ __forceinline__ bool chunk_ok(u32x4 v, uint32_t tag) {
+  return ((v.x & 0xffffu) == tag) & ((v.y & 0xffffu) == tag) & ((v.z & 0xffffu) == tag) & ((v.w & 0xffffu) == tag);
+}
+
+// Store four words (16 bytes) at word index ``w``.  XCD-visible stores write
+// through to the device-coherent level; XCD-local ones stay in this XCD's L2,
+// which is where the same-XCD consumers' device-scope loads find them.
+template <bool DEVICE>
+__device__ __forceinline__ void put4(uint32_t* buf, uint32_t w, u32x4 v) {
+  auto rs = make_rsrc(buf, 0x7fffffffu);
+  if (DEVICE)
+    __builtin_amdgcn_raw_buffer_store_b128(v, rs, w * 4u, 0, 0x10 /* sc1 */);
+  else
+    __builtin_amdgcn_raw_buffer_store_b128(v, rs, w * 4u, 0, 0);
+}
+
+__device__ __forceinline__ void put1_device(uint32_t* p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ u32x4 poll16(__amdgpu_buffer_rsrc_t rs, uint32_t byte_off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(rs, byte_off, 0, 0x10 /* sc1: miss the non-coherent caches */);
+}
+
+}  // namespace qmk

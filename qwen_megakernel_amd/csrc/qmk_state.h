@@ -1,0 +1,20 @@
+// Per-(device, stream) decode state kept in device memory by the library.
+#pragma once
+
+#include <stdint.h>
+
+namespace qmk {
+
+struct DecodeState {
+  uint32_t epoch;  // exchange-tag base; advanced by every completed launch
+  uint32_t err;    // error bits (0 = healthy); a non-zero value makes launches no-ops
+  uint32_t pad0[2];
+  int32_t pos;     // persistent mode: position, input token and step of the next launch
+  int32_t tok;
+  int32_t step;
+  int32_t pad1;
+  uint32_t reserved[56];  // header is 256 bytes; exchange words follow
+};
+static_assert(sizeof(DecodeState) == 256, "state header size");
+
+}  // namespace qmk

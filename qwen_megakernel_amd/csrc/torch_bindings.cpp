@@ -1,0 +1,263 @@
+// torch.ops.qwen_megakernel_C -- the reference's operator library, rebuilt on
+// PyTorch-ROCm over the C ABI of libqwen_megakernel_amd.so.
+//
+// `decode` and `generate_nosync` keep the reference's schemas exactly
+// (reference csrc/torch_bindings.cpp:129-155), so callers written against
+// torch.ops.qwen_megakernel_C work unchanged.  Unlike the reference, every
+// tensor argument is checked (device, dtype, contiguity, size) and the
+// position is range-checked before anything is launched; failures raise
+// through TORCH_CHECK instead of writing out of bounds.  Additive ops:
+// `decode_logits` (also returns the fp32 copy of the bf16 logits),
+// `device_error` and `reset`.
+
+#include <Python.h>
+#include <ATen/hip/impl/HIPGuardImplMasqueradingAsCUDA.h>
+#include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
+#include <torch/all.h>
+#include <torch/library.h>
+
+#include "../../include/qwen_megakernel.h"
+
+namespace {
+
+constexpr int64_t kHidden = 1024, kInter = 3072, kQ = 2048, kKV = 1024, kHeadDim = 128, kKVHeads = 8;
+constexpr int64_t kVocab = 151936, kMaxLayers = 28;
+
+void check_cuda(const torch::Tensor& t, const char* name) {
+  TORCH_CHECK(t.is_cuda(), name, " must be a GPU tensor");
+  TORCH_CHECK(t.is_contiguous(), name, " must be contiguous");
+}
+
+void check_bf16(const torch::Tensor& t, const char* name, int64_t numel) {
+  check_cuda(t, name);
+  TORCH_CHECK(t.scalar_type() == torch::kBFloat16, name, " must be bfloat16");
+  if (numel >= 0) TORCH_CHECK(t.numel() == numel, name, " must have ", numel, " elements, got ", t.numel());
+}
+
+void check_scratch(const torch::Tensor& t, const char* name, int64_t min_bytes) {
+  check_cuda(t, name);
+  TORCH_CHECK(t.numel() * t.element_size() >= min_bytes, name, " is smaller than ", min_bytes, " bytes");
+}
+
+struct Checked {
+  int num_layers;
+  int max_seq_len;
+};
+
+Checked check_common(const torch::Tensor& embed_weight, const torch::Tensor& layer_weights_packed,
+                     const torch::Tensor& final_norm_weight, const torch::Tensor& lm_head_weight,
+                     const torch::Tensor& cos_table, const torch::Tensor& sin_table, const torch::Tensor& k_cache,
+                     const torch::Tensor& v_cache, const torch::Tensor& hidden_buffer,
+                     const torch::Tensor& normalized, int64_t num_layers, int64_t max_seq_len, double attn_scale) {
+  TORCH_CHECK(num_layers >= 1 && num_layers <= kMaxLayers, "num_layers must be in [1, 28], got ", num_layers);
+  TORCH_CHECK(max_seq_len >= 1, "max_seq_len must be positive");
+  TORCH_CHECK(attn_scale > 0.0, "attn_scale must be positive");
+  check_bf16(embed_weight, "embed_weight", kVocab * kHidden);
+  check_bf16(lm_head_weight, "lm_head_weight", kVocab * kHidden);
+  check_bf16(final_norm_weight, "final_norm_weight", kHidden);
+  check_cuda(layer_weights_packed, "layer_weights_packed");
+  TORCH_CHECK(layer_weights_packed.scalar_type() == torch::kUInt8, "layer_weights_packed must be uint8");
+  TORCH_CHECK(layer_weights_packed.numel() >= num_layers * 11 * 8,
+              "layer_weights_packed must hold 11 pointers per layer");
+  TORCH_CHECK(cos_table.dim() == 2 && cos_table.size(1) == kHeadDim && cos_table.size(0) >= max_seq_len,
+              "cos_table must be [>= max_seq_len, 128]");
+  TORCH_CHECK(sin_table.sizes() == cos_table.sizes(), "sin_table must match cos_table");
+  check_bf16(cos_table, "cos_table", -1);
+  check_bf16(sin_table, "sin_table", -1);
+  const int64_t kv = num_layers * kKVHeads * max_seq_len * kHeadDim;
+  check_bf16(k_cache, "k_cache", -1);
+  check_bf16(v_cache, "v_cache", -1);
+  TORCH_CHECK(k_cache.dim() == 4 && k_cache.size(1) == kKVHeads && k_cache.size(2) == max_seq_len &&
+                  k_cache.size(3) == kHeadDim && k_cache.size(0) >= num_layers,
+              "k_cache must be [>= num_layers, 8, max_seq_len, 128]");
+  TORCH_CHECK(v_cache.sizes() == k_cache.sizes(), "v_cache must match k_cache");
+  TORCH_CHECK(k_cache.numel() >= kv, "k_cache too small");
+  check_bf16(hidden_buffer, "hidden_buffer", -1);
+  TORCH_CHECK(hidden_buffer.numel() >= kHidden, "hidden_buffer must hold 1024 bf16");
+  check_cuda(normalized, "normalized");
+  TORCH_CHECK(normalized.scalar_type() == torch::kFloat32 && normalized.numel() >= kHidden,
+              "normalized must be float32 with >= 1024 elements");
+  const auto dev = embed_weight.device();
+  for (const torch::Tensor* t : {&layer_weights_packed, &final_norm_weight, &lm_head_weight, &cos_table, &sin_table,
+                                 &k_cache, &v_cache, &hidden_buffer, &normalized})
+    TORCH_CHECK(t->device() == dev, "all tensors must be on the same device");
+  return Checked{(int)num_layers, (int)max_seq_len};
+}
+
+void check_unused_scratch(const torch::Tensor& activations, const torch::Tensor& residual, const torch::Tensor& q,
+                          const torch::Tensor& k, const torch::Tensor& v, const torch::Tensor& attn_out,
+                          const torch::Tensor& mlp_intermediate, const torch::Tensor& block_max_vals,
+                          const torch::Tensor& block_max_idxs) {
+  // Not used by this kernel, but the reference's callers pass them; keep the
+  // contract that they are GPU tensors of the reference's sizes.
+  check_scratch(activations, "activations", kHidden * 4);
+  check_scratch(residual, "residual", kHidden * 4);
+  check_scratch(q, "q", kQ * 4);
+  check_scratch(k, "k", kKV * 4);
+  check_scratch(v, "v", kKV * 4);
+  check_scratch(attn_out, "attn_out", kQ * 4);
+  check_scratch(mlp_intermediate, "mlp_intermediate", kInter * 4);
+  check_scratch(block_max_vals, "block_max_vals", 4);
+  check_scratch(block_max_idxs, "block_max_idxs", 4);
+}
+
+void raise_status(const char* what) {
+  const int s = qmk_last_status();
+  TORCH_CHECK(s == QMK_OK, what, " failed: ", qmk_status_string(s));
+}
+
+void decode(torch::Tensor output_token, int64_t input_token_id, torch::Tensor embed_weight,
+            torch::Tensor layer_weights_packed, torch::Tensor final_norm_weight, torch::Tensor lm_head_weight,
+            torch::Tensor cos_table, torch::Tensor sin_table, torch::Tensor k_cache, torch::Tensor v_cache,
+            torch::Tensor hidden_buffer, torch::Tensor activations, torch::Tensor residual, torch::Tensor q,
+            torch::Tensor k, torch::Tensor v, torch::Tensor attn_out, torch::Tensor mlp_intermediate,
+            torch::Tensor normalized, torch::Tensor block_max_vals, torch::Tensor block_max_idxs,
+            int64_t num_layers, int64_t position, int64_t max_seq_len, double attn_scale) {
+  const Checked c = check_common(embed_weight, layer_weights_packed, final_norm_weight, lm_head_weight, cos_table,
+                                 sin_table, k_cache, v_cache, hidden_buffer, normalized, num_layers, max_seq_len,
+                                 attn_scale);
+  check_unused_scratch(activations, residual, q, k, v, attn_out, mlp_intermediate, block_max_vals, block_max_idxs);
+  check_cuda(output_token, "output_token");
+  TORCH_CHECK(output_token.scalar_type() == torch::kInt32 && output_token.numel() >= 1, "output_token must be int32[1]");
+  TORCH_CHECK(position >= 0 && position < max_seq_len, "position ", position, " outside [0, ", max_seq_len, ")");
+  TORCH_CHECK(input_token_id >= 0 && input_token_id < kVocab, "input_token_id outside the vocabulary");
+  const c10::hip::HIPGuardMasqueradingAsCUDA guard(embed_weight.device());
+  launch_ldg_decode_direct(
+      (int)input_token_id, static_cast<int*>(output_token.data_ptr()), embed_weight.data_ptr(),
+      reinterpret_cast<const LDGLayerWeights*>(layer_weights_packed.data_ptr()), final_norm_weight.data_ptr(),
+      lm_head_weight.data_ptr(), cos_table.data_ptr(), sin_table.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+      hidden_buffer.data_ptr(), activations.data_ptr(), residual.data_ptr(), q.data_ptr(), k.data_ptr(),
+      v.data_ptr(), attn_out.data_ptr(), mlp_intermediate.data_ptr(), normalized.data_ptr(),
+      block_max_vals.data_ptr(), block_max_idxs.data_ptr(), c.num_layers, (int)position, c.max_seq_len,
+      (float)attn_scale, c10::hip::getCurrentHIPStreamMasqueradingAsCUDA().stream());
+  raise_status("decode");
+}
+
+torch::Tensor generate_nosync(int64_t first_token_id, int64_t num_steps, torch::Tensor embed_weight,
+                              torch::Tensor layer_weights_packed, torch::Tensor final_norm_weight,
+                              torch::Tensor lm_head_weight, torch::Tensor cos_table, torch::Tensor sin_table,
+                              torch::Tensor k_cache, torch::Tensor v_cache, torch::Tensor hidden_buffer,
+                              torch::Tensor activations, torch::Tensor residual, torch::Tensor q, torch::Tensor k,
+                              torch::Tensor v, torch::Tensor attn_out, torch::Tensor mlp_intermediate,
+                              torch::Tensor normalized, torch::Tensor block_max_vals, torch::Tensor block_max_idxs,
+                              int64_t num_layers, int64_t start_position, int64_t max_seq_len, double attn_scale) {
+  const Checked c = check_common(embed_weight, layer_weights_packed, final_norm_weight, lm_head_weight, cos_table,
+                                 sin_table, k_cache, v_cache, hidden_buffer, normalized, num_layers, max_seq_len,
+                                 attn_scale);
+  check_unused_scratch(activations, residual, q, k, v, attn_out, mlp_intermediate, block_max_vals, block_max_idxs);
+  TORCH_CHECK(num_steps >= 0, "num_steps must be non-negative");
+  TORCH_CHECK(start_position >= 0 && start_position + num_steps <= max_seq_len, "steps [", start_position, ", ",
+              start_position + num_steps, ") do not fit in max_seq_len ", max_seq_len);
+  TORCH_CHECK(first_token_id >= 0 && first_token_id < kVocab, "first_token_id outside the vocabulary");
+  const c10::hip::HIPGuardMasqueradingAsCUDA guard(embed_weight.device());
+  auto stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA().stream();
+  auto output_log = torch::empty({num_steps}, torch::dtype(torch::kInt32).device(embed_weight.device()));
+  if (num_steps == 0) return output_log;
+  launch_ldg_generate_nosync(
+      (int)first_token_id, (int)num_steps, embed_weight.data_ptr(),
+      reinterpret_cast<const LDGLayerWeights*>(layer_weights_packed.data_ptr()), final_norm_weight.data_ptr(),
+      lm_head_weight.data_ptr(), cos_table.data_ptr(), sin_table.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+      hidden_buffer.data_ptr(), activations.data_ptr(), residual.data_ptr(), q.data_ptr(), k.data_ptr(),
+      v.data_ptr(), attn_out.data_ptr(), mlp_intermediate.data_ptr(), normalized.data_ptr(),
+      block_max_vals.data_ptr(), block_max_idxs.data_ptr(), static_cast<int*>(output_log.data_ptr()), c.num_layers,
+      (int)start_position, c.max_seq_len, (float)attn_scale, stream);
+  raise_status("generate_nosync");
+  // Single synchronisation at the end, as the reference (csrc/torch_bindings.cpp:125).
+  const uint32_t err = qmk_device_error(stream);
+  TORCH_CHECK(err == 0, "generate_nosync: device error bits 0x", std::hex, err,
+              " (a bounded wait expired or a position left the cache); call reset()");
+  return output_log;
+}
+
+void decode_logits(torch::Tensor output_token, torch::Tensor logits, int64_t input_token_id,
+                   torch::Tensor embed_weight, torch::Tensor layer_weights_packed, torch::Tensor final_norm_weight,
+                   torch::Tensor lm_head_weight, torch::Tensor cos_table, torch::Tensor sin_table,
+                   torch::Tensor k_cache, torch::Tensor v_cache, torch::Tensor hidden_buffer,
+                   torch::Tensor normalized, int64_t num_layers, int64_t position, int64_t max_seq_len,
+                   double attn_scale) {
+  const Checked c = check_common(embed_weight, layer_weights_packed, final_norm_weight, lm_head_weight, cos_table,
+                                 sin_table, k_cache, v_cache, hidden_buffer, normalized, num_layers, max_seq_len,
+                                 attn_scale);
+  check_cuda(output_token, "output_token");
+  TORCH_CHECK(output_token.scalar_type() == torch::kInt32 && output_token.numel() >= 1, "output_token must be int32[1]");
+  check_cuda(logits, "logits");
+  TORCH_CHECK(logits.scalar_type() == torch::kFloat32 && logits.numel() == kVocab, "logits must be float32[151936]");
+  TORCH_CHECK(position >= 0 && position < max_seq_len, "position ", position, " outside [0, ", max_seq_len, ")");
+  TORCH_CHECK(input_token_id >= 0 && input_token_id < kVocab, "input_token_id outside the vocabulary");
+  const c10::hip::HIPGuardMasqueradingAsCUDA guard(embed_weight.device());
+  qmk_decode_logits((int)input_token_id, static_cast<int*>(output_token.data_ptr()),
+                    static_cast<float*>(logits.data_ptr()), embed_weight.data_ptr(),
+                    reinterpret_cast<const LDGLayerWeights*>(layer_weights_packed.data_ptr()),
+                    final_norm_weight.data_ptr(), lm_head_weight.data_ptr(), cos_table.data_ptr(),
+                    sin_table.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), hidden_buffer.data_ptr(),
+                    normalized.data_ptr(), c.num_layers, (int)position, c.max_seq_len, (float)attn_scale,
+                    c10::hip::getCurrentHIPStreamMasqueradingAsCUDA().stream());
+  raise_status("decode_logits");
+}
+
+int64_t device_error() {
+  return (int64_t)qmk_device_error(c10::hip::getCurrentHIPStreamMasqueradingAsCUDA().stream());
+}
+
+void reset() {
+  const int s = qmk_reset(c10::hip::getCurrentHIPStreamMasqueradingAsCUDA().stream());
+  TORCH_CHECK(s == QMK_OK, "reset failed: ", qmk_status_string(s));
+}
+
+void set_wait_limit(int64_t ticks) {
+  TORCH_CHECK(ticks >= 0 && ticks <= 0xffffffffLL, "ticks out of range");
+  const int s = qmk_set_wait_limit(c10::hip::getCurrentHIPStreamMasqueradingAsCUDA().stream(), (uint32_t)ticks);
+  TORCH_CHECK(s == QMK_OK, "set_wait_limit failed: ", qmk_status_string(s));
+}
+
+}  // namespace
+
+TORCH_LIBRARY(qwen_megakernel_C, ops) {
+  ops.def(
+      "decode(Tensor output_token, int input_token_id, "
+      "Tensor embed_weight, Tensor layer_weights_packed, "
+      "Tensor final_norm_weight, Tensor lm_head_weight, "
+      "Tensor cos_table, Tensor sin_table, "
+      "Tensor k_cache, Tensor v_cache, "
+      "Tensor hidden_buffer, Tensor activations, Tensor residual, "
+      "Tensor q, Tensor k, Tensor v, Tensor attn_out, "
+      "Tensor mlp_intermediate, Tensor normalized, "
+      "Tensor block_max_vals, Tensor block_max_idxs, "
+      "int num_layers, int position, int max_seq_len, "
+      "float attn_scale) -> ()");
+  ops.impl("decode", torch::kCUDA, &decode);
+
+  ops.def(
+      "generate_nosync(int first_token_id, int num_steps, "
+      "Tensor embed_weight, Tensor layer_weights_packed, "
+      "Tensor final_norm_weight, Tensor lm_head_weight, "
+      "Tensor cos_table, Tensor sin_table, "
+      "Tensor k_cache, Tensor v_cache, "
+      "Tensor hidden_buffer, Tensor activations, Tensor residual, "
+      "Tensor q, Tensor k, Tensor v, Tensor attn_out, "
+      "Tensor mlp_intermediate, Tensor normalized, "
+      "Tensor block_max_vals, Tensor block_max_idxs, "
+      "int num_layers, int start_position, int max_seq_len, "
+      "float attn_scale) -> Tensor");
+  ops.impl("generate_nosync", torch::kCUDA, &generate_nosync);
+
+  ops.def(
+      "decode_logits(Tensor output_token, Tensor logits, int input_token_id, "
+      "Tensor embed_weight, Tensor layer_weights_packed, "
+      "Tensor final_norm_weight, Tensor lm_head_weight, "
+      "Tensor cos_table, Tensor sin_table, Tensor k_cache, Tensor v_cache, "
+      "Tensor hidden_buffer, Tensor normalized, "
+      "int num_layers, int position, int max_seq_len, float attn_scale) -> ()");
+  ops.impl("decode_logits", torch::kCUDA, &decode_logits);
+
+  ops.def("device_error() -> int", &device_error);
+  ops.def("reset() -> ()", &reset);
+  ops.def("set_wait_limit(int ticks) -> ()", &set_wait_limit);
+}
+
+// Empty Python module so the shared object can also be imported by name
+// (reference csrc/torch_bindings.cpp:14-19, 157).
+extern "C" PyObject* PyInit_qwen_megakernel_C() {
+  static struct PyModuleDef module = {PyModuleDef_HEAD_INIT, "qwen_megakernel_C", nullptr, 0, nullptr};
+  return PyModule_Create(&module);
+}

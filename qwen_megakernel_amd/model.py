@@ -1,0 +1,228 @@
+"""Weight loading and the high-level decode API for Qwen3-0.6B on MI355X.
+
+Mirrors the reference's qwen_megakernel/model.py: the same constants, the same
+weights dict, the same packed 11-pointer layer table, the same ``Decoder``
+(``step``, ``reset``, ``position``, ``generate``) and module-level
+``generate``, calling ``torch.ops.qwen_megakernel_C.decode`` /
+``generate_nosync`` with the reference's argument lists.
+
+Differences, all additive:
+
+* ``load_weights`` has no network.  ``model_name`` may name a local directory
+  holding a Qwen3 checkpoint (``*.safetensors`` + tokenizer files); anything
+  else yields the seeded synthetic weights of :mod:`qwen_megakernel_amd.weights`
+  and no tokenizer.
+* RoPE theta is 1e6 (Qwen3), not the reference's 10000 (model.py:54-56).
+* ``max_seq_len`` is a parameter (the reference fixes 2048).
+* ``Decoder.step`` raises on a device failure instead of returning a stale token;
+  positions are range-checked.
+* ``Decoder.step_logits`` returns the logits as well, ``Decoder.load_kv`` injects
+  cache contents, and ``generate`` accepts token-id lists when there is no tokenizer.
+"""
+
+from __future__ import annotations
+
+import glob
+import math
+import os
+import struct
+
+import torch
+
+from .shapes import QWEN3_0_6B
+from . import weights as _w
+
+NUM_LAYERS = 28
+NUM_KV_HEADS = 8
+HEAD_DIM = 128
+HIDDEN_SIZE = 1024
+INTERMEDIATE_SIZE = 3072
+Q_SIZE = 16 * HEAD_DIM  # 2048
+KV_SIZE = 8 * HEAD_DIM  # 1024
+MAX_SEQ_LEN = 2048
+VOCAB_SIZE = 151936
+
+
+def _ops():
+    from .build import get_extension
+
+    return get_extension()
+
+
+def load_weights(model_name: str = "Qwen/Qwen3-0.6B", verbose: bool = True, *, max_seq_len: int = MAX_SEQ_LEN,
+                 seed: int = 0, device: str = "cuda"):
+    """Return ``(weights, tokenizer)`` in the reference's dict layout (model.py:21-94).
+
+    A local directory with ``*.safetensors`` is loaded as a real checkpoint;
+    otherwise the seeded synthetic Qwen3-0.6B weights are drawn (tokenizer None).
+    """
+    if os.path.isdir(model_name) and glob.glob(os.path.join(model_name, "*.safetensors")):
+        from safetensors.torch import load_file
+
+        state = {}
+        for f in sorted(glob.glob(os.path.join(model_name, "*.safetensors"))):
+            state.update(load_file(f))
+        if verbose:
+            print(f"Loading {model_name} (local safetensors)...")
+        weights = _w.load_weights_from_state_dict(state, QWEN3_0_6B, max_seq_len=max_seq_len, device=device)
+        tokenizer = None
+        try:
+            from transformers import AutoTokenizer
+
+            tokenizer = AutoTokenizer.from_pretrained(model_name)
+        except Exception:
+            tokenizer = None
+        return weights, tokenizer
+    if verbose:
+        print(f"{model_name}: no local checkpoint; using seeded synthetic Qwen3-0.6B weights (seed {seed})")
+    return _w.make_weights(QWEN3_0_6B, seed=seed, max_seq_len=max_seq_len, device=device), None
+
+
+def _pack_layer_weights(layer_weights: list[torch.Tensor], num_layers: int = NUM_LAYERS) -> torch.Tensor:
+    """Device blob of ``num_layers`` 11-pointer tables (model.py:97-108)."""
+    n_ptrs = 11
+    buf = bytearray(num_layers * n_ptrs * 8)
+    for i in range(num_layers):
+        for j in range(n_ptrs):
+            struct.pack_into("Q", buf, (i * n_ptrs + j) * 8, layer_weights[i * n_ptrs + j].data_ptr())
+    return torch.frombuffer(buf, dtype=torch.uint8).to(layer_weights[0].device)
+
+
+class Decoder:
+    """Stateful decoder over torch.ops.qwen_megakernel_C (model.py:111-245)."""
+
+    def __init__(self, weights=None, tokenizer=None, model_name: str = "Qwen/Qwen3-0.6B", verbose: bool = True,
+                 max_seq_len: int = MAX_SEQ_LEN, num_layers: int = NUM_LAYERS):
+        self._ops = _ops()
+        if weights is None:
+            weights, tokenizer = load_weights(model_name, verbose=verbose, max_seq_len=max_seq_len)
+        weights = _w.to_device(weights, "cuda")
+        if not 1 <= num_layers <= NUM_LAYERS or len(weights["layer_weights"]) < 11 * num_layers:
+            raise ValueError(f"num_layers={num_layers} does not match the weights")
+        if weights["cos_table"].shape[0] < max_seq_len:
+            raise ValueError("RoPE tables are shorter than max_seq_len")
+        self.tokenizer = tokenizer
+        self._position = 0
+        self._num_layers = num_layers
+        self._max_seq_len = max_seq_len
+        self._weights = weights  # keeps the storage the packed pointers refer to alive
+        self._embed_weight = weights["embed_weight"]
+        self._final_norm_weight = weights["final_norm_weight"]
+        self._lm_head_weight = weights["lm_head_weight"]
+        self._cos_table = weights["cos_table"]
+        self._sin_table = weights["sin_table"]
+        self._layer_weights_packed = _pack_layer_weights(weights["layer_weights"], num_layers)
+        self._attn_scale = 1.0 / math.sqrt(HEAD_DIM)
+        dev = self._embed_weight.device
+        self._k_cache = torch.zeros(num_layers, NUM_KV_HEADS, max_seq_len, HEAD_DIM, dtype=torch.bfloat16, device=dev)
+        self._v_cache = torch.zeros_like(self._k_cache)
+        f32 = dict(dtype=torch.float32, device=dev)
+        bf16 = dict(dtype=torch.bfloat16, device=dev)
+        self._hidden = torch.empty(HIDDEN_SIZE, **bf16)
+        self._act = torch.empty(HIDDEN_SIZE, **f32)
+        self._res = torch.empty(HIDDEN_SIZE, **f32)
+        self._q = torch.empty(Q_SIZE, **f32)
+        self._k = torch.empty(KV_SIZE, **f32)
+        self._v = torch.empty(KV_SIZE, **f32)
+        self._attn_out = torch.empty(Q_SIZE, **f32)
+        self._mlp_inter = torch.empty(INTERMEDIATE_SIZE, **f32)
+        self._norm_out = torch.empty(HIDDEN_SIZE, **f32)
+        self._bmax_vals = torch.empty(4096, **f32)
+        self._bmax_idxs = torch.empty(4096, dtype=torch.int32, device=dev)
+        self._out_token = torch.empty(1, dtype=torch.int32, device=dev)
+        self._logits = torch.empty(VOCAB_SIZE, **f32)
+
+    # -- reference API --------------------------------------------------
+
+    def _check_position(self, n: int = 1):
+        if self._position + n > self._max_seq_len:
+            raise ValueError(f"position {self._position} + {n} exceeds max_seq_len {self._max_seq_len}")
+
+    def _scratch(self):
+        return (self._embed_weight, self._layer_weights_packed, self._final_norm_weight, self._lm_head_weight,
+                self._cos_table, self._sin_table, self._k_cache, self._v_cache, self._hidden, self._act,
+                self._res, self._q, self._k, self._v, self._attn_out, self._mlp_inter, self._norm_out,
+                self._bmax_vals, self._bmax_idxs)
+
+    def _raise_device_error(self):
+        err = int(self._ops.device_error())
+        raise RuntimeError(f"decode failed on the device (error bits 0x{err:x}); call reset()")
+
+    def step(self, token_id: int) -> int:
+        """Decode one token. Returns the next token id."""
+        self._check_position()
+        self._ops.decode(self._out_token, int(token_id), *self._scratch(), self._num_layers, self._position,
+                         self._max_seq_len, self._attn_scale)
+        self._position += 1
+        tok = int(self._out_token.item())
+        if tok < 0:
+            self._raise_device_error()
+        return tok
+
+    def reset(self):
+        self._position = 0
+        self._k_cache.zero_()
+        self._v_cache.zero_()
+        self._ops.reset()
+
+    @property
+    def position(self) -> int:
+        return self._position
+
+    def generate(self, prompt, max_tokens: int = 100):
+        """Greedy continuation of ``prompt`` (text with a tokenizer, or a list of ids)."""
+        self.reset()
+        if isinstance(prompt, str):
+            if self.tokenizer is None:
+                raise ValueError("text prompts need a tokenizer; pass a list of token ids")
+            ids = self.tokenizer.encode(prompt, add_special_tokens=True)
+        else:
+            ids = [int(t) for t in prompt]
+        out = self.generate_ids(ids, max_tokens)
+        if not isinstance(prompt, str):
+            return out
+        eos = self.tokenizer.eos_token_id
+        if eos in out:
+            out = out[: out.index(eos)]
+        return self.tokenizer.decode(out, skip_special_tokens=True)
+
+    # -- additions --------------------------------------------------------
+
+    def generate_ids(self, ids: list[int], max_tokens: int) -> list[int]:
+        """Step ``ids[:-1]``, then ``max_tokens`` device-fed greedy steps from ``ids[-1]``."""
+        if not ids:
+            raise ValueError("empty prompt")
+        for tid in ids[:-1]:
+            self.step(tid)
+        self._check_position(max_tokens)
+        out = self._ops.generate_nosync(int(ids[-1]), int(max_tokens), *self._scratch(), self._num_layers,
+                                        self._position, self._max_seq_len, self._attn_scale)
+        self._position += max_tokens
+        return out.cpu().tolist()
+
+    def step_logits(self, token_id: int):
+        """Decode one token; returns ``(next_token, logits)`` with fp32 logits (bf16 values)."""
+        self._check_position()
+        self._ops.decode_logits(self._out_token, self._logits, int(token_id), self._embed_weight,
+                                self._layer_weights_packed, self._final_norm_weight, self._lm_head_weight,
+                                self._cos_table, self._sin_table, self._k_cache, self._v_cache, self._hidden,
+                                self._norm_out, self._num_layers, self._position, self._max_seq_len,
+                                self._attn_scale)
+        self._position += 1
+        tok = int(self._out_token.item())
+        if tok < 0:
+            self._raise_device_error()
+        return tok, self._logits.clone()
+
+    def load_kv(self, k: torch.Tensor, v: torch.Tensor, cache_len: int):
+        """Inject cache contents for positions ``[0, cache_len)``; decoding continues at ``cache_len``."""
+        if cache_len > self._max_seq_len:
+            raise ValueError("cache_len exceeds max_seq_len")
+        self._k_cache[:, :, :cache_len].copy_(k[: self._num_layers, :, :cache_len])
+        self._v_cache[:, :, :cache_len].copy_(v[: self._num_layers, :, :cache_len])
+        self._position = cache_len
+
+
+def generate(prompt, max_tokens: int = 100, verbose: bool = True):
+    """One-shot convenience: load weights, generate, return text (or ids)."""
+    return Decoder(verbose=verbose).generate(prompt, max_tokens)
