@@ -1,0 +1,169 @@
+#!/usr/bin/env python3
+"""Decode throughput of the gfx950 Qwen3-0.6B megakernel (one JSON line on stdout).
+
+Workload: Qwen3-0.6B architecture, seeded synthetic bf16 weights, a 128-token
+random prompt prefilled into the KV cache one decode step at a time, then K
+greedy batch-1 decode steps with device-side token feedback (the reference's
+``generate_nosync`` path).  A "step" is one decode token = one kernel launch.
+W warm-up steps run first on a separate pass (then the cache is reset and the
+prompt re-prefilled), so the K timed steps always cover contexts 129..128+K.
+
+``value`` is decode tok/s over the timed region (inputs resident in HBM).
+``roofline`` relates the decode kernel's algorithmic bytes per launch
+(weights + KV read + KV written, averaged over the timed contexts) to its
+average launch duration measured with HIP events on the launch stream.
+``cpu_baseline`` times the CPU oracle (HF-semantics bf16 decode) on the host.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+PEAK_HBM_GBS = 8000.0
+PROMPT_LEN = 128
+METRIC = "decode tok/s, batch 1, Qwen3-0.6B bf16; achieved HBM GB/s vs ~8 TB/s peak"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def cpu_baseline(steps: int = 32):
+    """Oracle decode on the host: 16-token prompt fed, then `steps` timed greedy steps."""
+    import torch
+
+    from oracle.qwen3_ref import OracleDecoder
+    from qwen_megakernel_amd.shapes import QWEN3_0_6B
+    from qwen_megakernel_amd.weights import make_prompt, make_weights
+
+    threads = max(1, min(len(os.sched_getaffinity(0)), 16))
+    torch.set_num_threads(threads)
+    w = make_weights(QWEN3_0_6B, seed=0, max_seq_len=128)
+    dec = OracleDecoder(w, QWEN3_0_6B, max_seq_len=128)
+    prompt = make_prompt(16, QWEN3_0_6B.vocab, seed=1)
+    tok = None
+    for t in prompt:
+        tok = dec.step(t)
+    for _ in range(2):  # warm-up
+        tok = dec.step(tok)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        tok = dec.step(tok)
+    dt = time.perf_counter() - t0
+    cpu = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    cpu = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"value": round(steps / dt, 3), "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": f"CPU oracle (HF-semantics bf16 PyTorch decode), Qwen3-0.6B, 16-token prompt, "
+                      f"{steps} greedy steps timed at context 19..{18 + steps}; {cpu}"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=1024)
+    ap.add_argument("--warmup", type=int, default=32)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-steps", type=int, default=32)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (this path does not shard "
+              f"across GPUs)", file=sys.stderr)
+        sys.exit(2)
+    if args.steps < 1 or args.warmup < 0:
+        sys.exit("steps must be >= 1 and warmup >= 0")
+
+    import torch
+
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from qwen_megakernel_amd.model import Decoder, HEAD_DIM
+    from qwen_megakernel_amd.shapes import QWEN3_0_6B
+    from qwen_megakernel_amd.weights import make_prompt, make_weights
+
+    max_seq = 2048
+    while PROMPT_LEN + max(args.steps, args.warmup) > max_seq:
+        max_seq *= 2
+    t0 = time.time()
+    w = make_weights(QWEN3_0_6B, seed=0, max_seq_len=max_seq, device="cuda")
+    dec = Decoder(weights=w, verbose=False, max_seq_len=max_seq)
+    prompt = make_prompt(PROMPT_LEN, QWEN3_0_6B.vocab, seed=1)
+    ops = torch.ops.qwen_megakernel_C
+    log(f"setup {time.time() - t0:.1f}s")
+
+    def prefill():
+        dec.reset()
+        for t in prompt[:-1]:
+            dec.step(t)
+
+    def run(n):
+        return ops.generate_nosync(prompt[-1], n, *dec._scratch(), QWEN3_0_6B.num_layers, dec.position,
+                                   max_seq, dec._attn_scale)
+
+    if args.warmup:
+        prefill()
+        run(args.warmup)
+    prefill()
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    e0.record(stream)
+    toks = run(args.steps)  # synchronises the stream at the end
+    e1.record(stream)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    gpu_ms = e0.elapsed_time(e1)
+    assert toks.numel() == args.steps and int(ops.device_error()) == 0
+
+    first_c = PROMPT_LEN + 1  # cache_len of the first timed step (position 128)
+    mean_c = first_c + (args.steps - 1) / 2.0
+    bytes_per_launch = QWEN3_0_6B.weight_bytes_per_token() + QWEN3_0_6B.kv_bytes_per_position() * (mean_c + 1)
+    avg_launch_s = gpu_ms / 1e3 / args.steps
+    achieved = bytes_per_launch / avg_launch_s / 1e9
+    value = args.steps / dt
+    result = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(dt * 1e3 / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "qwen3-0.6b greedy decode, batch 1, 128-token prompt prefilled, "
+                               f"{args.steps} device-fed decode steps (context {first_c}..{PROMPT_LEN + args.steps})",
+                   "batch": 1, "prompt_len": PROMPT_LEN, "decode_steps": args.steps, "max_seq_len": max_seq,
+                   "weights": "seeded N(0,0.02) bf16, norms 1, tied embeddings"},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
+                     "bytes_per_launch": int(bytes_per_launch), "avg_launch_us": round(avg_launch_s * 1e6, 2),
+                     "kernel": "qmk::decode_kernel<Qwen3_0_6B>"},
+        "cpu_baseline": None,
+    }
+    log(f"decode: {value:.1f} tok/s, {dt * 1e3 / args.steps:.3f} ms/token, kernel avg {avg_launch_s * 1e6:.1f} us, "
+        f"{achieved:.0f} GB/s algorithmic")
+    if not args.no_cpu_baseline:
+        del dec, w
+        torch.cuda.empty_cache()
+        t0 = time.time()
+        result["cpu_baseline"] = cpu_baseline(args.cpu_steps)
+        log(f"cpu baseline {result['cpu_baseline']['value']} tok/s ({time.time() - t0:.1f}s)")
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

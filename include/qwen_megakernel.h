@@ -145,6 +145,13 @@ int qmk_reset(hipStream_t stream);
  * bound to drive the failure path without any risk of a hang. */
 int qmk_set_wait_limit(hipStream_t stream, uint32_t ticks);
 
+/* Phase trace.  When `buf` (device uint64[qmk_trace_entries(28)]) is set,
+ * every launch on `stream` writes, for each workgroup w, the 100 MHz device
+ * wall clock at 13 points of each layer and 3 points after the last layer:
+ * buf[point * 256 + w], point = layer * 13 + k.  NULL disables tracing. */
+int qmk_set_trace(hipStream_t stream, uint64_t *buf, size_t entries);
+size_t qmk_trace_entries(int num_layers);
+
 /* Kernel launch geometry, for tools: workgroups and threads per workgroup. */
 void qmk_launch_geometry(int *workgroups, int *threads);
 

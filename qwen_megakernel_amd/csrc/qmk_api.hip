@@ -32,6 +32,7 @@ struct Ctx {
   uint32_t* host_err = nullptr;
   int xcd_local = 0;
   uint32_t timeout = kTimeoutDefault;
+  uint64_t* trace = nullptr;
 };
 
 struct DevInfo {
@@ -177,6 +178,7 @@ KArgs make_args(const Common& c, Ctx* ctx) {
   a.rms_eps = 1e-6f;
   a.timeout = ctx->timeout;
   a.xcd_local = ctx->xcd_local;
+  a.trace = ctx->trace;
   return a;
 }
 
@@ -339,6 +341,19 @@ int qmk_set_wait_limit(hipStream_t stream, uint32_t ticks) {
   }
   ctx->timeout = ticks;
   return fail(QMK_OK);
+}
+
+int qmk_set_trace(hipStream_t stream, uint64_t* buf, size_t entries) {
+  Ctx* ctx = nullptr;
+  int s = get_ctx(stream, &ctx);
+  if (s != QMK_OK) return fail(s);
+  if (buf && entries < (size_t)qmk_trace_entries(28)) return fail(QMK_ERR_ARG);
+  ctx->trace = buf;
+  return fail(QMK_OK);
+}
+
+size_t qmk_trace_entries(int num_layers) {
+  return (size_t)(num_layers * kTracePoints + 3) * kNumWG;
 }
 
 void qmk_launch_geometry(int* workgroups, int* threads) {

@@ -117,6 +117,7 @@ struct KArgs {
   DecodeState* st;
   uint32_t* x;             // exchange words
   uint32_t* host_err;      // optional host-visible error word
+  uint64_t* trace;         // optional: wall-clock stamps [layer*13 + point][workgroup], then 3 final points
   int num_layers;
   int max_seq_len;
   int position;            // < 0: read position/token/step from the state
@@ -303,6 +304,8 @@ __device__ __forceinline__ uint32_t orderable16(uint32_t h) { return (h & 0x8000
 //   k..l        .                                    LM-head rows
 //   l..         argmax keys, WG 0 picks the token    .
 
+constexpr int kTracePoints = 13;  // wall-clock stamps per layer (see the schedule above)
+
 struct Step {
   uint32_t epoch;
   int pos, tok, step, C, nl;
@@ -337,8 +340,13 @@ __device__ __forceinline__ void control_path(const KArgs& a, Smem<M>& s, const S
     };
   };
 
+  auto stamp = [&](int point) {
+    if (a.trace && lane == 0) a.trace[(size_t)point * kNumWG + b] = wall_clock64();
+  };
   for (int L = 0; L < p.nl; L++) {
     const LayerPtrs& w = a.layers[L];
+    const int tp = L * kTracePoints;
+    stamp(tp + 0);
     // ---------------------------------------------------------------- a
     if (L == 0) {
       const uint16_t* e = a.embed + (size_t)p.tok * Dm::H;
@@ -353,8 +361,10 @@ __device__ __forceinline__ void control_path(const KArgs& a, Smem<M>& s, const S
     } else if (ctl.template gather<Dm::H>(a.x + Dm::X_H, tag_of(L - 1, 5), to_f32(s.x))) {
       ctl.rmsnorm(s.x, w.in_ln);
     }
+    stamp(tp + 1);
     QMK_SYNC();  // a
     QMK_SYNC();  // b
+    stamp(tp + 2);
     {
       const uint32_t t = tag_of(L, 0);
       if (lane < Dm::RQ_WG / 4) {
@@ -381,8 +391,10 @@ __device__ __forceinline__ void control_path(const KArgs& a, Smem<M>& s, const S
         }
       }
     }
+    stamp(tp + 3);
     QMK_SYNC();  // c
     QMK_SYNC();  // d
+    stamp(tp + 4);
     {
       // workgroup partial = merge of the eight wave partials, then publish
       const uint32_t t = tag_of(L, 1);
@@ -411,6 +423,7 @@ __device__ __forceinline__ void control_path(const KArgs& a, Smem<M>& s, const S
           if (a.xcd_local) put4<false>(a.x, base, d); else put4<true>(a.x, base, d);
         }
       }
+      stamp(tp + 5);
       // combine: this workgroup owns (head hh, dims 8kb..8kb+7) of its group
       const int hh = r / (Dm::D / 8), kb = r % (Dm::D / 8);
       const uint32_t pbase = Dm::X_PART + (uint32_t)(g * kGroupSize * Dm::PART_WG + hh * Dm::PART_HEAD);
@@ -439,6 +452,7 @@ __device__ __forceinline__ void control_path(const KArgs& a, Smem<M>& s, const S
         if (!__any(pend != 0)) break;
         if (wall_clock64() - t0 > a.timeout) { ctl.fail(kErrTimeout); ok = false; break; }
       }
+      stamp(tp + 6);
       if (ok) {
 #pragma unroll
         for (int i = 0; i < PER; i++) {
@@ -475,8 +489,10 @@ __device__ __forceinline__ void control_path(const KArgs& a, Smem<M>& s, const S
         ctl.template gather<Dm::QS>(a.x + Dm::X_ATTN, tag_of(L, 2), to_bf16(s.attn));
       }
     }
+    stamp(tp + 7);
     QMK_SYNC();  // e
     QMK_SYNC();  // f
+    stamp(tp + 8);
     if (lane == 0) {
       float hv[4];
 #pragma unroll
@@ -489,8 +505,10 @@ __device__ __forceinline__ void control_path(const KArgs& a, Smem<M>& s, const S
       ctl.template publish4<true>(Dm::X_H2 + Dm::O_ROWS * b, hv[0], hv[1], hv[2], hv[3], tag_of(L, 3));
     }
     if (ctl.template gather<Dm::H>(a.x + Dm::X_H2, tag_of(L, 3), to_f32(s.h2))) ctl.rmsnorm(s.h2, w.post_ln);
+    stamp(tp + 9);
     QMK_SYNC();  // g
     QMK_SYNC();  // h
+    stamp(tp + 10);
     if (lane < Dm::M_WG / 4) {
       float mv[4];
 #pragma unroll
@@ -503,8 +521,10 @@ __device__ __forceinline__ void control_path(const KArgs& a, Smem<M>& s, const S
       ctl.template publish4<true>(Dm::X_M + Dm::M_WG * b + 4 * lane, mv[0], mv[1], mv[2], mv[3], tag_of(L, 4));
     }
     ctl.template gather<Dm::I>(a.x + Dm::X_M, tag_of(L, 4), to_bf16(s.m));
+    stamp(tp + 11);
     QMK_SYNC();  // i
     QMK_SYNC();  // j
+    stamp(tp + 12);
     if (lane == 0) {
       float hv[4];
 #pragma unroll
@@ -531,8 +551,10 @@ __device__ __forceinline__ void control_path(const KArgs& a, Smem<M>& s, const S
       }
     }
   }
+  stamp(p.nl * kTracePoints + 0);
   QMK_SYNC();  // k
   QMK_SYNC();  // l
+  stamp(p.nl * kTracePoints + 1);
   const uint32_t tk = make_tag(p.epoch, (uint32_t)(p.nl * Dm::N_X_PER_LAYER));
   if (lane == 0) {
     uint64_t best = 0;
@@ -553,6 +575,7 @@ __device__ __forceinline__ void control_path(const KArgs& a, Smem<M>& s, const S
       const uint64_t key = ((uint64_t)(v.x >> 16) << 32) | (uint64_t)(0xffffffffu - idx);
       best = key > best ? key : best;
     });
+    stamp(p.nl * kTracePoints + 2);
     if (ok) {
       best = wave_max_u64(best);
       const int token = (int)(0xffffffffu - (uint32_t)best);

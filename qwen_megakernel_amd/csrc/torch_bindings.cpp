@@ -210,6 +210,19 @@ void set_wait_limit(int64_t ticks) {
   TORCH_CHECK(s == QMK_OK, "set_wait_limit failed: ", qmk_status_string(s));
 }
 
+void set_trace(std::optional<torch::Tensor> buf) {
+  auto stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA().stream();
+  int s;
+  if (buf.has_value()) {
+    check_cuda(*buf, "trace");
+    TORCH_CHECK(buf->scalar_type() == torch::kInt64, "trace buffer must be int64");
+    s = qmk_set_trace(stream, reinterpret_cast<uint64_t*>(buf->data_ptr()), (size_t)buf->numel());
+  } else {
+    s = qmk_set_trace(stream, nullptr, 0);
+  }
+  TORCH_CHECK(s == QMK_OK, "set_trace failed: ", qmk_status_string(s));
+}
+
 }  // namespace
 
 TORCH_LIBRARY(qwen_megakernel_C, ops) {
@@ -253,6 +266,7 @@ TORCH_LIBRARY(qwen_megakernel_C, ops) {
   ops.def("device_error() -> int", &device_error);
   ops.def("reset() -> ()", &reset);
   ops.def("set_wait_limit(int ticks) -> ()", &set_wait_limit);
+  ops.def("set_trace(Tensor? buf) -> ()", &set_trace);
 }
 
 // Empty Python module so the shared object can also be imported by name

