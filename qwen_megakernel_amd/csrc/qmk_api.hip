@@ -152,7 +152,7 @@ struct Common {
 int validate(const Common& c) {
   if (!c.embed || !c.layers || !c.final_norm || !c.lm_head || !c.cos_t || !c.sin_t || !c.k_cache || !c.v_cache)
     return QMK_ERR_ARG;
-  if (c.num_layers < 1 || c.num_layers > 28 || c.max_seq_len < 1) return QMK_ERR_ARG;
+  if (c.num_layers < 1 || c.num_layers > 28 || c.max_seq_len < 1 || c.max_seq_len > kMaxSeqLen) return QMK_ERR_ARG;
   if (!(c.attn_scale > 0.f)) return QMK_ERR_ARG;
   return QMK_OK;
 }

@@ -4,33 +4,49 @@
 // Replaces the reference's ldg_decode_kernel_direct / _persistent +
 // ldg_lm_head_fused + ldg_update_step (reference csrc/kernel.cu:1189-1440).
 // The reference splits the work over 128 blocks of 16 warps that meet at
-// global atomic barriers (csrc/kernel.cu:94-119); here 256 workgroups (one per
-// CU, so b % 8 is the XCD) hand activations to each other through tagged words
-// (qmk_device.h), with no barrier anywhere:
+// global atomic barriers (csrc/kernel.cu:94-119).  Here 256 workgroups run,
+// one per CU; workgroup b sits on XCD x = b % 8 with rank r = b / 8 inside
+// it, and the eight XCDs split each layer the way eight GPUs would under
+// tensor parallelism, so that almost every hand-off stays inside one XCD's L2:
 //
-//   phase   producers -> consumers           exchange (words)
-//   QKV     256 WGs   -> the 32 WGs of an XCD  q/k/v of one KV-head group (512)
-//   ATT     32 WGs    -> same 32 WGs           split-K softmax partials
-//   COMB    32 WGs    -> all                   attention output (2048)
-//   O       all       -> all                   h' = h + o_proj(attn) (1024)
-//   GU      all       -> all                   m = silu(gate) * up (3072)
-//   DOWN    all       -> all                   h'' = h' + down(m) (1024)
-//   LMHEAD  all       -> WG 0                  (logit, index) argmax keys
+//   XCD x owns KV head x and its query heads 2x, 2x+1 (QKV rows, attention),
+//   the matching 256 input columns of o_proj, and the m slice
+//   [384x, 384x+384) (gate/up rows and the matching 384 input columns of
+//   down_proj).  o_proj and down_proj therefore produce per-XCD partial sums,
+//   which are reduced across XCDs: rank r of every XCD owns hidden rows
+//   [32r, 32r+32), sums the eight partials of those rows and applies the
+//   residual add.
 //
-// Numerics follow HF Qwen3's bf16 eager path: every op output is rounded to
-// bf16 where HF rounds it (norm outputs, projections, q/k norm, RoPE products
-// and sum, attention scores and output, residual adds, SiLU and its product,
-// logits); dot products accumulate in fp32.  One deliberate difference: the
-// softmax probabilities are not rounded to bf16 before the PV product (the
-// split-K combine rescales unnormalised partials).
+// Activations move between workgroups as tagged words (qmk_device.h).  Per
+// layer (k = exchange index inside the layer):
+//
+//   k  exchange   producers -> consumers                scope
+//   0  qkv        32 WGs of XCD x -> same 32 WGs         XCD-local
+//   1  ml         softmax (max, sum) per WG and head     XCD-local
+//   2  acc        P@V partial sums per WG and head       XCD-local
+//   3  attn       attention output of heads 2x, 2x+1     XCD-local
+//   4  o          o_proj partials, rows 32r..32r+31      across XCDs (8 -> 8)
+//   5  h2         h' = h + o_proj(attn)                  XCD-local
+//   6  m          silu(gate) * up, slice of XCD x        XCD-local
+//   7  d          down_proj partials, rows 32r..32r+31   across XCDs (8 -> 8)
+//   8  h          h'' = h' + down(m)                     XCD-local
+//
+// Numerics follow HF Qwen3's bf16 eager path, op for op: every output is
+// rounded to bf16 where HF rounds it (norm outputs, projections, q/k norm,
+// RoPE products and sum, attention scores and their scaling, softmax
+// probabilities, attention output, residual adds, SiLU and its product,
+// logits); dot products accumulate in fp32.  Attention is split over the 32
+// workgroups of an XCD in two passes so that probabilities are normalised
+// with the global max and sum before they are rounded, as HF does.
 //
 // Each workgroup has 9 waves.  Wave 0 ("control") moves activations: it polls
-// exchanges, applies norms/RoPE/residuals/SiLU, publishes results and fills
-// LDS.  Waves 1..8 ("compute") hold the current and next layer's weight
-// slices in VGPRs: each phase's weights are requested one layer before they
-// are used, so HBM streams while the control waves wait on exchanges.  The
-// control wave never has weight loads outstanding, so its polls are not
-// ordered behind them.
+// exchanges, applies norms / RoPE / residuals / SiLU, publishes results and
+// fills LDS.  Waves 1..8 ("compute") hold each phase's weight slice in VGPRs,
+// requested one layer before use, so HBM streams while the control wave
+// waits on exchanges; the control wave never has weight loads outstanding,
+// so its polls are not queued behind them.
+
+#pragma once
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -44,6 +60,11 @@ struct Qwen3_0_6B {
   static constexpr int H = 1024, I = 3072, NQ = 16, NKV = 8, D = 128, V = 151936;
 };
 
+constexpr int kMaxSeqLen = 65536;                          // longest cache the kernel accepts
+constexpr int kChunkMax = kMaxSeqLen / kGroupSize;         // attention positions per workgroup
+constexpr int kTracePoints = 13;                           // wall-clock stamps per layer
+constexpr int kMaxLayers = 28;
+
 template <class M>
 struct Dims {
   static constexpr int H = M::H, I = M::I, NQ = M::NQ, NKV = M::NKV, D = M::D, V = M::V;
@@ -53,37 +74,39 @@ struct Dims {
   static constexpr int RQ_WG = RG / kGroupSize; // QKV rows per workgroup
   static constexpr int RQ_W = RQ_WG / kComputeWaves;
   static constexpr int LH = H / 512;            // 16-byte chunks per lane for a K=H row
-  static constexpr int O_ROWS = H / kNumWG;
-  static constexpr int O_WPR = kComputeWaves / O_ROWS;   // waves per O row
-  static constexpr int LO = (QS / 512) / O_WPR;
-  static constexpr int M_WG = I / kNumWG;
+  static constexpr int OC = GQ * D;             // o_proj input columns per XCD
+  static constexpr int MS = I / kGroups;        // m slice per XCD
+  static constexpr int M_WG = MS / kGroupSize;  // m values per workgroup
   static constexpr int GU_W = 2 * M_WG / kComputeWaves;  // gate/up rows per wave
-  static constexpr int D_ROWS = H / kNumWG;
-  static constexpr int D_WPR = kComputeWaves / D_ROWS;
-  static constexpr int LD = (I / 512) / D_WPR;
+  static constexpr int ROWS_WG = H / kGroupSize;          // reduce-scatter rows per workgroup
+  static constexpr int ROWS_W = ROWS_WG / kComputeWaves;  // o/down rows per wave
+  static constexpr int LO = OC / 8 / 16;        // o_proj chunks per lane (16 lanes per row)
+  static constexpr int LD = MS / 8 / 16;        // down_proj chunks per lane
   static constexpr int LM_RPW = (V + kNumWG - 1) / kNumWG;
-  static constexpr int LM_U = 4;                         // LM-head rows per batch per wave
-  static constexpr int N_X_PER_LAYER = 6;
+  static constexpr int LM_U = 4;
+  static constexpr int NX = 9;                  // exchanges per layer
   // exchange layout (words)
-  static constexpr int PART_HEAD = 4 + 2 * D;          // m, l (2 words each) + acc
-  static constexpr int PART_WG = GQ * PART_HEAD;
-  static constexpr uint32_t X_QKV = 0;
-  static constexpr uint32_t X_PART = X_QKV + kGroups * RG;
-  static constexpr uint32_t X_ATTN = X_PART + kGroups * kGroupSize * PART_WG;
-  static constexpr uint32_t X_H2 = X_ATTN + QS;
-  static constexpr uint32_t X_M = X_H2 + H;
-  static constexpr uint32_t X_H = X_M + I;
-  static constexpr uint32_t X_KEY = X_H + H;
+  static constexpr uint32_t X_QKV = 0;                                        // [xcd][RG]
+  static constexpr uint32_t X_ML = X_QKV + kGroups * RG;                      // [xcd][rank][GQ*4]
+  static constexpr uint32_t X_ACC = X_ML + kGroups * kGroupSize * GQ * 4;     // [xcd][rank][GQ*D*2]
+  static constexpr uint32_t X_ATTN = X_ACC + kGroups * kGroupSize * GQ * D * 2;  // [xcd][OC]
+  static constexpr uint32_t X_O = X_ATTN + kGroups * OC;                      // [xcd][rank][ROWS_WG*2]
+  static constexpr uint32_t X_H2 = X_O + kGroups * kGroupSize * ROWS_WG * 2;  // [xcd][H]
+  static constexpr uint32_t X_M = X_H2 + kGroups * H;                         // [xcd][MS]
+  static constexpr uint32_t X_D = X_M + kGroups * MS;                         // [xcd][rank][ROWS_WG*2]
+  static constexpr uint32_t X_H = X_D + kGroups * kGroupSize * ROWS_WG * 2;   // [xcd][H]
+  static constexpr uint32_t X_KEY = X_H + kGroups * H;                        // [wg][4]
   static constexpr uint32_t X_WORDS = X_KEY + kNumWG * 4;
 
   static_assert(RG % kGroupSize == 0 && RQ_WG % kComputeWaves == 0, "QKV split");
-  static_assert(RQ_WG % 4 == 0 && (GQ * D) % RQ_WG == 0 && D % RQ_WG == 0, "QKV block inside one projection");
-  static_assert(H % 512 == 0 && QS % 512 == 0 && I % 512 == 0, "row chunks");
-  static_assert(O_ROWS * O_WPR == kComputeWaves && D_ROWS * D_WPR == kComputeWaves, "row split");
+  static_assert((GQ * D) % RQ_WG == 0 && D % RQ_WG == 0 && RQ_WG % 4 == 0, "QKV block inside one projection");
+  static_assert(H % 512 == 0, "K=H rows in 512-element wave loads");
+  static_assert(OC % 128 == 0 && MS % 128 == 0, "o/down slices in 16-lane row segments");
+  static_assert(ROWS_W == 4, "o/down: four rows per wave, one per 16-lane slot");
   static_assert(2 * M_WG == GU_W * kComputeWaves && M_WG % 4 == 0, "gate/up split");
-  static_assert(GQ * (D / 8) == kGroupSize, "combine: one (head, 8-dim block) per group member");
-  static_assert(H % 256 == 0 && QS % 256 == 0 && I % 256 == 0 && RG % 256 == 0, "gather granularity");
-  static_assert(O_ROWS == 4 && D_ROWS == 4, "publish of four residual rows per workgroup");
+  static_assert(GQ * (D / 8) == kGroupSize, "combine: one (head, 8-dim block) per workgroup");
+  static_assert(ROWS_WG % 16 == 0, "reduce-scatter: 16 lanes x 2 rows");
+  static_assert(X_WORDS % 4 == 0, "alignment");
 };
 
 struct LayerPtrs {  // same order as the reference's LDGLayerWeights (csrc/torch_bindings.cpp:21-33)
@@ -133,23 +156,47 @@ __device__ __forceinline__ float rcp_sqrt_torch(float v) {
   return __fdiv_rn(1.0f, __fsqrt_rn(v));
 }
 
+// A pointer read from LDS lands in VGPRs; all lanes hold the same value, so
+// move it to SGPRs for scalar address arithmetic.
+template <class T>
+__device__ __forceinline__ T* uniform_ptr(T* p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return reinterpret_cast<T*>(((uint64_t)hi << 32) | lo);
+}
+
+__device__ __forceinline__ float f32_from_words(uint32_t hi_word, uint32_t lo_word) {
+  return __uint_as_float((hi_word & 0xffff0000u) | (lo_word >> 16));
+}
+
 template <class M>
 struct Smem {
   using Dm = Dims<M>;
   float x[Dm::H];                    // layer input (residual), bf16 values
   float h2[Dm::H];                   // post-attention hidden
   uint16_t n[Dm::H];                 // normalised activation (bf16)
-  uint16_t attn[Dm::QS];
-  uint16_t m[Dm::I];
+  uint16_t attn[Dm::OC];             // attention output of this XCD's heads
+  uint16_t m[Dm::MS];                // this XCD's m slice
   float qkv[Dm::RG];
   uint16_t q[Dm::GQ * Dm::D];
   uint16_t k[Dm::D];
   uint16_t v[Dm::D];
-  float wp[kComputeWaves][Dm::GQ][Dm::D + 2];
-  uint32_t comb[kGroupSize][20];
+  float sc[Dm::GQ][kChunkMax];       // this workgroup's attention scores (bf16 values)
+  float wml[kComputeWaves][Dm::GQ][2];
+  float wacc[kComputeWaves][Dm::GQ][Dm::D];
+  float ml[Dm::GQ][2];               // global softmax max and sum per head
   float out[32];
   uint64_t best[kComputeWaves];
+  LayerPtrs layers[kMaxLayers];      // copy of the packed pointer table, read once per launch
   int abort_flag;
+};
+
+struct Step {
+  uint32_t epoch;
+  int pos, tok, step, C, nl;
+  int chunk, p_begin, p_end, n_act;  // this workgroup's attention positions
+  bool persistent;
 };
 
 // ------------------------------------------------------------- control wave
@@ -160,9 +207,8 @@ struct Ctl {
   const KArgs& a;
   Smem<M>& s;
   int lane;
-  uint32_t epoch;
 
-  __device__ Ctl(const KArgs& a_, Smem<M>& s_, int lane_, uint32_t epoch_) : a(a_), s(s_), lane(lane_), epoch(epoch_) {}
+  __device__ Ctl(const KArgs& a_, Smem<M>& s_, int lane_) : a(a_), s(s_), lane(lane_) {}
 
   __device__ void fail(uint32_t bits) {
     atomicOr(&a.st->err, bits);
@@ -170,44 +216,105 @@ struct Ctl {
     s.abort_flag = 1;
   }
 
-  // Wait until the NW words at ``buf`` all carry ``tag``; hand each 16-byte
-  // chunk (chunk index, 4 words) to ``sink``.
-  template <int NW, class F>
-  __device__ bool gather(const uint32_t* buf, uint32_t tag, F&& sink) {
-    constexpr int NC = NW / 256;
-    static_assert(NW % 256 == 0 && NC <= 32, "gather size");
-    auto rs = make_rsrc(buf, NW * 4);
-    u32x4 v[NC];
-    uint32_t pend = NC == 32 ? 0xffffffffu : ((1u << NC) - 1u);
+  // Waits until the NCH 16-byte chunks named by off(i) (word offsets into the
+  // exchange area, i < NCH) all carry ``tag``; calls sink(i, chunk) once per
+  // chunk as it arrives.  Two poll rounds are kept in flight so a chunk that
+  // lands while one round is out is seen by the next half a round trip later.
+  template <int NCH, class Off, class F>
+  __device__ bool gather(uint32_t tag, Off&& off, F&& sink) {
+    constexpr int NC = (NCH + 63) / 64;
+    static_assert(NC <= 16, "gather size");
+    auto rs = make_rsrc(a.x, 0x7fffffffu);
+    uint32_t o[NC];
+    uint32_t pend = 0;
+#pragma unroll
+    for (int j = 0; j < NC; j++) {
+      const int i = j * 64 + lane;
+      o[j] = i < NCH ? off(i) * 4u : 0u;
+      if (i < NCH) pend |= 1u << j;
+    }
+    // Every round issues all NC loads so the wait for the older round is a
+    // static vmcnt(NC); chunks already received are pointed past the end of the
+    // buffer descriptor, which makes their loads return 0 without memory traffic.
+    constexpr uint32_t kOOB = 0xfffffff0u;
+    u32x4 va[NC], vb[NC];
+#pragma unroll
+    for (int j = 0; j < NC; j++) va[j] = poll16(rs, (pend & (1u << j)) ? o[j] : kOOB);
     const uint64_t t0 = wall_clock64();
     while (true) {
 #pragma unroll
-      for (int j = 0; j < NC; j++)
-        if (pend & (1u << j)) v[j] = poll16(rs, (uint32_t)(j * 64 + lane) * 16u);
+      for (int j = 0; j < NC; j++) vb[j] = poll16(rs, (pend & (1u << j)) ? o[j] : kOOB);
 #pragma unroll
       for (int j = 0; j < NC; j++)
-        if ((pend & (1u << j)) && chunk_ok(v[j], tag)) pend &= ~(1u << j);
+        if ((pend & (1u << j)) && chunk_ok(va[j], tag)) {
+          sink(j * 64 + lane, va[j]);
+          pend &= ~(1u << j);
+        }
       if (!__any(pend != 0)) break;
-      if (wall_clock64() - t0 > a.timeout) { fail(kErrTimeout); return false; }
-    }
 #pragma unroll
-    for (int j = 0; j < NC; j++) sink(j * 64 + lane, v[j]);
+      for (int j = 0; j < NC; j++) va[j] = poll16(rs, (pend & (1u << j)) ? o[j] : kOOB);
+#pragma unroll
+      for (int j = 0; j < NC; j++)
+        if ((pend & (1u << j)) && chunk_ok(vb[j], tag)) {
+          sink(j * 64 + lane, vb[j]);
+          pend &= ~(1u << j);
+        }
+      if (!__any(pend != 0)) break;
+      if (wall_clock64() - t0 > a.timeout) {
+        fail(kErrTimeout);
+        return false;
+      }
+    }
     return true;
   }
 
-  template <bool DEVICE>
-  __device__ void publish4(uint32_t w, float v0, float v1, float v2, float v3, uint32_t tag) {
+  // Contiguous NW words at word offset ``base``.
+  template <int NW, class F>
+  __device__ bool gather_range(uint32_t base, uint32_t tag, F&& sink) {
+    static_assert(NW % 4 == 0, "whole chunks");
+    return gather<NW / 4>(tag, [&](int i) { return base + 4u * (uint32_t)i; }, sink);
+  }
+
+  __device__ void put(bool local, uint32_t w, u32x4 d) {
+    if (local && a.xcd_local) put4<false>(a.x, w, d);
+    else put4<true>(a.x, w, d);
+  }
+
+  __device__ void put_bf16x4(bool local, uint32_t w, float v0, float v1, float v2, float v3, uint32_t tag) {
     u32x4 d;
     d.x = word(f32_to_bf16(v0), tag);
     d.y = word(f32_to_bf16(v1), tag);
     d.z = word(f32_to_bf16(v2), tag);
     d.w = word(f32_to_bf16(v3), tag);
-    put4<DEVICE>(a.x, w, d);
+    put(local, w, d);
+  }
+
+  __device__ void put_f32x2(bool local, uint32_t w, float v0, float v1, uint32_t tag) {
+    const uint32_t b0 = __float_as_uint(v0), b1 = __float_as_uint(v1);
+    u32x4 d;
+    d.x = (b0 & 0xffff0000u) | tag;
+    d.y = (b0 << 16) | tag;
+    d.z = (b1 & 0xffff0000u) | tag;
+    d.w = (b1 << 16) | tag;
+    put(local, w, d);
+  }
+
+  // Norm weights are requested before the control wave starts polling, so
+  // their latency overlaps the wait instead of following it.
+  struct NormW {
+    uint32_t w[Dm::H / 128];  // bf16 pairs lane + 64*i
+  };
+  __device__ NormW load_norm(const uint16_t* w) {
+    NormW r;
+    const uint32_t* w2 = reinterpret_cast<const uint32_t*>(w);
+#pragma unroll
+    for (int i = 0; i < Dm::H / 128; i++) r.w[i] = w2[lane + 64 * i];
+    return r;
   }
 
   // RMSNorm of ``src`` (fp32 holding bf16 values) with bf16 weight -> s.n:
   // bf16(w * bf16(x * rsqrt(mean(x^2) + eps)))  (HF Qwen3RMSNorm).
-  __device__ void rmsnorm(const float* src, const uint16_t* w) {
+  __device__ void rmsnorm(const float* src, const NormW& nw) {
     constexpr int P = Dm::H / 128;  // element pairs per lane
     float2 xv[P];
     float ss = 0.f;
@@ -218,32 +325,96 @@ struct Ctl {
     }
     ss = wave_sum(ss);
     const float rstd = rcp_sqrt_torch(__fdiv_rn(ss, (float)Dm::H) + a.rms_eps);
-    const uint32_t* w2 = reinterpret_cast<const uint32_t*>(w);
 #pragma unroll
     for (int i = 0; i < P; i++) {
       const int pi = lane + 64 * i;
-      const uint32_t wp = w2[pi];
+      const uint32_t wp = nw.w[i];
       const float n0 = bf16r(lo_bf16(wp) * bf16r(xv[i].x * rstd));
       const float n1 = bf16r(hi_bf16(wp) * bf16r(xv[i].y * rstd));
       reinterpret_cast<uint32_t*>(s.n)[pi] = f32_to_bf16(n0) | (f32_to_bf16(n1) << 16);
     }
   }
 
+  // Per-head RMSNorm weight and RoPE row values for elements lane, lane + 64.
+  struct HeadW {
+    float w0, w1, c0, c1, s0, s1;
+  };
+  __device__ HeadW load_head(const uint16_t* w, const uint16_t* cosr, const uint16_t* sinr) {
+    HeadW h;
+    h.w0 = bf16_to_f32(w[lane]);
+    h.w1 = bf16_to_f32(w[lane + 64]);
+    h.c0 = bf16_to_f32(cosr[lane]);
+    h.c1 = bf16_to_f32(cosr[lane + 64]);
+    h.s0 = bf16_to_f32(sinr[lane]);
+    h.s1 = bf16_to_f32(sinr[lane + 64]);
+    return h;
+  }
+
   // Per-head RMSNorm + rotate-half RoPE of one 128-wide head held in s.qkv.
-  __device__ void head_norm_rope(int src_off, const uint16_t* w, const uint16_t* cosr, const uint16_t* sinr,
-                                 uint16_t* dst) {
+  __device__ void head_norm_rope(int src_off, const HeadW& hw, uint16_t* dst) {
     const float x0 = s.qkv[src_off + lane], x1 = s.qkv[src_off + lane + 64];
     const float ss = wave_sum(x0 * x0 + x1 * x1);
     const float rstd = rcp_sqrt_torch(__fdiv_rn(ss, (float)Dm::D) + a.rms_eps);
-    const float n0 = bf16r(bf16_to_f32(w[lane]) * bf16r(x0 * rstd));
-    const float n1 = bf16r(bf16_to_f32(w[lane + 64]) * bf16r(x1 * rstd));
-    const float c0 = bf16_to_f32(cosr[lane]), c1 = bf16_to_f32(cosr[lane + 64]);
-    const float s0 = bf16_to_f32(sinr[lane]), s1 = bf16_to_f32(sinr[lane + 64]);
-    // q*cos + rotate_half(q)*sin with rotate_half(q) = (-q[64:], q[:64])
-    const float y0 = bf16r(bf16r(n0 * c0) + bf16r(-n1 * s0));
-    const float y1 = bf16r(bf16r(n1 * c1) + bf16r(n0 * s1));
+    const float n0 = bf16r(hw.w0 * bf16r(x0 * rstd));
+    const float n1 = bf16r(hw.w1 * bf16r(x1 * rstd));
+    // x*cos + rotate_half(x)*sin with rotate_half(x) = (-x[64:], x[:64])
+    const float y0 = bf16r(bf16r(n0 * hw.c0) + bf16r(-n1 * hw.s0));
+    const float y1 = bf16r(bf16r(n1 * hw.c1) + bf16r(n0 * hw.s1));
     dst[lane] = (uint16_t)f32_to_bf16(y0);
     dst[lane + 64] = (uint16_t)f32_to_bf16(y1);
+  }
+
+  // Reduce-scatter across XCDs: sums the eight XCD partials of this rank's
+  // ROWS_WG hidden rows (fixed order), adds the residual ``res`` and rounds
+  // like HF: bf16(res + bf16(sum)).  Publishes the rows into this XCD's copy
+  // of ``x_dst``.  Returns false on timeout.
+  __device__ bool reduce_rows(uint32_t x_src, uint32_t src_tag, const float* res, uint32_t x_dst, uint32_t dst_tag,
+                              int xcd, int r) {
+    constexpr int R = Dm::ROWS_WG;       // 32 rows, 2 per chunk -> 16 chunks per source XCD
+    constexpr int CPX = R / 2;
+    float sum0 = 0.f, sum1 = 0.f;
+    // chunk i: source XCD i / CPX, rows 2*(i % CPX) .. +1
+    float part0[2], part1[2];
+    const bool ok = gather<kGroups * CPX>(
+        src_tag, [&](int i) { return x_src + (uint32_t)(((i / CPX) * kGroupSize + r) * R * 2 + (i % CPX) * 4); },
+        [&](int i, u32x4 v) {
+          // each lane holds chunks i = lane and lane + 64: sources lane/16 and lane/16 + 4
+          const int slot = i / 64;
+          part0[slot] = f32_from_words(v.x, v.y);
+          part1[slot] = f32_from_words(v.z, v.w);
+        });
+    if (!ok) return false;
+    // lane l: rows 2*(l%16), +1 from sources l/16 (slot 0) and l/16+4 (slot 1);
+    // sum sources in order 0..7 by gathering them into every lane of the row
+    float p0[kGroups], p1[kGroups];
+#pragma unroll
+    for (int src = 0; src < kGroups; src++) {
+      const int from = (src % 4) * 16 + (lane & 15);
+      p0[src] = __shfl(src < 4 ? part0[0] : part0[1], from);
+      p1[src] = __shfl(src < 4 ? part1[0] : part1[1], from);
+    }
+#pragma unroll
+    for (int src = 0; src < kGroups; src++) {
+      sum0 += p0[src];
+      sum1 += p1[src];
+    }
+    if (lane < CPX) {
+      const int row = R * r + 2 * lane;
+      const float h0 = bf16r(res[row] + bf16r(sum0));
+      const float h1 = bf16r(res[row + 1] + bf16r(sum1));
+      const uint32_t hb0 = f32_to_bf16(h0), hb1 = f32_to_bf16(h1);
+      // two words per lane: pairs of lanes form one 16-byte store
+      const uint32_t ob0 = __shfl_xor(hb0, 1), ob1 = __shfl_xor(hb1, 1);
+      if ((lane & 1) == 0) {
+        u32x4 d;
+        d.x = word(hb0, dst_tag);
+        d.y = word(hb1, dst_tag);
+        d.z = word(ob0, dst_tag);
+        d.w = word(ob1, dst_tag);
+        put(true, x_dst + (uint32_t)(xcd * Dm::H + row), d);
+      }
+    }
+    return true;
   }
 };
 
@@ -269,6 +440,22 @@ __device__ __forceinline__ float row_dot(const u32x4 (&w)[NL], const u32x4 (&x)[
   return wave_sum(acc);
 }
 
+// Four rows per wave, one per 16-lane slot: lane (slot, t) reads chunks
+// t, t+16, .. of its row's NL*16-chunk segment.
+template <int NL>
+__device__ __forceinline__ void load_seg(u32x4 (&dst)[NL], const uint16_t* row_seg, int t16) {
+#pragma unroll
+  for (int j = 0; j < NL; j++) dst[j] = ld_stream(row_seg + 8 * (t16 + 16 * j));
+}
+
+template <int NL>
+__device__ __forceinline__ float seg_dot(const u32x4 (&w)[NL], const uint16_t* act, int t16) {
+  float acc = 0.f;
+#pragma unroll
+  for (int j = 0; j < NL; j++) acc = dot8(w[j], *reinterpret_cast<const u32x4*>(act + 8 * (t16 + 16 * j)), acc);
+  return row16_sum(acc);
+}
+
 template <class M>
 __device__ __forceinline__ const uint16_t* qkv_row(const LayerPtrs& w, int g, int vr) {
   using Dm = Dims<M>;
@@ -287,30 +474,21 @@ __device__ __forceinline__ uint32_t orderable16(uint32_t h) { return (h & 0x8000
 // has its own loop so that the compute waves' weight registers and the
 // control wave's poll buffers never share live ranges):
 //
-//   per layer   control wave                        compute waves
-//   a           h (or embedding row) -> norm         .
-//   a..b        .                                    QKV rows
-//   b..c        publish qkv, gather qkv, qk-norm,    .
-//               RoPE, KV-cache append
-//   c..d        .                                    split-K attention
-//   d..e        publish partial, combine, gather o   .
-//   e..f        .                                    O rows
-//   f..g        publish h', gather h', norm          .
-//   g..h        .                                    gate/up rows
-//   h..i        publish m, gather m                  .
-//   i..j        .                                    down rows
-//   j..a'       publish h''                          .
-//   k           gather h, final norm                 .
-//   k..l        .                                    LM-head rows
-//   l..         argmax keys, WG 0 picks the token    .
-
-constexpr int kTracePoints = 13;  // wall-clock stamps per layer (see the schedule above)
-
-struct Step {
-  uint32_t epoch;
-  int pos, tok, step, C, nl;
-  bool persistent;
-};
+//   per layer   control wave                          compute waves
+//   ..a         h (or embedding row) -> RMSNorm        .
+//   a..b        .                                      QKV rows; K prefetch
+//   b..c        qkv exchange, q/k norm, RoPE, KV write .
+//   c..d        .                                      scores, local (max, sum)
+//   d..e        (max, sum) exchange -> global max/sum  .
+//   e..f        .                                      probabilities, P@V
+//   f..g        acc exchange, combine, attn exchange   .
+//   g..h        .                                      o_proj partial rows
+//   h..i        o reduce-scatter, h' exchange, norm    .
+//   i..j        .                                      gate/up rows
+//   j..k        m exchange                             .
+//   k..l        .                                      down_proj partial rows
+//   l..a'       d reduce-scatter, h'' publish          .
+//   final       gather h, final norm | LM-head rows | argmax keys, WG 0 picks the token
 
 #define QMK_SYNC()            \
   do {                        \
@@ -321,9 +499,12 @@ struct Step {
 template <class M>
 __device__ __forceinline__ void control_path(const KArgs& a, Smem<M>& s, const Step& p, int b, int lane) {
   using Dm = Dims<M>;
-  const int g = b & (kGroups - 1), r = b >> 3;
-  Ctl<M> ctl(a, s, lane, p.epoch);
-  auto tag_of = [&](int layer, int k) { return make_tag(p.epoch, (uint32_t)(layer * Dm::N_X_PER_LAYER + k)); };
+  const int xcd = b & (kGroups - 1), r = b >> 3;
+  Ctl<M> ctl(a, s, lane);
+  auto tag_of = [&](int layer, int k) { return make_tag(p.epoch, (uint32_t)(layer * Dm::NX + k)); };
+  auto stamp = [&](int point) {
+    if (a.trace && lane == 0) a.trace[(size_t)point * kNumWG + b] = wall_clock64();
+  };
   const size_t kv_layer_stride = (size_t)Dm::NKV * a.max_seq_len * Dm::D;
   auto to_f32 = [&](float* dst) {
     return [dst](int ci, u32x4 v) {
@@ -340,14 +521,12 @@ __device__ __forceinline__ void control_path(const KArgs& a, Smem<M>& s, const S
     };
   };
 
-  auto stamp = [&](int point) {
-    if (a.trace && lane == 0) a.trace[(size_t)point * kNumWG + b] = wall_clock64();
-  };
   for (int L = 0; L < p.nl; L++) {
-    const LayerPtrs& w = a.layers[L];
+    const LayerPtrs& w = s.layers[L];
     const int tp = L * kTracePoints;
     stamp(tp + 0);
-    // ---------------------------------------------------------------- a
+    // ------------------------------------------------------------ ..a
+    const auto nw_in = ctl.load_norm(w.in_ln);
     if (L == 0) {
       const uint16_t* e = a.embed + (size_t)p.tok * Dm::H;
 #pragma unroll
@@ -357,33 +536,34 @@ __device__ __forceinline__ void control_path(const KArgs& a, Smem<M>& s, const S
         d[0] = lo_bf16(v.x); d[1] = hi_bf16(v.x); d[2] = lo_bf16(v.y); d[3] = hi_bf16(v.y);
         d[4] = lo_bf16(v.z); d[5] = hi_bf16(v.z); d[6] = lo_bf16(v.w); d[7] = hi_bf16(v.w);
       }
-      ctl.rmsnorm(s.x, w.in_ln);
-    } else if (ctl.template gather<Dm::H>(a.x + Dm::X_H, tag_of(L - 1, 5), to_f32(s.x))) {
-      ctl.rmsnorm(s.x, w.in_ln);
+      ctl.rmsnorm(s.x, nw_in);
+    } else if (ctl.template gather_range<Dm::H>(Dm::X_H + xcd * Dm::H, tag_of(L - 1, 8), to_f32(s.x))) {
+      ctl.rmsnorm(s.x, nw_in);
     }
     stamp(tp + 1);
     QMK_SYNC();  // a
     QMK_SYNC();  // b
     stamp(tp + 2);
+    // ------------------------------------------------------------ b..c  qkv
     {
       const uint32_t t = tag_of(L, 0);
+      const uint16_t* cosr = a.cos_t + (size_t)p.pos * Dm::D;
+      const uint16_t* sinr = a.sin_t + (size_t)p.pos * Dm::D;
+      const auto hq = ctl.load_head(w.q_norm, cosr, sinr);
+      const auto hk = ctl.load_head(w.k_norm, cosr, sinr);
       if (lane < Dm::RQ_WG / 4) {
         const float* o = s.out + 4 * lane;
-        const uint32_t wi = Dm::X_QKV + g * Dm::RG + Dm::RQ_WG * r + 4 * lane;
-        if (a.xcd_local) ctl.template publish4<false>(wi, o[0], o[1], o[2], o[3], t);
-        else ctl.template publish4<true>(wi, o[0], o[1], o[2], o[3], t);
+        ctl.put_bf16x4(true, Dm::X_QKV + xcd * Dm::RG + Dm::RQ_WG * r + 4 * lane, o[0], o[1], o[2], o[3], t);
       }
-      if (ctl.template gather<Dm::RG>(a.x + Dm::X_QKV + g * Dm::RG, t, to_f32(s.qkv))) {
-        const uint16_t* cosr = a.cos_t + (size_t)p.pos * Dm::D;
-        const uint16_t* sinr = a.sin_t + (size_t)p.pos * Dm::D;
+      if (ctl.template gather_range<Dm::RG>(Dm::X_QKV + xcd * Dm::RG, t, to_f32(s.qkv))) {
 #pragma unroll
-        for (int h = 0; h < Dm::GQ; h++) ctl.head_norm_rope(h * Dm::D, w.q_norm, cosr, sinr, s.q + h * Dm::D);
-        ctl.head_norm_rope(Dm::GQ * Dm::D, w.k_norm, cosr, sinr, s.k);
+        for (int h = 0; h < Dm::GQ; h++) ctl.head_norm_rope(h * Dm::D, hq, s.q + h * Dm::D);
+        ctl.head_norm_rope(Dm::GQ * Dm::D, hk, s.k);
         const float v0 = s.qkv[(Dm::GQ + 1) * Dm::D + lane], v1 = s.qkv[(Dm::GQ + 1) * Dm::D + lane + 64];
         s.v[lane] = (uint16_t)f32_to_bf16(v0);
         s.v[lane + 64] = (uint16_t)f32_to_bf16(v1);
         if (r == 0) {
-          const size_t o = L * kv_layer_stride + ((size_t)g * a.max_seq_len + p.pos) * Dm::D;
+          const size_t o = L * kv_layer_stride + ((size_t)xcd * a.max_seq_len + p.pos) * Dm::D;
           a.k_cache[o + lane] = s.k[lane];
           a.k_cache[o + lane + 64] = s.k[lane + 64];
           a.v_cache[o + lane] = (uint16_t)f32_to_bf16(v0);
@@ -395,152 +575,146 @@ __device__ __forceinline__ void control_path(const KArgs& a, Smem<M>& s, const S
     QMK_SYNC();  // c
     QMK_SYNC();  // d
     stamp(tp + 4);
+    // ------------------------------------------------------------ d..e  softmax max and sum
     {
-      // workgroup partial = merge of the eight wave partials, then publish
       const uint32_t t = tag_of(L, 1);
+      // lanes 0..GQ-1: merge the eight wave (max, sum) pairs of head h = lane
+      float mx = -INFINITY, sm = 0.f;
+      if (lane < Dm::GQ) {
+#pragma unroll
+        for (int c = 0; c < kComputeWaves; c++) mx = fmaxf(mx, s.wml[c][lane][0]);
+#pragma unroll
+        for (int c = 0; c < kComputeWaves; c++) {
+          const float mc = s.wml[c][lane][0];
+          sm += mc == -INFINITY ? 0.f : s.wml[c][lane][1] * exp_acc(mc - mx);
+        }
+      }
+      if (lane < Dm::GQ) ctl.put_f32x2(true, Dm::X_ML + (xcd * kGroupSize + r) * Dm::GQ * 4 + 4 * lane, mx, sm, t);
+      // gather every active workgroup's pairs: chunk i = (rank i / GQ, head i % GQ)
+      float pm[2] = {-INFINITY, -INFINITY}, pl[2] = {0.f, 0.f};
+      const bool ok = ctl.template gather<kGroupSize * Dm::GQ>(
+          t, [&](int i) { return Dm::X_ML + (uint32_t)((xcd * kGroupSize + i / Dm::GQ) * Dm::GQ * 4 + 4 * (i % Dm::GQ)); },
+          [&](int i, u32x4 v) {
+            pm[i / 64] = f32_from_words(v.x, v.y);
+            pl[i / 64] = f32_from_words(v.z, v.w);
+          });
+      if (ok) {
+        // lane l holds chunks l and l+64 (64 chunks: only the first): head = l % GQ
+        static_assert(kGroupSize * Dm::GQ <= 64, "one chunk per lane");
+        const int h = lane % Dm::GQ;
+        const bool act = (lane / Dm::GQ) < p.n_act;
+        float m0 = act ? pm[0] : -INFINITY;
+        float gm = m0;
+        for (int o = Dm::GQ; o < 64; o <<= 1) gm = fmaxf(gm, __shfl_xor(gm, o));
+        float lsum = (act && m0 != -INFINITY) ? pl[0] * exp_acc(m0 - gm) : 0.f;
+        for (int o = Dm::GQ; o < 64; o <<= 1) lsum += __shfl_xor(lsum, o);
+        if (lane < Dm::GQ) {
+          s.ml[h][0] = gm;
+          s.ml[h][1] = lsum;
+        }
+      }
+    }
+    stamp(tp + 5);
+    QMK_SYNC();  // e
+    QMK_SYNC();  // f
+    stamp(tp + 6);
+    // ------------------------------------------------------------ f..g  P@V partials, combine, attn
+    {
+      const uint32_t t = tag_of(L, 2);
+      // this workgroup's P@V partial: lane holds dims 2*lane, 2*lane+1 of each head
 #pragma unroll
       for (int h = 0; h < Dm::GQ; h++) {
-        float mw[kComputeWaves];
-        float mx = -INFINITY;
+        float a0 = 0.f, a1 = 0.f;
 #pragma unroll
-        for (int cc = 0; cc < kComputeWaves; cc++) { mw[cc] = s.wp[cc][h][0]; mx = fmaxf(mx, mw[cc]); }
-        float lsum = 0.f, a0 = 0.f, a1 = 0.f;
-#pragma unroll
-        for (int cc = 0; cc < kComputeWaves; cc++) {
-          const float f = mw[cc] == -INFINITY ? 0.f : __expf(mw[cc] - mx);
-          lsum += s.wp[cc][h][1] * f;
-          a0 += s.wp[cc][h][2 + 2 * lane] * f;
-          a1 += s.wp[cc][h][3 + 2 * lane] * f;
+        for (int c = 0; c < kComputeWaves; c++) {
+          a0 += s.wacc[c][h][2 * lane];
+          a1 += s.wacc[c][h][2 * lane + 1];
         }
-        const uint32_t base = Dm::X_PART + (uint32_t)((g * kGroupSize + r) * Dm::PART_WG + h * Dm::PART_HEAD);
-        u32x4 d;
-        const uint32_t ba0 = __float_as_uint(a0), ba1 = __float_as_uint(a1);
-        d.x = word(ba0 >> 16, t); d.y = word(ba0 & 0xffffu, t); d.z = word(ba1 >> 16, t); d.w = word(ba1 & 0xffffu, t);
-        if (a.xcd_local) put4<false>(a.x, base + 4 + 4 * lane, d); else put4<true>(a.x, base + 4 + 4 * lane, d);
-        if (lane == 0) {
-          const uint32_t bm = __float_as_uint(mx), bl = __float_as_uint(lsum);
-          d.x = word(bm >> 16, t); d.y = word(bm & 0xffffu, t); d.z = word(bl >> 16, t); d.w = word(bl & 0xffffu, t);
-          if (a.xcd_local) put4<false>(a.x, base, d); else put4<true>(a.x, base, d);
-        }
+        ctl.put_f32x2(true, Dm::X_ACC + (uint32_t)((xcd * kGroupSize + r) * Dm::GQ * Dm::D * 2 + h * Dm::D * 2 + 4 * lane),
+                      a0, a1, t);
       }
-      stamp(tp + 5);
-      // combine: this workgroup owns (head hh, dims 8kb..8kb+7) of its group
+      // combine: this workgroup owns head hh, dims 8kb..8kb+7.  Chunk i = (rank i/4,
+      // dims 8kb+2(i%4), +1); lane l receives chunks l and l+64 (ranks l/4 and l/4+16).
       const int hh = r / (Dm::D / 8), kb = r % (Dm::D / 8);
-      const uint32_t pbase = Dm::X_PART + (uint32_t)(g * kGroupSize * Dm::PART_WG + hh * Dm::PART_HEAD);
-      auto rs = make_rsrc(a.x, 0x7fffffffu);
-      constexpr int NCH = kGroupSize * 5;  // (m,l) chunk + four acc chunks per partial
-      constexpr int PER = (NCH + 63) / 64;
-      u32x4 v[PER];
-      uint32_t off[PER];
-      uint32_t pend = 0;
+      static_assert(kGroupSize * 4 == 128, "two chunks per lane");
+      float v0[2] = {0.f, 0.f}, v1[2] = {0.f, 0.f};
+      const bool ok2 = ctl.template gather<kGroupSize * 4>(
+          t,
+          [&](int i) {
+            return Dm::X_ACC + (uint32_t)((xcd * kGroupSize + i / 4) * Dm::GQ * Dm::D * 2 + hh * Dm::D * 2 +
+                                          (8 * kb + 2 * (i % 4)) * 2);
+          },
+          [&](int i, u32x4 v) {
+            const bool act = (i / 4) < p.n_act;
+            v0[i / 64] = act ? f32_from_words(v.x, v.y) : 0.f;
+            v1[i / 64] = act ? f32_from_words(v.z, v.w) : 0.f;
+          });
+      if (ok2) {
+        float s0 = v0[0] + v0[1], s1 = v1[0] + v1[1];  // ranks l/4 and l/4 + 16
 #pragma unroll
-      for (int i = 0; i < PER; i++) {
-        const int ci = lane + 64 * i;
-        const int j = ci / 5, q = ci % 5;
-        off[i] = pbase + (uint32_t)(j * Dm::PART_WG) + (q == 0 ? 0u : (uint32_t)(4 + 16 * kb + 4 * (q - 1)));
-        if (ci < NCH) pend |= 1u << i;
-      }
-      const uint64_t t0 = wall_clock64();
-      bool ok = true;
-      while (true) {
-#pragma unroll
-        for (int i = 0; i < PER; i++)
-          if (pend & (1u << i)) v[i] = poll16(rs, off[i] * 4u);
-#pragma unroll
-        for (int i = 0; i < PER; i++)
-          if ((pend & (1u << i)) && chunk_ok(v[i], t)) pend &= ~(1u << i);
-        if (!__any(pend != 0)) break;
-        if (wall_clock64() - t0 > a.timeout) { ctl.fail(kErrTimeout); ok = false; break; }
-      }
-      stamp(tp + 6);
-      if (ok) {
-#pragma unroll
-        for (int i = 0; i < PER; i++) {
-          const int ci = lane + 64 * i;
-          if (ci < NCH) {
-            const int j = ci / 5, q = ci % 5;
-            s.comb[j][4 * q + 0] = v[i].x >> 16;
-            s.comb[j][4 * q + 1] = v[i].y >> 16;
-            s.comb[j][4 * q + 2] = v[i].z >> 16;
-            s.comb[j][4 * q + 3] = v[i].w >> 16;
-          }
+        for (int o = 4; o < 64; o <<= 1) {
+          s0 += __shfl_xor(s0, o);
+          s1 += __shfl_xor(s1, o);
         }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        if (lane < 2) {
-          float mx = -INFINITY;
-          for (int j = 0; j < kGroupSize; j++) mx = fmaxf(mx, __uint_as_float((s.comb[j][0] << 16) | s.comb[j][1]));
-          float lsum = 0.f, o[4] = {0.f, 0.f, 0.f, 0.f};
-          for (int j = 0; j < kGroupSize; j++) {
-            const float mj = __uint_as_float((s.comb[j][0] << 16) | s.comb[j][1]);
-            const float f = mj == -INFINITY ? 0.f : __expf(mj - mx);
-            lsum += __uint_as_float((s.comb[j][2] << 16) | s.comb[j][3]) * f;
-#pragma unroll
-            for (int d = 0; d < 4; d++) {
-              const int dd = 4 * lane + d;
-              o[d] += __uint_as_float((s.comb[j][4 + 2 * dd] << 16) | s.comb[j][5 + 2 * dd]) * f;
-            }
-          }
-          const uint32_t wi = Dm::X_ATTN + (uint32_t)((g * Dm::GQ + hh) * Dm::D + 8 * kb + 4 * lane);
-          ctl.template publish4<true>(wi, __fdiv_rn(o[0], lsum), __fdiv_rn(o[1], lsum), __fdiv_rn(o[2], lsum),
-                                      __fdiv_rn(o[3], lsum), tag_of(L, 2));
-        }
-        ctl.template gather<Dm::QS>(a.x + Dm::X_ATTN, tag_of(L, 2), to_bf16(s.attn));
+        // lanes with equal l%4 now hold the sum over all ranks of dims 8kb+2(l%4), +1;
+        // lanes 0 and 1 publish dims 8kb..8kb+3 and 8kb+4..8kb+7
+        const float d2 = __shfl(s0, (lane & 1) * 2 + 0), d3 = __shfl(s1, (lane & 1) * 2 + 0);
+        const float d4 = __shfl(s0, (lane & 1) * 2 + 1), d5 = __shfl(s1, (lane & 1) * 2 + 1);
+        if (lane < 2)
+          ctl.put_bf16x4(true, Dm::X_ATTN + (uint32_t)(xcd * Dm::OC + hh * Dm::D + 8 * kb + 4 * lane), d2, d3, d4, d5,
+                         tag_of(L, 3));
+        ctl.template gather_range<Dm::OC>(Dm::X_ATTN + xcd * Dm::OC, tag_of(L, 3), to_bf16(s.attn));
       }
     }
     stamp(tp + 7);
-    QMK_SYNC();  // e
-    QMK_SYNC();  // f
-    stamp(tp + 8);
-    if (lane == 0) {
-      float hv[4];
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        float o = 0.f;
-#pragma unroll
-        for (int q = 0; q < Dm::O_WPR; q++) o += s.out[i * Dm::O_WPR + q];
-        hv[i] = bf16r(s.x[Dm::O_ROWS * b + i] + bf16r(o));
-      }
-      ctl.template publish4<true>(Dm::X_H2 + Dm::O_ROWS * b, hv[0], hv[1], hv[2], hv[3], tag_of(L, 3));
-    }
-    if (ctl.template gather<Dm::H>(a.x + Dm::X_H2, tag_of(L, 3), to_f32(s.h2))) ctl.rmsnorm(s.h2, w.post_ln);
-    stamp(tp + 9);
     QMK_SYNC();  // g
     QMK_SYNC();  // h
-    stamp(tp + 10);
-    if (lane < Dm::M_WG / 4) {
-      float mv[4];
-#pragma unroll
-      for (int q = 0; q < 4; q++) {
-        const float gt = s.out[4 * lane + q];
-        const float up = s.out[Dm::M_WG + 4 * lane + q];
-        const float sg = bf16r(__fdiv_rn(gt, 1.0f + expf(-gt)));
-        mv[q] = bf16r(sg * up);
-      }
-      ctl.template publish4<true>(Dm::X_M + Dm::M_WG * b + 4 * lane, mv[0], mv[1], mv[2], mv[3], tag_of(L, 4));
+    stamp(tp + 8);
+    // ------------------------------------------------------------ h..i  o reduce-scatter, h', norm
+    {
+      const auto nw_post = ctl.load_norm(w.post_ln);
+      if (lane < Dm::ROWS_WG / 2)
+        ctl.put_f32x2(false, Dm::X_O + (uint32_t)((xcd * kGroupSize + r) * Dm::ROWS_WG * 2 + 4 * lane),
+                      s.out[2 * lane], s.out[2 * lane + 1], tag_of(L, 4));
+      if (ctl.reduce_rows(Dm::X_O, tag_of(L, 4), s.x, Dm::X_H2, tag_of(L, 5), xcd, r) &&
+          ctl.template gather_range<Dm::H>(Dm::X_H2 + xcd * Dm::H, tag_of(L, 5), to_f32(s.h2)))
+        ctl.rmsnorm(s.h2, nw_post);
     }
-    ctl.template gather<Dm::I>(a.x + Dm::X_M, tag_of(L, 4), to_bf16(s.m));
-    stamp(tp + 11);
+    stamp(tp + 9);
     QMK_SYNC();  // i
     QMK_SYNC();  // j
-    stamp(tp + 12);
-    if (lane == 0) {
-      float hv[4];
+    stamp(tp + 10);
+    // ------------------------------------------------------------ j..k  m
+    {
+      if (lane < Dm::M_WG / 4) {
+        float mv[4];
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        float d = 0.f;
-#pragma unroll
-        for (int q = 0; q < Dm::D_WPR; q++) d += s.out[i * Dm::D_WPR + q];
-        hv[i] = bf16r(s.h2[Dm::D_ROWS * b + i] + bf16r(d));
+        for (int q = 0; q < 4; q++) {
+          const float gt = s.out[4 * lane + q];
+          const float up = s.out[Dm::M_WG + 4 * lane + q];
+          const float sg = bf16r(__fdiv_rn(gt, 1.0f + expf(-gt)));
+          mv[q] = bf16r(sg * up);
+        }
+        ctl.put_bf16x4(true, Dm::X_M + (uint32_t)(xcd * Dm::MS + Dm::M_WG * r + 4 * lane), mv[0], mv[1], mv[2], mv[3],
+                       tag_of(L, 6));
       }
-      ctl.template publish4<true>(Dm::X_H + Dm::D_ROWS * b, hv[0], hv[1], hv[2], hv[3], tag_of(L, 5));
+      ctl.template gather_range<Dm::MS>(Dm::X_M + xcd * Dm::MS, tag_of(L, 6), to_bf16(s.m));
     }
+    stamp(tp + 11);
+    QMK_SYNC();  // k
+    QMK_SYNC();  // l
+    stamp(tp + 12);
+    // ------------------------------------------------------------ l..a'  d reduce-scatter, h''
+    if (lane < Dm::ROWS_WG / 2)
+      ctl.put_f32x2(false, Dm::X_D + (uint32_t)((xcd * kGroupSize + r) * Dm::ROWS_WG * 2 + 4 * lane),
+                    s.out[2 * lane], s.out[2 * lane + 1], tag_of(L, 7));
+    ctl.reduce_rows(Dm::X_D, tag_of(L, 7), s.h2, Dm::X_H, tag_of(L, 8), xcd, r);
   }
 
-  // ------------------------------------------------------------------ k
-  if (ctl.template gather<Dm::H>(a.x + Dm::X_H, tag_of(p.nl - 1, 5), to_f32(s.x))) {
-    ctl.rmsnorm(s.x, a.final_norm);
+  // ------------------------------------------------------------------ final
+  const auto nw_final = ctl.load_norm(a.final_norm);
+  if (ctl.template gather_range<Dm::H>(Dm::X_H + xcd * Dm::H, tag_of(p.nl - 1, 8), to_f32(s.x))) {
+    ctl.rmsnorm(s.x, nw_final);
     if (b == 0) {
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
@@ -552,10 +726,10 @@ __device__ __forceinline__ void control_path(const KArgs& a, Smem<M>& s, const S
     }
   }
   stamp(p.nl * kTracePoints + 0);
-  QMK_SYNC();  // k
-  QMK_SYNC();  // l
+  QMK_SYNC();  // final a
+  QMK_SYNC();  // final b
   stamp(p.nl * kTracePoints + 1);
-  const uint32_t tk = make_tag(p.epoch, (uint32_t)(p.nl * Dm::N_X_PER_LAYER));
+  const uint32_t tk = make_tag(p.epoch, (uint32_t)(p.nl * Dm::NX));
   if (lane == 0) {
     uint64_t best = 0;
 #pragma unroll
@@ -570,7 +744,7 @@ __device__ __forceinline__ void control_path(const KArgs& a, Smem<M>& s, const S
   }
   if (b == 0) {
     uint64_t best = 0;
-    const bool ok = ctl.template gather<kNumWG * 4>(a.x + Dm::X_KEY, tk, [&](int ci, u32x4 v) {
+    const bool ok = ctl.template gather_range<kNumWG * 4>(Dm::X_KEY, tk, [&](int ci, u32x4 v) {
       const uint32_t idx = (v.y >> 16) | (v.z & 0xffff0000u);
       const uint64_t key = ((uint64_t)(v.x >> 16) << 32) | (uint64_t)(0xffffffffu - idx);
       best = key > best ? key : best;
@@ -588,7 +762,7 @@ __device__ __forceinline__ void control_path(const KArgs& a, Smem<M>& s, const S
           st->pos = p.pos + 1;
           st->step = p.step + 1;
         }
-        st->epoch = p.epoch + (uint32_t)(p.nl * Dm::N_X_PER_LAYER + 1);
+        st->epoch = p.epoch + (uint32_t)(p.nl * Dm::NX + 1);
       }
     }
   }
@@ -597,7 +771,8 @@ __device__ __forceinline__ void control_path(const KArgs& a, Smem<M>& s, const S
 template <class M>
 __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const Step& p, int b, int c, int lane) {
   using Dm = Dims<M>;
-  const int g = b & (kGroups - 1), r = b >> 3;
+  const int xcd = b & (kGroups - 1), r = b >> 3;
+  const int slot = lane >> 4, t16 = lane & 15;
   const size_t kv_layer_stride = (size_t)Dm::NKV * a.max_seq_len * Dm::D;
 
   // Weight registers, requested one layer ahead.
@@ -606,40 +781,52 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
   u32x4 wgu[Dm::GU_W][Dm::LH];
   u32x4 wd[Dm::LD];
 
-  const int o_row = Dm::O_ROWS * b + c / Dm::O_WPR;
-  const int o_k0 = (c % Dm::O_WPR) * (Dm::QS / Dm::O_WPR);
-  const int d_row = Dm::D_ROWS * b + c / Dm::D_WPR;
-  const int d_k0 = (c % Dm::D_WPR) * (Dm::I / Dm::D_WPR);
+  // o_proj / down_proj: rows ROWS_WG*r + 4c + slot, this XCD's input columns
+  const int rs_row = Dm::ROWS_WG * r + Dm::ROWS_W * c + slot;
   const bool gu_up = c >= kComputeWaves / 2;
-  const int gu_m0 = Dm::M_WG * b + (gu_up ? c - kComputeWaves / 2 : c) * Dm::GU_W;
-  const int gu_out = (gu_up ? Dm::M_WG : 0) + (gu_up ? c - kComputeWaves / 2 : c) * Dm::GU_W;
+  const int gu_i = (gu_up ? c - kComputeWaves / 2 : c) * Dm::GU_W;          // within this workgroup's m values
+  const int gu_m0 = Dm::MS * xcd + Dm::M_WG * r + gu_i;                     // global m index
+  const int gu_out = (gu_up ? Dm::M_WG : 0) + gu_i;
 
   auto prefetch_qkv = [&](int layer) {
-    const LayerPtrs& w = a.layers[layer];
+    LayerPtrs w;
+    w.wq = uniform_ptr(s.layers[layer].wq);
+    w.wk = uniform_ptr(s.layers[layer].wk);
+    w.wv = uniform_ptr(s.layers[layer].wv);
 #pragma unroll
-    for (int i = 0; i < Dm::RQ_W; i++) load_row(wq[i], qkv_row<M>(w, g, Dm::RQ_WG * r + Dm::RQ_W * c + i), 0, lane);
+    for (int i = 0; i < Dm::RQ_W; i++) load_row(wq[i], qkv_row<M>(w, xcd, Dm::RQ_WG * r + Dm::RQ_W * c + i), 0, lane);
   };
-  auto prefetch_o = [&](int layer) { load_row(wo, a.layers[layer].wo + (size_t)o_row * Dm::QS, o_k0, lane); };
+  auto prefetch_o = [&](int layer) {
+    load_seg(wo, uniform_ptr(s.layers[layer].wo) + (size_t)rs_row * Dm::QS + Dm::OC * xcd, t16);
+  };
   auto prefetch_gu = [&](int layer) {
-    const uint16_t* base = gu_up ? a.layers[layer].wu : a.layers[layer].wg;
+    const uint16_t* base = uniform_ptr(gu_up ? s.layers[layer].wu : s.layers[layer].wg);
 #pragma unroll
     for (int i = 0; i < Dm::GU_W; i++) load_row(wgu[i], base + (size_t)(gu_m0 + i) * Dm::H, 0, lane);
   };
-  auto prefetch_dn = [&](int layer) { load_row(wd, a.layers[layer].wd + (size_t)d_row * Dm::I, d_k0, lane); };
+  auto prefetch_dn = [&](int layer) {
+    load_seg(wd, uniform_ptr(s.layers[layer].wd) + (size_t)rs_row * Dm::I + Dm::MS * xcd, t16);
+  };
 
   prefetch_qkv(0);
   prefetch_o(0);
   prefetch_gu(0);
   prefetch_dn(0);
 
-  const int chunk = (p.C + kGroupSize - 1) / kGroupSize;
-  const int p_begin = min(p.C, r * chunk);
-  const int p_end = min(p.C, p_begin + chunk);
-  const int slot = lane >> 4, t16 = lane & 15;
-
+  constexpr int U = 2;  // attention: each wave covers 4 positions per step, U steps per batch
   for (int L = 0; L < p.nl; L++) {
-    const uint16_t* kc = a.k_cache + L * kv_layer_stride + (size_t)g * a.max_seq_len * Dm::D;
-    const uint16_t* vc = a.v_cache + L * kv_layer_stride + (size_t)g * a.max_seq_len * Dm::D;
+    const uint16_t* kc = a.k_cache + L * kv_layer_stride + (size_t)xcd * a.max_seq_len * Dm::D;
+    const uint16_t* vc = a.v_cache + L * kv_layer_stride + (size_t)xcd * a.max_seq_len * Dm::D;
+    auto kv_load = [&](const uint16_t* base, u32x4 (&dst)[U], int bpos) {
+#pragma unroll
+      for (int u = 0; u < U; u++) {
+        const int pp = bpos + 32 * u + slot;
+        // positions outside this workgroup's range (and pos, whose K/V come from
+        // LDS) load row 0, which every cache has; their values are never used
+        const int pl = (pp < p.p_end && pp != p.pos) ? pp : 0;
+        dst[u] = ld16(base + (size_t)pl * Dm::D + 8 * t16);
+      }
+    };
     QMK_SYNC();  // a
     {
       u32x4 act[Dm::LH];
@@ -650,62 +837,44 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
         if (lane == 0) s.out[Dm::RQ_W * c + i] = bf16r(v);
       }
     }
+    // first batch of keys for the scores (the positions before pos are in the cache already)
+    const int base0 = p.p_begin + 4 * c;
+    u32x4 kk[U];
+    kv_load(kc, kk, base0);
     QMK_SYNC();  // b
     QMK_SYNC();  // c
+    // ------------------------------------------------ scores and local (max, sum)
     {
       u32x4 qv[Dm::GQ];
 #pragma unroll
       for (int h = 0; h < Dm::GQ; h++) qv[h] = *reinterpret_cast<const u32x4*>(s.q + h * Dm::D + 8 * t16);
       const u32x4 k_now = *reinterpret_cast<const u32x4*>(s.k + 8 * t16);
-      const u32x4 v_now = *reinterpret_cast<const u32x4*>(s.v + 8 * t16);
-      float mrun[Dm::GQ], lrun[Dm::GQ], acc[Dm::GQ][8];
+      float mrun[Dm::GQ], lrun[Dm::GQ];
 #pragma unroll
       for (int h = 0; h < Dm::GQ; h++) {
         mrun[h] = -INFINITY;
         lrun[h] = 0.f;
-#pragma unroll
-        for (int i = 0; i < 8; i++) acc[h][i] = 0.f;
       }
-      constexpr int U = 2;  // each wave covers 4 positions (one per 16-lane slot) per step, U steps per batch
-      for (int base = p_begin + 4 * c; base < p_end; base += 32 * U) {
-        u32x4 kk[U], vv[U];
-        bool valid[U];
-#pragma unroll
-        for (int u = 0; u < U; u++) {
-          const int pp = base + 32 * u + slot;
-          valid[u] = pp < p_end;
-          const int pl = (valid[u] && pp != p.pos) ? pp : p_begin;
-          kk[u] = ld16(kc + (size_t)pl * Dm::D + 8 * t16);
-          vv[u] = ld16(vc + (size_t)pl * Dm::D + 8 * t16);
-        }
+      for (int base = base0; base < p.p_end; base += 32 * U) {
+        if (base != base0) kv_load(kc, kk, base);
 #pragma unroll
         for (int u = 0; u < U; u++) {
           const int pp = base + 32 * u + slot;
           const u32x4 kx = pp == p.pos ? k_now : kk[u];
-          const u32x4 vx = pp == p.pos ? v_now : vv[u];
 #pragma unroll
           for (int h = 0; h < Dm::GQ; h++) {
             float sc = row16_sum(dot8(kx, qv[h], 0.f));
             sc = bf16r(bf16r(sc) * a.attn_scale);
-            if (valid[u]) {
+            if (pp < p.p_end) {
+              if (t16 == 0) s.sc[h][pp - p.p_begin] = sc;
               const float mn = fmaxf(mrun[h], sc);
-              const float corr = __expf(mrun[h] - mn);
-              const float pe = __expf(sc - mn);
-              lrun[h] = lrun[h] * corr + pe;
-              acc[h][0] = acc[h][0] * corr + pe * lo_bf16(vx.x);
-              acc[h][1] = acc[h][1] * corr + pe * hi_bf16(vx.x);
-              acc[h][2] = acc[h][2] * corr + pe * lo_bf16(vx.y);
-              acc[h][3] = acc[h][3] * corr + pe * hi_bf16(vx.y);
-              acc[h][4] = acc[h][4] * corr + pe * lo_bf16(vx.z);
-              acc[h][5] = acc[h][5] * corr + pe * hi_bf16(vx.z);
-              acc[h][6] = acc[h][6] * corr + pe * lo_bf16(vx.w);
-              acc[h][7] = acc[h][7] * corr + pe * hi_bf16(vx.w);
+              lrun[h] = lrun[h] * exp_acc(mrun[h] - mn) + exp_acc(sc - mn);
               mrun[h] = mn;
             }
           }
         }
       }
-      // merge the wave's four position slots
+      // merge the wave's four slots
 #pragma unroll
       for (int h = 0; h < Dm::GQ; h++) {
 #pragma unroll
@@ -713,38 +882,78 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
           const float mo = __shfl_xor(mrun[h], o);
           const float lo = __shfl_xor(lrun[h], o);
           const float mn = fmaxf(mrun[h], mo);
-          const float f1 = mrun[h] == -INFINITY ? 0.f : __expf(mrun[h] - mn);
-          const float f2 = mo == -INFINITY ? 0.f : __expf(mo - mn);
+          const float f1 = mrun[h] == -INFINITY ? 0.f : exp_acc(mrun[h] - mn);
+          const float f2 = mo == -INFINITY ? 0.f : exp_acc(mo - mn);
           lrun[h] = lrun[h] * f1 + lo * f2;
-#pragma unroll
-          for (int i = 0; i < 8; i++) {
-            const float ao = __shfl_xor(acc[h][i], o);
-            acc[h][i] = acc[h][i] * f1 + ao * f2;
-          }
           mrun[h] = mn;
+        }
+        if (lane == 0) {
+          s.wml[c][h][0] = mrun[h];
+          s.wml[c][h][1] = lrun[h];
+        }
+      }
+    }
+    u32x4 vv[U];
+    kv_load(vc, vv, base0);
+    QMK_SYNC();  // d
+    QMK_SYNC();  // e
+    // ------------------------------------------------ probabilities and P@V
+    {
+      const u32x4 v_now = *reinterpret_cast<const u32x4*>(s.v + 8 * t16);
+      float gm[Dm::GQ], ginv[Dm::GQ];
+#pragma unroll
+      for (int h = 0; h < Dm::GQ; h++) {
+        gm[h] = s.ml[h][0];
+        ginv[h] = __fdiv_rn(1.0f, s.ml[h][1]);
+      }
+      float acc[Dm::GQ][8];
+#pragma unroll
+      for (int h = 0; h < Dm::GQ; h++)
+#pragma unroll
+        for (int i = 0; i < 8; i++) acc[h][i] = 0.f;
+      for (int base = base0; base < p.p_end; base += 32 * U) {
+        if (base != base0) kv_load(vc, vv, base);
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+          const int pp = base + 32 * u + slot;
+          if (pp < p.p_end) {
+            const u32x4 vx = pp == p.pos ? v_now : vv[u];
+            const float vf[8] = {lo_bf16(vx.x), hi_bf16(vx.x), lo_bf16(vx.y), hi_bf16(vx.y),
+                                 lo_bf16(vx.z), hi_bf16(vx.z), lo_bf16(vx.w), hi_bf16(vx.w)};
+#pragma unroll
+            for (int h = 0; h < Dm::GQ; h++) {
+              // HF: softmax in fp32, probabilities rounded to bf16 before P@V
+              const float pr = bf16r(exp_acc(s.sc[h][pp - p.p_begin] - gm[h]) * ginv[h]);
+#pragma unroll
+              for (int i = 0; i < 8; i++) acc[h][i] += pr * vf[i];
+            }
+          }
+        }
+      }
+      // sum the wave's four slots; lanes 0..15 then hold dims 8*t16..+7
+#pragma unroll
+      for (int h = 0; h < Dm::GQ; h++) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+          acc[h][i] += __shfl_xor(acc[h][i], 16);
+          acc[h][i] += __shfl_xor(acc[h][i], 32);
         }
         if (lane < 16) {
 #pragma unroll
-          for (int i = 0; i < 8; i++) s.wp[c][h][2 + 8 * t16 + i] = acc[h][i];
-          if (lane == 0) {
-            s.wp[c][h][0] = mrun[h];
-            s.wp[c][h][1] = lrun[h];
-          }
+          for (int i = 0; i < 8; i++) s.wacc[c][h][8 * t16 + i] = acc[h][i];
         }
       }
     }
     if (L + 1 < p.nl) prefetch_qkv(L + 1);
-    QMK_SYNC();  // d
-    QMK_SYNC();  // e
-    {
-      u32x4 act[Dm::LO];
-      load_act(act, s.attn, o_k0, lane);
-      const float v = row_dot(wo, act);
-      if (lane == 0) s.out[c] = v;
-    }
-    if (L + 1 < p.nl) prefetch_o(L + 1);
     QMK_SYNC();  // f
     QMK_SYNC();  // g
+    {
+      const float v = seg_dot(wo, s.attn, t16);
+      if (t16 == 0) s.out[Dm::ROWS_W * c + slot] = v;
+    }
+    if (L + 1 < p.nl) prefetch_o(L + 1);
+    QMK_SYNC();  // h
+    QMK_SYNC();  // i
     {
       u32x4 act[Dm::LH];
       load_act(act, s.n, 0, lane);
@@ -755,19 +964,17 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
       }
     }
     if (L + 1 < p.nl) prefetch_gu(L + 1);
-    QMK_SYNC();  // h
-    QMK_SYNC();  // i
+    QMK_SYNC();  // j
+    QMK_SYNC();  // k
     {
-      u32x4 act[Dm::LD];
-      load_act(act, s.m, d_k0, lane);
-      const float v = row_dot(wd, act);
-      if (lane == 0) s.out[c] = v;
+      const float v = seg_dot(wd, s.m, t16);
+      if (t16 == 0) s.out[Dm::ROWS_W * c + slot] = v;
     }
     if (L + 1 < p.nl) prefetch_dn(L + 1);
-    QMK_SYNC();  // j
+    QMK_SYNC();  // l
   }
 
-  QMK_SYNC();  // k
+  QMK_SYNC();  // final a
   {
     u32x4 act[Dm::LH];
     load_act(act, s.n, 0, lane);
@@ -806,7 +1013,7 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
     }
     if (lane == 0) s.best[c] = best;
   }
-  QMK_SYNC();  // l
+  QMK_SYNC();  // final b
 }
 
 template <class M>
@@ -818,6 +1025,13 @@ __global__ void __launch_bounds__(kBlock, 1) decode_kernel(KArgs a) {
   const int lane = threadIdx.x & 63;
 
   DecodeState* st = a.st;
+  {
+    // copy the per-layer pointer table (num_layers x 11 pointers) into LDS
+    const int n = min(a.num_layers, kMaxLayers) * (int)(sizeof(LayerPtrs) / sizeof(void*));
+    const uint64_t* src = reinterpret_cast<const uint64_t*>(a.layers);
+    uint64_t* dst = reinterpret_cast<uint64_t*>(s.layers);
+    for (int i = threadIdx.x; i < n; i += kBlock) dst[i] = src[i];
+  }
   if (threadIdx.x == 0) {
     // One thread reads the state's error word so the whole workgroup takes the
     // same decision; a non-zero value (an earlier launch failed) makes this
@@ -844,6 +1058,11 @@ __global__ void __launch_bounds__(kBlock, 1) decode_kernel(KArgs a) {
     }
     return;
   }
+  p.chunk = (p.C + kGroupSize - 1) / kGroupSize;
+  const int r = b >> 3;
+  p.p_begin = min(p.C, r * p.chunk);
+  p.p_end = min(p.C, p.p_begin + p.chunk);
+  p.n_act = (p.C + p.chunk - 1) / p.chunk;
   if (wave == 0)
     control_path<M>(a, s, p, b, lane);
   else

@@ -58,6 +58,20 @@ __device__ __forceinline__ float dot8(u32x4 w, u32x4 x, float acc) {
   return acc;
 }
 
+// exp(x) for the softmax: 2^(x*log2(e)) with the product split into a rounded
+// high part and its exact low remainder (Cody-Waite style), so that the
+// argument error stays within an ulp for any |x|; the hardware exp2 covers the
+// rest.  The argument is clamped at -128, whose exp underflows to 0, so -inf
+// (an empty softmax row) gives 0 instead of the NaN of inf - inf.
+__device__ __forceinline__ float exp_acc(float x) {
+  constexpr float kL2eHi = 1.44269502162933349609375f;   // log2(e) rounded to fp32
+  constexpr float kL2eLo = 1.925963033500011e-08f;        // log2(e) - kL2eHi
+  x = fmaxf(x, -128.0f);
+  const float hi = x * kL2eHi;
+  const float lo = __builtin_fmaf(x, kL2eHi, -hi) + x * kL2eLo;
+  return __builtin_amdgcn_exp2f(hi) * __builtin_amdgcn_exp2f(lo);
+}
+
 // ------------------------------------------------------------ reductions
 
 template <int CTRL>

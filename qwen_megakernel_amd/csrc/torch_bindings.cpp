@@ -50,7 +50,7 @@ Checked check_common(const torch::Tensor& embed_weight, const torch::Tensor& lay
                      const torch::Tensor& v_cache, const torch::Tensor& hidden_buffer,
                      const torch::Tensor& normalized, int64_t num_layers, int64_t max_seq_len, double attn_scale) {
   TORCH_CHECK(num_layers >= 1 && num_layers <= kMaxLayers, "num_layers must be in [1, 28], got ", num_layers);
-  TORCH_CHECK(max_seq_len >= 1, "max_seq_len must be positive");
+  TORCH_CHECK(max_seq_len >= 1 && max_seq_len <= 65536, "max_seq_len must be in [1, 65536]");
   TORCH_CHECK(attn_scale > 0.0, "attn_scale must be positive");
   check_bf16(embed_weight, "embed_weight", kVocab * kHidden);
   check_bf16(lm_head_weight, "lm_head_weight", kVocab * kHidden);
