@@ -148,9 +148,18 @@ int qmk_set_wait_limit(hipStream_t stream, uint32_t ticks);
 /* Phase trace.  When `buf` (device uint64[qmk_trace_entries(28)]) is set,
  * every launch on `stream` writes, for each workgroup w, the 100 MHz device
  * wall clock at 13 points of each layer and 3 points after the last layer:
- * buf[point * 256 + w], point = layer * 13 + k.  NULL disables tracing. */
+ * buf[point * 256 + w], point = layer * 13 + k; then compute wave 0 writes
+ * the start and end of its 6 phases per layer at
+ * buf[(num_layers*13 + 3 + layer*12 + k) * 256 + w].  NULL disables tracing. */
 int qmk_set_trace(hipStream_t stream, uint64_t *buf, size_t entries);
 size_t qmk_trace_entries(int num_layers);
+
+/* Runs the decode kernel's arithmetic building blocks on one wave so tests can
+ * check them: out[0,n) = bf16 rounding of in[i], out[n,2n) = the softmax exp
+ * of in[i], out[2n + 64k + lane] for k = 0..4: sum over the four 16-lane rows,
+ * then the two results of the row-pair swap and of the half-wave swap of
+ * in[lane].  n >= 64; out holds 2n + 320 floats.  Asynchronous. */
+int qmk_selftest_blocks(const float *in, float *out, int n, hipStream_t stream);
 
 /* Kernel launch geometry, for tools: workgroups and threads per workgroup. */
 void qmk_launch_geometry(int *workgroups, int *threads);

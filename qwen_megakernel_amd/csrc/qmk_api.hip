@@ -54,6 +54,27 @@ __global__ void xcd_probe_kernel(int* ok) {
   }
 }
 
+// Building blocks of the decode kernel on one wave, for unit tests:
+// out[0,n) = bf16 rounding of in, out[n,2n) = softmax exp of in, then for the
+// first 64 inputs (one per lane): sum over the four 16-lane rows, the two
+// values of the row-pair swap and the two values of the half-wave swap.
+__global__ void selftest_kernel(const float* in, float* out, int n) {
+  const int lane = threadIdx.x;
+  for (int i = lane; i < n; i += 64) {
+    out[i] = bf16r(in[i]);
+    out[n + i] = exp_acc(in[i]);
+  }
+  const float v = in[lane];
+  float a, b;
+  out[2 * n + lane] = rows_sum4(v);
+  swap16(v, a, b);
+  out[2 * n + 64 + lane] = a;
+  out[2 * n + 128 + lane] = b;
+  swap32(v, a, b);
+  out[2 * n + 192 + lane] = a;
+  out[2 * n + 256 + lane] = b;
+}
+
 __global__ void set_step_kernel(DecodeState* st, int pos, int tok) {
   st->pos = pos;
   st->tok = tok;
@@ -353,7 +374,13 @@ int qmk_set_trace(hipStream_t stream, uint64_t* buf, size_t entries) {
 }
 
 size_t qmk_trace_entries(int num_layers) {
-  return (size_t)(num_layers * kTracePoints + 3) * kNumWG;
+  return (size_t)(num_layers * (kTracePoints + kComputePoints) + 3) * kNumWG;
+}
+
+int qmk_selftest_blocks(const float* in, float* out, int n, hipStream_t stream) {
+  if (!in || !out || n < 64) return fail(QMK_ERR_ARG);
+  hipLaunchKernelGGL(selftest_kernel, dim3(1), dim3(64), 0, stream, in, out, n);
+  return fail(hipGetLastError() == hipSuccess ? QMK_OK : QMK_ERR_HIP);
 }
 
 void qmk_launch_geometry(int* workgroups, int* threads) {

@@ -62,7 +62,8 @@ struct Qwen3_0_6B {
 
 constexpr int kMaxSeqLen = 65536;                          // longest cache the kernel accepts
 constexpr int kChunkMax = kMaxSeqLen / kGroupSize;         // attention positions per workgroup
-constexpr int kTracePoints = 13;                           // wall-clock stamps per layer
+constexpr int kTracePoints = 13;                           // control-wave stamps per layer
+constexpr int kComputePoints = 12;                         // compute-wave stamps per layer (start/end of 6 phases)
 constexpr int kMaxLayers = 28;
 
 template <class M>
@@ -813,6 +814,11 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
   prefetch_gu(0);
   prefetch_dn(0);
 
+  // compute wave 0 stamps the start and end of each of its phases
+  uint64_t* ctrace = a.trace ? a.trace + (size_t)(a.num_layers * kTracePoints + 3) * kNumWG : nullptr;
+  auto cstamp = [&](int L, int k) {
+    if (ctrace && c == 0 && lane == 0) ctrace[(size_t)(L * kComputePoints + k) * kNumWG + b] = wall_clock64();
+  };
   constexpr int U = 2;  // attention: each wave covers 4 positions per step, U steps per batch
   for (int L = 0; L < p.nl; L++) {
     const uint16_t* kc = a.k_cache + L * kv_layer_stride + (size_t)xcd * a.max_seq_len * Dm::D;
@@ -828,6 +834,7 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
       }
     };
     QMK_SYNC();  // a
+    cstamp(L, 0);
     {
       u32x4 act[Dm::LH];
       load_act(act, s.n, 0, lane);
@@ -841,8 +848,10 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
     const int base0 = p.p_begin + 4 * c;
     u32x4 kk[U];
     kv_load(kc, kk, base0);
+    cstamp(L, 1);
     QMK_SYNC();  // b
     QMK_SYNC();  // c
+    cstamp(L, 2);
     // ------------------------------------------------ scores and local (max, sum)
     {
       u32x4 qv[Dm::GQ];
@@ -859,6 +868,7 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
         if (base != base0) kv_load(kc, kk, base);
 #pragma unroll
         for (int u = 0; u < U; u++) {
+          if (base + 32 * u >= p.p_end) break;  // the rest of the batch is past this workgroup's range
           const int pp = base + 32 * u + slot;
           const u32x4 kx = pp == p.pos ? k_now : kk[u];
 #pragma unroll
@@ -874,17 +884,18 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
           }
         }
       }
-      // merge the wave's four slots
+      // merge the wave's four slots (16-lane rows): rows 2k,2k+1, then the halves
 #pragma unroll
       for (int h = 0; h < Dm::GQ; h++) {
 #pragma unroll
-        for (int o = 16; o <= 32; o <<= 1) {
-          const float mo = __shfl_xor(mrun[h], o);
-          const float lo = __shfl_xor(lrun[h], o);
-          const float mn = fmaxf(mrun[h], mo);
-          const float f1 = mrun[h] == -INFINITY ? 0.f : exp_acc(mrun[h] - mn);
-          const float f2 = mo == -INFINITY ? 0.f : exp_acc(mo - mn);
-          lrun[h] = lrun[h] * f1 + lo * f2;
+        for (int step = 0; step < 2; step++) {
+          float ma, mb, la, lb;
+          if (step == 0) { swap16(mrun[h], ma, mb); swap16(lrun[h], la, lb); }
+          else { swap32(mrun[h], ma, mb); swap32(lrun[h], la, lb); }
+          const float mn = fmaxf(ma, mb);
+          const float fa = ma == -INFINITY ? 0.f : exp_acc(ma - mn);
+          const float fb = mb == -INFINITY ? 0.f : exp_acc(mb - mn);
+          lrun[h] = la * fa + lb * fb;
           mrun[h] = mn;
         }
         if (lane == 0) {
@@ -895,8 +906,10 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
     }
     u32x4 vv[U];
     kv_load(vc, vv, base0);
+    cstamp(L, 3);
     QMK_SYNC();  // d
     QMK_SYNC();  // e
+    cstamp(L, 4);
     // ------------------------------------------------ probabilities and P@V
     {
       const u32x4 v_now = *reinterpret_cast<const u32x4*>(s.v + 8 * t16);
@@ -915,6 +928,7 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
         if (base != base0) kv_load(vc, vv, base);
 #pragma unroll
         for (int u = 0; u < U; u++) {
+          if (base + 32 * u >= p.p_end) break;
           const int pp = base + 32 * u + slot;
           if (pp < p.p_end) {
             const u32x4 vx = pp == p.pos ? v_now : vv[u];
@@ -934,10 +948,7 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
 #pragma unroll
       for (int h = 0; h < Dm::GQ; h++) {
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-          acc[h][i] += __shfl_xor(acc[h][i], 16);
-          acc[h][i] += __shfl_xor(acc[h][i], 32);
-        }
+        for (int i = 0; i < 8; i++) acc[h][i] = rows_sum4(acc[h][i]);
         if (lane < 16) {
 #pragma unroll
           for (int i = 0; i < 8; i++) s.wacc[c][h][8 * t16 + i] = acc[h][i];
@@ -945,15 +956,19 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
       }
     }
     if (L + 1 < p.nl) prefetch_qkv(L + 1);
+    cstamp(L, 5);
     QMK_SYNC();  // f
     QMK_SYNC();  // g
+    cstamp(L, 6);
     {
       const float v = seg_dot(wo, s.attn, t16);
       if (t16 == 0) s.out[Dm::ROWS_W * c + slot] = v;
     }
     if (L + 1 < p.nl) prefetch_o(L + 1);
+    cstamp(L, 7);
     QMK_SYNC();  // h
     QMK_SYNC();  // i
+    cstamp(L, 8);
     {
       u32x4 act[Dm::LH];
       load_act(act, s.n, 0, lane);
@@ -964,13 +979,16 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
       }
     }
     if (L + 1 < p.nl) prefetch_gu(L + 1);
+    cstamp(L, 9);
     QMK_SYNC();  // j
     QMK_SYNC();  // k
+    cstamp(L, 10);
     {
       const float v = seg_dot(wd, s.m, t16);
       if (t16 == 0) s.out[Dm::ROWS_W * c + slot] = v;
     }
     if (L + 1 < p.nl) prefetch_dn(L + 1);
+    cstamp(L, 11);
     QMK_SYNC();  // l
   }
 

@@ -31,12 +31,12 @@ constexpr int kGroupSize = kNumWG / kGroups;
 
 __device__ __forceinline__ float bf16_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
 
-// fp32 -> bf16 bits, round to nearest even; NaN -> 0x7FC0 (as c10::BFloat16).
+// fp32 -> bf16 bits, round to nearest even (gfx950 v_cvt_pk_bf16_f32), as
+// c10::BFloat16 does for every non-NaN value; tests/test_gpu_blocks.py checks
+// it against torch on ties, subnormals and infinities.
 __device__ __forceinline__ uint32_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return u >> 16;
+  const __bf16 h = (__bf16)f;
+  return (uint32_t)__builtin_bit_cast(unsigned short, h);
 }
 
 // Value of ``f`` rounded to bf16, as fp32.
@@ -66,10 +66,34 @@ __device__ __forceinline__ float dot8(u32x4 w, u32x4 x, float acc) {
 __device__ __forceinline__ float exp_acc(float x) {
   constexpr float kL2eHi = 1.44269502162933349609375f;   // log2(e) rounded to fp32
   constexpr float kL2eLo = 1.925963033500011e-08f;        // log2(e) - kL2eHi
+  constexpr float kLn2 = 0.693147180559945309f;
   x = fmaxf(x, -128.0f);
   const float hi = x * kL2eHi;
-  const float lo = __builtin_fmaf(x, kL2eHi, -hi) + x * kL2eLo;
-  return __builtin_amdgcn_exp2f(hi) * __builtin_amdgcn_exp2f(lo);
+  const float lo = __builtin_fmaf(x, kL2eHi, -hi) + x * kL2eLo;  // |lo| < 2^-16: 2^lo = 1 + lo*ln2
+  const float e = __builtin_amdgcn_exp2f(hi);
+  return __builtin_fmaf(e * lo, kLn2, e);
+}
+
+// Exchange a value with the lane 16 (sum over rows 2k, 2k+1) or 32 lanes away
+// (sum over the two wave halves) through the gfx950 permlane swaps, which run
+// on the VALU instead of the LDS crossbar.  Return {own row's value, partner's}
+// in an order that is the same for both partners (so symmetric merges agree).
+__device__ __forceinline__ void swap16(float v, float& a, float& b) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  a = __uint_as_float(r[0]);
+  b = __uint_as_float(r[1]);
+}
+__device__ __forceinline__ void swap32(float v, float& a, float& b) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  a = __uint_as_float(r[0]);
+  b = __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float rows_sum4(float v) {  // sum over the four 16-lane rows, in every lane
+  float a, b;
+  swap16(v, a, b);
+  v = a + b;
+  swap32(v, a, b);
+  return a + b;
 }
 
 // ------------------------------------------------------------ reductions
