@@ -9,6 +9,7 @@
 """
 
 import ctypes
+import math
 import os
 import re
 
@@ -139,3 +140,17 @@ def test_pack_layer_weights_layout():
     assert blob.dtype == torch.uint8 and blob.numel() == 2 * 11 * 8
     ptrs = struct.unpack("22Q", bytes(blob.tolist()))
     assert list(ptrs) == [t.data_ptr() for t in ts]
+
+
+def test_algorithmic_bytes():
+    """Bytes per token that the roofline divides by, summed tensor by tensor."""
+    from qwen_megakernel_amd.shapes import QWEN3_0_6B, layer_tensor_shapes
+
+    s = QWEN3_0_6B
+    layer = sum(2 * math.prod(shp) for shp in layer_tensor_shapes(s).values())
+    assert layer == 31_461_888
+    lm_head = 2 * s.vocab * s.hidden
+    assert lm_head == 311_164_928
+    assert s.weight_bytes_per_token() == 28 * layer + lm_head + 2 * s.hidden + 2 * s.hidden == 1_192_101_888
+    assert s.kv_bytes_per_position() == 28 * 8 * 128 * 2 * 2 == 114_688
+    assert s.bytes_per_token(1024) == 1_192_101_888 + 114_688 * 1025
