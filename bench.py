@@ -13,6 +13,12 @@ prompt re-prefilled), so the K timed steps always cover contexts 129..128+K.
 (weights + KV read + KV written, averaged over the timed contexts) to its
 average launch duration measured with HIP events on the launch stream.
 ``cpu_baseline`` times the CPU oracle (HF-semantics bf16 decode) on the host.
+
+Options for profiling runs: ``--phase-trace`` adds the in-kernel phase trace
+of one more step (at the last timed context) to the JSON line;
+``--copy-calibration`` first runs a plain 1 GiB device-to-device copy five
+times, so that a counter run (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE) sees a
+kernel of known traffic beside the decode kernel.
 """
 
 from __future__ import annotations
@@ -25,6 +31,11 @@ import time
 
 PEAK_HBM_GBS = 8000.0
 PROMPT_LEN = 128
+# HBM bytes per decode launch (fetch + write) on the default workload (steps, warmup), from two
+# rocprofv3 --pmc runs of this script with --copy-calibration (FETCH_SIZE, then WRITE_SIZE), each
+# counter scaled by its own reading for the 1 GiB calibration copy and averaged over the timed
+# dispatches by ``python -m qwen_megakernel_amd.counters``.  Remeasured whenever the kernel changes.
+MEASURED_TRAFFIC_BYTES = {(1024, 32): 1_304_622_046}
 METRIC = "decode tok/s, batch 1, Qwen3-0.6B bf16; achieved HBM GB/s vs ~8 TB/s peak"
 
 
@@ -75,6 +86,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=32)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-steps", type=int, default=32)
+    ap.add_argument("--phase-trace", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (this path does not shard "
@@ -108,6 +121,16 @@ def main():
     def run(n):
         return ops.generate_nosync(prompt[-1], n, *dec._scratch(), QWEN3_0_6B.num_layers, dec.position,
                                    max_seq, dec._attn_scale)
+
+    if args.copy_calibration:
+        src = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        src.fill_(1)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+        log("copy calibration: 5 x 1 GiB device copies")
 
     if args.warmup:
         prefill()
@@ -149,11 +172,23 @@ def main():
                    "batch": 1, "prompt_len": PROMPT_LEN, "decode_steps": args.steps, "max_seq_len": max_seq,
                    "weights": "seeded N(0,0.02) bf16, norms 1, tied embeddings"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
+                     "frac": round(achieved / PEAK_HBM_GBS, 4),
+                     "traffic": MEASURED_TRAFFIC_BYTES.get((args.steps, args.warmup)),
                      "bytes_per_launch": int(bytes_per_launch), "avg_launch_us": round(avg_launch_s * 1e6, 2),
                      "kernel": "qmk::decode_kernel<Qwen3_0_6B>"},
         "cpu_baseline": None,
     }
+    if args.phase_trace:
+        from qwen_megakernel_amd import trace
+
+        last = PROMPT_LEN - 1 + args.steps  # position after the timed steps
+        dec._position = last
+
+        stamps = trace.capture(lambda: dec.step(int(toks[-1])), QWEN3_0_6B.num_layers)
+        summ = trace.summarize(stamps, QWEN3_0_6B.num_layers)
+        summ["context"] = last + 1
+        result["phase_trace"] = summ
+        log(f"phase trace at context {last + 1}:\n" + trace.format_table(summ))
     log(f"decode: {value:.1f} tok/s, {dt * 1e3 / args.steps:.3f} ms/token, kernel avg {avg_launch_s * 1e6:.1f} us, "
         f"{achieved:.0f} GB/s algorithmic")
     if not args.no_cpu_baseline:
