@@ -309,7 +309,7 @@ struct Ctl {
     NormW r;
     const uint32_t* w2 = reinterpret_cast<const uint32_t*>(w);
 #pragma unroll
-    for (int i = 0; i < Dm::H / 128; i++) r.w[i] = w2[lane + 64 * i];
+    for (int i = 0; i < Dm::H / 128; i++) r.w[i] = ld32(w2 + lane + 64 * i);
     return r;
   }
 
@@ -342,12 +342,12 @@ struct Ctl {
   };
   __device__ HeadW load_head(const uint16_t* w, const uint16_t* cosr, const uint16_t* sinr) {
     HeadW h;
-    h.w0 = bf16_to_f32(w[lane]);
-    h.w1 = bf16_to_f32(w[lane + 64]);
-    h.c0 = bf16_to_f32(cosr[lane]);
-    h.c1 = bf16_to_f32(cosr[lane + 64]);
-    h.s0 = bf16_to_f32(sinr[lane]);
-    h.s1 = bf16_to_f32(sinr[lane + 64]);
+    h.w0 = bf16_to_f32(ldu16(w + lane));
+    h.w1 = bf16_to_f32(ldu16(w + lane + 64));
+    h.c0 = bf16_to_f32(ldu16(cosr + lane));
+    h.c1 = bf16_to_f32(ldu16(cosr + lane + 64));
+    h.s0 = bf16_to_f32(ldu16(sinr + lane));
+    h.s1 = bf16_to_f32(ldu16(sinr + lane + 64));
     return h;
   }
 
@@ -844,12 +844,15 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
         if (lane == 0) s.out[Dm::RQ_W * c + i] = bf16r(v);
       }
     }
-    // first batch of keys for the scores (the positions before pos are in the cache already)
     const int base0 = p.p_begin + 4 * c;
-    u32x4 kk[U];
-    kv_load(kc, kk, base0);
     cstamp(L, 1);
     QMK_SYNC();  // b
+    // Loads are issued while the control wave exchanges (issuing 16-byte loads
+    // is paced by the CU's load path, so doing it inside a compute phase would
+    // lengthen the critical path).  First batch of keys for the scores; the
+    // positions before pos are in the cache already.
+    u32x4 kk[U];
+    kv_load(kc, kk, base0);
     QMK_SYNC();  // c
     cstamp(L, 2);
     // ------------------------------------------------ scores and local (max, sum)
@@ -904,10 +907,10 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
         }
       }
     }
-    u32x4 vv[U];
-    kv_load(vc, vv, base0);
     cstamp(L, 3);
     QMK_SYNC();  // d
+    u32x4 vv[U];
+    kv_load(vc, vv, base0);
     QMK_SYNC();  // e
     cstamp(L, 4);
     // ------------------------------------------------ probabilities and P@V

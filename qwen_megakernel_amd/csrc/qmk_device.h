@@ -142,12 +142,26 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint3
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, bytes, 0x00020000);
 }
 
-// Streaming 16-byte weight load (non-temporal: weights are read once per token).
-__device__ __forceinline__ u32x4 ld_stream(const void* p) {
-  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+// Global-memory loads.  Pointers that reach the kernel through the LDS copy of
+// the layer table are generic, and a generic load compiles to a FLAT
+// instruction, which also counts in lgkmcnt; the s_waitcnt lgkmcnt(0) of every
+// workgroup barrier would then wait for all weight prefetches in flight.  The
+// address-space cast makes these VMEM-only (global_load), so only the
+// instructions that consume the data wait for it.
+template <class T>
+using gptr = const __attribute__((address_space(1))) T*;
+
+template <class T>
+__device__ __forceinline__ gptr<T> as_global(const void* p) {
+  return (gptr<T>)(p);
 }
 
-__device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+// Streaming 16-byte weight load (non-temporal: weights are read once per token).
+__device__ __forceinline__ u32x4 ld_stream(const void* p) { return __builtin_nontemporal_load(as_global<u32x4>(p)); }
+
+__device__ __forceinline__ u32x4 ld16(const void* p) { return *as_global<u32x4>(p); }
+__device__ __forceinline__ uint32_t ld32(const void* p) { return *as_global<uint32_t>(p); }
+__device__ __forceinline__ uint32_t ldu16(const void* p) { return *as_global<uint16_t>(p); }
 
 // ------------------------------------------------------- tagged exchange
 
