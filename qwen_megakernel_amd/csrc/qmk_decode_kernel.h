@@ -471,24 +471,24 @@ __device__ __forceinline__ uint32_t orderable16(uint32_t h) { return (h & 0x8000
 
 // ------------------------------------------------------------- the kernel
 //
-// Barrier schedule (both roles execute the same s_barrier sequence; each role
-// has its own loop so that the compute waves' weight registers and the
-// control wave's poll buffers never share live ranges):
+// Barrier schedule (both roles execute the same s_barrier sequence, 9 per
+// layer; each role has its own loop so that the compute waves' weight
+// registers and the control wave's poll buffers never share live ranges).
+// Where a compute phase's result goes straight to other workgroups (QKV rows,
+// o_proj and down_proj partials) the compute waves publish it themselves and
+// no barrier follows the phase: the control wave starts polling right away.
 //
 //   per layer   control wave                          compute waves
 //   ..a         h (or embedding row) -> RMSNorm        .
-//   a..b        .                                      QKV rows; K prefetch
-//   b..c        qkv exchange, q/k norm, RoPE, KV write .
+//   a..c        qkv exchange, q/k norm, RoPE, KV write QKV rows -> publish; K prefetch
 //   c..d        .                                      scores, local (max, sum)
-//   d..e        (max, sum) exchange -> global max/sum  .
+//   d..e        (max, sum) exchange -> global max/sum  V prefetch
 //   e..f        .                                      probabilities, P@V
 //   f..g        acc exchange, combine, attn exchange   .
-//   g..h        .                                      o_proj partial rows
-//   h..i        o reduce-scatter, h' exchange, norm    .
+//   g..i        o reduce-scatter, h' exchange, norm    o_proj partial rows -> publish
 //   i..j        .                                      gate/up rows
 //   j..k        m exchange                             .
-//   k..l        .                                      down_proj partial rows
-//   l..a'       d reduce-scatter, h'' publish          .
+//   k..a'       d reduce-scatter, h'' publish          down_proj partial rows -> publish
 //   final       gather h, final norm | LM-head rows | argmax keys, WG 0 picks the token
 
 #define QMK_SYNC()            \
@@ -543,19 +543,14 @@ __device__ __forceinline__ void control_path(const KArgs& a, Smem<M>& s, const S
     }
     stamp(tp + 1);
     QMK_SYNC();  // a
-    QMK_SYNC();  // b
     stamp(tp + 2);
-    // ------------------------------------------------------------ b..c  qkv
+    // ------------------------------------------------------------ a..c  qkv (the compute waves publish their rows)
     {
       const uint32_t t = tag_of(L, 0);
       const uint16_t* cosr = a.cos_t + (size_t)p.pos * Dm::D;
       const uint16_t* sinr = a.sin_t + (size_t)p.pos * Dm::D;
       const auto hq = ctl.load_head(w.q_norm, cosr, sinr);
       const auto hk = ctl.load_head(w.k_norm, cosr, sinr);
-      if (lane < Dm::RQ_WG / 4) {
-        const float* o = s.out + 4 * lane;
-        ctl.put_bf16x4(true, Dm::X_QKV + xcd * Dm::RG + Dm::RQ_WG * r + 4 * lane, o[0], o[1], o[2], o[3], t);
-      }
       if (ctl.template gather_range<Dm::RG>(Dm::X_QKV + xcd * Dm::RG, t, to_f32(s.qkv))) {
 #pragma unroll
         for (int h = 0; h < Dm::GQ; h++) ctl.head_norm_rope(h * Dm::D, hq, s.q + h * Dm::D);
@@ -669,14 +664,11 @@ __device__ __forceinline__ void control_path(const KArgs& a, Smem<M>& s, const S
     }
     stamp(tp + 7);
     QMK_SYNC();  // g
-    QMK_SYNC();  // h
     stamp(tp + 8);
-    // ------------------------------------------------------------ h..i  o reduce-scatter, h', norm
+    // ------------------------------------------------------------ g..i  o reduce-scatter (the compute waves publish
+    //                                                                    the partials), h', norm
     {
       const auto nw_post = ctl.load_norm(w.post_ln);
-      if (lane < Dm::ROWS_WG / 2)
-        ctl.put_f32x2(false, Dm::X_O + (uint32_t)((xcd * kGroupSize + r) * Dm::ROWS_WG * 2 + 4 * lane),
-                      s.out[2 * lane], s.out[2 * lane + 1], tag_of(L, 4));
       if (ctl.reduce_rows(Dm::X_O, tag_of(L, 4), s.x, Dm::X_H2, tag_of(L, 5), xcd, r) &&
           ctl.template gather_range<Dm::H>(Dm::X_H2 + xcd * Dm::H, tag_of(L, 5), to_f32(s.h2)))
         ctl.rmsnorm(s.h2, nw_post);
@@ -703,12 +695,9 @@ __device__ __forceinline__ void control_path(const KArgs& a, Smem<M>& s, const S
     }
     stamp(tp + 11);
     QMK_SYNC();  // k
-    QMK_SYNC();  // l
     stamp(tp + 12);
-    // ------------------------------------------------------------ l..a'  d reduce-scatter, h''
-    if (lane < Dm::ROWS_WG / 2)
-      ctl.put_f32x2(false, Dm::X_D + (uint32_t)((xcd * kGroupSize + r) * Dm::ROWS_WG * 2 + 4 * lane),
-                    s.out[2 * lane], s.out[2 * lane + 1], tag_of(L, 7));
+    // ------------------------------------------------------------ k..a'  d reduce-scatter (the compute waves publish
+    //                                                                     the partials), h''
     ctl.reduce_rows(Dm::X_D, tag_of(L, 7), s.h2, Dm::X_H, tag_of(L, 8), xcd, r);
   }
 
@@ -836,21 +825,24 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
     QMK_SYNC();  // a
     cstamp(L, 0);
     {
+      // rows RQ_W*c, +1 of this workgroup's RQ_WG q/k/v rows, published as two words
+      static_assert(Dm::RQ_W == 2, "one 8-byte store per wave");
       u32x4 act[Dm::LH];
       load_act(act, s.n, 0, lane);
-#pragma unroll
-      for (int i = 0; i < Dm::RQ_W; i++) {
-        const float v = row_dot(wq[i], act);
-        if (lane == 0) s.out[Dm::RQ_W * c + i] = bf16r(v);
+      const float v0 = row_dot(wq[0], act);
+      const float v1 = row_dot(wq[1], act);
+      if (lane == 0) {
+        const uint32_t t = make_tag(p.epoch, (uint32_t)(L * Dm::NX + 0));
+        put2(a.x, Dm::X_QKV + xcd * Dm::RG + Dm::RQ_WG * r + Dm::RQ_W * c, word(f32_to_bf16(v0), t),
+             word(f32_to_bf16(v1), t), !a.xcd_local);
       }
     }
     const int base0 = p.p_begin + 4 * c;
     cstamp(L, 1);
-    QMK_SYNC();  // b
-    // Loads are issued while the control wave exchanges (issuing 16-byte loads
-    // is paced by the CU's load path, so doing it inside a compute phase would
-    // lengthen the critical path).  First batch of keys for the scores; the
-    // positions before pos are in the cache already.
+    // First batch of keys for the scores (the positions before pos are in the
+    // cache already), requested while the control wave exchanges q/k/v.  The
+    // weight prefetches stay inside the compute phases: issued during an
+    // exchange they delay its polls by as much as they would save here.
     u32x4 kk[U];
     kv_load(kc, kk, base0);
     QMK_SYNC();  // c
@@ -861,14 +853,15 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
 #pragma unroll
       for (int h = 0; h < Dm::GQ; h++) qv[h] = *reinterpret_cast<const u32x4*>(s.q + h * Dm::D + 8 * t16);
       const u32x4 k_now = *reinterpret_cast<const u32x4*>(s.k + 8 * t16);
-      float mrun[Dm::GQ], lrun[Dm::GQ];
+      // Scores of this wave's positions (to LDS) and their maximum; the keys of
+      // the next batch are requested before the current batch is used.
+      float mloc[Dm::GQ];
 #pragma unroll
-      for (int h = 0; h < Dm::GQ; h++) {
-        mrun[h] = -INFINITY;
-        lrun[h] = 0.f;
-      }
+      for (int h = 0; h < Dm::GQ; h++) mloc[h] = -INFINITY;
       for (int base = base0; base < p.p_end; base += 32 * U) {
-        if (base != base0) kv_load(kc, kk, base);
+        const bool more = base + 32 * U < p.p_end;
+        u32x4 kn[U];
+        if (more) kv_load(kc, kn, base + 32 * U);
 #pragma unroll
         for (int u = 0; u < U; u++) {
           if (base + 32 * u >= p.p_end) break;  // the rest of the batch is past this workgroup's range
@@ -880,30 +873,47 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
             sc = bf16r(bf16r(sc) * a.attn_scale);
             if (pp < p.p_end) {
               if (t16 == 0) s.sc[h][pp - p.p_begin] = sc;
-              const float mn = fmaxf(mrun[h], sc);
-              lrun[h] = lrun[h] * exp_acc(mrun[h] - mn) + exp_acc(sc - mn);
-              mrun[h] = mn;
+              mloc[h] = fmaxf(mloc[h], sc);
             }
           }
         }
+        if (more) {
+#pragma unroll
+          for (int u = 0; u < U; u++) kk[u] = kn[u];
+        }
       }
-      // merge the wave's four slots (16-lane rows): rows 2k,2k+1, then the halves
+      // wave maximum over the four 16-lane rows, then the sum of exp(s - max)
+      // with one exponential per position
 #pragma unroll
       for (int h = 0; h < Dm::GQ; h++) {
+        float x, y;
+        swap16(mloc[h], x, y);
+        mloc[h] = fmaxf(x, y);
+        swap32(mloc[h], x, y);
+        mloc[h] = fmaxf(x, y);
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      float lsum[Dm::GQ];
 #pragma unroll
-        for (int step = 0; step < 2; step++) {
-          float ma, mb, la, lb;
-          if (step == 0) { swap16(mrun[h], ma, mb); swap16(lrun[h], la, lb); }
-          else { swap32(mrun[h], ma, mb); swap32(lrun[h], la, lb); }
-          const float mn = fmaxf(ma, mb);
-          const float fa = ma == -INFINITY ? 0.f : exp_acc(ma - mn);
-          const float fb = mb == -INFINITY ? 0.f : exp_acc(mb - mn);
-          lrun[h] = la * fa + lb * fb;
-          mrun[h] = mn;
+      for (int h = 0; h < Dm::GQ; h++) lsum[h] = 0.f;
+      for (int base = base0; base < p.p_end; base += 32 * U) {
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+          const int pp = base + 32 * u + slot;
+          if (pp < p.p_end) {
+#pragma unroll
+            for (int h = 0; h < Dm::GQ; h++) lsum[h] += exp_acc(s.sc[h][pp - p.p_begin] - mloc[h]);
+          }
         }
+      }
+#pragma unroll
+      for (int h = 0; h < Dm::GQ; h++) {
+        lsum[h] = rows_sum4(lsum[h]);  // rows hold different positions; lanes of a row the same one
         if (lane == 0) {
-          s.wml[c][h][0] = mrun[h];
-          s.wml[c][h][1] = lrun[h];
+          s.wml[c][h][0] = mloc[h];
+          s.wml[c][h][1] = lsum[h];
         }
       }
     }
@@ -928,7 +938,9 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
 #pragma unroll
         for (int i = 0; i < 8; i++) acc[h][i] = 0.f;
       for (int base = base0; base < p.p_end; base += 32 * U) {
-        if (base != base0) kv_load(vc, vv, base);
+        const bool more = base + 32 * U < p.p_end;
+        u32x4 vn[U];
+        if (more) kv_load(vc, vn, base + 32 * U);
 #pragma unroll
         for (int u = 0; u < U; u++) {
           if (base + 32 * u >= p.p_end) break;
@@ -945,6 +957,10 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
               for (int i = 0; i < 8; i++) acc[h][i] += pr * vf[i];
             }
           }
+        }
+        if (more) {
+#pragma unroll
+          for (int u = 0; u < U; u++) vv[u] = vn[u];
         }
       }
       // sum the wave's four slots; lanes 0..15 then hold dims 8*t16..+7
@@ -964,12 +980,16 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
     QMK_SYNC();  // g
     cstamp(L, 6);
     {
+      // o_proj partial of row ROWS_W*c + slot of this workgroup's rows, to every XCD's reducer
       const float v = seg_dot(wo, s.attn, t16);
-      if (t16 == 0) s.out[Dm::ROWS_W * c + slot] = v;
+      if (t16 == 0) {
+        const uint32_t t = make_tag(p.epoch, (uint32_t)(L * Dm::NX + 4));
+        put2(a.x, Dm::X_O + (uint32_t)((xcd * kGroupSize + r) * Dm::ROWS_WG + Dm::ROWS_W * c + slot) * 2,
+             f32_hi_word(v, t), f32_lo_word(v, t), true);
+      }
     }
     if (L + 1 < p.nl) prefetch_o(L + 1);
     cstamp(L, 7);
-    QMK_SYNC();  // h
     QMK_SYNC();  // i
     cstamp(L, 8);
     {
@@ -988,11 +1008,14 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
     cstamp(L, 10);
     {
       const float v = seg_dot(wd, s.m, t16);
-      if (t16 == 0) s.out[Dm::ROWS_W * c + slot] = v;
+      if (t16 == 0) {
+        const uint32_t t = make_tag(p.epoch, (uint32_t)(L * Dm::NX + 7));
+        put2(a.x, Dm::X_D + (uint32_t)((xcd * kGroupSize + r) * Dm::ROWS_WG + Dm::ROWS_W * c + slot) * 2,
+             f32_hi_word(v, t), f32_lo_word(v, t), true);
+      }
     }
     if (L + 1 < p.nl) prefetch_dn(L + 1);
     cstamp(L, 11);
-    QMK_SYNC();  // l
   }
 
   QMK_SYNC();  // final a

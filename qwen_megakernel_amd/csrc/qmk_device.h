@@ -195,6 +195,23 @@ __device__ __forceinline__ void put4(uint32_t* buf, uint32_t w, u32x4 v) {
     __builtin_amdgcn_raw_buffer_store_b128(v, rs, w * 4u, 0, 0);
 }
 
+// Two words (8 bytes) at word index ``w`` (even), same scopes as put4.
+__device__ __forceinline__ void put2(uint32_t* buf, uint32_t w, uint32_t w0, uint32_t w1, bool device) {
+  typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+  auto rs = make_rsrc(buf, 0x7fffffffu);
+  u32x2 v;
+  v.x = w0;
+  v.y = w1;
+  if (device)
+    __builtin_amdgcn_raw_buffer_store_b64(v, rs, w * 4u, 0, 0x10 /* sc1 */);
+  else
+    __builtin_amdgcn_raw_buffer_store_b64(v, rs, w * 4u, 0, 0);
+}
+
+// An fp32 value as two tagged words: high 16 bits first, then the low 16 bits.
+__device__ __forceinline__ uint32_t f32_hi_word(float v, uint32_t tag) { return (__float_as_uint(v) & 0xffff0000u) | tag; }
+__device__ __forceinline__ uint32_t f32_lo_word(float v, uint32_t tag) { return (__float_as_uint(v) << 16) | tag; }
+
 __device__ __forceinline__ void put1_device(uint32_t* p, uint32_t v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }

@@ -25,18 +25,18 @@ TICK_US = 0.01         # 100 MHz
 # control-wave segments: stamp k -> k+1 inside a layer, then the hand-off to the next layer
 CTL_SEGMENTS = [
     "gather h + RMSNorm",
-    "QKV rows (compute waves)",
-    "qkv exchange + q/k norm + RoPE + KV append",
+    "barrier a (wake-up)",
+    "QKV rows + qkv exchange + q/k norm + RoPE + KV append",
     "scores (compute waves)",
     "softmax (max, sum) exchange",
     "probabilities + P@V (compute waves)",
     "P@V partial exchange + combine + attention-output exchange",
-    "o_proj partial rows (compute waves)",
-    "o reduce-scatter across XCDs + h' exchange + RMSNorm",
+    "barrier g (wake-up)",
+    "o_proj rows + o reduce-scatter across XCDs + h' exchange + RMSNorm",
     "gate/up rows (compute waves)",
     "SiLU*up + m exchange",
-    "down_proj partial rows (compute waves)",
-    "d reduce-scatter across XCDs + publish h''",
+    "barrier k (wake-up)",
+    "down_proj rows + d reduce-scatter across XCDs + publish h''",
 ]
 COMPUTE_PHASES = ["QKV", "scores", "P@V", "O", "gate/up", "down"]
 CTL_READY = [1, 3, 5, 7, 9, 11]  # control stamp after which each compute phase may start
