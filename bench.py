@@ -14,6 +14,11 @@ prompt re-prefilled), so the K timed steps always cover contexts 129..128+K.
 average launch duration measured with HIP events on the launch stream.
 ``cpu_baseline`` times the CPU oracle (HF-semantics bf16 decode) on the host.
 
+``phases`` (skip with ``--no-phases``) is the per-phase weight-streaming
+microbenchmark: each GEMV phase of the step (RMSNorm + QKV, O, gate/up +
+SiLU*mul, down, LM head + argmax) run alone over >= 1 GiB of rotating seeded
+N(0, 0.02) weight copies with N(0, 1) activations, in GB/s.
+
 Options for profiling runs: ``--phase-trace`` adds the in-kernel phase trace
 of one more step (at the last timed context) to the JSON line;
 ``--copy-calibration`` first runs a plain 1 GiB device-to-device copy five
@@ -87,6 +92,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-steps", type=int, default=32)
     ap.add_argument("--phase-trace", action="store_true")
+    ap.add_argument("--no-phases", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -189,10 +195,23 @@ def main():
         summ["context"] = last + 1
         result["phase_trace"] = summ
         log(f"phase trace at context {last + 1}:\n" + trace.format_table(summ))
+    if not args.no_phases:
+        from qwen_megakernel_amd import phases as P
+
+        del dec, w
+        torch.cuda.empty_cache()
+        result["phases"] = {}
+        for ph in P.phases():
+            r = P.bench(ph)
+            r["frac_of_peak"] = round(r["GBps"] / PEAK_HBM_GBS, 4)
+            result["phases"][ph.name] = r
+            log(f"phase {ph.name:18s} {r['GBps']:8.1f} GB/s ({r['us_per_copy']:.2f} us per "
+                f"{ph.bytes / 1e6:.1f} MB copy, {r['copies']} copies)")
+            torch.cuda.empty_cache()
     log(f"decode: {value:.1f} tok/s, {dt * 1e3 / args.steps:.3f} ms/token, kernel avg {avg_launch_s * 1e6:.1f} us, "
         f"{achieved:.0f} GB/s algorithmic")
     if not args.no_cpu_baseline:
-        del dec, w
+        dec = w = None
         torch.cuda.empty_cache()
         t0 = time.time()
         result["cpu_baseline"] = cpu_baseline(args.cpu_steps)

@@ -161,6 +161,28 @@ size_t qmk_trace_entries(int num_layers);
  * in[lane].  n >= 64; out holds 2n + 320 floats.  Asynchronous. */
 int qmk_selftest_blocks(const float *in, float *out, int n, hipStream_t stream);
 
+/* Per-phase weight-streaming microbenchmark.  Runs one GEMV phase of the
+ * decode step over n_copies distinct weight copies laid out one after another
+ * (qmk_phase_copy_elems(phase) bf16 elements each), with the decode kernel's
+ * work split and one-copy-ahead prefetch, so the phase's HBM rate can be
+ * measured on its own.  Phases:
+ *   0 QKV      RMSNorm(act[1024], norm_weight) then [4096][1024] (q, k, v rows);
+ *              out bf16[4096]
+ *   1 O        [1024][2048] x act[2048]; out f32[8][1024] per-XCD partial sums
+ *              over input columns [256x, 256x+256)
+ *   2 GATE_UP  gate [3072][1024] then up [3072][1024] x act[1024];
+ *              out bf16[3072] = bf16(bf16(silu(g)) * u)
+ *   3 DOWN     [1024][3072] x act[3072]; out f32[8][1024] partials over
+ *              columns [384x, 384x+384)
+ *   4 LM_HEAD  [151936][1024] x act[1024]; out uint64[256*8] per-wave best
+ *              keys (orderable bf16 logit << 32 | ~row): the largest key is
+ *              the argmax
+ * out holds the last copy's results.  Asynchronous; returns a status code. */
+int qmk_phase_bench(int phase, const void *weights, int n_copies,
+                    const void *norm_weight, const void *act, void *out,
+                    hipStream_t stream);
+size_t qmk_phase_copy_elems(int phase);
+
 /* Kernel launch geometry, for tools: workgroups and threads per workgroup. */
 void qmk_launch_geometry(int *workgroups, int *threads);
 

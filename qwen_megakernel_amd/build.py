@@ -46,7 +46,7 @@ HIP_FLAGS = [
     f"-I{_INCLUDE}",
 ]
 
-_LIB_SOURCES = ["qmk_api.hip", "qmk_decode_kernel.h", "qmk_device.h", "qmk_state.h"]
+_LIB_SOURCES = ["qmk_api.hip", "qmk_decode_kernel.h", "qmk_device.h", "qmk_state.h", "qmk_phase_bench.h"]
 _OPS_SOURCES = ["torch_bindings.cpp"]
 
 _module = None

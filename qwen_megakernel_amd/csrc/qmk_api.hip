@@ -16,6 +16,7 @@
 
 #include "../../include/qwen_megakernel.h"
 #include "qmk_decode_kernel.h"
+#include "qmk_phase_bench.h"
 
 namespace qmk {
 namespace {
@@ -232,6 +233,22 @@ int decode_impl(const Common& c, int token, int position, int* out_token, float*
   return fail(launch(a, stream));
 }
 
+size_t phase_copy_elems(int phase) {
+  switch (phase) {
+    case kPhaseQKV: return (size_t)(Dm::QS + 2 * Dm::NKV * Dm::D) * Dm::H;
+    case kPhaseO: return (size_t)Dm::H * Dm::QS;
+    case kPhaseGateUp: return (size_t)2 * Dm::I * Dm::H;
+    case kPhaseDown: return (size_t)Dm::H * Dm::I;
+    case kPhaseLmHead: return (size_t)Dm::V * Dm::H;
+    default: return 0;
+  }
+}
+
+template <int P>
+void launch_phase(const PhaseArgs& pa, hipStream_t stream) {
+  hipLaunchKernelGGL((phase_kernel<Model, P>), dim3(kNumWG), dim3(kBlock), 0, stream, pa);
+}
+
 }  // namespace
 }  // namespace qmk
 
@@ -380,6 +397,32 @@ size_t qmk_trace_entries(int num_layers) {
 int qmk_selftest_blocks(const float* in, float* out, int n, hipStream_t stream) {
   if (!in || !out || n < 64) return fail(QMK_ERR_ARG);
   hipLaunchKernelGGL(selftest_kernel, dim3(1), dim3(64), 0, stream, in, out, n);
+  return fail(hipGetLastError() == hipSuccess ? QMK_OK : QMK_ERR_HIP);
+}
+
+size_t qmk_phase_copy_elems(int phase) { return phase_copy_elems(phase); }
+
+int qmk_phase_bench(int phase, const void* weights, int n_copies, const void* norm_weight, const void* act, void* out,
+                    hipStream_t stream) {
+  if (phase_copy_elems(phase) == 0 || !weights || n_copies < 1 || !act || !out || (phase == kPhaseQKV && !norm_weight))
+    return fail(QMK_ERR_ARG);
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess) return fail(QMK_ERR_HIP);
+  {
+    std::lock_guard<std::mutex> lk(g_mu);
+    DevInfo* di = nullptr;
+    const int s = check_device(dev, &di);
+    if (s != QMK_OK) return fail(s);
+  }
+  PhaseArgs pa{static_cast<const uint16_t*>(weights), phase_copy_elems(phase), n_copies,
+               static_cast<const uint16_t*>(norm_weight), static_cast<const uint16_t*>(act), out, 1e-6f};
+  switch (phase) {
+    case kPhaseQKV: launch_phase<kPhaseQKV>(pa, stream); break;
+    case kPhaseO: launch_phase<kPhaseO>(pa, stream); break;
+    case kPhaseGateUp: launch_phase<kPhaseGateUp>(pa, stream); break;
+    case kPhaseDown: launch_phase<kPhaseDown>(pa, stream); break;
+    default: launch_phase<kPhaseLmHead>(pa, stream); break;
+  }
   return fail(hipGetLastError() == hipSuccess ? QMK_OK : QMK_ERR_HIP);
 }
 

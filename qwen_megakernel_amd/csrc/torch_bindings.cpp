@@ -8,7 +8,8 @@
 // position is range-checked before anything is launched; failures raise
 // through TORCH_CHECK instead of writing out of bounds.  Additive ops:
 // `decode_logits` (also returns the fp32 copy of the bf16 logits),
-// `device_error` and `reset`.
+// `device_error`, `reset`, `set_wait_limit`, `set_trace` (phase trace) and
+// `phase_bench` (per-phase weight-streaming microbenchmark).
 
 #include <Python.h>
 #include <ATen/hip/impl/HIPGuardImplMasqueradingAsCUDA.h>
@@ -223,6 +224,32 @@ void set_trace(std::optional<torch::Tensor> buf) {
   TORCH_CHECK(s == QMK_OK, "set_trace failed: ", qmk_status_string(s));
 }
 
+// Per-phase weight-streaming microbenchmark (qmk_phase_bench): `weights`
+// holds n_copies copies of the phase's matrices back to back.
+void phase_bench(int64_t phase, torch::Tensor weights, int64_t n_copies, std::optional<torch::Tensor> norm_weight,
+                 torch::Tensor act, torch::Tensor out) {
+  const size_t per = qmk_phase_copy_elems((int)phase);
+  TORCH_CHECK(per > 0, "phase must be 0 (QKV), 1 (O), 2 (GATE_UP), 3 (DOWN) or 4 (LM_HEAD)");
+  TORCH_CHECK(n_copies >= 1 && n_copies <= (1 << 20), "n_copies out of range");
+  check_bf16(weights, "weights", -1);
+  TORCH_CHECK(weights.numel() >= (int64_t)per * n_copies, "weights holds fewer than n_copies copies");
+  static const int64_t in_len[5] = {kHidden, kQ, kHidden, kInter, kHidden};
+  check_bf16(act, "act", in_len[phase]);
+  check_cuda(out, "out");
+  static const int64_t out_bytes[5] = {(kQ + 2 * kKV) * 2, 8 * kHidden * 4, kInter * 2, 8 * kHidden * 4, 256 * 8 * 8};
+  TORCH_CHECK(out.numel() * out.element_size() >= out_bytes[phase], "out is smaller than ", out_bytes[phase], " bytes");
+  const void* nw = nullptr;
+  if (phase == 0) {
+    TORCH_CHECK(norm_weight.has_value(), "phase 0 needs norm_weight");
+    check_bf16(*norm_weight, "norm_weight", kHidden);
+    nw = norm_weight->data_ptr();
+  }
+  const c10::hip::HIPGuardMasqueradingAsCUDA guard(weights.device());
+  const int s = qmk_phase_bench((int)phase, weights.data_ptr(), (int)n_copies, nw, act.data_ptr(), out.data_ptr(),
+                                c10::hip::getCurrentHIPStreamMasqueradingAsCUDA().stream());
+  TORCH_CHECK(s == QMK_OK, "phase_bench failed: ", qmk_status_string(s));
+}
+
 }  // namespace
 
 TORCH_LIBRARY(qwen_megakernel_C, ops) {
@@ -267,6 +294,8 @@ TORCH_LIBRARY(qwen_megakernel_C, ops) {
   ops.def("reset() -> ()", &reset);
   ops.def("set_wait_limit(int ticks) -> ()", &set_wait_limit);
   ops.def("set_trace(Tensor? buf) -> ()", &set_trace);
+  ops.def("phase_bench(int phase, Tensor weights, int n_copies, Tensor? norm_weight, Tensor act, Tensor out) -> ()");
+  ops.impl("phase_bench", torch::kCUDA, &phase_bench);
 }
 
 // Empty Python module so the shared object can also be imported by name
