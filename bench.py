@@ -12,7 +12,14 @@ prompt re-prefilled), so the K timed steps always cover contexts 129..128+K.
 ``roofline`` relates the decode kernel's algorithmic bytes per launch
 (weights + KV read + KV written, averaged over the timed contexts) to its
 average launch duration measured with HIP events on the launch stream.
-``cpu_baseline`` times the CPU oracle (HF-semantics bf16 decode) on the host.
+``cpu_baseline`` times the CPU oracle (HF-semantics bf16 decode) on the host,
+on a bounded sample of the same workload (the 128-token prompt, then 384
+greedy steps).
+
+``long_context`` (skip with ``--no-long-context``): the same model with the KV
+cache prefilled to 8192 and to 32768 positions with seeded N(0, 1) bf16 K/V
+(28 layers x 8 KV heads x 128 dims), then 256 device-fed greedy steps each,
+in tok/s and algorithmic GB/s (weights + KV read + KV written per token).
 
 ``phases`` (skip with ``--no-phases``) is the per-phase weight-streaming
 microbenchmark: each GEMV phase of the step (RMSNorm + QKV, O, gate/up +
@@ -48,8 +55,9 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def cpu_baseline(steps: int = 32):
-    """Oracle decode on the host: 16-token prompt fed, then `steps` timed greedy steps."""
+def cpu_baseline(steps: int = 384):
+    """The CPU oracle on a bounded sample of the bench workload: the same seeded weights and
+    128-token prompt (prefilled untimed), then `steps` timed greedy steps (context 129..)."""
     import torch
 
     from oracle.qwen3_ref import OracleDecoder
@@ -58,14 +66,12 @@ def cpu_baseline(steps: int = 32):
 
     threads = max(1, min(len(os.sched_getaffinity(0)), 16))
     torch.set_num_threads(threads)
-    w = make_weights(QWEN3_0_6B, seed=0, max_seq_len=128)
-    dec = OracleDecoder(w, QWEN3_0_6B, max_seq_len=128)
-    prompt = make_prompt(16, QWEN3_0_6B.vocab, seed=1)
+    w = make_weights(QWEN3_0_6B, seed=0, max_seq_len=PROMPT_LEN + steps + 8)
+    dec = OracleDecoder(w, QWEN3_0_6B, max_seq_len=PROMPT_LEN + steps + 8)
+    prompt = make_prompt(PROMPT_LEN, QWEN3_0_6B.vocab, seed=1)
     tok = None
     for t in prompt:
         tok = dec.step(t)
-    for _ in range(2):  # warm-up
-        tok = dec.step(tok)
     t0 = time.perf_counter()
     for _ in range(steps):
         tok = dec.step(tok)
@@ -80,8 +86,52 @@ def cpu_baseline(steps: int = 32):
     except OSError:
         pass
     return {"value": round(steps / dt, 3), "unit": "tok/s", "cores": threads, "kind": "port",
-            "sample": f"CPU oracle (HF-semantics bf16 PyTorch decode), Qwen3-0.6B, 16-token prompt, "
-                      f"{steps} greedy steps timed at context 19..{18 + steps}; {cpu}"}
+            "sample": f"CPU oracle (HF-semantics bf16 PyTorch decode, torch CPU ops), Qwen3-0.6B seeded weights, "
+                      f"{PROMPT_LEN}-token prompt prefilled untimed, {steps} greedy steps timed at context "
+                      f"{PROMPT_LEN + 1}..{PROMPT_LEN + steps} ({dt:.1f} s); {cpu}"}
+
+
+def long_context(w, steps: int, contexts=(8192, 32768)):
+    """Decode `steps` device-fed greedy tokens after a KV cache prefilled with N(0, 1) K/V."""
+    import torch
+
+    from qwen_megakernel_amd.model import Decoder
+    from qwen_megakernel_amd.shapes import QWEN3_0_6B as S
+    from qwen_megakernel_amd.weights import rope_tables
+
+    out = {}
+    max_seq = max(contexts) + steps + 64
+    ww = dict(w)
+    cos, sin = rope_tables(max_seq, S.head_dim, 1e6)
+    ww["cos_table"], ww["sin_table"] = cos.cuda(), sin.cuda()
+    dec = Decoder(weights=ww, verbose=False, max_seq_len=max_seq)
+    ops = torch.ops.qwen_megakernel_C
+    shp = (S.num_layers, S.num_kv_heads, max(contexts), S.head_dim)
+    g = torch.Generator(device="cuda").manual_seed(2)
+    k = torch.randn(shp, generator=g, device="cuda").to(torch.bfloat16)
+    v = torch.randn(shp, generator=g, device="cuda").to(torch.bfloat16)
+    for c0 in contexts:
+        dec.reset()
+        dec.load_kv(k, v, c0)
+        ops.generate_nosync(11, 4, *dec._scratch(), S.num_layers, c0, max_seq, dec._attn_scale)  # warm-up
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        stream = torch.cuda.current_stream()
+        torch.cuda.synchronize()
+        e0.record(stream)
+        ops.generate_nosync(11, steps, *dec._scratch(), S.num_layers, c0 + 4, max_seq, dec._attn_scale)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        assert int(ops.device_error()) == 0
+        t = e0.elapsed_time(e1) / 1e3 / steps
+        mean_c = c0 + 5 + (steps - 1) / 2.0
+        byts = S.weight_bytes_per_token() + S.kv_bytes_per_position() * (mean_c + 1)
+        out[str(c0)] = {"tok_per_s": round(1.0 / t, 2), "ms_per_token": round(t * 1e3, 4), "steps": steps,
+                        "context": f"{c0 + 5}..{c0 + 4 + steps}", "achieved_GBps": round(byts / t / 1e9, 1),
+                        "roofline_frac": round(byts / t / 1e9 / PEAK_HBM_GBS, 4)}
+        log(f"long context {c0}: {1.0 / t:.1f} tok/s, {byts / t / 1e9:.0f} GB/s algorithmic")
+    del dec, k, v
+    torch.cuda.empty_cache()
+    return out
 
 
 def main():
@@ -90,9 +140,11 @@ def main():
     ap.add_argument("--steps", type=int, default=1024)
     ap.add_argument("--warmup", type=int, default=32)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-steps", type=int, default=32)
+    ap.add_argument("--cpu-steps", type=int, default=384)
     ap.add_argument("--phase-trace", action="store_true")
     ap.add_argument("--no-phases", action="store_true")
+    ap.add_argument("--no-long-context", action="store_true")
+    ap.add_argument("--long-steps", type=int, default=256)
     ap.add_argument("--copy-calibration", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -195,11 +247,15 @@ def main():
         summ["context"] = last + 1
         result["phase_trace"] = summ
         log(f"phase trace at context {last + 1}:\n" + trace.format_table(summ))
+    del dec  # frees the 128-token run's caches; the weights stay for the long-context runs
+    torch.cuda.empty_cache()
+    if not args.no_long_context:
+        result["long_context"] = long_context(w, args.long_steps)
+    del w
+    torch.cuda.empty_cache()
     if not args.no_phases:
         from qwen_megakernel_amd import phases as P
 
-        del dec, w
-        torch.cuda.empty_cache()
         result["phases"] = {}
         for ph in P.phases():
             r = P.bench(ph)
@@ -211,8 +267,6 @@ def main():
     log(f"decode: {value:.1f} tok/s, {dt * 1e3 / args.steps:.3f} ms/token, kernel avg {avg_launch_s * 1e6:.1f} us, "
         f"{achieved:.0f} GB/s algorithmic")
     if not args.no_cpu_baseline:
-        dec = w = None
-        torch.cuda.empty_cache()
         t0 = time.time()
         result["cpu_baseline"] = cpu_baseline(args.cpu_steps)
         log(f"cpu baseline {result['cpu_baseline']['value']} tok/s ({time.time() - t0:.1f}s)")

@@ -65,6 +65,8 @@ constexpr int kChunkMax = kMaxSeqLen / kGroupSize;         // attention position
 constexpr int kTracePoints = 13;                           // control-wave stamps per layer
 constexpr int kComputePoints = 12;                         // compute-wave stamps per layer (start/end of 6 phases)
 constexpr int kMaxLayers = 28;
+constexpr int kKvU = 2;        // attention: each wave covers 4 positions (16-lane rows) x kKvU per batch
+constexpr int kKvStages = 4;   // K/V batches in flight per wave (LDS ring)
 
 template <class M>
 struct Dims {
@@ -184,6 +186,7 @@ struct Smem {
   uint16_t k[Dm::D];
   uint16_t v[Dm::D];
   float sc[Dm::GQ][kChunkMax];       // this workgroup's attention scores (bf16 values)
+  u32x4 kv[kKvStages][kComputeWaves][kKvU][kWave];  // K/V batches, written by the loads themselves (LDS DMA)
   float wml[kComputeWaves][Dm::GQ][2];
   float wacc[kComputeWaves][Dm::GQ][Dm::D];
   float ml[Dm::GQ][2];               // global softmax max and sum per head
@@ -808,18 +811,33 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
   auto cstamp = [&](int L, int k) {
     if (ctrace && c == 0 && lane == 0) ctrace[(size_t)(L * kComputePoints + k) * kNumWG + b] = wall_clock64();
   };
-  constexpr int U = 2;  // attention: each wave covers 4 positions per step, U steps per batch
+  constexpr int U = kKvU;
+  auto base0_of = [&](int wave_c) { return p.p_begin + 4 * wave_c; };  // first position of a wave's batches
   for (int L = 0; L < p.nl; L++) {
     const uint16_t* kc = a.k_cache + L * kv_layer_stride + (size_t)xcd * a.max_seq_len * Dm::D;
     const uint16_t* vc = a.v_cache + L * kv_layer_stride + (size_t)xcd * a.max_seq_len * Dm::D;
-    auto kv_load = [&](const uint16_t* base, u32x4 (&dst)[U], int bpos) {
+    // K/V batches go straight from HBM into this wave's slots of an LDS ring
+    // (kKvStages batches in flight) and are read back with the same lane
+    // layout: lane (slot, t16) holds dims 8*t16..+7 of position base + 32u + slot.
+    const int nb = base0_of(c) < p.p_end ? (p.p_end - base0_of(c) + 32 * U - 1) / (32 * U) : 0;  // batches of this wave
+    auto kv_issue = [&](const uint16_t* base, int j) {
+      const int bpos = base0_of(c) + 32 * U * j;
 #pragma unroll
       for (int u = 0; u < U; u++) {
         const int pp = bpos + 32 * u + slot;
         // positions outside this workgroup's range (and pos, whose K/V come from
         // LDS) load row 0, which every cache has; their values are never used
         const int pl = (pp < p.p_end && pp != p.pos) ? pp : 0;
-        dst[u] = ld16(base + (size_t)pl * Dm::D + 8 * t16);
+        __builtin_amdgcn_global_load_lds(as_global<void>(base + (size_t)pl * Dm::D + 8 * t16),
+                                         (__attribute__((address_space(3))) void*)&s.kv[j % kKvStages][c][u][0], 16, 0, 0);
+      }
+    };
+    // wait until batch j has landed: the batches issued after it may stay in flight
+    auto kv_wait = [&](int j) { wait_vmcnt(U * min(kKvStages - 1, nb - 1 - j)); };
+    auto kv_refill = [&](const uint16_t* base, int j) {
+      if (j + kKvStages < nb) {
+        __builtin_amdgcn_s_waitcnt(kWaitLgkm0);  // this wave's reads of the slot are done
+        kv_issue(base, j + kKvStages);
       }
     };
     QMK_SYNC();  // a
@@ -837,15 +855,17 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
              word(f32_to_bf16(v1), t), !a.xcd_local);
       }
     }
-    const int base0 = p.p_begin + 4 * c;
+    const int base0 = base0_of(c);
     cstamp(L, 1);
-    // First batch of keys for the scores (the positions before pos are in the
-    // cache already), requested while the control wave exchanges q/k/v.  The
-    // weight prefetches stay inside the compute phases: issued during an
-    // exchange they delay its polls by as much as they would save here.
-    u32x4 kk[U];
-    kv_load(kc, kk, base0);
+    // Keys of the positions before pos are in the cache already.  Batch 0 is
+    // requested while the control wave exchanges q/k/v (the barrier below
+    // waits for it, as it waits for every LDS write); the rest of the ring
+    // fills after the barrier, behind the first batch's compute.  The weight
+    // prefetches stay inside the compute phases: issued during an exchange
+    // they delay its polls by as much as they would save here.
+    if (nb > 0) kv_issue(kc, 0);
     QMK_SYNC();  // c
+    for (int j = 1; j < min(nb, kKvStages); j++) kv_issue(kc, j);
     cstamp(L, 2);
     // ------------------------------------------------ scores and local (max, sum)
     {
@@ -858,15 +878,14 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
       float mloc[Dm::GQ];
 #pragma unroll
       for (int h = 0; h < Dm::GQ; h++) mloc[h] = -INFINITY;
-      for (int base = base0; base < p.p_end; base += 32 * U) {
-        const bool more = base + 32 * U < p.p_end;
-        u32x4 kn[U];
-        if (more) kv_load(kc, kn, base + 32 * U);
+      for (int j = 0; j < nb; j++) {
+        const int base = base0 + 32 * U * j;
+        kv_wait(j);
 #pragma unroll
         for (int u = 0; u < U; u++) {
           if (base + 32 * u >= p.p_end) break;  // the rest of the batch is past this workgroup's range
           const int pp = base + 32 * u + slot;
-          const u32x4 kx = pp == p.pos ? k_now : kk[u];
+          const u32x4 kx = pp == p.pos ? k_now : s.kv[j % kKvStages][c][u][lane];
 #pragma unroll
           for (int h = 0; h < Dm::GQ; h++) {
             float sc = row16_sum(dot8(kx, qv[h], 0.f));
@@ -877,11 +896,12 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
             }
           }
         }
-        if (more) {
-#pragma unroll
-          for (int u = 0; u < U; u++) kk[u] = kn[u];
-        }
+        kv_refill(kc, j);
       }
+      // Every K batch has landed (the last wait was vmcnt(0)); saying so here
+      // lets the compiler drop the vmcnt(0) it would otherwise put before the
+      // next workgroup barriers, which would also wait for weight prefetches.
+      wait_vmcnt(0);
       // wave maximum over the four 16-lane rows, then the sum of exp(s - max)
       // with one exponential per position
 #pragma unroll
@@ -898,7 +918,8 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
       float lsum[Dm::GQ];
 #pragma unroll
       for (int h = 0; h < Dm::GQ; h++) lsum[h] = 0.f;
-      for (int base = base0; base < p.p_end; base += 32 * U) {
+      for (int j = 0; j < nb; j++) {
+        const int base = base0 + 32 * U * j;
 #pragma unroll
         for (int u = 0; u < U; u++) {
           const int pp = base + 32 * u + slot;
@@ -919,9 +940,9 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
     }
     cstamp(L, 3);
     QMK_SYNC();  // d
-    u32x4 vv[U];
-    kv_load(vc, vv, base0);
+    if (nb > 0) kv_issue(vc, 0);
     QMK_SYNC();  // e
+    for (int j = 1; j < min(nb, kKvStages); j++) kv_issue(vc, j);
     cstamp(L, 4);
     // ------------------------------------------------ probabilities and P@V
     {
@@ -937,16 +958,15 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
       for (int h = 0; h < Dm::GQ; h++)
 #pragma unroll
         for (int i = 0; i < 8; i++) acc[h][i] = 0.f;
-      for (int base = base0; base < p.p_end; base += 32 * U) {
-        const bool more = base + 32 * U < p.p_end;
-        u32x4 vn[U];
-        if (more) kv_load(vc, vn, base + 32 * U);
+      for (int j = 0; j < nb; j++) {
+        const int base = base0 + 32 * U * j;
+        kv_wait(j);
 #pragma unroll
         for (int u = 0; u < U; u++) {
           if (base + 32 * u >= p.p_end) break;
           const int pp = base + 32 * u + slot;
           if (pp < p.p_end) {
-            const u32x4 vx = pp == p.pos ? v_now : vv[u];
+            const u32x4 vx = pp == p.pos ? v_now : s.kv[j % kKvStages][c][u][lane];
             const float vf[8] = {lo_bf16(vx.x), hi_bf16(vx.x), lo_bf16(vx.y), hi_bf16(vx.y),
                                  lo_bf16(vx.z), hi_bf16(vx.z), lo_bf16(vx.w), hi_bf16(vx.w)};
 #pragma unroll
@@ -958,11 +978,9 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
             }
           }
         }
-        if (more) {
-#pragma unroll
-          for (int u = 0; u < U; u++) vv[u] = vn[u];
-        }
+        kv_refill(vc, j);
       }
+      wait_vmcnt(0);  // every V batch has landed (see above)
       // sum the wave's four slots; lanes 0..15 then hold dims 8*t16..+7
 #pragma unroll
       for (int h = 0; h < Dm::GQ; h++) {
@@ -1065,7 +1083,7 @@ __global__ void __launch_bounds__(kBlock, 1) decode_kernel(KArgs a) {
   using Dm = Dims<M>;
   __shared__ Smem<M> s;
   const int b = blockIdx.x;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar branches on the role
   const int lane = threadIdx.x & 63;
 
   DecodeState* st = a.st;

@@ -163,6 +163,26 @@ __device__ __forceinline__ u32x4 ld16(const void* p) { return *as_global<u32x4>(
 __device__ __forceinline__ uint32_t ld32(const void* p) { return *as_global<uint32_t>(p); }
 __device__ __forceinline__ uint32_t ldu16(const void* p) { return *as_global<uint16_t>(p); }
 
+// s_waitcnt immediates (gfx9 encoding: vmcnt [3:0] + [15:14], expcnt [6:4],
+// lgkmcnt [11:8]); a field at its maximum does not wait.
+constexpr int kWaitLgkm0 = 0xF | (0x3 << 14) | (0x7 << 4);  // lgkmcnt(0) only
+
+// Waits until at most n vector-memory operations of this wave are outstanding
+// (n a small even count: the attention ring uses 0, 2, 4, 6).
+__device__ __forceinline__ void wait_vmcnt(int n) {
+  constexpr int kKeep = (0x7 << 4) | (0xF << 8);
+  switch (n) {
+    case 0: __builtin_amdgcn_s_waitcnt(0 | kKeep); break;
+    case 1: __builtin_amdgcn_s_waitcnt(1 | kKeep); break;
+    case 2: __builtin_amdgcn_s_waitcnt(2 | kKeep); break;
+    case 3: __builtin_amdgcn_s_waitcnt(3 | kKeep); break;
+    case 4: __builtin_amdgcn_s_waitcnt(4 | kKeep); break;
+    case 5: __builtin_amdgcn_s_waitcnt(5 | kKeep); break;
+    default: __builtin_amdgcn_s_waitcnt(6 | kKeep); break;
+  }
+  asm volatile("" ::: "memory");  // LDS written by the completed loads is read only after this point
+}
+
 // ------------------------------------------------------- tagged exchange
 
 constexpr uint32_t kTimeoutDefault = 100u * 1000u * 1000u;  // 1 s of the 100 MHz wall clock
