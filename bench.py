@@ -21,6 +21,10 @@ cache prefilled to 8192 and to 32768 positions with seeded N(0, 1) bf16 K/V
 (28 layers x 8 KV heads x 128 dims), then 256 device-fed greedy steps each,
 in tok/s and algorithmic GB/s (weights + KV read + KV written per token).
 
+``qwen3_1p7b`` (skip with ``--no-1p7b``): the Qwen3-1.7B shape (hidden 2048,
+MLP 6144, seeded N(0, 0.02) weights) on the same kernel: a 512-token prompt
+prefilled, then 256 device-fed greedy steps at batch 1 (context 513..768).
+
 ``phases`` (skip with ``--no-phases``) is the per-phase weight-streaming
 microbenchmark: each GEMV phase of the step (RMSNorm + QKV, O, gate/up +
 SiLU*mul, down, LM head + argmax) run alone over >= 1 GiB of rotating seeded
@@ -134,6 +138,40 @@ def long_context(w, steps: int, contexts=(8192, 32768)):
     return out
 
 
+def qwen3_1p7b(steps: int = 256, prompt_len: int = 512):
+    """Qwen3-1.7B: `prompt_len` tokens prefilled one step at a time, then `steps` device-fed steps."""
+    import torch
+
+    from qwen_megakernel_amd.model import Decoder
+    from qwen_megakernel_amd.shapes import QWEN3_1_7B as S
+    from qwen_megakernel_amd.weights import make_prompt, make_weights
+
+    max_seq = prompt_len + steps + 64
+    w = make_weights(S, seed=0, max_seq_len=max_seq, device="cuda")
+    dec = Decoder(weights=w, verbose=False, max_seq_len=max_seq)
+    ops = torch.ops.qwen_megakernel_C
+    prompt = make_prompt(prompt_len, S.vocab, seed=1)
+    for t in prompt[:-1]:
+        dec.step(t)
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    ops.generate_nosync(prompt[-1], steps, *dec._scratch(), S.num_layers, dec.position, max_seq, dec._attn_scale)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    assert int(ops.device_error()) == 0
+    t = e0.elapsed_time(e1) / 1e3 / steps
+    mean_c = prompt_len + (steps - 1) / 2.0
+    byts = S.weight_bytes_per_token() + S.kv_bytes_per_position() * (mean_c + 1)
+    del dec, w
+    torch.cuda.empty_cache()
+    log(f"qwen3-1.7b: {1.0 / t:.1f} tok/s, {byts / t / 1e9:.0f} GB/s algorithmic")
+    return {"tok_per_s": round(1.0 / t, 2), "ms_per_token": round(t * 1e3, 4), "batch": 1, "steps": steps,
+            "context": f"{prompt_len}..{prompt_len + steps - 1}", "bytes_per_token": int(byts),
+            "achieved_GBps": round(byts / t / 1e9, 1), "roofline_frac": round(byts / t / 1e9 / PEAK_HBM_GBS, 4)}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -145,6 +183,7 @@ def main():
     ap.add_argument("--no-phases", action="store_true")
     ap.add_argument("--no-long-context", action="store_true")
     ap.add_argument("--long-steps", type=int, default=256)
+    ap.add_argument("--no-1p7b", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -253,6 +292,8 @@ def main():
         result["long_context"] = long_context(w, args.long_steps)
     del w
     torch.cuda.empty_cache()
+    if not args.no_1p7b:
+        result["qwen3_1p7b"] = qwen3_1p7b()
     if not args.no_phases:
         from qwen_megakernel_amd import phases as P
 

@@ -129,6 +129,34 @@ int qmk_decode_logits(
     void *hidden_buffer, void *g_normalized, int num_layers, int position,
     int max_seq_len, float attn_scale, hipStream_t stream);
 
+/* Model shapes for the *_model entry points.  The reference's launchers above
+ * serve Qwen3-0.6B, the model the reference is written for. */
+enum {
+  QMK_MODEL_QWEN3_0_6B = 0, /* 28 layers, hidden 1024, MLP 3072 */
+  QMK_MODEL_QWEN3_1_7B = 1, /* 28 layers, hidden 2048, MLP 6144 */
+};
+/* Both: 16 query heads, 8 KV heads, head_dim 128, vocab 151936, tied LM head;
+ * tensors laid out as for the launchers above with the model's dimensions. */
+
+/* One decode step of `model` (and the fp32 copy of its bf16 logits when
+ * logits_out is not NULL).  Returns a status code.  Asynchronous. */
+int qmk_decode_model(
+    int model, int input_token_id, int *output_token_id, float *logits_out,
+    const void *embed_weight, const LDGLayerWeights *layer_weights,
+    const void *final_norm_weight, const void *lm_head_weight,
+    const void *cos_table, const void *sin_table, void *k_cache, void *v_cache,
+    void *hidden_buffer, void *g_normalized, int num_layers, int position,
+    int max_seq_len, float attn_scale, hipStream_t stream);
+
+/* launch_ldg_generate_nosync for `model`.  Returns a status code. */
+int qmk_generate_model(
+    int model, int first_token_id, int num_steps, const void *embed_weight,
+    const LDGLayerWeights *layer_weights, const void *final_norm_weight,
+    const void *lm_head_weight, const void *cos_table, const void *sin_table,
+    void *k_cache, void *v_cache, void *hidden_buffer, void *g_normalized,
+    int *output_log, int num_layers, int start_position, int max_seq_len,
+    float attn_scale, hipStream_t stream);
+
 /* Status of the last call made on this thread. */
 int qmk_last_status(void);
 const char *qmk_status_string(int status);

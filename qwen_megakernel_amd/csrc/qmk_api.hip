@@ -21,8 +21,11 @@
 namespace qmk {
 namespace {
 
-using Model = Qwen3_0_6B;
+using Model = Qwen3_0_6B;  // the reference's model; the shape the reference launchers serve
 using Dm = Dims<Model>;
+// One exchange area per stream serves every model.
+constexpr uint32_t kXWords = Dims<Qwen3_0_6B>::X_WORDS > Dims<Qwen3_1_7B>::X_WORDS ? Dims<Qwen3_0_6B>::X_WORDS
+                                                                                    : Dims<Qwen3_1_7B>::X_WORDS;
 
 thread_local int t_status = QMK_OK;
 
@@ -96,11 +99,13 @@ int check_device(int dev, DevInfo** out) {
   di.checked = true;
   hipDeviceProp_t prop;
   if (hipGetDeviceProperties(&prop, dev) != hipSuccess) return QMK_ERR_HIP;
-  int occ = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, reinterpret_cast<const void*>(decode_kernel<Model>), kBlock, 0) !=
-      hipSuccess)
+  int occ = 0, occ17 = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, reinterpret_cast<const void*>(decode_kernel<Qwen3_0_6B>), kBlock,
+                                                   0) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ17, reinterpret_cast<const void*>(decode_kernel<Qwen3_1_7B>), kBlock,
+                                                   0) != hipSuccess)
     return QMK_ERR_HIP;
-  if (prop.multiProcessorCount < kNumWG || occ < 1) return QMK_ERR_DEVICE;
+  if (prop.multiProcessorCount < kNumWG || occ < 1 || occ17 < 1) return QMK_ERR_DEVICE;
   int khz = 0;
   if (hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev) == hipSuccess && khz > 0)
     di.ticks_per_s = (uint32_t)khz * 1000u;
@@ -136,7 +141,7 @@ int get_ctx(hipStream_t stream, Ctx** out) {
   c->device = dev;
   c->xcd_local = di->xcd_local;
   c->timeout = di->ticks_per_s;  // 1 second
-  const size_t bytes = sizeof(DecodeState) + (size_t)Dm::X_WORDS * 4;
+  const size_t bytes = sizeof(DecodeState) + (size_t)kXWords * 4;
   void* mem = nullptr;
   if (hipMalloc(&mem, bytes) != hipSuccess) {
     delete c;
@@ -156,6 +161,7 @@ int get_ctx(hipStream_t stream, Ctx** out) {
 }
 
 struct Common {
+  int model;  // QMK_MODEL_*
   const void* embed;
   const LDGLayerWeights* layers;
   const void* final_norm;
@@ -174,6 +180,7 @@ struct Common {
 int validate(const Common& c) {
   if (!c.embed || !c.layers || !c.final_norm || !c.lm_head || !c.cos_t || !c.sin_t || !c.k_cache || !c.v_cache)
     return QMK_ERR_ARG;
+  if (c.model != QMK_MODEL_QWEN3_0_6B && c.model != QMK_MODEL_QWEN3_1_7B) return QMK_ERR_ARG;
   if (c.num_layers < 1 || c.num_layers > 28 || c.max_seq_len < 1 || c.max_seq_len > kMaxSeqLen) return QMK_ERR_ARG;
   if (!(c.attn_scale > 0.f)) return QMK_ERR_ARG;
   return QMK_OK;
@@ -204,8 +211,11 @@ KArgs make_args(const Common& c, Ctx* ctx) {
   return a;
 }
 
-int launch(const KArgs& a, hipStream_t stream) {
-  hipLaunchKernelGGL(decode_kernel<Model>, dim3(kNumWG), dim3(kBlock), 0, stream, a);
+int launch(const KArgs& a, int model, hipStream_t stream) {
+  if (model == QMK_MODEL_QWEN3_1_7B)
+    hipLaunchKernelGGL(decode_kernel<Qwen3_1_7B>, dim3(kNumWG), dim3(kBlock), 0, stream, a);
+  else
+    hipLaunchKernelGGL(decode_kernel<Qwen3_0_6B>, dim3(kNumWG), dim3(kBlock), 0, stream, a);
   return hipGetLastError() == hipSuccess ? QMK_OK : QMK_ERR_HIP;
 }
 
@@ -230,7 +240,7 @@ int decode_impl(const Common& c, int token, int position, int* out_token, float*
     a.position = position;
     a.token = token;
   }
-  return fail(launch(a, stream));
+  return fail(launch(a, c.model, stream));
 }
 
 size_t phase_copy_elems(int phase) {
@@ -265,7 +275,7 @@ void launch_ldg_decode_direct(int input_token_id, int* output_token_id, const vo
                               int max_seq_len, float attn_scale, hipStream_t stream) {
   (void)g_activations; (void)g_residual; (void)g_q; (void)g_k; (void)g_v; (void)g_attn_out;
   (void)g_mlp_intermediate; (void)block_max_vals; (void)block_max_idxs;
-  Common c{embed_weight, layer_weights, final_norm_weight, lm_head_weight, cos_table, sin_table, k_cache, v_cache,
+  Common c{QMK_MODEL_QWEN3_0_6B, embed_weight, layer_weights, final_norm_weight, lm_head_weight, cos_table, sin_table, k_cache, v_cache,
            hidden_buffer, g_normalized, num_layers, max_seq_len, attn_scale};
   decode_impl(c, input_token_id, position, output_token_id, nullptr, stream, false);
 }
@@ -284,7 +294,7 @@ void launch_ldg_decode_persistent(int input_token_id, int* output_token_id, cons
     fail(QMK_ERR_ARG);
     return;
   }
-  Common c{embed_weight, layer_weights, final_norm_weight, lm_head_weight, cos_table, sin_table, k_cache, v_cache,
+  Common c{QMK_MODEL_QWEN3_0_6B, embed_weight, layer_weights, final_norm_weight, lm_head_weight, cos_table, sin_table, k_cache, v_cache,
            hidden_buffer, g_normalized, num_layers, max_seq_len, attn_scale};
   decode_impl(c, input_token_id, position, output_token_id, nullptr, stream, true);
 }
@@ -299,29 +309,46 @@ void launch_ldg_generate_nosync(int first_token_id, int num_steps, const void* e
                                 int max_seq_len, float attn_scale, hipStream_t stream) {
   (void)g_activations; (void)g_residual; (void)g_q; (void)g_k; (void)g_v; (void)g_attn_out;
   (void)g_mlp_intermediate; (void)block_max_vals; (void)block_max_idxs;
-  Common c{embed_weight, layer_weights, final_norm_weight, lm_head_weight, cos_table, sin_table, k_cache, v_cache,
+  qmk_generate_model(QMK_MODEL_QWEN3_0_6B, first_token_id, num_steps, embed_weight, layer_weights, final_norm_weight,
+                     lm_head_weight, cos_table, sin_table, k_cache, v_cache, hidden_buffer, g_normalized, output_log,
+                     num_layers, start_position, max_seq_len, attn_scale, stream);
+}
+
+int qmk_generate_model(int model, int first_token_id, int num_steps, const void* embed_weight,
+                       const LDGLayerWeights* layer_weights, const void* final_norm_weight, const void* lm_head_weight,
+                       const void* cos_table, const void* sin_table, void* k_cache, void* v_cache,
+                       void* hidden_buffer, void* g_normalized, int* output_log, int num_layers, int start_position,
+                       int max_seq_len, float attn_scale, hipStream_t stream) {
+  Common c{model, embed_weight, layer_weights, final_norm_weight, lm_head_weight, cos_table, sin_table, k_cache, v_cache,
            hidden_buffer, g_normalized, num_layers, max_seq_len, attn_scale};
   int s = validate(c);
-  if (s != QMK_OK) { fail(s); return; }
-  if (num_steps < 0 || !output_log) { fail(QMK_ERR_ARG); return; }
-  if (num_steps == 0) { fail(QMK_OK); return; }
+  if (s != QMK_OK) return fail(s);
+  if (num_steps < 0 || !output_log) return fail(QMK_ERR_ARG);
+  if (num_steps == 0) return fail(QMK_OK);
   // every step must stay inside the cache: the last one runs at start+num_steps-1
-  if (start_position < 0 || (long long)start_position + num_steps > (long long)max_seq_len) {
-    fail(QMK_ERR_POSITION);
-    return;
-  }
-  if (first_token_id < 0 || first_token_id >= Dm::V) { fail(QMK_ERR_ARG); return; }
+  if (start_position < 0 || (long long)start_position + num_steps > (long long)max_seq_len) return fail(QMK_ERR_POSITION);
+  if (first_token_id < 0 || first_token_id >= Dm::V) return fail(QMK_ERR_ARG);
   Ctx* ctx = nullptr;
-  if ((s = get_ctx(stream, &ctx)) != QMK_OK) { fail(s); return; }
-  if ((s = poisoned(ctx)) != QMK_OK) { fail(s); return; }
+  if ((s = get_ctx(stream, &ctx)) != QMK_OK) return fail(s);
+  if ((s = poisoned(ctx)) != QMK_OK) return fail(s);
   KArgs a = make_args(c, ctx);
   a.position = -1;
   a.out_log = output_log;
   hipLaunchKernelGGL(set_step_kernel, dim3(1), dim3(1), 0, stream, ctx->st, start_position, first_token_id);
   for (int i = 0; i < num_steps; i++) {
-    if ((s = launch(a, stream)) != QMK_OK) { fail(s); return; }
+    if ((s = launch(a, c.model, stream)) != QMK_OK) return fail(s);
   }
-  fail(QMK_OK);
+  return fail(QMK_OK);
+}
+
+int qmk_decode_model(int model, int input_token_id, int* output_token_id, float* logits_out,
+                     const void* embed_weight, const LDGLayerWeights* layer_weights, const void* final_norm_weight,
+                     const void* lm_head_weight, const void* cos_table, const void* sin_table, void* k_cache,
+                     void* v_cache, void* hidden_buffer, void* g_normalized, int num_layers, int position,
+                     int max_seq_len, float attn_scale, hipStream_t stream) {
+  Common c{model, embed_weight, layer_weights, final_norm_weight, lm_head_weight, cos_table, sin_table, k_cache, v_cache,
+           hidden_buffer, g_normalized, num_layers, max_seq_len, attn_scale};
+  return decode_impl(c, input_token_id, position, output_token_id, logits_out, stream, false);
 }
 
 int qmk_decode_logits(int input_token_id, int* output_token_id, float* logits_out, const void* embed_weight,
@@ -329,7 +356,7 @@ int qmk_decode_logits(int input_token_id, int* output_token_id, float* logits_ou
                       const void* cos_table, const void* sin_table, void* k_cache, void* v_cache, void* hidden_buffer,
                       void* g_normalized, int num_layers, int position, int max_seq_len, float attn_scale,
                       hipStream_t stream) {
-  Common c{embed_weight, layer_weights, final_norm_weight, lm_head_weight, cos_table, sin_table, k_cache, v_cache,
+  Common c{QMK_MODEL_QWEN3_0_6B, embed_weight, layer_weights, final_norm_weight, lm_head_weight, cos_table, sin_table, k_cache, v_cache,
            hidden_buffer, g_normalized, num_layers, max_seq_len, attn_scale};
   return decode_impl(c, input_token_id, position, output_token_id, logits_out, stream, false);
 }
@@ -362,7 +389,7 @@ int qmk_reset(hipStream_t stream) {
   int s = get_ctx(stream, &ctx);
   if (s != QMK_OK) return fail(s);
   if (hipStreamSynchronize(stream) != hipSuccess) return fail(QMK_ERR_HIP);
-  const size_t bytes = sizeof(DecodeState) + (size_t)Dm::X_WORDS * 4;
+  const size_t bytes = sizeof(DecodeState) + (size_t)kXWords * 4;
   if (hipMemset(ctx->st, 0, bytes) != hipSuccess) return fail(QMK_ERR_HIP);
   *ctx->host_err = 0;
   return fail(QMK_OK);

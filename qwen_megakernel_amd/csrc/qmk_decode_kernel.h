@@ -60,6 +60,10 @@ struct Qwen3_0_6B {
   static constexpr int H = 1024, I = 3072, NQ = 16, NKV = 8, D = 128, V = 151936;
 };
 
+struct Qwen3_1_7B {
+  static constexpr int H = 2048, I = 6144, NQ = 16, NKV = 8, D = 128, V = 151936;
+};
+
 constexpr int kMaxSeqLen = 65536;                          // longest cache the kernel accepts
 constexpr int kChunkMax = kMaxSeqLen / kGroupSize;         // attention positions per workgroup
 constexpr int kTracePoints = 13;                           // control-wave stamps per layer
@@ -83,11 +87,23 @@ struct Dims {
   static constexpr int GU_W = 2 * M_WG / kComputeWaves;  // gate/up rows per wave
   static constexpr int ROWS_WG = H / kGroupSize;          // reduce-scatter rows per workgroup
   static constexpr int ROWS_W = ROWS_WG / kComputeWaves;  // o/down rows per wave
+  static constexpr int OP = ROWS_W / 4;         // o/down passes per wave (four rows, one per 16-lane slot)
   static constexpr int LO = OC / 8 / 16;        // o_proj chunks per lane (16 lanes per row)
   static constexpr int LD = MS / 8 / 16;        // down_proj chunks per lane
   static constexpr int LM_RPW = (V + kNumWG - 1) / kNumWG;
-  static constexpr int LM_U = 4;
+  static constexpr int LM_U = 8 / LH;           // LM-head rows per wave per batch (two batches in flight)
   static constexpr int NX = 9;                  // exchanges per layer
+  static constexpr int OUT = 2 * M_WG > 32 ? 2 * M_WG : 32;  // per-workgroup results handed to the control wave
+  // Weight prefetch.  When a workgroup's share of a layer fits the compute
+  // waves' registers (Qwen3-0.6B: 120 KB per workgroup), every phase's slice is
+  // requested one layer ahead into its own registers.  Otherwise (Qwen3-1.7B:
+  // 384 KB per workgroup) each phase's slice is requested at the end of the
+  // compute phase before it, into a buffer the QKV, gate/up and down phases
+  // share (o_proj keeps its own, being loaded before attention).
+  static constexpr bool kStream = H > 1024;
+  static constexpr int NBUF = (RQ_W * LH > GU_W * LH ? RQ_W * LH : GU_W * LH) > OP * LD
+                                  ? (RQ_W * LH > GU_W * LH ? RQ_W * LH : GU_W * LH)
+                                  : OP * LD;
   // exchange layout (words)
   static constexpr uint32_t X_QKV = 0;                                        // [xcd][RG]
   static constexpr uint32_t X_ML = X_QKV + kGroups * RG;                      // [xcd][rank][GQ*4]
@@ -105,7 +121,9 @@ struct Dims {
   static_assert((GQ * D) % RQ_WG == 0 && D % RQ_WG == 0 && RQ_WG % 4 == 0, "QKV block inside one projection");
   static_assert(H % 512 == 0, "K=H rows in 512-element wave loads");
   static_assert(OC % 128 == 0 && MS % 128 == 0, "o/down slices in 16-lane row segments");
-  static_assert(ROWS_W == 4, "o/down: four rows per wave, one per 16-lane slot");
+  static_assert(ROWS_W % 4 == 0, "o/down: passes of four rows, one per 16-lane slot");
+  static_assert(8 % LH == 0, "LM-head batch");
+  static_assert(64 % (ROWS_WG / 2) == 0 || (ROWS_WG / 2) % 64 == 0, "reduce-scatter lane mapping");
   static_assert(2 * M_WG == GU_W * kComputeWaves && M_WG % 4 == 0, "gate/up split");
   static_assert(GQ * (D / 8) == kGroupSize, "combine: one (head, 8-dim block) per workgroup");
   static_assert(ROWS_WG % 16 == 0, "reduce-scatter: 16 lanes x 2 rows");
@@ -190,7 +208,7 @@ struct Smem {
   float wml[kComputeWaves][Dm::GQ][2];
   float wacc[kComputeWaves][Dm::GQ][Dm::D];
   float ml[Dm::GQ][2];               // global softmax max and sum per head
-  float out[32];
+  float out[Dm::OUT];
   uint64_t best[kComputeWaves];
   LayerPtrs layers[kMaxLayers];      // copy of the packed pointer table, read once per launch
   int abort_flag;
@@ -374,28 +392,30 @@ struct Ctl {
   // of ``x_dst``.  Returns false on timeout.
   __device__ bool reduce_rows(uint32_t x_src, uint32_t src_tag, const float* res, uint32_t x_dst, uint32_t dst_tag,
                               int xcd, int r) {
-    constexpr int R = Dm::ROWS_WG;       // 32 rows, 2 per chunk -> 16 chunks per source XCD
-    constexpr int CPX = R / 2;
+    constexpr int R = Dm::ROWS_WG;       // rows per rank, 2 per chunk
+    constexpr int CPX = R / 2;           // chunks per source XCD
+    constexpr int NSL = kGroups * CPX / 64;  // chunks per lane
+    static_assert(CPX <= 64 && 64 % CPX == 0, "a source XCD's chunks within one 64-chunk slot");
     float sum0 = 0.f, sum1 = 0.f;
-    // chunk i: source XCD i / CPX, rows 2*(i % CPX) .. +1
-    float part0[2], part1[2];
+    // chunk i: source XCD i / CPX, rows 2*(i % CPX) .. +1; lane l receives chunks l + 64*slot
+    float part0[NSL], part1[NSL];
     const bool ok = gather<kGroups * CPX>(
         src_tag, [&](int i) { return x_src + (uint32_t)(((i / CPX) * kGroupSize + r) * R * 2 + (i % CPX) * 4); },
         [&](int i, u32x4 v) {
-          // each lane holds chunks i = lane and lane + 64: sources lane/16 and lane/16 + 4
           const int slot = i / 64;
           part0[slot] = f32_from_words(v.x, v.y);
           part1[slot] = f32_from_words(v.z, v.w);
         });
     if (!ok) return false;
-    // lane l: rows 2*(l%16), +1 from sources l/16 (slot 0) and l/16+4 (slot 1);
-    // sum sources in order 0..7 by gathering them into every lane of the row
+    // lane l sums row pair rp = l % CPX over the sources in order 0..7, each
+    // fetched from the lane and slot that received it
+    const int rp = lane % CPX;
     float p0[kGroups], p1[kGroups];
 #pragma unroll
     for (int src = 0; src < kGroups; src++) {
-      const int from = (src % 4) * 16 + (lane & 15);
-      p0[src] = __shfl(src < 4 ? part0[0] : part0[1], from);
-      p1[src] = __shfl(src < 4 ? part1[0] : part1[1], from);
+      const int from = (src * CPX) % 64 + rp;
+      p0[src] = __shfl(part0[(src * CPX) / 64], from);
+      p1[src] = __shfl(part1[(src * CPX) / 64], from);
     }
 #pragma unroll
     for (int src = 0; src < kGroups; src++) {
@@ -454,6 +474,36 @@ __device__ __forceinline__ void load_seg(u32x4 (&dst)[NL], const uint16_t* row_s
 
 template <int NL>
 __device__ __forceinline__ float seg_dot(const u32x4 (&w)[NL], const uint16_t* act, int t16) {
+  float acc = 0.f;
+#pragma unroll
+  for (int j = 0; j < NL; j++) acc = dot8(w[j], *reinterpret_cast<const u32x4*>(act + 8 * (t16 + 16 * j)), acc);
+  return row16_sum(acc);
+}
+
+// The same on register slices addressed from a base pointer with constant
+// offsets (fully unrolled, so they stay in registers).
+template <int NL>
+__device__ __forceinline__ void load_row_p(u32x4* dst, const uint16_t* row, int lane) {
+#pragma unroll
+  for (int j = 0; j < NL; j++) dst[j] = ld_stream(row + 512 * j + 8 * lane);
+}
+
+template <int NL>
+__device__ __forceinline__ float row_dot_p(const u32x4* w, const u32x4 (&x)[NL]) {
+  float acc = 0.f;
+#pragma unroll
+  for (int j = 0; j < NL; j++) acc = dot8(w[j], x[j], acc);
+  return wave_sum(acc);
+}
+
+template <int NL>
+__device__ __forceinline__ void load_seg_p(u32x4* dst, const uint16_t* row_seg, int t16) {
+#pragma unroll
+  for (int j = 0; j < NL; j++) dst[j] = ld_stream(row_seg + 8 * (t16 + 16 * j));
+}
+
+template <int NL>
+__device__ __forceinline__ float seg_dot_p(const u32x4* w, const uint16_t* act, int t16) {
   float acc = 0.f;
 #pragma unroll
   for (int j = 0; j < NL; j++) acc = dot8(w[j], *reinterpret_cast<const u32x4*>(act + 8 * (t16 + 16 * j)), acc);
@@ -768,14 +818,20 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
   const int slot = lane >> 4, t16 = lane & 15;
   const size_t kv_layer_stride = (size_t)Dm::NKV * a.max_seq_len * Dm::D;
 
-  // Weight registers, requested one layer ahead.
-  u32x4 wq[Dm::RQ_W][Dm::LH];
-  u32x4 wo[Dm::LO];
-  u32x4 wgu[Dm::GU_W][Dm::LH];
-  u32x4 wd[Dm::LD];
+  // Weight registers (see Dims::kStream): one layer ahead in per-phase
+  // registers, or one phase ahead in a buffer shared by QKV, gate/up and down.
+  constexpr bool ST = Dm::kStream;
+  u32x4 w_q[ST ? 1 : Dm::RQ_W * Dm::LH];
+  u32x4 w_gu[ST ? 1 : Dm::GU_W * Dm::LH];
+  u32x4 w_d[ST ? 1 : Dm::OP * Dm::LD];
+  u32x4 w_buf[ST ? Dm::NBUF : 1];
+  u32x4 w_o[Dm::OP * Dm::LO];
+  u32x4* const wq = ST ? w_buf : w_q;
+  u32x4* const wgu = ST ? w_buf : w_gu;
+  u32x4* const wd = ST ? w_buf : w_d;
 
-  // o_proj / down_proj: rows ROWS_WG*r + 4c + slot, this XCD's input columns
-  const int rs_row = Dm::ROWS_WG * r + Dm::ROWS_W * c + slot;
+  // o_proj / down_proj: rows ROWS_WG*r + ROWS_W*c + 4*pass + slot, this XCD's input columns
+  auto rs_row = [&](int pass) { return Dm::ROWS_WG * r + Dm::ROWS_W * c + 4 * pass + slot; };
   const bool gu_up = c >= kComputeWaves / 2;
   const int gu_i = (gu_up ? c - kComputeWaves / 2 : c) * Dm::GU_W;          // within this workgroup's m values
   const int gu_m0 = Dm::MS * xcd + Dm::M_WG * r + gu_i;                     // global m index
@@ -787,24 +843,33 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
     w.wk = uniform_ptr(s.layers[layer].wk);
     w.wv = uniform_ptr(s.layers[layer].wv);
 #pragma unroll
-    for (int i = 0; i < Dm::RQ_W; i++) load_row(wq[i], qkv_row<M>(w, xcd, Dm::RQ_WG * r + Dm::RQ_W * c + i), 0, lane);
+    for (int i = 0; i < Dm::RQ_W; i++)
+      load_row_p<Dm::LH>(wq + i * Dm::LH, qkv_row<M>(w, xcd, Dm::RQ_WG * r + Dm::RQ_W * c + i), lane);
   };
   auto prefetch_o = [&](int layer) {
-    load_seg(wo, uniform_ptr(s.layers[layer].wo) + (size_t)rs_row * Dm::QS + Dm::OC * xcd, t16);
+    const uint16_t* wo_base = uniform_ptr(s.layers[layer].wo);
+#pragma unroll
+    for (int op = 0; op < Dm::OP; op++)
+      load_seg_p<Dm::LO>(w_o + op * Dm::LO, wo_base + (size_t)rs_row(op) * Dm::QS + Dm::OC * xcd, t16);
   };
   auto prefetch_gu = [&](int layer) {
     const uint16_t* base = uniform_ptr(gu_up ? s.layers[layer].wu : s.layers[layer].wg);
 #pragma unroll
-    for (int i = 0; i < Dm::GU_W; i++) load_row(wgu[i], base + (size_t)(gu_m0 + i) * Dm::H, 0, lane);
+    for (int i = 0; i < Dm::GU_W; i++) load_row_p<Dm::LH>(wgu + i * Dm::LH, base + (size_t)(gu_m0 + i) * Dm::H, lane);
   };
   auto prefetch_dn = [&](int layer) {
-    load_seg(wd, uniform_ptr(s.layers[layer].wd) + (size_t)rs_row * Dm::I + Dm::MS * xcd, t16);
+    const uint16_t* wd_base = uniform_ptr(s.layers[layer].wd);
+#pragma unroll
+    for (int op = 0; op < Dm::OP; op++)
+      load_seg_p<Dm::LD>(wd + op * Dm::LD, wd_base + (size_t)rs_row(op) * Dm::I + Dm::MS * xcd, t16);
   };
 
   prefetch_qkv(0);
-  prefetch_o(0);
-  prefetch_gu(0);
-  prefetch_dn(0);
+  if (!ST) {
+    prefetch_o(0);
+    prefetch_gu(0);
+    prefetch_dn(0);
+  }
 
   // compute wave 0 stamps the start and end of each of its phases
   uint64_t* ctrace = a.trace ? a.trace + (size_t)(a.num_layers * kTracePoints + 3) * kNumWG : nullptr;
@@ -847,14 +912,15 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
       static_assert(Dm::RQ_W == 2, "one 8-byte store per wave");
       u32x4 act[Dm::LH];
       load_act(act, s.n, 0, lane);
-      const float v0 = row_dot(wq[0], act);
-      const float v1 = row_dot(wq[1], act);
+      const float v0 = row_dot_p<Dm::LH>(wq, act);
+      const float v1 = row_dot_p<Dm::LH>(wq + Dm::LH, act);
       if (lane == 0) {
         const uint32_t t = make_tag(p.epoch, (uint32_t)(L * Dm::NX + 0));
         put2(a.x, Dm::X_QKV + xcd * Dm::RG + Dm::RQ_WG * r + Dm::RQ_W * c, word(f32_to_bf16(v0), t),
              word(f32_to_bf16(v1), t), !a.xcd_local);
       }
     }
+    if (ST) prefetch_o(L);  // o_proj slice, kept through attention
     const int base0 = base0_of(c);
     cstamp(L, 1);
     // Keys of the positions before pos are in the cache already.  Batch 0 is
@@ -992,21 +1058,23 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
         }
       }
     }
-    if (L + 1 < p.nl) prefetch_qkv(L + 1);
+    if (!ST && L + 1 < p.nl) prefetch_qkv(L + 1);
     cstamp(L, 5);
     QMK_SYNC();  // f
     QMK_SYNC();  // g
     cstamp(L, 6);
-    {
-      // o_proj partial of row ROWS_W*c + slot of this workgroup's rows, to every XCD's reducer
-      const float v = seg_dot(wo, s.attn, t16);
+#pragma unroll
+    for (int op = 0; op < Dm::OP; op++) {
+      // o_proj partial of row ROWS_W*c + 4*op + slot of this workgroup's rows, to every XCD's reducer
+      const float v = seg_dot_p<Dm::LO>(w_o + op * Dm::LO, s.attn, t16);
       if (t16 == 0) {
         const uint32_t t = make_tag(p.epoch, (uint32_t)(L * Dm::NX + 4));
-        put2(a.x, Dm::X_O + (uint32_t)((xcd * kGroupSize + r) * Dm::ROWS_WG + Dm::ROWS_W * c + slot) * 2,
+        put2(a.x, Dm::X_O + (uint32_t)((xcd * kGroupSize + r) * Dm::ROWS_WG + Dm::ROWS_W * c + 4 * op + slot) * 2,
              f32_hi_word(v, t), f32_lo_word(v, t), true);
       }
     }
-    if (L + 1 < p.nl) prefetch_o(L + 1);
+    if (ST) prefetch_gu(L);
+    else if (L + 1 < p.nl) prefetch_o(L + 1);
     cstamp(L, 7);
     QMK_SYNC();  // i
     cstamp(L, 8);
@@ -1015,24 +1083,30 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
       load_act(act, s.n, 0, lane);
 #pragma unroll
       for (int i = 0; i < Dm::GU_W; i++) {
-        const float v = row_dot(wgu[i], act);
+        const float v = row_dot_p<Dm::LH>(wgu + i * Dm::LH, act);
         if (lane == 0) s.out[gu_out + i] = bf16r(v);
       }
     }
-    if (L + 1 < p.nl) prefetch_gu(L + 1);
+    if (ST) prefetch_dn(L);
+    else if (L + 1 < p.nl) prefetch_gu(L + 1);
     cstamp(L, 9);
     QMK_SYNC();  // j
     QMK_SYNC();  // k
     cstamp(L, 10);
-    {
-      const float v = seg_dot(wd, s.m, t16);
+#pragma unroll
+    for (int op = 0; op < Dm::OP; op++) {
+      const float v = seg_dot_p<Dm::LD>(wd + op * Dm::LD, s.m, t16);
       if (t16 == 0) {
         const uint32_t t = make_tag(p.epoch, (uint32_t)(L * Dm::NX + 7));
-        put2(a.x, Dm::X_D + (uint32_t)((xcd * kGroupSize + r) * Dm::ROWS_WG + Dm::ROWS_W * c + slot) * 2,
+        put2(a.x, Dm::X_D + (uint32_t)((xcd * kGroupSize + r) * Dm::ROWS_WG + Dm::ROWS_W * c + 4 * op + slot) * 2,
              f32_hi_word(v, t), f32_lo_word(v, t), true);
       }
     }
-    if (L + 1 < p.nl) prefetch_dn(L + 1);
+    if (ST) {
+      if (L + 1 < p.nl) prefetch_qkv(L + 1);
+    } else if (L + 1 < p.nl) {
+      prefetch_dn(L + 1);
+    }
     cstamp(L, 11);
   }
 

@@ -43,6 +43,9 @@ void check_scratch(const torch::Tensor& t, const char* name, int64_t min_bytes) 
 struct Checked {
   int num_layers;
   int max_seq_len;
+  int model;       // QMK_MODEL_*, from the embedding's row length
+  int64_t hidden;
+  int64_t inter;
 };
 
 Checked check_common(const torch::Tensor& embed_weight, const torch::Tensor& layer_weights_packed,
@@ -53,9 +56,16 @@ Checked check_common(const torch::Tensor& embed_weight, const torch::Tensor& lay
   TORCH_CHECK(num_layers >= 1 && num_layers <= kMaxLayers, "num_layers must be in [1, 28], got ", num_layers);
   TORCH_CHECK(max_seq_len >= 1 && max_seq_len <= 65536, "max_seq_len must be in [1, 65536]");
   TORCH_CHECK(attn_scale > 0.0, "attn_scale must be positive");
-  check_bf16(embed_weight, "embed_weight", kVocab * kHidden);
-  check_bf16(lm_head_weight, "lm_head_weight", kVocab * kHidden);
-  check_bf16(final_norm_weight, "final_norm_weight", kHidden);
+  // The model is Qwen3-0.6B (hidden 1024, the reference's) or Qwen3-1.7B (hidden 2048), told apart by
+  // the embedding's size; every other tensor is checked against that model's dimensions.
+  check_bf16(embed_weight, "embed_weight", -1);
+  const int64_t hidden = embed_weight.numel() / kVocab;
+  TORCH_CHECK(embed_weight.numel() == kVocab * hidden && (hidden == 1024 || hidden == 2048),
+              "embed_weight must be [151936, 1024] (Qwen3-0.6B) or [151936, 2048] (Qwen3-1.7B)");
+  const int model = hidden == 1024 ? QMK_MODEL_QWEN3_0_6B : QMK_MODEL_QWEN3_1_7B;
+  const int64_t inter = 3 * hidden;
+  check_bf16(lm_head_weight, "lm_head_weight", kVocab * hidden);
+  check_bf16(final_norm_weight, "final_norm_weight", hidden);
   check_cuda(layer_weights_packed, "layer_weights_packed");
   TORCH_CHECK(layer_weights_packed.scalar_type() == torch::kUInt8, "layer_weights_packed must be uint8");
   TORCH_CHECK(layer_weights_packed.numel() >= num_layers * 11 * 8,
@@ -74,30 +84,30 @@ Checked check_common(const torch::Tensor& embed_weight, const torch::Tensor& lay
   TORCH_CHECK(v_cache.sizes() == k_cache.sizes(), "v_cache must match k_cache");
   TORCH_CHECK(k_cache.numel() >= kv, "k_cache too small");
   check_bf16(hidden_buffer, "hidden_buffer", -1);
-  TORCH_CHECK(hidden_buffer.numel() >= kHidden, "hidden_buffer must hold 1024 bf16");
+  TORCH_CHECK(hidden_buffer.numel() >= hidden, "hidden_buffer must hold ", hidden, " bf16");
   check_cuda(normalized, "normalized");
-  TORCH_CHECK(normalized.scalar_type() == torch::kFloat32 && normalized.numel() >= kHidden,
-              "normalized must be float32 with >= 1024 elements");
+  TORCH_CHECK(normalized.scalar_type() == torch::kFloat32 && normalized.numel() >= hidden,
+              "normalized must be float32 with >= ", hidden, " elements");
   const auto dev = embed_weight.device();
   for (const torch::Tensor* t : {&layer_weights_packed, &final_norm_weight, &lm_head_weight, &cos_table, &sin_table,
                                  &k_cache, &v_cache, &hidden_buffer, &normalized})
     TORCH_CHECK(t->device() == dev, "all tensors must be on the same device");
-  return Checked{(int)num_layers, (int)max_seq_len};
+  return Checked{(int)num_layers, (int)max_seq_len, model, hidden, inter};
 }
 
-void check_unused_scratch(const torch::Tensor& activations, const torch::Tensor& residual, const torch::Tensor& q,
-                          const torch::Tensor& k, const torch::Tensor& v, const torch::Tensor& attn_out,
-                          const torch::Tensor& mlp_intermediate, const torch::Tensor& block_max_vals,
-                          const torch::Tensor& block_max_idxs) {
+void check_unused_scratch(const Checked& c, const torch::Tensor& activations, const torch::Tensor& residual,
+                          const torch::Tensor& q, const torch::Tensor& k, const torch::Tensor& v,
+                          const torch::Tensor& attn_out, const torch::Tensor& mlp_intermediate,
+                          const torch::Tensor& block_max_vals, const torch::Tensor& block_max_idxs) {
   // Not used by this kernel, but the reference's callers pass them; keep the
-  // contract that they are GPU tensors of the reference's sizes.
-  check_scratch(activations, "activations", kHidden * 4);
-  check_scratch(residual, "residual", kHidden * 4);
+  // contract that they are GPU tensors of the reference's sizes (for the model).
+  check_scratch(activations, "activations", c.hidden * 4);
+  check_scratch(residual, "residual", c.hidden * 4);
   check_scratch(q, "q", kQ * 4);
   check_scratch(k, "k", kKV * 4);
   check_scratch(v, "v", kKV * 4);
   check_scratch(attn_out, "attn_out", kQ * 4);
-  check_scratch(mlp_intermediate, "mlp_intermediate", kInter * 4);
+  check_scratch(mlp_intermediate, "mlp_intermediate", c.inter * 4);
   check_scratch(block_max_vals, "block_max_vals", 4);
   check_scratch(block_max_idxs, "block_max_idxs", 4);
 }
@@ -117,12 +127,22 @@ void decode(torch::Tensor output_token, int64_t input_token_id, torch::Tensor em
   const Checked c = check_common(embed_weight, layer_weights_packed, final_norm_weight, lm_head_weight, cos_table,
                                  sin_table, k_cache, v_cache, hidden_buffer, normalized, num_layers, max_seq_len,
                                  attn_scale);
-  check_unused_scratch(activations, residual, q, k, v, attn_out, mlp_intermediate, block_max_vals, block_max_idxs);
+  check_unused_scratch(c, activations, residual, q, k, v, attn_out, mlp_intermediate, block_max_vals, block_max_idxs);
   check_cuda(output_token, "output_token");
   TORCH_CHECK(output_token.scalar_type() == torch::kInt32 && output_token.numel() >= 1, "output_token must be int32[1]");
   TORCH_CHECK(position >= 0 && position < max_seq_len, "position ", position, " outside [0, ", max_seq_len, ")");
   TORCH_CHECK(input_token_id >= 0 && input_token_id < kVocab, "input_token_id outside the vocabulary");
   const c10::hip::HIPGuardMasqueradingAsCUDA guard(embed_weight.device());
+  if (c.model != QMK_MODEL_QWEN3_0_6B) {
+    qmk_decode_model(c.model, (int)input_token_id, static_cast<int*>(output_token.data_ptr()), nullptr,
+                     embed_weight.data_ptr(), reinterpret_cast<const LDGLayerWeights*>(layer_weights_packed.data_ptr()),
+                     final_norm_weight.data_ptr(), lm_head_weight.data_ptr(), cos_table.data_ptr(), sin_table.data_ptr(),
+                     k_cache.data_ptr(), v_cache.data_ptr(), hidden_buffer.data_ptr(), normalized.data_ptr(),
+                     c.num_layers, (int)position, c.max_seq_len, (float)attn_scale,
+                     c10::hip::getCurrentHIPStreamMasqueradingAsCUDA().stream());
+    raise_status("decode");
+    return;
+  }
   launch_ldg_decode_direct(
       (int)input_token_id, static_cast<int*>(output_token.data_ptr()), embed_weight.data_ptr(),
       reinterpret_cast<const LDGLayerWeights*>(layer_weights_packed.data_ptr()), final_norm_weight.data_ptr(),
@@ -145,7 +165,7 @@ torch::Tensor generate_nosync(int64_t first_token_id, int64_t num_steps, torch::
   const Checked c = check_common(embed_weight, layer_weights_packed, final_norm_weight, lm_head_weight, cos_table,
                                  sin_table, k_cache, v_cache, hidden_buffer, normalized, num_layers, max_seq_len,
                                  attn_scale);
-  check_unused_scratch(activations, residual, q, k, v, attn_out, mlp_intermediate, block_max_vals, block_max_idxs);
+  check_unused_scratch(c, activations, residual, q, k, v, attn_out, mlp_intermediate, block_max_vals, block_max_idxs);
   TORCH_CHECK(num_steps >= 0, "num_steps must be non-negative");
   TORCH_CHECK(start_position >= 0 && start_position + num_steps <= max_seq_len, "steps [", start_position, ", ",
               start_position + num_steps, ") do not fit in max_seq_len ", max_seq_len);
@@ -154,14 +174,22 @@ torch::Tensor generate_nosync(int64_t first_token_id, int64_t num_steps, torch::
   auto stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA().stream();
   auto output_log = torch::empty({num_steps}, torch::dtype(torch::kInt32).device(embed_weight.device()));
   if (num_steps == 0) return output_log;
-  launch_ldg_generate_nosync(
-      (int)first_token_id, (int)num_steps, embed_weight.data_ptr(),
-      reinterpret_cast<const LDGLayerWeights*>(layer_weights_packed.data_ptr()), final_norm_weight.data_ptr(),
-      lm_head_weight.data_ptr(), cos_table.data_ptr(), sin_table.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
-      hidden_buffer.data_ptr(), activations.data_ptr(), residual.data_ptr(), q.data_ptr(), k.data_ptr(),
-      v.data_ptr(), attn_out.data_ptr(), mlp_intermediate.data_ptr(), normalized.data_ptr(),
-      block_max_vals.data_ptr(), block_max_idxs.data_ptr(), static_cast<int*>(output_log.data_ptr()), c.num_layers,
-      (int)start_position, c.max_seq_len, (float)attn_scale, stream);
+  if (c.model != QMK_MODEL_QWEN3_0_6B)
+    qmk_generate_model(c.model, (int)first_token_id, (int)num_steps, embed_weight.data_ptr(),
+                       reinterpret_cast<const LDGLayerWeights*>(layer_weights_packed.data_ptr()),
+                       final_norm_weight.data_ptr(), lm_head_weight.data_ptr(), cos_table.data_ptr(),
+                       sin_table.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), hidden_buffer.data_ptr(),
+                       normalized.data_ptr(), static_cast<int*>(output_log.data_ptr()), c.num_layers,
+                       (int)start_position, c.max_seq_len, (float)attn_scale, stream);
+  else
+    launch_ldg_generate_nosync(
+        (int)first_token_id, (int)num_steps, embed_weight.data_ptr(),
+        reinterpret_cast<const LDGLayerWeights*>(layer_weights_packed.data_ptr()), final_norm_weight.data_ptr(),
+        lm_head_weight.data_ptr(), cos_table.data_ptr(), sin_table.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+        hidden_buffer.data_ptr(), activations.data_ptr(), residual.data_ptr(), q.data_ptr(), k.data_ptr(),
+        v.data_ptr(), attn_out.data_ptr(), mlp_intermediate.data_ptr(), normalized.data_ptr(),
+        block_max_vals.data_ptr(), block_max_idxs.data_ptr(), static_cast<int*>(output_log.data_ptr()), c.num_layers,
+        (int)start_position, c.max_seq_len, (float)attn_scale, stream);
   raise_status("generate_nosync");
   // Single synchronisation at the end, as the reference (csrc/torch_bindings.cpp:125).
   const uint32_t err = qmk_device_error(stream);
@@ -186,7 +214,7 @@ void decode_logits(torch::Tensor output_token, torch::Tensor logits, int64_t inp
   TORCH_CHECK(position >= 0 && position < max_seq_len, "position ", position, " outside [0, ", max_seq_len, ")");
   TORCH_CHECK(input_token_id >= 0 && input_token_id < kVocab, "input_token_id outside the vocabulary");
   const c10::hip::HIPGuardMasqueradingAsCUDA guard(embed_weight.device());
-  qmk_decode_logits((int)input_token_id, static_cast<int*>(output_token.data_ptr()),
+  qmk_decode_model(c.model, (int)input_token_id, static_cast<int*>(output_token.data_ptr()),
                     static_cast<float*>(logits.data_ptr()), embed_weight.data_ptr(),
                     reinterpret_cast<const LDGLayerWeights*>(layer_weights_packed.data_ptr()),
                     final_norm_weight.data_ptr(), lm_head_weight.data_ptr(), cos_table.data_ptr(),

@@ -14,6 +14,8 @@ Differences, all additive:
   and no tokenizer.
 * RoPE theta is 1e6 (Qwen3), not the reference's 10000 (model.py:54-56).
 * ``max_seq_len`` is a parameter (the reference fixes 2048).
+* ``Decoder`` also serves Qwen3-1.7B weights (hidden 2048, MLP 6144); the
+  model is recognised from the embedding's width.
 * ``Decoder.step`` raises on a device failure instead of returning a stale token;
   positions are range-checked.
 * ``Decoder.step_logits`` returns the logits as well, ``Decoder.load_kv`` injects
@@ -29,7 +31,7 @@ import struct
 
 import torch
 
-from .shapes import QWEN3_0_6B
+from .shapes import QWEN3_0_6B, QWEN3_1_7B
 from . import weights as _w
 
 NUM_LAYERS = 28
@@ -101,6 +103,11 @@ class Decoder:
             raise ValueError(f"num_layers={num_layers} does not match the weights")
         if weights["cos_table"].shape[0] < max_seq_len:
             raise ValueError("RoPE tables are shorter than max_seq_len")
+        hidden = weights["embed_weight"].shape[-1]
+        shapes = {QWEN3_0_6B.hidden: QWEN3_0_6B, QWEN3_1_7B.hidden: QWEN3_1_7B}
+        if hidden not in shapes:
+            raise ValueError(f"embed_weight width {hidden}: expected 1024 (Qwen3-0.6B) or 2048 (Qwen3-1.7B)")
+        self.shape = shapes[hidden]
         self.tokenizer = tokenizer
         self._position = 0
         self._num_layers = num_layers
@@ -118,15 +125,16 @@ class Decoder:
         self._v_cache = torch.zeros_like(self._k_cache)
         f32 = dict(dtype=torch.float32, device=dev)
         bf16 = dict(dtype=torch.bfloat16, device=dev)
-        self._hidden = torch.empty(HIDDEN_SIZE, **bf16)
-        self._act = torch.empty(HIDDEN_SIZE, **f32)
-        self._res = torch.empty(HIDDEN_SIZE, **f32)
+        h, inter = self.shape.hidden, self.shape.intermediate
+        self._hidden = torch.empty(h, **bf16)
+        self._act = torch.empty(h, **f32)
+        self._res = torch.empty(h, **f32)
         self._q = torch.empty(Q_SIZE, **f32)
         self._k = torch.empty(KV_SIZE, **f32)
         self._v = torch.empty(KV_SIZE, **f32)
         self._attn_out = torch.empty(Q_SIZE, **f32)
-        self._mlp_inter = torch.empty(INTERMEDIATE_SIZE, **f32)
-        self._norm_out = torch.empty(HIDDEN_SIZE, **f32)
+        self._mlp_inter = torch.empty(inter, **f32)
+        self._norm_out = torch.empty(h, **f32)
         self._bmax_vals = torch.empty(4096, **f32)
         self._bmax_idxs = torch.empty(4096, dtype=torch.int32, device=dev)
         self._out_token = torch.empty(1, dtype=torch.int32, device=dev)
