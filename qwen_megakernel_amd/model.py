@@ -52,11 +52,13 @@ def _ops():
 
 
 def load_weights(model_name: str = "Qwen/Qwen3-0.6B", verbose: bool = True, *, max_seq_len: int = MAX_SEQ_LEN,
-                 seed: int = 0, device: str = "cuda"):
+                 seed: int = 0, device: str = "cuda", shape=None):
     """Return ``(weights, tokenizer)`` in the reference's dict layout (model.py:21-94).
 
-    A local directory with ``*.safetensors`` is loaded as a real checkpoint;
-    otherwise the seeded synthetic Qwen3-0.6B weights are drawn (tokenizer None).
+    A local directory with ``*.safetensors`` is loaded as a real checkpoint (its
+    ``config.json`` ``hidden_size`` picks Qwen3-0.6B or -1.7B unless ``shape`` is
+    given); otherwise the seeded synthetic weights of ``shape`` (default
+    Qwen3-0.6B) are drawn and there is no tokenizer.
     """
     if os.path.isdir(model_name) and glob.glob(os.path.join(model_name, "*.safetensors")):
         from safetensors.torch import load_file
@@ -64,9 +66,20 @@ def load_weights(model_name: str = "Qwen/Qwen3-0.6B", verbose: bool = True, *, m
         state = {}
         for f in sorted(glob.glob(os.path.join(model_name, "*.safetensors"))):
             state.update(load_file(f))
+        if shape is None:
+            hidden = state["model.embed_tokens.weight"].shape[-1]
+            cfg_path = os.path.join(model_name, "config.json")
+            if os.path.exists(cfg_path):
+                import json
+
+                with open(cfg_path) as fh:
+                    hidden = json.load(fh).get("hidden_size", hidden)
+            shape = {QWEN3_0_6B.hidden: QWEN3_0_6B, QWEN3_1_7B.hidden: QWEN3_1_7B}.get(hidden)
+            if shape is None:
+                raise ValueError(f"{model_name}: hidden size {hidden} is neither Qwen3-0.6B nor Qwen3-1.7B")
         if verbose:
-            print(f"Loading {model_name} (local safetensors)...")
-        weights = _w.load_weights_from_state_dict(state, QWEN3_0_6B, max_seq_len=max_seq_len, device=device)
+            print(f"Loading {model_name} (local safetensors, {shape.name})...")
+        weights = _w.load_weights_from_state_dict(state, shape, max_seq_len=max_seq_len, device=device)
         tokenizer = None
         try:
             from transformers import AutoTokenizer
@@ -75,9 +88,10 @@ def load_weights(model_name: str = "Qwen/Qwen3-0.6B", verbose: bool = True, *, m
         except Exception:
             tokenizer = None
         return weights, tokenizer
+    shape = QWEN3_0_6B if shape is None else shape
     if verbose:
-        print(f"{model_name}: no local checkpoint; using seeded synthetic Qwen3-0.6B weights (seed {seed})")
-    return _w.make_weights(QWEN3_0_6B, seed=seed, max_seq_len=max_seq_len, device=device), None
+        print(f"{model_name}: no local checkpoint; using seeded synthetic {shape.name} weights (seed {seed})")
+    return _w.make_weights(shape, seed=seed, max_seq_len=max_seq_len, device=device), None
 
 
 def _pack_layer_weights(layer_weights: list[torch.Tensor], num_layers: int = NUM_LAYERS) -> torch.Tensor:

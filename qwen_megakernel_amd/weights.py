@@ -113,7 +113,11 @@ def load_weights_from_state_dict(state: dict, shape: Qwen3Shape = QWEN3_0_6B,
     """Build the weights dict from a Qwen3 ``state_dict`` (HF key names).
 
     Mirrors the key walk of qwen_megakernel/model.py:63-90 without the hub
-    download; the caller supplies the tensors (e.g. from a local safetensors file).
+    download; the caller supplies the tensors (e.g. from a local safetensors
+    file).  Every tensor is checked against ``shape``.  ``lm_head.weight`` is
+    used when the checkpoint holds a separate one; otherwise (Qwen3-0.6B and
+    -1.7B tie it) the LM head is the embedding, as in the reference
+    (qwen_megakernel/model.py:87).
     """
     hf_names = {
         "input_layernorm": "input_layernorm.weight",
@@ -128,15 +132,30 @@ def load_weights_from_state_dict(state: dict, shape: Qwen3Shape = QWEN3_0_6B,
         "up_proj": "mlp.up_proj.weight",
         "down_proj": "mlp.down_proj.weight",
     }
+    expect = layer_tensor_shapes(shape)
+
+    def get(key, shp):
+        if key not in state:
+            raise KeyError(f"checkpoint has no {key}")
+        t = state[key]
+        if tuple(t.shape) != tuple(shp):
+            raise ValueError(f"{key}: shape {tuple(t.shape)}, expected {tuple(shp)} for {shape.name}")
+        return t.to(BF16).contiguous()
+
     flat = []
     for i in range(shape.num_layers):
         for name in LAYER_TENSOR_NAMES:
-            flat.append(state[f"model.layers.{i}.{hf_names[name]}"].to(BF16).contiguous())
-    embed = state["model.embed_tokens.weight"].to(BF16).contiguous()
+            flat.append(get(f"model.layers.{i}.{hf_names[name]}", expect[name]))
+    embed = get("model.embed_tokens.weight", (shape.vocab, shape.hidden))
+    lm_head = embed
+    if "lm_head.weight" in state:
+        head = get("lm_head.weight", (shape.vocab, shape.hidden))
+        if not torch.equal(head, embed):
+            lm_head = head
     cos, sin = rope_tables(max_seq_len, shape.head_dim, shape.rope_theta)
     w = dict(embed_weight=embed, layer_weights=flat,
-             final_norm_weight=state["model.norm.weight"].to(BF16).contiguous(),
-             lm_head_weight=embed, cos_table=cos, sin_table=sin)
+             final_norm_weight=get("model.norm.weight", (shape.hidden,)),
+             lm_head_weight=lm_head, cos_table=cos, sin_table=sin)
     return to_device(w, device)
 
 

@@ -15,6 +15,8 @@ token-at-a-time decode (the reference's ``Decoder.step`` pattern):
   weight fingerprint, and HF ``generate()`` tokens (batched prefill).
 * ``hf_rope.npz``         -- HF rotary-embedding cos/sin rows for selected
   positions (head_dim 128, theta 1e6).
+* ``hf_tiny_keys.json``   -- HF's state-dict names and shapes for the tiny
+  config (``python tests/golden/make_hf_golden.py keys`` writes only this).
 
 Run:  python tests/golden/make_hf_golden.py   (about a minute on 8 cores)
 """
@@ -121,9 +123,23 @@ def weight_fingerprint(w: dict) -> np.ndarray:
     return torch.stack(rows).numpy()
 
 
+def write_state_dict_keys():
+    """HF's own parameter names and shapes for the tiny config (pins the checkpoint loader's key walk)."""
+    import json
+
+    w = make_weights(TINY, seed=0, norm_std=0.1, max_seq_len=64)
+    m = hf_model(TINY, w, TINY.num_layers)
+    keys = {k: list(v.shape) for k, v in m.state_dict().items()}
+    with open(os.path.join(HERE, "hf_tiny_keys.json"), "w") as f:
+        json.dump({"config": {"num_layers": TINY.num_layers, "hidden": TINY.hidden,
+                              "intermediate": TINY.intermediate, "vocab": TINY.vocab},
+                   "state_dict": keys}, f, indent=0, sort_keys=True)
+
+
 def main():
     torch.set_num_threads(max(1, len(os.sched_getaffinity(0))))
     sig = cpu_signature()
+    write_state_dict_keys()
 
     # tiny config, full logits
     w = make_weights(TINY, seed=0, norm_std=0.1, max_seq_len=64)
@@ -167,5 +183,7 @@ def main():
     print("golden fixtures written:", sig)
 
 
-if __name__ == "__main__":
+if __name__ == "__main__" and sys.argv[1:] == ["keys"]:
+    write_state_dict_keys()
+elif __name__ == "__main__":
     main()
