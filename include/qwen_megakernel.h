@@ -214,6 +214,49 @@ size_t qmk_phase_copy_elems(int phase);
 /* Kernel launch geometry, for tools: workgroups and threads per workgroup. */
 void qmk_launch_geometry(int *workgroups, int *threads);
 
+/* ---- batched forward (no counterpart in the reference, which feeds a
+ * prompt one decode step per token, qwen_megakernel/model.py:207-211) ---- */
+
+/* Workspace bytes qmk_forward_tokens needs for `num_tokens` tokens,
+ * `num_emit` emitted rows (<= 256) and contexts of at most `max_context`
+ * positions.  0 for invalid arguments. */
+size_t qmk_forward_workspace_bytes(int model, int num_tokens, int num_emit,
+                                   int max_context);
+
+/* One forward pass of `num_tokens` tokens through `model`, on MFMA GEMMs
+ * (one weight read serves every token).  Token t is token id tokens[t] of
+ * sequence seq_ids[t] at position positions[t]: its K/V are written into that
+ * sequence's cache at that position, and it attends to positions
+ * 0..positions[t] of the sequence, so the tokens of one sequence at
+ * consecutive positions form a prompt prefill (causal), and one token per
+ * sequence a batched decode step.  Sequence s's cache is the
+ * [num_layers][8][max_seq_len][128] block at k_cache + s * seq_stride
+ * (elements; seq_stride is ignored when num_seqs == 1).  For the emitted rows
+ * e = emit_rows[r] (r < num_emit), out_tokens[r] receives the greedy next
+ * token after token e and, when logits_out is not NULL, logits_out[r][vocab]
+ * the fp32 copy of its bf16 logits.  A token with an id outside the
+ * vocabulary, a sequence outside [0, num_seqs) or a position outside
+ * [0, max_context) writes no cache and emits -1; so does an emit row outside
+ * [0, num_tokens).  tokens, seq_ids, positions, emit_rows, out_tokens and
+ * logits_out are device pointers; layer_weights_host is a HOST array of
+ * num_layers tables (device pointers inside).  max_context <= max_seq_len
+ * bounds every position + 1 (it sizes the workspace).  Asynchronous; returns
+ * a status code. */
+int qmk_forward_tokens(
+    int model, int num_tokens, const int *tokens, const int *seq_ids,
+    const int *positions, int num_emit, const int *emit_rows, int *out_tokens,
+    float *logits_out, const void *embed_weight,
+    const LDGLayerWeights *layer_weights_host, const void *final_norm_weight,
+    const void *lm_head_weight, const void *cos_table, const void *sin_table,
+    void *k_cache, void *v_cache, int num_seqs, long long seq_stride,
+    int num_layers, int max_seq_len, int max_context, float attn_scale,
+    void *workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* One 16x16x32 bf16 MFMA with the operand layouts the batched GEMM assumes:
+ * c[16][16] (f32) = a[16][32] . b[16][32]^T (bf16, row-major).  For tests.
+ * Asynchronous; returns a status code. */
+int qmk_selftest_mfma(const void *a, const void *b, float *c, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

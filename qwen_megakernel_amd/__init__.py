@@ -5,6 +5,6 @@ library is built by ``qwen_megakernel_amd.build.build()`` (or on first use by
 ``Decoder``); importing the package does not compile anything.
 """
 
-from .model import Decoder, generate, load_weights  # noqa: F401
+from .model import BatchDecoder, Decoder, generate, load_weights  # noqa: F401
 
-__all__ = ["load_weights", "Decoder", "generate"]
+__all__ = ["load_weights", "Decoder", "generate", "BatchDecoder"]

@@ -46,7 +46,9 @@ HIP_FLAGS = [
     f"-I{_INCLUDE}",
 ]
 
-_LIB_SOURCES = ["qmk_api.hip", "qmk_decode_kernel.h", "qmk_device.h", "qmk_state.h", "qmk_phase_bench.h"]
+_LIB_SOURCES = ["qmk_api.hip", "qmk_batch.hip", "qmk_decode_kernel.h", "qmk_device.h", "qmk_state.h",
+                "qmk_phase_bench.h"]
+_LIB_UNITS = ["qmk_api.hip", "qmk_batch.hip"]
 _OPS_SOURCES = ["torch_bindings.cpp"]
 
 _module = None
@@ -75,7 +77,7 @@ def _run(cmd, verbose):
 def build_library(verbose: bool = False) -> str:
     """Compile libqwen_megakernel_amd.so (HIP kernels + C ABI)."""
     tmp = LIB + ".tmp"
-    _run([HIPCC, *HIP_FLAGS, os.path.join(_CSRC, "qmk_api.hip"), "-o", tmp], verbose)
+    _run([HIPCC, *HIP_FLAGS, *[os.path.join(_CSRC, n) for n in _LIB_UNITS], "-o", tmp], verbose)
     os.replace(tmp, LIB)
     return LIB
 

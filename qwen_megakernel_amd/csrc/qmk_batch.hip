@@ -1,0 +1,876 @@
+// Batched forward of T tokens through Qwen3 on gfx950: prompt prefill (T
+// tokens of one sequence at consecutive positions) and batched decode (one
+// token of each of B sequences, each at its own position), or any mix.
+// Unlike the per-token decode kernel, the work here has T rows per weight
+// read, so the projections run as MFMA GEMMs (v_mfma_f32_16x16x32_bf16) and a
+// layer is a short sequence of kernels on the caller's stream instead of one
+// persistent launch.  Numerics follow HF Qwen3's bf16 eager path op for op, as
+// the decode kernel does: every projection is an fp32 sum rounded once to
+// bf16; norms, RoPE, softmax probabilities, residual adds and SiLU*up round
+// where HF rounds.
+//
+// The reference prefills one token per step() (qwen_megakernel/model.py:210-211)
+// and decodes one sequence; the batched forward is an addition.
+//
+// Per layer (kernels in launch order):
+//   gemm_partial(qkv)  -> qkv_finish (split-K sum, q/k RMSNorm + RoPE, K/V append)
+//   attention          (one kernel per (token, KV head) for many tokens; a
+//                       context-split pair + merge for few tokens)
+//   gemm_partial(o)    -> residual_norm (residual add, post-attention RMSNorm)
+//   gemm_partial(g|u)  -> gate_up_finish (SiLU(g) * u)
+//   gemm_partial(down) -> residual_norm (residual add, next layer's input RMSNorm
+//                                        or the final norm)
+// then lm_head_gemm over the emitted rows (bf16 logits, per-tile argmax keys)
+// -> keys_reduce (per-row argmax).
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+
+#include "../../include/qwen_megakernel.h"
+#include "qmk_decode_kernel.h"
+
+namespace qmk {
+namespace batch {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kD = 128, kNQ = 16, kNKV = 8, kQS = kNQ * kD, kNQKV = (kNQ + 2 * kNKV) * kD;
+constexpr int kAttnChunk = 2048;  // one-kernel attention: scores of this many positions per LDS pass
+constexpr int kSplitChunk = 64;   // split attention: positions per workgroup
+constexpr int kSplitBelow = 32;   // fewer tokens than this use the split attention
+constexpr int kTargetWaves = 2048;
+constexpr int kMaxSplit = 32;     // K splits of one GEMM (their partials are summed in a fixed order)
+constexpr int kMaxEmit = 256;
+
+static_assert(Qwen3_0_6B::D == kD && Qwen3_0_6B::NQ == kNQ && Qwen3_0_6B::NKV == kNKV, "head layout");
+static_assert(Qwen3_1_7B::D == kD && Qwen3_1_7B::NQ == kNQ && Qwen3_1_7B::NKV == kNKV, "head layout");
+
+// Per-token metadata, checked once (prep_tokens).  An invalid token (id outside
+// the vocabulary, sequence or position out of range) reads embedding row 0,
+// writes nothing into any cache and emits -1.
+struct Tok {
+  int token, seq, pos, valid;
+};
+
+struct Cache {
+  uint16_t* k;
+  uint16_t* v;
+  long long seq_stride;  // elements from one sequence's [L][NKV][S][D] block to the next
+  int max_seq_len;
+};
+
+__device__ __forceinline__ bf16x8 ld_bf16x8(const uint16_t* p) { return __builtin_bit_cast(bf16x8, ld16(p)); }
+__device__ __forceinline__ bf16x8 ld_bf16x8_stream(const uint16_t* p) {
+  return __builtin_bit_cast(bf16x8, ld_stream(p));
+}
+
+__device__ __forceinline__ size_t cache_base(const Cache& c, const Tok& tk, int L, int g) {
+  return (size_t)tk.seq * c.seq_stride + ((size_t)L * kNKV + g) * c.max_seq_len * kD;
+}
+
+// Sum over the block (256 threads) of one value per head; `red` is [2][4].
+__device__ __forceinline__ void block_sum2(float (&v)[2], float (*red)[4]) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  v[0] = wave_sum(v[0]);
+  v[1] = wave_sum(v[1]);
+  __syncthreads();
+  if (lane == 0) {
+    red[0][wave] = v[0];
+    red[1][wave] = v[1];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int h = 0; h < 2; h++) v[h] = (red[h][0] + red[h][1]) + (red[h][2] + red[h][3]);
+}
+
+__device__ __forceinline__ void block_max2(float (&v)[2], float (*red)[4]) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  v[0] = wave_max(v[0]);
+  v[1] = wave_max(v[1]);
+  __syncthreads();
+  if (lane == 0) {
+    red[0][wave] = v[0];
+    red[1][wave] = v[1];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int h = 0; h < 2; h++) v[h] = fmaxf(fmaxf(red[h][0], red[h][1]), fmaxf(red[h][2], red[h][3]));
+}
+
+// ---------------------------------------------------------------- tokens
+
+__global__ void __launch_bounds__(256) prep_tokens(const int* __restrict__ tokens, const int* __restrict__ seqs,
+                                                   const int* __restrict__ pos, int T, const int* __restrict__ emit,
+                                                   int R, int num_seqs, int max_context, int vocab,
+                                                   Tok* __restrict__ tok, int* __restrict__ erow) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < T) {
+    const int id = tokens[i], sq = seqs[i], p = pos[i];
+    const bool ok = id >= 0 && id < vocab && sq >= 0 && sq < num_seqs && p >= 0 && p < max_context;
+    tok[i] = Tok{ok ? id : 0, ok ? sq : 0, ok ? p : 0, ok ? 1 : 0};
+  }
+  if (i < R) {
+    const int e = emit[i];
+    erow[i] = (e >= 0 && e < T) ? e : -1;
+  }
+}
+
+// X[t] = embed[token[t]]
+__global__ void __launch_bounds__(256) embed_rows(const uint16_t* __restrict__ embed, const Tok* __restrict__ tok,
+                                                  int H, uint16_t* __restrict__ X) {
+  const int t = blockIdx.x;
+  const uint16_t* e = embed + (size_t)tok[t].token * H;
+  for (int i = threadIdx.x; i < H / 8; i += 256) reinterpret_cast<u32x4*>(X + (size_t)t * H)[i] = ld16(e + 8 * i);
+}
+
+// ---------------------------------------------------------------- GEMM
+//
+// part[s][t][n] = sum over k in split s of X[row(t)][k] * W[n][k]   (fp32)
+// W rows come from up to three row-major [rows][K] matrices laid end to end
+// (q, k, v; or gate, up).  One wave computes a 16-row x 16*NB-column tile of
+// one K split with 16x16x32 bf16 MFMAs.  Operand layouts (checked by
+// qmk_selftest_mfma): lane l supplies A[l%16][8*(l/16) .. +7] and
+// B[8*(l/16) .. +7][l%16], i.e. 16 contiguous bytes of an X row and of a W
+// row; it receives C[4*(l/16) + i][l%16], i = 0..3.  Waves are numbered with
+// the row tile fastest, then the column tile, then the split, and workgroups
+// are renumbered so that consecutive numbers share an XCD: the row tiles that
+// read one weight tile run on one XCD and share its L2.
+struct Seg {
+  const uint16_t* w[3];
+  int rows[3];
+};
+
+__device__ __forceinline__ const uint16_t* seg_row(const Seg& s, int n, int K) {
+  if (n < s.rows[0]) return s.w[0] + (size_t)n * K;
+  n -= s.rows[0];
+  if (n < s.rows[1]) return s.w[1] + (size_t)n * K;
+  n -= s.rows[1];
+  return s.w[2] + (size_t)n * K;
+}
+
+template <int NB, bool STREAM>
+__global__ void __launch_bounds__(256) gemm_partial(const uint16_t* __restrict__ X, const int* __restrict__ rows,
+                                                    int T, int K, Seg seg, int N, int ksplit,
+                                                    float* __restrict__ part) {
+  const int nblk = gridDim.x;
+  const int b = blockIdx.x;
+  const int lb = (nblk % kGroups == 0) ? (b % kGroups) * (nblk / kGroups) + b / kGroups : b;
+  const int wave = lb * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int mtiles = (T + 15) / 16, ntiles = N / (16 * NB);
+  const int mt = wave % mtiles;
+  const int nt = (wave / mtiles) % ntiles;
+  const int sp = wave / (mtiles * ntiles);
+  if (sp >= ksplit) return;
+  const int kchunk = K / ksplit, k0 = sp * kchunk, k1 = k0 + kchunk;
+  const int kq = 8 * (lane >> 4);
+  int xr = min(mt * 16 + (lane & 15), T - 1);
+  if (rows) xr = max(rows[xr], 0);
+  const uint16_t* xa = X + (size_t)xr * K + kq;
+  const uint16_t* wb[NB];
+#pragma unroll
+  for (int j = 0; j < NB; j++) wb[j] = seg_row(seg, nt * 16 * NB + 16 * j + (lane & 15), K) + kq;
+  f32x4 acc[NB];
+#pragma unroll
+  for (int j = 0; j < NB; j++) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  bf16x8 a0, a1, b0[NB], b1[NB];
+  auto load = [&](int k, bf16x8& x0, bf16x8& x1, bf16x8 (&y0)[NB], bf16x8 (&y1)[NB]) {
+    x0 = ld_bf16x8(xa + k);
+    x1 = ld_bf16x8(xa + k + 32);
+#pragma unroll
+    for (int j = 0; j < NB; j++) {
+      y0[j] = STREAM ? ld_bf16x8_stream(wb[j] + k) : ld_bf16x8(wb[j] + k);
+      y1[j] = STREAM ? ld_bf16x8_stream(wb[j] + k + 32) : ld_bf16x8(wb[j] + k + 32);
+    }
+  };
+  load(k0, a0, a1, b0, b1);
+  for (int k = k0; k < k1; k += 64) {
+    bf16x8 na0, na1, nb0[NB], nb1[NB];
+    if (k + 64 < k1) load(k + 64, na0, na1, nb0, nb1);
+#pragma unroll
+    for (int j = 0; j < NB; j++) {
+      acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b0[j], acc[j], 0, 0, 0);
+      acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b1[j], acc[j], 0, 0, 0);
+    }
+    if (k + 64 < k1) {
+      a0 = na0;
+      a1 = na1;
+#pragma unroll
+      for (int j = 0; j < NB; j++) {
+        b0[j] = nb0[j];
+        b1[j] = nb1[j];
+      }
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < NB; j++) {
+    const int n = nt * 16 * NB + 16 * j + (lane & 15);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int t = mt * 16 + 4 * (lane >> 4) + i;
+      if (t < T) part[((size_t)sp * T + t) * N + n] = acc[j][i];
+    }
+  }
+}
+
+// Sum of the K-split partials of element (t, n), in split order.  All loads
+// are issued before the first add.
+__device__ __forceinline__ float sum_splits(const float* part, int ksplit, int T, int N, int t, int n) {
+  const size_t stride = (size_t)T * N, idx = (size_t)t * N + n;
+  float v[kMaxSplit];
+#pragma unroll
+  for (int s = 0; s < kMaxSplit; s++) v[s] = s < ksplit ? part[s * stride + idx] : 0.f;
+  float y = v[0];
+#pragma unroll
+  for (int s = 1; s < kMaxSplit; s++)
+    if (s < ksplit) y += v[s];
+  return y;
+}
+
+// ---------------------------------------------------------------- row kernels
+
+// One workgroup of 1024 threads per token.  x = X[t] (+ bf16(sum of the split
+// partials) when `part` is given, written back: HF's bf16 residual add);
+// N[t] = bf16(w * bf16(x * rsqrt(mean(x^2) + eps))) (Qwen3RMSNorm).
+template <int H>
+__global__ void __launch_bounds__(1024) residual_norm(const float* __restrict__ part, int ksplit, int T,
+                                                      uint16_t* __restrict__ X, const uint16_t* __restrict__ w,
+                                                      float eps, uint16_t* __restrict__ Nout) {
+  constexpr int J = H / 1024;
+  __shared__ float red[16];
+  const int t = blockIdx.x, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  uint16_t* x = X + (size_t)t * H;
+  float y[J];
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < J; j++) {
+    const int i = threadIdx.x + 1024 * j;
+    float v = bf16_to_f32(x[i]);
+    if (part) {
+      v = bf16r(v + bf16r(sum_splits(part, ksplit, T, H, t, i)));
+      x[i] = (uint16_t)f32_to_bf16(v);
+    }
+    y[j] = v;
+    ss += v * v;
+  }
+  ss = wave_sum(ss);
+  if (lane == 0) red[wave] = ss;
+  __syncthreads();
+  ss = 0.f;
+#pragma unroll
+  for (int q = 0; q < 16; q++) ss += red[q];
+  const float rstd = rcp_sqrt_torch(__fdiv_rn(ss, (float)H) + eps);
+#pragma unroll
+  for (int j = 0; j < J; j++) {
+    const int i = threadIdx.x + 1024 * j;
+    Nout[(size_t)t * H + i] = (uint16_t)f32_to_bf16(bf16r(bf16_to_f32(ldu16(w + i)) * bf16r(y[j] * rstd)));
+  }
+}
+
+// One wave per (token, head) of the 32 q/k/v heads.  Sums the split partials
+// and rounds (the bf16 projections), then q: RMSNorm over head_dim + RoPE ->
+// Q;  k: the same -> K cache at the token's position;  v: -> V cache.
+// (modeling_qwen3.py:252-253, 168)
+__global__ void __launch_bounds__(64) qkv_finish(const float* __restrict__ part, int ksplit, int T,
+                                                 const Tok* __restrict__ tok, int L, const uint16_t* q_norm,
+                                                 const uint16_t* k_norm, const uint16_t* cos_t,
+                                                 const uint16_t* sin_t, Cache c, float eps,
+                                                 uint16_t* __restrict__ Q) {
+  const int t = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
+  const Tok tk = tok[t];
+  const float x0 = bf16r(sum_splits(part, ksplit, T, kNQKV, t, h * kD + lane));
+  const float x1 = bf16r(sum_splits(part, ksplit, T, kNQKV, t, h * kD + lane + 64));
+  if (h >= kNQ + kNKV) {
+    if (tk.valid) {
+      uint16_t* dst = c.v + cache_base(c, tk, L, h - kNQ - kNKV) + (size_t)tk.pos * kD;
+      dst[lane] = (uint16_t)f32_to_bf16(x0);
+      dst[lane + 64] = (uint16_t)f32_to_bf16(x1);
+    }
+    return;
+  }
+  const bool is_q = h < kNQ;
+  if (!is_q && !tk.valid) return;
+  const uint16_t* nw = is_q ? q_norm : k_norm;
+  const uint16_t* cr = cos_t + (size_t)tk.pos * kD;
+  const uint16_t* sr = sin_t + (size_t)tk.pos * kD;
+  const float ss = wave_sum(x0 * x0 + x1 * x1);
+  const float rstd = rcp_sqrt_torch(__fdiv_rn(ss, (float)kD) + eps);
+  const float n0 = bf16r(bf16_to_f32(ldu16(nw + lane)) * bf16r(x0 * rstd));
+  const float n1 = bf16r(bf16_to_f32(ldu16(nw + lane + 64)) * bf16r(x1 * rstd));
+  const float c0 = bf16_to_f32(ldu16(cr + lane)), c1 = bf16_to_f32(ldu16(cr + lane + 64));
+  const float s0 = bf16_to_f32(ldu16(sr + lane)), s1 = bf16_to_f32(ldu16(sr + lane + 64));
+  // x*cos + rotate_half(x)*sin, rotate_half(x) = (-x[64:], x[:64])
+  const float y0 = bf16r(bf16r(n0 * c0) + bf16r(-n1 * s0));
+  const float y1 = bf16r(bf16r(n1 * c1) + bf16r(n0 * s1));
+  uint16_t* dst = is_q ? Q + (size_t)t * kQS + h * kD : c.k + cache_base(c, tk, L, h - kNQ) + (size_t)tk.pos * kD;
+  dst[lane] = (uint16_t)f32_to_bf16(y0);
+  dst[lane + 64] = (uint16_t)f32_to_bf16(y1);
+}
+
+// M[t][n] = bf16(bf16(silu(g)) * u); g and u are columns n and I + n of the
+// gate/up product (modeling_qwen3.py:82).
+__global__ void __launch_bounds__(256) gate_up_finish(const float* __restrict__ part, int ksplit, int T, int I,
+                                                      uint16_t* __restrict__ M) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (size_t)T * I) return;
+  const int t = (int)(i / I), n = (int)(i % I);
+  const float g = bf16r(sum_splits(part, ksplit, T, 2 * I, t, n));
+  const float u = bf16r(sum_splits(part, ksplit, T, 2 * I, t, I + n));
+  const float sg = bf16r(__fdiv_rn(g, 1.0f + expf(-g)));
+  M[i] = (uint16_t)f32_to_bf16(bf16r(sg * u));
+}
+
+// ---------------------------------------------------------------- attention
+//
+// Eager GQA attention of token t over positions 0..pos of its sequence, for
+// the two query heads of KV head g (modeling_qwen3.py:185-203): scores
+// bf16(bf16(q.k) * scale), softmax in fp32 with the global max, probabilities
+// rounded to bf16, P@V summed in fp32 and rounded to bf16.
+
+// Scores of positions [c0, cend) into sc[h][p - c0]; running max in m.
+// Each 16-lane row takes one position (16 lanes x 8 dims); a wave four.
+__device__ __forceinline__ void score_chunk(const uint16_t* kc, const u32x4 (&qv)[2], float scale, int c0, int cend,
+                                            float* sc0, float* sc1, float (&m)[2]) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, slot = lane >> 4, t16 = lane & 15;
+  for (int p = c0 + wave * 4 + slot; p < cend; p += 16) {
+    const u32x4 kx = ld16(kc + (size_t)p * kD + 8 * t16);
+    const float s0 = bf16r(bf16r(row16_sum(dot8(kx, qv[0], 0.f))) * scale);
+    const float s1 = bf16r(bf16r(row16_sum(dot8(kx, qv[1], 0.f))) * scale);
+    if (t16 == 0) {
+      sc0[p - c0] = s0;
+      sc1[p - c0] = s1;
+    }
+    m[0] = fmaxf(m[0], s0);
+    m[1] = fmaxf(m[1], s1);
+  }
+}
+
+// Probability-weighted V rows [0, n) of the chunk, dims 2*lane..+1 of both
+// heads, wave w taking rows w, w+4, ...
+__device__ __forceinline__ void pv_chunk(const uint16_t* vc, const float* p0, const float* p1, int n,
+                                         float (&acc)[2][2]) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+#pragma unroll 4
+  for (int i = wave; i < n; i += 4) {
+    const uint32_t v2 = ld32(vc + (size_t)i * kD + 2 * lane);
+    const float va = lo_bf16(v2), vb = hi_bf16(v2);
+    const float pa = p0[i], pb = p1[i];
+    acc[0][0] += pa * va;
+    acc[0][1] += pa * vb;
+    acc[1][0] += pb * va;
+    acc[1][1] += pb * vb;
+  }
+}
+
+// Sum of the four waves' P@V partials (fixed order); thread (h = tid/128, d = tid%128).
+__device__ __forceinline__ float pv_merge_waves(const float (&acc)[2][2], float (*pv)[2][kD]) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  __syncthreads();
+#pragma unroll
+  for (int h = 0; h < 2; h++) {
+    pv[wave][h][2 * lane] = acc[h][0];
+    pv[wave][h][2 * lane + 1] = acc[h][1];
+  }
+  __syncthreads();
+  const int h = threadIdx.x >> 7, d = threadIdx.x & 127;
+  return ((pv[0][h][d] + pv[1][h][d]) + pv[2][h][d]) + pv[3][h][d];
+}
+
+// One workgroup per (token, KV head), for many tokens.  Contexts longer than
+// kAttnChunk are processed in chunks, recomputing the scores in each of the
+// three passes (max, sum, P@V) instead of keeping them.
+__global__ void __launch_bounds__(256) attention_rows(const uint16_t* __restrict__ Q, const Tok* __restrict__ tok,
+                                                      int L, Cache c, float scale, uint16_t* __restrict__ out) {
+  __shared__ float sc[2][kAttnChunk];
+  __shared__ float red[2][4];
+  __shared__ float pv[4][2][kD];
+  const int t = blockIdx.x, g = blockIdx.y, t16 = threadIdx.x & 15;
+  const Tok tk = tok[t];
+  uint16_t* dst = out + (size_t)t * kQS + 2 * g * kD;  // both heads: 256 contiguous values
+  if (!tk.valid) {
+    dst[threadIdx.x] = 0;
+    return;
+  }
+  const int C = tk.pos + 1;
+  const size_t base = cache_base(c, tk, L, g);
+  const uint16_t* kc = c.k + base;
+  const uint16_t* vc = c.v + base;
+  u32x4 qv[2];
+#pragma unroll
+  for (int h = 0; h < 2; h++) qv[h] = ld16(Q + (size_t)t * kQS + (2 * g + h) * kD + 8 * t16);
+  const int nch = (C + kAttnChunk - 1) / kAttnChunk;
+  float M[2] = {-INFINITY, -INFINITY};
+  for (int ch = 0; ch < nch; ch++)
+    score_chunk(kc, qv, scale, ch * kAttnChunk, min(C, (ch + 1) * kAttnChunk), sc[0], sc[1], M);
+  block_max2(M, red);
+  float S[2] = {0.f, 0.f};
+  float dummy[2];
+  for (int ch = 0; ch < nch; ch++) {
+    const int c0 = ch * kAttnChunk, n = min(C - c0, kAttnChunk);
+    if (nch > 1) {
+      __syncthreads();
+      score_chunk(kc, qv, scale, c0, c0 + n, sc[0], sc[1], dummy);
+      __syncthreads();
+    }
+    for (int i = threadIdx.x; i < n; i += 256) {
+      S[0] += exp_acc(sc[0][i] - M[0]);
+      S[1] += exp_acc(sc[1][i] - M[1]);
+    }
+  }
+  block_sum2(S, red);
+  const float inv0 = __fdiv_rn(1.0f, S[0]), inv1 = __fdiv_rn(1.0f, S[1]);
+  float acc[2][2] = {{0.f, 0.f}, {0.f, 0.f}};
+  for (int ch = 0; ch < nch; ch++) {
+    const int c0 = ch * kAttnChunk, n = min(C - c0, kAttnChunk);
+    __syncthreads();
+    if (nch > 1) {
+      score_chunk(kc, qv, scale, c0, c0 + n, sc[0], sc[1], dummy);
+      __syncthreads();
+    }
+    for (int i = threadIdx.x; i < n; i += 256) {
+      sc[0][i] = bf16r(exp_acc(sc[0][i] - M[0]) * inv0);
+      sc[1][i] = bf16r(exp_acc(sc[1][i] - M[1]) * inv1);
+    }
+    __syncthreads();
+    pv_chunk(vc + (size_t)c0 * kD, sc[0], sc[1], n, acc);
+  }
+  dst[threadIdx.x] = (uint16_t)f32_to_bf16(pv_merge_waves(acc, pv));
+}
+
+// Few tokens: the context of each (token, KV head) is split over workgroups of
+// kSplitChunk positions.  attn_split_scores writes the chunk's scores and its
+// (max m_j, sum l_j of exp(s - m_j)) per head; attn_split_pv takes the global
+// max M and the sum S = sum_j l_j * exp(m_j - M) (fixed order, identical in
+// every workgroup of the token), forms the probabilities and a partial P@V;
+// attn_split_merge adds the partials in chunk order.
+__global__ void __launch_bounds__(256) attn_split_scores(const uint16_t* __restrict__ Q, const Tok* __restrict__ tok,
+                                                         int L, Cache c, float scale, int nch,
+                                                         float* __restrict__ scores, float2* __restrict__ ml) {
+  __shared__ float sc[2][kSplitChunk];
+  __shared__ float red[2][4];
+  const int t = blockIdx.x, g = blockIdx.y, j = blockIdx.z, t16 = threadIdx.x & 15;
+  const Tok tk = tok[t];
+  const int C = tk.valid ? tk.pos + 1 : 0;
+  const int c0 = j * kSplitChunk;
+  if (c0 >= C) return;
+  const int n = min(C - c0, kSplitChunk);
+  const size_t base = cache_base(c, tk, L, g);
+  u32x4 qv[2];
+#pragma unroll
+  for (int h = 0; h < 2; h++) qv[h] = ld16(Q + (size_t)t * kQS + (2 * g + h) * kD + 8 * t16);
+  float m[2] = {-INFINITY, -INFINITY};
+  score_chunk(c.k + base, qv, scale, c0, c0 + n, sc[0], sc[1], m);
+  block_max2(m, red);
+  float l[2] = {0.f, 0.f};
+  const size_t ncap = (size_t)nch * kSplitChunk;
+  for (int i = threadIdx.x; i < n; i += 256) {
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      const float s = sc[h][i];
+      scores[((size_t)t * kNQ + 2 * g + h) * ncap + c0 + i] = s;
+      l[h] += exp_acc(s - m[h]);
+    }
+  }
+  block_sum2(l, red);
+  if (threadIdx.x < 2)
+    ml[((size_t)t * kNQ + 2 * g + threadIdx.x) * nch + j] = make_float2(m[threadIdx.x], l[threadIdx.x]);
+}
+
+__global__ void __launch_bounds__(256) attn_split_pv(const Tok* __restrict__ tok, int L, Cache c, int nch,
+                                                     const float* __restrict__ scores, const float2* __restrict__ ml,
+                                                     float* __restrict__ pvp) {
+  __shared__ float pr[2][kSplitChunk];
+  __shared__ float pv[4][2][kD];
+  const int t = blockIdx.x, g = blockIdx.y, j = blockIdx.z;
+  const Tok tk = tok[t];
+  const int C = tk.valid ? tk.pos + 1 : 0;
+  const int c0 = j * kSplitChunk;
+  if (c0 >= C) return;
+  const int n = min(C - c0, kSplitChunk), used = (C + kSplitChunk - 1) / kSplitChunk;
+  const size_t ncap = (size_t)nch * kSplitChunk;
+  float M[2], inv[2];
+#pragma unroll
+  for (int h = 0; h < 2; h++) {
+    const float2* mlh = ml + ((size_t)t * kNQ + 2 * g + h) * nch;
+    float mx = -INFINITY;
+    for (int q = 0; q < used; q++) mx = fmaxf(mx, mlh[q].x);
+    float s = 0.f;
+    for (int q = 0; q < used; q++) s += mlh[q].y * exp_acc(mlh[q].x - mx);
+    M[h] = mx;
+    inv[h] = __fdiv_rn(1.0f, s);
+  }
+  for (int i = threadIdx.x; i < n; i += 256) {
+#pragma unroll
+    for (int h = 0; h < 2; h++)
+      pr[h][i] = bf16r(exp_acc(scores[((size_t)t * kNQ + 2 * g + h) * ncap + c0 + i] - M[h]) * inv[h]);
+  }
+  __syncthreads();
+  float acc[2][2] = {{0.f, 0.f}, {0.f, 0.f}};
+  pv_chunk(c.v + cache_base(c, tk, L, g) + (size_t)c0 * kD, pr[0], pr[1], n, acc);
+  const float y = pv_merge_waves(acc, pv);
+  pvp[(((size_t)t * nch + j) * kNQ + 2 * g) * kD + threadIdx.x] = y;
+}
+
+// out[t][i] = bf16(sum over the token's chunks of the partial P@V), i over
+// the 16 x 128 head outputs; grid (token, 8 slices of 256).
+__global__ void __launch_bounds__(256) attn_split_merge(const Tok* __restrict__ tok, int nch,
+                                                        const float* __restrict__ pvp, uint16_t* __restrict__ out) {
+  const int t = blockIdx.x, i = blockIdx.y * 256 + threadIdx.x;
+  const Tok tk = tok[t];
+  const int C = tk.valid ? tk.pos + 1 : 0;
+  const int used = (C + kSplitChunk - 1) / kSplitChunk;
+  const float* src = pvp + (size_t)t * nch * kQS + i;
+  float y = 0.f;
+#pragma unroll 8
+  for (int q = 0; q < used; q++) y += src[(size_t)q * kQS];
+  out[(size_t)t * kQS + i] = (uint16_t)f32_to_bf16(y);
+}
+
+// ---------------------------------------------------------------- LM head
+//
+// The LM head runs as lm_head_gemm (the GEMM above over the full K, one wave
+// per 16-row x 64-column tile) whose epilogue rounds each logit to bf16,
+// optionally writes its fp32 copy, and keeps, per row and tile, the largest
+// key (orderable bf16 logit << 32 | ~index): the first index of the maximum,
+// HF's greedy argmax.  keys_reduce then takes each row's largest key over the
+// tiles; no atomics, so the result is independent of scheduling.
+
+__device__ __forceinline__ unsigned long long key_max(unsigned long long a, unsigned long long b) { return a > b ? a : b; }
+
+__global__ void __launch_bounds__(256) lm_head_gemm(const uint16_t* __restrict__ X, const int* __restrict__ rows,
+                                                    int R, const uint16_t* __restrict__ W, int K, int V,
+                                                    unsigned long long* __restrict__ keys_part,
+                                                    float* __restrict__ logits) {
+  constexpr int NB = 4;
+  const int nblk = gridDim.x;
+  const int b = blockIdx.x;
+  const int lb = (nblk % kGroups == 0) ? (b % kGroups) * (nblk / kGroups) + b / kGroups : b;
+  const int wave = lb * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int mtiles = (R + 15) / 16, ntiles = V / (16 * NB);
+  const int mt = wave % mtiles, nt = wave / mtiles;
+  if (nt >= ntiles) return;
+  const int kq = 8 * (lane >> 4);
+  const int xr = max(rows[min(mt * 16 + (lane & 15), R - 1)], 0);
+  const uint16_t* xa = X + (size_t)xr * K + kq;
+  const uint16_t* wb[NB];
+#pragma unroll
+  for (int j = 0; j < NB; j++) wb[j] = W + (size_t)(nt * 16 * NB + 16 * j + (lane & 15)) * K + kq;
+  f32x4 acc[NB];
+#pragma unroll
+  for (int j = 0; j < NB; j++) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  bf16x8 a0 = ld_bf16x8(xa), a1 = ld_bf16x8(xa + 32), b0[NB], b1[NB];
+#pragma unroll
+  for (int j = 0; j < NB; j++) {
+    b0[j] = ld_bf16x8_stream(wb[j]);
+    b1[j] = ld_bf16x8_stream(wb[j] + 32);
+  }
+  for (int k = 0; k < K; k += 64) {
+    bf16x8 na0, na1, nb0[NB], nb1[NB];
+    const bool more = k + 64 < K;
+    if (more) {
+      na0 = ld_bf16x8(xa + k + 64);
+      na1 = ld_bf16x8(xa + k + 96);
+#pragma unroll
+      for (int j = 0; j < NB; j++) {
+        nb0[j] = ld_bf16x8_stream(wb[j] + k + 64);
+        nb1[j] = ld_bf16x8_stream(wb[j] + k + 96);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < NB; j++) {
+      acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b0[j], acc[j], 0, 0, 0);
+      acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b1[j], acc[j], 0, 0, 0);
+    }
+    if (more) {
+      a0 = na0;
+      a1 = na1;
+#pragma unroll
+      for (int j = 0; j < NB; j++) {
+        b0[j] = nb0[j];
+        b1[j] = nb1[j];
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int t = mt * 16 + 4 * (lane >> 4) + i;
+    unsigned long long best = 0;
+#pragma unroll
+    for (int j = 0; j < NB; j++) {
+      const int n = nt * 16 * NB + 16 * j + (lane & 15);
+      const uint32_t hb = f32_to_bf16(acc[j][i]);
+      if (logits && t < R) logits[(size_t)t * V + n] = bf16_to_f32(hb);
+      best = key_max(best, ((unsigned long long)orderable16(hb) << 32) | (unsigned long long)(0xffffffffu - (uint32_t)n));
+    }
+    // max over the 16 lanes that hold row t
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) best = key_max(best, __shfl_xor(best, o));
+    if ((lane & 15) == 0 && t < R) keys_part[(size_t)t * ntiles + nt] = best;
+  }
+}
+
+// out[r] = token of row r's largest key over the LM head's tiles (-1 for an
+// invalid emit row or token).  One workgroup per row.
+__global__ void __launch_bounds__(256) keys_reduce(const unsigned long long* __restrict__ keys_part, int ntiles,
+                                                   const int* __restrict__ erow, const Tok* __restrict__ tok,
+                                                   int* __restrict__ out) {
+  __shared__ unsigned long long red[4];
+  const int r = blockIdx.x, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  unsigned long long best = 0;
+  for (int i = threadIdx.x; i < ntiles; i += 256) best = key_max(best, keys_part[(size_t)r * ntiles + i]);
+  best = wave_max_u64(best);
+  if (lane == 0) red[wave] = best;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    best = key_max(key_max(red[0], red[1]), key_max(red[2], red[3]));
+    const int e = erow[r];
+    out[r] = (e >= 0 && tok[e].valid) ? (int)(0xffffffffu - (uint32_t)best) : -1;
+  }
+}
+
+// ---------------------------------------------------------------- self-test
+
+// C[16][16] = A[16][32] . B[16][32]^T through one MFMA with the operand
+// layouts gemm_partial assumes.
+__global__ void mfma_selftest(const uint16_t* A, const uint16_t* B, float* C) {
+  const int lane = threadIdx.x, kq = 8 * (lane >> 4);
+  const bf16x8 a = ld_bf16x8(A + (lane & 15) * 32 + kq);
+  const bf16x8 b = ld_bf16x8(B + (lane & 15) * 32 + kq);
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
+#pragma unroll
+  for (int i = 0; i < 4; i++) C[(4 * (lane >> 4) + i) * 16 + (lane & 15)] = acc[i];
+}
+
+// ---------------------------------------------------------------- host side
+
+struct Gemm {
+  int nb, ksplit;
+};
+
+// 64-column tiles (16 for N not a multiple of 64); the K range is split
+// (up to kMaxSplit ways, >= 64 K per wave) until about kTargetWaves waves
+// stream the weights.
+Gemm plan_gemm(int T, int N, int K) {
+  const int mt = (T + 15) / 16;
+  const int nb = N % 64 == 0 ? 4 : 1;
+  int ks = 1;
+  while ((long long)mt * (N / (16 * nb)) * ks < kTargetWaves && ks * 2 <= kMaxSplit && K % (ks * 2 * 64) == 0)
+    ks *= 2;
+  return {nb, ks};
+}
+
+void launch_gemm(const uint16_t* X, const int* rows, int T, int K, const Seg& seg, int N, float* part, hipStream_t s,
+                 int* ks_out) {
+  const Gemm g = plan_gemm(T, N, K);
+  const int mt = (T + 15) / 16;
+  const long long waves = (long long)mt * (N / (16 * g.nb)) * g.ksplit;
+  const dim3 grid((unsigned)((waves + 3) / 4));
+  const bool stream = mt == 1;  // each weight tile is read once: bypass the caches
+  if (g.nb == 4) {
+    if (stream)
+      hipLaunchKernelGGL((gemm_partial<4, true>), grid, dim3(256), 0, s, X, rows, T, K, seg, N, g.ksplit, part);
+    else
+      hipLaunchKernelGGL((gemm_partial<4, false>), grid, dim3(256), 0, s, X, rows, T, K, seg, N, g.ksplit, part);
+  } else {
+    if (stream)
+      hipLaunchKernelGGL((gemm_partial<1, true>), grid, dim3(256), 0, s, X, rows, T, K, seg, N, g.ksplit, part);
+    else
+      hipLaunchKernelGGL((gemm_partial<1, false>), grid, dim3(256), 0, s, X, rows, T, K, seg, N, g.ksplit, part);
+  }
+  *ks_out = g.ksplit;
+}
+
+size_t part_floats(int T, int N, int K) { return (size_t)plan_gemm(T, N, K).ksplit * T * N; }
+
+int split_chunks(int max_context) { return (max_context + kSplitChunk - 1) / kSplitChunk; }
+
+struct Layout {
+  size_t tok, erow, keys, x, n, q, att, m, part, scores, ml, pv, total;
+};
+
+constexpr int kLmTiles(int V) { return V / 64; }
+
+template <class M>
+Layout layout(int T, int R, int max_context) {
+  using Dm = Dims<M>;
+  auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
+  Layout l{};
+  size_t off = 0;
+  auto take = [&](size_t& field, size_t bytes) {
+    field = off;
+    off += al(bytes);
+  };
+  take(l.tok, (size_t)T * sizeof(Tok));
+  take(l.erow, (size_t)R * 4);
+  take(l.keys, (size_t)R * kLmTiles(Dm::V) * 8);
+  take(l.x, (size_t)T * Dm::H * 2);
+  take(l.n, (size_t)T * Dm::H * 2);
+  take(l.q, (size_t)T * kQS * 2);
+  take(l.att, (size_t)T * kQS * 2);
+  take(l.m, (size_t)T * Dm::I * 2);
+  size_t pf = part_floats(T, kNQKV, Dm::H);
+  pf = std::max(pf, part_floats(T, Dm::H, kQS));
+  pf = std::max(pf, part_floats(T, 2 * Dm::I, Dm::H));
+  pf = std::max(pf, part_floats(T, Dm::H, Dm::I));
+  take(l.part, pf * 4);
+  if (T < kSplitBelow) {
+    const int nch = split_chunks(max_context);
+    take(l.scores, (size_t)T * kNQ * nch * kSplitChunk * 4);
+    take(l.ml, (size_t)T * kNQ * nch * 8);
+    take(l.pv, (size_t)T * nch * kQS * 4);
+  }
+  l.total = off;
+  return l;
+}
+
+struct Args {
+  int T, R, num_seqs, max_context;
+  const int *tokens, *seqs, *pos, *emit;
+  int* out_tokens;
+  float* logits;
+  const uint16_t *embed, *final_norm, *lm_head, *cos_t, *sin_t;
+  const LDGLayerWeights* layers;  // host array
+  Cache cache;
+  int num_layers;
+  float attn_scale;
+  char* ws;
+};
+
+template <class M>
+int forward(const Args& a, hipStream_t s) {
+  using Dm = Dims<M>;
+  const int T = a.T, R = a.R;
+  const Layout l = layout<M>(T, R, a.max_context);
+  Tok* tok = reinterpret_cast<Tok*>(a.ws + l.tok);
+  int* erow = reinterpret_cast<int*>(a.ws + l.erow);
+  auto* keys = reinterpret_cast<unsigned long long*>(a.ws + l.keys);
+  uint16_t* X = reinterpret_cast<uint16_t*>(a.ws + l.x);
+  uint16_t* N = reinterpret_cast<uint16_t*>(a.ws + l.n);
+  uint16_t* Qb = reinterpret_cast<uint16_t*>(a.ws + l.q);
+  uint16_t* ATT = reinterpret_cast<uint16_t*>(a.ws + l.att);
+  uint16_t* MM = reinterpret_cast<uint16_t*>(a.ws + l.m);
+  float* part = reinterpret_cast<float*>(a.ws + l.part);
+  const float eps = 1e-6f;
+  const bool split = T < kSplitBelow;
+  const int nch = split ? split_chunks(a.max_context) : 0;
+  auto blocks = [](size_t n) { return dim3((unsigned)((n + 255) / 256)); };
+  auto u16 = [](const void* p) { return static_cast<const uint16_t*>(p); };
+  int ks = 1;
+
+  hipLaunchKernelGGL(prep_tokens, blocks(std::max(T, R)), dim3(256), 0, s, a.tokens, a.seqs, a.pos, T, a.emit, R,
+                     a.num_seqs, a.max_context, Dm::V, tok, erow);
+  hipLaunchKernelGGL(embed_rows, dim3(T), dim3(256), 0, s, a.embed, tok, Dm::H, X);
+  hipLaunchKernelGGL((residual_norm<Dm::H>), dim3(T), dim3(1024), 0, s, nullptr, 0, T, X,
+                     u16(a.layers[0].input_layernorm_weight), eps, N);
+  for (int L = 0; L < a.num_layers; L++) {
+    const LDGLayerWeights& w = a.layers[L];
+    const Seg qkv{{u16(w.q_proj_weight), u16(w.k_proj_weight), u16(w.v_proj_weight)}, {kQS, kNKV * kD, kNKV * kD}};
+    launch_gemm(N, nullptr, T, Dm::H, qkv, kNQKV, part, s, &ks);
+    hipLaunchKernelGGL(qkv_finish, dim3(T, kNQ + 2 * kNKV), dim3(64), 0, s, part, ks, T, tok, L, u16(w.q_norm_weight),
+                       u16(w.k_norm_weight), a.cos_t, a.sin_t, a.cache, eps, Qb);
+    if (split) {
+      float* scores = reinterpret_cast<float*>(a.ws + l.scores);
+      float2* ml = reinterpret_cast<float2*>(a.ws + l.ml);
+      float* pvp = reinterpret_cast<float*>(a.ws + l.pv);
+      hipLaunchKernelGGL(attn_split_scores, dim3(T, kNKV, nch), dim3(256), 0, s, Qb, tok, L, a.cache, a.attn_scale,
+                         nch, scores, ml);
+      hipLaunchKernelGGL(attn_split_pv, dim3(T, kNKV, nch), dim3(256), 0, s, tok, L, a.cache, nch, scores, ml, pvp);
+      hipLaunchKernelGGL(attn_split_merge, dim3(T, kQS / 256), dim3(256), 0, s, tok, nch, pvp, ATT);
+    } else {
+      hipLaunchKernelGGL(attention_rows, dim3(T, kNKV), dim3(256), 0, s, Qb, tok, L, a.cache, a.attn_scale, ATT);
+    }
+    const Seg o{{u16(w.o_proj_weight), nullptr, nullptr}, {Dm::H, 0, 0}};
+    launch_gemm(ATT, nullptr, T, kQS, o, Dm::H, part, s, &ks);
+    hipLaunchKernelGGL((residual_norm<Dm::H>), dim3(T), dim3(1024), 0, s, part, ks, T, X,
+                       u16(w.post_attn_layernorm_weight), eps, N);
+    const Seg gu{{u16(w.gate_proj_weight), u16(w.up_proj_weight), nullptr}, {Dm::I, Dm::I, 0}};
+    launch_gemm(N, nullptr, T, Dm::H, gu, 2 * Dm::I, part, s, &ks);
+    hipLaunchKernelGGL(gate_up_finish, blocks((size_t)T * Dm::I), dim3(256), 0, s, part, ks, T, Dm::I, MM);
+    const Seg dn{{u16(w.down_proj_weight), nullptr, nullptr}, {Dm::H, 0, 0}};
+    launch_gemm(MM, nullptr, T, Dm::I, dn, Dm::H, part, s, &ks);
+    const uint16_t* next_norm = L + 1 < a.num_layers ? u16(a.layers[L + 1].input_layernorm_weight) : a.final_norm;
+    hipLaunchKernelGGL((residual_norm<Dm::H>), dim3(T), dim3(1024), 0, s, part, ks, T, X, next_norm, eps, N);
+  }
+  const int lm_waves = ((R + 15) / 16) * kLmTiles(Dm::V);
+  hipLaunchKernelGGL(lm_head_gemm, dim3((lm_waves + 3) / 4), dim3(256), 0, s, N, erow, R, a.lm_head, Dm::H, Dm::V,
+                     keys, a.logits);
+  hipLaunchKernelGGL(keys_reduce, dim3(R), dim3(256), 0, s, keys, kLmTiles(Dm::V), erow, tok, a.out_tokens);
+  return hipGetLastError() == hipSuccess ? QMK_OK : QMK_ERR_HIP;
+}
+
+}  // namespace batch
+}  // namespace qmk
+
+using namespace qmk;
+
+extern "C" {
+
+size_t qmk_forward_workspace_bytes(int model, int num_tokens, int num_emit, int max_context) {
+  if (num_tokens < 1 || num_emit < 1 || num_emit > batch::kMaxEmit || max_context < 1) return 0;
+  if (model == QMK_MODEL_QWEN3_1_7B) return batch::layout<Qwen3_1_7B>(num_tokens, num_emit, max_context).total;
+  if (model == QMK_MODEL_QWEN3_0_6B) return batch::layout<Qwen3_0_6B>(num_tokens, num_emit, max_context).total;
+  return 0;
+}
+
+int qmk_forward_tokens(int model, int num_tokens, const int* tokens, const int* seq_ids, const int* positions,
+                       int num_emit, const int* emit_rows, int* out_tokens, float* logits_out,
+                       const void* embed_weight, const LDGLayerWeights* layer_weights_host,
+                       const void* final_norm_weight, const void* lm_head_weight, const void* cos_table,
+                       const void* sin_table, void* k_cache, void* v_cache, int num_seqs, long long seq_stride,
+                       int num_layers, int max_seq_len, int max_context, float attn_scale, void* workspace,
+                       size_t workspace_bytes, hipStream_t stream) {
+  if (model != QMK_MODEL_QWEN3_0_6B && model != QMK_MODEL_QWEN3_1_7B) return QMK_ERR_ARG;
+  if (num_tokens < 1 || num_emit < 1 || num_emit > batch::kMaxEmit || !tokens || !seq_ids || !positions ||
+      !emit_rows || !out_tokens || !embed_weight || !layer_weights_host || !final_norm_weight || !lm_head_weight ||
+      !cos_table || !sin_table || !k_cache || !v_cache || !workspace || num_seqs < 1 || num_layers < 1 ||
+      num_layers > kMaxLayers || max_seq_len < 1 || max_context < 1 || max_context > max_seq_len ||
+      !(attn_scale > 0.f))
+    return QMK_ERR_ARG;
+  const long long kv_per_seq = (long long)num_layers * batch::kNKV * max_seq_len * batch::kD;
+  if (num_seqs > 1 && seq_stride < kv_per_seq) return QMK_ERR_ARG;
+  for (int L = 0; L < num_layers; L++) {
+    const LDGLayerWeights& w = layer_weights_host[L];
+    const void* p[11] = {w.input_layernorm_weight, w.q_proj_weight, w.k_proj_weight, w.v_proj_weight,
+                         w.q_norm_weight, w.k_norm_weight, w.o_proj_weight, w.post_attn_layernorm_weight,
+                         w.gate_proj_weight, w.up_proj_weight, w.down_proj_weight};
+    for (const void* q : p)
+      if (!q) return QMK_ERR_ARG;
+  }
+  if (workspace_bytes < qmk_forward_workspace_bytes(model, num_tokens, num_emit, max_context)) return QMK_ERR_ARG;
+  batch::Args a{};
+  a.T = num_tokens;
+  a.R = num_emit;
+  a.num_seqs = num_seqs;
+  a.max_context = max_context;
+  a.tokens = tokens;
+  a.seqs = seq_ids;
+  a.pos = positions;
+  a.emit = emit_rows;
+  a.out_tokens = out_tokens;
+  a.logits = logits_out;
+  a.embed = static_cast<const uint16_t*>(embed_weight);
+  a.final_norm = static_cast<const uint16_t*>(final_norm_weight);
+  a.lm_head = static_cast<const uint16_t*>(lm_head_weight);
+  a.cos_t = static_cast<const uint16_t*>(cos_table);
+  a.sin_t = static_cast<const uint16_t*>(sin_table);
+  a.layers = layer_weights_host;
+  a.cache = batch::Cache{static_cast<uint16_t*>(k_cache), static_cast<uint16_t*>(v_cache),
+                         num_seqs > 1 ? seq_stride : 0, max_seq_len};
+  a.num_layers = num_layers;
+  a.attn_scale = attn_scale;
+  a.ws = static_cast<char*>(workspace);
+  return model == QMK_MODEL_QWEN3_1_7B ? batch::forward<Qwen3_1_7B>(a, stream) : batch::forward<Qwen3_0_6B>(a, stream);
+}
+
+int qmk_selftest_mfma(const void* a, const void* b, float* c, hipStream_t stream) {
+  if (!a || !b || !c) return QMK_ERR_ARG;
+  hipLaunchKernelGGL(batch::mfma_selftest, dim3(1), dim3(64), 0, stream, static_cast<const uint16_t*>(a),
+                     static_cast<const uint16_t*>(b), c);
+  return hipGetLastError() == hipSuccess ? QMK_OK : QMK_ERR_HIP;
+}
+
+}  // extern "C"

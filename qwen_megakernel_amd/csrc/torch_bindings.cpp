@@ -8,8 +8,10 @@
 // position is range-checked before anything is launched; failures raise
 // through TORCH_CHECK instead of writing out of bounds.  Additive ops:
 // `decode_logits` (also returns the fp32 copy of the bf16 logits),
-// `device_error`, `reset`, `set_wait_limit`, `set_trace` (phase trace) and
-// `phase_bench` (per-phase weight-streaming microbenchmark).
+// `device_error`, `reset`, `set_wait_limit`, `set_trace` (phase trace),
+// `phase_bench` (per-phase weight-streaming microbenchmark), and the batched
+// forward `forward_tokens` (prefill, batched decode) with
+// `forward_workspace_bytes` and `selftest_mfma`.
 
 #include <Python.h>
 #include <ATen/hip/impl/HIPGuardImplMasqueradingAsCUDA.h>
@@ -278,6 +280,116 @@ void phase_bench(int64_t phase, torch::Tensor weights, int64_t n_copies, std::op
   TORCH_CHECK(s == QMK_OK, "phase_bench failed: ", qmk_status_string(s));
 }
 
+// Batched forward (qmk_forward_tokens): T tokens of any sequences at any
+// positions through the MFMA path; prefill and batched decode.  k_cache /
+// v_cache are [L, 8, S, 128] (one sequence) or [B, L, 8, S, 128];
+// layer_weights is the reference's flat list of 11 tensors per layer
+// (qwen_megakernel/model.py:82-89).
+int model_of_hidden(int64_t hidden) {
+  TORCH_CHECK(hidden == 1024 || hidden == 2048, "hidden must be 1024 (Qwen3-0.6B) or 2048 (Qwen3-1.7B)");
+  return hidden == 1024 ? QMK_MODEL_QWEN3_0_6B : QMK_MODEL_QWEN3_1_7B;
+}
+
+int64_t forward_workspace_bytes(int64_t hidden, int64_t num_tokens, int64_t num_emit, int64_t max_context) {
+  TORCH_CHECK(num_tokens >= 1 && num_tokens <= (1 << 20), "num_tokens out of range");
+  TORCH_CHECK(num_emit >= 1 && num_emit <= 256, "num_emit must be in [1, 256]");
+  TORCH_CHECK(max_context >= 1 && max_context <= 65536, "max_context must be in [1, 65536]");
+  return (int64_t)qmk_forward_workspace_bytes(model_of_hidden(hidden), (int)num_tokens, (int)num_emit,
+                                              (int)max_context);
+}
+
+void forward_tokens(torch::Tensor tokens, torch::Tensor seq_ids, torch::Tensor positions, torch::Tensor emit_rows,
+                    torch::Tensor out_tokens, std::optional<torch::Tensor> logits, torch::Tensor embed_weight,
+                    std::vector<torch::Tensor> layer_weights, torch::Tensor final_norm_weight,
+                    torch::Tensor lm_head_weight, torch::Tensor cos_table, torch::Tensor sin_table,
+                    torch::Tensor k_cache, torch::Tensor v_cache, torch::Tensor workspace, int64_t num_layers,
+                    int64_t max_context, double attn_scale) {
+  check_bf16(embed_weight, "embed_weight", -1);
+  const int64_t hidden = embed_weight.numel() / kVocab;
+  TORCH_CHECK(embed_weight.numel() == kVocab * hidden, "embed_weight must be [151936, hidden]");
+  const int model = model_of_hidden(hidden);
+  const int64_t inter = 3 * hidden;
+  TORCH_CHECK(num_layers >= 1 && num_layers <= kMaxLayers, "num_layers must be in [1, 28], got ", num_layers);
+  TORCH_CHECK(attn_scale > 0.0, "attn_scale must be positive");
+  check_bf16(final_norm_weight, "final_norm_weight", hidden);
+  check_bf16(lm_head_weight, "lm_head_weight", kVocab * hidden);
+  TORCH_CHECK((int64_t)layer_weights.size() >= 11 * num_layers, "layer_weights must hold 11 tensors per layer");
+  const int64_t sizes[11] = {hidden, kQ * hidden, kKV * hidden, kKV * hidden, kHeadDim, kHeadDim,
+                             hidden * kQ, hidden, inter * hidden, inter * hidden, hidden * inter};
+  std::vector<LDGLayerWeights> table((size_t)num_layers);
+  for (int64_t L = 0; L < num_layers; L++) {
+    const void* p[11];
+    for (int i = 0; i < 11; i++) {
+      const torch::Tensor& t = layer_weights[(size_t)(11 * L + i)];
+      check_bf16(t, "layer weight", sizes[i]);
+      TORCH_CHECK(t.device() == embed_weight.device(), "all tensors must be on the same device");
+      p[i] = t.data_ptr();
+    }
+    table[(size_t)L] = LDGLayerWeights{p[0], p[1], p[2], p[3], p[4], p[5], p[6], p[7], p[8], p[9], p[10]};
+  }
+  check_bf16(k_cache, "k_cache", -1);
+  check_bf16(v_cache, "v_cache", -1);
+  TORCH_CHECK(v_cache.sizes() == k_cache.sizes(), "v_cache must match k_cache");
+  TORCH_CHECK((k_cache.dim() == 4 || k_cache.dim() == 5) && k_cache.size(-3) == kKVHeads &&
+                  k_cache.size(-1) == kHeadDim && k_cache.size(-4) >= num_layers,
+              "k_cache must be [>= num_layers, 8, S, 128] or [B, >= num_layers, 8, S, 128]");
+  const int64_t max_seq_len = k_cache.size(-2);
+  const int64_t num_seqs = k_cache.dim() == 5 ? k_cache.size(0) : 1;
+  TORCH_CHECK(num_seqs >= 1 && max_seq_len >= 1 && max_seq_len <= 65536, "k_cache sizes out of range");
+  const int64_t seq_stride = k_cache.size(-4) * kKVHeads * max_seq_len * kHeadDim;
+  TORCH_CHECK(max_context >= 1 && max_context <= max_seq_len, "max_context must be in [1, ", max_seq_len, "]");
+  check_bf16(cos_table, "cos_table", -1);
+  check_bf16(sin_table, "sin_table", -1);
+  TORCH_CHECK(cos_table.dim() == 2 && cos_table.size(1) == kHeadDim && cos_table.size(0) >= max_seq_len,
+              "cos_table must be [>= max_seq_len, 128]");
+  TORCH_CHECK(sin_table.sizes() == cos_table.sizes(), "sin_table must match cos_table");
+  for (const torch::Tensor* t : {&tokens, &seq_ids, &positions, &emit_rows, &out_tokens}) {
+    check_cuda(*t, "token arrays");
+    TORCH_CHECK(t->scalar_type() == torch::kInt32, "tokens, seq_ids, positions, emit_rows, out_tokens must be int32");
+    TORCH_CHECK(t->device() == embed_weight.device(), "all tensors must be on the same device");
+  }
+  const int64_t T = tokens.numel(), R = emit_rows.numel();
+  TORCH_CHECK(T >= 1 && T <= (1 << 20), "tokens must hold 1 .. 2^20 entries");
+  TORCH_CHECK(seq_ids.numel() == T && positions.numel() == T, "seq_ids and positions must match tokens");
+  TORCH_CHECK(R >= 1 && R <= 256, "emit_rows must hold 1 .. 256 entries");
+  TORCH_CHECK(out_tokens.numel() == R, "out_tokens must match emit_rows");
+  float* lg = nullptr;
+  if (logits.has_value()) {
+    check_cuda(*logits, "logits");
+    TORCH_CHECK(logits->scalar_type() == torch::kFloat32 && logits->numel() == R * kVocab,
+                "logits must be float32[num_emit, 151936]");
+    lg = static_cast<float*>(logits->data_ptr());
+  }
+  check_cuda(workspace, "workspace");
+  const size_t need = qmk_forward_workspace_bytes(model, (int)T, (int)R, (int)max_context);
+  TORCH_CHECK((size_t)(workspace.numel() * workspace.element_size()) >= need, "workspace is smaller than ", need,
+              " bytes");
+  for (const torch::Tensor* t : {&final_norm_weight, &lm_head_weight, &cos_table, &sin_table, &k_cache, &v_cache,
+                                 &workspace})
+    TORCH_CHECK(t->device() == embed_weight.device(), "all tensors must be on the same device");
+  const c10::hip::HIPGuardMasqueradingAsCUDA guard(embed_weight.device());
+  const int s = qmk_forward_tokens(
+      model, (int)T, static_cast<const int*>(tokens.data_ptr()), static_cast<const int*>(seq_ids.data_ptr()),
+      static_cast<const int*>(positions.data_ptr()), (int)R, static_cast<const int*>(emit_rows.data_ptr()),
+      static_cast<int*>(out_tokens.data_ptr()), lg, embed_weight.data_ptr(), table.data(),
+      final_norm_weight.data_ptr(), lm_head_weight.data_ptr(), cos_table.data_ptr(), sin_table.data_ptr(),
+      k_cache.data_ptr(), v_cache.data_ptr(), (int)num_seqs, (long long)seq_stride, (int)num_layers,
+      (int)max_seq_len, (int)max_context, (float)attn_scale, workspace.data_ptr(), need,
+      c10::hip::getCurrentHIPStreamMasqueradingAsCUDA().stream());
+  TORCH_CHECK(s == QMK_OK, "forward_tokens failed: ", qmk_status_string(s));
+}
+
+void selftest_mfma(torch::Tensor a, torch::Tensor b, torch::Tensor c) {
+  check_bf16(a, "a", 16 * 32);
+  check_bf16(b, "b", 16 * 32);
+  check_cuda(c, "c");
+  TORCH_CHECK(c.scalar_type() == torch::kFloat32 && c.numel() == 256, "c must be float32[16, 16]");
+  const c10::hip::HIPGuardMasqueradingAsCUDA guard(a.device());
+  const int s = qmk_selftest_mfma(a.data_ptr(), b.data_ptr(), static_cast<float*>(c.data_ptr()),
+                                  c10::hip::getCurrentHIPStreamMasqueradingAsCUDA().stream());
+  TORCH_CHECK(s == QMK_OK, "selftest_mfma failed: ", qmk_status_string(s));
+}
+
 }  // namespace
 
 TORCH_LIBRARY(qwen_megakernel_C, ops) {
@@ -324,6 +436,18 @@ TORCH_LIBRARY(qwen_megakernel_C, ops) {
   ops.def("set_trace(Tensor? buf) -> ()", &set_trace);
   ops.def("phase_bench(int phase, Tensor weights, int n_copies, Tensor? norm_weight, Tensor act, Tensor out) -> ()");
   ops.impl("phase_bench", torch::kCUDA, &phase_bench);
+
+  ops.def("forward_workspace_bytes(int hidden, int num_tokens, int num_emit, int max_context) -> int",
+          &forward_workspace_bytes);
+  ops.def(
+      "forward_tokens(Tensor tokens, Tensor seq_ids, Tensor positions, Tensor emit_rows, "
+      "Tensor out_tokens, Tensor? logits, Tensor embed_weight, Tensor[] layer_weights, "
+      "Tensor final_norm_weight, Tensor lm_head_weight, Tensor cos_table, Tensor sin_table, "
+      "Tensor k_cache, Tensor v_cache, Tensor workspace, int num_layers, int max_context, "
+      "float attn_scale) -> ()");
+  ops.impl("forward_tokens", torch::kCUDA, &forward_tokens);
+  ops.def("selftest_mfma(Tensor a, Tensor b, Tensor c) -> ()");
+  ops.impl("selftest_mfma", torch::kCUDA, &selftest_mfma);
 }
 
 // Empty Python module so the shared object can also be imported by name

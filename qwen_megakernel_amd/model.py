@@ -20,6 +20,12 @@ Differences, all additive:
   positions are range-checked.
 * ``Decoder.step_logits`` returns the logits as well, ``Decoder.load_kv`` injects
   cache contents, and ``generate`` accepts token-id lists when there is no tokenizer.
+* ``Decoder.prefill`` runs a whole prompt through the batched MFMA forward
+  (``torch.ops.qwen_megakernel_C.forward_tokens``) in one pass; ``generate``
+  uses it for the prompt instead of one decode step per prompt token
+  (``use_prefill=False`` restores the reference's per-token feeding).
+* ``BatchDecoder`` decodes several independent sequences together, one batched
+  forward per step.
 """
 
 from __future__ import annotations
@@ -104,12 +110,47 @@ def _pack_layer_weights(layer_weights: list[torch.Tensor], num_layers: int = NUM
     return torch.frombuffer(buf, dtype=torch.uint8).to(layer_weights[0].device)
 
 
+def _as_i32(values, device) -> torch.Tensor:
+    return torch.tensor([int(v) for v in values], dtype=torch.int32, device=device)
+
+
+class _Forward:
+    """Calls ``forward_tokens`` with one model's weights; caches workspaces by size."""
+
+    def __init__(self, ops, weights: dict, num_layers: int):
+        self._ops = ops
+        self.embed = weights["embed_weight"]
+        self.layers = list(weights["layer_weights"][: 11 * num_layers])
+        self.final_norm = weights["final_norm_weight"]
+        self.lm_head = weights["lm_head_weight"]
+        self.cos = weights["cos_table"]
+        self.sin = weights["sin_table"]
+        self.num_layers = num_layers
+        self.hidden = self.embed.shape[-1]
+        self.scale = 1.0 / math.sqrt(HEAD_DIM)
+        self._ws = torch.empty(0, dtype=torch.uint8, device=self.embed.device)
+
+    def workspace(self, num_tokens: int, num_emit: int, max_context: int) -> torch.Tensor:
+        need = int(self._ops.forward_workspace_bytes(self.hidden, num_tokens, num_emit, max_context))
+        if self._ws.numel() < need:
+            self._ws = torch.empty(need, dtype=torch.uint8, device=self.embed.device)
+        return self._ws
+
+    def __call__(self, tokens, seq_ids, positions, emit_rows, out_tokens, logits, k_cache, v_cache,
+                 max_context: int):
+        ws = self.workspace(tokens.numel(), emit_rows.numel(), max_context)
+        self._ops.forward_tokens(tokens, seq_ids, positions, emit_rows, out_tokens, logits, self.embed, self.layers,
+                                 self.final_norm, self.lm_head, self.cos, self.sin, k_cache, v_cache, ws,
+                                 self.num_layers, max_context, self.scale)
+
+
 class Decoder:
     """Stateful decoder over torch.ops.qwen_megakernel_C (model.py:111-245)."""
 
     def __init__(self, weights=None, tokenizer=None, model_name: str = "Qwen/Qwen3-0.6B", verbose: bool = True,
-                 max_seq_len: int = MAX_SEQ_LEN, num_layers: int = NUM_LAYERS):
+                 max_seq_len: int = MAX_SEQ_LEN, num_layers: int = NUM_LAYERS, use_prefill: bool = True):
         self._ops = _ops()
+        self.use_prefill = use_prefill
         if weights is None:
             weights, tokenizer = load_weights(model_name, verbose=verbose, max_seq_len=max_seq_len)
         weights = _w.to_device(weights, "cuda")
@@ -153,6 +194,7 @@ class Decoder:
         self._bmax_idxs = torch.empty(4096, dtype=torch.int32, device=dev)
         self._out_token = torch.empty(1, dtype=torch.int32, device=dev)
         self._logits = torch.empty(VOCAB_SIZE, **f32)
+        self._forward = _Forward(self._ops, weights, num_layers)
 
     # -- reference API --------------------------------------------------
 
@@ -214,8 +256,11 @@ class Decoder:
         """Step ``ids[:-1]``, then ``max_tokens`` device-fed greedy steps from ``ids[-1]``."""
         if not ids:
             raise ValueError("empty prompt")
-        for tid in ids[:-1]:
-            self.step(tid)
+        if self.use_prefill and len(ids) > 1:
+            self.prefill(ids[:-1])
+        else:
+            for tid in ids[:-1]:
+                self.step(tid)
         self._check_position(max_tokens)
         out = self._ops.generate_nosync(int(ids[-1]), int(max_tokens), *self._scratch(), self._num_layers,
                                         self._position, self._max_seq_len, self._attn_scale)
@@ -236,6 +281,35 @@ class Decoder:
             self._raise_device_error()
         return tok, self._logits.clone()
 
+    def prefill(self, ids, return_logits: bool = False):
+        """Run ``ids`` at positions ``position .. position+len-1`` in one batched forward.
+
+        Writes their K/V into the cache exactly as that many ``step`` calls
+        would, and returns the greedy token after the last one (with its fp32
+        logits when ``return_logits``).
+        """
+        ids = [int(t) for t in ids]
+        if not ids:
+            raise ValueError("empty prompt")
+        if any(not 0 <= t < VOCAB_SIZE for t in ids):
+            raise ValueError("token id outside the vocabulary")
+        n = len(ids)
+        self._check_position(n)
+        dev = self._embed_weight.device
+        start = self._position
+        tokens = _as_i32(ids, dev)
+        positions = torch.arange(start, start + n, dtype=torch.int32, device=dev)
+        seqs = torch.zeros(n, dtype=torch.int32, device=dev)
+        emit = _as_i32([n - 1], dev)
+        out = torch.empty(1, dtype=torch.int32, device=dev)
+        logits = torch.empty(1, VOCAB_SIZE, dtype=torch.float32, device=dev) if return_logits else None
+        self._forward(tokens, seqs, positions, emit, out, logits, self._k_cache, self._v_cache, start + n)
+        self._position += n
+        tok = int(out.item())
+        if tok < 0:
+            raise RuntimeError("prefill produced no token (invalid input)")
+        return (tok, logits[0].clone()) if return_logits else tok
+
     def load_kv(self, k: torch.Tensor, v: torch.Tensor, cache_len: int):
         """Inject cache contents for positions ``[0, cache_len)``; decoding continues at ``cache_len``."""
         if cache_len > self._max_seq_len:
@@ -243,6 +317,138 @@ class Decoder:
         self._k_cache[:, :, :cache_len].copy_(k[: self._num_layers, :, :cache_len])
         self._v_cache[:, :, :cache_len].copy_(v[: self._num_layers, :, :cache_len])
         self._position = cache_len
+
+
+class BatchDecoder:
+    """Greedy decoding of ``batch_size`` independent sequences together.
+
+    Each step is one batched forward (``forward_tokens``) over one token per
+    sequence, so one read of the weights serves the whole batch.  Sequence b
+    keeps its own K/V cache (``[B, L, 8, S, 128]``) and position.  Not in the
+    reference, which decodes one sequence.
+    """
+
+    def __init__(self, weights=None, batch_size: int = 4, tokenizer=None, model_name: str = "Qwen/Qwen3-0.6B",
+                 verbose: bool = True, max_seq_len: int = MAX_SEQ_LEN, num_layers: int = NUM_LAYERS):
+        self._ops = _ops()
+        if weights is None:
+            weights, tokenizer = load_weights(model_name, verbose=verbose, max_seq_len=max_seq_len)
+        weights = _w.to_device(weights, "cuda")
+        if not 1 <= num_layers <= NUM_LAYERS or len(weights["layer_weights"]) < 11 * num_layers:
+            raise ValueError(f"num_layers={num_layers} does not match the weights")
+        if weights["cos_table"].shape[0] < max_seq_len:
+            raise ValueError("RoPE tables are shorter than max_seq_len")
+        if not 1 <= batch_size <= 256:
+            raise ValueError("batch_size must be in [1, 256]")
+        self.tokenizer = tokenizer
+        self.batch_size = batch_size
+        self._weights = weights
+        self._num_layers = num_layers
+        self._max_seq_len = max_seq_len
+        self._forward = _Forward(self._ops, weights, num_layers)
+        dev = weights["embed_weight"].device
+        self._dev = dev
+        self._k_cache = torch.zeros(batch_size, num_layers, NUM_KV_HEADS, max_seq_len, HEAD_DIM,
+                                    dtype=torch.bfloat16, device=dev)
+        self._v_cache = torch.zeros_like(self._k_cache)
+        self._positions = [0] * batch_size
+        self._all = torch.arange(batch_size, dtype=torch.int32, device=dev)
+
+    @property
+    def positions(self) -> list[int]:
+        return list(self._positions)
+
+    def reset(self):
+        self._positions = [0] * self.batch_size
+        self._k_cache.zero_()
+        self._v_cache.zero_()
+
+    def _check(self, seq: int, n: int):
+        if not 0 <= seq < self.batch_size:
+            raise ValueError(f"sequence {seq} outside [0, {self.batch_size})")
+        if self._positions[seq] + n > self._max_seq_len:
+            raise ValueError(f"sequence {seq}: position {self._positions[seq]} + {n} exceeds max_seq_len")
+
+    def load_kv(self, seq: int, k: torch.Tensor, v: torch.Tensor, cache_len: int):
+        """Inject ``[L, 8, >=cache_len, 128]`` cache contents into sequence ``seq``; it continues at ``cache_len``."""
+        self._check(seq, 0)
+        if cache_len > self._max_seq_len:
+            raise ValueError("cache_len exceeds max_seq_len")
+        self._k_cache[seq, :, :, :cache_len].copy_(k[: self._num_layers, :, :cache_len])
+        self._v_cache[seq, :, :, :cache_len].copy_(v[: self._num_layers, :, :cache_len])
+        self._positions[seq] = cache_len
+
+    def prefill(self, seq: int, ids, return_logits: bool = False):
+        """Append ``ids`` to sequence ``seq`` in one forward; returns the next greedy token."""
+        ids = [int(t) for t in ids]
+        if not ids or any(not 0 <= t < VOCAB_SIZE for t in ids):
+            raise ValueError("empty prompt or token id outside the vocabulary")
+        n = len(ids)
+        self._check(seq, n)
+        start = self._positions[seq]
+        tokens = _as_i32(ids, self._dev)
+        positions = torch.arange(start, start + n, dtype=torch.int32, device=self._dev)
+        seqs = torch.full((n,), seq, dtype=torch.int32, device=self._dev)
+        out = torch.empty(1, dtype=torch.int32, device=self._dev)
+        logits = torch.empty(1, VOCAB_SIZE, dtype=torch.float32, device=self._dev) if return_logits else None
+        self._forward(tokens, seqs, positions, _as_i32([n - 1], self._dev), out, logits, self._k_cache,
+                      self._v_cache, start + n)
+        self._positions[seq] += n
+        tok = int(out.item())
+        if tok < 0:
+            raise RuntimeError("prefill produced no token (invalid input)")
+        return (tok, logits[0].clone()) if return_logits else tok
+
+    def step_logits(self, tokens):
+        """One token per sequence at its current position; returns (next tokens, fp32 logits [B, V])."""
+        tokens = [int(t) for t in tokens]
+        if len(tokens) != self.batch_size:
+            raise ValueError(f"expected {self.batch_size} tokens")
+        for b in range(self.batch_size):
+            self._check(b, 1)
+        out = torch.empty(self.batch_size, dtype=torch.int32, device=self._dev)
+        logits = torch.empty(self.batch_size, VOCAB_SIZE, dtype=torch.float32, device=self._dev)
+        self._forward(_as_i32(tokens, self._dev), self._all, _as_i32(self._positions, self._dev), self._all, out,
+                      logits, self._k_cache, self._v_cache, max(self._positions) + 1)
+        self._positions = [p + 1 for p in self._positions]
+        res = out.cpu().tolist()
+        if any(t < 0 for t in res):
+            raise RuntimeError("batched step produced no token (invalid input)")
+        return res, logits
+
+    def step(self, tokens) -> list[int]:
+        return self.step_logits(tokens)[0]
+
+    def generate_ids(self, prompts, max_tokens: int) -> list[list[int]]:
+        """Greedy continuations (``max_tokens`` each) of one prompt per sequence.
+
+        Each prompt is prefilled, then the batch is stepped with the tokens fed
+        back on the device: no host synchronisation until the end.
+        """
+        if len(prompts) != self.batch_size:
+            raise ValueError(f"expected {self.batch_size} prompts")
+        if max_tokens < 1:
+            return [[] for _ in prompts]
+        self.reset()
+        for b, ids in enumerate(prompts):
+            self._check(b, len(ids) + max_tokens - 1)
+        first = [self.prefill(b, ids) for b, ids in enumerate(prompts)]
+        steps = max_tokens - 1
+        log = torch.empty(max_tokens, self.batch_size, dtype=torch.int32, device=self._dev)
+        log[0] = _as_i32(first, self._dev)
+        if steps:
+            start = torch.tensor(self._positions, dtype=torch.int32, device=self._dev)
+            pos_table = start[None, :] + torch.arange(steps, dtype=torch.int32, device=self._dev)[:, None]
+            max_context = max(self._positions) + steps
+            self._forward.workspace(self.batch_size, self.batch_size, max_context)
+            for i in range(steps):
+                self._forward(log[i], self._all, pos_table[i], self._all, log[i + 1], None, self._k_cache,
+                              self._v_cache, max_context)
+            self._positions = [p + steps for p in self._positions]
+        out = log.t().cpu().tolist()
+        if any(t < 0 for row in out for t in row):
+            raise RuntimeError("batched generation produced an invalid token")
+        return out
 
 
 def generate(prompt, max_tokens: int = 100, verbose: bool = True):

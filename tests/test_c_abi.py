@@ -122,7 +122,8 @@ def test_torch_op_schemas_match_reference():
 def test_package_exports_reference_names():
     import qwen_megakernel_amd as q
 
-    assert set(q.__all__) == {"load_weights", "Decoder", "generate"}
+    # the reference's three names, plus the batched decoder
+    assert set(q.__all__) == {"load_weights", "Decoder", "generate", "BatchDecoder"}
     from qwen_megakernel_amd import model
 
     assert (model.NUM_LAYERS, model.HIDDEN_SIZE, model.INTERMEDIATE_SIZE, model.VOCAB_SIZE) == (28, 1024, 3072, 151936)
@@ -154,3 +155,54 @@ def test_algorithmic_bytes():
     assert s.weight_bytes_per_token() == 28 * layer + lm_head + 2 * s.hidden + 2 * s.hidden == 1_192_101_888
     assert s.kv_bytes_per_position() == 28 * 8 * 128 * 2 * 2 == 114_688
     assert s.bytes_per_token(1024) == 1_192_101_888 + 114_688 * 1025
+
+
+class _LayerTable(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_void_p) for n in (
+        "input_layernorm", "q_proj", "k_proj", "v_proj", "q_norm", "k_norm", "o_proj", "post_attn_layernorm",
+        "gate_proj", "up_proj", "down_proj")]
+
+
+def test_forward_workspace_bytes(lib):
+    """Workspace grows with tokens and (for few tokens) with the context bound; invalid -> 0."""
+    f = lib.qmk_forward_workspace_bytes
+    f.restype = ctypes.c_size_t
+    a = f(0, 4, 4, 512)
+    b = f(0, 4, 4, 4096)
+    c = f(1, 4, 4, 512)
+    d = f(0, 128, 1, 128)
+    assert 0 < a < b and a < c and d > 0
+    assert f(0, 0, 1, 16) == 0 and f(0, 4, 0, 16) == 0 and f(0, 4, 257, 16) == 0 and f(2, 4, 4, 16) == 0
+    # few tokens keep scores of max_context positions per (token, query head): 4 x 16 x 4096 fp32
+    assert b - a >= 4 * 16 * (4096 - 512) * 4
+
+
+def test_forward_tokens_host_validation(lib):
+    """qmk_forward_tokens rejects bad arguments on the host, before any launch."""
+    f = lib.qmk_forward_tokens
+    f.restype = ctypes.c_int
+    table = (_LayerTable * 2)()
+    for t in table:
+        for name, _ in _LayerTable._fields_:
+            setattr(t, name, 4096)
+    ws_bytes = lib.qmk_forward_workspace_bytes
+    ws_bytes.restype = ctypes.c_size_t
+    need = ws_bytes(0, 4, 4, 64)
+    p = V(4096)
+
+    def call(model=0, T=4, R=4, table_ptr=table, num_seqs=4, stride=2 * 8 * 64 * 128, layers=2, max_seq=64,
+             max_ctx=64, ws=need, null_tokens=False):
+        return f(ctypes.c_int(model), ctypes.c_int(T), V(0) if null_tokens else p, p, p, ctypes.c_int(R), p, p,
+                 V(0), p, table_ptr, p, p, p, p, p, p, ctypes.c_int(num_seqs), ctypes.c_longlong(stride),
+                 ctypes.c_int(layers), ctypes.c_int(max_seq), ctypes.c_int(max_ctx), ctypes.c_float(0.088), p,
+                 ctypes.c_size_t(ws), V(0))
+
+    assert call(model=3) == QMK_ERR_ARG
+    assert call(null_tokens=True) == QMK_ERR_ARG
+    assert call(max_ctx=65) == QMK_ERR_ARG            # context bound above the cache
+    assert call(ws=need - 1) == QMK_ERR_ARG           # workspace too small
+    assert call(stride=100) == QMK_ERR_ARG            # sequences would overlap
+    assert call(R=257) == QMK_ERR_ARG
+    assert call(layers=29) == QMK_ERR_ARG
+    table[1].o_proj = None
+    assert call() == QMK_ERR_ARG                      # a null weight pointer in the host table

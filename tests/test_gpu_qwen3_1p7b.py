@@ -74,13 +74,14 @@ def test_qwen3_1p7b_context_512(w17):
 
 
 def test_qwen3_1p7b_generate_matches_steps(w17):
-    """generate_nosync (device-fed) gives the same tokens as step-by-step decode."""
+    """generate_nosync (device-fed) gives the same tokens as step-by-step decode (the prompt fed one
+    step per token in both, so the two runs are the same kernel on the same inputs)."""
     from qwen_megakernel_amd.shapes import QWEN3_1_7B
     from qwen_megakernel_amd.weights import make_prompt
 
     _, wg = w17
     prompt = make_prompt(6, QWEN3_1_7B.vocab, seed=4)
-    a = _decoder(wg, max_seq_len=256)
+    a = _decoder(wg, max_seq_len=256, use_prefill=False)
     toks_a = a.generate(prompt, 24)
     b = _decoder(wg, max_seq_len=256)
     t = None
