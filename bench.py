@@ -2,7 +2,7 @@
 """Decode throughput of the gfx950 Qwen3-0.6B megakernel (one JSON line on stdout).
 
 Workload: Qwen3-0.6B architecture, seeded synthetic bf16 weights, a 128-token
-random prompt prefilled into the KV cache one decode step at a time, then K
+random prompt prefilled into the KV cache (batched forward, untimed), then K
 greedy batch-1 decode steps with device-side token feedback (the reference's
 ``generate_nosync`` path).  A "step" is one decode token = one kernel launch.
 W warm-up steps run first on a separate pass (then the cache is reset and the
@@ -22,8 +22,13 @@ cache prefilled to 8192 and to 32768 positions with seeded N(0, 1) bf16 K/V
 in tok/s and algorithmic GB/s (weights + KV read + KV written per token).
 
 ``qwen3_1p7b`` (skip with ``--no-1p7b``): the Qwen3-1.7B shape (hidden 2048,
-MLP 6144, seeded N(0, 0.02) weights) on the same kernel: a 512-token prompt
-prefilled, then 256 device-fed greedy steps at batch 1 (context 513..768).
+MLP 6144, seeded N(0, 0.02) weights): a 512-token prompt prefilled, then 256
+device-fed greedy steps at batch 1 on the decode megakernel (context
+513..768); and ``batch4``: four sequences with their own 512-token prompts,
+256 device-fed steps of the batched forward (MFMA GEMMs), in tok/s over all
+four and algorithmic GB/s per step (weights once + each sequence's KV).
+
+``prefill``: the 128-token prompt through the batched forward, ms and tok/s.
 
 ``phases`` (skip with ``--no-phases``) is the per-phase weight-streaming
 microbenchmark: each GEMV phase of the step (RMSNorm + QKV, O, gate/up +
@@ -138,11 +143,17 @@ def long_context(w, steps: int, contexts=(8192, 32768)):
     return out
 
 
-def qwen3_1p7b(steps: int = 256, prompt_len: int = 512):
-    """Qwen3-1.7B: `prompt_len` tokens prefilled one step at a time, then `steps` device-fed steps."""
+def qwen3_1p7b(steps: int = 256, prompt_len: int = 512, batch: int = 4):
+    """Qwen3-1.7B at batch 1 and at batch `batch`.
+
+    Batch 1: a `prompt_len`-token prompt prefilled, then `steps` device-fed steps of the decode
+    megakernel.  Batch `batch`: `batch` sequences, each with its own `prompt_len`-token prompt
+    (seeds 1..batch) prefilled by the batched forward, then `steps` device-fed batched steps
+    (one MFMA forward over `batch` tokens per step; context 513..768 per sequence).
+    """
     import torch
 
-    from qwen_megakernel_amd.model import Decoder
+    from qwen_megakernel_amd.model import BatchDecoder, Decoder
     from qwen_megakernel_amd.shapes import QWEN3_1_7B as S
     from qwen_megakernel_amd.weights import make_prompt, make_weights
 
@@ -151,8 +162,7 @@ def qwen3_1p7b(steps: int = 256, prompt_len: int = 512):
     dec = Decoder(weights=w, verbose=False, max_seq_len=max_seq)
     ops = torch.ops.qwen_megakernel_C
     prompt = make_prompt(prompt_len, S.vocab, seed=1)
-    for t in prompt[:-1]:
-        dec.step(t)
+    dec.prefill(prompt[:-1])
     stream = torch.cuda.current_stream()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -164,12 +174,71 @@ def qwen3_1p7b(steps: int = 256, prompt_len: int = 512):
     t = e0.elapsed_time(e1) / 1e3 / steps
     mean_c = prompt_len + (steps - 1) / 2.0
     byts = S.weight_bytes_per_token() + S.kv_bytes_per_position() * (mean_c + 1)
-    del dec, w
+    del dec
     torch.cuda.empty_cache()
-    log(f"qwen3-1.7b: {1.0 / t:.1f} tok/s, {byts / t / 1e9:.0f} GB/s algorithmic")
-    return {"tok_per_s": round(1.0 / t, 2), "ms_per_token": round(t * 1e3, 4), "batch": 1, "steps": steps,
-            "context": f"{prompt_len}..{prompt_len + steps - 1}", "bytes_per_token": int(byts),
-            "achieved_GBps": round(byts / t / 1e9, 1), "roofline_frac": round(byts / t / 1e9 / PEAK_HBM_GBS, 4)}
+    log(f"qwen3-1.7b batch 1: {1.0 / t:.1f} tok/s, {byts / t / 1e9:.0f} GB/s algorithmic")
+    out = {"tok_per_s": round(1.0 / t, 2), "ms_per_token": round(t * 1e3, 4), "batch": 1, "steps": steps,
+           "context": f"{prompt_len}..{prompt_len + steps - 1}", "bytes_per_token": int(byts),
+           "achieved_GBps": round(byts / t / 1e9, 1), "roofline_frac": round(byts / t / 1e9 / PEAK_HBM_GBS, 4)}
+
+    bd = BatchDecoder(weights=w, batch_size=batch, max_seq_len=max_seq, verbose=False)
+    prompts = [make_prompt(prompt_len, S.vocab, seed=1 + b) for b in range(batch)]
+    torch.cuda.synchronize()
+    tp = time.perf_counter()
+    first = [bd.prefill(b, p) for b, p in enumerate(prompts)]
+    prefill_s = time.perf_counter() - tp
+    first_t = torch.tensor(first, dtype=torch.int32, device="cuda")
+    start_pos = bd.positions
+    bd.decode_steps(first_t, 4)  # warm-up (contexts 513..516), then rewind to the prefilled state
+    bd._positions = list(start_pos)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    log_t = bd.decode_steps(first_t, steps)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    assert int(log_t.min()) >= 0
+    tb = e0.elapsed_time(e1) / 1e3 / steps  # seconds per batched step
+    # per step: the weights once, each sequence's KV read over its context plus its new K/V row
+    byts_b = S.weight_bytes_per_token() + batch * S.kv_bytes_per_position() * (mean_c + 1)
+    del bd, w
+    torch.cuda.empty_cache()
+    log(f"qwen3-1.7b batch {batch}: {batch / tb:.1f} tok/s ({tb * 1e3:.3f} ms/step), "
+        f"{byts_b / tb / 1e9:.0f} GB/s algorithmic; prefill {batch} x {prompt_len} tokens {prefill_s * 1e3:.1f} ms")
+    out["batch4"] = {"tok_per_s": round(batch / tb, 2), "ms_per_step": round(tb * 1e3, 4), "batch": batch,
+                     "steps": steps, "context": f"{prompt_len + 1}..{prompt_len + steps} per sequence",
+                     "bytes_per_step": int(byts_b), "achieved_GBps": round(byts_b / tb / 1e9, 1),
+                     "roofline_frac": round(byts_b / tb / 1e9 / PEAK_HBM_GBS, 4),
+                     "prefill_ms": round(prefill_s * 1e3, 2),
+                     "path": "batched forward: MFMA GEMMs + split-context attention, one launch sequence per step"}
+    return out
+
+
+def prefill_rate(w, prompt_len: int = PROMPT_LEN, iters: int = 10):
+    """Qwen3-0.6B prompt prefill through the batched forward: ms and tokens/s for `prompt_len` tokens."""
+    import torch
+
+    from qwen_megakernel_amd.model import Decoder
+    from qwen_megakernel_amd.shapes import QWEN3_0_6B as S
+    from qwen_megakernel_amd.weights import make_prompt
+
+    dec = Decoder(weights=w, verbose=False, max_seq_len=2048)
+    prompt = make_prompt(prompt_len, S.vocab, seed=1)
+    dec.prefill(prompt)
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for _ in range(iters):
+        dec._position = 0
+        dec.prefill(prompt)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    t = e0.elapsed_time(e1) / 1e3 / iters
+    del dec
+    torch.cuda.empty_cache()
+    log(f"prefill {prompt_len} tokens: {t * 1e3:.3f} ms ({prompt_len / t:.0f} tok/s); one decode step per "
+        f"token would take {prompt_len} launches")
+    return {"prompt_len": prompt_len, "ms": round(t * 1e3, 3), "tok_per_s": round(prompt_len / t, 1)}
 
 
 def main():
@@ -212,8 +281,7 @@ def main():
 
     def prefill():
         dec.reset()
-        for t in prompt[:-1]:
-            dec.step(t)
+        dec.prefill(prompt[:-1])
 
     def run(n):
         return ops.generate_nosync(prompt[-1], n, *dec._scratch(), QWEN3_0_6B.num_layers, dec.position,
@@ -288,6 +356,7 @@ def main():
         log(f"phase trace at context {last + 1}:\n" + trace.format_table(summ))
     del dec  # frees the 128-token run's caches; the weights stay for the long-context runs
     torch.cuda.empty_cache()
+    result["prefill"] = prefill_rate(w)
     if not args.no_long_context:
         result["long_context"] = long_context(w, args.long_steps)
     del w

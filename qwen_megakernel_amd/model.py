@@ -419,6 +419,27 @@ class BatchDecoder:
     def step(self, tokens) -> list[int]:
         return self.step_logits(tokens)[0]
 
+    def decode_steps(self, tokens: torch.Tensor, steps: int) -> torch.Tensor:
+        """``steps`` batched greedy steps from device tokens (one per sequence, at the current positions),
+        each step's outputs fed to the next on the device; no host synchronisation.  Returns the device
+        log ``[steps + 1, B]`` whose row 0 is ``tokens`` and row i the tokens after step i."""
+        if tokens.numel() != self.batch_size:
+            raise ValueError(f"expected {self.batch_size} tokens")
+        for b in range(self.batch_size):
+            self._check(b, steps)
+        log = torch.empty(steps + 1, self.batch_size, dtype=torch.int32, device=self._dev)
+        log[0] = tokens.to(device=self._dev, dtype=torch.int32)
+        if steps:
+            start = torch.tensor(self._positions, dtype=torch.int32, device=self._dev)
+            pos_table = start[None, :] + torch.arange(steps, dtype=torch.int32, device=self._dev)[:, None]
+            max_context = max(self._positions) + steps
+            self._forward.workspace(self.batch_size, self.batch_size, max_context)
+            for i in range(steps):
+                self._forward(log[i], self._all, pos_table[i], self._all, log[i + 1], None, self._k_cache,
+                              self._v_cache, max_context)
+            self._positions = [p + steps for p in self._positions]
+        return log
+
     def generate_ids(self, prompts, max_tokens: int) -> list[list[int]]:
         """Greedy continuations (``max_tokens`` each) of one prompt per sequence.
 
@@ -433,18 +454,7 @@ class BatchDecoder:
         for b, ids in enumerate(prompts):
             self._check(b, len(ids) + max_tokens - 1)
         first = [self.prefill(b, ids) for b, ids in enumerate(prompts)]
-        steps = max_tokens - 1
-        log = torch.empty(max_tokens, self.batch_size, dtype=torch.int32, device=self._dev)
-        log[0] = _as_i32(first, self._dev)
-        if steps:
-            start = torch.tensor(self._positions, dtype=torch.int32, device=self._dev)
-            pos_table = start[None, :] + torch.arange(steps, dtype=torch.int32, device=self._dev)[:, None]
-            max_context = max(self._positions) + steps
-            self._forward.workspace(self.batch_size, self.batch_size, max_context)
-            for i in range(steps):
-                self._forward(log[i], self._all, pos_table[i], self._all, log[i + 1], None, self._k_cache,
-                              self._v_cache, max_context)
-            self._positions = [p + steps for p in self._positions]
+        log = self.decode_steps(_as_i32(first, self._dev), max_tokens - 1)
         out = log.t().cpu().tolist()
         if any(t < 0 for row in out for t in row):
             raise RuntimeError("batched generation produced an invalid token")
