@@ -157,6 +157,28 @@ int qmk_generate_model(
     int *output_log, int num_layers, int start_position, int max_seq_len,
     float attn_scale, hipStream_t stream);
 
+/* qmk_generate_model that stops at a token (the text path's EOS on the
+ * device, no counterpart in the reference, which always runs num_steps,
+ * csrc/kernel.cu:1547-1605): once a step emits eos_token_id (>= 0), the
+ * remaining launches touch no position, cache or exchange and only write
+ * eos_token_id into output_log (HF pads finished sequences with
+ * pad_token_id = eos_token_id).  The number of generated tokens is the index
+ * of the first eos_token_id in output_log plus one (num_steps if absent).
+ * Returns a status code.  Asynchronous. */
+int qmk_generate_eos(
+    int model, int first_token_id, int num_steps, int eos_token_id,
+    const void *embed_weight, const LDGLayerWeights *layer_weights,
+    const void *final_norm_weight, const void *lm_head_weight,
+    const void *cos_table, const void *sin_table, void *k_cache, void *v_cache,
+    void *hidden_buffer, void *g_normalized, int *output_log, int num_layers,
+    int start_position, int max_seq_len, float attn_scale, hipStream_t stream);
+
+/* The generate entry points record 32 persistent launches into a HIP graph
+ * once per stream and argument set and replay it (the remainder is launched
+ * directly); enable = 0 launches every step directly, as the reference's loop
+ * does (csrc/kernel.cu:1584-1600).  Default on.  Returns a status code. */
+int qmk_set_graph_launch(hipStream_t stream, int enable);
+
 /* Status of the last call made on this thread. */
 int qmk_last_status(void);
 const char *qmk_status_string(int status);

@@ -10,6 +10,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <cstring>
 #include <map>
 #include <mutex>
 #include <utility>
@@ -29,6 +30,10 @@ constexpr uint32_t kXWords = Dims<Qwen3_0_6B>::X_WORDS > Dims<Qwen3_1_7B>::X_WOR
 
 thread_local int t_status = QMK_OK;
 
+// generate: persistent launches recorded once into a HIP graph and replayed
+// in groups of this many steps (the rest launched directly)
+constexpr int kGraphSteps = 32;
+
 struct Ctx {
   int device = -1;
   DecodeState* st = nullptr;
@@ -37,6 +42,14 @@ struct Ctx {
   int xcd_local = 0;
   uint32_t timeout = kTimeoutDefault;
   uint64_t* trace = nullptr;
+  // persistent-mode token log (int[kMaxSeqLen]); the kernel always writes here, so the recorded
+  // launch arguments do not depend on the caller's output tensor
+  int* log = nullptr;
+  bool use_graphs = true;
+  hipStream_t cap = nullptr;      // private stream the graph is recorded on
+  hipGraphExec_t graph = nullptr;
+  KArgs graph_args{};
+  int graph_model = -1;
 };
 
 struct DevInfo {
@@ -79,10 +92,12 @@ __global__ void selftest_kernel(const float* in, float* out, int n) {
   out[2 * n + 256 + lane] = b;
 }
 
-__global__ void set_step_kernel(DecodeState* st, int pos, int tok) {
+__global__ void set_step_kernel(DecodeState* st, int pos, int tok, int eos) {
   st->pos = pos;
   st->tok = tok;
   st->step = 0;
+  st->eos = eos;
+  st->done = 0;
 }
 
 int fail(int s) {
@@ -153,6 +168,12 @@ int get_ctx(hipStream_t stream, Ctx** out) {
     return QMK_ERR_HIP;
   }
   *c->host_err = 0;
+  if (hipMalloc(&c->log, (size_t)kMaxSeqLen * sizeof(int)) != hipSuccess) {
+    hipFree(mem);
+    hipHostFree(c->host_err);
+    delete c;
+    return QMK_ERR_HIP;
+  }
   c->st = reinterpret_cast<DecodeState*>(mem);
   c->x = reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(mem) + sizeof(DecodeState));
   g_ctx[key] = c;
@@ -234,13 +255,79 @@ int decode_impl(const Common& c, int token, int position, int* out_token, float*
   a.out_token = out_token;
   a.logits = logits;
   if (persistent) {
-    hipLaunchKernelGGL(set_step_kernel, dim3(1), dim3(1), 0, stream, ctx->st, position, token);
+    hipLaunchKernelGGL(set_step_kernel, dim3(1), dim3(1), 0, stream, ctx->st, position, token, -1);
     a.position = -1;
   } else {
     a.position = position;
     a.token = token;
   }
   return fail(launch(a, c.model, stream));
+}
+
+// The instantiated graph of kGraphSteps persistent launches with arguments
+// `a` (recorded again when the arguments or the model change).
+int graph_for(Ctx* ctx, const KArgs& a, int model, hipGraphExec_t* out) {
+  if (ctx->graph && ctx->graph_model == model && std::memcmp(&ctx->graph_args, &a, sizeof(KArgs)) == 0) {
+    *out = ctx->graph;
+    return QMK_OK;
+  }
+  if (ctx->graph) {
+    hipGraphExecDestroy(ctx->graph);
+    ctx->graph = nullptr;
+  }
+  if (!ctx->cap && hipStreamCreateWithFlags(&ctx->cap, hipStreamNonBlocking) != hipSuccess) return QMK_ERR_HIP;
+  if (hipStreamBeginCapture(ctx->cap, hipStreamCaptureModeThreadLocal) != hipSuccess) return QMK_ERR_HIP;
+  int s = QMK_OK;
+  for (int i = 0; i < kGraphSteps && s == QMK_OK; i++) s = launch(a, model, ctx->cap);
+  hipGraph_t g = nullptr;
+  const hipError_t e = hipStreamEndCapture(ctx->cap, &g);
+  if (s != QMK_OK || e != hipSuccess || !g) {
+    if (g) hipGraphDestroy(g);
+    return QMK_ERR_HIP;
+  }
+  hipGraphExec_t ex = nullptr;
+  const hipError_t ie = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+  hipGraphDestroy(g);
+  if (ie != hipSuccess) return QMK_ERR_HIP;
+  ctx->graph = ex;
+  ctx->graph_args = a;
+  ctx->graph_model = model;
+  *out = ex;
+  return QMK_OK;
+}
+
+// num_steps persistent launches from (start_position, first_token_id); the
+// log is copied into output_log at the end.  eos >= 0: stop token.
+int generate_impl(const Common& c, int first_token_id, int num_steps, int eos, int* output_log, int start_position,
+                  hipStream_t stream) {
+  int s = validate(c);
+  if (s != QMK_OK) return fail(s);
+  if (num_steps < 0 || !output_log) return fail(QMK_ERR_ARG);
+  if (num_steps == 0) return fail(QMK_OK);
+  // every step must stay inside the cache: the last one runs at start+num_steps-1
+  if (start_position < 0 || (long long)start_position + num_steps > (long long)c.max_seq_len)
+    return fail(QMK_ERR_POSITION);
+  if (first_token_id < 0 || first_token_id >= Dm::V || eos >= Dm::V) return fail(QMK_ERR_ARG);
+  Ctx* ctx = nullptr;
+  if ((s = get_ctx(stream, &ctx)) != QMK_OK) return fail(s);
+  if ((s = poisoned(ctx)) != QMK_OK) return fail(s);
+  KArgs a = make_args(c, ctx);
+  a.position = -1;
+  a.out_log = ctx->log;
+  hipLaunchKernelGGL(set_step_kernel, dim3(1), dim3(1), 0, stream, ctx->st, start_position, first_token_id,
+                     eos < 0 ? -1 : eos);
+  int done = 0;
+  hipGraphExec_t g = nullptr;
+  if (ctx->use_graphs && num_steps >= kGraphSteps && graph_for(ctx, a, c.model, &g) == QMK_OK) {
+    for (; done + kGraphSteps <= num_steps; done += kGraphSteps)
+      if (hipGraphLaunch(g, stream) != hipSuccess) return fail(QMK_ERR_HIP);
+  }
+  for (; done < num_steps; done++)
+    if ((s = launch(a, c.model, stream)) != QMK_OK) return fail(s);
+  if (hipMemcpyAsync(output_log, ctx->log, (size_t)num_steps * sizeof(int), hipMemcpyDeviceToDevice, stream) !=
+      hipSuccess)
+    return fail(QMK_ERR_HIP);
+  return fail(QMK_OK);
 }
 
 size_t phase_copy_elems(int phase) {
@@ -321,23 +408,25 @@ int qmk_generate_model(int model, int first_token_id, int num_steps, const void*
                        int max_seq_len, float attn_scale, hipStream_t stream) {
   Common c{model, embed_weight, layer_weights, final_norm_weight, lm_head_weight, cos_table, sin_table, k_cache, v_cache,
            hidden_buffer, g_normalized, num_layers, max_seq_len, attn_scale};
-  int s = validate(c);
-  if (s != QMK_OK) return fail(s);
-  if (num_steps < 0 || !output_log) return fail(QMK_ERR_ARG);
-  if (num_steps == 0) return fail(QMK_OK);
-  // every step must stay inside the cache: the last one runs at start+num_steps-1
-  if (start_position < 0 || (long long)start_position + num_steps > (long long)max_seq_len) return fail(QMK_ERR_POSITION);
-  if (first_token_id < 0 || first_token_id >= Dm::V) return fail(QMK_ERR_ARG);
+  return generate_impl(c, first_token_id, num_steps, -1, output_log, start_position, stream);
+}
+
+int qmk_generate_eos(int model, int first_token_id, int num_steps, int eos_token_id, const void* embed_weight,
+                     const LDGLayerWeights* layer_weights, const void* final_norm_weight, const void* lm_head_weight,
+                     const void* cos_table, const void* sin_table, void* k_cache, void* v_cache, void* hidden_buffer,
+                     void* g_normalized, int* output_log, int num_layers, int start_position, int max_seq_len,
+                     float attn_scale, hipStream_t stream) {
+  if (eos_token_id < 0) return fail(QMK_ERR_ARG);
+  Common c{model, embed_weight, layer_weights, final_norm_weight, lm_head_weight, cos_table, sin_table, k_cache, v_cache,
+           hidden_buffer, g_normalized, num_layers, max_seq_len, attn_scale};
+  return generate_impl(c, first_token_id, num_steps, eos_token_id, output_log, start_position, stream);
+}
+
+int qmk_set_graph_launch(hipStream_t stream, int enable) {
   Ctx* ctx = nullptr;
-  if ((s = get_ctx(stream, &ctx)) != QMK_OK) return fail(s);
-  if ((s = poisoned(ctx)) != QMK_OK) return fail(s);
-  KArgs a = make_args(c, ctx);
-  a.position = -1;
-  a.out_log = output_log;
-  hipLaunchKernelGGL(set_step_kernel, dim3(1), dim3(1), 0, stream, ctx->st, start_position, first_token_id);
-  for (int i = 0; i < num_steps; i++) {
-    if ((s = launch(a, c.model, stream)) != QMK_OK) return fail(s);
-  }
+  const int s = get_ctx(stream, &ctx);
+  if (s != QMK_OK) return fail(s);
+  ctx->use_graphs = enable != 0;
   return fail(QMK_OK);
 }
 

@@ -212,6 +212,7 @@ struct Smem {
   uint64_t best[kComputeWaves];
   LayerPtrs layers[kMaxLayers];      // copy of the packed pointer table, read once per launch
   int abort_flag;
+  int stop_flag;                     // persistent mode: the stop token was emitted by an earlier launch
 };
 
 struct Step {
@@ -804,6 +805,7 @@ __device__ __forceinline__ void control_path(const KArgs& a, Smem<M>& s, const S
           st->tok = token;
           st->pos = p.pos + 1;
           st->step = p.step + 1;
+          if (token == st->eos) st->done = 1;
         }
         st->epoch = p.epoch + (uint32_t)(p.nl * Dm::NX + 1);
       }
@@ -1175,9 +1177,22 @@ __global__ void __launch_bounds__(kBlock, 1) decode_kernel(KArgs a) {
     s.abort_flag = __hip_atomic_load(&st->err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
     // A step that fails on the device leaves -1 here, never a stale token.
     if (b == 0 && a.out_token) *a.out_token = -1;
+    // `done` is written only by workgroup 0 at the end of a launch, after every workgroup of that
+    // launch has read it, so all workgroups of one launch see the same value.
+    s.stop_flag = (a.position < 0 && st->done != 0) ? 1 : 0;
   }
   __syncthreads();
   if (s.abort_flag) return;
+  if (s.stop_flag) {
+    // after the stop token: no position, cache or exchange is touched; the log gets the stop token
+    // (HF pads finished sequences with pad_token_id = eos_token_id)
+    if (b == 0 && threadIdx.x == 0) {
+      const int step = st->step;
+      if (a.out_log) a.out_log[step] = st->eos;
+      st->step = step + 1;
+    }
+    return;
+  }
   Step p;
   p.epoch = st->epoch;
   p.persistent = a.position < 0;

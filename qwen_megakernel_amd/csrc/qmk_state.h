@@ -8,7 +8,8 @@ namespace qmk {
 struct DecodeState {
   uint32_t epoch;  // exchange-tag base; advanced by every completed launch
   uint32_t err;    // error bits (0 = healthy); a non-zero value makes launches no-ops
-  uint32_t pad0[2];
+  int32_t eos;     // persistent mode: stop token (-1: none)
+  uint32_t done;   // persistent mode: `eos` was emitted; later launches only pad the log with it
   int32_t pos;     // persistent mode: position, input token and step of the next launch
   int32_t tok;
   int32_t step;

@@ -11,7 +11,8 @@
 // `device_error`, `reset`, `set_wait_limit`, `set_trace` (phase trace),
 // `phase_bench` (per-phase weight-streaming microbenchmark), and the batched
 // forward `forward_tokens` (prefill, batched decode) with
-// `forward_workspace_bytes` and `selftest_mfma`.
+// `forward_workspace_bytes` and `selftest_mfma`, `generate_eos` (stop token on
+// the device) and `set_graph_launch`.
 
 #include <Python.h>
 #include <ATen/hip/impl/HIPGuardImplMasqueradingAsCUDA.h>
@@ -198,6 +199,43 @@ torch::Tensor generate_nosync(int64_t first_token_id, int64_t num_steps, torch::
   TORCH_CHECK(err == 0, "generate_nosync: device error bits 0x", std::hex, err,
               " (a bounded wait expired or a position left the cache); call reset()");
   return output_log;
+}
+
+// generate_nosync that stops at eos_token_id on the device (qmk_generate_eos):
+// the returned log holds the generated tokens, then eos_token_id padding.
+torch::Tensor generate_eos(int64_t first_token_id, int64_t num_steps, int64_t eos_token_id,
+                           torch::Tensor embed_weight, torch::Tensor layer_weights_packed,
+                           torch::Tensor final_norm_weight, torch::Tensor lm_head_weight, torch::Tensor cos_table,
+                           torch::Tensor sin_table, torch::Tensor k_cache, torch::Tensor v_cache,
+                           torch::Tensor hidden_buffer, torch::Tensor normalized, int64_t num_layers,
+                           int64_t start_position, int64_t max_seq_len, double attn_scale) {
+  const Checked c = check_common(embed_weight, layer_weights_packed, final_norm_weight, lm_head_weight, cos_table,
+                                 sin_table, k_cache, v_cache, hidden_buffer, normalized, num_layers, max_seq_len,
+                                 attn_scale);
+  TORCH_CHECK(num_steps >= 0, "num_steps must be non-negative");
+  TORCH_CHECK(start_position >= 0 && start_position + num_steps <= max_seq_len, "steps [", start_position, ", ",
+              start_position + num_steps, ") do not fit in max_seq_len ", max_seq_len);
+  TORCH_CHECK(first_token_id >= 0 && first_token_id < kVocab, "first_token_id outside the vocabulary");
+  TORCH_CHECK(eos_token_id >= 0 && eos_token_id < kVocab, "eos_token_id outside the vocabulary");
+  const c10::hip::HIPGuardMasqueradingAsCUDA guard(embed_weight.device());
+  auto stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA().stream();
+  auto output_log = torch::empty({num_steps}, torch::dtype(torch::kInt32).device(embed_weight.device()));
+  if (num_steps == 0) return output_log;
+  qmk_generate_eos(c.model, (int)first_token_id, (int)num_steps, (int)eos_token_id, embed_weight.data_ptr(),
+                   reinterpret_cast<const LDGLayerWeights*>(layer_weights_packed.data_ptr()),
+                   final_norm_weight.data_ptr(), lm_head_weight.data_ptr(), cos_table.data_ptr(), sin_table.data_ptr(),
+                   k_cache.data_ptr(), v_cache.data_ptr(), hidden_buffer.data_ptr(), normalized.data_ptr(),
+                   static_cast<int*>(output_log.data_ptr()), c.num_layers, (int)start_position, c.max_seq_len,
+                   (float)attn_scale, stream);
+  raise_status("generate_eos");
+  const uint32_t err = qmk_device_error(stream);
+  TORCH_CHECK(err == 0, "generate_eos: device error bits 0x", std::hex, err, "; call reset()");
+  return output_log;
+}
+
+void set_graph_launch(bool enable) {
+  const int s = qmk_set_graph_launch(c10::hip::getCurrentHIPStreamMasqueradingAsCUDA().stream(), enable ? 1 : 0);
+  TORCH_CHECK(s == QMK_OK, "set_graph_launch failed: ", qmk_status_string(s));
 }
 
 void decode_logits(torch::Tensor output_token, torch::Tensor logits, int64_t input_token_id,
@@ -430,6 +468,15 @@ TORCH_LIBRARY(qwen_megakernel_C, ops) {
       "int num_layers, int position, int max_seq_len, float attn_scale) -> ()");
   ops.impl("decode_logits", torch::kCUDA, &decode_logits);
 
+  ops.def(
+      "generate_eos(int first_token_id, int num_steps, int eos_token_id, "
+      "Tensor embed_weight, Tensor layer_weights_packed, "
+      "Tensor final_norm_weight, Tensor lm_head_weight, "
+      "Tensor cos_table, Tensor sin_table, Tensor k_cache, Tensor v_cache, "
+      "Tensor hidden_buffer, Tensor normalized, "
+      "int num_layers, int start_position, int max_seq_len, float attn_scale) -> Tensor");
+  ops.impl("generate_eos", torch::kCUDA, &generate_eos);
+  ops.def("set_graph_launch(bool enable) -> ()", &set_graph_launch);
   ops.def("device_error() -> int", &device_error);
   ops.def("reset() -> ()", &reset);
   ops.def("set_wait_limit(int ticks) -> ()", &set_wait_limit);

@@ -242,18 +242,23 @@ class Decoder:
             ids = self.tokenizer.encode(prompt, add_special_tokens=True)
         else:
             ids = [int(t) for t in prompt]
-        out = self.generate_ids(ids, max_tokens)
         if not isinstance(prompt, str):
-            return out
+            return self.generate_ids(ids, max_tokens)
         eos = self.tokenizer.eos_token_id
+        out = self.generate_ids(ids, max_tokens, eos_token_id=eos)
         if eos in out:
             out = out[: out.index(eos)]
         return self.tokenizer.decode(out, skip_special_tokens=True)
 
     # -- additions --------------------------------------------------------
 
-    def generate_ids(self, ids: list[int], max_tokens: int) -> list[int]:
-        """Step ``ids[:-1]``, then ``max_tokens`` device-fed greedy steps from ``ids[-1]``."""
+    def generate_ids(self, ids: list[int], max_tokens: int, eos_token_id: int | None = None) -> list[int]:
+        """Step ``ids[:-1]``, then ``max_tokens`` device-fed greedy steps from ``ids[-1]``.
+
+        With ``eos_token_id`` the device stops after emitting it: the rest of the
+        returned list is ``eos_token_id`` padding and the position advances only by
+        the tokens actually generated.
+        """
         if not ids:
             raise ValueError("empty prompt")
         if self.use_prefill and len(ids) > 1:
@@ -262,10 +267,19 @@ class Decoder:
             for tid in ids[:-1]:
                 self.step(tid)
         self._check_position(max_tokens)
-        out = self._ops.generate_nosync(int(ids[-1]), int(max_tokens), *self._scratch(), self._num_layers,
-                                        self._position, self._max_seq_len, self._attn_scale)
-        self._position += max_tokens
-        return out.cpu().tolist()
+        if eos_token_id is None:
+            out = self._ops.generate_nosync(int(ids[-1]), int(max_tokens), *self._scratch(), self._num_layers,
+                                            self._position, self._max_seq_len, self._attn_scale)
+            self._position += max_tokens
+            return out.cpu().tolist()
+        out = self._ops.generate_eos(int(ids[-1]), int(max_tokens), int(eos_token_id), self._embed_weight,
+                                     self._layer_weights_packed, self._final_norm_weight, self._lm_head_weight,
+                                     self._cos_table, self._sin_table, self._k_cache, self._v_cache, self._hidden,
+                                     self._norm_out, self._num_layers, self._position, self._max_seq_len,
+                                     self._attn_scale).cpu().tolist()
+        eos = int(eos_token_id)
+        self._position += out.index(eos) + 1 if eos in out else max_tokens
+        return out
 
     def step_logits(self, token_id: int):
         """Decode one token; returns ``(next_token, logits)`` with fp32 logits (bf16 values)."""

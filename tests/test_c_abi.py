@@ -206,3 +206,18 @@ def test_forward_tokens_host_validation(lib):
     assert call(layers=29) == QMK_ERR_ARG
     table[1].o_proj = None
     assert call() == QMK_ERR_ARG                      # a null weight pointer in the host table
+
+
+def test_generate_eos_validation(lib):
+    """qmk_generate_eos rejects a negative stop token and out-of-range steps before any launch."""
+    f = lib.qmk_generate_eos
+    f.restype = ctypes.c_int
+    p = V(4096)
+
+    def call(eos=5, steps=10, start=0, max_seq=64):
+        return f(ctypes.c_int(0), ctypes.c_int(1), ctypes.c_int(steps), ctypes.c_int(eos), p, p, p, p, p, p, p, p,
+                 p, p, p, ctypes.c_int(28), ctypes.c_int(start), ctypes.c_int(max_seq), ctypes.c_float(0.088), V(0))
+
+    assert call(eos=-1) == QMK_ERR_ARG
+    assert call(eos=151936) == QMK_ERR_ARG
+    assert call(start=60, steps=10) == QMK_ERR_POSITION
