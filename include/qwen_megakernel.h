@@ -173,6 +173,38 @@ int qmk_generate_eos(
     void *hidden_buffer, void *g_normalized, int *output_log, int num_layers,
     int start_position, int max_seq_len, float attn_scale, hipStream_t stream);
 
+/* ---- sampling (no counterpart in the reference, which is greedy only,
+ * csrc/kernel.cu:1020-1183) ----
+ * HF's warpers in HF's order: scores s = logit / temperature; top-k keeps
+ * s >= the top_k-th largest s (ties kept); top-p keeps a token when the
+ * probability mass of the kept scores strictly above it is < top_p (HF removes
+ * sorted tokens whose ascending cumulative probability is <= 1 - top_p; the
+ * top token always stays); then one draw from the softmax of the kept scores
+ * by the Gumbel-max method, argmax of s + G, G = -log(-log(U)), U from the
+ * SplitMix64 hash of (seed, counter, token id).  temperature <= 0 is greedy
+ * (first index of the maximum); top_k <= 0 or >= vocab and top_p outside
+ * (0, 1) switch those filters off.  Same (seed, counter, logits) -> same token.
+ */
+
+/* One token per row of logits (float[rows][vocab], device) into out_tokens
+ * (int[rows], device); counters (int64[rows], device) give each row its own
+ * random numbers.  Asynchronous; returns a status code. */
+int qmk_sample_rows(const float *logits, int rows, int vocab, float temperature,
+                    int top_k, float top_p, unsigned long long seed,
+                    const long long *counters, int *out_tokens, hipStream_t stream);
+
+/* qmk_generate_eos with sampling: every step's greedy token is replaced by a
+ * draw from its logits (counter = the step's position) before it is fed to the
+ * next step.  eos_token_id < 0: no stop token.  Returns a status code. */
+int qmk_generate_sample(
+    int model, int first_token_id, int num_steps, int eos_token_id,
+    float temperature, int top_k, float top_p, unsigned long long seed,
+    const void *embed_weight, const LDGLayerWeights *layer_weights,
+    const void *final_norm_weight, const void *lm_head_weight,
+    const void *cos_table, const void *sin_table, void *k_cache, void *v_cache,
+    void *hidden_buffer, void *g_normalized, int *output_log, int num_layers,
+    int start_position, int max_seq_len, float attn_scale, hipStream_t stream);
+
 /* The generate entry points record 32 persistent launches into a HIP graph
  * once per stream and argument set and replay it (the remainder is launched
  * directly); enable = 0 launches every step directly, as the reference's loop

@@ -18,6 +18,7 @@
 #include "../../include/qwen_megakernel.h"
 #include "qmk_decode_kernel.h"
 #include "qmk_phase_bench.h"
+#include "qmk_sample.h"
 
 namespace qmk {
 namespace {
@@ -50,6 +51,9 @@ struct Ctx {
   hipGraphExec_t graph = nullptr;
   KArgs graph_args{};
   int graph_model = -1;
+  bool graph_sampled = false;
+  SampleParams graph_sp{};
+  float* logits = nullptr;        // sampled generate: the step's logits (float[vocab])
 };
 
 struct DevInfo {
@@ -98,6 +102,7 @@ __global__ void set_step_kernel(DecodeState* st, int pos, int tok, int eos) {
   st->step = 0;
   st->eos = eos;
   st->done = 0;
+  st->ran = 0;
 }
 
 int fail(int s) {
@@ -264,10 +269,20 @@ int decode_impl(const Common& c, int token, int position, int* out_token, float*
   return fail(launch(a, c.model, stream));
 }
 
-// The instantiated graph of kGraphSteps persistent launches with arguments
-// `a` (recorded again when the arguments or the model change).
-int graph_for(Ctx* ctx, const KArgs& a, int model, hipGraphExec_t* out) {
-  if (ctx->graph && ctx->graph_model == model && std::memcmp(&ctx->graph_args, &a, sizeof(KArgs)) == 0) {
+// One step of the generate loop: the decode launch, and with sampling the
+// sampler that replaces its greedy token.
+int launch_step(const KArgs& a, int model, const SampleParams* sp, hipStream_t stream) {
+  int s = launch(a, model, stream);
+  if (s == QMK_OK && sp) s = launch_sample_state(a.logits, Dims<Qwen3_0_6B>::V, *sp, a.st, a.out_log, stream);
+  return s;
+}
+
+// The instantiated graph of kGraphSteps steps with arguments `a` (and `sp`),
+// recorded again when the arguments, the model or the sampling change.
+int graph_for(Ctx* ctx, const KArgs& a, int model, const SampleParams* sp, hipGraphExec_t* out) {
+  const bool sampled = sp != nullptr;
+  if (ctx->graph && ctx->graph_model == model && std::memcmp(&ctx->graph_args, &a, sizeof(KArgs)) == 0 &&
+      ctx->graph_sampled == sampled && (!sampled || std::memcmp(&ctx->graph_sp, sp, sizeof(SampleParams)) == 0)) {
     *out = ctx->graph;
     return QMK_OK;
   }
@@ -278,7 +293,7 @@ int graph_for(Ctx* ctx, const KArgs& a, int model, hipGraphExec_t* out) {
   if (!ctx->cap && hipStreamCreateWithFlags(&ctx->cap, hipStreamNonBlocking) != hipSuccess) return QMK_ERR_HIP;
   if (hipStreamBeginCapture(ctx->cap, hipStreamCaptureModeThreadLocal) != hipSuccess) return QMK_ERR_HIP;
   int s = QMK_OK;
-  for (int i = 0; i < kGraphSteps && s == QMK_OK; i++) s = launch(a, model, ctx->cap);
+  for (int i = 0; i < kGraphSteps && s == QMK_OK; i++) s = launch_step(a, model, sp, ctx->cap);
   hipGraph_t g = nullptr;
   const hipError_t e = hipStreamEndCapture(ctx->cap, &g);
   if (s != QMK_OK || e != hipSuccess || !g) {
@@ -292,6 +307,8 @@ int graph_for(Ctx* ctx, const KArgs& a, int model, hipGraphExec_t* out) {
   ctx->graph = ex;
   ctx->graph_args = a;
   ctx->graph_model = model;
+  ctx->graph_sampled = sampled;
+  if (sampled) ctx->graph_sp = *sp;
   *out = ex;
   return QMK_OK;
 }
@@ -299,7 +316,7 @@ int graph_for(Ctx* ctx, const KArgs& a, int model, hipGraphExec_t* out) {
 // num_steps persistent launches from (start_position, first_token_id); the
 // log is copied into output_log at the end.  eos >= 0: stop token.
 int generate_impl(const Common& c, int first_token_id, int num_steps, int eos, int* output_log, int start_position,
-                  hipStream_t stream) {
+                  hipStream_t stream, const SampleParams* sp = nullptr) {
   int s = validate(c);
   if (s != QMK_OK) return fail(s);
   if (num_steps < 0 || !output_log) return fail(QMK_ERR_ARG);
@@ -314,16 +331,20 @@ int generate_impl(const Common& c, int first_token_id, int num_steps, int eos, i
   KArgs a = make_args(c, ctx);
   a.position = -1;
   a.out_log = ctx->log;
+  if (sp) {
+    if (!ctx->logits && hipMalloc(&ctx->logits, (size_t)Dm::V * sizeof(float)) != hipSuccess) return fail(QMK_ERR_HIP);
+    a.logits = ctx->logits;
+  }
   hipLaunchKernelGGL(set_step_kernel, dim3(1), dim3(1), 0, stream, ctx->st, start_position, first_token_id,
                      eos < 0 ? -1 : eos);
   int done = 0;
   hipGraphExec_t g = nullptr;
-  if (ctx->use_graphs && num_steps >= kGraphSteps && graph_for(ctx, a, c.model, &g) == QMK_OK) {
+  if (ctx->use_graphs && num_steps >= kGraphSteps && graph_for(ctx, a, c.model, sp, &g) == QMK_OK) {
     for (; done + kGraphSteps <= num_steps; done += kGraphSteps)
       if (hipGraphLaunch(g, stream) != hipSuccess) return fail(QMK_ERR_HIP);
   }
   for (; done < num_steps; done++)
-    if ((s = launch(a, c.model, stream)) != QMK_OK) return fail(s);
+    if ((s = launch_step(a, c.model, sp, stream)) != QMK_OK) return fail(s);
   if (hipMemcpyAsync(output_log, ctx->log, (size_t)num_steps * sizeof(int), hipMemcpyDeviceToDevice, stream) !=
       hipSuccess)
     return fail(QMK_ERR_HIP);
@@ -420,6 +441,20 @@ int qmk_generate_eos(int model, int first_token_id, int num_steps, int eos_token
   Common c{model, embed_weight, layer_weights, final_norm_weight, lm_head_weight, cos_table, sin_table, k_cache, v_cache,
            hidden_buffer, g_normalized, num_layers, max_seq_len, attn_scale};
   return generate_impl(c, first_token_id, num_steps, eos_token_id, output_log, start_position, stream);
+}
+
+int qmk_generate_sample(int model, int first_token_id, int num_steps, int eos_token_id, float temperature, int top_k,
+                        float top_p, unsigned long long seed, const void* embed_weight,
+                        const LDGLayerWeights* layer_weights, const void* final_norm_weight,
+                        const void* lm_head_weight, const void* cos_table, const void* sin_table, void* k_cache,
+                        void* v_cache, void* hidden_buffer, void* g_normalized, int* output_log, int num_layers,
+                        int start_position, int max_seq_len, float attn_scale, hipStream_t stream) {
+  if (!(temperature == temperature) || !(top_p == top_p)) return fail(QMK_ERR_ARG);
+  Common c{model, embed_weight, layer_weights, final_norm_weight, lm_head_weight, cos_table, sin_table, k_cache, v_cache,
+           hidden_buffer, g_normalized, num_layers, max_seq_len, attn_scale};
+  const SampleParams sp{temperature, top_k, top_p, (uint64_t)seed};
+  return generate_impl(c, first_token_id, num_steps, eos_token_id < 0 ? -1 : eos_token_id, output_log,
+                       start_position, stream, &sp);
 }
 
 int qmk_set_graph_launch(hipStream_t stream, int enable) {

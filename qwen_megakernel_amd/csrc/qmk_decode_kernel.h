@@ -805,6 +805,7 @@ __device__ __forceinline__ void control_path(const KArgs& a, Smem<M>& s, const S
           st->tok = token;
           st->pos = p.pos + 1;
           st->step = p.step + 1;
+          st->ran = 1;
           if (token == st->eos) st->done = 1;
         }
         st->epoch = p.epoch + (uint32_t)(p.nl * Dm::NX + 1);
@@ -1190,6 +1191,7 @@ __global__ void __launch_bounds__(kBlock, 1) decode_kernel(KArgs a) {
       const int step = st->step;
       if (a.out_log) a.out_log[step] = st->eos;
       st->step = step + 1;
+      st->ran = 0;
     }
     return;
   }

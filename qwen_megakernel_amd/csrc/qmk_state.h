@@ -13,7 +13,7 @@ struct DecodeState {
   int32_t pos;     // persistent mode: position, input token and step of the next launch
   int32_t tok;
   int32_t step;
-  int32_t pad1;
+  int32_t ran;     // persistent mode: 1 if the last launch decoded a token, 0 if it only padded the log
   uint32_t reserved[56];  // header is 256 bytes; exchange words follow
 };
 static_assert(sizeof(DecodeState) == 256, "state header size");

@@ -12,7 +12,8 @@
 // `phase_bench` (per-phase weight-streaming microbenchmark), and the batched
 // forward `forward_tokens` (prefill, batched decode) with
 // `forward_workspace_bytes` and `selftest_mfma`, `generate_eos` (stop token on
-// the device) and `set_graph_launch`.
+// the device), `set_graph_launch`, and sampling: `sample` over logits rows and
+// the sampled loop `generate_sample`.
 
 #include <Python.h>
 #include <ATen/hip/impl/HIPGuardImplMasqueradingAsCUDA.h>
@@ -231,6 +232,65 @@ torch::Tensor generate_eos(int64_t first_token_id, int64_t num_steps, int64_t eo
   const uint32_t err = qmk_device_error(stream);
   TORCH_CHECK(err == 0, "generate_eos: device error bits 0x", std::hex, err, "; call reset()");
   return output_log;
+}
+
+// Sampled generate loop (qmk_generate_sample); eos_token_id < 0: none.
+torch::Tensor generate_sample(int64_t first_token_id, int64_t num_steps, int64_t eos_token_id, double temperature,
+                              int64_t top_k, double top_p, int64_t seed, torch::Tensor embed_weight,
+                              torch::Tensor layer_weights_packed, torch::Tensor final_norm_weight,
+                              torch::Tensor lm_head_weight, torch::Tensor cos_table, torch::Tensor sin_table,
+                              torch::Tensor k_cache, torch::Tensor v_cache, torch::Tensor hidden_buffer,
+                              torch::Tensor normalized, int64_t num_layers, int64_t start_position,
+                              int64_t max_seq_len, double attn_scale) {
+  const Checked c = check_common(embed_weight, layer_weights_packed, final_norm_weight, lm_head_weight, cos_table,
+                                 sin_table, k_cache, v_cache, hidden_buffer, normalized, num_layers, max_seq_len,
+                                 attn_scale);
+  TORCH_CHECK(num_steps >= 0, "num_steps must be non-negative");
+  TORCH_CHECK(start_position >= 0 && start_position + num_steps <= max_seq_len, "steps [", start_position, ", ",
+              start_position + num_steps, ") do not fit in max_seq_len ", max_seq_len);
+  TORCH_CHECK(first_token_id >= 0 && first_token_id < kVocab, "first_token_id outside the vocabulary");
+  TORCH_CHECK(eos_token_id < kVocab, "eos_token_id outside the vocabulary");
+  TORCH_CHECK(temperature == temperature && top_p == top_p, "temperature and top_p must not be NaN");
+  const c10::hip::HIPGuardMasqueradingAsCUDA guard(embed_weight.device());
+  auto stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA().stream();
+  auto output_log = torch::empty({num_steps}, torch::dtype(torch::kInt32).device(embed_weight.device()));
+  if (num_steps == 0) return output_log;
+  qmk_generate_sample(c.model, (int)first_token_id, (int)num_steps, (int)eos_token_id, (float)temperature, (int)top_k,
+                      (float)top_p, (unsigned long long)seed, embed_weight.data_ptr(),
+                      reinterpret_cast<const LDGLayerWeights*>(layer_weights_packed.data_ptr()),
+                      final_norm_weight.data_ptr(), lm_head_weight.data_ptr(), cos_table.data_ptr(),
+                      sin_table.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), hidden_buffer.data_ptr(),
+                      normalized.data_ptr(), static_cast<int*>(output_log.data_ptr()), c.num_layers,
+                      (int)start_position, c.max_seq_len, (float)attn_scale, stream);
+  raise_status("generate_sample");
+  const uint32_t err = qmk_device_error(stream);
+  TORCH_CHECK(err == 0, "generate_sample: device error bits 0x", std::hex, err, "; call reset()");
+  return output_log;
+}
+
+// One sampled token per row of fp32 logits (qmk_sample_rows).
+void sample(torch::Tensor logits, double temperature, int64_t top_k, double top_p, int64_t seed,
+            torch::Tensor counters, torch::Tensor out_tokens) {
+  check_cuda(logits, "logits");
+  TORCH_CHECK(logits.scalar_type() == torch::kFloat32 && logits.dim() == 2 && logits.size(0) >= 1 &&
+                  logits.size(0) <= 65535 && logits.size(1) >= 1,
+              "logits must be float32 [rows, vocab]");
+  check_cuda(counters, "counters");
+  TORCH_CHECK(counters.scalar_type() == torch::kInt64 && counters.numel() == logits.size(0),
+              "counters must be int64 [rows]");
+  check_cuda(out_tokens, "out_tokens");
+  TORCH_CHECK(out_tokens.scalar_type() == torch::kInt32 && out_tokens.numel() == logits.size(0),
+              "out_tokens must be int32 [rows]");
+  TORCH_CHECK(counters.device() == logits.device() && out_tokens.device() == logits.device(),
+              "all tensors must be on the same device");
+  TORCH_CHECK(temperature == temperature && top_p == top_p, "temperature and top_p must not be NaN");
+  const c10::hip::HIPGuardMasqueradingAsCUDA guard(logits.device());
+  const int s = qmk_sample_rows(static_cast<const float*>(logits.data_ptr()), (int)logits.size(0),
+                                (int)logits.size(1), (float)temperature, (int)top_k, (float)top_p,
+                                (unsigned long long)seed, static_cast<const long long*>(counters.data_ptr()),
+                                static_cast<int*>(out_tokens.data_ptr()),
+                                c10::hip::getCurrentHIPStreamMasqueradingAsCUDA().stream());
+  TORCH_CHECK(s == QMK_OK, "sample failed: ", qmk_status_string(s));
 }
 
 void set_graph_launch(bool enable) {
@@ -477,6 +537,17 @@ TORCH_LIBRARY(qwen_megakernel_C, ops) {
       "int num_layers, int start_position, int max_seq_len, float attn_scale) -> Tensor");
   ops.impl("generate_eos", torch::kCUDA, &generate_eos);
   ops.def("set_graph_launch(bool enable) -> ()", &set_graph_launch);
+  ops.def(
+      "generate_sample(int first_token_id, int num_steps, int eos_token_id, float temperature, int top_k, "
+      "float top_p, int seed, Tensor embed_weight, Tensor layer_weights_packed, "
+      "Tensor final_norm_weight, Tensor lm_head_weight, "
+      "Tensor cos_table, Tensor sin_table, Tensor k_cache, Tensor v_cache, "
+      "Tensor hidden_buffer, Tensor normalized, "
+      "int num_layers, int start_position, int max_seq_len, float attn_scale) -> Tensor");
+  ops.impl("generate_sample", torch::kCUDA, &generate_sample);
+  ops.def("sample(Tensor logits, float temperature, int top_k, float top_p, int seed, Tensor counters, "
+          "Tensor out_tokens) -> ()");
+  ops.impl("sample", torch::kCUDA, &sample);
   ops.def("device_error() -> int", &device_error);
   ops.def("reset() -> ()", &reset);
   ops.def("set_wait_limit(int ticks) -> ()", &set_wait_limit);

@@ -233,8 +233,10 @@ class Decoder:
     def position(self) -> int:
         return self._position
 
-    def generate(self, prompt, max_tokens: int = 100):
-        """Greedy continuation of ``prompt`` (text with a tokenizer, or a list of ids)."""
+    def generate(self, prompt, max_tokens: int = 100, temperature: float = 0.0, top_k: int = 0, top_p: float = 1.0,
+                 seed: int = 0):
+        """Continuation of ``prompt`` (text with a tokenizer, or a list of ids): greedy, or sampled when
+        ``temperature > 0`` (HF's temperature / top-k / top-p, one Gumbel-max draw per step on the GPU)."""
         self.reset()
         if isinstance(prompt, str):
             if self.tokenizer is None:
@@ -242,18 +244,21 @@ class Decoder:
             ids = self.tokenizer.encode(prompt, add_special_tokens=True)
         else:
             ids = [int(t) for t in prompt]
+        samp = dict(temperature=temperature, top_k=top_k, top_p=top_p, seed=seed)
         if not isinstance(prompt, str):
-            return self.generate_ids(ids, max_tokens)
+            return self.generate_ids(ids, max_tokens, **samp)
         eos = self.tokenizer.eos_token_id
-        out = self.generate_ids(ids, max_tokens, eos_token_id=eos)
+        out = self.generate_ids(ids, max_tokens, eos_token_id=eos, **samp)
         if eos in out:
             out = out[: out.index(eos)]
         return self.tokenizer.decode(out, skip_special_tokens=True)
 
     # -- additions --------------------------------------------------------
 
-    def generate_ids(self, ids: list[int], max_tokens: int, eos_token_id: int | None = None) -> list[int]:
-        """Step ``ids[:-1]``, then ``max_tokens`` device-fed greedy steps from ``ids[-1]``.
+    def generate_ids(self, ids: list[int], max_tokens: int, eos_token_id: int | None = None,
+                     temperature: float = 0.0, top_k: int = 0, top_p: float = 1.0, seed: int = 0) -> list[int]:
+        """Step ``ids[:-1]``, then ``max_tokens`` device-fed steps from ``ids[-1]``: greedy, or with
+        ``temperature > 0`` sampled (the draw of the step at position p uses counter p).
 
         With ``eos_token_id`` the device stops after emitting it: the rest of the
         returned list is ``eos_token_id`` padding and the position advances only by
@@ -267,6 +272,16 @@ class Decoder:
             for tid in ids[:-1]:
                 self.step(tid)
         self._check_position(max_tokens)
+        if temperature > 0:
+            eos = -1 if eos_token_id is None else int(eos_token_id)
+            out = self._ops.generate_sample(int(ids[-1]), int(max_tokens), eos, float(temperature), int(top_k),
+                                            float(top_p), int(seed), self._embed_weight,
+                                            self._layer_weights_packed, self._final_norm_weight,
+                                            self._lm_head_weight, self._cos_table, self._sin_table, self._k_cache,
+                                            self._v_cache, self._hidden, self._norm_out, self._num_layers,
+                                            self._position, self._max_seq_len, self._attn_scale).cpu().tolist()
+            self._position += out.index(eos) + 1 if eos >= 0 and eos in out else max_tokens
+            return out
         if eos_token_id is None:
             out = self._ops.generate_nosync(int(ids[-1]), int(max_tokens), *self._scratch(), self._num_layers,
                                             self._position, self._max_seq_len, self._attn_scale)
@@ -433,10 +448,17 @@ class BatchDecoder:
     def step(self, tokens) -> list[int]:
         return self.step_logits(tokens)[0]
 
-    def decode_steps(self, tokens: torch.Tensor, steps: int) -> torch.Tensor:
-        """``steps`` batched greedy steps from device tokens (one per sequence, at the current positions),
-        each step's outputs fed to the next on the device; no host synchronisation.  Returns the device
-        log ``[steps + 1, B]`` whose row 0 is ``tokens`` and row i the tokens after step i."""
+    def _counters(self, positions: torch.Tensor) -> torch.Tensor:
+        """Per-row random-number counters: position + (sequence << 32) (sequence 0: the position, as the
+        single-sequence sampled loop uses)."""
+        return positions.to(torch.int64) + (self._all.to(torch.int64) << 32)
+
+    def decode_steps(self, tokens: torch.Tensor, steps: int, temperature: float = 0.0, top_k: int = 0,
+                     top_p: float = 1.0, seed: int = 0) -> torch.Tensor:
+        """``steps`` batched steps from device tokens (one per sequence, at the current positions),
+        each step's outputs fed to the next on the device; no host synchronisation.  Greedy, or with
+        ``temperature > 0`` sampled from each step's logits (``sample`` op).  Returns the device log
+        ``[steps + 1, B]`` whose row 0 is ``tokens`` and row i the tokens after step i."""
         if tokens.numel() != self.batch_size:
             raise ValueError(f"expected {self.batch_size} tokens")
         for b in range(self.batch_size):
@@ -448,14 +470,25 @@ class BatchDecoder:
             pos_table = start[None, :] + torch.arange(steps, dtype=torch.int32, device=self._dev)[:, None]
             max_context = max(self._positions) + steps
             self._forward.workspace(self.batch_size, self.batch_size, max_context)
+            sampled = temperature > 0
+            if sampled:
+                logits = torch.empty(self.batch_size, VOCAB_SIZE, dtype=torch.float32, device=self._dev)
+                greedy = torch.empty(self.batch_size, dtype=torch.int32, device=self._dev)
             for i in range(steps):
-                self._forward(log[i], self._all, pos_table[i], self._all, log[i + 1], None, self._k_cache,
+                if not sampled:
+                    self._forward(log[i], self._all, pos_table[i], self._all, log[i + 1], None, self._k_cache,
+                                  self._v_cache, max_context)
+                    continue
+                self._forward(log[i], self._all, pos_table[i], self._all, greedy, logits, self._k_cache,
                               self._v_cache, max_context)
+                self._ops.sample(logits, float(temperature), int(top_k), float(top_p), int(seed),
+                                 self._counters(pos_table[i]), log[i + 1])
             self._positions = [p + steps for p in self._positions]
         return log
 
-    def generate_ids(self, prompts, max_tokens: int) -> list[list[int]]:
-        """Greedy continuations (``max_tokens`` each) of one prompt per sequence.
+    def generate_ids(self, prompts, max_tokens: int, temperature: float = 0.0, top_k: int = 0, top_p: float = 1.0,
+                     seed: int = 0) -> list[list[int]]:
+        """Continuations (``max_tokens`` each) of one prompt per sequence, greedy or sampled.
 
         Each prompt is prefilled, then the batch is stepped with the tokens fed
         back on the device: no host synchronisation until the end.
@@ -467,8 +500,16 @@ class BatchDecoder:
         self.reset()
         for b, ids in enumerate(prompts):
             self._check(b, len(ids) + max_tokens - 1)
-        first = [self.prefill(b, ids) for b, ids in enumerate(prompts)]
-        log = self.decode_steps(_as_i32(first, self._dev), max_tokens - 1)
+        if temperature > 0:
+            first_t = torch.empty(self.batch_size, dtype=torch.int32, device=self._dev)
+            for b, ids in enumerate(prompts):
+                _, lg = self.prefill(b, ids, return_logits=True)
+                pos = torch.tensor([self._positions[b] - 1], dtype=torch.int64, device=self._dev)
+                self._ops.sample(lg[None, :].contiguous(), float(temperature), int(top_k), float(top_p), int(seed),
+                                 pos + (b << 32), first_t[b:b + 1])
+        else:
+            first_t = _as_i32([self.prefill(b, ids) for b, ids in enumerate(prompts)], self._dev)
+        log = self.decode_steps(first_t, max_tokens - 1, temperature, top_k, top_p, seed)
         out = log.t().cpu().tolist()
         if any(t < 0 for row in out for t in row):
             raise RuntimeError("batched generation produced an invalid token")
