@@ -306,6 +306,28 @@ int qmk_forward_tokens(
     int num_layers, int max_seq_len, int max_context, float attn_scale,
     void *workspace, size_t workspace_bytes, hipStream_t stream);
 
+/* Workspace bytes qmk_decode_batch needs.  0 for invalid arguments. */
+size_t qmk_decode_batch_workspace_bytes(int model, int batch, int max_context);
+
+/* One batched decode step: token b (tokens[b], device) of sequence b at
+ * positions[b] (device), b < batch; out_tokens[b] (device) receives its greedy
+ * next token, logits_out[b][vocab] its logits when not NULL.  Sequence b's
+ * cache is the [num_layers][8][max_seq_len][128] block at k_cache + b *
+ * seq_stride.  The same as qmk_forward_tokens with seq_ids = emit_rows =
+ * 0..batch-1, but since each sequence has one token, batches of up to 16 with
+ * max_context <= 4096 run five fused launches per layer (RMSNorm in the GEMM
+ * prologues, q/k norm + RoPE + K/V append inside attention, residual and
+ * SiLU*up in the GEMM epilogues).  Invalid ids or positions emit -1.
+ * Asynchronous; returns a status code. */
+int qmk_decode_batch(
+    int model, int batch, const int *tokens, const int *positions, int *out_tokens,
+    float *logits_out, const void *embed_weight,
+    const LDGLayerWeights *layer_weights_host, const void *final_norm_weight,
+    const void *lm_head_weight, const void *cos_table, const void *sin_table,
+    void *k_cache, void *v_cache, long long seq_stride, int num_layers,
+    int max_seq_len, int max_context, float attn_scale, void *workspace,
+    size_t workspace_bytes, hipStream_t stream);
+
 /* One 16x16x32 bf16 MFMA with the operand layouts the batched GEMM assumes:
  * c[16][16] (f32) = a[16][32] . b[16][32]^T (bf16, row-major).  For tests.
  * Asynchronous; returns a status code. */

@@ -107,12 +107,12 @@ __global__ void __launch_bounds__(256) prep_tokens(const int* __restrict__ token
                                                    Tok* __restrict__ tok, int* __restrict__ erow) {
   const int i = blockIdx.x * 256 + threadIdx.x;
   if (i < T) {
-    const int id = tokens[i], sq = seqs[i], p = pos[i];
+    const int id = tokens[i], sq = seqs ? seqs[i] : i, p = pos[i];
     const bool ok = id >= 0 && id < vocab && sq >= 0 && sq < num_seqs && p >= 0 && p < max_context;
     tok[i] = Tok{ok ? id : 0, ok ? sq : 0, ok ? p : 0, ok ? 1 : 0};
   }
   if (i < R) {
-    const int e = emit[i];
+    const int e = emit ? emit[i] : i;
     erow[i] = (e >= 0 && e < T) ? e : -1;
   }
 }
@@ -631,6 +631,316 @@ __global__ void __launch_bounds__(256) keys_reduce(const unsigned long long* __r
   }
 }
 
+// ---------------------------------------------------------------- decode step, few sequences
+//
+// One token per sequence, at most 16 sequences (one MFMA row tile), contexts
+// up to kFusedCtx: five launches per layer instead of eleven.
+//
+//   gemm_rows<NORM>(q,k,v)   input RMSNorm in the prologue, bf16 q|k|v out
+//   attention_fused          q/k head norm + RoPE, K/V append, attention
+//   gemm_rows(o)             epilogue: residual add into the hidden rows
+//   gemm_rows<NORM>(g|u)     post-attention RMSNorm in the prologue, SiLU(g)*u out
+//   gemm_rows(down)          epilogue: residual add
+//
+// gemm_rows: one workgroup of 16 waves per 16*NB-column tile; wave w takes
+// K/16 of the K range (the same MFMA operand layout as gemm_partial) and the
+// 16 partial tiles are summed in LDS in wave order, so every column is one
+// fp32 sum rounded once, with no partials in memory and no finish kernel.
+
+constexpr int kRowWaves = 16;
+constexpr int kMaxRowsH = 2048;   // largest hidden size a NORM prologue stages in LDS
+constexpr int kFusedCtx = 4096;   // longest context of the fused decode attention
+
+enum RowEpi : int { kEpiStore = 0, kEpiResidual = 1, kEpiSiluMul = 2 };
+
+// Row of W feeding column `col` of tile `tile` (NC columns): kEpiSiluMul takes
+// gate rows in columns 0..NC/2-1 and the up rows of the same NC/2 outputs in
+// columns NC/2..NC-1; otherwise the seg rows in order.
+template <int EPI, int NC>
+__device__ __forceinline__ const uint16_t* tile_row(const Seg& seg, int tile, int col, int K) {
+  if (EPI == kEpiSiluMul) return seg.w[col / (NC / 2)] + (size_t)(tile * (NC / 2) + col % (NC / 2)) * K;
+  return seg_row(seg, tile * NC + col, K);
+}
+
+// Dynamic LDS of gemm_rows: the normalised input rows (NORM), then the NW
+// partial tiles, then the per-wave sums of squares.
+template <int NB, int NW, bool NORM>
+constexpr size_t rows_lds(int T, int K) {
+  return (NORM ? (size_t)((T * K * 2 + 15) / 16 * 16) : 0) + (size_t)NW * 16 * 16 * NB * 4 + (size_t)NW * 16 * 4 + 64;
+}
+
+template <int NB, int EPI, bool NORM, int NW, int ITERS>
+__global__ void __launch_bounds__(NW * 64) gemm_rows(const uint16_t* __restrict__ X, const uint16_t* __restrict__ norm_w,
+                                                     float eps, int T, int K, Seg seg, uint16_t* __restrict__ Y,
+                                                     int ldy) {
+  constexpr int NC = 16 * NB;
+  extern __shared__ __align__(16) unsigned char smem[];
+  uint16_t* xs = reinterpret_cast<uint16_t*>(smem);
+  const size_t xs_bytes = NORM ? (size_t)((T * K * 2 + 15) / 16 * 16) : 0;
+  float (*red)[16][NC] = reinterpret_cast<float (*)[16][NC]>(smem + xs_bytes);
+  float (*ssr)[16] = reinterpret_cast<float (*)[16]>(smem + xs_bytes + (size_t)NW * 16 * NC * 4);
+  float* rstd_s = reinterpret_cast<float*>(smem + xs_bytes + (size_t)NW * 16 * NC * 4 + (size_t)NW * 16 * 4);
+  const int tile = blockIdx.x;
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int kq = 8 * (lane >> 4);
+  const int k0 = w * (64 * ITERS);
+  const int row = min(lane & 15, T - 1);
+  // the wave's whole weight slice is requested first: it streams while the prologue runs
+  bf16x8 b[ITERS][2][NB];
+#pragma unroll
+  for (int j = 0; j < NB; j++) {
+    const uint16_t* wr = tile_row<EPI, NC>(seg, tile, 16 * j + (lane & 15), K) + kq + k0;
+#pragma unroll
+    for (int it = 0; it < ITERS; it++) {
+      b[it][0][j] = ld_bf16x8_stream(wr + 64 * it);
+      b[it][1][j] = ld_bf16x8_stream(wr + 64 * it + 32);
+    }
+  }
+  if (NORM) {
+    // RMSNorm of the T input rows into LDS: bf16(w * bf16(x * rstd)), as HF
+    for (int t = 0; t < T; t++) {
+      float part = 0.f;
+      for (int i = threadIdx.x; i < K; i += NW * 64) {
+        const float v = bf16_to_f32(X[(size_t)t * K + i]);
+        part += v * v;
+      }
+      part = wave_sum(part);
+      if (lane == 0) ssr[w][t] = part;
+    }
+    __syncthreads();
+    if ((int)threadIdx.x < T) {
+      float ss = 0.f;
+      for (int q = 0; q < NW; q++) ss += ssr[q][threadIdx.x];
+      rstd_s[threadIdx.x] = rcp_sqrt_torch(__fdiv_rn(ss, (float)K) + eps);
+    }
+    __syncthreads();
+    for (int t = 0; t < T; t++) {
+      const float r = rstd_s[t];
+      for (int i = threadIdx.x; i < K; i += NW * 64) {
+        const float v = bf16_to_f32(X[(size_t)t * K + i]);
+        xs[t * K + i] = (uint16_t)f32_to_bf16(bf16r(bf16_to_f32(ldu16(norm_w + i)) * bf16r(v * r)));
+      }
+    }
+    __syncthreads();
+  }
+  auto load_a = [&](int k) -> bf16x8 {
+    if (NORM) return *reinterpret_cast<const bf16x8*>(xs + row * K + kq + k);
+    return ld_bf16x8(X + (size_t)row * K + kq + k);
+  };
+  bf16x8 a[ITERS][2];
+#pragma unroll
+  for (int it = 0; it < ITERS; it++) {
+    a[it][0] = load_a(k0 + 64 * it);
+    a[it][1] = load_a(k0 + 64 * it + 32);
+  }
+  f32x4 acc[NB];
+#pragma unroll
+  for (int j = 0; j < NB; j++) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int it = 0; it < ITERS; it++)
+#pragma unroll
+    for (int j = 0; j < NB; j++) {
+      acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[it][0], b[it][0][j], acc[j], 0, 0, 0);
+      acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[it][1], b[it][1][j], acc[j], 0, 0, 0);
+    }
+#pragma unroll
+  for (int j = 0; j < NB; j++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) red[w][4 * (lane >> 4) + i][16 * j + (lane & 15)] = acc[j][i];
+  __syncthreads();
+  const int t = threadIdx.x / NC, c = threadIdx.x % NC;
+  if (t >= T || t >= 16) return;
+  auto col_sum = [&](int cc) {
+    float y = 0.f;
+#pragma unroll
+    for (int q = 0; q < NW; q++) y += red[q][t][cc];  // wave order
+    return y;
+  };
+  if (EPI == kEpiSiluMul) {
+    if (c >= NC / 2) return;
+    const float g = bf16r(col_sum(c)), u = bf16r(col_sum(c + NC / 2));
+    const float sg = bf16r(__fdiv_rn(g, 1.0f + expf(-g)));
+    Y[(size_t)t * ldy + tile * (NC / 2) + c] = (uint16_t)f32_to_bf16(bf16r(sg * u));
+    return;
+  }
+  const float y = bf16r(col_sum(c));
+  uint16_t* dst = Y + (size_t)t * ldy + tile * NC + c;
+  if (EPI == kEpiResidual) *dst = (uint16_t)f32_to_bf16(bf16r(bf16_to_f32(*dst) + y));
+  else *dst = (uint16_t)f32_to_bf16(y);
+}
+
+// One workgroup of 16 waves per (sequence's token, KV head g): the q heads 2g,
+// 2g+1 and k head g get their head RMSNorm + RoPE, K/V of the token are
+// appended at its position, then eager attention over positions 0..pos (the
+// token's own K/V taken from LDS).  Valid only when no other token of the
+// launch writes this sequence's cache (one token per sequence).
+__global__ void __launch_bounds__(1024) attention_fused(const uint16_t* __restrict__ QKV, const Tok* __restrict__ tok,
+                                                        int L, const uint16_t* q_norm, const uint16_t* k_norm,
+                                                        const uint16_t* cos_t, const uint16_t* sin_t, Cache c,
+                                                        float eps, float scale, uint16_t* __restrict__ out) {
+  __shared__ float sc[2][kFusedCtx];
+  __shared__ uint16_t qs[2][kD], kn[kD], vn[kD];
+  __shared__ float redm[2][kRowWaves];
+  __shared__ float pv[kRowWaves][2][kD];
+  const int t = blockIdx.x, g = blockIdx.y;
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, slot = lane >> 4, t16 = lane & 15;
+  const Tok tk = tok[t];
+  uint16_t* dst = out + (size_t)t * kQS + 2 * g * kD;
+  if (!tk.valid) {
+    if (threadIdx.x < 2 * kD) dst[threadIdx.x] = 0;
+    return;
+  }
+  const int pos = tk.pos, C = pos + 1;
+  const size_t base = cache_base(c, tk, L, g);
+  if (w < 4) {
+    // waves 0,1: q heads 2g, 2g+1; wave 2: k head g; wave 3: v head g
+    const int h = w < 2 ? 2 * g + w : (w == 2 ? kNQ + g : kNQ + kNKV + g);
+    const uint16_t* src = QKV + (size_t)t * kNQKV + h * kD;
+    const float x0 = bf16_to_f32(src[lane]), x1 = bf16_to_f32(src[lane + 64]);
+    if (w == 3) {
+      vn[lane] = src[lane];
+      vn[lane + 64] = src[lane + 64];
+      c.v[base + (size_t)pos * kD + lane] = src[lane];
+      c.v[base + (size_t)pos * kD + lane + 64] = src[lane + 64];
+    } else {
+      const uint16_t* nw = w < 2 ? q_norm : k_norm;
+      const float ss = wave_sum(x0 * x0 + x1 * x1);
+      const float rstd = rcp_sqrt_torch(__fdiv_rn(ss, (float)kD) + eps);
+      const float n0 = bf16r(bf16_to_f32(ldu16(nw + lane)) * bf16r(x0 * rstd));
+      const float n1 = bf16r(bf16_to_f32(ldu16(nw + lane + 64)) * bf16r(x1 * rstd));
+      const uint16_t* cr = cos_t + (size_t)pos * kD;
+      const uint16_t* sr = sin_t + (size_t)pos * kD;
+      const float c0 = bf16_to_f32(ldu16(cr + lane)), c1 = bf16_to_f32(ldu16(cr + lane + 64));
+      const float s0 = bf16_to_f32(ldu16(sr + lane)), s1 = bf16_to_f32(ldu16(sr + lane + 64));
+      const uint16_t y0 = (uint16_t)f32_to_bf16(bf16r(bf16r(n0 * c0) + bf16r(-n1 * s0)));
+      const uint16_t y1 = (uint16_t)f32_to_bf16(bf16r(bf16r(n1 * c1) + bf16r(n0 * s1)));
+      if (w < 2) {
+        qs[w][lane] = y0;
+        qs[w][lane + 64] = y1;
+      } else {
+        kn[lane] = y0;
+        kn[lane + 64] = y1;
+        c.k[base + (size_t)pos * kD + lane] = y0;
+        c.k[base + (size_t)pos * kD + lane + 64] = y1;
+      }
+    }
+  }
+  __syncthreads();
+  const uint16_t* kc = c.k + base;
+  const uint16_t* vc = c.v + base;
+  u32x4 qv[2];
+#pragma unroll
+  for (int h = 0; h < 2; h++) qv[h] = *reinterpret_cast<const u32x4*>(&qs[h][8 * t16]);
+  const u32x4 k_now = *reinterpret_cast<const u32x4*>(&kn[8 * t16]);
+  // scores: each 16-lane row one position, 64 per round, four rounds in flight
+  float m0 = -INFINITY, m1 = -INFINITY;
+  for (int p0 = 4 * w + slot; p0 < C; p0 += 4 * 64) {
+    u32x4 kx[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      const int p = p0 + 64 * u;
+      kx[u] = (p < C && p != pos) ? ld16(kc + (size_t)p * kD + 8 * t16) : k_now;
+    }
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      const int p = p0 + 64 * u;
+      if (p < C) {
+        const float s0 = bf16r(bf16r(row16_sum(dot8(kx[u], qv[0], 0.f))) * scale);
+        const float s1 = bf16r(bf16r(row16_sum(dot8(kx[u], qv[1], 0.f))) * scale);
+        if (t16 == 0) {
+          sc[0][p] = s0;
+          sc[1][p] = s1;
+        }
+        m0 = fmaxf(m0, s0);
+        m1 = fmaxf(m1, s1);
+      }
+    }
+  }
+  m0 = wave_max(m0);
+  m1 = wave_max(m1);
+  if (lane == 0) {
+    redm[0][w] = m0;
+    redm[1][w] = m1;
+  }
+  __syncthreads();
+  float M0 = redm[0][0], M1 = redm[1][0];
+  for (int q = 1; q < kRowWaves; q++) {
+    M0 = fmaxf(M0, redm[0][q]);
+    M1 = fmaxf(M1, redm[1][q]);
+  }
+  float l0 = 0.f, l1 = 0.f;
+  for (int i = threadIdx.x; i < C; i += 1024) {
+    l0 += exp_acc(sc[0][i] - M0);
+    l1 += exp_acc(sc[1][i] - M1);
+  }
+  l0 = wave_sum(l0);
+  l1 = wave_sum(l1);
+  __syncthreads();
+  if (lane == 0) {
+    redm[0][w] = l0;
+    redm[1][w] = l1;
+  }
+  __syncthreads();
+  float S0 = 0.f, S1 = 0.f;
+  for (int q = 0; q < kRowWaves; q++) {
+    S0 += redm[0][q];
+    S1 += redm[1][q];
+  }
+  const float inv0 = __fdiv_rn(1.0f, S0), inv1 = __fdiv_rn(1.0f, S1);
+  for (int i = threadIdx.x; i < C; i += 1024) {
+    sc[0][i] = bf16r(exp_acc(sc[0][i] - M0) * inv0);
+    sc[1][i] = bf16r(exp_acc(sc[1][i] - M1) * inv1);
+  }
+  __syncthreads();
+  // P @ V: each 16-lane row takes one position (lane t16: dims 8*t16..+7 of both heads), 64 per
+  // round, four rounds in flight; then the four rows of a wave and the 16 waves are summed in order
+  const u32x4 v_now = *reinterpret_cast<const u32x4*>(&vn[8 * t16]);
+  float acc0[8], acc1[8];
+#pragma unroll
+  for (int i = 0; i < 8; i++) acc0[i] = acc1[i] = 0.f;
+  for (int p0 = 4 * w + slot; p0 < C; p0 += 4 * 64) {
+    u32x4 vx[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      const int p = p0 + 64 * u;
+      vx[u] = (p < C && p != pos) ? ld16(vc + (size_t)p * kD + 8 * t16) : v_now;
+    }
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      const int p = p0 + 64 * u;
+      if (p < C) {
+        const float pa = sc[0][p], pb = sc[1][p];
+        const float vf[8] = {lo_bf16(vx[u].x), hi_bf16(vx[u].x), lo_bf16(vx[u].y), hi_bf16(vx[u].y),
+                             lo_bf16(vx[u].z), hi_bf16(vx[u].z), lo_bf16(vx[u].w), hi_bf16(vx[u].w)};
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+          acc0[i] += pa * vf[i];
+          acc1[i] += pb * vf[i];
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    acc0[i] = rows_sum4(acc0[i]);
+    acc1[i] = rows_sum4(acc1[i]);
+  }
+  if (lane < 16) {
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      pv[w][0][8 * t16 + i] = acc0[i];
+      pv[w][1][8 * t16 + i] = acc1[i];
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x < 2 * kD) {
+    const int h = threadIdx.x >> 7, d = threadIdx.x & 127;
+    float y = 0.f;
+    for (int q = 0; q < kRowWaves; q++) y += pv[q][h][d];
+    dst[threadIdx.x] = (uint16_t)f32_to_bf16(y);
+  }
+}
+
 // ---------------------------------------------------------------- self-test
 
 // C[16][16] = A[16][32] . B[16][32]^T through one MFMA with the operand
@@ -689,13 +999,16 @@ size_t part_floats(int T, int N, int K) { return (size_t)plan_gemm(T, N, K).kspl
 int split_chunks(int max_context) { return (max_context + kSplitChunk - 1) / kSplitChunk; }
 
 struct Layout {
-  size_t tok, erow, keys, x, n, q, att, m, part, scores, ml, pv, total;
+  size_t tok, erow, keys, x, n, q, att, m, qkv, part, scores, ml, pv, total;
 };
 
 constexpr int kLmTiles(int V) { return V / 64; }
 
+// The decode step of few sequences (one token each) takes the fused path.
+bool fused_decode(int T, int max_context) { return T <= 16 && max_context <= kFusedCtx; }
+
 template <class M>
-Layout layout(int T, int R, int max_context) {
+Layout layout(int T, int R, int max_context, bool one_per_seq = false) {
   using Dm = Dims<M>;
   auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
   Layout l{};
@@ -712,6 +1025,11 @@ Layout layout(int T, int R, int max_context) {
   take(l.q, (size_t)T * kQS * 2);
   take(l.att, (size_t)T * kQS * 2);
   take(l.m, (size_t)T * Dm::I * 2);
+  if (one_per_seq && fused_decode(T, max_context)) {
+    take(l.qkv, (size_t)T * kNQKV * 2);
+    l.total = off;
+    return l;
+  }
   size_t pf = part_floats(T, kNQKV, Dm::H);
   pf = std::max(pf, part_floats(T, Dm::H, kQS));
   pf = std::max(pf, part_floats(T, 2 * Dm::I, Dm::H));
@@ -729,6 +1047,7 @@ Layout layout(int T, int R, int max_context) {
 
 struct Args {
   int T, R, num_seqs, max_context;
+  bool one_per_seq;  // token t is sequence t's only token (batched decode step)
   const int *tokens, *seqs, *pos, *emit;
   int* out_tokens;
   float* logits;
@@ -740,10 +1059,84 @@ struct Args {
   char* ws;
 };
 
+// gemm_rows over `tiles` 16-column tiles (NB = 1), NW waves each taking
+// K / NW = 64 * ITERS of the K range; ITERS picked from K.
+template <int EPI, bool NORM, int NW, int ITERS>
+void launch_rows_it(int tiles, const uint16_t* X, const uint16_t* nw, float eps, int T, int K, const Seg& seg,
+                    uint16_t* Y, int ldy, hipStream_t s) {
+  const size_t lds = rows_lds<1, NW, NORM>(T, K);
+  if (lds > 64 * 1024) {
+    // 16 normalised rows of 2048: above the default dynamic LDS limit (gfx950 has 160 KB per CU)
+    static bool raised = false;
+    if (!raised)
+      raised = hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_rows<1, EPI, NORM, NW, ITERS>),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024) == hipSuccess;
+  }
+  hipLaunchKernelGGL((gemm_rows<1, EPI, NORM, NW, ITERS>), dim3(tiles), dim3(NW * 64), lds, s, X, nw, eps, T, K, seg,
+                     Y, ldy);
+}
+
+template <int EPI, bool NORM, int NW>
+void launch_rows(int tiles, const uint16_t* X, const uint16_t* nw, float eps, int T, int K, const Seg& seg,
+                 uint16_t* Y, int ldy, hipStream_t s) {
+  switch (K / (64 * NW)) {
+    case 1: launch_rows_it<EPI, NORM, NW, 1>(tiles, X, nw, eps, T, K, seg, Y, ldy, s); break;
+    case 2: launch_rows_it<EPI, NORM, NW, 2>(tiles, X, nw, eps, T, K, seg, Y, ldy, s); break;
+    case 3: launch_rows_it<EPI, NORM, NW, 3>(tiles, X, nw, eps, T, K, seg, Y, ldy, s); break;
+    case 4: launch_rows_it<EPI, NORM, NW, 4>(tiles, X, nw, eps, T, K, seg, Y, ldy, s); break;
+    default: launch_rows_it<EPI, NORM, NW, 6>(tiles, X, nw, eps, T, K, seg, Y, ldy, s); break;
+  }
+}
+
+template <class M>
+int forward_fused(const Args& a, hipStream_t s) {
+  using Dm = Dims<M>;
+  const int T = a.T, R = a.R;
+  const Layout l = layout<M>(T, R, a.max_context, true);
+  Tok* tok = reinterpret_cast<Tok*>(a.ws + l.tok);
+  int* erow = reinterpret_cast<int*>(a.ws + l.erow);
+  auto* keys = reinterpret_cast<unsigned long long*>(a.ws + l.keys);
+  uint16_t* X = reinterpret_cast<uint16_t*>(a.ws + l.x);
+  uint16_t* N = reinterpret_cast<uint16_t*>(a.ws + l.n);
+  uint16_t* ATT = reinterpret_cast<uint16_t*>(a.ws + l.att);
+  uint16_t* MM = reinterpret_cast<uint16_t*>(a.ws + l.m);
+  uint16_t* QKV = reinterpret_cast<uint16_t*>(a.ws + l.qkv);
+  const float eps = 1e-6f;
+  auto u16 = [](const void* p) { return static_cast<const uint16_t*>(p); };
+  // every K is split into 16 (8 for gate/up) slices of 64 * {1, 2, 3, 4, 6}
+  static_assert(Dm::H == 1024 || Dm::H == 2048, "K splits of the hidden size");
+  static_assert(Dm::I == 3072 || Dm::I == 6144, "K splits of the MLP size");
+  static_assert(kQS == 2048 && Dm::H <= kMaxRowsH, "K splits of the attention output");
+  hipLaunchKernelGGL(prep_tokens, dim3((std::max(T, R) + 255) / 256), dim3(256), 0, s, a.tokens, a.seqs, a.pos, T,
+                     a.emit, R, a.num_seqs, a.max_context, Dm::V, tok, erow);
+  hipLaunchKernelGGL(embed_rows, dim3(T), dim3(256), 0, s, a.embed, tok, Dm::H, X);
+  for (int L = 0; L < a.num_layers; L++) {
+    const LDGLayerWeights& w = a.layers[L];
+    const Seg qkv{{u16(w.q_proj_weight), u16(w.k_proj_weight), u16(w.v_proj_weight)}, {kQS, kNKV * kD, kNKV * kD}};
+    launch_rows<kEpiStore, true, 16>(kNQKV / 16, X, u16(w.input_layernorm_weight), eps, T, Dm::H, qkv, QKV, kNQKV, s);
+    hipLaunchKernelGGL(attention_fused, dim3(T, kNKV), dim3(1024), 0, s, QKV, tok, L, u16(w.q_norm_weight),
+                       u16(w.k_norm_weight), a.cos_t, a.sin_t, a.cache, eps, a.attn_scale, ATT);
+    const Seg o{{u16(w.o_proj_weight), nullptr, nullptr}, {Dm::H, 0, 0}};
+    launch_rows<kEpiResidual, false, 16>(Dm::H / 16, ATT, nullptr, eps, T, kQS, o, X, Dm::H, s);
+    const Seg gu{{u16(w.gate_proj_weight), u16(w.up_proj_weight), nullptr}, {Dm::I, Dm::I, 0}};
+    launch_rows<kEpiSiluMul, true, 8>(Dm::I / 8, X, u16(w.post_attn_layernorm_weight), eps, T, Dm::H, gu, MM, Dm::I,
+                                      s);
+    const Seg dn{{u16(w.down_proj_weight), nullptr, nullptr}, {Dm::H, 0, 0}};
+    launch_rows<kEpiResidual, false, 16>(Dm::H / 16, MM, nullptr, eps, T, Dm::I, dn, X, Dm::H, s);
+  }
+  hipLaunchKernelGGL((residual_norm<Dm::H>), dim3(T), dim3(1024), 0, s, nullptr, 0, T, X, a.final_norm, eps, N);
+  const int lm_waves = ((R + 15) / 16) * kLmTiles(Dm::V);
+  hipLaunchKernelGGL(lm_head_gemm, dim3((lm_waves + 3) / 4), dim3(256), 0, s, N, erow, R, a.lm_head, Dm::H, Dm::V,
+                     keys, a.logits);
+  hipLaunchKernelGGL(keys_reduce, dim3(R), dim3(256), 0, s, keys, kLmTiles(Dm::V), erow, tok, a.out_tokens);
+  return hipGetLastError() == hipSuccess ? QMK_OK : QMK_ERR_HIP;
+}
+
 template <class M>
 int forward(const Args& a, hipStream_t s) {
   using Dm = Dims<M>;
   const int T = a.T, R = a.R;
+  if (a.one_per_seq && fused_decode(T, a.max_context)) return forward_fused<M>(a, s);
   const Layout l = layout<M>(T, R, a.max_context);
   Tok* tok = reinterpret_cast<Tok*>(a.ws + l.tok);
   int* erow = reinterpret_cast<int*>(a.ws + l.erow);
@@ -860,6 +1253,62 @@ int qmk_forward_tokens(int model, int num_tokens, const int* tokens, const int* 
   a.layers = layer_weights_host;
   a.cache = batch::Cache{static_cast<uint16_t*>(k_cache), static_cast<uint16_t*>(v_cache),
                          num_seqs > 1 ? seq_stride : 0, max_seq_len};
+  a.num_layers = num_layers;
+  a.attn_scale = attn_scale;
+  a.ws = static_cast<char*>(workspace);
+  return model == QMK_MODEL_QWEN3_1_7B ? batch::forward<Qwen3_1_7B>(a, stream) : batch::forward<Qwen3_0_6B>(a, stream);
+}
+
+size_t qmk_decode_batch_workspace_bytes(int model, int batch, int max_context) {
+  if (batch < 1 || batch > batch::kMaxEmit || max_context < 1) return 0;
+  if (model == QMK_MODEL_QWEN3_1_7B) return batch::layout<Qwen3_1_7B>(batch, batch, max_context, true).total;
+  if (model == QMK_MODEL_QWEN3_0_6B) return batch::layout<Qwen3_0_6B>(batch, batch, max_context, true).total;
+  return 0;
+}
+
+int qmk_decode_batch(int model, int batch, const int* tokens, const int* positions, int* out_tokens,
+                     float* logits_out, const void* embed_weight, const LDGLayerWeights* layer_weights_host,
+                     const void* final_norm_weight, const void* lm_head_weight, const void* cos_table,
+                     const void* sin_table, void* k_cache, void* v_cache, long long seq_stride, int num_layers,
+                     int max_seq_len, int max_context, float attn_scale, void* workspace, size_t workspace_bytes,
+                     hipStream_t stream) {
+  if (model != QMK_MODEL_QWEN3_0_6B && model != QMK_MODEL_QWEN3_1_7B) return QMK_ERR_ARG;
+  if (batch < 1 || batch > batch::kMaxEmit || !tokens || !positions || !out_tokens || !embed_weight ||
+      !layer_weights_host || !final_norm_weight || !lm_head_weight || !cos_table || !sin_table || !k_cache ||
+      !v_cache || !workspace || num_layers < 1 || num_layers > kMaxLayers || max_seq_len < 1 || max_context < 1 ||
+      max_context > max_seq_len || !(attn_scale > 0.f))
+    return QMK_ERR_ARG;
+  const long long kv_per_seq = (long long)num_layers * batch::kNKV * max_seq_len * batch::kD;
+  if (batch > 1 && seq_stride < kv_per_seq) return QMK_ERR_ARG;
+  for (int L = 0; L < num_layers; L++) {
+    const LDGLayerWeights& w = layer_weights_host[L];
+    const void* p[11] = {w.input_layernorm_weight, w.q_proj_weight, w.k_proj_weight, w.v_proj_weight,
+                         w.q_norm_weight, w.k_norm_weight, w.o_proj_weight, w.post_attn_layernorm_weight,
+                         w.gate_proj_weight, w.up_proj_weight, w.down_proj_weight};
+    for (const void* q : p)
+      if (!q) return QMK_ERR_ARG;
+  }
+  if (workspace_bytes < qmk_decode_batch_workspace_bytes(model, batch, max_context)) return QMK_ERR_ARG;
+  batch::Args a{};
+  a.T = batch;
+  a.R = batch;
+  a.num_seqs = batch;
+  a.max_context = max_context;
+  a.one_per_seq = true;
+  a.tokens = tokens;
+  a.seqs = nullptr;
+  a.pos = positions;
+  a.emit = nullptr;
+  a.out_tokens = out_tokens;
+  a.logits = logits_out;
+  a.embed = static_cast<const uint16_t*>(embed_weight);
+  a.final_norm = static_cast<const uint16_t*>(final_norm_weight);
+  a.lm_head = static_cast<const uint16_t*>(lm_head_weight);
+  a.cos_t = static_cast<const uint16_t*>(cos_table);
+  a.sin_t = static_cast<const uint16_t*>(sin_table);
+  a.layers = layer_weights_host;
+  a.cache = batch::Cache{static_cast<uint16_t*>(k_cache), static_cast<uint16_t*>(v_cache), batch > 1 ? seq_stride : 0,
+                         max_seq_len};
   a.num_layers = num_layers;
   a.attn_scale = attn_scale;
   a.ws = static_cast<char*>(workspace);

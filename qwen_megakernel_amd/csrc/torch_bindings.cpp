@@ -396,6 +396,111 @@ int64_t forward_workspace_bytes(int64_t hidden, int64_t num_tokens, int64_t num_
                                               (int)max_context);
 }
 
+struct BatchModel {
+  int model;
+  std::vector<LDGLayerWeights> table;
+  int64_t num_seqs, max_seq_len, seq_stride;
+};
+
+// Checks the weights (reference flat list of 11 per layer) and the caches
+// ([L, 8, S, 128] or [B, L, 8, S, 128]) of a batched call.
+BatchModel check_batch_model(const torch::Tensor& embed_weight, const std::vector<torch::Tensor>& layer_weights,
+                             const torch::Tensor& final_norm_weight, const torch::Tensor& lm_head_weight,
+                             const torch::Tensor& cos_table, const torch::Tensor& sin_table,
+                             const torch::Tensor& k_cache, const torch::Tensor& v_cache, int64_t num_layers,
+                             int64_t max_context, double attn_scale) {
+  check_bf16(embed_weight, "embed_weight", -1);
+  const int64_t hidden = embed_weight.numel() / kVocab;
+  TORCH_CHECK(embed_weight.numel() == kVocab * hidden, "embed_weight must be [151936, hidden]");
+  BatchModel bm;
+  bm.model = model_of_hidden(hidden);
+  const int64_t inter = 3 * hidden;
+  TORCH_CHECK(num_layers >= 1 && num_layers <= kMaxLayers, "num_layers must be in [1, 28], got ", num_layers);
+  TORCH_CHECK(attn_scale > 0.0, "attn_scale must be positive");
+  check_bf16(final_norm_weight, "final_norm_weight", hidden);
+  check_bf16(lm_head_weight, "lm_head_weight", kVocab * hidden);
+  TORCH_CHECK((int64_t)layer_weights.size() >= 11 * num_layers, "layer_weights must hold 11 tensors per layer");
+  const int64_t sizes[11] = {hidden, kQ * hidden, kKV * hidden, kKV * hidden, kHeadDim, kHeadDim,
+                             hidden * kQ, hidden, inter * hidden, inter * hidden, hidden * inter};
+  bm.table.resize((size_t)num_layers);
+  for (int64_t L = 0; L < num_layers; L++) {
+    const void* p[11];
+    for (int i = 0; i < 11; i++) {
+      const torch::Tensor& t = layer_weights[(size_t)(11 * L + i)];
+      check_bf16(t, "layer weight", sizes[i]);
+      TORCH_CHECK(t.device() == embed_weight.device(), "all tensors must be on the same device");
+      p[i] = t.data_ptr();
+    }
+    bm.table[(size_t)L] = LDGLayerWeights{p[0], p[1], p[2], p[3], p[4], p[5], p[6], p[7], p[8], p[9], p[10]};
+  }
+  check_bf16(k_cache, "k_cache", -1);
+  check_bf16(v_cache, "v_cache", -1);
+  TORCH_CHECK(v_cache.sizes() == k_cache.sizes(), "v_cache must match k_cache");
+  TORCH_CHECK((k_cache.dim() == 4 || k_cache.dim() == 5) && k_cache.size(-3) == kKVHeads &&
+                  k_cache.size(-1) == kHeadDim && k_cache.size(-4) >= num_layers,
+              "k_cache must be [>= num_layers, 8, S, 128] or [B, >= num_layers, 8, S, 128]");
+  bm.max_seq_len = k_cache.size(-2);
+  bm.num_seqs = k_cache.dim() == 5 ? k_cache.size(0) : 1;
+  TORCH_CHECK(bm.num_seqs >= 1 && bm.max_seq_len >= 1 && bm.max_seq_len <= 65536, "k_cache sizes out of range");
+  bm.seq_stride = k_cache.size(-4) * kKVHeads * bm.max_seq_len * kHeadDim;
+  TORCH_CHECK(max_context >= 1 && max_context <= bm.max_seq_len, "max_context must be in [1, ", bm.max_seq_len, "]");
+  check_bf16(cos_table, "cos_table", -1);
+  check_bf16(sin_table, "sin_table", -1);
+  TORCH_CHECK(cos_table.dim() == 2 && cos_table.size(1) == kHeadDim && cos_table.size(0) >= bm.max_seq_len,
+              "cos_table must be [>= max_seq_len, 128]");
+  TORCH_CHECK(sin_table.sizes() == cos_table.sizes(), "sin_table must match cos_table");
+  for (const torch::Tensor* t : {&final_norm_weight, &lm_head_weight, &cos_table, &sin_table, &k_cache, &v_cache})
+    TORCH_CHECK(t->device() == embed_weight.device(), "all tensors must be on the same device");
+  return bm;
+}
+
+int64_t decode_batch_workspace_bytes(int64_t hidden, int64_t batch, int64_t max_context) {
+  TORCH_CHECK(batch >= 1 && batch <= 256, "batch must be in [1, 256]");
+  TORCH_CHECK(max_context >= 1 && max_context <= 65536, "max_context must be in [1, 65536]");
+  return (int64_t)qmk_decode_batch_workspace_bytes(model_of_hidden(hidden), (int)batch, (int)max_context);
+}
+
+// One batched decode step (qmk_decode_batch): tokens[b] of sequence b at positions[b].
+void decode_batch(torch::Tensor tokens, torch::Tensor positions, torch::Tensor out_tokens,
+                  std::optional<torch::Tensor> logits, torch::Tensor embed_weight,
+                  std::vector<torch::Tensor> layer_weights, torch::Tensor final_norm_weight,
+                  torch::Tensor lm_head_weight, torch::Tensor cos_table, torch::Tensor sin_table,
+                  torch::Tensor k_cache, torch::Tensor v_cache, torch::Tensor workspace, int64_t num_layers,
+                  int64_t max_context, double attn_scale) {
+  const BatchModel bm = check_batch_model(embed_weight, layer_weights, final_norm_weight, lm_head_weight, cos_table,
+                                          sin_table, k_cache, v_cache, num_layers, max_context, attn_scale);
+  const int64_t B = tokens.numel();
+  for (const torch::Tensor* t : {&tokens, &positions, &out_tokens}) {
+    check_cuda(*t, "token arrays");
+    TORCH_CHECK(t->scalar_type() == torch::kInt32, "tokens, positions, out_tokens must be int32");
+    TORCH_CHECK(t->device() == embed_weight.device(), "all tensors must be on the same device");
+  }
+  TORCH_CHECK(B >= 1 && B <= 256, "tokens must hold 1 .. 256 entries");
+  TORCH_CHECK(positions.numel() == B && out_tokens.numel() == B, "positions and out_tokens must match tokens");
+  TORCH_CHECK(bm.num_seqs == B, "k_cache must hold one sequence per token (", B, "), got ", bm.num_seqs);
+  float* lg = nullptr;
+  if (logits.has_value()) {
+    check_cuda(*logits, "logits");
+    TORCH_CHECK(logits->scalar_type() == torch::kFloat32 && logits->numel() == B * kVocab,
+                "logits must be float32[batch, 151936]");
+    lg = static_cast<float*>(logits->data_ptr());
+  }
+  check_cuda(workspace, "workspace");
+  TORCH_CHECK(workspace.device() == embed_weight.device(), "all tensors must be on the same device");
+  const size_t need = qmk_decode_batch_workspace_bytes(bm.model, (int)B, (int)max_context);
+  TORCH_CHECK((size_t)(workspace.numel() * workspace.element_size()) >= need, "workspace is smaller than ", need,
+              " bytes");
+  const c10::hip::HIPGuardMasqueradingAsCUDA guard(embed_weight.device());
+  const int s = qmk_decode_batch(
+      bm.model, (int)B, static_cast<const int*>(tokens.data_ptr()), static_cast<const int*>(positions.data_ptr()),
+      static_cast<int*>(out_tokens.data_ptr()), lg, embed_weight.data_ptr(), bm.table.data(),
+      final_norm_weight.data_ptr(), lm_head_weight.data_ptr(), cos_table.data_ptr(), sin_table.data_ptr(),
+      k_cache.data_ptr(), v_cache.data_ptr(), (long long)bm.seq_stride, (int)num_layers, (int)bm.max_seq_len,
+      (int)max_context, (float)attn_scale, workspace.data_ptr(), need,
+      c10::hip::getCurrentHIPStreamMasqueradingAsCUDA().stream());
+  TORCH_CHECK(s == QMK_OK, "decode_batch failed: ", qmk_status_string(s));
+}
+
 void forward_tokens(torch::Tensor tokens, torch::Tensor seq_ids, torch::Tensor positions, torch::Tensor emit_rows,
                     torch::Tensor out_tokens, std::optional<torch::Tensor> logits, torch::Tensor embed_weight,
                     std::vector<torch::Tensor> layer_weights, torch::Tensor final_norm_weight,
@@ -564,6 +669,14 @@ TORCH_LIBRARY(qwen_megakernel_C, ops) {
       "Tensor k_cache, Tensor v_cache, Tensor workspace, int num_layers, int max_context, "
       "float attn_scale) -> ()");
   ops.impl("forward_tokens", torch::kCUDA, &forward_tokens);
+  ops.def("decode_batch_workspace_bytes(int hidden, int batch, int max_context) -> int",
+          &decode_batch_workspace_bytes);
+  ops.def(
+      "decode_batch(Tensor tokens, Tensor positions, Tensor out_tokens, Tensor? logits, Tensor embed_weight, "
+      "Tensor[] layer_weights, Tensor final_norm_weight, Tensor lm_head_weight, Tensor cos_table, "
+      "Tensor sin_table, Tensor k_cache, Tensor v_cache, Tensor workspace, int num_layers, int max_context, "
+      "float attn_scale) -> ()");
+  ops.impl("decode_batch", torch::kCUDA, &decode_batch);
   ops.def("selftest_mfma(Tensor a, Tensor b, Tensor c) -> ()");
   ops.impl("selftest_mfma", torch::kCUDA, &selftest_mfma);
 }

@@ -136,6 +136,15 @@ class _Forward:
             self._ws = torch.empty(need, dtype=torch.uint8, device=self.embed.device)
         return self._ws
 
+    def decode(self, tokens, positions, out_tokens, logits, k_cache, v_cache, max_context: int):
+        """One batched decode step (``decode_batch`` op): token b of sequence b at positions[b]."""
+        need = int(self._ops.decode_batch_workspace_bytes(self.hidden, tokens.numel(), max_context))
+        if self._ws.numel() < need:
+            self._ws = torch.empty(need, dtype=torch.uint8, device=self.embed.device)
+        self._ops.decode_batch(tokens, positions, out_tokens, logits, self.embed, self.layers, self.final_norm,
+                               self.lm_head, self.cos, self.sin, k_cache, v_cache, self._ws, self.num_layers,
+                               max_context, self.scale)
+
     def __call__(self, tokens, seq_ids, positions, emit_rows, out_tokens, logits, k_cache, v_cache,
                  max_context: int):
         ws = self.workspace(tokens.numel(), emit_rows.numel(), max_context)
@@ -349,10 +358,11 @@ class Decoder:
 
 
 class BatchDecoder:
-    """Greedy decoding of ``batch_size`` independent sequences together.
+    """Greedy (or sampled) decoding of ``batch_size`` independent sequences together.
 
-    Each step is one batched forward (``forward_tokens``) over one token per
-    sequence, so one read of the weights serves the whole batch.  Sequence b
+    Each step is one batched decode step (``decode_batch``) over one token per
+    sequence, so one read of the weights serves the whole batch; prompts are
+    prefilled with ``forward_tokens``.  Sequence b
     keeps its own K/V cache (``[B, L, 8, S, 128]``) and position.  Not in the
     reference, which decodes one sequence.
     """
@@ -437,8 +447,8 @@ class BatchDecoder:
             self._check(b, 1)
         out = torch.empty(self.batch_size, dtype=torch.int32, device=self._dev)
         logits = torch.empty(self.batch_size, VOCAB_SIZE, dtype=torch.float32, device=self._dev)
-        self._forward(_as_i32(tokens, self._dev), self._all, _as_i32(self._positions, self._dev), self._all, out,
-                      logits, self._k_cache, self._v_cache, max(self._positions) + 1)
+        self._forward.decode(_as_i32(tokens, self._dev), _as_i32(self._positions, self._dev), out, logits,
+                             self._k_cache, self._v_cache, max(self._positions) + 1)
         self._positions = [p + 1 for p in self._positions]
         res = out.cpu().tolist()
         if any(t < 0 for t in res):
@@ -469,18 +479,17 @@ class BatchDecoder:
             start = torch.tensor(self._positions, dtype=torch.int32, device=self._dev)
             pos_table = start[None, :] + torch.arange(steps, dtype=torch.int32, device=self._dev)[:, None]
             max_context = max(self._positions) + steps
-            self._forward.workspace(self.batch_size, self.batch_size, max_context)
             sampled = temperature > 0
             if sampled:
                 logits = torch.empty(self.batch_size, VOCAB_SIZE, dtype=torch.float32, device=self._dev)
                 greedy = torch.empty(self.batch_size, dtype=torch.int32, device=self._dev)
             for i in range(steps):
                 if not sampled:
-                    self._forward(log[i], self._all, pos_table[i], self._all, log[i + 1], None, self._k_cache,
-                                  self._v_cache, max_context)
+                    self._forward.decode(log[i], pos_table[i], log[i + 1], None, self._k_cache, self._v_cache,
+                                         max_context)
                     continue
-                self._forward(log[i], self._all, pos_table[i], self._all, greedy, logits, self._k_cache,
-                              self._v_cache, max_context)
+                self._forward.decode(log[i], pos_table[i], greedy, logits, self._k_cache, self._v_cache,
+                                     max_context)
                 self._ops.sample(logits, float(temperature), int(top_k), float(top_p), int(seed),
                                  self._counters(pos_table[i]), log[i + 1])
             self._positions = [p + steps for p in self._positions]

@@ -309,3 +309,89 @@ def test_batched_forward_deterministic(weights_gpu):
         dec = _decoder(weights_gpu, num_layers=4, max_seq_len=128)
         outs.append(_forward_rows(dec._forward, ids, 0, dec._k_cache, dec._v_cache)[1])
     assert torch.equal(outs[0], outs[1])
+
+
+def test_decode_batch_16_sequences(shape, weights_cpu, weights_gpu):
+    """A full 16-row MFMA tile of the fused decode step: 16 sequences, 2 layers, each row against its
+    own oracle for three teacher-forced steps."""
+    from oracle.qwen3_ref import OracleDecoder
+    from qwen_megakernel_amd.model import BatchDecoder
+    from qwen_megakernel_amd.weights import make_prompt
+
+    B, layers = 16, 2
+    prompts = [make_prompt(3 + b, shape.vocab, seed=40 + b) for b in range(B)]
+    bd = BatchDecoder(weights=weights_gpu, batch_size=B, max_seq_len=128, num_layers=layers, verbose=False)
+    orcs = [OracleDecoder(weights_cpu, shape, num_layers=layers, max_seq_len=128) for _ in range(B)]
+    nxt = []
+    for b, p in enumerate(prompts):
+        ref = _oracle_feed(orcs[b], p)
+        tok, lg = bd.prefill(b, p, return_logits=True)
+        _check_step(len(p) - 1, lg.cpu(), ref["logits"][-1], tok, ref["tokens"][-1], ref["gaps"][-1])
+        nxt.append(ref["tokens"][-1])
+    for s in range(3):
+        toks, logits = bd.step_logits(nxt)
+        refs = [_oracle_feed(orcs[b], [nxt[b]]) for b in range(B)]
+        for b in range(B):
+            _check_step(s, logits[b].cpu(), refs[b]["logits"][0], toks[b], refs[b]["tokens"][0], refs[b]["gaps"][0])
+        nxt = [r["tokens"][0] for r in refs]
+
+
+def test_decode_batch_long_context_general_path(shape, weights_cpu, weights_gpu):
+    """Contexts beyond the fused step's 4096 positions take the general path (split attention); two
+    sequences after injected N(0,1) caches of 5000 and 4200 positions, 2 layers."""
+    from oracle.qwen3_ref import OracleDecoder
+    from qwen_megakernel_amd.model import BatchDecoder
+    from qwen_megakernel_amd.weights import make_kv_prefill
+
+    layers, max_seq = 2, 5100
+    wc = _with_rope(weights_cpu, max_seq, "cpu")
+    wg = _with_rope(weights_gpu, max_seq, "cuda")
+    bd = BatchDecoder(weights=wg, batch_size=2, max_seq_len=max_seq, num_layers=layers, verbose=False)
+    orcs = []
+    for b, c0 in enumerate((5000, 4200)):
+        k, v = make_kv_prefill(shape, c0, seed=2 + b)
+        orc = OracleDecoder(wc, shape, num_layers=layers, max_seq_len=max_seq)
+        orc.load_kv(k, v, c0)
+        orcs.append(orc)
+        bd.load_kv(b, k.cuda(), v.cuda(), c0)
+    nxt = [11, 22]
+    for s in range(2):
+        toks, logits = bd.step_logits(nxt)
+        refs = [_oracle_feed(orcs[b], [nxt[b]]) for b in range(2)]
+        for b in range(2):
+            _check_step(s, logits[b].cpu(), refs[b]["logits"][0], toks[b], refs[b]["tokens"][0], refs[b]["gaps"][0])
+        nxt = [r["tokens"][0] for r in refs]
+
+
+def test_decode_batch_equals_general_forward(weights_gpu):
+    """The fused decode step and forward_tokens (general path) on the same inputs: same tokens
+    wherever the logits' top two are not within rounding, logits within the same bar."""
+    from qwen_megakernel_amd.model import BatchDecoder
+    from qwen_megakernel_amd.weights import make_prompt
+
+    bd = BatchDecoder(weights=weights_gpu, batch_size=4, max_seq_len=256, verbose=False)
+    for b in range(4):
+        bd.prefill(b, make_prompt(5 + 3 * b, V, seed=60 + b))
+    k0, v0 = bd._k_cache.clone(), bd._v_cache.clone()
+    toks = _i32([1, 2, 3, 4])
+    pos = _i32(bd.positions)
+    out_a = torch.empty(4, dtype=torch.int32, device="cuda")
+    lg_a = torch.empty(4, V, dtype=torch.float32, device="cuda")
+    bd._forward.decode(toks, pos, out_a, lg_a, bd._k_cache, bd._v_cache, 64)
+    ka = bd._k_cache.clone()
+    bd._k_cache.copy_(k0)
+    bd._v_cache.copy_(v0)
+    out_b = torch.empty(4, dtype=torch.int32, device="cuda")
+    lg_b = torch.empty(4, V, dtype=torch.float32, device="cuda")
+    ar = torch.arange(4, dtype=torch.int32, device="cuda")
+    bd._forward(toks, ar, pos, ar, out_b, lg_b, bd._k_cache, bd._v_cache, 64)
+    for b in range(4):
+        cos = torch.nn.functional.cosine_similarity(lg_a[b].double(), lg_b[b].double(), dim=0).item()
+        assert cos >= COS_MIN and (lg_a[b] - lg_b[b]).abs().max().item() <= ABS_MAX
+    # the appended K rows agree up to rounding: layer 0 within 0.05 (one or two bf16 ulps of its
+    # values), every layer's rows with cosine >= 0.999 (deeper layers carry the summation-order noise)
+    d = (ka[:, 0].float() - bd._k_cache[:, 0].float()).abs().max().item()
+    assert d <= 0.05, d
+    cos = torch.nn.functional.cosine_similarity(ka.float().flatten().double(),
+                                                bd._k_cache.float().flatten().double(), dim=0).item()
+    assert cos >= 0.999, cos
