@@ -612,6 +612,83 @@ __global__ void __launch_bounds__(256) lm_head_gemm(const uint16_t* __restrict__
   }
 }
 
+// LM head for at most 16 emitted rows, streamed by a persistent grid: 256
+// workgroups of 8 waves; wave g takes the 16-column vocabulary tiles g, g+2048,
+// ... (4 or 5 each, so every CU streams within 8% of the mean), walking them as
+// one sequence of 64-K steps with kLmDepth steps of weights in flight across
+// tile boundaries.  The emitted rows sit in LDS.  Each wave keeps its best key
+// per row; keys_reduce takes the best over the 2048 waves.
+constexpr int kLmWaves = 8, kLmBlocks = 256, kLmDepth = 4;
+
+__global__ void __launch_bounds__(kLmWaves * 64) lm_head_stream(const uint16_t* __restrict__ X,
+                                                                const int* __restrict__ rows, int R,
+                                                                const uint16_t* __restrict__ W, int K, int V,
+                                                                unsigned long long* __restrict__ keys_part,
+                                                                float* __restrict__ logits) {
+  extern __shared__ __align__(16) uint16_t xl[];  // [R][K]
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  for (int i = threadIdx.x; i < R * K / 8; i += kLmWaves * 64) {
+    const int r = (i * 8) / K, k = (i * 8) % K;
+    *reinterpret_cast<u32x4*>(xl + r * K + k) = ld16(X + (size_t)max(rows[r], 0) * K + k);
+  }
+  const int nw = gridDim.x * kLmWaves, gw = blockIdx.x * kLmWaves + wave;
+  const int ntiles = V / 16, KS = K / 64;
+  const int mine = gw < ntiles ? (ntiles - gw + nw - 1) / nw : 0;
+  const int nsteps = mine * KS;
+  const int kq = 8 * (lane >> 4);
+  const int row = min(lane & 15, R - 1);
+  auto wptr = [&](int step) {
+    return W + (size_t)((gw + (step / KS) * nw) * 16 + (lane & 15)) * K + kq + (step % KS) * 64;
+  };
+  bf16x8 buf[kLmDepth][2];
+#pragma unroll
+  for (int u = 0; u < kLmDepth; u++)
+    if (u < nsteps) {
+      buf[u][0] = ld_bf16x8_stream(wptr(u));
+      buf[u][1] = ld_bf16x8_stream(wptr(u) + 32);
+    }
+  __syncthreads();
+  unsigned long long best[4] = {0, 0, 0, 0};
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int s0 = 0; s0 < nsteps; s0 += kLmDepth) {
+#pragma unroll
+    for (int u = 0; u < kLmDepth; u++) {
+      const int step = s0 + u;
+      if (step < nsteps) {
+        const int k = (step % KS) * 64;
+        const bf16x8 a0 = *reinterpret_cast<const bf16x8*>(xl + row * K + kq + k);
+        const bf16x8 a1 = *reinterpret_cast<const bf16x8*>(xl + row * K + kq + k + 32);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, buf[u][0], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, buf[u][1], acc, 0, 0, 0);
+        if (step + kLmDepth < nsteps) {
+          buf[u][0] = ld_bf16x8_stream(wptr(step + kLmDepth));
+          buf[u][1] = ld_bf16x8_stream(wptr(step + kLmDepth) + 32);
+        }
+        if (step % KS == KS - 1) {  // the tile is complete
+          const int n = (gw + (step / KS) * nw) * 16 + (lane & 15);
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            const int t = 4 * (lane >> 4) + i;
+            const uint32_t hb = f32_to_bf16(acc[i]);
+            if (logits && t < R) logits[(size_t)t * V + n] = bf16_to_f32(hb);
+            best[i] = key_max(best[i], ((unsigned long long)orderable16(hb) << 32) |
+                                           (unsigned long long)(0xffffffffu - (uint32_t)n));
+          }
+          acc = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    unsigned long long b = best[i];
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) b = key_max(b, __shfl_xor(b, o));
+    const int t = 4 * (lane >> 4) + i;
+    if ((lane & 15) == 0 && t < R) keys_part[(size_t)t * nw + gw] = b;
+  }
+}
+
 // out[r] = token of row r's largest key over the LM head's tiles (-1 for an
 // invalid emit row or token).  One workgroup per row.
 __global__ void __launch_bounds__(256) keys_reduce(const unsigned long long* __restrict__ keys_part, int ntiles,
@@ -669,7 +746,7 @@ constexpr size_t rows_lds(int T, int K) {
   return (NORM ? (size_t)((T * K * 2 + 15) / 16 * 16) : 0) + (size_t)NW * 16 * 16 * NB * 4 + (size_t)NW * 16 * 4 + 64;
 }
 
-template <int NB, int EPI, bool NORM, int NW, int ITERS>
+template <int NB, int EPI, bool NORM, int NW, int ITERS, int MAXT>
 __global__ void __launch_bounds__(NW * 64) gemm_rows(const uint16_t* __restrict__ X, const uint16_t* __restrict__ norm_w,
                                                      float eps, int T, int K, Seg seg, uint16_t* __restrict__ Y,
                                                      int ldy) {
@@ -685,40 +762,79 @@ __global__ void __launch_bounds__(NW * 64) gemm_rows(const uint16_t* __restrict_
   const int kq = 8 * (lane >> 4);
   const int k0 = w * (64 * ITERS);
   const int row = min(lane & 15, T - 1);
-  // the wave's whole weight slice is requested first: it streams while the prologue runs
+  // NORM: the T input rows in 16-byte chunks (chunk c = thread + NT * q covers row 8c / K) and
+  // their norm weights are requested first, then the wave's whole weight slice, so that waiting
+  // for the rows (vector memory returns in order) never waits for the weights
+  constexpr int NT = NW * 64, MAXQ = NORM ? (MAXT * kMaxRowsH / 8 + NT - 1) / NT : 1;  // T <= MAXT
+  const int nchunks = T * K / 8;
+  u32x4 xr[MAXQ], wr[MAXQ];
+  if (NORM) {
+#pragma unroll
+    for (int q = 0; q < MAXQ; q++) {
+      const int c = threadIdx.x + NT * q;
+      if (c < nchunks) {
+        xr[q] = ld16(X + (size_t)c * 8);
+        wr[q] = ld16(norm_w + (c * 8) % K);
+      }
+    }
+  }
   bf16x8 b[ITERS][2][NB];
 #pragma unroll
   for (int j = 0; j < NB; j++) {
-    const uint16_t* wr = tile_row<EPI, NC>(seg, tile, 16 * j + (lane & 15), K) + kq + k0;
+    const uint16_t* wrow = tile_row<EPI, NC>(seg, tile, 16 * j + (lane & 15), K) + kq + k0;
 #pragma unroll
     for (int it = 0; it < ITERS; it++) {
-      b[it][0][j] = ld_bf16x8_stream(wr + 64 * it);
-      b[it][1][j] = ld_bf16x8_stream(wr + 64 * it + 32);
+      b[it][0][j] = ld_bf16x8_stream(wrow + 64 * it);
+      b[it][1][j] = ld_bf16x8_stream(wrow + 64 * it + 32);
     }
   }
   if (NORM) {
-    // RMSNorm of the T input rows into LDS: bf16(w * bf16(x * rstd)), as HF
-    for (int t = 0; t < T; t++) {
-      float part = 0.f;
-      for (int i = threadIdx.x; i < K; i += NW * 64) {
-        const float v = bf16_to_f32(X[(size_t)t * K + i]);
-        part += v * v;
+    // RMSNorm of the rows into LDS, bf16(w * bf16(x * rstd)) as HF.  A wave's 64 chunks of one q
+    // lie in one row (K / 8 is a multiple of 64), so each wave sum belongs to one row.
+    float (*ssq)[NW] = reinterpret_cast<float (*)[NW]>(&ssr[0][0]);  // [MAXQ][NW] <= [16][NW]
+#pragma unroll
+    for (int q = 0; q < MAXQ; q++) {
+      const int c0 = w * 64 + NT * q;  // the wave's first chunk of this q
+      if (c0 < nchunks) {
+        float part = 0.f;
+        const u32x4 v = xr[q];
+        const uint32_t u4[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          const float lo = lo_bf16(u4[e]), hi = hi_bf16(u4[e]);
+          part += lo * lo + hi * hi;
+        }
+        part = wave_sum(part);
+        if (lane == 0) ssq[q][w] = part;
       }
-      part = wave_sum(part);
-      if (lane == 0) ssr[w][t] = part;
     }
     __syncthreads();
     if ((int)threadIdx.x < T) {
+      // row t's wave sums, in (q, wave) order
       float ss = 0.f;
-      for (int q = 0; q < NW; q++) ss += ssr[q][threadIdx.x];
+      for (int q = 0; q < MAXQ; q++)
+        for (int ww = 0; ww < NW; ww++) {
+          const int c0 = ww * 64 + NT * q;
+          if (c0 < nchunks && (c0 * 8) / K == (int)threadIdx.x) ss += ssq[q][ww];
+        }
       rstd_s[threadIdx.x] = rcp_sqrt_torch(__fdiv_rn(ss, (float)K) + eps);
     }
     __syncthreads();
-    for (int t = 0; t < T; t++) {
-      const float r = rstd_s[t];
-      for (int i = threadIdx.x; i < K; i += NW * 64) {
-        const float v = bf16_to_f32(X[(size_t)t * K + i]);
-        xs[t * K + i] = (uint16_t)f32_to_bf16(bf16r(bf16_to_f32(ldu16(norm_w + i)) * bf16r(v * r)));
+#pragma unroll
+    for (int q = 0; q < MAXQ; q++) {
+      const int c = threadIdx.x + NT * q;
+      if (c < nchunks) {
+        const float r = rstd_s[(c * 8) / K];
+        const uint32_t xv[4] = {xr[q].x, xr[q].y, xr[q].z, xr[q].w};
+        const uint32_t wv[4] = {wr[q].x, wr[q].y, wr[q].z, wr[q].w};
+        uint32_t o[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          const float n0 = bf16r(lo_bf16(wv[e]) * bf16r(lo_bf16(xv[e]) * r));
+          const float n1 = bf16r(hi_bf16(wv[e]) * bf16r(hi_bf16(xv[e]) * r));
+          o[e] = f32_to_bf16(n0) | (f32_to_bf16(n1) << 16);
+        }
+        *reinterpret_cast<u32x4*>(xs + (size_t)c * 8) = u32x4{o[0], o[1], o[2], o[3]};
       }
     }
     __syncthreads();
@@ -1019,7 +1135,7 @@ Layout layout(int T, int R, int max_context, bool one_per_seq = false) {
   };
   take(l.tok, (size_t)T * sizeof(Tok));
   take(l.erow, (size_t)R * 4);
-  take(l.keys, (size_t)R * kLmTiles(Dm::V) * 8);
+  take(l.keys, (size_t)R * std::max(kLmTiles(Dm::V), kLmBlocks * kLmWaves) * 8);
   take(l.x, (size_t)T * Dm::H * 2);
   take(l.n, (size_t)T * Dm::H * 2);
   take(l.q, (size_t)T * kQS * 2);
@@ -1059,21 +1175,48 @@ struct Args {
   char* ws;
 };
 
+// LM head + argmax of R emitted rows: the streamed persistent form for R <= 16,
+// the tiled GEMM above that.
+template <class M>
+void launch_lm_head(const uint16_t* N, const int* erow, int R, const uint16_t* W, unsigned long long* keys,
+                    float* logits, const Tok* tok, int* out, hipStream_t s) {
+  using Dm = Dims<M>;
+  if (R <= 16) {
+    const size_t lds = (size_t)R * Dm::H * 2;
+    hipLaunchKernelGGL(lm_head_stream, dim3(kLmBlocks), dim3(kLmWaves * 64), lds, s, N, erow, R, W, Dm::H, Dm::V,
+                       keys, logits);
+    hipLaunchKernelGGL(keys_reduce, dim3(R), dim3(256), 0, s, keys, kLmBlocks * kLmWaves, erow, tok, out);
+    return;
+  }
+  const int lm_waves = ((R + 15) / 16) * kLmTiles(Dm::V);
+  hipLaunchKernelGGL(lm_head_gemm, dim3((lm_waves + 3) / 4), dim3(256), 0, s, N, erow, R, W, Dm::H, Dm::V, keys,
+                     logits);
+  hipLaunchKernelGGL(keys_reduce, dim3(R), dim3(256), 0, s, keys, kLmTiles(Dm::V), erow, tok, out);
+}
+
 // gemm_rows over `tiles` 16-column tiles (NB = 1), NW waves each taking
 // K / NW = 64 * ITERS of the K range; ITERS picked from K.
-template <int EPI, bool NORM, int NW, int ITERS>
-void launch_rows_it(int tiles, const uint16_t* X, const uint16_t* nw, float eps, int T, int K, const Seg& seg,
-                    uint16_t* Y, int ldy, hipStream_t s) {
+template <int EPI, bool NORM, int NW, int ITERS, int MAXT>
+void launch_rows_t(int tiles, const uint16_t* X, const uint16_t* nw, float eps, int T, int K, const Seg& seg,
+                   uint16_t* Y, int ldy, hipStream_t s) {
   const size_t lds = rows_lds<1, NW, NORM>(T, K);
   if (lds > 64 * 1024) {
     // 16 normalised rows of 2048: above the default dynamic LDS limit (gfx950 has 160 KB per CU)
     static bool raised = false;
     if (!raised)
-      raised = hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_rows<1, EPI, NORM, NW, ITERS>),
+      raised = hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_rows<1, EPI, NORM, NW, ITERS, MAXT>),
                                    hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024) == hipSuccess;
   }
-  hipLaunchKernelGGL((gemm_rows<1, EPI, NORM, NW, ITERS>), dim3(tiles), dim3(NW * 64), lds, s, X, nw, eps, T, K, seg,
-                     Y, ldy);
+  hipLaunchKernelGGL((gemm_rows<1, EPI, NORM, NW, ITERS, MAXT>), dim3(tiles), dim3(NW * 64), lds, s, X, nw, eps, T,
+                     K, seg, Y, ldy);
+}
+
+// NORM kernels stage the rows in registers sized for T <= 4 (the common batch) or T <= 16.
+template <int EPI, bool NORM, int NW, int ITERS>
+void launch_rows_it(int tiles, const uint16_t* X, const uint16_t* nw, float eps, int T, int K, const Seg& seg,
+                    uint16_t* Y, int ldy, hipStream_t s) {
+  if (!NORM || T <= 4) launch_rows_t<EPI, NORM, NW, ITERS, 4>(tiles, X, nw, eps, T, K, seg, Y, ldy, s);
+  else launch_rows_t<EPI, NORM, NW, ITERS, 16>(tiles, X, nw, eps, T, K, seg, Y, ldy, s);
 }
 
 template <int EPI, bool NORM, int NW>
@@ -1125,10 +1268,7 @@ int forward_fused(const Args& a, hipStream_t s) {
     launch_rows<kEpiResidual, false, 16>(Dm::H / 16, MM, nullptr, eps, T, Dm::I, dn, X, Dm::H, s);
   }
   hipLaunchKernelGGL((residual_norm<Dm::H>), dim3(T), dim3(1024), 0, s, nullptr, 0, T, X, a.final_norm, eps, N);
-  const int lm_waves = ((R + 15) / 16) * kLmTiles(Dm::V);
-  hipLaunchKernelGGL(lm_head_gemm, dim3((lm_waves + 3) / 4), dim3(256), 0, s, N, erow, R, a.lm_head, Dm::H, Dm::V,
-                     keys, a.logits);
-  hipLaunchKernelGGL(keys_reduce, dim3(R), dim3(256), 0, s, keys, kLmTiles(Dm::V), erow, tok, a.out_tokens);
+  launch_lm_head<M>(N, erow, R, a.lm_head, keys, a.logits, tok, a.out_tokens, s);
   return hipGetLastError() == hipSuccess ? QMK_OK : QMK_ERR_HIP;
 }
 
@@ -1188,10 +1328,7 @@ int forward(const Args& a, hipStream_t s) {
     const uint16_t* next_norm = L + 1 < a.num_layers ? u16(a.layers[L + 1].input_layernorm_weight) : a.final_norm;
     hipLaunchKernelGGL((residual_norm<Dm::H>), dim3(T), dim3(1024), 0, s, part, ks, T, X, next_norm, eps, N);
   }
-  const int lm_waves = ((R + 15) / 16) * kLmTiles(Dm::V);
-  hipLaunchKernelGGL(lm_head_gemm, dim3((lm_waves + 3) / 4), dim3(256), 0, s, N, erow, R, a.lm_head, Dm::H, Dm::V,
-                     keys, a.logits);
-  hipLaunchKernelGGL(keys_reduce, dim3(R), dim3(256), 0, s, keys, kLmTiles(Dm::V), erow, tok, a.out_tokens);
+  launch_lm_head<M>(N, erow, R, a.lm_head, keys, a.logits, tok, a.out_tokens, s);
   return hipGetLastError() == hipSuccess ? QMK_OK : QMK_ERR_HIP;
 }
 
