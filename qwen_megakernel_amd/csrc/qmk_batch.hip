@@ -727,6 +727,7 @@ __global__ void __launch_bounds__(256) keys_reduce(const unsigned long long* __r
 constexpr int kRowWaves = 16;
 constexpr int kMaxRowsH = 2048;   // largest hidden size a NORM prologue stages in LDS
 constexpr int kFusedCtx = 4096;   // longest context of the fused decode attention
+constexpr int kAttnRounds = 4;    // fused attention: 64-position rounds of K or V loads in flight per wave
 
 enum RowEpi : int { kEpiStore = 0, kEpiResidual = 1, kEpiSiluMul = 2 };
 
@@ -948,17 +949,17 @@ __global__ void __launch_bounds__(1024) attention_fused(const uint16_t* __restri
 #pragma unroll
   for (int h = 0; h < 2; h++) qv[h] = *reinterpret_cast<const u32x4*>(&qs[h][8 * t16]);
   const u32x4 k_now = *reinterpret_cast<const u32x4*>(&kn[8 * t16]);
-  // scores: each 16-lane row one position, 64 per round, four rounds in flight
+  // scores: each 16-lane row one position, 64 per round, kAttnRounds rounds in flight
   float m0 = -INFINITY, m1 = -INFINITY;
-  for (int p0 = 4 * w + slot; p0 < C; p0 += 4 * 64) {
-    u32x4 kx[4];
+  for (int p0 = 4 * w + slot; p0 < C; p0 += kAttnRounds * 64) {
+    u32x4 kx[kAttnRounds];
 #pragma unroll
-    for (int u = 0; u < 4; u++) {
+    for (int u = 0; u < kAttnRounds; u++) {
       const int p = p0 + 64 * u;
       kx[u] = (p < C && p != pos) ? ld16(kc + (size_t)p * kD + 8 * t16) : k_now;
     }
 #pragma unroll
-    for (int u = 0; u < 4; u++) {
+    for (int u = 0; u < kAttnRounds; u++) {
       const int p = p0 + 64 * u;
       if (p < C) {
         const float s0 = bf16r(bf16r(row16_sum(dot8(kx[u], qv[0], 0.f))) * scale);
@@ -1009,20 +1010,20 @@ __global__ void __launch_bounds__(1024) attention_fused(const uint16_t* __restri
   }
   __syncthreads();
   // P @ V: each 16-lane row takes one position (lane t16: dims 8*t16..+7 of both heads), 64 per
-  // round, four rounds in flight; then the four rows of a wave and the 16 waves are summed in order
+  // round, kAttnRounds rounds in flight; then the four rows of a wave and the 16 waves are summed in order
   const u32x4 v_now = *reinterpret_cast<const u32x4*>(&vn[8 * t16]);
   float acc0[8], acc1[8];
 #pragma unroll
   for (int i = 0; i < 8; i++) acc0[i] = acc1[i] = 0.f;
-  for (int p0 = 4 * w + slot; p0 < C; p0 += 4 * 64) {
-    u32x4 vx[4];
+  for (int p0 = 4 * w + slot; p0 < C; p0 += kAttnRounds * 64) {
+    u32x4 vx[kAttnRounds];
 #pragma unroll
-    for (int u = 0; u < 4; u++) {
+    for (int u = 0; u < kAttnRounds; u++) {
       const int p = p0 + 64 * u;
       vx[u] = (p < C && p != pos) ? ld16(vc + (size_t)p * kD + 8 * t16) : v_now;
     }
 #pragma unroll
-    for (int u = 0; u < 4; u++) {
+    for (int u = 0; u < kAttnRounds; u++) {
       const int p = p0 + 64 * u;
       if (p < C) {
         const float pa = sc[0][p], pb = sc[1][p];
