@@ -209,7 +209,8 @@ def qwen3_1p7b(steps: int = 256, prompt_len: int = 512, batch: int = 4):
                      "bytes_per_step": int(byts_b), "achieved_GBps": round(byts_b / tb / 1e9, 1),
                      "roofline_frac": round(byts_b / tb / 1e9 / PEAK_HBM_GBS, 4),
                      "prefill_ms": round(prefill_s * 1e3, 2),
-                     "path": "batched forward: MFMA GEMMs + split-context attention, one launch sequence per step"}
+                     "path": "decode_batch: 5 launches per layer (norm-prologue / residual- and SiLU-epilogue "
+                             "K-split MFMA GEMMs, fused attention), streamed LM head"}
     return out
 
 
