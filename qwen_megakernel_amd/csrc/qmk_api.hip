@@ -120,9 +120,9 @@ int check_device(int dev, DevInfo** out) {
   hipDeviceProp_t prop;
   if (hipGetDeviceProperties(&prop, dev) != hipSuccess) return QMK_ERR_HIP;
   int occ = 0, occ17 = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, reinterpret_cast<const void*>(decode_kernel<Qwen3_0_6B>), kBlock,
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, reinterpret_cast<const void*>(decode_kernel<Qwen3_0_6B, false>), kBlock,
                                                    0) != hipSuccess ||
-      hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ17, reinterpret_cast<const void*>(decode_kernel<Qwen3_1_7B>), kBlock,
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ17, reinterpret_cast<const void*>(decode_kernel<Qwen3_1_7B, false>), kBlock,
                                                    0) != hipSuccess)
     return QMK_ERR_HIP;
   if (prop.multiProcessorCount < kNumWG || occ < 1 || occ17 < 1) return QMK_ERR_DEVICE;
@@ -238,10 +238,14 @@ KArgs make_args(const Common& c, Ctx* ctx) {
 }
 
 int launch(const KArgs& a, int model, hipStream_t stream) {
-  if (model == QMK_MODEL_QWEN3_1_7B)
-    hipLaunchKernelGGL(decode_kernel<Qwen3_1_7B>, dim3(kNumWG), dim3(kBlock), 0, stream, a);
-  else
-    hipLaunchKernelGGL(decode_kernel<Qwen3_0_6B>, dim3(kNumWG), dim3(kBlock), 0, stream, a);
+  const bool sampled = a.temperature > 0.f;
+  if (model == QMK_MODEL_QWEN3_1_7B) {
+    if (sampled) hipLaunchKernelGGL((decode_kernel<Qwen3_1_7B, true>), dim3(kNumWG), dim3(kBlock), 0, stream, a);
+    else hipLaunchKernelGGL((decode_kernel<Qwen3_1_7B, false>), dim3(kNumWG), dim3(kBlock), 0, stream, a);
+  } else {
+    if (sampled) hipLaunchKernelGGL((decode_kernel<Qwen3_0_6B, true>), dim3(kNumWG), dim3(kBlock), 0, stream, a);
+    else hipLaunchKernelGGL((decode_kernel<Qwen3_0_6B, false>), dim3(kNumWG), dim3(kBlock), 0, stream, a);
+  }
   return hipGetLastError() == hipSuccess ? QMK_OK : QMK_ERR_HIP;
 }
 
@@ -331,6 +335,12 @@ int generate_impl(const Common& c, int first_token_id, int num_steps, int eos, i
   KArgs a = make_args(c, ctx);
   a.position = -1;
   a.out_log = ctx->log;
+  if (sp && sp->temperature > 0.f && sp->top_k <= 0 && !(sp->top_p > 0.f && sp->top_p < 1.f)) {
+    // temperature only: the draw is the decode kernel's own LM-head argmax over perturbed scores
+    a.temperature = sp->temperature;
+    a.seed = sp->seed;
+    sp = nullptr;
+  }
   if (sp) {
     if (!ctx->logits && hipMalloc(&ctx->logits, (size_t)Dm::V * sizeof(float)) != hipSuccess) return fail(QMK_ERR_HIP);
     a.logits = ctx->logits;

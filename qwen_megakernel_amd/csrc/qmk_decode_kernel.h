@@ -52,6 +52,7 @@
 #include <stdint.h>
 
 #include "qmk_device.h"
+#include "qmk_sample.h"
 #include "qmk_state.h"
 
 namespace qmk {
@@ -168,6 +169,8 @@ struct KArgs {
   int token;
   float attn_scale;
   float rms_eps;
+  float temperature;       // > 0: the step's token is a Gumbel-max draw from softmax(logits / temperature)
+  uint64_t seed;           //      with the random numbers of (seed, position); 0: greedy
   uint32_t timeout;
   int xcd_local;           // 1: XCD-local exchanges stay in the XCD's L2
 };
@@ -779,18 +782,20 @@ __device__ __forceinline__ void control_path(const KArgs& a, Smem<M>& s, const S
 #pragma unroll
     for (int cc = 0; cc < kComputeWaves; cc++) best = s.best[cc] > best ? s.best[cc] : best;
     const uint32_t idx = 0xffffffffu - (uint32_t)best;
+    const uint32_t score32 = (uint32_t)(best >> 32);
     u32x4 d;
-    d.x = word((uint32_t)(best >> 32) & 0xffffu, tk);
+    d.x = word(score32 >> 16, tk);
     d.y = word(idx & 0xffffu, tk);
     d.z = word(idx >> 16, tk);
-    d.w = word(0, tk);
+    d.w = word(score32 & 0xffffu, tk);
     put4<true>(a.x, Dm::X_KEY + 4 * b, d);
   }
   if (b == 0) {
     uint64_t best = 0;
     const bool ok = ctl.template gather_range<kNumWG * 4>(Dm::X_KEY, tk, [&](int ci, u32x4 v) {
       const uint32_t idx = (v.y >> 16) | (v.z & 0xffff0000u);
-      const uint64_t key = ((uint64_t)(v.x >> 16) << 32) | (uint64_t)(0xffffffffu - idx);
+      const uint32_t score32 = (v.x & 0xffff0000u) | (v.w >> 16);
+      const uint64_t key = ((uint64_t)score32 << 32) | (uint64_t)(0xffffffffu - idx);
       best = key > best ? key : best;
     });
     stamp(p.nl * kTracePoints + 2);
@@ -814,7 +819,7 @@ __device__ __forceinline__ void control_path(const KArgs& a, Smem<M>& s, const S
   }
 }
 
-template <class M>
+template <class M, bool SAMPLED>
 __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const Step& p, int b, int c, int lane) {
   using Dm = Dims<M>;
   const int xcd = b & (kGroups - 1), r = b >> 3;
@@ -1130,6 +1135,9 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
         load_row(buf[u], a.lm_head + (size_t)row_of(i) * Dm::H, 0, lane);
       }
     };
+    // key = score32 << 32 | ~row: score32 = orderable bf16 logit << 16 (greedy, the first index of
+    // the maximum) or the order-preserving key of logit / T + Gumbel noise (a draw)
+    const uint64_t base = SAMPLED ? draw_base(a.seed, (uint64_t)p.pos) : 0;
     auto do_batch = [&](u32x4 (&buf)[Dm::LM_U][Dm::LH], int i0) {
 #pragma unroll
       for (int u = 0; u < Dm::LM_U; u++) {
@@ -1137,7 +1145,10 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
         if (i0 + u < nmine) {
           const int row = row_of(i0 + u);
           const uint32_t hb = f32_to_bf16(v);
-          const uint64_t key = ((uint64_t)orderable16(hb) << 32) | (uint64_t)(0xffffffffu - (uint32_t)row);
+          uint32_t score32;
+          if constexpr (SAMPLED) score32 = gumbel_key(bf16_to_f32(hb), a.temperature, base, row);
+          else score32 = orderable16(hb) << 16;
+          const uint64_t key = ((uint64_t)score32 << 32) | (uint64_t)(0xffffffffu - (uint32_t)row);
           best = key > best ? key : best;
           if (a.logits && lane == 0) a.logits[row] = bf16_to_f32(hb);
         }
@@ -1155,7 +1166,9 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
   QMK_SYNC();  // final b
 }
 
-template <class M>
+// SAMPLED: the LM-head keys are Gumbel-perturbed (temperature sampling, KArgs::temperature > 0);
+// a separate instantiation so the greedy kernel carries none of it.
+template <class M, bool SAMPLED = false>
 __global__ void __launch_bounds__(kBlock, 1) decode_kernel(KArgs a) {
   using Dm = Dims<M>;
   __shared__ Smem<M> s;
@@ -1219,7 +1232,7 @@ __global__ void __launch_bounds__(kBlock, 1) decode_kernel(KArgs a) {
   if (wave == 0)
     control_path<M>(a, s, p, b, lane);
   else
-    compute_path<M>(a, s, p, b, wave - 1, lane);
+    compute_path<M, SAMPLED>(a, s, p, b, wave - 1, lane);
 }
 
 #undef QMK_SYNC

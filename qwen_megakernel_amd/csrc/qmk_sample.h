@@ -12,6 +12,36 @@
 
 namespace qmk {
 
+// SplitMix64 finaliser with its golden-ratio increment (G. Steele, D. Lea,
+// C. Flood, "Fast splittable pseudorandom number generators", OOPSLA 2014).
+__device__ __forceinline__ uint64_t mix64(uint64_t z) {
+  z += 0x9E3779B97F4A7C15ull;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+// Per-draw base of the random numbers: (seed, counter).
+__device__ __forceinline__ uint64_t draw_base(uint64_t seed, uint64_t counter) { return mix64(seed ^ mix64(counter)); }
+
+// U in (0, 1) for token v: the top 24 bits of the hash, centred in their interval.
+__device__ __forceinline__ float draw_uniform(uint64_t base, int v) {
+  const uint64_t h = mix64(base + (uint64_t)(uint32_t)v);
+  return ((float)(uint32_t)(h >> 40) + 0.5f) * (1.0f / 16777216.0f);
+}
+
+// Order-preserving uint32 key of a float.
+__device__ __forceinline__ uint32_t key32(float f) {
+  const uint32_t u = __float_as_uint(f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// Key of token v's Gumbel-perturbed score: key32(logit / T + G), G = -log(-log(U)).
+__device__ __forceinline__ uint32_t gumbel_key(float logit, float temperature, uint64_t base, int v) {
+  const float s = __fdiv_rn(logit, temperature);
+  return key32(s + -logf(-logf(draw_uniform(base, v))));
+}
+
 struct SampleParams {
   float temperature;  // <= 0: greedy (first index of the maximum)
   int top_k;          // keep scores >= the top_k-th largest; <= 0 or >= vocab: off

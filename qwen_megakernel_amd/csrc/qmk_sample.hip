@@ -28,24 +28,6 @@ constexpr int kThreads = 1024;
 constexpr int kWaves = kThreads / 64;
 constexpr double kFix = 1099511627776.0;  // 2^40
 
-__device__ __forceinline__ uint64_t mix64(uint64_t z) {
-  z += 0x9E3779B97F4A7C15ull;
-  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
-  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
-  return z ^ (z >> 31);
-}
-
-// U in (0, 1): the top 24 bits of the hash, centred in their interval
-__device__ __forceinline__ float uniform(uint64_t base, int v) {
-  const uint64_t h = mix64(base + (uint64_t)(uint32_t)v);
-  return ((float)(uint32_t)(h >> 40) + 0.5f) * (1.0f / 16777216.0f);
-}
-
-__device__ __forceinline__ uint32_t key32(float f) {
-  const uint32_t u = __float_as_uint(f);
-  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
-
 __device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v) {
   for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
   return v;
@@ -186,13 +168,12 @@ __device__ int sample_row(const float* x, int V, const SampleParams& sp, uint64_
 
   // ---- Gumbel-max draw over the kept scores
   const uint32_t kkeep = kmin > pmin ? kmin : pmin;
-  const uint64_t base = mix64(sp.seed ^ mix64(counter));
+  const uint64_t base = draw_base(sp.seed, counter);
   unsigned long long best = 0;
   for (int v = threadIdx.x; v < V; v += kThreads) {
-    const float s = score(v);
-    if (key32(s) < kkeep) continue;
-    const float g = -logf(-logf(uniform(base, v)));
-    const unsigned long long k = ((unsigned long long)key32(s + g) << 32) | (0xffffffffu - (uint32_t)v);
+    if (key32(score(v)) < kkeep) continue;
+    const unsigned long long k = ((unsigned long long)gumbel_key(x[v], T, base, v) << 32) |
+                                 (0xffffffffu - (uint32_t)v);
     best = k > best ? k : best;
   }
   return (int)(0xffffffffu - (uint32_t)block_max_u64(best, sh));

@@ -20,7 +20,9 @@ pytestmark = pytest.mark.gpu
 
 
 def _ops():
-    return torch.ops.qwen_megakernel_C
+    from qwen_megakernel_amd.build import get_extension
+
+    return get_extension()
 
 
 def _gpu_sample(logits, T, k, p, seed, counters):
@@ -162,3 +164,19 @@ def test_batch_sampled_generate_matches_host_loop(shape, weights_gpu):
             row = lg[b].cpu().numpy()
             want = S.sample_row(row, T, k, p, seed, c)[0]
             assert out[b][i] == want or _explained(row, T, k, p, seed, c, out[b][i]), f"seq {b} step {i}"
+
+
+def test_fused_temperature_draw_equals_sampler(weights_gpu, prompt):
+    """Temperature-only sampling runs inside the decode kernel's LM-head argmax (perturbed keys);
+    with top_k = vocab (a filter that keeps everything) the loop takes the separate sampling
+    kernel instead. Same draws, so the same tokens, with and without graph replay."""
+    T, seed = 0.85, 77
+    fused = _decoder(weights_gpu).generate(prompt, 48, temperature=T, seed=seed)
+    separate = _decoder(weights_gpu).generate(prompt, 48, temperature=T, top_k=151936, seed=seed)
+    assert fused == separate
+    _ops().set_graph_launch(False)
+    try:
+        direct = _decoder(weights_gpu).generate(prompt, 48, temperature=T, seed=seed)
+    finally:
+        _ops().set_graph_launch(True)
+    assert direct == fused

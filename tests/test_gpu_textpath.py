@@ -16,7 +16,9 @@ pytestmark = pytest.mark.gpu
 
 
 def _ops():
-    return torch.ops.qwen_megakernel_C
+    from qwen_megakernel_amd.build import get_extension
+
+    return get_extension()
 
 
 def _stream(dec, prompt, n, graphs=True):
