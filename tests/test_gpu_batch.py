@@ -395,3 +395,24 @@ def test_decode_batch_equals_general_forward(weights_gpu):
     cos = torch.nn.functional.cosine_similarity(ka.float().flatten().double(),
                                                 bd._k_cache.float().flatten().double(), dim=0).item()
     assert cos >= 0.999, cos
+
+
+def test_long_prefill_tiled_gemm(shape, weights_cpu, weights_gpu):
+    """A 300-token prefill takes the LDS-tiled MFMA GEMM (128 x 128 tiles, K split across
+    workgroups): every 25th row and the last against the oracle, 2 layers."""
+    from oracle.qwen3_ref import OracleDecoder
+    from qwen_megakernel_amd.weights import make_prompt
+
+    n, layers = 300, 2
+    ids = make_prompt(n, shape.vocab, seed=13)
+    ref = _oracle_feed(OracleDecoder(weights_cpu, shape, num_layers=layers, max_seq_len=512), ids)
+    dec = _decoder(weights_gpu, num_layers=layers, max_seq_len=512)
+    emit = list(range(0, n, 25)) + [n - 1]
+    out = torch.empty(len(emit), dtype=torch.int32, device="cuda")
+    logits = torch.empty(len(emit), V, dtype=torch.float32, device="cuda")
+    dec._forward(_i32(ids), torch.zeros(n, dtype=torch.int32, device="cuda"),
+                 torch.arange(n, dtype=torch.int32, device="cuda"), _i32(emit), out, logits, dec._k_cache,
+                 dec._v_cache, n)
+    toks, lg = out.cpu().tolist(), logits.cpu()
+    for r, e in enumerate(emit):
+        _check_step(e, lg[r], ref["logits"][e], toks[r], ref["tokens"][e], ref["gaps"][e])
