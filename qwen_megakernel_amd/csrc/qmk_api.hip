@@ -10,6 +10,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstring>
 #include <map>
 #include <mutex>
@@ -48,11 +49,13 @@ struct Ctx {
   int* log = nullptr;
   bool use_graphs = true;
   hipStream_t cap = nullptr;      // private stream the graph is recorded on
-  hipGraphExec_t graph = nullptr;
-  KArgs graph_args{};
-  int graph_model = -1;
-  bool graph_sampled = false;
-  SampleParams graph_sp{};
+  struct Graph {
+    hipGraphExec_t exec = nullptr;
+    KArgs args{};
+    int model = -1;
+    bool sampled = false;
+    SampleParams sp{};
+  } graphs[2];                    // by attention form: [0] contexts <= kLongContext, [1] beyond
   float* logits = nullptr;        // sampled generate: the step's logits (float[vocab])
 };
 
@@ -120,12 +123,17 @@ int check_device(int dev, DevInfo** out) {
   hipDeviceProp_t prop;
   if (hipGetDeviceProperties(&prop, dev) != hipSuccess) return QMK_ERR_HIP;
   int occ = 0, occ17 = 0;
+  int occl = 0, occl17 = 0;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, reinterpret_cast<const void*>(decode_kernel<Qwen3_0_6B, false>), kBlock,
                                                    0) != hipSuccess ||
       hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ17, reinterpret_cast<const void*>(decode_kernel<Qwen3_1_7B, false>), kBlock,
-                                                   0) != hipSuccess)
+                                                   0) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(
+          &occl, reinterpret_cast<const void*>(decode_kernel<Qwen3_0_6B, false, true>), kBlock, 0) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(
+          &occl17, reinterpret_cast<const void*>(decode_kernel<Qwen3_1_7B, false, true>), kBlock, 0) != hipSuccess)
     return QMK_ERR_HIP;
-  if (prop.multiProcessorCount < kNumWG || occ < 1 || occ17 < 1) return QMK_ERR_DEVICE;
+  if (prop.multiProcessorCount < kNumWG || occ < 1 || occ17 < 1 || occl < 1 || occl17 < 1) return QMK_ERR_DEVICE;
   int khz = 0;
   if (hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev) == hipSuccess && khz > 0)
     di.ticks_per_s = (uint32_t)khz * 1000u;
@@ -237,14 +245,20 @@ KArgs make_args(const Common& c, Ctx* ctx) {
   return a;
 }
 
-int launch(const KArgs& a, int model, hipStream_t stream) {
-  const bool sampled = a.temperature > 0.f;
+template <class M, bool LONG>
+void launch_model(const KArgs& a, hipStream_t stream) {
+  if (a.temperature > 0.f) hipLaunchKernelGGL((decode_kernel<M, true, LONG>), dim3(kNumWG), dim3(kBlock), 0, stream, a);
+  else hipLaunchKernelGGL((decode_kernel<M, false, LONG>), dim3(kNumWG), dim3(kBlock), 0, stream, a);
+}
+
+// One decode launch; long_ctx: the step's context exceeds kLongContext.
+int launch(const KArgs& a, int model, bool long_ctx, hipStream_t stream) {
   if (model == QMK_MODEL_QWEN3_1_7B) {
-    if (sampled) hipLaunchKernelGGL((decode_kernel<Qwen3_1_7B, true>), dim3(kNumWG), dim3(kBlock), 0, stream, a);
-    else hipLaunchKernelGGL((decode_kernel<Qwen3_1_7B, false>), dim3(kNumWG), dim3(kBlock), 0, stream, a);
+    if (long_ctx) launch_model<Qwen3_1_7B, true>(a, stream);
+    else launch_model<Qwen3_1_7B, false>(a, stream);
   } else {
-    if (sampled) hipLaunchKernelGGL((decode_kernel<Qwen3_0_6B, true>), dim3(kNumWG), dim3(kBlock), 0, stream, a);
-    else hipLaunchKernelGGL((decode_kernel<Qwen3_0_6B, false>), dim3(kNumWG), dim3(kBlock), 0, stream, a);
+    if (long_ctx) launch_model<Qwen3_0_6B, true>(a, stream);
+    else launch_model<Qwen3_0_6B, false>(a, stream);
   }
   return hipGetLastError() == hipSuccess ? QMK_OK : QMK_ERR_HIP;
 }
@@ -270,34 +284,36 @@ int decode_impl(const Common& c, int token, int position, int* out_token, float*
     a.position = position;
     a.token = token;
   }
-  return fail(launch(a, c.model, stream));
+  return fail(launch(a, c.model, position + 1 > kLongContext, stream));
 }
 
 // One step of the generate loop: the decode launch, and with sampling the
 // sampler that replaces its greedy token.
-int launch_step(const KArgs& a, int model, const SampleParams* sp, hipStream_t stream) {
-  int s = launch(a, model, stream);
+int launch_step(const KArgs& a, int model, const SampleParams* sp, bool long_ctx, hipStream_t stream) {
+  int s = launch(a, model, long_ctx, stream);
   if (s == QMK_OK && sp) s = launch_sample_state(a.logits, Dims<Qwen3_0_6B>::V, *sp, a.st, a.out_log, stream);
   return s;
 }
 
-// The instantiated graph of kGraphSteps steps with arguments `a` (and `sp`),
-// recorded again when the arguments, the model or the sampling change.
-int graph_for(Ctx* ctx, const KArgs& a, int model, const SampleParams* sp, hipGraphExec_t* out) {
+// The instantiated graph of kGraphSteps steps with arguments `a` (and `sp`) in
+// one attention form, recorded again when the arguments, the model or the
+// sampling change.
+int graph_for(Ctx* ctx, const KArgs& a, int model, const SampleParams* sp, bool long_ctx, hipGraphExec_t* out) {
   const bool sampled = sp != nullptr;
-  if (ctx->graph && ctx->graph_model == model && std::memcmp(&ctx->graph_args, &a, sizeof(KArgs)) == 0 &&
-      ctx->graph_sampled == sampled && (!sampled || std::memcmp(&ctx->graph_sp, sp, sizeof(SampleParams)) == 0)) {
-    *out = ctx->graph;
+  Ctx::Graph& gr = ctx->graphs[long_ctx ? 1 : 0];
+  if (gr.exec && gr.model == model && std::memcmp(&gr.args, &a, sizeof(KArgs)) == 0 && gr.sampled == sampled &&
+      (!sampled || std::memcmp(&gr.sp, sp, sizeof(SampleParams)) == 0)) {
+    *out = gr.exec;
     return QMK_OK;
   }
-  if (ctx->graph) {
-    hipGraphExecDestroy(ctx->graph);
-    ctx->graph = nullptr;
+  if (gr.exec) {
+    hipGraphExecDestroy(gr.exec);
+    gr.exec = nullptr;
   }
   if (!ctx->cap && hipStreamCreateWithFlags(&ctx->cap, hipStreamNonBlocking) != hipSuccess) return QMK_ERR_HIP;
   if (hipStreamBeginCapture(ctx->cap, hipStreamCaptureModeThreadLocal) != hipSuccess) return QMK_ERR_HIP;
   int s = QMK_OK;
-  for (int i = 0; i < kGraphSteps && s == QMK_OK; i++) s = launch_step(a, model, sp, ctx->cap);
+  for (int i = 0; i < kGraphSteps && s == QMK_OK; i++) s = launch_step(a, model, sp, long_ctx, ctx->cap);
   hipGraph_t g = nullptr;
   const hipError_t e = hipStreamEndCapture(ctx->cap, &g);
   if (s != QMK_OK || e != hipSuccess || !g) {
@@ -308,11 +324,11 @@ int graph_for(Ctx* ctx, const KArgs& a, int model, const SampleParams* sp, hipGr
   const hipError_t ie = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
   hipGraphDestroy(g);
   if (ie != hipSuccess) return QMK_ERR_HIP;
-  ctx->graph = ex;
-  ctx->graph_args = a;
-  ctx->graph_model = model;
-  ctx->graph_sampled = sampled;
-  if (sampled) ctx->graph_sp = *sp;
+  gr.exec = ex;
+  gr.args = a;
+  gr.model = model;
+  gr.sampled = sampled;
+  if (sampled) gr.sp = *sp;
   *out = ex;
   return QMK_OK;
 }
@@ -347,14 +363,22 @@ int generate_impl(const Common& c, int first_token_id, int num_steps, int eos, i
   }
   hipLaunchKernelGGL(set_step_kernel, dim3(1), dim3(1), 0, stream, ctx->st, start_position, first_token_id,
                      eos < 0 ? -1 : eos);
-  int done = 0;
-  hipGraphExec_t g = nullptr;
-  if (ctx->use_graphs && num_steps >= kGraphSteps && graph_for(ctx, a, c.model, sp, &g) == QMK_OK) {
-    for (; done + kGraphSteps <= num_steps; done += kGraphSteps)
-      if (hipGraphLaunch(g, stream) != hipSuccess) return fail(QMK_ERR_HIP);
+  // Step i runs at context start_position + i + 1.  The steps up to context
+  // kLongContext take the short-context kernel, the rest the long-context one;
+  // each run of steps replays its form's graph, with direct launches for the remainder.
+  for (int done = 0; done < num_steps;) {
+    const long long ctx0 = (long long)start_position + done + 1;
+    const bool lg = ctx0 > kLongContext;
+    int run = num_steps - done;
+    if (!lg) run = (int)std::min<long long>(run, kLongContext - ctx0 + 1);
+    hipGraphExec_t g = nullptr;
+    if (ctx->use_graphs && run >= kGraphSteps && graph_for(ctx, a, c.model, sp, lg, &g) == QMK_OK) {
+      for (; run >= kGraphSteps; run -= kGraphSteps, done += kGraphSteps)
+        if (hipGraphLaunch(g, stream) != hipSuccess) return fail(QMK_ERR_HIP);
+    }
+    for (; run > 0; run--, done++)
+      if ((s = launch_step(a, c.model, sp, lg, stream)) != QMK_OK) return fail(s);
   }
-  for (; done < num_steps; done++)
-    if ((s = launch_step(a, c.model, sp, stream)) != QMK_OK) return fail(s);
   if (hipMemcpyAsync(output_log, ctx->log, (size_t)num_steps * sizeof(int), hipMemcpyDeviceToDevice, stream) !=
       hipSuccess)
     return fail(QMK_ERR_HIP);

@@ -51,6 +51,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "qmk_device.h"
 #include "qmk_sample.h"
 #include "qmk_state.h"
@@ -72,6 +74,7 @@ constexpr int kComputePoints = 12;                         // compute-wave stamp
 constexpr int kMaxLayers = 28;
 constexpr int kKvU = 2;        // attention: each wave covers 4 positions (16-lane rows) x kKvU per batch
 constexpr int kKvStages = 4;   // K/V batches in flight per wave (LDS ring)
+constexpr int kLongContext = 2048;  // contexts above this run decode_kernel<M, S, true>
 
 template <class M>
 struct Dims {
@@ -216,6 +219,14 @@ struct Smem {
   LayerPtrs layers[kMaxLayers];      // copy of the packed pointer table, read once per launch
   int abort_flag;
   int stop_flag;                     // persistent mode: the stop token was emitted by an earlier launch
+};
+
+// The long-context kernel's LDS: the same object with the probability array
+// appended (one object, so the compiler can tell that reads of the other
+// fields never alias the K/V ring's in-flight DMA).
+template <class M>
+struct SmemLong : Smem<M> {
+  uint32_t pw[kChunkMax];            // bf16 probabilities of a position, head 1 << 16 | head 0
 };
 
 struct Step {
@@ -819,8 +830,11 @@ __device__ __forceinline__ void control_path(const KArgs& a, Smem<M>& s, const S
   }
 }
 
-template <class M, bool SAMPLED>
-__device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const Step& p, int b, int c, int lane) {
+// LONG: the long-context attention form; pw is its LDS array of packed
+// probabilities (kChunkMax words), unused otherwise.
+template <class M, bool SAMPLED, bool LONG>
+__device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const Step& p, int b, int c, int lane,
+                                             [[maybe_unused]] uint32_t* pw) {
   using Dm = Dims<M>;
   const int xcd = b & (kGroups - 1), r = b >> 3;
   const int slot = lane >> 4, t16 = lane & 15;
@@ -942,73 +956,147 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
     for (int j = 1; j < min(nb, kKvStages); j++) kv_issue(kc, j);
     cstamp(L, 2);
     // ------------------------------------------------ scores and local (max, sum)
-    {
-      u32x4 qv[Dm::GQ];
-#pragma unroll
-      for (int h = 0; h < Dm::GQ; h++) qv[h] = *reinterpret_cast<const u32x4*>(s.q + h * Dm::D + 8 * t16);
-      const u32x4 k_now = *reinterpret_cast<const u32x4*>(s.k + 8 * t16);
-      // Scores of this wave's positions (to LDS) and their maximum; the keys of
-      // the next batch are requested before the current batch is used.
-      float mloc[Dm::GQ];
-#pragma unroll
-      for (int h = 0; h < Dm::GQ; h++) mloc[h] = -INFINITY;
-      for (int j = 0; j < nb; j++) {
-        const int base = base0 + 32 * U * j;
-        kv_wait(j);
-#pragma unroll
-        for (int u = 0; u < U; u++) {
-          if (base + 32 * u >= p.p_end) break;  // the rest of the batch is past this workgroup's range
-          const int pp = base + 32 * u + slot;
-          const u32x4 kx = pp == p.pos ? k_now : s.kv[j % kKvStages][c][u][lane];
-#pragma unroll
-          for (int h = 0; h < Dm::GQ; h++) {
-            float sc = row16_sum(dot8(kx, qv[h], 0.f));
-            sc = bf16r(bf16r(sc) * a.attn_scale);
+    // position of entry i of this wave's batches (i = 8 batch + 4 u + slot)
+    [[maybe_unused]] auto wave_pos = [&](int i) { return base0 + 32 * U * (i >> 3) + 32 * ((i >> 2) & 1) + (i & 3); };
+    if constexpr (LONG) {
+      // A batch gives each 16-lane row two positions (u = 0, 1) and two heads: four
+      // partial dot products per lane, summed over the row in one transposed
+      // reduction, after which lane t16 < 4 of the row owns the score of
+      // (u = t16 & 1, head = (t16 >> 1) & 1) and alone scales, stores and maxes it.
+      // The softmax terms are then computed once per position, one position per
+      // lane, instead of once per lane of its row.
+      static_assert(Dm::GQ == 2 && U == 2, "four (position, head) scores per lane and batch");
+      const int own_u = t16 & 1, own_h = (t16 >> 1) & 1;
+      const bool owner = t16 < 4;
+      {
+        u32x4 qv[Dm::GQ];
+  #pragma unroll
+        for (int h = 0; h < Dm::GQ; h++) qv[h] = *reinterpret_cast<const u32x4*>(s.q + h * Dm::D + 8 * t16);
+        const u32x4 k_now = *reinterpret_cast<const u32x4*>(s.k + 8 * t16);
+        // Scores of this wave's positions (to LDS) and their maximum; the keys of
+        // the next batch are requested before the current batch is used.
+        float mloc = -INFINITY;  // owners: the maximum of head own_h over their positions
+        for (int j = 0; j < nb; j++) {
+          const int base = base0 + 32 * U * j;
+          kv_wait(j);
+          const int pp0 = base + slot, pp1 = base + 32 + slot;
+          const u32x4 k0 = pp0 == p.pos ? k_now : s.kv[j % kKvStages][c][0][lane];
+          const u32x4 k1 = pp1 == p.pos ? k_now : s.kv[j % kKvStages][c][1][lane];
+          const float x = row16_sum_t4(dot8(k0, qv[0], 0.f), dot8(k0, qv[1], 0.f), dot8(k1, qv[0], 0.f),
+                                       dot8(k1, qv[1], 0.f), t16);
+          const float sc = bf16r(bf16r(x) * a.attn_scale);
+          const int pp = own_u ? pp1 : pp0;
+          if (owner && pp < p.p_end) {
+            s.sc[own_h][pp - p.p_begin] = sc;
+            mloc = fmaxf(mloc, sc);
+          }
+          kv_refill(kc, j);
+        }
+        // Every K batch has landed (the last wait was vmcnt(0)); saying so here
+        // lets the compiler drop the vmcnt(0) it would otherwise put before the
+        // next workgroup barriers, which would also wait for weight prefetches.
+        wait_vmcnt(0);
+        // wave maximum per head: lanes 0, 1 of each row hold head 0, lanes 2, 3 head 1
+        {
+          float x, y;
+          mloc = fmaxf(mloc, dpp_get<0xB1>(mloc));
+          swap16(mloc, x, y);
+          mloc = fmaxf(x, y);
+          swap32(mloc, x, y);
+          mloc = fmaxf(x, y);
+        }
+        const float wm[2] = {__int_as_float(__builtin_amdgcn_readlane(__float_as_int(mloc), 0)),
+                             __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mloc), 2))};
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        // sum of exp(s - max), one position per lane
+        float lsum[Dm::GQ] = {0.f, 0.f};
+        for (int i = lane; i < 8 * nb; i += kWave) {
+          const int pp = wave_pos(i);
+          if (pp < p.p_end) {
+  #pragma unroll
+            for (int h = 0; h < Dm::GQ; h++) lsum[h] += exp_acc(s.sc[h][pp - p.p_begin] - wm[h]);
+          }
+        }
+  #pragma unroll
+        for (int h = 0; h < Dm::GQ; h++) {
+          lsum[h] = wave_total(lsum[h]);
+          if (lane == 0) {
+            s.wml[c][h][0] = wm[h];
+            s.wml[c][h][1] = lsum[h];
+          }
+        }
+      }
+    } else {
+      {
+        u32x4 qv[Dm::GQ];
+  #pragma unroll
+        for (int h = 0; h < Dm::GQ; h++) qv[h] = *reinterpret_cast<const u32x4*>(s.q + h * Dm::D + 8 * t16);
+        const u32x4 k_now = *reinterpret_cast<const u32x4*>(s.k + 8 * t16);
+        // Scores of this wave's positions (to LDS) and their maximum; the keys of
+        // the next batch are requested before the current batch is used.
+        float mloc[Dm::GQ];
+  #pragma unroll
+        for (int h = 0; h < Dm::GQ; h++) mloc[h] = -INFINITY;
+        for (int j = 0; j < nb; j++) {
+          const int base = base0 + 32 * U * j;
+          kv_wait(j);
+  #pragma unroll
+          for (int u = 0; u < U; u++) {
+            if (base + 32 * u >= p.p_end) break;  // the rest of the batch is past this workgroup's range
+            const int pp = base + 32 * u + slot;
+            const u32x4 kx = pp == p.pos ? k_now : s.kv[j % kKvStages][c][u][lane];
+  #pragma unroll
+            for (int h = 0; h < Dm::GQ; h++) {
+              float sc = row16_sum(dot8(kx, qv[h], 0.f));
+              sc = bf16r(bf16r(sc) * a.attn_scale);
+              if (pp < p.p_end) {
+                if (t16 == 0) s.sc[h][pp - p.p_begin] = sc;
+                mloc[h] = fmaxf(mloc[h], sc);
+              }
+            }
+          }
+          kv_refill(kc, j);
+        }
+        // Every K batch has landed (the last wait was vmcnt(0)); saying so here
+        // lets the compiler drop the vmcnt(0) it would otherwise put before the
+        // next workgroup barriers, which would also wait for weight prefetches.
+        wait_vmcnt(0);
+        // wave maximum over the four 16-lane rows, then the sum of exp(s - max)
+        // with one exponential per position
+  #pragma unroll
+        for (int h = 0; h < Dm::GQ; h++) {
+          float x, y;
+          swap16(mloc[h], x, y);
+          mloc[h] = fmaxf(x, y);
+          swap32(mloc[h], x, y);
+          mloc[h] = fmaxf(x, y);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        float lsum[Dm::GQ];
+  #pragma unroll
+        for (int h = 0; h < Dm::GQ; h++) lsum[h] = 0.f;
+        for (int j = 0; j < nb; j++) {
+          const int base = base0 + 32 * U * j;
+  #pragma unroll
+          for (int u = 0; u < U; u++) {
+            const int pp = base + 32 * u + slot;
             if (pp < p.p_end) {
-              if (t16 == 0) s.sc[h][pp - p.p_begin] = sc;
-              mloc[h] = fmaxf(mloc[h], sc);
+  #pragma unroll
+              for (int h = 0; h < Dm::GQ; h++) lsum[h] += exp_acc(s.sc[h][pp - p.p_begin] - mloc[h]);
             }
           }
         }
-        kv_refill(kc, j);
-      }
-      // Every K batch has landed (the last wait was vmcnt(0)); saying so here
-      // lets the compiler drop the vmcnt(0) it would otherwise put before the
-      // next workgroup barriers, which would also wait for weight prefetches.
-      wait_vmcnt(0);
-      // wave maximum over the four 16-lane rows, then the sum of exp(s - max)
-      // with one exponential per position
-#pragma unroll
-      for (int h = 0; h < Dm::GQ; h++) {
-        float x, y;
-        swap16(mloc[h], x, y);
-        mloc[h] = fmaxf(x, y);
-        swap32(mloc[h], x, y);
-        mloc[h] = fmaxf(x, y);
-      }
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      float lsum[Dm::GQ];
-#pragma unroll
-      for (int h = 0; h < Dm::GQ; h++) lsum[h] = 0.f;
-      for (int j = 0; j < nb; j++) {
-        const int base = base0 + 32 * U * j;
-#pragma unroll
-        for (int u = 0; u < U; u++) {
-          const int pp = base + 32 * u + slot;
-          if (pp < p.p_end) {
-#pragma unroll
-            for (int h = 0; h < Dm::GQ; h++) lsum[h] += exp_acc(s.sc[h][pp - p.p_begin] - mloc[h]);
+  #pragma unroll
+        for (int h = 0; h < Dm::GQ; h++) {
+          lsum[h] = rows_sum4(lsum[h]);  // rows hold different positions; lanes of a row the same one
+          if (lane == 0) {
+            s.wml[c][h][0] = mloc[h];
+            s.wml[c][h][1] = lsum[h];
           }
-        }
-      }
-#pragma unroll
-      for (int h = 0; h < Dm::GQ; h++) {
-        lsum[h] = rows_sum4(lsum[h]);  // rows hold different positions; lanes of a row the same one
-        if (lane == 0) {
-          s.wml[c][h][0] = mloc[h];
-          s.wml[c][h][1] = lsum[h];
         }
       }
     }
@@ -1019,6 +1107,73 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
     for (int j = 1; j < min(nb, kKvStages); j++) kv_issue(vc, j);
     cstamp(L, 4);
     // ------------------------------------------------ probabilities and P@V
+    if constexpr (LONG)
+    {
+      const u32x4 v_now = *reinterpret_cast<const u32x4*>(s.v + 8 * t16);
+      float gm[Dm::GQ], ginv[Dm::GQ];
+#pragma unroll
+      for (int h = 0; h < Dm::GQ; h++) {
+        gm[h] = s.ml[h][0];
+        ginv[h] = __fdiv_rn(1.0f, s.ml[h][1]);
+      }
+      // HF: softmax in fp32, probabilities rounded to bf16 before P@V; one
+      // position per lane, both heads' bf16 bits in one word
+      for (int i = lane; i < 8 * nb; i += kWave) {
+        const int pp = wave_pos(i);
+        if (pp < p.p_end) {
+          const int e = pp - p.p_begin;
+          const uint32_t p0 = f32_to_bf16(exp_acc(s.sc[0][e] - gm[0]) * ginv[0]);
+          const uint32_t p1 = f32_to_bf16(exp_acc(s.sc[1][e] - gm[1]) * ginv[1]);
+          pw[e] = p1 << 16 | p0;
+        }
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      float acc[Dm::GQ][8];
+#pragma unroll
+      for (int h = 0; h < Dm::GQ; h++)
+#pragma unroll
+        for (int i = 0; i < 8; i++) acc[h][i] = 0.f;
+      for (int j = 0; j < nb; j++) {
+        const int base = base0 + 32 * U * j;
+        kv_wait(j);
+        // the row's two positions are paired in bf16x2 operands: probabilities
+        // (head h of both) and values (one dimension of both), so one dot2
+        // accumulates two positions; a position past the range has probability 0
+        const int pp0 = base + slot, pp1 = base + 32 + slot;
+        const u32x4 v0 = pp0 == p.pos ? v_now : s.kv[j % kKvStages][c][0][lane];
+        const u32x4 v1 = pp1 == p.pos ? v_now : s.kv[j % kKvStages][c][1][lane];
+        const uint32_t w0 = pp0 < p.p_end ? pw[min(pp0 - p.p_begin, kChunkMax - 1)] : 0u;
+        const uint32_t w1 = pp1 < p.p_end ? pw[min(pp1 - p.p_begin, kChunkMax - 1)] : 0u;
+        const bf16x2 pr[2] = {as_bf2(__builtin_amdgcn_perm(w1, w0, 0x05040100u)),
+                              as_bf2(__builtin_amdgcn_perm(w1, w0, 0x07060302u))};
+        const uint32_t va[4] = {v0.x, v0.y, v0.z, v0.w}, vb[4] = {v1.x, v1.y, v1.z, v1.w};
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+          const bf16x2 lo = as_bf2(__builtin_amdgcn_perm(vb[k], va[k], 0x05040100u));  // dim 2k
+          const bf16x2 hi = as_bf2(__builtin_amdgcn_perm(vb[k], va[k], 0x07060302u));  // dim 2k+1
+#pragma unroll
+          for (int h = 0; h < Dm::GQ; h++) {
+            acc[h][2 * k] = __builtin_amdgcn_fdot2_f32_bf16(pr[h], lo, acc[h][2 * k], false);
+            acc[h][2 * k + 1] = __builtin_amdgcn_fdot2_f32_bf16(pr[h], hi, acc[h][2 * k + 1], false);
+          }
+        }
+        kv_refill(vc, j);
+      }
+      wait_vmcnt(0);  // every V batch has landed (see above)
+      // sum the wave's four slots; lanes 0..15 then hold dims 8*t16..+7
+#pragma unroll
+      for (int h = 0; h < Dm::GQ; h++) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) acc[h][i] = rows_sum4(acc[h][i]);
+        if (lane < 16) {
+#pragma unroll
+          for (int i = 0; i < 8; i++) s.wacc[c][h][8 * t16 + i] = acc[h][i];
+        }
+      }
+    }
+    else
     {
       const u32x4 v_now = *reinterpret_cast<const u32x4*>(s.v + 8 * t16);
       float gm[Dm::GQ], ginv[Dm::GQ];
@@ -1168,10 +1323,14 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
 
 // SAMPLED: the LM-head keys are Gumbel-perturbed (temperature sampling, KArgs::temperature > 0);
 // a separate instantiation so the greedy kernel carries none of it.
-template <class M, bool SAMPLED = false>
+// LONG: the attention form for contexts beyond kLongContext (each score and
+// softmax term computed once per position, P@V on bf16 pairs).  Both forms are
+// exact for every context; the host picks by the step's context, because the
+// long form, compiled into the same kernel, slows the short-context exchanges.
+template <class M, bool SAMPLED = false, bool LONG = false>
 __global__ void __launch_bounds__(kBlock, 1) decode_kernel(KArgs a) {
   using Dm = Dims<M>;
-  __shared__ Smem<M> s;
+  __shared__ std::conditional_t<LONG, SmemLong<M>, Smem<M>> s;
   const int b = blockIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar branches on the role
   const int lane = threadIdx.x & 63;
@@ -1229,10 +1388,13 @@ __global__ void __launch_bounds__(kBlock, 1) decode_kernel(KArgs a) {
   p.p_begin = min(p.C, r * p.chunk);
   p.p_end = min(p.C, p.p_begin + p.chunk);
   p.n_act = (p.C + p.chunk - 1) / p.chunk;
-  if (wave == 0)
+  if (wave == 0) {
     control_path<M>(a, s, p, b, lane);
-  else
-    compute_path<M, SAMPLED>(a, s, p, b, wave - 1, lane);
+  } else if constexpr (LONG) {
+    compute_path<M, SAMPLED, true>(a, s, p, b, wave - 1, lane, s.pw);
+  } else {
+    compute_path<M, SAMPLED, false>(a, s, p, b, wave - 1, lane, nullptr);
+  }
 }
 
 #undef QMK_SYNC

@@ -113,6 +113,33 @@ __device__ __forceinline__ float row16_sum(float v) {
   return v;
 }
 
+template <int CTRL>
+__device__ __forceinline__ float dpp_get(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+
+// Four row sums at once, transposed: every lane contributes v[u][h] for
+// u, h in {0, 1}, and lane t16 of each 16-lane row receives the row sum of
+// v[t16 & 1][(t16 >> 1) & 1].  Two quad exchanges halve the values carried
+// (each lane keeps the half its index selects and adds its partner's copy of
+// it), then rotations by 4 and 8 lanes add the four quads.  The last steps
+// associate differently in different lanes, so only one lane per value
+// (t16 < 4) should be read when bit-identical copies matter.
+__device__ __forceinline__ float row16_sum_t4(float v00, float v01, float v10, float v11, int t16) {
+  const bool b0 = (t16 & 1) != 0, b1 = (t16 & 2) != 0;
+  const float k0 = b0 ? v10 : v00, k1 = b0 ? v11 : v01;  // kept: u = bit 0
+  const float s0 = b0 ? v00 : v10, s1 = b0 ? v01 : v11;  // the partner's u
+  const float n0 = k0 + dpp_get<0xB1>(s0);               // quad_perm [1,0,3,2]
+  const float n1 = k1 + dpp_get<0xB1>(s1);
+  float r = (b1 ? n1 : n0) + dpp_get<0x4E>(b1 ? n0 : n1);  // quad_perm [2,3,0,1]; kept: h = bit 1
+  r += dpp_get<0x124>(r);                                // row_ror:4
+  r += dpp_get<0x128>(r);                                // row_ror:8
+  return r;
+}
+
+// Sum over the wave, the same value in every lane.
+__device__ __forceinline__ float wave_total(float v) { return rows_sum4(row16_sum(v)); }
+
 // Sum over the wave; uniform result.
 __device__ __forceinline__ float wave_sum(float v) {
   v = row16_sum(v);

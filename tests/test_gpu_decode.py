@@ -169,11 +169,13 @@ def _with_rope(weights, max_seq_len, device):
 
 @pytest.mark.parametrize(
     "c0,layers,steps,strict",
-    [(1500, 4, 6, True), (1500, 28, 4, False), (8192, 4, 4, True), (8192, 28, 3, False), (32768, 28, 2, False)],
-    ids=["1500-4layers", "1500-28layers", "8192-4layers", "8192-28layers", "32768-28layers"])
+    [(1500, 4, 6, True), (1500, 28, 4, False), (2100, 4, 6, True), (8192, 4, 4, True), (8192, 28, 3, False),
+     (32768, 28, 2, False)],
+    ids=["1500-4layers", "1500-28layers", "2100-4layers", "8192-4layers", "8192-28layers", "32768-28layers"])
 def test_long_context_parity(shape, weights_cpu, weights_gpu, c0, layers, steps, strict):
     """Attention over an injected N(0,1) cache of c0 positions (split-K over the 32 workgroups of
-    an XCD; above 2048 positions each wave streams several K/V batches through the LDS ring).
+    an XCD; above 2048 positions each wave streams several K/V batches through the LDS ring, and
+    the long-context kernel runs: at 2100 wave 0 has a second, partial batch).
 
     Cosine >= 0.999 at every step.  Max abs <= 0.1 for the 4-layer cases; for 28 layers the
     bound is max(0.1, 1.5 x the reference's own noise floor at this workload, measured live):
@@ -216,6 +218,41 @@ def test_long_context_parity(shape, weights_cpu, weights_gpu, c0, layers, steps,
         assert d <= 0.05, f"{name} cache rows written by the kernel differ by {d}"
     print(f"long context {c0} x {layers} layers: worst max abs {worst:.4f}"
           + (f", reference noise floor {floor:.4f}" if floor is not None else ""))
+
+
+def test_generate_across_long_context_boundary(shape, weights_gpu):
+    """generate_nosync from position 1990 for 100 steps runs contexts 1991..2090: the loop switches
+    from the short-context kernel to the long-context one after context 2048, each form with its
+    own recorded graph.  Its tokens equal those of 100 per-step launches, which pick the kernel by
+    the same rule, with graph replay and with direct launches."""
+    from qwen_megakernel_amd.build import get_extension
+    from qwen_megakernel_amd.weights import make_kv_prefill
+
+    c0, n, max_seq = 1990, 100, 2200
+    wg = _with_rope(weights_gpu, max_seq, "cuda")
+    k, v = make_kv_prefill(shape, c0, seed=3)
+
+    def fresh():
+        d = _decoder(wg, max_seq_len=max_seq)
+        d.load_kv(k.cuda(), v.cuda(), c0)
+        return d
+
+    ref = fresh()
+    toks, t = [], 11
+    for _ in range(n):
+        t = ref.step(t)
+        toks.append(t)
+    ops = get_extension()
+    for graphs in (True, False, True):
+        ops.set_graph_launch(graphs)
+        try:
+            dec = fresh()
+            out = ops.generate_nosync(11, n, *dec._scratch(), shape.num_layers, c0, max_seq,
+                                      dec._attn_scale).cpu().tolist()
+        finally:
+            ops.set_graph_launch(True)
+        assert out == toks, f"graphs={graphs}: first difference at step {next(i for i in range(n) if out[i] != toks[i])}"
+    assert int(ops.device_error()) == 0
 
 
 def test_last_position_and_bounds(shape, weights_gpu):

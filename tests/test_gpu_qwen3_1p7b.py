@@ -53,24 +53,29 @@ def test_qwen3_1p7b_decode_parity(w17):
     print(f"qwen3-1.7b: worst max abs {worst:.4f}, reference noise floor {floor:.4f}")
 
 
-def test_qwen3_1p7b_context_512(w17):
-    """28 layers over an injected 512-position N(0,1) cache, bound max(0.1, 1.5 x the reference's noise floor)."""
+@pytest.mark.parametrize("c0,layers", [(512, 28), (3000, 4)], ids=["512-28layers", "3000-4layers"])
+def test_qwen3_1p7b_context(w17, c0, layers):
+    """Attention over an injected N(0,1) cache of c0 positions, bound max(0.1, 1.5 x the reference's
+    noise floor); at 3000 positions the long-context kernel runs."""
     from oracle.qwen3_ref import OracleDecoder, greedy_stream
     from qwen_megakernel_amd.shapes import QWEN3_1_7B
     from qwen_megakernel_amd.weights import make_kv_prefill
+    from test_gpu_decode import _with_rope
 
     wc, wg = w17
-    c0 = 512
+    max_seq = max(1024, c0 + 64)
+    if max_seq > 1024:
+        wc, wg = _with_rope(wc, max_seq, "cpu"), _with_rope(wg, max_seq, "cuda")
     k, v = make_kv_prefill(QWEN3_1_7B, c0, seed=2)
-    orc = OracleDecoder(wc, QWEN3_1_7B, max_seq_len=1024)
+    orc = OracleDecoder(wc, QWEN3_1_7B, num_layers=layers, max_seq_len=max_seq)
     orc.load_kv(k, v, c0)
     ref = greedy_stream(orc, [11, 22], 3, record_logits=True)
-    floor = _fp32_order_noise_floor(wc, QWEN3_1_7B, lambda d: d.load_kv(k, v, c0), ref["inputs"], 1024)
+    floor = _fp32_order_noise_floor(wc, QWEN3_1_7B, lambda d: d.load_kv(k, v, c0), ref["inputs"], max_seq, layers)
     bound = max(ABS_MAX, 1.5 * floor)
-    dec = _decoder(wg, max_seq_len=1024)
+    dec = _decoder(wg, num_layers=layers, max_seq_len=max_seq)
     dec.load_kv(k.cuda(), v.cuda(), c0)
     worst = _compare(dec, ref, bound, floor)
-    print(f"qwen3-1.7b context 512: worst max abs {worst:.4f}, reference noise floor {floor:.4f}")
+    print(f"qwen3-1.7b context {c0} x {layers} layers: worst max abs {worst:.4f}, reference noise floor {floor:.4f}")
 
 
 def test_qwen3_1p7b_generate_matches_steps(w17):
