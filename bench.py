@@ -341,7 +341,7 @@ def main():
                      "frac": round(achieved / PEAK_HBM_GBS, 4),
                      "traffic": MEASURED_TRAFFIC_BYTES.get((args.steps, args.warmup)),
                      "bytes_per_launch": int(bytes_per_launch), "avg_launch_us": round(avg_launch_s * 1e6, 2),
-                     "kernel": "qmk::decode_kernel<Qwen3_0_6B, false>"},
+                     "kernel": "qmk::decode_kernel<Qwen3_0_6B, false, false>"},
         "cpu_baseline": None,
     }
     if args.phase_trace:
