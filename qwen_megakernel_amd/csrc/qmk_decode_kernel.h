@@ -221,12 +221,18 @@ struct Smem {
   int stop_flag;                     // persistent mode: the stop token was emitted by an earlier launch
 };
 
-// The long-context kernel's LDS: the same object with the probability array
-// appended (one object, so the compiler can tell that reads of the other
-// fields never alias the K/V ring's in-flight DMA).
+// The long-context kernel's LDS: the same object with per-wave score and
+// probability arrays appended (one object, so the compiler can tell that reads
+// of the other fields never alias the K/V ring's in-flight DMA).  They are
+// indexed by the wave's entry i = 8 batch + 4 u + slot, so the one-position-
+// per-lane passes touch consecutive words; indexed by position, a wave's
+// positions (4 wave + slot + 32 u + 64 batch) would fall on four banks.
+constexpr int kWaveEntries = 8 * (kChunkMax / (32 * kKvU));  // entries of one wave's batches
+constexpr int kHeadStride = kWaveEntries + 8;                 // head 1 starts eight banks after head 0
 template <class M>
 struct SmemLong : Smem<M> {
-  uint32_t pw[kChunkMax];            // bf16 probabilities of a position, head 1 << 16 | head 0
+  float sw[kComputeWaves][2 * kHeadStride];  // scores of head h at [wave][h * kHeadStride + i] (bf16 values)
+  uint32_t pw[kComputeWaves][kWaveEntries];  // bf16 probabilities, head 1 << 16 | head 0
 };
 
 struct Step {
@@ -830,11 +836,11 @@ __device__ __forceinline__ void control_path(const KArgs& a, Smem<M>& s, const S
   }
 }
 
-// LONG: the long-context attention form; pw is its LDS array of packed
-// probabilities (kChunkMax words), unused otherwise.
+// LONG: the long-context attention form; sw and pw are this wave's rows of
+// SmemLong::sw and SmemLong::pw, unused otherwise.
 template <class M, bool SAMPLED, bool LONG>
 __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const Step& p, int b, int c, int lane,
-                                             [[maybe_unused]] uint32_t* pw) {
+                                             [[maybe_unused]] float* sw, [[maybe_unused]] uint32_t* pw) {
   using Dm = Dims<M>;
   const int xcd = b & (kGroups - 1), r = b >> 3;
   const int slot = lane >> 4, t16 = lane & 15;
@@ -987,7 +993,7 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
           const float sc = bf16r(bf16r(x) * a.attn_scale);
           const int pp = own_u ? pp1 : pp0;
           if (owner && pp < p.p_end) {
-            s.sc[own_h][pp - p.p_begin] = sc;
+            sw[own_h * kHeadStride + 8 * j + 4 * own_u + slot] = sc;
             mloc = fmaxf(mloc, sc);
           }
           kv_refill(kc, j);
@@ -1016,7 +1022,7 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
           const int pp = wave_pos(i);
           if (pp < p.p_end) {
   #pragma unroll
-            for (int h = 0; h < Dm::GQ; h++) lsum[h] += exp_acc(s.sc[h][pp - p.p_begin] - wm[h]);
+            for (int h = 0; h < Dm::GQ; h++) lsum[h] += exp_acc(sw[h * kHeadStride + i] - wm[h]);
           }
         }
   #pragma unroll
@@ -1121,10 +1127,9 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
       for (int i = lane; i < 8 * nb; i += kWave) {
         const int pp = wave_pos(i);
         if (pp < p.p_end) {
-          const int e = pp - p.p_begin;
-          const uint32_t p0 = f32_to_bf16(exp_acc(s.sc[0][e] - gm[0]) * ginv[0]);
-          const uint32_t p1 = f32_to_bf16(exp_acc(s.sc[1][e] - gm[1]) * ginv[1]);
-          pw[e] = p1 << 16 | p0;
+          const uint32_t p0 = f32_to_bf16(exp_acc(sw[i] - gm[0]) * ginv[0]);
+          const uint32_t p1 = f32_to_bf16(exp_acc(sw[kHeadStride + i] - gm[1]) * ginv[1]);
+          pw[i] = p1 << 16 | p0;
         }
       }
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -1144,8 +1149,8 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
         const int pp0 = base + slot, pp1 = base + 32 + slot;
         const u32x4 v0 = pp0 == p.pos ? v_now : s.kv[j % kKvStages][c][0][lane];
         const u32x4 v1 = pp1 == p.pos ? v_now : s.kv[j % kKvStages][c][1][lane];
-        const uint32_t w0 = pp0 < p.p_end ? pw[min(pp0 - p.p_begin, kChunkMax - 1)] : 0u;
-        const uint32_t w1 = pp1 < p.p_end ? pw[min(pp1 - p.p_begin, kChunkMax - 1)] : 0u;
+        const uint32_t w0 = pp0 < p.p_end ? pw[8 * j + slot] : 0u;
+        const uint32_t w1 = pp1 < p.p_end ? pw[8 * j + 4 + slot] : 0u;
         const bf16x2 pr[2] = {as_bf2(__builtin_amdgcn_perm(w1, w0, 0x05040100u)),
                               as_bf2(__builtin_amdgcn_perm(w1, w0, 0x07060302u))};
         const uint32_t va[4] = {v0.x, v0.y, v0.z, v0.w}, vb[4] = {v1.x, v1.y, v1.z, v1.w};
@@ -1391,9 +1396,9 @@ __global__ void __launch_bounds__(kBlock, 1) decode_kernel(KArgs a) {
   if (wave == 0) {
     control_path<M>(a, s, p, b, lane);
   } else if constexpr (LONG) {
-    compute_path<M, SAMPLED, true>(a, s, p, b, wave - 1, lane, s.pw);
+    compute_path<M, SAMPLED, true>(a, s, p, b, wave - 1, lane, s.sw[wave - 1], s.pw[wave - 1]);
   } else {
-    compute_path<M, SAMPLED, false>(a, s, p, b, wave - 1, lane, nullptr);
+    compute_path<M, SAMPLED, false>(a, s, p, b, wave - 1, lane, nullptr, nullptr);
   }
 }
 
