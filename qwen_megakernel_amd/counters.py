@@ -16,10 +16,12 @@ Shader-sequencer counters per kernel (any ``SQ_*`` / ``GRBM_*`` set):
     python -m qwen_megakernel_amd.counters sq A.csv [B.csv ...] --timed 256
 
 gives, for every decode-kernel instantiation, the mean of each counter over
-its last ``--timed`` dispatches and, where the counters are present, the LDS
+its last ``--timed`` dispatches (a counter present in several files is read
+from the last of them) and, where the counters are present, the LDS
 bank-conflict share (``SQ_LDS_BANK_CONFLICT / SQ_ACTIVE_INST_LDS``: stalled
 cycles per LDS-active cycle), ROCm's ``LDSBankConflict`` (``100 *
-SQ_LDS_BANK_CONFLICT / GRBM_GUI_ACTIVE / CUs``: percent of GPU time per CU) and
+SQ_LDS_BANK_CONFLICT / GRBM_GUI_ACTIVE / CUs``, percent of GPU time per CU,
+with ``GRBM_GUI_ACTIVE`` per XCD: rocprofv3 writes it summed over the XCDs) and
 the wait share (``SQ_WAIT_ANY / SQ_WAVE_CYCLES``: wave time spent waiting,
 barriers and memory included).
 """
@@ -64,7 +66,7 @@ def traffic(fetch_csv: str, write_csv: str, timed: int) -> dict:
     return out
 
 
-def sq_summary(paths, timed: int, cus: int = 256) -> dict:
+def sq_summary(paths, timed: int, cus: int = 256, xcds: int = 8) -> dict:
     """Per decode-kernel instantiation: mean of each counter over its last `timed` dispatches."""
     per = {}  # kernel -> counter -> [values in dispatch order]
     for path in paths:
@@ -78,11 +80,11 @@ def sq_summary(paths, timed: int, cus: int = 256) -> dict:
     out = {}
     for k, cs in per.items():
         m = {c: sum(v[-timed:]) / len(v[-timed:]) for c, v in cs.items()}
-        d = {"dispatches": max(len(v) for v in cs.values()), "mean": {c: round(x, 1) for c, x in m.items()}}
+        d = {"dispatches": min(len(v) for v in cs.values()), "mean": {c: round(x, 1) for c, x in m.items()}}
         if "SQ_LDS_BANK_CONFLICT" in m and m.get("SQ_ACTIVE_INST_LDS"):
             d["lds_bank_conflict_per_active_cycle"] = round(m["SQ_LDS_BANK_CONFLICT"] / m["SQ_ACTIVE_INST_LDS"], 5)
         if "SQ_LDS_BANK_CONFLICT" in m and m.get("GRBM_GUI_ACTIVE"):
-            d["LDSBankConflict_pct"] = round(100 * m["SQ_LDS_BANK_CONFLICT"] / m["GRBM_GUI_ACTIVE"] / cus, 4)
+            d["LDSBankConflict_pct"] = round(100 * m["SQ_LDS_BANK_CONFLICT"] / (m["GRBM_GUI_ACTIVE"] / xcds) / cus, 4)
         if "SQ_WAIT_ANY" in m and m.get("SQ_WAVE_CYCLES"):
             d["wait_share"] = round(m["SQ_WAIT_ANY"] / m["SQ_WAVE_CYCLES"], 4)
         out[k] = d

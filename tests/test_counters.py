@@ -48,13 +48,13 @@ def test_sq_summary_per_instantiation_and_ratios(tmp_path):
                  (SHORT, "GRBM_GUI_ACTIVE", 50.0), (LONG, "SQ_LDS_BANK_CONFLICT", 0.0),
                  (LONG, "SQ_ACTIVE_INST_LDS", 10.0)]
     _write(a, rows)
-    _write(b, [(SHORT, "SQ_WAIT_ANY", 30.0), (SHORT, "SQ_WAVE_CYCLES", 40.0), ("other_kernel", "SQ_WAIT_ANY", 1.0)])
+    _write(b, [(SHORT, "SQ_WAIT_ANY", 30.0), (SHORT, "SQ_WAVE_CYCLES", 40.0)] * 3 + [("other_kernel", "SQ_WAIT_ANY", 1.0)])
     s = counters.sq_summary([str(a), str(b)], timed=2)
     assert set(s) == {"decode_kernel<qmk::Qwen3_0_6B, false, false>", "decode_kernel<qmk::Qwen3_0_6B, false, true>"}
     short = s["decode_kernel<qmk::Qwen3_0_6B, false, false>"]
     assert short["dispatches"] == 3
     assert short["mean"]["SQ_LDS_BANK_CONFLICT"] == 250.0  # mean of the last two
     assert short["lds_bank_conflict_per_active_cycle"] == 0.25
-    assert short["LDSBankConflict_pct"] == round(100 * 250.0 / 50.0 / 256, 4)
+    assert short["LDSBankConflict_pct"] == round(100 * 250.0 / (50.0 / 8) / 256, 4)  # GRBM summed over 8 XCDs
     assert short["wait_share"] == 0.75
     assert s["decode_kernel<qmk::Qwen3_0_6B, false, true>"]["lds_bank_conflict_per_active_cycle"] == 0.0
