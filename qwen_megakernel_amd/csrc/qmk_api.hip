@@ -57,6 +57,7 @@ struct Ctx {
     SampleParams sp{};
   } graphs[2];                    // by attention form: [0] contexts <= kLongContext, [1] beyond
   float* logits = nullptr;        // sampled generate: the step's logits (float[vocab])
+  SampleWork* swork = nullptr;    // sampled generate: the sampler's work between its launches
 };
 
 struct DevInfo {
@@ -289,9 +290,10 @@ int decode_impl(const Common& c, int token, int position, int* out_token, float*
 
 // One step of the generate loop: the decode launch, and with sampling the
 // sampler that replaces its greedy token.
-int launch_step(const KArgs& a, int model, const SampleParams* sp, bool long_ctx, hipStream_t stream) {
+int launch_step(const KArgs& a, int model, const SampleParams* sp, SampleWork* sw, bool long_ctx,
+                hipStream_t stream) {
   int s = launch(a, model, long_ctx, stream);
-  if (s == QMK_OK && sp) s = launch_sample_state(a.logits, Dims<Qwen3_0_6B>::V, *sp, a.st, a.out_log, stream);
+  if (s == QMK_OK && sp) s = launch_sample_state(a.logits, Dims<Qwen3_0_6B>::V, *sp, a.st, a.out_log, sw, stream);
   return s;
 }
 
@@ -313,7 +315,7 @@ int graph_for(Ctx* ctx, const KArgs& a, int model, const SampleParams* sp, bool 
   if (!ctx->cap && hipStreamCreateWithFlags(&ctx->cap, hipStreamNonBlocking) != hipSuccess) return QMK_ERR_HIP;
   if (hipStreamBeginCapture(ctx->cap, hipStreamCaptureModeThreadLocal) != hipSuccess) return QMK_ERR_HIP;
   int s = QMK_OK;
-  for (int i = 0; i < kGraphSteps && s == QMK_OK; i++) s = launch_step(a, model, sp, long_ctx, ctx->cap);
+  for (int i = 0; i < kGraphSteps && s == QMK_OK; i++) s = launch_step(a, model, sp, ctx->swork, long_ctx, ctx->cap);
   hipGraph_t g = nullptr;
   const hipError_t e = hipStreamEndCapture(ctx->cap, &g);
   if (s != QMK_OK || e != hipSuccess || !g) {
@@ -359,6 +361,7 @@ int generate_impl(const Common& c, int first_token_id, int num_steps, int eos, i
   }
   if (sp) {
     if (!ctx->logits && hipMalloc(&ctx->logits, (size_t)Dm::V * sizeof(float)) != hipSuccess) return fail(QMK_ERR_HIP);
+    if (!ctx->swork && alloc_sample_work(&ctx->swork, 1) != QMK_OK) return fail(QMK_ERR_HIP);
     a.logits = ctx->logits;
   }
   hipLaunchKernelGGL(set_step_kernel, dim3(1), dim3(1), 0, stream, ctx->st, start_position, first_token_id,
@@ -377,7 +380,7 @@ int generate_impl(const Common& c, int first_token_id, int num_steps, int eos, i
         if (hipGraphLaunch(g, stream) != hipSuccess) return fail(QMK_ERR_HIP);
     }
     for (; run > 0; run--, done++)
-      if ((s = launch_step(a, c.model, sp, lg, stream)) != QMK_OK) return fail(s);
+      if ((s = launch_step(a, c.model, sp, ctx->swork, lg, stream)) != QMK_OK) return fail(s);
   }
   if (hipMemcpyAsync(output_log, ctx->log, (size_t)num_steps * sizeof(int), hipMemcpyDeviceToDevice, stream) !=
       hipSuccess)

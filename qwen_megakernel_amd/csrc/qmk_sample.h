@@ -49,10 +49,24 @@ struct SampleParams {
   uint64_t seed;
 };
 
+// Device work of one logits row between the launches of a sampling call: the
+// row's radix histogram (counts or fixed-point masses) and selection state.
+// Zero between calls: the call's last launch clears it.
+struct SampleWork {
+  unsigned long long hist[256];  // bins of the current 8-bit radix digit
+  unsigned long long z, target, need, best;  // need: top-k rank still sought / top-p mass above the prefix
+  unsigned int maxkey, prefix, mask, kmin, pmin, ticket;
+};
+constexpr int kSampleRowsMax = 256;  // rows per launch sequence of qmk_sample_rows
+
+// hipMalloc + zero fill of `rows` work blocks.
+int alloc_sample_work(SampleWork** out, int rows);
+
 // Persistent-mode sampler of the generate loop: when the decode step just run
 // produced `logits`, replace its greedy token in the state and the log by a
 // sampled one (counter = the step's position) and set `done` for the stop token.
+// `work`: one zeroed SampleWork owned by the caller's stream.
 int launch_sample_state(const float* logits, int vocab, const SampleParams& sp, DecodeState* st, int* log,
-                        hipStream_t stream);
+                        SampleWork* work, hipStream_t stream);
 
 }  // namespace qmk
