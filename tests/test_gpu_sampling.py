@@ -71,6 +71,15 @@ def test_sample_rows_match_oracle_full_vocab(T, k, p):
     _compare(logits, T, k, p, 7, [5, 6, 7, 1 << 33])
 
 
+def test_sample_rows_beyond_one_launch_sequence_and_repeatable():
+    """300 rows: more than one launch sequence (256 rows each, the per-row work is reused and must
+    be left zeroed); every row matches the oracle, and a second call gives the same tokens."""
+    rng = np.random.default_rng(4)
+    logits = (rng.standard_normal((300, 1000)) * 3).astype(np.float32)
+    first = _compare(logits, 0.9, 20, 0.9, 99, list(range(300)))
+    assert _gpu_sample(logits, 0.9, 20, 0.9, 99, list(range(300))) == first
+
+
 def test_gpu_draws_follow_softmax():
     """4096 draws from one row (distinct counters): frequencies within 5 sd of softmax(logits / T)."""
     row = np.array([1.0, 0.2, -0.5, 2.0, 0.0, -3.0, 1.5, 0.7], dtype=np.float32)
