@@ -836,11 +836,16 @@ constexpr size_t rows_lds(int T, int K) {
   return (NORM ? (size_t)((T * K * 2 + 15) / 16 * 16) : 0) + (size_t)NW * 16 * 16 * NB * 4 + (size_t)NW * 16 * 4 + 64;
 }
 
-template <int NB, int EPI, bool NORM, int NW, int ITERS, int MAXT>
+// HALF: 8 output columns per tile (the MFMA's columns 8-15 repeat rows 0-7,
+// whose loads the same instruction already makes), twice the workgroups of an
+// N / 16 grid for the narrow o and down projections.
+template <int NB, int EPI, bool NORM, int NW, int ITERS, int MAXT, bool HALF = false>
 __global__ void __launch_bounds__(NW * 64) gemm_rows(const uint16_t* __restrict__ X, const uint16_t* __restrict__ norm_w,
                                                      float eps, int T, int K, Seg seg, uint16_t* __restrict__ Y,
                                                      int ldy) {
   constexpr int NC = 16 * NB;
+  constexpr int NO = HALF ? 8 : NC;  // output columns per tile
+  static_assert(!HALF || (NB == 1 && EPI != kEpiSiluMul), "half tiles: one 16-column MFMA tile, plain rows");
   extern __shared__ __align__(16) unsigned char smem[];
   uint16_t* xs = reinterpret_cast<uint16_t*>(smem);
   const size_t xs_bytes = NORM ? (size_t)((T * K * 2 + 15) / 16 * 16) : 0;
@@ -871,7 +876,8 @@ __global__ void __launch_bounds__(NW * 64) gemm_rows(const uint16_t* __restrict_
   bf16x8 b[ITERS][2][NB];
 #pragma unroll
   for (int j = 0; j < NB; j++) {
-    const uint16_t* wrow = tile_row<EPI, NC>(seg, tile, 16 * j + (lane & 15), K) + kq + k0;
+    const uint16_t* wrow = (HALF ? tile_row<EPI, NO>(seg, tile, lane & 7, K)
+                                 : tile_row<EPI, NC>(seg, tile, 16 * j + (lane & 15), K)) + kq + k0;
 #pragma unroll
     for (int it = 0; it < ITERS; it++) {
       b[it][0][j] = ld_bf16x8_stream(wrow + 64 * it);
@@ -954,7 +960,7 @@ __global__ void __launch_bounds__(NW * 64) gemm_rows(const uint16_t* __restrict_
 #pragma unroll
     for (int i = 0; i < 4; i++) red[w][4 * (lane >> 4) + i][16 * j + (lane & 15)] = acc[j][i];
   __syncthreads();
-  const int t = threadIdx.x / NC, c = threadIdx.x % NC;
+  const int t = threadIdx.x / NO, c = threadIdx.x % NO;
   if (t >= T || t >= 16) return;
   auto col_sum = [&](int cc) {
     float y = 0.f;
@@ -970,7 +976,7 @@ __global__ void __launch_bounds__(NW * 64) gemm_rows(const uint16_t* __restrict_
     return;
   }
   const float y = bf16r(col_sum(c));
-  uint16_t* dst = Y + (size_t)t * ldy + tile * NC + c;
+  uint16_t* dst = Y + (size_t)t * ldy + tile * NO + c;
   if (EPI == kEpiResidual) *dst = (uint16_t)f32_to_bf16(bf16r(bf16_to_f32(*dst) + y));
   else *dst = (uint16_t)f32_to_bf16(y);
 }
@@ -1304,7 +1310,7 @@ void launch_lm_head(const uint16_t* N, const int* erow, int R, const uint16_t* W
 
 // gemm_rows over `tiles` 16-column tiles (NB = 1), NW waves each taking
 // K / NW = 64 * ITERS of the K range; ITERS picked from K.
-template <int EPI, bool NORM, int NW, int ITERS, int MAXT>
+template <int EPI, bool NORM, int NW, int ITERS, int MAXT, bool HALF>
 void launch_rows_t(int tiles, const uint16_t* X, const uint16_t* nw, float eps, int T, int K, const Seg& seg,
                    uint16_t* Y, int ldy, hipStream_t s) {
   const size_t lds = rows_lds<1, NW, NORM>(T, K);
@@ -1312,30 +1318,31 @@ void launch_rows_t(int tiles, const uint16_t* X, const uint16_t* nw, float eps, 
     // 16 normalised rows of 2048: above the default dynamic LDS limit (gfx950 has 160 KB per CU)
     static bool raised = false;
     if (!raised)
-      raised = hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_rows<1, EPI, NORM, NW, ITERS, MAXT>),
+      raised = hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_rows<1, EPI, NORM, NW, ITERS, MAXT, HALF>),
                                    hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024) == hipSuccess;
   }
-  hipLaunchKernelGGL((gemm_rows<1, EPI, NORM, NW, ITERS, MAXT>), dim3(tiles), dim3(NW * 64), lds, s, X, nw, eps, T,
+  hipLaunchKernelGGL((gemm_rows<1, EPI, NORM, NW, ITERS, MAXT, HALF>), dim3(tiles), dim3(NW * 64), lds, s, X, nw, eps, T,
                      K, seg, Y, ldy);
 }
 
 // NORM kernels stage the rows in registers sized for T <= 4 (the common batch) or T <= 16.
-template <int EPI, bool NORM, int NW, int ITERS>
+template <int EPI, bool NORM, int NW, int ITERS, bool HALF>
 void launch_rows_it(int tiles, const uint16_t* X, const uint16_t* nw, float eps, int T, int K, const Seg& seg,
                     uint16_t* Y, int ldy, hipStream_t s) {
-  if (!NORM || T <= 4) launch_rows_t<EPI, NORM, NW, ITERS, 4>(tiles, X, nw, eps, T, K, seg, Y, ldy, s);
-  else launch_rows_t<EPI, NORM, NW, ITERS, 16>(tiles, X, nw, eps, T, K, seg, Y, ldy, s);
+  if (!NORM || T <= 4) launch_rows_t<EPI, NORM, NW, ITERS, 4, HALF>(tiles, X, nw, eps, T, K, seg, Y, ldy, s);
+  else launch_rows_t<EPI, NORM, NW, ITERS, 16, HALF>(tiles, X, nw, eps, T, K, seg, Y, ldy, s);
 }
 
-template <int EPI, bool NORM, int NW>
+// `tiles` tiles of 16 output columns, or of 8 (HALF)
+template <int EPI, bool NORM, int NW, bool HALF = false>
 void launch_rows(int tiles, const uint16_t* X, const uint16_t* nw, float eps, int T, int K, const Seg& seg,
                  uint16_t* Y, int ldy, hipStream_t s) {
   switch (K / (64 * NW)) {
-    case 1: launch_rows_it<EPI, NORM, NW, 1>(tiles, X, nw, eps, T, K, seg, Y, ldy, s); break;
-    case 2: launch_rows_it<EPI, NORM, NW, 2>(tiles, X, nw, eps, T, K, seg, Y, ldy, s); break;
-    case 3: launch_rows_it<EPI, NORM, NW, 3>(tiles, X, nw, eps, T, K, seg, Y, ldy, s); break;
-    case 4: launch_rows_it<EPI, NORM, NW, 4>(tiles, X, nw, eps, T, K, seg, Y, ldy, s); break;
-    default: launch_rows_it<EPI, NORM, NW, 6>(tiles, X, nw, eps, T, K, seg, Y, ldy, s); break;
+    case 1: launch_rows_it<EPI, NORM, NW, 1, HALF>(tiles, X, nw, eps, T, K, seg, Y, ldy, s); break;
+    case 2: launch_rows_it<EPI, NORM, NW, 2, HALF>(tiles, X, nw, eps, T, K, seg, Y, ldy, s); break;
+    case 3: launch_rows_it<EPI, NORM, NW, 3, HALF>(tiles, X, nw, eps, T, K, seg, Y, ldy, s); break;
+    case 4: launch_rows_it<EPI, NORM, NW, 4, HALF>(tiles, X, nw, eps, T, K, seg, Y, ldy, s); break;
+    default: launch_rows_it<EPI, NORM, NW, 6, HALF>(tiles, X, nw, eps, T, K, seg, Y, ldy, s); break;
   }
 }
 
@@ -1368,12 +1375,12 @@ int forward_fused(const Args& a, hipStream_t s) {
     hipLaunchKernelGGL(attention_fused, dim3(T, kNKV), dim3(1024), 0, s, QKV, tok, L, u16(w.q_norm_weight),
                        u16(w.k_norm_weight), a.cos_t, a.sin_t, a.cache, eps, a.attn_scale, ATT);
     const Seg o{{u16(w.o_proj_weight), nullptr, nullptr}, {Dm::H, 0, 0}};
-    launch_rows<kEpiResidual, false, 16>(Dm::H / 16, ATT, nullptr, eps, T, kQS, o, X, Dm::H, s);
+    launch_rows<kEpiResidual, false, 16, true>(Dm::H / 8, ATT, nullptr, eps, T, kQS, o, X, Dm::H, s);
     const Seg gu{{u16(w.gate_proj_weight), u16(w.up_proj_weight), nullptr}, {Dm::I, Dm::I, 0}};
     launch_rows<kEpiSiluMul, true, 8>(Dm::I / 8, X, u16(w.post_attn_layernorm_weight), eps, T, Dm::H, gu, MM, Dm::I,
                                       s);
     const Seg dn{{u16(w.down_proj_weight), nullptr, nullptr}, {Dm::H, 0, 0}};
-    launch_rows<kEpiResidual, false, 16>(Dm::H / 16, MM, nullptr, eps, T, Dm::I, dn, X, Dm::H, s);
+    launch_rows<kEpiResidual, false, 16, true>(Dm::H / 8, MM, nullptr, eps, T, Dm::I, dn, X, Dm::H, s);
   }
   hipLaunchKernelGGL((residual_norm<Dm::H>), dim3(T), dim3(1024), 0, s, nullptr, 0, T, X, a.final_norm, eps, N);
   launch_lm_head<M>(N, erow, R, a.lm_head, keys, a.logits, tok, a.out_tokens, s);
