@@ -114,18 +114,17 @@ __device__ unsigned long long block_reduce_u64(unsigned long long v, F&& op) {
 }
 
 // True in every thread of the last workgroup of this pass to finish; the
-// other workgroups' atomics are then visible to it.
+// other workgroups' atomics are then visible to it.  Each thread waits until
+// its device-scope atomics are acknowledged before the ticket is taken, and
+// the last workgroup reads the results with agent-scope atomic loads; no
+// fence, which on this part would write back the L2.
 __device__ bool last_block(SampleWork* w) {
   __shared__ int last;
+  wait_vmcnt(0);
   __syncthreads();
-  if (threadIdx.x == 0) {
-    __threadfence();
-    last = atomicAdd(&w->ticket, 1u) == gridDim.x - 1;
-  }
+  if (threadIdx.x == 0) last = atomicAdd(&w->ticket, 1u) == gridDim.x - 1;
   __syncthreads();
-  if (!last) return false;
-  __threadfence();
-  return true;
+  return last != 0;
 }
 
 __device__ __forceinline__ unsigned long long load_u64(const unsigned long long* p) {
