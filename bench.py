@@ -30,6 +30,11 @@ four and algorithmic GB/s per step (weights once + each sequence's KV).
 
 ``prefill``: the 128-token prompt through the batched forward, ms and tok/s.
 
+``sampling`` (skip with ``--no-sampling``): the same prompt and model, 512
+device-fed steps of the sampled generate loop (counter-based Gumbel-max draws,
+seed 0) with temperature only (drawn inside the decode kernel), top-k 50,
+top-p 0.9, and both (temperature 0.8), in tok/s; greedy is ``value``.
+
 ``phases`` (skip with ``--no-phases``) is the per-phase weight-streaming
 microbenchmark: each GEMV phase of the step (RMSNorm + QKV, O, gate/up +
 SiLU*mul, down, LM head + argmax) run alone over >= 1 GiB of rotating seeded
@@ -242,6 +247,43 @@ def prefill_rate(w, prompt_len: int = PROMPT_LEN, iters: int = 10):
     return {"prompt_len": prompt_len, "ms": round(t * 1e3, 3), "tok_per_s": round(prompt_len / t, 1)}
 
 
+def sampling(dec, prompt, max_seq: int, steps: int):
+    """Sampled generate loop (generate_sample) from the prefilled prompt, per sampling setting."""
+    import torch
+
+    from qwen_megakernel_amd.shapes import QWEN3_0_6B as S
+
+    ops = torch.ops.qwen_megakernel_C
+    steps = min(steps, max_seq - len(prompt))
+    out = {"steps": steps, "context": f"{len(prompt)}..{len(prompt) + steps - 1}"}
+
+    def run(n, T, k, p):
+        return ops.generate_sample(prompt[-1], n, -1, T, k, p, 0, dec._embed_weight, dec._layer_weights_packed,
+                                   dec._final_norm_weight, dec._lm_head_weight, dec._cos_table, dec._sin_table,
+                                   dec._k_cache, dec._v_cache, dec._hidden, dec._norm_out, S.num_layers,
+                                   dec.position, max_seq, dec._attn_scale)
+
+    for name, (T, k, p) in (("temperature_1.0", (1.0, 0, 1.0)), ("top_k_50", (1.0, 50, 1.0)),
+                            ("top_p_0.9", (1.0, 0, 0.9)), ("top_k_50_top_p_0.9_T0.8", (0.8, 50, 0.9))):
+        dec.reset()
+        dec.prefill(prompt[:-1])
+        run(min(64, steps), T, k, p)  # records the loop's graph for these arguments
+        dec.reset()
+        dec.prefill(prompt[:-1])
+        stream = torch.cuda.current_stream()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record(stream)
+        toks = run(steps, T, k, p)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        assert toks.numel() == steps and int(ops.device_error()) == 0
+        t = e0.elapsed_time(e1) / 1e3 / steps
+        out[name] = {"tok_per_s": round(1.0 / t, 1), "ms_per_token": round(t * 1e3, 4)}
+        log(f"sampling {name}: {1.0 / t:.1f} tok/s")
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -255,6 +297,8 @@ def main():
     ap.add_argument("--long-steps", type=int, default=256)
     ap.add_argument("--no-1p7b", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true")
+    ap.add_argument("--no-sampling", action="store_true")
+    ap.add_argument("--sample-steps", type=int, default=512)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (this path does not shard "
@@ -355,6 +399,8 @@ def main():
         summ["context"] = last + 1
         result["phase_trace"] = summ
         log(f"phase trace at context {last + 1}:\n" + trace.format_table(summ))
+    if not args.no_sampling:
+        result["sampling"] = sampling(dec, prompt, max_seq, args.sample_steps)
     del dec  # frees the 128-token run's caches; the weights stay for the long-context runs
     torch.cuda.empty_cache()
     result["prefill"] = prefill_rate(w)
