@@ -35,6 +35,7 @@
 
 #include <map>
 #include <mutex>
+#include <utility>
 
 namespace qmk {
 namespace sample {
@@ -322,19 +323,21 @@ int launch(const Args& a, int rows, hipStream_t stream) {
   return hipGetLastError() == hipSuccess ? QMK_OK : QMK_ERR_HIP;
 }
 
-// Per-device work for qmk_sample_rows (kSampleRowsMax rows, kept until the process ends).
+// Work of qmk_sample_rows per (device, stream), kSampleRowsMax rows, kept until
+// the process ends: calls on one stream are ordered, so they may share it;
+// calls on different streams may overlap, so they do not.
 std::mutex g_mu;
-std::map<int, SampleWork*> g_work;
+std::map<std::pair<int, hipStream_t>, SampleWork*> g_work;
 
-int device_work(SampleWork** out) {
+int stream_work(hipStream_t stream, SampleWork** out) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return QMK_ERR_HIP;
   std::lock_guard<std::mutex> lk(g_mu);
-  auto it = g_work.find(dev);
+  auto it = g_work.find({dev, stream});
   if (it == g_work.end()) {
     SampleWork* w = nullptr;
     if (alloc_sample_work(&w, kSampleRowsMax) != QMK_OK) return QMK_ERR_HIP;
-    it = g_work.emplace(dev, w).first;
+    it = g_work.emplace(std::make_pair(dev, stream), w).first;
   }
   *out = it->second;
   return QMK_OK;
@@ -370,7 +373,7 @@ extern "C" int qmk_sample_rows(const float* logits, int rows, int vocab, float t
   if (!(top_p == top_p) || !(temperature == temperature)) return QMK_ERR_ARG;  // NaN
   const SampleParams sp{temperature, top_k, top_p, (uint64_t)seed};
   SampleWork* work = nullptr;
-  int s = sample::device_work(&work);
+  int s = sample::stream_work(stream, &work);
   if (s != QMK_OK) return s;
   for (int r0 = 0; r0 < rows && s == QMK_OK; r0 += kSampleRowsMax) {
     const int n = rows - r0 < kSampleRowsMax ? rows - r0 : kSampleRowsMax;

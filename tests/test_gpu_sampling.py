@@ -80,6 +80,33 @@ def test_sample_rows_beyond_one_launch_sequence_and_repeatable():
     assert _gpu_sample(logits, 0.9, 20, 0.9, 99, list(range(300))) == first
 
 
+def test_sample_rows_on_two_streams_at_once():
+    """Each stream has its own sampler work: two calls in flight on two streams draw what the same
+    calls draw one after the other."""
+    rng = np.random.default_rng(6)
+    lg = torch.from_numpy((rng.standard_normal((8, 20000)) * 2).astype(np.float32)).cuda()
+    ctr = torch.arange(8, dtype=torch.int64).cuda()
+    cfgs = [(0.9, 30, 0.95, 1), (1.2, 0, 0.8, 2)]
+
+    def call(cfg):
+        out = torch.empty(8, dtype=torch.int32, device="cuda")
+        T, k, p, seed = cfg
+        _ops().sample(lg, T, k, p, seed, ctr, out)
+        return out
+
+    seq = []
+    for cfg in cfgs:
+        seq.append(call(cfg).cpu().tolist())
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    torch.cuda.synchronize()
+    outs = []
+    for st, cfg in zip(streams, cfgs):
+        with torch.cuda.stream(st):
+            outs.append(call(cfg))
+    torch.cuda.synchronize()
+    assert [o.cpu().tolist() for o in outs] == seq
+
+
 def test_gpu_draws_follow_softmax():
     """4096 draws from one row (distinct counters): frequencies within 5 sd of softmax(logits / T)."""
     row = np.array([1.0, 0.2, -0.5, 2.0, 0.0, -3.0, 1.5, 0.7], dtype=np.float32)
