@@ -3,7 +3,9 @@
 * libqwen_megakernel_amd.so loads and exports every function declared in
   include/qwen_megakernel.h.
 * The C entry points validate their arguments on the host before touching the
-  device (the reference validates nothing: SURVEY quirks 5-6).
+  device. The reference validates nothing: csrc/torch_bindings.cpp has no
+  TORCH_CHECK, and csrc/kernel.cu:344-356 indexes the tables and caches with the position it
+  is given, never compared with max_seq_len.
 * torch.ops.qwen_megakernel_C registers the reference's two schemas verbatim
   (reference csrc/torch_bindings.cpp:130-153).
 """
