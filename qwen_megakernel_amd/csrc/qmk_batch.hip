@@ -215,59 +215,66 @@ __global__ void __launch_bounds__(256) gemm_partial(const uint16_t* __restrict__
   }
 }
 
-// Sum of the K-split partials of element (t, n), in split order.  All loads
-// are issued before the first add.
 // Large T (prompt prefill): an LDS-tiled MFMA GEMM, part[z][t][n] = the sum
-// over K split z of X[t][k] W[n][k].  Workgroup tile 128 rows x 128 columns,
-// BK = 64; wave w computes rows 64*(w&1)..+63 x columns 64*(w>>1)..+63 as
-// 4 x 4 MFMA tiles (8 LDS reads per 16 MFMAs).  Both operands are staged
-// through LDS, double buffered: the global loads of step s+1 are issued before
-// the MFMAs of step s.  Rows are padded by 16 bytes so the 16 lanes reading one
-// 16-byte column of 16 rows spread over the LDS banks.
-constexpr int kTM = 128, kTN = 128, kTK = 64, kTPad = kTK + 8;
+// over K split z of X[t][k] W[n][k].  Workgroup tile 128 rows x TN columns
+// (TN = 128, or 64 for narrow N so that more workgroups run), BK = 64; wave w
+// computes rows 64*(w&1)..+63 x columns (TN/2)*(w>>1)..+TN/2-1 as 4 x TN/32
+// MFMA tiles.  Both operands are staged through LDS, double buffered: the
+// global loads of step s+1 are issued before the MFMAs of step s.  Rows are
+// padded by 16 bytes so the 16 lanes reading one 16-byte column of 16 rows
+// spread over the LDS banks.
+constexpr int kTM = 128, kTK = 64, kTPad = kTK + 8;
 
+template <int TN>
 __global__ void __launch_bounds__(256) gemm_tiled(const uint16_t* __restrict__ X, int T, int K, Seg seg, int N,
                                                   int ksplit, float* __restrict__ part) {
+  static_assert(TN == 64 || TN == 128, "tile width");
+  constexpr int BQ = TN / 32;  // 16-byte B chunks per thread per step (TN rows x 8 chunks over 256 threads)
+  constexpr int WJ = TN / 32;  // 16-column MFMA tiles per wave (a wave covers TN / 2 columns)
   __shared__ __align__(16) uint16_t As[2][kTM][kTPad];
-  __shared__ __align__(16) uint16_t Bs[2][kTN][kTPad];
-  const int n0 = blockIdx.x * kTN, t0 = blockIdx.y * kTM;
+  __shared__ __align__(16) uint16_t Bs[2][TN][kTPad];
+  const int n0 = blockIdx.x * TN, t0 = blockIdx.y * kTM;
   // K split z of ksplit (blockIdx.z): columns [kz, kz + K / ksplit); partial sums to part[z]
   const int kz = blockIdx.z * (K / ksplit);
   part += (size_t)blockIdx.z * T * N;
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int wm = w & 1, wn = w >> 1;
-  // global -> register staging: A and B 128 rows x 8 chunks of 16 B each (4 per thread each)
+  // global -> register staging: A 128 rows and B TN rows, 8 chunks of 16 B each
   const uint16_t* asrc[4];
-  const uint16_t* bsrc[4];
-  int srow[4], scol[4];
+  const uint16_t* bsrc[BQ];
+  int arow[4], acol[4], brow[BQ], bcol[BQ];
 #pragma unroll
   for (int i = 0; i < 4; i++) {
     const int c = threadIdx.x + 256 * i;
-    srow[i] = c >> 3;
-    scol[i] = (c & 7) * 8;
-    asrc[i] = X + (size_t)min(t0 + srow[i], T - 1) * K + kz + scol[i];
-    bsrc[i] = seg_row(seg, n0 + srow[i], K) + kz + scol[i];
+    arow[i] = c >> 3;
+    acol[i] = (c & 7) * 8;
+    asrc[i] = X + (size_t)min(t0 + arow[i], T - 1) * K + kz + acol[i];
   }
-  u32x4 ra[4], rb[4];
+#pragma unroll
+  for (int i = 0; i < BQ; i++) {
+    const int c = threadIdx.x + 256 * i;
+    brow[i] = c >> 3;
+    bcol[i] = (c & 7) * 8;
+    bsrc[i] = seg_row(seg, n0 + brow[i], K) + kz + bcol[i];
+  }
+  u32x4 ra[4], rb[BQ];
   auto gload = [&](int k) {
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      ra[i] = ld16(asrc[i] + k);
-      rb[i] = ld16(bsrc[i] + k);
-    }
+    for (int i = 0; i < 4; i++) ra[i] = ld16(asrc[i] + k);
+#pragma unroll
+    for (int i = 0; i < BQ; i++) rb[i] = ld16(bsrc[i] + k);
   };
   auto lstore = [&](int buf) {
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      *reinterpret_cast<u32x4*>(&As[buf][srow[i]][scol[i]]) = ra[i];
-      *reinterpret_cast<u32x4*>(&Bs[buf][srow[i]][scol[i]]) = rb[i];
-    }
+    for (int i = 0; i < 4; i++) *reinterpret_cast<u32x4*>(&As[buf][arow[i]][acol[i]]) = ra[i];
+#pragma unroll
+    for (int i = 0; i < BQ; i++) *reinterpret_cast<u32x4*>(&Bs[buf][brow[i]][bcol[i]]) = rb[i];
   };
-  f32x4 acc[4][4];
+  f32x4 acc[4][WJ];
 #pragma unroll
   for (int i = 0; i < 4; i++)
 #pragma unroll
-    for (int j = 0; j < 4; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < WJ; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
   const int kq = 8 * (lane >> 4), l16 = lane & 15;
   const int steps = K / ksplit / kTK;
   gload(0);
@@ -278,15 +285,16 @@ __global__ void __launch_bounds__(256) gemm_tiled(const uint16_t* __restrict__ X
     if (st + 1 < steps) gload((st + 1) * kTK);
 #pragma unroll
     for (int kk = 0; kk < kTK; kk += 32) {
-      bf16x8 a[4], b[4];
+      bf16x8 a[4], b[WJ];
 #pragma unroll
       for (int i = 0; i < 4; i++) a[i] = *reinterpret_cast<const bf16x8*>(&As[buf][64 * wm + 16 * i + l16][kk + kq]);
 #pragma unroll
-      for (int j = 0; j < 4; j++) b[j] = *reinterpret_cast<const bf16x8*>(&Bs[buf][64 * wn + 16 * j + l16][kk + kq]);
+      for (int j = 0; j < WJ; j++)
+        b[j] = *reinterpret_cast<const bf16x8*>(&Bs[buf][(TN / 2) * wn + 16 * j + l16][kk + kq]);
 #pragma unroll
       for (int i = 0; i < 4; i++)
 #pragma unroll
-        for (int j = 0; j < 4; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < WJ; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
     }
     if (st + 1 < steps) {
       lstore(buf ^ 1);  // the other buffer was last read in step st-1, before the barrier below it
@@ -296,8 +304,8 @@ __global__ void __launch_bounds__(256) gemm_tiled(const uint16_t* __restrict__ X
 #pragma unroll
   for (int i = 0; i < 4; i++)
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const int n = n0 + 64 * wn + 16 * j + l16;
+    for (int j = 0; j < WJ; j++) {
+      const int n = n0 + (TN / 2) * wn + 16 * j + l16;
 #pragma unroll
       for (int r = 0; r < 4; r++) {
         const int t = t0 + 64 * wm + 16 * i + 4 * (lane >> 4) + r;
@@ -306,6 +314,8 @@ __global__ void __launch_bounds__(256) gemm_tiled(const uint16_t* __restrict__ X
     }
 }
 
+// Sum of the K-split partials of element (t, n), in split order.  All loads
+// are issued before the first add.
 __device__ __forceinline__ float sum_splits(const float* part, int ksplit, int T, int N, int t, int n) {
   const size_t stride = (size_t)T * N, idx = (size_t)t * N + n;
   float v[kMaxSplit];
@@ -1170,39 +1180,62 @@ __global__ void mfma_selftest(const uint16_t* A, const uint16_t* B, float* C) {
 // ---------------------------------------------------------------- host side
 
 struct Gemm {
-  int nb, ksplit;
+  int nb, ksplit, tn;  // nb = 0: LDS-tiled with tile width tn
 };
 
 // 64-column tiles (16 for N not a multiple of 64); the K range is split
 // (up to kMaxSplit ways, >= 64 K per wave) until about kTargetWaves waves
 // stream the weights.
-bool use_tiled(int T, int N, int K) { return T >= 96 && N % kTN == 0 && K % (4 * kTK) == 0; }
+bool use_tiled(int T, int N, int K) { return T >= 96 && N % 128 == 0 && K % (4 * kTK) == 0; }
 
-// Tiled: K split (at most 8 ways, >= 4 steps of 64 each) until about 512
-// workgroups run, two per CU.
+// Tiled, 128-column tiles: K split (at most 8 ways, >= 4 steps of 64 each)
+// until about 512 workgroups run, two per CU.
 int tiled_splits(int T, int N, int K) {
-  const long long tiles = (long long)((T + kTM - 1) / kTM) * (N / kTN);
+  const long long tiles = (long long)((T + kTM - 1) / kTM) * (N / 128);
   int ks = 1;
   while (tiles * ks < 512 && ks < 8 && K % (ks * 2 * 4 * kTK) == 0) ks *= 2;
   return ks;
 }
 
+// Tiled, 64-column tiles, for problems whose 128-column plan leaves CUs idle
+// (narrow N at a few hundred rows): K split (at most 16 ways, >= 2 steps of
+// 64 each) until 256 workgroups run, while the fp32 partials
+// (ksplit * T * N * 4 bytes) stay within twice the weight bytes (N * K * 2).
+int narrow_splits(int T, int N, int K) {
+  const long long tiles = (long long)((T + kTM - 1) / kTM) * (N / 64);
+  int ks = 1;
+  while (tiles * ks < 256 && ks * 2 <= 16 && K % (ks * 2 * kTK) == 0 && K / (ks * 2) >= 2 * kTK &&
+         (long long)ks * 2 * T * 4 <= 2LL * K * 2)
+    ks *= 2;
+  return ks;
+}
+
 Gemm plan_gemm(int T, int N, int K) {
-  if (use_tiled(T, N, K)) return {0, tiled_splits(T, N, K)};
+  if (use_tiled(T, N, K)) {
+    const int ks = tiled_splits(T, N, K);
+    const long long wgs = (long long)((T + kTM - 1) / kTM) * (N / 128) * ks;
+    if (wgs >= 256) return {0, ks, 128};
+    const int ks64 = narrow_splits(T, N, K);
+    if ((long long)((T + kTM - 1) / kTM) * (N / 64) * ks64 > wgs) return {0, ks64, 64};
+    return {0, ks, 128};
+  }
   const int mt = (T + 15) / 16;
   const int nb = N % 64 == 0 ? 4 : 1;
   int ks = 1;
   while ((long long)mt * (N / (16 * nb)) * ks < kTargetWaves && ks * 2 <= kMaxSplit && K % (ks * 2 * 64) == 0)
     ks *= 2;
-  return {nb, ks};
+  return {nb, ks, 0};
 }
 
 void launch_gemm(const uint16_t* X, const int* rows, int T, int K, const Seg& seg, int N, float* part, hipStream_t s,
                  int* ks_out) {
   const Gemm g = plan_gemm(T, N, K);
   if (g.nb == 0) {  // LDS-tiled
-    hipLaunchKernelGGL(gemm_tiled, dim3(N / kTN, (T + kTM - 1) / kTM, g.ksplit), dim3(256), 0, s, X, T, K, seg, N,
-                       g.ksplit, part);
+    const dim3 grid(N / g.tn, (T + kTM - 1) / kTM, g.ksplit);
+    if (g.tn == 128)
+      hipLaunchKernelGGL(gemm_tiled<128>, grid, dim3(256), 0, s, X, T, K, seg, N, g.ksplit, part);
+    else
+      hipLaunchKernelGGL(gemm_tiled<64>, grid, dim3(256), 0, s, X, T, K, seg, N, g.ksplit, part);
     *ks_out = g.ksplit;
     return;
   }
