@@ -397,13 +397,16 @@ def test_decode_batch_equals_general_forward(weights_gpu):
     assert cos >= 0.999, cos
 
 
-def test_long_prefill_tiled_gemm(shape, weights_cpu, weights_gpu):
-    """A 300-token prefill takes the LDS-tiled MFMA GEMM (128 x 128 tiles, K split across
-    workgroups): every 25th row and the last against the oracle, 2 layers."""
+@pytest.mark.parametrize("n", [128, 300], ids=["128tok-64col-tiles", "300tok-mixed-tiles"])
+def test_long_prefill_tiled_gemm(shape, weights_cpu, weights_gpu, n):
+    """Prefills of 96+ tokens take the LDS-tiled MFMA GEMM: every 25th row and the last against
+    the oracle, 2 layers.  128 tokens: 64-column tiles for all four projections, o and down split
+    16 ways over K; 300 tokens: 128-column tiles (a partial last row tile) and 64-column tiles
+    for down."""
     from oracle.qwen3_ref import OracleDecoder
     from qwen_megakernel_amd.weights import make_prompt
 
-    n, layers = 300, 2
+    layers = 2
     ids = make_prompt(n, shape.vocab, seed=13)
     ref = _oracle_feed(OracleDecoder(weights_cpu, shape, num_layers=layers, max_seq_len=512), ids)
     dec = _decoder(weights_gpu, num_layers=layers, max_seq_len=512)
