@@ -438,6 +438,38 @@ class BatchDecoder:
             raise RuntimeError("prefill produced no token (invalid input)")
         return (tok, logits[0].clone()) if return_logits else tok
 
+    def prefill_all(self, prompts, return_logits: bool = False):
+        """Append ``prompts[b]`` to sequence b for every b in one forward (the prompts' tokens
+        concatenated, each with its sequence and position); returns each sequence's next greedy
+        token, and with ``return_logits`` also the fp32 logits ``[B, V]`` of its last prompt token.
+        One pass reads the weights once for all the prompts, instead of once per sequence."""
+        if len(prompts) != self.batch_size:
+            raise ValueError(f"expected {self.batch_size} prompts")
+        prompts = [[int(t) for t in ids] for ids in prompts]
+        if any(not ids or any(not 0 <= t < VOCAB_SIZE for t in ids) for ids in prompts):
+            raise ValueError("empty prompt or token id outside the vocabulary")
+        for b, ids in enumerate(prompts):
+            self._check(b, len(ids))
+        toks, seqs, pos, emit = [], [], [], []
+        for b, ids in enumerate(prompts):
+            start = self._positions[b]
+            toks += ids
+            seqs += [b] * len(ids)
+            pos += range(start, start + len(ids))
+            emit.append(len(toks) - 1)
+        max_context = max(self._positions[b] + len(ids) for b, ids in enumerate(prompts))
+        out = torch.empty(self.batch_size, dtype=torch.int32, device=self._dev)
+        logits = (torch.empty(self.batch_size, VOCAB_SIZE, dtype=torch.float32, device=self._dev)
+                  if return_logits else None)
+        self._forward(_as_i32(toks, self._dev), _as_i32(seqs, self._dev), _as_i32(pos, self._dev),
+                      _as_i32(emit, self._dev), out, logits, self._k_cache, self._v_cache, max_context)
+        for b, ids in enumerate(prompts):
+            self._positions[b] += len(ids)
+        res = out.cpu().tolist()
+        if any(t < 0 for t in res):
+            raise RuntimeError("prefill produced no token (invalid input)")
+        return (res, logits) if return_logits else res
+
     def step_logits(self, tokens):
         """One token per sequence at its current position; returns (next tokens, fp32 logits [B, V])."""
         tokens = [int(t) for t in tokens]
@@ -499,8 +531,9 @@ class BatchDecoder:
                      seed: int = 0) -> list[list[int]]:
         """Continuations (``max_tokens`` each) of one prompt per sequence, greedy or sampled.
 
-        Each prompt is prefilled, then the batch is stepped with the tokens fed
-        back on the device: no host synchronisation until the end.
+        The prompts are prefilled together in one forward, then the batch is
+        stepped with the tokens fed back on the device: no host synchronisation
+        until the end.
         """
         if len(prompts) != self.batch_size:
             raise ValueError(f"expected {self.batch_size} prompts")
@@ -511,13 +544,13 @@ class BatchDecoder:
             self._check(b, len(ids) + max_tokens - 1)
         if temperature > 0:
             first_t = torch.empty(self.batch_size, dtype=torch.int32, device=self._dev)
-            for b, ids in enumerate(prompts):
-                _, lg = self.prefill(b, ids, return_logits=True)
-                pos = torch.tensor([self._positions[b] - 1], dtype=torch.int64, device=self._dev)
-                self._ops.sample(lg[None, :].contiguous(), float(temperature), int(top_k), float(top_p), int(seed),
-                                 pos + (b << 32), first_t[b:b + 1])
+            _, lg = self.prefill_all(prompts, return_logits=True)
+            # counter of the draw after each prompt: its last position + (sequence << 32)
+            last = torch.tensor([p - 1 for p in self._positions], dtype=torch.int32, device=self._dev)
+            self._ops.sample(lg, float(temperature), int(top_k), float(top_p), int(seed), self._counters(last),
+                             first_t)
         else:
-            first_t = _as_i32([self.prefill(b, ids) for b, ids in enumerate(prompts)], self._dev)
+            first_t = _as_i32(self.prefill_all(prompts), self._dev)
         log = self.decode_steps(first_t, max_tokens - 1, temperature, top_k, top_p, seed)
         out = log.t().cpu().tolist()
         if any(t < 0 for row in out for t in row):

@@ -214,6 +214,32 @@ def test_batch_generate_matches_oracle_streams(weights_gpu, batch_case):
     assert bd.positions == [len(p) + 10 for p in prompts]
 
 
+def test_prefill_all_matches_per_sequence_prefill(shape, weights_gpu):
+    """Three prompts of different lengths in one forward (tokens of three sequences interleaved in
+    one batch, each attending only to its own cache) against one prefill per sequence: the same
+    logits to the decode bar, the same positions, and the next batched step continues alike."""
+    from qwen_megakernel_amd.model import BatchDecoder
+    from qwen_megakernel_amd.weights import make_prompt
+
+    prompts = [make_prompt(m, shape.vocab, seed=50 + m) for m in (5, 17, 33)]
+    one = BatchDecoder(weights=weights_gpu, batch_size=3, max_seq_len=128, verbose=False)
+    each = BatchDecoder(weights=weights_gpu, batch_size=3, max_seq_len=128, verbose=False)
+    toks, lg = one.prefill_all(prompts, return_logits=True)
+    ref = [each.prefill(b, p, return_logits=True) for b, p in enumerate(prompts)]
+    assert one.positions == each.positions == [5, 17, 33]
+    for b in range(3):
+        r = ref[b][1].cpu()
+        top2 = torch.topk(r, 2).values
+        _check_step(b, lg[b].cpu(), r, toks[b], ref[b][0], float(top2[0] - top2[1]))
+    feed = [ref[b][0] for b in range(3)]  # the same inputs to both
+    s1, l1 = one.step_logits(feed)
+    s2, l2 = each.step_logits(feed)
+    for b in range(3):
+        r = l2[b].cpu()
+        top2 = torch.topk(r, 2).values
+        _check_step(b, l1[b].cpu(), r, s1[b], s2[b], float(top2[0] - top2[1]))
+
+
 @pytest.mark.parametrize("n", [8, 40], ids=["8tok-split", "40tok-rowwise"])
 def test_long_context_prefill(shape, weights_cpu, weights_gpu, n):
     """Prefill after an injected N(0,1) cache of 2100 positions: the row-wise attention takes two

@@ -187,8 +187,9 @@ def test_batch_sampled_generate_matches_host_loop(shape, weights_gpu):
     bd = BatchDecoder(weights=weights_gpu, batch_size=2, max_seq_len=256, verbose=False)
     out = bd.generate_ids(prompts, n, temperature=T, top_k=k, top_p=p, seed=seed)
     ref = BatchDecoder(weights=weights_gpu, batch_size=2, max_seq_len=256, verbose=False)
+    _, lg_all = ref.prefill_all(prompts, return_logits=True)  # the prompts in one forward, as generate_ids
     for b, pr in enumerate(prompts):
-        _, lg = ref.prefill(b, pr, return_logits=True)
+        lg = lg_all[b]
         c = (len(pr) - 1) + (b << 32)
         want = S.sample_row(lg.cpu().numpy(), T, k, p, seed, c)[0]
         assert out[b][0] == want or _explained(lg.cpu().numpy(), T, k, p, seed, c, out[b][0])
