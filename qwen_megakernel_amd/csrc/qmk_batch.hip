@@ -38,6 +38,8 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kD = 128, kNQ = 16, kNKV = 8, kQS = kNQ * kD, kNQKV = (kNQ + 2 * kNKV) * kD;
 constexpr int kAttnChunk = 2048;  // one-kernel attention: scores of this many positions per LDS pass
+constexpr int kQT = 64, kKB = 64, kKPad = kD + 8, kVPad = kKB + 8;  // MFMA prefill attention tiles
+constexpr int kMfmaAttnFrom = 1024;  // tokens or context positions from which attention_mfma runs
 constexpr int kSplitChunk = 64;   // split attention: positions per workgroup
 constexpr int kSplitBelow = 32;   // fewer tokens than this use the split attention
 constexpr int kTargetWaves = 2048;
@@ -481,11 +483,13 @@ __device__ __forceinline__ float pv_merge_waves(const float (&acc)[2][2], float 
 // kAttnChunk are processed in chunks, recomputing the scores in each of the
 // three passes (max, sum, P@V) instead of keeping them.
 __global__ void __launch_bounds__(256) attention_rows(const uint16_t* __restrict__ Q, const Tok* __restrict__ tok,
-                                                      int L, Cache c, float scale, uint16_t* __restrict__ out) {
+                                                      int L, Cache c, float scale, uint16_t* __restrict__ out,
+                                                      const int* __restrict__ redo) {
   __shared__ float sc[2][kAttnChunk];
   __shared__ float red[2][4];
   __shared__ float pv[4][2][kD];
   const int t = blockIdx.x, g = blockIdx.y, t16 = threadIdx.x & 15;
+  if (redo && redo[t / kQT] == 0) return;  // attention_mfma covered this token's tile
   const Tok tk = tok[t];
   uint16_t* dst = out + (size_t)t * kQS + 2 * g * kD;  // both heads: 256 contiguous values
   if (!tk.valid) {
@@ -536,6 +540,221 @@ __global__ void __launch_bounds__(256) attention_rows(const uint16_t* __restrict
     pv_chunk(vc + (size_t)c0 * kD, sc[0], sc[1], n, acc);
   }
   dst[threadIdx.x] = (uint16_t)f32_to_bf16(pv_merge_waves(acc, pv));
+}
+
+// Prompt prefill attention on MFMA.  One workgroup of 4 waves per (tile of kQT
+// consecutive tokens, KV head g): when the tile's tokens are one sequence at
+// consecutive positions (every prompt prefill), the tile's query rows of heads
+// 2g and 2g+1 share each block of kKB cached keys and values, staged through
+// LDS, instead of every row reading its whole context.  Two passes over the
+// keys, as HF's eager softmax: pass 1 gives each row's max M and sum L of
+// exp(s - M) (per lane online over the blocks, then across the lanes); pass 2
+// recomputes the scores, rounds the probabilities bf16(exp(s - M) / L) and
+// multiplies them with V on MFMA.  Scores are bf16(bf16(q.k) * scale), as in
+// attention_rows.  A tile that is not one such run (several sequences, an
+// invalid token) is marked in redo[tile] and left to attention_rows.
+//
+// MFMA 16x16x32 bf16 layout: lane l supplies A[l%16][8(l/16)..+7] and
+// B[8(l/16)..+7][l%16] and receives C[4(l/16)+i][l%16].  Wave w owns query rows
+// 16w..16w+15 of the tile.  Scores: A = the rows' q (dims as k), B = K rows of
+// the block (its positions as columns).  P@V: A = the wave's probabilities
+// (positions as k, through LDS), B = V transposed in LDS (dims as columns).
+__global__ void __launch_bounds__(256) attention_mfma(const uint16_t* __restrict__ Q, const Tok* __restrict__ tok,
+                                                      int T, int L, Cache c, float scale,
+                                                      uint16_t* __restrict__ out, int* __restrict__ redo) {
+  __shared__ __align__(16) uint16_t Ks[kKB][kKPad];
+  __shared__ __align__(16) uint16_t Vt[kD][kVPad];
+  __shared__ __align__(16) uint16_t Ps[4][2][16][kVPad];
+  __shared__ int s_ok;
+  const int tile = blockIdx.x, g = blockIdx.y;
+  const int t0 = tile * kQT, nrows = min(kQT, T - t0);
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, l16 = lane & 15, lg = lane >> 4;
+  const Tok first = tok[t0];
+  if (threadIdx.x == 0) s_ok = 1;
+  __syncthreads();
+  if ((int)threadIdx.x < nrows) {
+    const Tok tk = tok[t0 + threadIdx.x];
+    if (!tk.valid || tk.seq != first.seq || tk.pos != first.pos + (int)threadIdx.x) s_ok = 0;
+  }
+  __syncthreads();
+  const bool ok = s_ok != 0;
+  if (g == 0 && threadIdx.x == 0) redo[tile] = ok ? 0 : 1;
+  if (!ok) return;
+  const int pos0 = first.pos, pmax = pos0 + nrows - 1;
+  const size_t base = cache_base(c, first, L, g);
+  const uint16_t* kc = c.k + base;
+  const uint16_t* vc = c.v + base;
+  // A operands of this lane's query row (rows past the tile's tokens repeat its last one)
+  const int tq = t0 + min(16 * w + l16, nrows - 1);
+  bf16x8 qa[2][4];
+#pragma unroll
+  for (int h = 0; h < 2; h++)
+#pragma unroll
+    for (int kk = 0; kk < 4; kk++) qa[h][kk] = ld_bf16x8(Q + (size_t)tq * kQS + (2 * g + h) * kD + 32 * kk + 8 * lg);
+  // positions of the rows this lane's accumulators hold: rows 16w + 4lg + i
+  int rpos[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) rpos[i] = pos0 + 16 * w + 4 * lg + i;
+  const int wave_last = pos0 + 16 * w + 15;  // the wave's largest row position
+  const int nkb = (pmax + kKB) / kKB;        // blocks covering positions 0..pmax
+  // Block kb: positions kb*kKB + pr; rows past pmax load row pmax (masked
+  // below).  Each thread carries two 16-byte chunks of K (and of V): block kb+1
+  // is requested into registers before block kb's MFMAs, so its memory latency
+  // overlaps them, and written to LDS after the next barrier.
+  constexpr int kCh = kKB * (kD / 8) / 256;  // 16-byte chunks per thread per block
+  u32x4 rk[kCh], rv[kCh];
+  auto load_k = [&](int kb) {
+#pragma unroll
+    for (int j = 0; j < kCh; j++) {
+      const int ci = threadIdx.x + 256 * j, pr = ci >> 4, col = (ci & 15) * 8;
+      rk[j] = ld16(kc + (size_t)min(kb * kKB + pr, pmax) * kD + col);
+    }
+  };
+  auto load_v = [&](int kb) {
+#pragma unroll
+    for (int j = 0; j < kCh; j++) {
+      const int ci = threadIdx.x + 256 * j, pr = ci >> 4, col = (ci & 15) * 8;
+      rv[j] = ld16(vc + (size_t)min(kb * kKB + pr, pmax) * kD + col);
+    }
+  };
+  auto put_k = [&]() {
+#pragma unroll
+    for (int j = 0; j < kCh; j++) {
+      const int ci = threadIdx.x + 256 * j, pr = ci >> 4, col = (ci & 15) * 8;
+      *reinterpret_cast<u32x4*>(&Ks[pr][col]) = rk[j];
+    }
+  };
+  auto put_v = [&]() {  // transposed: Vt[dim][position]
+#pragma unroll
+    for (int j = 0; j < kCh; j++) {
+      const int ci = threadIdx.x + 256 * j, pr = ci >> 4, col = (ci & 15) * 8;
+      const uint32_t u[4] = {rv[j].x, rv[j].y, rv[j].z, rv[j].w};
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        Vt[col + 2 * e][pr] = (uint16_t)(u[e] & 0xffffu);
+        Vt[col + 2 * e + 1][pr] = (uint16_t)(u[e] >> 16);
+      }
+    }
+  };
+  // raw q.k of the block's positions kb*kKB + 16n + l16 for rows 4lg + i (both heads)
+  auto tile_scores = [&](int n, f32x4 (&sc)[2]) {
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      sc[h] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kk = 0; kk < 4; kk++)
+        sc[h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+            qa[h][kk], *reinterpret_cast<const bf16x8*>(&Ks[16 * n + l16][32 * kk + 8 * lg]), sc[h], 0, 0, 0);
+    }
+  };
+  // ---- pass 1: per lane, online max and sum of exp over its positions
+  float m[2][4], ls[2][4];
+#pragma unroll
+  for (int h = 0; h < 2; h++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      m[h][i] = -INFINITY;
+      ls[h][i] = 0.f;
+    }
+  load_k(0);
+  for (int kb = 0; kb < nkb; kb++) {
+    __syncthreads();  // the previous block's reads are done
+    put_k();
+    __syncthreads();
+    if (kb + 1 < nkb) load_k(kb + 1);
+    if (kb * kKB > wave_last) continue;  // every position of the block follows the wave's rows
+#pragma unroll
+    for (int n = 0; n < kKB / 16; n++) {
+      if (kb * kKB + 16 * n > wave_last) break;
+      f32x4 sc[2];
+      tile_scores(n, sc);
+      const int p = kb * kKB + 16 * n + l16;
+#pragma unroll
+      for (int h = 0; h < 2; h++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          if (p <= rpos[i]) {
+            const float x = bf16r(bf16r(sc[h][i]) * scale);
+            const float mn = fmaxf(m[h][i], x);
+            ls[h][i] = ls[h][i] * exp_acc(m[h][i] - mn) + exp_acc(x - mn);
+            m[h][i] = mn;
+          }
+        }
+    }
+  }
+  // each row's M and 1/L over its 16 lanes (lanes with equal lg hold the same rows)
+  float gm[2][4], ginv[2][4];
+#pragma unroll
+  for (int h = 0; h < 2; h++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      float mx = m[h][i];
+#pragma unroll
+      for (int o = 1; o < 16; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+      float sm = m[h][i] == -INFINITY ? 0.f : ls[h][i] * exp_acc(m[h][i] - mx);
+#pragma unroll
+      for (int o = 1; o < 16; o <<= 1) sm += __shfl_xor(sm, o);
+      gm[h][i] = mx;
+      ginv[h][i] = __fdiv_rn(1.0f, sm);
+    }
+  // ---- pass 2: probabilities (bf16, as HF rounds them) times V
+  f32x4 acc[2][8];
+#pragma unroll
+  for (int h = 0; h < 2; h++)
+#pragma unroll
+    for (int j = 0; j < 8; j++) acc[h][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  load_k(0);
+  load_v(0);
+  for (int kb = 0; kb < nkb; kb++) {
+    __syncthreads();
+    put_k();
+    put_v();
+    __syncthreads();
+    if (kb + 1 < nkb) {
+      load_k(kb + 1);
+      load_v(kb + 1);
+    }
+    if (kb * kKB > wave_last) continue;
+#pragma unroll
+    for (int n = 0; n < kKB / 16; n++) {
+      f32x4 sc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+      if (kb * kKB + 16 * n <= wave_last) tile_scores(n, sc);  // otherwise every row masks the tile
+      const int p = kb * kKB + 16 * n + l16;
+#pragma unroll
+      for (int h = 0; h < 2; h++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const float pr =
+              p <= rpos[i] ? bf16r(exp_acc(bf16r(bf16r(sc[h][i]) * scale) - gm[h][i]) * ginv[h][i]) : 0.f;
+          Ps[w][h][4 * lg + i][16 * n + l16] = (uint16_t)f32_to_bf16(pr);
+        }
+    }
+    // the wave's own probabilities, written by its lanes, read back in the A layout
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int ks = 0; ks < kKB / 32; ks++)
+#pragma unroll
+      for (int h = 0; h < 2; h++) {
+        const bf16x8 pa = *reinterpret_cast<const bf16x8*>(&Ps[w][h][l16][32 * ks + 8 * lg]);
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+          acc[h][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              pa, *reinterpret_cast<const bf16x8*>(&Vt[16 * j + l16][32 * ks + 8 * lg]), acc[h][j], 0, 0, 0);
+      }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int r = 16 * w + 4 * lg + i;
+    if (r < nrows) {
+      uint16_t* dst = out + (size_t)(t0 + r) * kQS + 2 * g * kD;
+#pragma unroll
+      for (int h = 0; h < 2; h++)
+#pragma unroll
+        for (int j = 0; j < 8; j++) dst[h * kD + 16 * j + l16] = (uint16_t)f32_to_bf16(acc[h][j][i]);
+    }
+  }
 }
 
 // Few tokens: the context of each (token, KV head) is split over workgroups of
@@ -1262,7 +1481,7 @@ size_t part_floats(int T, int N, int K) { return (size_t)plan_gemm(T, N, K).kspl
 int split_chunks(int max_context) { return (max_context + kSplitChunk - 1) / kSplitChunk; }
 
 struct Layout {
-  size_t tok, erow, keys, x, n, q, att, m, qkv, part, scores, ml, pv, total;
+  size_t tok, erow, keys, x, n, q, att, m, qkv, part, scores, ml, pv, redo, total;
 };
 
 constexpr int kLmTiles(int V) { return V / 64; }
@@ -1303,6 +1522,8 @@ Layout layout(int T, int R, int max_context, bool one_per_seq = false) {
     take(l.scores, (size_t)T * kNQ * nch * kSplitChunk * 4);
     take(l.ml, (size_t)T * kNQ * nch * 8);
     take(l.pv, (size_t)T * nch * kQS * 4);
+  } else {
+    take(l.redo, (size_t)((T + kQT - 1) / kQT) * 4);
   }
   l.total = off;
   return l;
@@ -1438,6 +1659,9 @@ int forward(const Args& a, hipStream_t s) {
   const float eps = 1e-6f;
   const bool split = T < kSplitBelow;
   const int nch = split ? split_chunks(a.max_context) : 0;
+  // attention_mfma pays off from about 1024 tokens or 1024 positions of context
+  // (below that the row kernel's per-token reads are cheaper than its passes)
+  const bool mfma_attn = !split && (T >= kMfmaAttnFrom || a.max_context >= kMfmaAttnFrom);
   auto blocks = [](size_t n) { return dim3((unsigned)((n + 255) / 256)); };
   auto u16 = [](const void* p) { return static_cast<const uint16_t*>(p); };
   int ks = 1;
@@ -1462,7 +1686,17 @@ int forward(const Args& a, hipStream_t s) {
       hipLaunchKernelGGL(attn_split_pv, dim3(T, kNKV, nch), dim3(256), 0, s, tok, L, a.cache, nch, scores, ml, pvp);
       hipLaunchKernelGGL(attn_split_merge, dim3(T, kQS / 256), dim3(256), 0, s, tok, nch, pvp, ATT);
     } else {
-      hipLaunchKernelGGL(attention_rows, dim3(T, kNKV), dim3(256), 0, s, Qb, tok, L, a.cache, a.attn_scale, ATT);
+      if (mfma_attn) {
+        // tiles of one sequence's consecutive tokens on MFMA; any other tile row by row
+        int* redo = reinterpret_cast<int*>(a.ws + l.redo);
+        hipLaunchKernelGGL(attention_mfma, dim3((T + kQT - 1) / kQT, kNKV), dim3(256), 0, s, Qb, tok, T, L,
+                           a.cache, a.attn_scale, ATT, redo);
+        hipLaunchKernelGGL(attention_rows, dim3(T, kNKV), dim3(256), 0, s, Qb, tok, L, a.cache, a.attn_scale, ATT,
+                           redo);
+      } else {
+        hipLaunchKernelGGL(attention_rows, dim3(T, kNKV), dim3(256), 0, s, Qb, tok, L, a.cache, a.attn_scale, ATT,
+                           nullptr);
+      }
     }
     const Seg o{{u16(w.o_proj_weight), nullptr, nullptr}, {Dm::H, 0, 0}};
     launch_gemm(ATT, nullptr, T, kQS, o, Dm::H, part, s, &ks);

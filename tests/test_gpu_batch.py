@@ -214,6 +214,38 @@ def test_batch_generate_matches_oracle_streams(weights_gpu, batch_case):
     assert bd.positions == [len(p) + 10 for p in prompts]
 
 
+def test_long_two_sequence_prefill_mfma_attention(shape, weights_cpu, weights_gpu):
+    """1100 tokens of two sequences (600 + 500) in one forward, 2 layers: the MFMA attention
+    (1024+ tokens) over 64-token tiles, a partial last tile and the tile holding the end of
+    sequence 0 and the start of sequence 1 (row-by-row fallback); every 50th row of each
+    sequence and each sequence's last row against its own oracle, and a repeat bit-exact."""
+    from oracle.qwen3_ref import OracleDecoder
+    from qwen_megakernel_amd.model import BatchDecoder
+    from qwen_megakernel_amd.weights import make_prompt
+
+    layers, lens = 2, (600, 500)
+    prompts = [make_prompt(n, shape.vocab, seed=70 + i) for i, n in enumerate(lens)]
+    refs = [_oracle_feed(OracleDecoder(weights_cpu, shape, num_layers=layers, max_seq_len=1024), p) for p in prompts]
+    bd = BatchDecoder(weights=weights_gpu, batch_size=2, max_seq_len=1024, num_layers=layers, verbose=False)
+    toks = prompts[0] + prompts[1]
+    seqs = [0] * lens[0] + [1] * lens[1]
+    pos = list(range(lens[0])) + list(range(lens[1]))
+    rows = [(0, i) for i in list(range(0, lens[0], 50)) + [lens[0] - 1]]
+    rows += [(1, i) for i in list(range(0, lens[1], 50)) + [lens[1] - 1]]
+    emit = [i if s == 0 else lens[0] + i for s, i in rows]
+    runs = []
+    for _ in range(2):
+        out = torch.empty(len(emit), dtype=torch.int32, device="cuda")
+        logits = torch.empty(len(emit), V, dtype=torch.float32, device="cuda")
+        bd._forward(_i32(toks), _i32(seqs), _i32(pos), _i32(emit), out, logits, bd._k_cache, bd._v_cache, max(lens))
+        runs.append((out.cpu().tolist(), logits.cpu()))
+    got, lg = runs[0]
+    assert runs[1][0] == got and torch.equal(runs[1][1], lg), "second forward differs"
+    for r, (sq, i) in enumerate(rows):
+        ref = refs[sq]
+        _check_step(i, lg[r], ref["logits"][i], got[r], ref["tokens"][i], ref["gaps"][i])
+
+
 def test_prefill_all_matches_per_sequence_prefill(shape, weights_gpu):
     """Three prompts of different lengths in one forward (tokens of three sequences interleaved in
     one batch, each attending only to its own cache) against one prefill per sequence: the same
@@ -423,12 +455,12 @@ def test_decode_batch_equals_general_forward(weights_gpu):
     assert cos >= 0.999, cos
 
 
-@pytest.mark.parametrize("n", [128, 300], ids=["128tok-64col-tiles", "300tok-mixed-tiles"])
+@pytest.mark.parametrize("n", [128, 200, 300], ids=["128tok-64col-tiles", "200tok-128col-tiles", "300tok-mixed-tiles"])
 def test_long_prefill_tiled_gemm(shape, weights_cpu, weights_gpu, n):
     """Prefills of 96+ tokens take the LDS-tiled MFMA GEMM: every 25th row and the last against
-    the oracle, 2 layers.  128 tokens: 64-column tiles for all four projections, o and down split
-    16 ways over K; 300 tokens: 128-column tiles (a partial last row tile) and 64-column tiles
-    for down."""
+    the oracle, 2 layers, and a second identical forward bit-exact.  128 tokens: 64-column tiles
+    for all four projections, o and down split 16 ways over K; 200 tokens: 128-column tiles with
+    a partial last row tile; 300 tokens: 128-column tiles and 64-column tiles for down."""
     from oracle.qwen3_ref import OracleDecoder
     from qwen_megakernel_amd.weights import make_prompt
 
@@ -437,11 +469,15 @@ def test_long_prefill_tiled_gemm(shape, weights_cpu, weights_gpu, n):
     ref = _oracle_feed(OracleDecoder(weights_cpu, shape, num_layers=layers, max_seq_len=512), ids)
     dec = _decoder(weights_gpu, num_layers=layers, max_seq_len=512)
     emit = list(range(0, n, 25)) + [n - 1]
-    out = torch.empty(len(emit), dtype=torch.int32, device="cuda")
-    logits = torch.empty(len(emit), V, dtype=torch.float32, device="cuda")
-    dec._forward(_i32(ids), torch.zeros(n, dtype=torch.int32, device="cuda"),
-                 torch.arange(n, dtype=torch.int32, device="cuda"), _i32(emit), out, logits, dec._k_cache,
-                 dec._v_cache, n)
-    toks, lg = out.cpu().tolist(), logits.cpu()
+    runs = []
+    for _ in range(2):
+        out = torch.empty(len(emit), dtype=torch.int32, device="cuda")
+        logits = torch.empty(len(emit), V, dtype=torch.float32, device="cuda")
+        dec._forward(_i32(ids), torch.zeros(n, dtype=torch.int32, device="cuda"),
+                     torch.arange(n, dtype=torch.int32, device="cuda"), _i32(emit), out, logits, dec._k_cache,
+                     dec._v_cache, n)
+        runs.append((out.cpu().tolist(), logits.cpu()))
+    toks, lg = runs[0]
+    assert runs[1][0] == toks and torch.equal(runs[1][1], lg), "second forward differs"
     for r, e in enumerate(emit):
         _check_step(e, lg[r], ref["logits"][e], toks[r], ref["tokens"][e], ref["gaps"][e])
