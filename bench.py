@@ -28,7 +28,8 @@ device-fed greedy steps at batch 1 on the decode megakernel (context
 256 device-fed steps of the batched forward (MFMA GEMMs), in tok/s over all
 four and algorithmic GB/s per step (weights once + each sequence's KV).
 
-``prefill``: the 128-token prompt through the batched forward, ms and tok/s.
+``prefill``: the 128-token prompt through the batched forward, ms and tok/s;
+``prefill_long``: a 2048-token prompt the same way (its attention on MFMA).
 
 ``sampling`` (skip with ``--no-sampling``): the same prompt and model, 512
 device-fed steps of the sampled generate loop (counter-based Gumbel-max draws,
@@ -404,6 +405,7 @@ def main():
     del dec  # frees the 128-token run's caches; the weights stay for the long-context runs
     torch.cuda.empty_cache()
     result["prefill"] = prefill_rate(w)
+    result["prefill_long"] = prefill_rate(w, 2048, iters=5)
     if not args.no_long_context:
         result["long_context"] = long_context(w, args.long_steps)
     del w
