@@ -542,7 +542,7 @@ __global__ void __launch_bounds__(256) attention_rows(const uint16_t* __restrict
   dst[threadIdx.x] = (uint16_t)f32_to_bf16(pv_merge_waves(acc, pv));
 }
 
-// Prompt prefill attention on MFMA.  One workgroup of 4 waves per (tile of kQT
+// Prompt prefill attention on MFMA.  One workgroup of 8 waves per (tile of kQT
 // consecutive tokens, KV head g): when the tile's tokens are one sequence at
 // consecutive positions (every prompt prefill), the tile's query rows of heads
 // 2g and 2g+1 share each block of kKB cached keys and values, staged through
@@ -556,19 +556,26 @@ __global__ void __launch_bounds__(256) attention_rows(const uint16_t* __restrict
 //
 // MFMA 16x16x32 bf16 layout: lane l supplies A[l%16][8(l/16)..+7] and
 // B[8(l/16)..+7][l%16] and receives C[4(l/16)+i][l%16].  Wave w owns query rows
-// 16w..16w+15 of the tile.  Scores: A = the rows' q (dims as k), B = K rows of
-// the block (its positions as columns).  P@V: A = the wave's probabilities
-// (positions as k, through LDS), B = V transposed in LDS (dims as columns).
-__global__ void __launch_bounds__(256) attention_mfma(const uint16_t* __restrict__ Q, const Tok* __restrict__ tok,
-                                                      int T, int L, Cache c, float scale,
-                                                      uint16_t* __restrict__ out, int* __restrict__ redo) {
+// 16(w/2)..+15 of the tile for q head 2g + w%2 (the two heads of a row group in
+// two waves: half the serial work per wave, two waves per SIMD).  Scores: A =
+// the rows' q (dims as k), B = K rows of the block (its positions as columns).
+// P@V: A = the wave's probabilities (positions as k, through LDS), B = V
+// transposed in LDS (dims as columns).
+constexpr int kAttnWaves = 8;
+
+__global__ void __launch_bounds__(kAttnWaves * 64) attention_mfma(const uint16_t* __restrict__ Q,
+                                                                 const Tok* __restrict__ tok, int T, int L, Cache c,
+                                                                 float scale, uint16_t* __restrict__ out,
+                                                                 int* __restrict__ redo) {
+  constexpr int NT = kAttnWaves * 64;
   __shared__ __align__(16) uint16_t Ks[kKB][kKPad];
   __shared__ __align__(16) uint16_t Vt[kD][kVPad];
-  __shared__ __align__(16) uint16_t Ps[4][2][16][kVPad];
+  __shared__ __align__(16) uint16_t Ps[kAttnWaves][16][kVPad];
   __shared__ int s_ok;
   const int tile = blockIdx.x, g = blockIdx.y;
   const int t0 = tile * kQT, nrows = min(kQT, T - t0);
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, l16 = lane & 15, lg = lane >> 4;
+  const int hq = w & 1, rg = w >> 1;  // q head 2g + hq, rows 16rg..16rg+15
   const Tok first = tok[t0];
   if (threadIdx.x == 0) s_ok = 1;
   __syncthreads();
@@ -585,49 +592,47 @@ __global__ void __launch_bounds__(256) attention_mfma(const uint16_t* __restrict
   const uint16_t* kc = c.k + base;
   const uint16_t* vc = c.v + base;
   // A operands of this lane's query row (rows past the tile's tokens repeat its last one)
-  const int tq = t0 + min(16 * w + l16, nrows - 1);
-  bf16x8 qa[2][4];
+  const int tq = t0 + min(16 * rg + l16, nrows - 1);
+  bf16x8 qa[4];
 #pragma unroll
-  for (int h = 0; h < 2; h++)
-#pragma unroll
-    for (int kk = 0; kk < 4; kk++) qa[h][kk] = ld_bf16x8(Q + (size_t)tq * kQS + (2 * g + h) * kD + 32 * kk + 8 * lg);
-  // positions of the rows this lane's accumulators hold: rows 16w + 4lg + i
+  for (int kk = 0; kk < 4; kk++) qa[kk] = ld_bf16x8(Q + (size_t)tq * kQS + (2 * g + hq) * kD + 32 * kk + 8 * lg);
+  // positions of the rows this lane's accumulators hold: rows 16rg + 4lg + i
   int rpos[4];
 #pragma unroll
-  for (int i = 0; i < 4; i++) rpos[i] = pos0 + 16 * w + 4 * lg + i;
-  const int wave_last = pos0 + 16 * w + 15;  // the wave's largest row position
-  const int nkb = (pmax + kKB) / kKB;        // blocks covering positions 0..pmax
+  for (int i = 0; i < 4; i++) rpos[i] = pos0 + 16 * rg + 4 * lg + i;
+  const int wave_last = pos0 + 16 * rg + 15;  // the wave's largest row position
+  const int nkb = (pmax + kKB) / kKB;         // blocks covering positions 0..pmax
   // Block kb: positions kb*kKB + pr; rows past pmax load row pmax (masked
-  // below).  Each thread carries two 16-byte chunks of K (and of V): block kb+1
+  // below).  Each thread carries kCh 16-byte chunks of K (and of V): block kb+1
   // is requested into registers before block kb's MFMAs, so its memory latency
   // overlaps them, and written to LDS after the next barrier.
-  constexpr int kCh = kKB * (kD / 8) / 256;  // 16-byte chunks per thread per block
+  constexpr int kCh = kKB * (kD / 8) / NT;
   u32x4 rk[kCh], rv[kCh];
   auto load_k = [&](int kb) {
 #pragma unroll
     for (int j = 0; j < kCh; j++) {
-      const int ci = threadIdx.x + 256 * j, pr = ci >> 4, col = (ci & 15) * 8;
+      const int ci = threadIdx.x + NT * j, pr = ci >> 4, col = (ci & 15) * 8;
       rk[j] = ld16(kc + (size_t)min(kb * kKB + pr, pmax) * kD + col);
     }
   };
   auto load_v = [&](int kb) {
 #pragma unroll
     for (int j = 0; j < kCh; j++) {
-      const int ci = threadIdx.x + 256 * j, pr = ci >> 4, col = (ci & 15) * 8;
+      const int ci = threadIdx.x + NT * j, pr = ci >> 4, col = (ci & 15) * 8;
       rv[j] = ld16(vc + (size_t)min(kb * kKB + pr, pmax) * kD + col);
     }
   };
   auto put_k = [&]() {
 #pragma unroll
     for (int j = 0; j < kCh; j++) {
-      const int ci = threadIdx.x + 256 * j, pr = ci >> 4, col = (ci & 15) * 8;
+      const int ci = threadIdx.x + NT * j, pr = ci >> 4, col = (ci & 15) * 8;
       *reinterpret_cast<u32x4*>(&Ks[pr][col]) = rk[j];
     }
   };
   auto put_v = [&]() {  // transposed: Vt[dim][position]
 #pragma unroll
     for (int j = 0; j < kCh; j++) {
-      const int ci = threadIdx.x + 256 * j, pr = ci >> 4, col = (ci & 15) * 8;
+      const int ci = threadIdx.x + NT * j, pr = ci >> 4, col = (ci & 15) * 8;
       const uint32_t u[4] = {rv[j].x, rv[j].y, rv[j].z, rv[j].w};
 #pragma unroll
       for (int e = 0; e < 4; e++) {
@@ -636,26 +641,22 @@ __global__ void __launch_bounds__(256) attention_mfma(const uint16_t* __restrict
       }
     }
   };
-  // raw q.k of the block's positions kb*kKB + 16n + l16 for rows 4lg + i (both heads)
-  auto tile_scores = [&](int n, f32x4 (&sc)[2]) {
+  // raw q.k of the block's positions kb*kKB + 16n + l16 for rows 4lg + i
+  auto tile_scores = [&](int n) {
+    f32x4 sc = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int h = 0; h < 2; h++) {
-      sc[h] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int kk = 0; kk < 4; kk++)
-        sc[h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-            qa[h][kk], *reinterpret_cast<const bf16x8*>(&Ks[16 * n + l16][32 * kk + 8 * lg]), sc[h], 0, 0, 0);
-    }
+    for (int kk = 0; kk < 4; kk++)
+      sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+          qa[kk], *reinterpret_cast<const bf16x8*>(&Ks[16 * n + l16][32 * kk + 8 * lg]), sc, 0, 0, 0);
+    return sc;
   };
   // ---- pass 1: per lane, online max and sum of exp over its positions
-  float m[2][4], ls[2][4];
+  float m[4], ls[4];
 #pragma unroll
-  for (int h = 0; h < 2; h++)
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      m[h][i] = -INFINITY;
-      ls[h][i] = 0.f;
-    }
+  for (int i = 0; i < 4; i++) {
+    m[i] = -INFINITY;
+    ls[i] = 0.f;
+  }
   load_k(0);
   for (int kb = 0; kb < nkb; kb++) {
     __syncthreads();  // the previous block's reads are done
@@ -666,43 +667,36 @@ __global__ void __launch_bounds__(256) attention_mfma(const uint16_t* __restrict
 #pragma unroll
     for (int n = 0; n < kKB / 16; n++) {
       if (kb * kKB + 16 * n > wave_last) break;
-      f32x4 sc[2];
-      tile_scores(n, sc);
+      const f32x4 sc = tile_scores(n);
       const int p = kb * kKB + 16 * n + l16;
 #pragma unroll
-      for (int h = 0; h < 2; h++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-          if (p <= rpos[i]) {
-            const float x = bf16r(bf16r(sc[h][i]) * scale);
-            const float mn = fmaxf(m[h][i], x);
-            ls[h][i] = ls[h][i] * exp_acc(m[h][i] - mn) + exp_acc(x - mn);
-            m[h][i] = mn;
-          }
+      for (int i = 0; i < 4; i++) {
+        if (p <= rpos[i]) {
+          const float x = bf16r(bf16r(sc[i]) * scale);
+          const float mn = fmaxf(m[i], x);
+          ls[i] = ls[i] * exp_acc(m[i] - mn) + exp_acc(x - mn);
+          m[i] = mn;
         }
+      }
     }
   }
   // each row's M and 1/L over its 16 lanes (lanes with equal lg hold the same rows)
-  float gm[2][4], ginv[2][4];
+  float gm[4], ginv[4];
 #pragma unroll
-  for (int h = 0; h < 2; h++)
+  for (int i = 0; i < 4; i++) {
+    float mx = m[i];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      float mx = m[h][i];
+    for (int o = 1; o < 16; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    float sm = m[i] == -INFINITY ? 0.f : ls[i] * exp_acc(m[i] - mx);
 #pragma unroll
-      for (int o = 1; o < 16; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
-      float sm = m[h][i] == -INFINITY ? 0.f : ls[h][i] * exp_acc(m[h][i] - mx);
-#pragma unroll
-      for (int o = 1; o < 16; o <<= 1) sm += __shfl_xor(sm, o);
-      gm[h][i] = mx;
-      ginv[h][i] = __fdiv_rn(1.0f, sm);
-    }
+    for (int o = 1; o < 16; o <<= 1) sm += __shfl_xor(sm, o);
+    gm[i] = mx;
+    ginv[i] = __fdiv_rn(1.0f, sm);
+  }
   // ---- pass 2: probabilities (bf16, as HF rounds them) times V
-  f32x4 acc[2][8];
+  f32x4 acc[8];
 #pragma unroll
-  for (int h = 0; h < 2; h++)
-#pragma unroll
-    for (int j = 0; j < 8; j++) acc[h][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int j = 0; j < 8; j++) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
   load_k(0);
   load_v(0);
   for (int kb = 0; kb < nkb; kb++) {
@@ -717,42 +711,35 @@ __global__ void __launch_bounds__(256) attention_mfma(const uint16_t* __restrict
     if (kb * kKB > wave_last) continue;
 #pragma unroll
     for (int n = 0; n < kKB / 16; n++) {
-      f32x4 sc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
-      if (kb * kKB + 16 * n <= wave_last) tile_scores(n, sc);  // otherwise every row masks the tile
+      // a tile wholly past the wave's rows is masked for every row: no MFMA for it
+      const f32x4 sc = kb * kKB + 16 * n <= wave_last ? tile_scores(n) : f32x4{0.f, 0.f, 0.f, 0.f};
       const int p = kb * kKB + 16 * n + l16;
 #pragma unroll
-      for (int h = 0; h < 2; h++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-          const float pr =
-              p <= rpos[i] ? bf16r(exp_acc(bf16r(bf16r(sc[h][i]) * scale) - gm[h][i]) * ginv[h][i]) : 0.f;
-          Ps[w][h][4 * lg + i][16 * n + l16] = (uint16_t)f32_to_bf16(pr);
-        }
+      for (int i = 0; i < 4; i++) {
+        const float pr = p <= rpos[i] ? bf16r(exp_acc(bf16r(bf16r(sc[i]) * scale) - gm[i]) * ginv[i]) : 0.f;
+        Ps[w][4 * lg + i][16 * n + l16] = (uint16_t)f32_to_bf16(pr);
+      }
     }
     // the wave's own probabilities, written by its lanes, read back in the A layout
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
-    for (int ks = 0; ks < kKB / 32; ks++)
+    for (int ks = 0; ks < kKB / 32; ks++) {
+      const bf16x8 pa = *reinterpret_cast<const bf16x8*>(&Ps[w][l16][32 * ks + 8 * lg]);
 #pragma unroll
-      for (int h = 0; h < 2; h++) {
-        const bf16x8 pa = *reinterpret_cast<const bf16x8*>(&Ps[w][h][l16][32 * ks + 8 * lg]);
-#pragma unroll
-        for (int j = 0; j < 8; j++)
-          acc[h][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-              pa, *reinterpret_cast<const bf16x8*>(&Vt[16 * j + l16][32 * ks + 8 * lg]), acc[h][j], 0, 0, 0);
-      }
+      for (int j = 0; j < 8; j++)
+        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+            pa, *reinterpret_cast<const bf16x8*>(&Vt[16 * j + l16][32 * ks + 8 * lg]), acc[j], 0, 0, 0);
+    }
   }
 #pragma unroll
   for (int i = 0; i < 4; i++) {
-    const int r = 16 * w + 4 * lg + i;
+    const int r = 16 * rg + 4 * lg + i;
     if (r < nrows) {
-      uint16_t* dst = out + (size_t)(t0 + r) * kQS + 2 * g * kD;
+      uint16_t* dst = out + (size_t)(t0 + r) * kQS + (2 * g + hq) * kD;
 #pragma unroll
-      for (int h = 0; h < 2; h++)
-#pragma unroll
-        for (int j = 0; j < 8; j++) dst[h * kD + 16 * j + l16] = (uint16_t)f32_to_bf16(acc[h][j][i]);
+      for (int j = 0; j < 8; j++) dst[16 * j + l16] = (uint16_t)f32_to_bf16(acc[j][i]);
     }
   }
 }
@@ -1689,8 +1676,8 @@ int forward(const Args& a, hipStream_t s) {
       if (mfma_attn) {
         // tiles of one sequence's consecutive tokens on MFMA; any other tile row by row
         int* redo = reinterpret_cast<int*>(a.ws + l.redo);
-        hipLaunchKernelGGL(attention_mfma, dim3((T + kQT - 1) / kQT, kNKV), dim3(256), 0, s, Qb, tok, T, L,
-                           a.cache, a.attn_scale, ATT, redo);
+        hipLaunchKernelGGL(attention_mfma, dim3((T + kQT - 1) / kQT, kNKV), dim3(kAttnWaves * 64), 0, s, Qb, tok, T,
+                           L, a.cache, a.attn_scale, ATT, redo);
         hipLaunchKernelGGL(attention_rows, dim3(T, kNKV), dim3(256), 0, s, Qb, tok, L, a.cache, a.attn_scale, ATT,
                            redo);
       } else {
