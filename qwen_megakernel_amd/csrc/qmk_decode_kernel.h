@@ -895,8 +895,21 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
       load_seg_p<Dm::LD>(wd + op * Dm::LD, wd_base + (size_t)rs_row(op) * Dm::I + Dm::MS * xcd, t16);
   };
 
+  // EARLY (short-context form, weights one layer ahead): the weight slices are
+  // requested in the three windows in which the control wave does not poll,
+  // so fewer exchange polls queue behind them (a CU returns vector-memory data
+  // in order): the next layer's QKV slice at barrier c (scores), this layer's
+  // gate/up slice at e (P@V), the next layer's o_proj slice and this layer's
+  // down slice at i (gate/up).  The K/V waits in the first two windows leave
+  // those newer loads outstanding.  Requested right after each compute phase
+  // instead, i.e. just before an exchange: 1,899 against 1,960 tok/s.
+  constexpr bool EARLY = !ST && !LONG;
+  constexpr int NB_C = EARLY ? Dm::RQ_W * Dm::LH : 0;  // loads issued at barrier c
+  constexpr int NB_E = EARLY ? Dm::GU_W * Dm::LH : 0;  // loads issued at barrier e
+  static_assert(NB_C <= 12 && NB_E <= 12, "wait_vmcnt range");
   prefetch_qkv(0);
-  if (!ST) {
+  if (EARLY) prefetch_o(0);
+  if (!ST && !EARLY) {
     prefetch_o(0);
     prefetch_gu(0);
     prefetch_dn(0);
@@ -929,7 +942,7 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
       }
     };
     // wait until batch j has landed: the batches issued after it may stay in flight
-    auto kv_wait = [&](int j) { wait_vmcnt(U * min(kKvStages - 1, nb - 1 - j)); };
+    auto kv_wait = [&](int j, int newer) { wait_vmcnt(U * min(kKvStages - 1, nb - 1 - j) + newer); };
     auto kv_refill = [&](const uint16_t* base, int j) {
       if (j + kKvStages < nb) {
         __builtin_amdgcn_s_waitcnt(kWaitLgkm0);  // this wave's reads of the slot are done
@@ -957,12 +970,19 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
     // Keys of the positions before pos are in the cache already.  Batch 0 is
     // requested while the control wave exchanges q/k/v (the barrier below
     // waits for it, as it waits for every LDS write); the rest of the ring
-    // fills after the barrier, behind the first batch's compute.  The weight
-    // prefetches stay inside the compute phases: issued during an exchange
-    // they delay its polls by as much as they would save here.
+    // fills after the barrier, behind the first batch's compute.  (Requested
+    // right after barrier a instead, batch 0 measured slower: 1,946 against
+    // 1,960 tok/s.)
     if (nb > 0) kv_issue(kc, 0);
     QMK_SYNC();  // c
     for (int j = 1; j < min(nb, kKvStages); j++) kv_issue(kc, j);
+    if constexpr (EARLY) {
+      static_assert(!EARLY || kLongContext / kGroupSize <= 32 * U, "EARLY: at most one K/V batch per wave");
+      // the last layer reloads its own slice, so the waits below count a static
+      // number of loads (8 MB more reads per token; loading a 2 KB row instead
+      // measured no faster)
+      prefetch_qkv(L + 1 < p.nl ? L + 1 : L);
+    }
     cstamp(L, 2);
     // ------------------------------------------------ scores and local (max, sum)
     // position of entry i of this wave's batches (i = 8 batch + 4 u + slot)
@@ -987,7 +1007,7 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
         float mloc = -INFINITY;  // owners: the maximum of head own_h over their positions
         for (int j = 0; j < nb; j++) {
           const int base = base0 + 32 * U * j;
-          kv_wait(j);
+          kv_wait(j, 0);
           const int pp0 = base + slot, pp1 = base + 32 + slot;
           const u32x4 k0 = pp0 == p.pos ? k_now : s.kv[j % kKvStages][c][0][lane];
           const u32x4 k1 = pp1 == p.pos ? k_now : s.kv[j % kKvStages][c][1][lane];
@@ -1050,7 +1070,7 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
         for (int h = 0; h < Dm::GQ; h++) mloc[h] = -INFINITY;
         for (int j = 0; j < nb; j++) {
           const int base = base0 + 32 * U * j;
-          kv_wait(j);
+          if constexpr (EARLY) wait_vmcnt(NB_C); else kv_wait(j, 0);
   #pragma unroll
           for (int u = 0; u < U; u++) {
             if (base + 32 * u >= p.p_end) break;  // the rest of the batch is past this workgroup's range
@@ -1066,12 +1086,12 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
               }
             }
           }
-          kv_refill(kc, j);
+          if constexpr (!EARLY) kv_refill(kc, j);  // EARLY: one batch per wave, no refill
         }
         // Every K batch has landed (the last wait was vmcnt(0)); saying so here
         // lets the compiler drop the vmcnt(0) it would otherwise put before the
         // next workgroup barriers, which would also wait for weight prefetches.
-        wait_vmcnt(0);
+        wait_vmcnt(NB_C);  // the weight slices requested at c may stay in flight
         // wave maximum over the four 16-lane rows, then the sum of exp(s - max)
         // with one exponential per position
   #pragma unroll
@@ -1114,6 +1134,9 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
     if (nb > 0) kv_issue(vc, 0);
     QMK_SYNC();  // e
     for (int j = 1; j < min(nb, kKvStages); j++) kv_issue(vc, j);
+    if constexpr (EARLY) {
+      prefetch_gu(L);
+    }
     cstamp(L, 4);
     // ------------------------------------------------ probabilities and P@V
     if constexpr (LONG)
@@ -1145,7 +1168,7 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
         for (int i = 0; i < 8; i++) acc[h][i] = 0.f;
       for (int j = 0; j < nb; j++) {
         const int base = base0 + 32 * U * j;
-        kv_wait(j);
+        kv_wait(j, 0);
         // the row's two positions are paired in bf16x2 operands: probabilities
         // (head h of both) and values (one dimension of both), so one dot2
         // accumulates two positions; a position past the range has probability 0
@@ -1197,7 +1220,7 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
         for (int i = 0; i < 8; i++) acc[h][i] = 0.f;
       for (int j = 0; j < nb; j++) {
         const int base = base0 + 32 * U * j;
-        kv_wait(j);
+        if constexpr (EARLY) wait_vmcnt(NB_E); else kv_wait(j, 0);
 #pragma unroll
         for (int u = 0; u < U; u++) {
           if (base + 32 * u >= p.p_end) break;
@@ -1215,9 +1238,9 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
             }
           }
         }
-        kv_refill(vc, j);
+        if constexpr (!EARLY) kv_refill(vc, j);  // EARLY: one batch per wave, no refill
       }
-      wait_vmcnt(0);  // every V batch has landed (see above)
+      wait_vmcnt(NB_E);  // every V batch has landed; the slices requested at e may stay in flight
       // sum the wave's four slots; lanes 0..15 then hold dims 8*t16..+7
 #pragma unroll
       for (int h = 0; h < Dm::GQ; h++) {
@@ -1229,7 +1252,7 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
         }
       }
     }
-    if (!ST && L + 1 < p.nl) prefetch_qkv(L + 1);
+    if (!ST && !EARLY && L + 1 < p.nl) prefetch_qkv(L + 1);
     cstamp(L, 5);
     QMK_SYNC();  // f
     QMK_SYNC();  // g
@@ -1245,10 +1268,13 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
       }
     }
     if (ST) prefetch_gu(L);
-    else if (L + 1 < p.nl) prefetch_o(L + 1);
+    else if (!EARLY && L + 1 < p.nl) prefetch_o(L + 1);
     cstamp(L, 7);
     QMK_SYNC();  // i
     cstamp(L, 8);
+    if constexpr (EARLY) {
+      if (L + 1 < p.nl) { prefetch_o(L + 1); } prefetch_dn(L);
+    }
     {
       u32x4 act[Dm::LH];
       load_act(act, s.n, 0, lane);
@@ -1259,7 +1285,7 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
       }
     }
     if (ST) prefetch_dn(L);
-    else if (L + 1 < p.nl) prefetch_gu(L + 1);
+    else if (!EARLY && L + 1 < p.nl) prefetch_gu(L + 1);
     cstamp(L, 9);
     QMK_SYNC();  // j
     QMK_SYNC();  // k
@@ -1275,7 +1301,7 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
     }
     if (ST) {
       if (L + 1 < p.nl) prefetch_qkv(L + 1);
-    } else if (L + 1 < p.nl) {
+    } else if (!EARLY && L + 1 < p.nl) {
       prefetch_dn(L + 1);
     }
     cstamp(L, 11);

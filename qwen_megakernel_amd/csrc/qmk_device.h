@@ -195,7 +195,7 @@ __device__ __forceinline__ uint32_t ldu16(const void* p) { return *as_global<uin
 constexpr int kWaitLgkm0 = 0xF | (0x3 << 14) | (0x7 << 4);  // lgkmcnt(0) only
 
 // Waits until at most n vector-memory operations of this wave are outstanding
-// (n a small even count: the attention ring uses 0, 2, 4, 6).
+// (n <= 12; larger n waits for 12, which is safe, only later than needed).
 __device__ __forceinline__ void wait_vmcnt(int n) {
   constexpr int kKeep = (0x7 << 4) | (0xF << 8);
   switch (n) {
@@ -205,7 +205,13 @@ __device__ __forceinline__ void wait_vmcnt(int n) {
     case 3: __builtin_amdgcn_s_waitcnt(3 | kKeep); break;
     case 4: __builtin_amdgcn_s_waitcnt(4 | kKeep); break;
     case 5: __builtin_amdgcn_s_waitcnt(5 | kKeep); break;
-    default: __builtin_amdgcn_s_waitcnt(6 | kKeep); break;
+    case 6: __builtin_amdgcn_s_waitcnt(6 | kKeep); break;
+    case 7: __builtin_amdgcn_s_waitcnt(7 | kKeep); break;
+    case 8: __builtin_amdgcn_s_waitcnt(8 | kKeep); break;
+    case 9: __builtin_amdgcn_s_waitcnt(9 | kKeep); break;
+    case 10: __builtin_amdgcn_s_waitcnt(10 | kKeep); break;
+    case 11: __builtin_amdgcn_s_waitcnt(11 | kKeep); break;
+    default: __builtin_amdgcn_s_waitcnt(12 | kKeep); break;
   }
   asm volatile("" ::: "memory");  // LDS written by the completed loads is read only after this point
 }
