@@ -877,6 +877,13 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
     for (int i = 0; i < Dm::RQ_W; i++)
       load_row_p<Dm::LH>(wq + i * Dm::LH, qkv_row<M>(w, xcd, Dm::RQ_WG * r + Dm::RQ_W * c + i), lane);
   };
+  auto prefetch_qkv_row = [&](int layer, int i) {
+    LayerPtrs w;
+    w.wq = uniform_ptr(s.layers[layer].wq);
+    w.wk = uniform_ptr(s.layers[layer].wk);
+    w.wv = uniform_ptr(s.layers[layer].wv);
+    load_row_p<Dm::LH>(wq + i * Dm::LH, qkv_row<M>(w, xcd, Dm::RQ_WG * r + Dm::RQ_W * c + i), lane);
+  };
   auto prefetch_o = [&](int layer) {
     const uint16_t* wo_base = uniform_ptr(s.layers[layer].wo);
 #pragma unroll
@@ -898,14 +905,15 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
   // EARLY (short-context form, weights one layer ahead): the weight slices are
   // requested in the three windows in which the control wave does not poll,
   // so fewer exchange polls queue behind them (a CU returns vector-memory data
-  // in order): the next layer's QKV slice at barrier c (scores), this layer's
-  // gate/up slice at e (P@V), the next layer's o_proj slice and this layer's
-  // down slice at i (gate/up).  The K/V waits in the first two windows leave
-  // those newer loads outstanding.  Requested right after each compute phase
-  // instead, i.e. just before an exchange: 1,899 against 1,960 tok/s.
+  // in order): one of the next layer's two QKV rows at barrier c (scores),
+  // this layer's gate/up slice and the other QKV row at e (P@V), the next
+  // layer's o_proj slice and this layer's down slice at i (gate/up).  The K/V
+  // waits in the first two windows leave those newer loads outstanding.
+  // Requested right after each compute phase instead, i.e. just before an
+  // exchange: 1,899 against 1,974 tok/s.
   constexpr bool EARLY = !ST && !LONG;
-  constexpr int NB_C = EARLY ? Dm::RQ_W * Dm::LH : 0;  // loads issued at barrier c
-  constexpr int NB_E = EARLY ? Dm::GU_W * Dm::LH : 0;  // loads issued at barrier e
+  constexpr int NB_C = EARLY ? Dm::LH : 0;  // loads issued at barrier c
+  constexpr int NB_E = EARLY ? Dm::GU_W * Dm::LH + Dm::LH : 0;  // loads issued at barrier e
   static_assert(NB_C <= 12 && NB_E <= 12, "wait_vmcnt range");
   prefetch_qkv(0);
   if (EARLY) prefetch_o(0);
@@ -978,10 +986,10 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
     for (int j = 1; j < min(nb, kKvStages); j++) kv_issue(kc, j);
     if constexpr (EARLY) {
       static_assert(!EARLY || kLongContext / kGroupSize <= 32 * U, "EARLY: at most one K/V batch per wave");
-      // the last layer reloads its own slice, so the waits below count a static
+      // the last layer reloads its own rows, so the waits below count a static
       // number of loads (8 MB more reads per token; loading a 2 KB row instead
       // measured no faster)
-      prefetch_qkv(L + 1 < p.nl ? L + 1 : L);
+      prefetch_qkv_row(L + 1 < p.nl ? L + 1 : L, 0);
     }
     cstamp(L, 2);
     // ------------------------------------------------ scores and local (max, sum)
@@ -1136,6 +1144,7 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
     for (int j = 1; j < min(nb, kKvStages); j++) kv_issue(vc, j);
     if constexpr (EARLY) {
       prefetch_gu(L);
+      prefetch_qkv_row(L + 1 < p.nl ? L + 1 : L, 1);
     }
     cstamp(L, 4);
     // ------------------------------------------------ probabilities and P@V
