@@ -30,6 +30,8 @@ four and algorithmic GB/s per step (weights once + each sequence's KV).
 
 ``prefill``: the 128-token prompt through the batched forward, ms and tok/s;
 ``prefill_long``: a 2048-token prompt the same way (its attention on MFMA).
+``context_1024``: the decode rate at exactly 1024 positions of context (a
+1023-token prompt prefilled, then 512 decode launches at position 1023).
 
 ``sampling`` (skip with ``--no-sampling``): the same prompt and model, 512
 device-fed steps of the sampled generate loop (counter-based Gumbel-max draws,
@@ -220,6 +222,41 @@ def qwen3_1p7b(steps: int = 256, prompt_len: int = 512, batch: int = 4):
     return out
 
 
+def context_1024_rate(w, launches: int = 512):
+    """Decode rate at exactly 1024 positions of context: a 1023-token prompt prefilled, then
+    `launches` back-to-back `decode` launches at position 1023 (each rewrites that position's K/V
+    and attends over 1024 positions), timed with HIP events on the launch stream."""
+    import torch
+
+    from qwen_megakernel_amd.model import Decoder
+    from qwen_megakernel_amd.shapes import QWEN3_0_6B as S
+    from qwen_megakernel_amd.weights import make_prompt
+
+    dec = Decoder(weights=w, verbose=False, max_seq_len=2048)
+    dec.prefill(make_prompt(1023, S.vocab, seed=1))
+    args = (*dec._scratch(), dec._num_layers, 1023, dec._max_seq_len, dec._attn_scale)
+
+    def run(n):
+        for _ in range(n):
+            dec._ops.decode(dec._out_token, 11, *args)
+
+    run(32)
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    run(launches)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / launches
+    if int(dec._out_token.item()) < 0:
+        raise RuntimeError("decode at context 1024 failed on the device")
+    del dec
+    torch.cuda.empty_cache()
+    log(f"context 1024: {1e6 / us:.1f} tok/s, {us:.1f} us per step")
+    return {"context": 1024, "launches": launches, "us_per_step": round(us, 2), "tok_per_s": round(1e6 / us, 1)}
+
+
 def prefill_rate(w, prompt_len: int = PROMPT_LEN, iters: int = 10):
     """Qwen3-0.6B prompt prefill through the batched forward: ms and tokens/s for `prompt_len` tokens."""
     import torch
@@ -404,6 +441,7 @@ def main():
         result["sampling"] = sampling(dec, prompt, max_seq, args.sample_steps)
     del dec  # frees the 128-token run's caches; the weights stay for the long-context runs
     torch.cuda.empty_cache()
+    result["context_1024"] = context_1024_rate(w)
     result["prefill"] = prefill_rate(w)
     result["prefill_long"] = prefill_rate(w, 2048, iters=5)
     if not args.no_long_context:
