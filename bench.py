@@ -12,9 +12,12 @@ prompt re-prefilled), so the K timed steps always cover contexts 129..128+K.
 ``roofline`` relates the decode kernel's algorithmic bytes per launch
 (weights + KV read + KV written, averaged over the timed contexts) to its
 average launch duration measured with HIP events on the launch stream.
-``cpu_baseline`` times the CPU oracle (HF-semantics bf16 decode) on the host,
-on a bounded sample of the same workload (the 128-token prompt, then 384
-greedy steps).
+``roofline.traffic`` is the kernel's HBM traffic per launch from the committed
+counter profile (see TRAFFIC_PROFILE).  ``cpu_baseline`` times the repo's
+PyTorch bf16 decode path (the CPU oracle, HF Qwen3 bf16 eager semantics) on
+every core of the host's affinity set: the CPU reference configuration (16-token
+prompt, 2 warm-up and 64 timed greedy steps), and a bounded sample of the GPU
+workload (the 128-token prompt, then 384 greedy steps).
 
 ``long_context`` (skip with ``--no-long-context``): the same model with the KV
 cache prefilled to 8192 and to 32768 positions with seeded N(0, 1) bf16 K/V
@@ -60,11 +63,19 @@ import time
 
 PEAK_HBM_GBS = 8000.0
 PROMPT_LEN = 128
-# HBM bytes per decode launch (fetch + write) on the default workload (steps, warmup), from two
-# rocprofv3 --pmc runs of this script with --copy-calibration (FETCH_SIZE, then WRITE_SIZE), each
-# counter scaled by its own reading for the 1 GiB calibration copy and averaged over the timed
-# dispatches by ``python -m qwen_megakernel_amd.counters``.  Remeasured whenever the kernel changes.
-MEASURED_TRAFFIC_BYTES = {(1024, 32): 1_315_038_787}
+# HBM traffic of the decode kernel per launch (FETCH_SIZE + WRITE_SIZE), from two rocprofv3 --pmc
+# runs of this script with --copy-calibration, each counter scaled by its own reading for the
+# 1 GiB calibration copy and averaged over the timed dispatches by ``python -m
+# qwen_megakernel.counters``; remeasured whenever the kernel changes.  The traffic beyond the
+# algorithmic bytes (exchange words and their write-backs, the last layer's QKV rows read twice)
+# does not depend on the context, so a run at other contexts reports its own algorithmic bytes
+# plus that excess.
+TRAFFIC_PROFILE = {
+    "file": "profiles/decode_kernel_qwen3_0p6b_ctx129-1152_xcd_parallel.md",
+    "contexts": "129..1152",
+    "measured_bytes": 1_315_038_787,
+    "algorithmic_bytes": 1_265_674_240,
+}
 METRIC = "decode tok/s, batch 1, Qwen3-0.6B bf16; achieved HBM GB/s vs ~8 TB/s peak"
 
 
@@ -72,49 +83,70 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def cpu_baseline(steps: int = 384):
-    """The CPU oracle on a bounded sample of the bench workload: the same seeded weights and
-    128-token prompt (prefilled untimed), then `steps` timed greedy steps (context 129..)."""
-    import torch
-
-    from oracle.qwen3_ref import OracleDecoder
-    from qwen_megakernel_amd.shapes import QWEN3_0_6B
-    from qwen_megakernel_amd.weights import make_prompt, make_weights
-
-    threads = max(1, min(len(os.sched_getaffinity(0)), 16))
-    torch.set_num_threads(threads)
-    w = make_weights(QWEN3_0_6B, seed=0, max_seq_len=PROMPT_LEN + steps + 8)
-    dec = OracleDecoder(w, QWEN3_0_6B, max_seq_len=PROMPT_LEN + steps + 8)
-    prompt = make_prompt(PROMPT_LEN, QWEN3_0_6B.vocab, seed=1)
-    tok = None
-    for t in prompt:
-        tok = dec.step(t)
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        tok = dec.step(tok)
-    dt = time.perf_counter() - t0
-    cpu = "unknown"
+def _cpu_model():
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
                 if line.startswith("model name"):
-                    cpu = line.split(":", 1)[1].strip()
-                    break
+                    return line.split(":", 1)[1].strip()
     except OSError:
         pass
-    return {"value": round(steps / dt, 3), "unit": "tok/s", "cores": threads, "kind": "port",
-            "sample": f"CPU oracle (HF-semantics bf16 PyTorch decode, torch CPU ops), Qwen3-0.6B seeded weights, "
-                      f"{PROMPT_LEN}-token prompt prefilled untimed, {steps} greedy steps timed at context "
-                      f"{PROMPT_LEN + 1}..{PROMPT_LEN + steps} ({dt:.1f} s); {cpu}"}
+    return "unknown"
+
+
+def cpu_baseline(sample_steps: int = 384):
+    """The repo's PyTorch bf16 decode path (the CPU oracle: HF Qwen3's bf16 eager semantics with
+    torch CPU ops) on the host, on every core of the process's affinity set.
+
+    ``value``: the CPU reference configuration -- Qwen3-0.6B seeded weights, the seeded 16-token
+    prompt fed one step at a time, 2 warm-up greedy steps, then 64 timed greedy steps.  Also
+    reported: a bounded sample of the GPU workload itself (the 128-token prompt, then
+    ``sample_steps`` timed greedy steps at contexts 129..)."""
+    import torch
+
+    from oracle.qwen3_ref import OracleDecoder
+    from qwen_megakernel.shapes import QWEN3_0_6B
+    from qwen_megakernel.weights import make_prompt, make_weights
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    max_seq = PROMPT_LEN + sample_steps + 8
+    w = make_weights(QWEN3_0_6B, seed=0, max_seq_len=max_seq)
+
+    def timed(prompt_len, warm, steps):
+        dec = OracleDecoder(w, QWEN3_0_6B, max_seq_len=max_seq)
+        tok = None
+        for t in make_prompt(prompt_len, QWEN3_0_6B.vocab, seed=1):
+            tok = dec.step(t)
+        for _ in range(warm):
+            tok = dec.step(tok)
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            tok = dec.step(tok)
+        return time.perf_counter() - t0
+
+    dt0 = timed(16, 2, 64)
+    dt1 = timed(PROMPT_LEN, 0, sample_steps)
+    cpu = _cpu_model()
+    return {"value": round(64 / dt0, 3), "unit": "tok/s", "cores": threads, "kind": "port",
+            "ms_per_token": round(dt0 * 1e3 / 64, 2),
+            "sample": f"CPU reference configuration: the repo's PyTorch bf16 decode (HF Qwen3 bf16 eager "
+                      f"semantics, torch CPU ops), Qwen3-0.6B seeded weights, seeded 16-token prompt fed one "
+                      f"step at a time, 2 warm-up steps, 64 greedy steps timed ({dt0:.1f} s); {cpu}, "
+                      f"{threads} threads",
+            "bench_workload_sample": {
+                "tok_per_s": round(sample_steps / dt1, 3),
+                "sample": f"the GPU workload's 128-token prompt fed untimed, then {sample_steps} greedy steps "
+                          f"timed at context {PROMPT_LEN + 1}..{PROMPT_LEN + sample_steps} ({dt1:.1f} s)"}}
 
 
 def long_context(w, steps: int, contexts=(8192, 32768)):
     """Decode `steps` device-fed greedy tokens after a KV cache prefilled with N(0, 1) K/V."""
     import torch
 
-    from qwen_megakernel_amd.model import Decoder
-    from qwen_megakernel_amd.shapes import QWEN3_0_6B as S
-    from qwen_megakernel_amd.weights import rope_tables
+    from qwen_megakernel.model import Decoder
+    from qwen_megakernel.shapes import QWEN3_0_6B as S
+    from qwen_megakernel.weights import rope_tables
 
     out = {}
     max_seq = max(contexts) + steps + 64
@@ -161,9 +193,9 @@ def qwen3_1p7b(steps: int = 256, prompt_len: int = 512, batch: int = 4):
     """
     import torch
 
-    from qwen_megakernel_amd.model import BatchDecoder, Decoder
-    from qwen_megakernel_amd.shapes import QWEN3_1_7B as S
-    from qwen_megakernel_amd.weights import make_prompt, make_weights
+    from qwen_megakernel.model import BatchDecoder, Decoder
+    from qwen_megakernel.shapes import QWEN3_1_7B as S
+    from qwen_megakernel.weights import make_prompt, make_weights
 
     max_seq = prompt_len + steps + 64
     w = make_weights(S, seed=0, max_seq_len=max_seq, device="cuda")
@@ -228,9 +260,9 @@ def context_1024_rate(w, launches: int = 512):
     and attends over 1024 positions), timed with HIP events on the launch stream."""
     import torch
 
-    from qwen_megakernel_amd.model import Decoder
-    from qwen_megakernel_amd.shapes import QWEN3_0_6B as S
-    from qwen_megakernel_amd.weights import make_prompt
+    from qwen_megakernel.model import Decoder
+    from qwen_megakernel.shapes import QWEN3_0_6B as S
+    from qwen_megakernel.weights import make_prompt
 
     dec = Decoder(weights=w, verbose=False, max_seq_len=2048)
     dec.prefill(make_prompt(1023, S.vocab, seed=1))
@@ -261,9 +293,9 @@ def prefill_rate(w, prompt_len: int = PROMPT_LEN, iters: int = 10):
     """Qwen3-0.6B prompt prefill through the batched forward: ms and tokens/s for `prompt_len` tokens."""
     import torch
 
-    from qwen_megakernel_amd.model import Decoder
-    from qwen_megakernel_amd.shapes import QWEN3_0_6B as S
-    from qwen_megakernel_amd.weights import make_prompt
+    from qwen_megakernel.model import Decoder
+    from qwen_megakernel.shapes import QWEN3_0_6B as S
+    from qwen_megakernel.weights import make_prompt
 
     dec = Decoder(weights=w, verbose=False, max_seq_len=2048)
     prompt = make_prompt(prompt_len, S.vocab, seed=1)
@@ -289,7 +321,7 @@ def sampling(dec, prompt, max_seq: int, steps: int):
     """Sampled generate loop (generate_sample) from the prefilled prompt, per sampling setting."""
     import torch
 
-    from qwen_megakernel_amd.shapes import QWEN3_0_6B as S
+    from qwen_megakernel.shapes import QWEN3_0_6B as S
 
     ops = torch.ops.qwen_megakernel_C
     steps = min(steps, max_seq - len(prompt))
@@ -348,9 +380,9 @@ def main():
     import torch
 
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
-    from qwen_megakernel_amd.model import Decoder, HEAD_DIM
-    from qwen_megakernel_amd.shapes import QWEN3_0_6B
-    from qwen_megakernel_amd.weights import make_prompt, make_weights
+    from qwen_megakernel.model import Decoder, HEAD_DIM
+    from qwen_megakernel.shapes import QWEN3_0_6B
+    from qwen_megakernel.weights import make_prompt, make_weights
 
     max_seq = 2048
     while PROMPT_LEN + max(args.steps, args.warmup) > max_seq:
@@ -421,13 +453,18 @@ def main():
                    "weights": "seeded N(0,0.02) bf16, norms 1, tied embeddings"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(achieved / PEAK_HBM_GBS, 4),
-                     "traffic": MEASURED_TRAFFIC_BYTES.get((args.steps, args.warmup)),
+                     "traffic": int(bytes_per_launch + TRAFFIC_PROFILE["measured_bytes"]
+                                    - TRAFFIC_PROFILE["algorithmic_bytes"]),
+                     "traffic_source": f"{TRAFFIC_PROFILE['file']}: FETCH_SIZE + WRITE_SIZE per launch at contexts "
+                                       f"{TRAFFIC_PROFILE['contexts']}, {TRAFFIC_PROFILE['measured_bytes']} B against "
+                                       f"{TRAFFIC_PROFILE['algorithmic_bytes']} algorithmic; the same excess "
+                                       f"added to this run's algorithmic bytes",
                      "bytes_per_launch": int(bytes_per_launch), "avg_launch_us": round(avg_launch_s * 1e6, 2),
                      "kernel": "qmk::decode_kernel<Qwen3_0_6B, false, false>"},
         "cpu_baseline": None,
     }
     if args.phase_trace:
-        from qwen_megakernel_amd import trace
+        from qwen_megakernel import trace
 
         last = PROMPT_LEN - 1 + args.steps  # position after the timed steps
         dec._position = last
@@ -451,7 +488,7 @@ def main():
     if not args.no_1p7b:
         result["qwen3_1p7b"] = qwen3_1p7b()
     if not args.no_phases:
-        from qwen_megakernel_amd import phases as P
+        from qwen_megakernel import phases as P
 
         result["phases"] = {}
         for ph in P.phases():

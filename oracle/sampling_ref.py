@@ -2,7 +2,7 @@
 
 TEST INFRASTRUCTURE ONLY: imported by ``tests/`` as the checker; the product
 path (``qmk_sample_rows`` / ``qmk_generate_sample`` in
-qwen_megakernel_amd/csrc/qmk_sample.hip) never calls it.
+qwen_megakernel/csrc/qmk_sample.hip) never calls it.
 
 The reference decodes greedily only (csrc/kernel.cu:1020-1183); sampling follows
 HF transformers' logits warpers, applied in HF's order (generation/utils.py

@@ -132,8 +132,8 @@ def get_extension(build_if_missing: bool = True):
                              or _stale(OPS, _sources(_OPS_SOURCES))):
         build(force=False)
     if not is_built():
-        raise RuntimeError("qwen_megakernel_amd: the HIP library is not built; run "
-                           "python -c 'import qwen_megakernel_amd.build as b; b.build()'")
+        raise RuntimeError("qwen_megakernel: the HIP library is not built; run "
+                           "QMK_NO_IMPORT_LOAD=1 python -m qwen_megakernel.build")
     torch.ops.load_library(OPS)
     _module = torch.ops.qwen_megakernel_C
     return _module

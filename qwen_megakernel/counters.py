@@ -4,7 +4,7 @@ HBM traffic per decode launch, after two counter runs of ``bench.py
 --copy-calibration``, one with ``--pmc FETCH_SIZE`` and one with ``--pmc
 WRITE_SIZE``:
 
-    python -m qwen_megakernel_amd.counters FETCH.csv WRITE.csv --timed 1024
+    python -m qwen_megakernel.counters FETCH.csv WRITE.csv --timed 1024
 
 ``FETCH_SIZE`` / ``WRITE_SIZE`` are in KiB per dispatch.  Each counter is
 scaled by the ratio of the known size of the calibration copy (1 GiB read and
@@ -13,7 +13,7 @@ over the last ``--timed`` decode dispatches (the timed region of the run).
 
 Shader-sequencer counters per kernel (any ``SQ_*`` / ``GRBM_*`` set):
 
-    python -m qwen_megakernel_amd.counters sq A.csv [B.csv ...] --timed 256
+    python -m qwen_megakernel.counters sq A.csv [B.csv ...] --timed 256
 
 gives, for every decode-kernel instantiation, the mean of each counter over
 its last ``--timed`` dispatches (a counter present in several files is read

@@ -5,8 +5,12 @@
 // singletons allocated on first use with unchecked cudaMalloc
 // (csrc/kernel.cu:1446-1473), so two decoders on two streams corrupt each
 // other.  Here each (device, stream) pair owns a DecodeState plus exchange
-// buffers, created on first use and checked; launches on one stream are
-// ordered by the stream, launches on different streams use different state.
+// buffers, created on first use and checked.  Launches on one stream are
+// ordered by the stream.  Launches of the decode kernel on different streams
+// of one device are ordered by the library (DeviceOrder below): the kernel
+// needs all 256 workgroups resident at once, one per CU, and its workgroups
+// wait on each other, so two overlapping instances could each hold part of
+// the CUs and wait for workgroups that cannot start.
 
 #include <hip/hip_runtime.h>
 
@@ -36,8 +40,13 @@ thread_local int t_status = QMK_OK;
 // in groups of this many steps (the rest launched directly)
 constexpr int kGraphSteps = 32;
 
+struct DevInfo;
+
 struct Ctx {
   int device = -1;
+  DevInfo* dev = nullptr;
+  uint32_t ticks_per_s = 100000000u;  // the device's wall-clock rate (the default wait bound is one second)
+  int last_model = -1;                // model of the last launch on this stream's exchange area
   DecodeState* st = nullptr;
   uint32_t* x = nullptr;
   uint32_t* host_err = nullptr;
@@ -61,15 +70,24 @@ struct Ctx {
 };
 
 struct DevInfo {
-  bool checked = false;
+  bool checked = false;  // set only once the checks ran to completion (a HIP failure leaves it unset)
   bool ok = false;
   int xcd_local = 0;
   uint32_t ticks_per_s = 100000000u;
+  // cross-stream ordering of decode launches on this device
+  std::mutex order_mu;
+  hipEvent_t order_evt = nullptr;      // recorded after the last decode launch group
+  hipStream_t order_stream = nullptr;  // the stream it was recorded on
+  bool order_valid = false;
 };
 
 std::mutex g_mu;
 std::map<std::pair<int, hipStream_t>, Ctx*> g_ctx;
 std::map<int, DevInfo> g_dev;
+
+// XCD probe results (one per workgroup), read back once per device; a static
+// array, so the device check allocates no device memory.
+__device__ int g_xcd_probe[kNumWG];
 
 __global__ void xcd_probe_kernel(int* ok) {
   if (threadIdx.x == 0) {
@@ -114,13 +132,16 @@ int fail(int s) {
   return s;
 }
 
-// Checks the current device once: gfx950-class with >= 256 CUs, the decode
-// kernel fits one workgroup per CU, and whether workgroup b runs on XCD b%8.
+// Checks the current device: gfx950-class with >= 256 CUs, the decode kernel
+// fits one workgroup per CU, and whether workgroup b runs on XCD b%8.  The
+// result is kept only when every HIP call succeeded, so a transient failure
+// leaves the device unchecked and the next call checks again.  The probe runs
+// on a private stream (not the null stream, which another stream's graph
+// capture would forbid).  Called with g_mu held.
 int check_device(int dev, DevInfo** out) {
   DevInfo& di = g_dev[dev];
   *out = &di;
   if (di.checked) return di.ok ? QMK_OK : QMK_ERR_DEVICE;
-  di.checked = true;
   hipDeviceProp_t prop;
   if (hipGetDeviceProperties(&prop, dev) != hipSuccess) return QMK_ERR_HIP;
   int occ = 0, occ17 = 0;
@@ -134,22 +155,90 @@ int check_device(int dev, DevInfo** out) {
       hipOccupancyMaxActiveBlocksPerMultiprocessor(
           &occl17, reinterpret_cast<const void*>(decode_kernel<Qwen3_1_7B, false, true>), kBlock, 0) != hipSuccess)
     return QMK_ERR_HIP;
-  if (prop.multiProcessorCount < kNumWG || occ < 1 || occ17 < 1 || occl < 1 || occl17 < 1) return QMK_ERR_DEVICE;
+  if (prop.multiProcessorCount < kNumWG || occ < 1 || occ17 < 1 || occl < 1 || occl17 < 1) {
+    di.checked = true;
+    di.ok = false;
+    return QMK_ERR_DEVICE;
+  }
+  uint32_t ticks = 100000000u;
   int khz = 0;
   if (hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev) == hipSuccess && khz > 0)
-    di.ticks_per_s = (uint32_t)khz * 1000u;
+    ticks = (uint32_t)khz * 1000u;
+  hipStream_t ps = nullptr;
+  if (hipStreamCreateWithFlags(&ps, hipStreamNonBlocking) != hipSuccess) return QMK_ERR_HIP;
   int* d_ok = nullptr;
-  if (hipMalloc(&d_ok, kNumWG * sizeof(int)) != hipSuccess) return QMK_ERR_HIP;
-  hipLaunchKernelGGL(xcd_probe_kernel, dim3(kNumWG), dim3(64), 0, 0, d_ok);
   int h_ok[kNumWG];
-  bool good = hipGetLastError() == hipSuccess &&
-              hipMemcpy(h_ok, d_ok, sizeof(h_ok), hipMemcpyDeviceToHost) == hipSuccess;
-  hipFree(d_ok);
+  bool good = hipGetSymbolAddress(reinterpret_cast<void**>(&d_ok), HIP_SYMBOL(g_xcd_probe)) == hipSuccess;
+  if (good) {
+    hipLaunchKernelGGL(xcd_probe_kernel, dim3(kNumWG), dim3(64), 0, ps, d_ok);
+    good = hipGetLastError() == hipSuccess &&
+           hipMemcpyAsync(h_ok, d_ok, sizeof(h_ok), hipMemcpyDeviceToHost, ps) == hipSuccess &&
+           hipStreamSynchronize(ps) == hipSuccess;
+  }
+  hipStreamDestroy(ps);
   if (!good) return QMK_ERR_HIP;
+  if (!di.order_evt && hipEventCreateWithFlags(&di.order_evt, hipEventDisableTiming) != hipSuccess) return QMK_ERR_HIP;
   int all = 1;
   for (int i = 0; i < kNumWG; i++) all &= h_ok[i];
   di.xcd_local = all;
+  di.ticks_per_s = ticks;
   di.ok = true;
+  di.checked = true;
+  return QMK_OK;
+}
+
+// Orders one group of decode launches on `stream` after the previous group on
+// the same device, whatever stream that was on: a wait on the event recorded
+// after it (nothing when it was on the same stream), then, once the group is
+// enqueued, an event record on `stream`.  The lock keeps the wait, the
+// launches and the record of one group together against other host threads.
+// A stream under graph capture is left alone (the graph's owner orders its
+// replays).
+class DeviceOrder {
+ public:
+  DeviceOrder(DevInfo* di, hipStream_t stream) : di_(di), stream_(stream), lk_(di->order_mu) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &cs) != hipSuccess) cs = hipStreamCaptureStatusNone;
+    capturing_ = cs != hipStreamCaptureStatusNone;
+    if (!capturing_ && di_->order_valid && di_->order_stream != stream_)
+      ok_ = hipStreamWaitEvent(stream_, di_->order_evt, 0) == hipSuccess;
+  }
+  bool ok() const { return ok_; }
+  // call after the group's launches were enqueued
+  int finish() {
+    if (capturing_) return QMK_OK;
+    if (hipEventRecord(di_->order_evt, stream_) != hipSuccess) {
+      di_->order_valid = false;
+      return QMK_ERR_HIP;
+    }
+    di_->order_stream = stream_;
+    di_->order_valid = true;
+    return QMK_OK;
+  }
+
+ private:
+  DevInfo* di_;
+  hipStream_t stream_;
+  std::lock_guard<std::mutex> lk_;
+  bool capturing_ = false;
+  bool ok_ = true;
+};
+
+// Zeroes a stream's exchange words and restarts its tags (epoch 0), keeping
+// the error word: run when the stream switches models, whose exchange layouts
+// differ, so no word left by the other layout is ever read as current.
+__global__ void clear_exchange_kernel(DecodeState* st, uint32_t* x, uint32_t n) {
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) x[i] = 0u;
+  if (blockIdx.x == 0 && threadIdx.x == 0) st->epoch = 0u;
+}
+
+int prepare_model(Ctx* ctx, int model, hipStream_t stream) {
+  if (ctx->last_model == model) return QMK_OK;
+  if (ctx->last_model >= 0) {
+    hipLaunchKernelGGL(clear_exchange_kernel, dim3(kNumWG), dim3(256), 0, stream, ctx->st, ctx->x, kXWords);
+    if (hipGetLastError() != hipSuccess) return QMK_ERR_HIP;
+  }
+  ctx->last_model = model;
   return QMK_OK;
 }
 
@@ -168,7 +257,9 @@ int get_ctx(hipStream_t stream, Ctx** out) {
   if (s != QMK_OK) return s;
   Ctx* c = new Ctx();
   c->device = dev;
+  c->dev = di;
   c->xcd_local = di->xcd_local;
+  c->ticks_per_s = di->ticks_per_s;
   c->timeout = di->ticks_per_s;  // 1 second
   const size_t bytes = sizeof(DecodeState) + (size_t)kXWords * 4;
   void* mem = nullptr;
@@ -278,6 +369,9 @@ int decode_impl(const Common& c, int token, int position, int* out_token, float*
   KArgs a = make_args(c, ctx);
   a.out_token = out_token;
   a.logits = logits;
+  DeviceOrder order(ctx->dev, stream);
+  if (!order.ok()) return fail(QMK_ERR_HIP);
+  if ((s = prepare_model(ctx, c.model, stream)) != QMK_OK) return fail(s);
   if (persistent) {
     hipLaunchKernelGGL(set_step_kernel, dim3(1), dim3(1), 0, stream, ctx->st, position, token, -1);
     a.position = -1;
@@ -285,7 +379,9 @@ int decode_impl(const Common& c, int token, int position, int* out_token, float*
     a.position = position;
     a.token = token;
   }
-  return fail(launch(a, c.model, position + 1 > kLongContext, stream));
+  s = launch(a, c.model, position + 1 > kLongContext, stream);
+  const int so = order.finish();
+  return fail(s != QMK_OK ? s : so);
 }
 
 // One step of the generate loop: the decode launch, and with sampling the
@@ -335,6 +431,34 @@ int graph_for(Ctx* ctx, const KArgs& a, int model, const SampleParams* sp, bool 
   return QMK_OK;
 }
 
+// The launches of generate_impl, in order on `stream`.
+int generate_steps(Ctx* ctx, const Common& c, const KArgs& a, int first_token_id, int num_steps, int eos,
+                   int* output_log, int start_position, hipStream_t stream, const SampleParams* sp) {
+  int s = QMK_OK;
+  hipLaunchKernelGGL(set_step_kernel, dim3(1), dim3(1), 0, stream, ctx->st, start_position, first_token_id,
+                     eos < 0 ? -1 : eos);
+  // Step i runs at context start_position + i + 1.  The steps up to context
+  // kLongContext take the short-context kernel, the rest the long-context one;
+  // each run of steps replays its form's graph, with direct launches for the remainder.
+  for (int done = 0; done < num_steps;) {
+    const long long ctx0 = (long long)start_position + done + 1;
+    const bool lg = ctx0 > kLongContext;
+    int run = num_steps - done;
+    if (!lg) run = (int)std::min<long long>(run, kLongContext - ctx0 + 1);
+    hipGraphExec_t g = nullptr;
+    if (ctx->use_graphs && run >= kGraphSteps && graph_for(ctx, a, c.model, sp, lg, &g) == QMK_OK) {
+      for (; run >= kGraphSteps; run -= kGraphSteps, done += kGraphSteps)
+        if (hipGraphLaunch(g, stream) != hipSuccess) return QMK_ERR_HIP;
+    }
+    for (; run > 0; run--, done++)
+      if ((s = launch_step(a, c.model, sp, ctx->swork, lg, stream)) != QMK_OK) return s;
+  }
+  if (hipMemcpyAsync(output_log, ctx->log, (size_t)num_steps * sizeof(int), hipMemcpyDeviceToDevice, stream) !=
+      hipSuccess)
+    return QMK_ERR_HIP;
+  return QMK_OK;
+}
+
 // num_steps persistent launches from (start_position, first_token_id); the
 // log is copied into output_log at the end.  eos >= 0: stop token.
 int generate_impl(const Common& c, int first_token_id, int num_steps, int eos, int* output_log, int start_position,
@@ -364,28 +488,12 @@ int generate_impl(const Common& c, int first_token_id, int num_steps, int eos, i
     if (!ctx->swork && alloc_sample_work(&ctx->swork, 1) != QMK_OK) return fail(QMK_ERR_HIP);
     a.logits = ctx->logits;
   }
-  hipLaunchKernelGGL(set_step_kernel, dim3(1), dim3(1), 0, stream, ctx->st, start_position, first_token_id,
-                     eos < 0 ? -1 : eos);
-  // Step i runs at context start_position + i + 1.  The steps up to context
-  // kLongContext take the short-context kernel, the rest the long-context one;
-  // each run of steps replays its form's graph, with direct launches for the remainder.
-  for (int done = 0; done < num_steps;) {
-    const long long ctx0 = (long long)start_position + done + 1;
-    const bool lg = ctx0 > kLongContext;
-    int run = num_steps - done;
-    if (!lg) run = (int)std::min<long long>(run, kLongContext - ctx0 + 1);
-    hipGraphExec_t g = nullptr;
-    if (ctx->use_graphs && run >= kGraphSteps && graph_for(ctx, a, c.model, sp, lg, &g) == QMK_OK) {
-      for (; run >= kGraphSteps; run -= kGraphSteps, done += kGraphSteps)
-        if (hipGraphLaunch(g, stream) != hipSuccess) return fail(QMK_ERR_HIP);
-    }
-    for (; run > 0; run--, done++)
-      if ((s = launch_step(a, c.model, sp, ctx->swork, lg, stream)) != QMK_OK) return fail(s);
-  }
-  if (hipMemcpyAsync(output_log, ctx->log, (size_t)num_steps * sizeof(int), hipMemcpyDeviceToDevice, stream) !=
-      hipSuccess)
-    return fail(QMK_ERR_HIP);
-  return fail(QMK_OK);
+  DeviceOrder order(ctx->dev, stream);
+  if (!order.ok()) return fail(QMK_ERR_HIP);
+  if ((s = prepare_model(ctx, c.model, stream)) != QMK_OK) return fail(s);
+  s = generate_steps(ctx, c, a, first_token_id, num_steps, eos, output_log, start_position, stream, sp);
+  const int so = order.finish();
+  return fail(s != QMK_OK ? s : so);
 }
 
 size_t phase_copy_elems(int phase) {
@@ -560,11 +668,7 @@ int qmk_set_wait_limit(hipStream_t stream, uint32_t ticks) {
   Ctx* ctx = nullptr;
   int s = get_ctx(stream, &ctx);
   if (s != QMK_OK) return fail(s);
-  if (ticks == 0) {
-    DevInfo* di = nullptr;
-    check_device(ctx->device, &di);
-    ticks = di->ticks_per_s;
-  }
+  if (ticks == 0) ticks = ctx->ticks_per_s;
   ctx->timeout = ticks;
   return fail(QMK_OK);
 }

@@ -10,7 +10,7 @@ Differences, all additive:
 
 * ``load_weights`` has no network.  ``model_name`` may name a local directory
   holding a Qwen3 checkpoint (``*.safetensors`` + tokenizer files); anything
-  else yields the seeded synthetic weights of :mod:`qwen_megakernel_amd.weights`
+  else yields the seeded synthetic weights of :mod:`qwen_megakernel.weights`
   and no tokenizer.
 * RoPE theta is 1e6 (Qwen3), not the reference's 10000 (model.py:54-56).
 * ``max_seq_len`` is a parameter (the reference fixes 2048).

@@ -4,7 +4,7 @@ The reference checks its kernel against HF Qwen3 (qwen_megakernel/bench.py:83-13
 HF is a third-party package (transformers 5.15.0 in this image), not part of the
 reference.  This script builds ``Qwen3ForCausalLM`` from a local ``Qwen3Config``
 (no network), loads the seeded synthetic weights of
-``qwen_megakernel_amd.weights.make_weights`` into it, and records, for a
+``qwen_megakernel.weights.make_weights`` into it, and records, for a
 token-at-a-time decode (the reference's ``Decoder.step`` pattern):
 
 * ``hf_tiny.npz``         -- a 2-layer toy Qwen3 (hidden 256, 4/2 heads,
@@ -17,6 +17,10 @@ token-at-a-time decode (the reference's ``Decoder.step`` pattern):
   positions (head_dim 128, theta 1e6).
 * ``hf_tiny_keys.json``   -- HF's state-dict names and shapes for the tiny
   config (``python tests/golden/make_hf_golden.py keys`` writes only this).
+* ``qwen_megakernel/data/hf_greedy_qwen3_0p6b.json`` -- the prompt, HF's
+  greedy tokens and top-2 gaps of ``hf_qwen3_0p6b.npz`` as JSON, for
+  ``qwen_megakernel.bench.correctness_check`` (``python
+  tests/golden/make_hf_golden.py package`` rewrites it from the npz alone).
 
 Run:  python tests/golden/make_hf_golden.py   (about a minute on 8 cores)
 """
@@ -33,8 +37,8 @@ import torch
 HERE = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.dirname(os.path.dirname(HERE)))
 
-from qwen_megakernel_amd.shapes import QWEN3_0_6B, Qwen3Shape  # noqa: E402
-from qwen_megakernel_amd.weights import make_prompt, make_weights  # noqa: E402
+from qwen_megakernel.shapes import QWEN3_0_6B, Qwen3Shape  # noqa: E402
+from qwen_megakernel.weights import make_prompt, make_weights  # noqa: E402
 
 TINY = Qwen3Shape("tiny", 2, 256, 512, 4, 2, 64, 1000)
 HF_PARAM_NAMES = [
@@ -183,7 +187,33 @@ def main():
     print("golden fixtures written:", sig)
 
 
+def write_package_tokens():
+    """HF's greedy continuation of the config-0 prompt, from hf_qwen3_0p6b.npz, as package data."""
+    import json
+
+    d = np.load(os.path.join(HERE, "hf_qwen3_0p6b.npz"))
+    n0 = len(d["prompt"]) - 1
+    out = {
+        "source": "HF transformers Qwen3ForCausalLM, bf16 eager, CPU; tests/golden/make_hf_golden.py",
+        "weights": "qwen_megakernel.weights.make_weights(QWEN3_0_6B, seed=0): N(0, 0.02) bf16, norms 1, tied",
+        "prompt": [int(t) for t in d["prompt"]],
+        "greedy_tokens": [int(t) for t in d["tokens"][n0:]],
+        "top2_gaps": [float(g) for g in d["gaps"][n0:]],
+        "top_logits": [float(x) for x in
+                       torch.from_numpy(d["top16_bf16"][n0:, 0].view(np.int16)).view(torch.bfloat16).float()],
+        "generate_tokens": [int(t) for t in d["generate_tokens"]],
+        "weight_fingerprint_head": [float(x) for x in d["weight_fingerprint"][:4]],
+    }
+    dst = os.path.join(os.path.dirname(os.path.dirname(HERE)), "qwen_megakernel", "data")
+    os.makedirs(dst, exist_ok=True)
+    with open(os.path.join(dst, "hf_greedy_qwen3_0p6b.json"), "w") as f:
+        json.dump(out, f, indent=1)
+
+
 if __name__ == "__main__" and sys.argv[1:] == ["keys"]:
     write_state_dict_keys()
+elif __name__ == "__main__" and sys.argv[1:] == ["package"]:
+    write_package_tokens()
 elif __name__ == "__main__":
     main()
+    write_package_tokens()

@@ -35,7 +35,7 @@ REF_GENERATE = ("generate_nosync(int first_token_id, int num_steps, Tensor embed
 
 @pytest.fixture(scope="module")
 def lib():
-    from qwen_megakernel_amd import build
+    from qwen_megakernel import build
 
     if not os.path.exists(build.LIB):
         build.build(force=False)
@@ -114,7 +114,7 @@ def _norm_schema(s):
 
 
 def test_torch_op_schemas_match_reference():
-    from qwen_megakernel_amd.build import get_extension
+    from qwen_megakernel.build import get_extension
 
     ops = get_extension(build_if_missing=True)
     assert _norm_schema(str(ops.decode.default._schema)) == REF_DECODE
@@ -122,11 +122,11 @@ def test_torch_op_schemas_match_reference():
 
 
 def test_package_exports_reference_names():
-    import qwen_megakernel_amd as q
+    import qwen_megakernel as q
 
     # the reference's three names, plus the batched decoder
     assert set(q.__all__) == {"load_weights", "Decoder", "generate", "BatchDecoder"}
-    from qwen_megakernel_amd import model
+    from qwen_megakernel import model
 
     assert (model.NUM_LAYERS, model.HIDDEN_SIZE, model.INTERMEDIATE_SIZE, model.VOCAB_SIZE) == (28, 1024, 3072, 151936)
 
@@ -136,7 +136,7 @@ def test_pack_layer_weights_layout():
 
     import torch
 
-    from qwen_megakernel_amd.model import _pack_layer_weights
+    from qwen_megakernel.model import _pack_layer_weights
 
     ts = [torch.zeros(4) for _ in range(22)]
     blob = _pack_layer_weights(ts, num_layers=2)
@@ -147,7 +147,7 @@ def test_pack_layer_weights_layout():
 
 def test_algorithmic_bytes():
     """Bytes per token that the roofline divides by, summed tensor by tensor."""
-    from qwen_megakernel_amd.shapes import QWEN3_0_6B, layer_tensor_shapes
+    from qwen_megakernel.shapes import QWEN3_0_6B, layer_tensor_shapes
 
     s = QWEN3_0_6B
     layer = sum(2 * math.prod(shp) for shp in layer_tensor_shapes(s).values())
@@ -223,3 +223,37 @@ def test_generate_eos_validation(lib):
     assert call(eos=-1) == QMK_ERR_ARG
     assert call(eos=151936) == QMK_ERR_ARG
     assert call(start=60, steps=10) == QMK_ERR_POSITION
+
+
+def test_reference_import_surface():
+    """The reference's import names (qwen_megakernel/__init__.py:1-9, model.py, build.py, bench.py):
+    importing the package registers torch.ops.qwen_megakernel_C, and the bench module has the
+    reference's entry points and constants."""
+    import torch
+
+    import qwen_megakernel
+    from qwen_megakernel import Decoder, generate, load_weights  # noqa: F401
+    from qwen_megakernel.bench import (CHECK_TOKENS, PROMPT, RUNS, TOKENS, WARMUP, bench_megakernel,  # noqa: F401
+                                       correctness_check, golden)
+    from qwen_megakernel.build import get_extension
+    from qwen_megakernel.model import Decoder as D2
+
+    assert D2 is Decoder and qwen_megakernel.__all__[:3] == ["load_weights", "Decoder", "generate"]
+    assert get_extension() is torch.ops.qwen_megakernel_C
+    assert hasattr(torch.ops.qwen_megakernel_C, "decode") and hasattr(torch.ops.qwen_megakernel_C, "generate_nosync")
+    assert (TOKENS, WARMUP, RUNS, PROMPT, CHECK_TOKENS) == (100, 3, 5, "Hello", 8)
+
+
+def test_bench_golden_tokens_are_hf_fixture():
+    """correctness_check's HF tokens are the HF fixture's (tests/golden/hf_qwen3_0p6b.npz)."""
+    import numpy as np
+
+    from qwen_megakernel.bench import golden
+    from qwen_megakernel.shapes import QWEN3_0_6B
+    from qwen_megakernel.weights import make_prompt
+
+    g = golden()
+    d = np.load(os.path.join(os.path.dirname(__file__), "golden", "hf_qwen3_0p6b.npz"))
+    assert g["prompt"] == d["prompt"].tolist() == make_prompt(16, QWEN3_0_6B.vocab, seed=1)
+    assert g["greedy_tokens"] == d["tokens"][15:].tolist()
+    assert len(g["top_logits"]) == len(g["greedy_tokens"]) == 64

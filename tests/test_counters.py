@@ -1,11 +1,11 @@
-"""CPU tests of the rocprofv3 counter summaries (qwen_megakernel_amd/counters.py) on small
+"""CPU tests of the rocprofv3 counter summaries (qwen_megakernel/counters.py) on small
 synthetic CSVs in rocprofv3's ``-f csv`` counter-collection layout."""
 
 import csv
 
 import pytest
 
-from qwen_megakernel_amd import counters
+from qwen_megakernel import counters
 
 FIELDS = ["Dispatch_Id", "Kernel_Name", "Counter_Name", "Counter_Value"]
 SHORT = "void qmk::decode_kernel<qmk::Qwen3_0_6B, false, false>(qmk::KArgs)"

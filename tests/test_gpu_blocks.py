@@ -18,7 +18,7 @@ pytestmark = pytest.mark.gpu
 
 
 def _run(x):
-    from qwen_megakernel_amd.build import load_c_library
+    from qwen_megakernel.build import load_c_library
 
     lib = load_c_library()
     n = x.numel()

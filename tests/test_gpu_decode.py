@@ -1,311 +1,132 @@
-"""GPU parity tests: the HIP decode kernel against the CPU oracle.
+"""GPU parity tests: the HIP decode kernel against the exact CPU oracle.
 
-Parity bar (the reference's PyTorch bf16 path is the target): per-step logits
-cosine similarity >= 0.999 and max abs error <= 0.1; greedy tokens identical
-except at steps where the oracle's top-2 logit gap is a tie: < 1e-2, or no
-more than one bf16 ulp of the top logit.  Logits are bf16 values, so for
-|logit| >= 1.28 two distinct logits are at least 0.0078 apart, and in the
-usual range [2, 4) at least 0.0156: a gap of one ulp is the closest two
-distinct bf16 logits can be, and which of two adjacent values a kernel lands
-on depends on fp32 accumulation order.
+The bar and the near-tie rule are in tests/parity.py: per step, logits cosine
+>= 0.999 and max abs <= 0.1 against oracle/qwen3_exact.py (HF Qwen3's bf16
+rounding points, exact arithmetic between them), and the greedy token equal to
+the oracle's argmax given the same prefix except at a near-tie (gap below
+max(1e-2, one bf16 ulp)).  No bound depends on the CPU the test runs on.
 """
 
 import ctypes
 import math
-import os
 
 import pytest
 import torch
 
+from parity import DEEP, LITERAL, Tally, check_rows, decoder, exact_oracle, kernel_stream, stream_rows, with_rope
+
 pytestmark = pytest.mark.gpu
 
-COS_MIN = 0.999
-ABS_MAX = 0.1
-TIE_GAP = 1e-2
 
-
-def bf16_ulp(x: float) -> float:
-    """Spacing of bf16 values at |x| (8 significant bits)."""
-    return 2.0 ** (math.floor(math.log2(abs(x))) - 7) if x != 0 else 2.0 ** -133
-
-
-def is_tie(gap: float, top: float) -> bool:
-    return gap < TIE_GAP or gap <= bf16_ulp(top)
-
-
-@pytest.fixture(scope="module")
-def shape():
-    from qwen_megakernel_amd.shapes import QWEN3_0_6B
-
-    return QWEN3_0_6B
-
-
-@pytest.fixture(scope="module")
-def weights_cpu(shape):
-    from qwen_megakernel_amd.weights import make_weights
-
-    torch.set_num_threads(min(16, len(os.sched_getaffinity(0))))
-    return make_weights(shape, seed=0, max_seq_len=2048)
-
-
-@pytest.fixture(scope="module")
-def weights_gpu(weights_cpu):
-    from qwen_megakernel_amd.weights import to_device
-
-    return to_device(weights_cpu, "cuda")
-
-
-@pytest.fixture(scope="module")
-def prompt(shape):
-    from qwen_megakernel_amd.weights import make_prompt
-
-    return make_prompt(16, shape.vocab, seed=1)
-
-
-def _decoder(weights, **kw):
-    from qwen_megakernel_amd.model import Decoder
-
-    return Decoder(weights=weights, verbose=False, max_seq_len=kw.pop("max_seq_len", 2048), **kw)
-
-
-def _check_step(i, g, r, tok, ref_tok, gap):
-    cos = torch.nn.functional.cosine_similarity(g.double(), r.double(), dim=0).item()
-    mab = (g - r).abs().max().item()
-    assert cos >= COS_MIN, f"step {i}: cos {cos}"
-    assert mab <= ABS_MAX, f"step {i}: max abs {mab}"
-    if tok != ref_tok:
-        top = float(r.max())
-        assert is_tie(gap, top), f"step {i}: token {tok} != {ref_tok} with top-2 gap {gap} (top {top})"
-    return cos, mab
-
-
-def _teacher_forced(dec, orc_res):
-    worst = (1.0, 0.0)
-    for i, t in enumerate(orc_res["inputs"]):
-        tok, lg = dec.step_logits(t)
-        c, m = _check_step(i, lg.cpu(), orc_res["logits"][i], tok, orc_res["tokens"][i], orc_res["gaps"][i])
-        worst = (min(worst[0], c), max(worst[1], m))
-    return worst
-
-
-def test_decode_parity_qwen3_0p6b(shape, weights_cpu, weights_gpu, prompt):
-    """Qwen3-0.6B, 16-token prompt + 64 greedy steps, teacher-forced on the oracle's tokens."""
-    from oracle.qwen3_ref import OracleDecoder, greedy_stream
-
-    ref = greedy_stream(OracleDecoder(weights_cpu, shape, max_seq_len=2048), prompt, 64, record_logits=True)
-    worst = _teacher_forced(_decoder(weights_gpu), ref)
-    print("worst cos / max abs:", worst)
+def test_decode_parity_qwen3_0p6b(shape, exact06, weights_gpu, prompt):
+    """Config-0 shapes: 16-token prompt fed one step at a time, then 64 greedy steps; every row."""
+    feed, toks, lgs = kernel_stream(decoder(weights_gpu), prompt, 64)
+    ref = exact_oracle(exact06, shape, 2048).forward(feed)
+    print(check_rows(Tally("qwen3-0.6b 16+64"), ref, toks, lgs))
 
 
 def test_decode_parity_random_norm_weights(shape, prompt):
     """Non-unit norm weights (q/k/input/post/final) so an ignored norm weight fails."""
-    from oracle.qwen3_ref import OracleDecoder, greedy_stream
-    from qwen_megakernel_amd.weights import make_weights, to_device
+    from oracle.qwen3_exact import ExactOracle
+    from qwen_megakernel.weights import make_weights, to_device
 
     w = make_weights(shape, seed=5, norm_std=0.1, num_layers=3, max_seq_len=256)
-    ref = greedy_stream(OracleDecoder(w, shape, num_layers=3, max_seq_len=256), prompt, 16, record_logits=True)
-    _teacher_forced(_decoder(to_device(w, "cuda"), num_layers=3, max_seq_len=256), ref)
+    feed, toks, lgs = kernel_stream(decoder(to_device(w, "cuda"), num_layers=3, max_seq_len=256), prompt, 16)
+    ref = ExactOracle(w, shape, num_layers=3, max_seq_len=256).forward(feed)
+    print(check_rows(Tally("random norm weights, 3 layers"), ref, toks, lgs))
 
 
-def test_generate_nosync_matches_oracle_stream(shape, weights_cpu, weights_gpu, prompt):
-    """Free-running device-fed greedy stream equals the oracle's until its first near-tie."""
-    from oracle.qwen3_ref import OracleDecoder, greedy_stream
-
-    steps = 64
-    ref = greedy_stream(OracleDecoder(weights_cpu, shape, max_seq_len=2048), prompt, steps, record_logits=True)
-    dec = _decoder(weights_gpu)
-    out = dec.generate(prompt, steps)
-    assert len(out) == steps and dec.position == len(prompt) - 1 + steps
-    n0 = len(prompt) - 1
-    exp = ref["tokens"][n0:]
-    for i in range(steps):
-        if is_tie(ref["gaps"][n0 + i], float(ref["logits"][n0 + i].max())):
-            break  # the stream may legitimately diverge from the first tie on
-        assert out[i] == exp[i], f"generated token {i}: {out[i]} != {exp[i]}"
+def test_generate_nosync_matches_oracle_stream(shape, exact06, weights_gpu, prompt):
+    """The device-fed greedy stream (generate_nosync) is the oracle's, up to near-ties."""
+    dec = decoder(weights_gpu)
+    out = dec.generate(prompt, 64)
+    assert len(out) == 64 and dec.position == len(prompt) - 1 + 64
+    ref = stream_rows(exact_oracle(exact06, shape, 2048), prompt, out)
+    print(check_rows(Tally("generate 64"), ref, out))
 
 
 @pytest.fixture(scope="module")
-def bench_workload_ref(shape, weights_cpu):
-    """Oracle run of the decode benchmark's workload: the seeded 128-token prompt (seed 1), then
-    1024 greedy steps (contexts 129..1152), logits recorded at every step.
-
-    Also measures the reference path's own rounding noise on the first 383 steps: the largest
-    logit change when only its GEMV summation order changes (every projection as an fp32 matmul
-    rounded to bf16, fed the same tokens).  At this workload it is about 0.04, more than two bf16
-    ulps of a logit near 3, and the oracle's own token can flip under it: at step 200 the two
-    orders pick different tokens, and the same oracle gives a top-2 gap of one ulp on one host's
-    CPU and two on another's."""
-    import oracle.qwen3_ref as R
-    from qwen_megakernel_amd.weights import make_prompt
+def bench_workload(shape, exact06, weights_gpu):
+    """The decode benchmark's workload: the seeded 128-token prompt (seed 1) through the batched
+    prefill, then 1024 device-fed greedy steps (contexts 129..1152), and the exact oracle's
+    logits for every row that produced a generated token."""
+    from qwen_megakernel.weights import make_prompt
 
     prompt = make_prompt(128, shape.vocab, seed=1)
-    ref = R.greedy_stream(R.OracleDecoder(weights_cpu, shape, max_seq_len=2048), prompt, 1024, record_logits=True)
-
-    class _F:
-        pass
-
-    f = _F()
-    f.__dict__.update({k: getattr(R.F, k) for k in ("silu", "softmax")})
-    f.linear = lambda x, w: (x.float() @ w.float().t()).to(torch.bfloat16)
-    alt = R.OracleDecoder(weights_cpu, shape, max_seq_len=2048)
-    saved, floor = R.F, 0.0
-    R.F = f
-    try:
-        for i in range(len(prompt) - 1 + 256):
-            floor = max(floor, (alt.step_logits(ref["inputs"][i]) - ref["logits"][i]).abs().max().item())
-    finally:
-        R.F = saved
-    return prompt, ref, floor
-
-
-def _near_argmax(ref_logits: torch.Tensor, tok: int, floor: float) -> bool:
-    """``tok`` is within the reference path's rounding noise of the oracle's top logit."""
-    top = float(ref_logits.max())
-    return float(ref_logits[tok]) >= top - max(TIE_GAP, bf16_ulp(top), floor)
-
-
-def test_bench_workload_256_teacher_forced_steps(shape, weights_gpu, bench_workload_ref):
-    """The benchmark's prompt prefilled by the batched forward, then 256 decode steps fed the
-    oracle's tokens.  Every step: logits within cos >= 0.999 / max abs <= 0.1, and the argmax
-    equal to the oracle's, or else a token whose oracle logit is within the reference path's own
-    summation-order noise (measured live) of the top one."""
-    prompt, ref, floor = bench_workload_ref
-    n0 = len(prompt) - 1
-    dec = _decoder(weights_gpu)
-    worst, flips = (1.0, 0.0), []
-    tok, lg = dec.prefill(prompt[:-1], return_logits=True)
-    for i in range(n0 - 1, n0 + 256):
-        if i >= n0:
-            tok, lg = dec.step_logits(ref["inputs"][i])
-        g, r = lg.cpu(), ref["logits"][i]
-        cos = torch.nn.functional.cosine_similarity(g.double(), r.double(), dim=0).item()
-        mab = (g - r).abs().max().item()
-        assert cos >= COS_MIN, f"step {i}: cos {cos}"
-        assert mab <= ABS_MAX, f"step {i}: max abs {mab}"
-        if tok != ref["tokens"][i]:
-            assert _near_argmax(r, tok, floor), (
-                f"step {i}: token {tok} (oracle logit {float(r[tok])}) != {ref['tokens'][i]} "
-                f"(top {float(r.max())}), reference noise floor {floor}")
-            flips.append(i)
-        worst = (min(worst[0], cos), max(worst[1], mab))
-    print("256 teacher-forced steps after a 128-token prompt: worst cos %.6f, max abs %.4f; "
-          "reference noise floor %.4f; near-tie flips at steps %s" % (worst + (floor, flips)))
-
-
-def test_bench_workload_1024_step_stream(shape, weights_gpu, bench_workload_ref):
-    """The benchmark's generate path (batched prefill of the 128-token prompt, 1024 device-fed
-    greedy steps) emits the oracle's token stream until the two first differ, and at that step
-    the kernel's token is within the reference path's own rounding noise of the oracle's top
-    logit (a near-tie; after it the streams continue from different tokens)."""
-    prompt, ref, floor = bench_workload_ref
-    n0 = len(prompt) - 1
-    dec = _decoder(weights_gpu)
+    dec = decoder(weights_gpu)
     out = dec.generate(prompt, 1024)
-    assert len(out) == 1024 and dec.position == n0 + 1024
-    exp = ref["tokens"][n0:]
-    first = next((i for i in range(1024) if out[i] != exp[i]), 1024)
-    if first < 1024:
-        r = ref["logits"][n0 + first]
-        assert _near_argmax(r, out[first], floor), (
-            f"generated token {first}: {out[first]} (oracle logit {float(r[out[first]])}) != {exp[first]} "
-            f"(top {float(r.max())}), reference noise floor {floor}")
-    print(f"1024-step stream: the first {first} tokens equal the oracle's (noise floor {floor:.4f})")
+    assert len(out) == 1024 and dec.position == len(prompt) - 1 + 1024
+    assert int(torch.ops.qwen_megakernel_C.device_error()) == 0
+    orc = exact_oracle(exact06, shape, 2048)
+    seq = list(prompt) + out[:-1]
+    n0 = len(prompt) - 1
+    ref = orc.forward(seq, emit=list(range(n0 - 1, len(seq))))  # row n0-1: the prefill's last row
+    return prompt, out, ref
 
 
-def _fp32_order_noise_floor(weights_cpu, shape, setup, inputs, max_seq_len=2048, num_layers=None):
-    """Max abs logit deviation of the oracle from itself when only its GEMV summation order changes.
-
-    Runs the oracle with every projection computed as an fp32 matmul rounded to
-    bf16 (same semantics as torch's bf16 linear, different accumulation order)
-    and compares with the exact oracle.  This is the rounding-noise level of the
-    reference path itself at this workload.
-    """
-    import oracle.qwen3_ref as R
-
-    class _F:
-        pass
-
-    exact = R.OracleDecoder(weights_cpu, shape, max_seq_len=max_seq_len, num_layers=num_layers)
-    setup(exact)
-    alt = R.OracleDecoder(weights_cpu, shape, max_seq_len=max_seq_len, num_layers=num_layers)
-    setup(alt)
-    saved = R.F
-    f = _F()
-    f.__dict__.update({k: getattr(saved, k) for k in ("silu", "softmax")})
-    f.linear = lambda x, w: (x.float() @ w.float().t()).to(torch.bfloat16)
-    worst = 0.0
-    for t in inputs:
-        a = exact.step_logits(t)
-        R.F = f
-        try:
-            b = alt.step_logits(t)
-        finally:
-            R.F = saved
-        worst = max(worst, (a - b).abs().max().item())
-    return worst
+def test_bench_workload_1024_step_stream(bench_workload):
+    """Every one of the 1024 generated tokens is the oracle's argmax given the same prefix, up to
+    near-ties: the free-running stream equals the oracle's except where a near-tie lets them part.
+    The first 256 steps (the north star's stream length) at the literal bar, the rest at the deep
+    bar (the reference's own fp32 stream departs from the exact centre at 2-ulp gaps there)."""
+    prompt, out, ref = bench_workload
+    t = Tally("1024-step stream")
+    check_rows(t, ref[1:257], out[:256], bar=LITERAL)
+    print(check_rows(t, ref[257:], out[256:], labels=list(range(256, 1024)), bar=DEEP))
 
 
-def _with_rope(weights, max_seq_len, device):
-    """The same weights with RoPE tables long enough for ``max_seq_len`` positions."""
-    from qwen_megakernel_amd.weights import rope_tables
-
-    cos, sin = rope_tables(max_seq_len, 128, 1e6)
-    w = dict(weights)
-    w["cos_table"], w["sin_table"] = cos.to(device), sin.to(device)
-    return w
+def test_bench_workload_256_steps_with_logits(shape, exact06, weights_gpu, bench_workload):
+    """The same prompt prefilled, then 256 decode steps (one launch each, logits out) on the
+    decoder's own tokens: every row's logits within the bar, the prefill's last row too."""
+    prompt, out, ref = bench_workload
+    n0 = len(prompt) - 1
+    dec = decoder(weights_gpu)
+    tok, lg = dec.prefill(prompt[:-1], return_logits=True)
+    t = Tally("prefill + 256 steps")
+    check_rows(t, ref[:1], [tok], lg[None].cpu(), labels=["prefill"])
+    feed, toks, lgs = [prompt[-1]], [], []
+    for i in range(256):
+        tk, l = dec.step_logits(feed[-1])
+        toks.append(tk)
+        lgs.append(l.cpu())
+        feed.append(tk)
+    if toks == out[:256]:
+        rows = ref[1:257]
+    else:  # a different stream (it may part from generate's at a near-tie): its own oracle rows
+        rows = stream_rows(exact_oracle(exact06, shape, 2048), prompt, toks)
+    print(check_rows(t, rows, toks, torch.stack(lgs)))
 
 
 @pytest.mark.parametrize(
-    "c0,layers,steps,strict",
-    [(1500, 4, 6, True), (1500, 28, 4, False), (2100, 4, 6, True), (8192, 4, 4, True), (8192, 28, 3, False),
-     (32768, 28, 2, False)],
-    ids=["1500-4layers", "1500-28layers", "2100-4layers", "8192-4layers", "8192-28layers", "32768-28layers"])
-def test_long_context_parity(shape, weights_cpu, weights_gpu, c0, layers, steps, strict):
+    "c0,layers,steps",
+    [(1500, 4, 6), (1500, 28, 8), (2100, 4, 6), (2100, 28, 8), (8192, 4, 4), (8192, 28, 16), (32768, 28, 8)],
+    ids=["1500-4layers", "1500-28layers", "2100-4layers", "2100-28layers", "8192-4layers", "8192-28layers",
+         "32768-28layers"])
+def test_long_context_parity(shape, exact06, weights_gpu, c0, layers, steps):
     """Attention over an injected N(0,1) cache of c0 positions (split-K over the 32 workgroups of
-    an XCD; above 2048 positions each wave streams several K/V batches through the LDS ring, and
-    the long-context kernel runs: at 2100 wave 0 has a second, partial batch).
-
-    Cosine >= 0.999 at every step.  Max abs <= 0.1 for the 4-layer cases; for 28 layers the
-    bound is max(0.1, 1.5 x the reference's own noise floor at this workload, measured live):
-    with random N(0,1) K/V the reference path moves by ~0.1 when only its GEMV summation order
-    changes, so 0.1 alone would test the summation order, not the kernel.
-    """
-    from oracle.qwen3_ref import OracleDecoder, greedy_stream
-    from qwen_megakernel_amd.weights import make_kv_prefill
+    an XCD; above 2048 positions the long-context kernel runs, each wave streaming several K/V
+    batches through the LDS ring; at 2100 wave 0 has a second, partial batch).  Every step
+    against the exact oracle, and the K/V rows the kernel appended.  4 layers: the literal bar;
+    28 layers: the deep bar (no fp32 implementation holds the literal one there, tests/parity.py)."""
+    from qwen_megakernel.weights import make_kv_prefill
 
     max_seq = c0 + 64
-    wc = _with_rope(weights_cpu, max_seq, "cpu")
-    wg = _with_rope(weights_gpu, max_seq, "cuda")
     k, v = make_kv_prefill(shape, c0, seed=2)
-    orc = OracleDecoder(wc, shape, num_layers=layers, max_seq_len=max_seq)
-    orc.load_kv(k, v, c0)
-    ref = greedy_stream(orc, [11, 22], steps, record_logits=True)
-    bound, floor = ABS_MAX, None
-    if not strict:
-        floor = _fp32_order_noise_floor(wc, shape, lambda d: d.load_kv(k, v, c0), ref["inputs"], max_seq, layers)
-        bound = max(ABS_MAX, 1.5 * floor)
-    dec = _decoder(wg, num_layers=layers, max_seq_len=max_seq)
+    dec = decoder(with_rope(weights_gpu, max_seq, "cuda"), num_layers=layers, max_seq_len=max_seq)
     dec.load_kv(k.cuda(), v.cuda(), c0)
-    worst = 0.0
-    for i, t in enumerate(ref["inputs"]):
-        tok, lg = dec.step_logits(t)
-        g, r = lg.cpu(), ref["logits"][i]
-        cos = torch.nn.functional.cosine_similarity(g.double(), r.double(), dim=0).item()
-        mab = (g - r).abs().max().item()
-        worst = max(worst, mab)
-        assert cos >= COS_MIN, f"step {i}: cos {cos}"
-        assert mab <= bound, f"step {i}: max abs {mab} > {bound} (reference noise floor {floor})"
-        if tok != ref["tokens"][i]:
-            assert is_tie(ref["gaps"][i], float(r.max())), f"step {i}: token {tok} != {ref['tokens'][i]}"
-    # the kernel appended K/V for the new positions like the oracle did (every layer for the
-    # 4-layer cases; layer 0 only for 28 layers, where deeper layers carry the noise above)
-    pos = c0 + len(ref["inputs"])
-    nl = layers if strict else 1
+    feed, toks, lgs = kernel_stream(dec, [11, 22], steps)
+    orc = exact_oracle(exact06, shape, max_seq, num_layers=layers, kv=(k, v), cache_len=c0)
+    ref = orc.forward(feed)
+    print(check_rows(Tally(f"context {c0} x {layers} layers"), ref, toks, lgs, bar=DEEP if layers == 28 else LITERAL))
+    # the appended K/V rows: layer 0 within one bf16 ulp of |v| <= 8 (0.0625), every layer's rows
+    # with cosine >= 0.999 (deeper layers carry the accumulated rounding differences)
+    pos = c0 + len(feed)
     for name, got, exp in (("K", dec._k_cache, orc.k_cache), ("V", dec._v_cache, orc.v_cache)):
-        d = (got[:nl, :, c0:pos].float().cpu() - exp[:nl, :, c0:pos].float()).abs().max().item()
-        assert d <= 0.05, f"{name} cache rows written by the kernel differ by {d}"
-    print(f"long context {c0} x {layers} layers: worst max abs {worst:.4f}"
-          + (f", reference noise floor {floor:.4f}" if floor is not None else ""))
+        g, e = got[:, :, c0:pos].float().cpu(), exp[:, :, c0:pos].float()
+        d0 = (g[0] - e[0]).abs().max().item()
+        assert d0 <= 0.0625, f"layer-0 {name} rows differ by {d0}"
+        cos = torch.nn.functional.cosine_similarity(g.flatten().double(), e.flatten().double(), dim=0).item()
+        assert cos >= 0.999, f"{name} rows cosine {cos}"
 
 
 def test_generate_across_long_context_boundary(shape, weights_gpu):
@@ -313,15 +134,15 @@ def test_generate_across_long_context_boundary(shape, weights_gpu):
     from the short-context kernel to the long-context one after context 2048, each form with its
     own recorded graph.  Its tokens equal those of 100 per-step launches, which pick the kernel by
     the same rule, with graph replay and with direct launches."""
-    from qwen_megakernel_amd.build import get_extension
-    from qwen_megakernel_amd.weights import make_kv_prefill
+    from qwen_megakernel.build import get_extension
+    from qwen_megakernel.weights import make_kv_prefill
 
     c0, n, max_seq = 1990, 100, 2200
-    wg = _with_rope(weights_gpu, max_seq, "cuda")
+    wg = with_rope(weights_gpu, max_seq, "cuda")
     k, v = make_kv_prefill(shape, c0, seed=3)
 
     def fresh():
-        d = _decoder(wg, max_seq_len=max_seq)
+        d = decoder(wg, max_seq_len=max_seq)
         d.load_kv(k.cuda(), v.cuda(), c0)
         return d
 
@@ -344,7 +165,7 @@ def test_generate_across_long_context_boundary(shape, weights_gpu):
 
 
 def test_last_position_and_bounds(shape, weights_gpu):
-    dec = _decoder(weights_gpu, max_seq_len=64)
+    dec = decoder(weights_gpu, max_seq_len=64)
     dec._position = 63
     tok = dec.step(5)
     assert 0 <= tok < shape.vocab and dec.position == 64
@@ -356,8 +177,8 @@ def test_last_position_and_bounds(shape, weights_gpu):
 
 
 def test_deterministic(weights_gpu, prompt):
-    a = _decoder(weights_gpu)
-    b = _decoder(weights_gpu)
+    a = decoder(weights_gpu)
+    b = decoder(weights_gpu)
     for t in prompt[:6]:
         ta, la = a.step_logits(t)
         tb, lb = b.step_logits(t)
@@ -365,11 +186,11 @@ def test_deterministic(weights_gpu, prompt):
 
 
 def test_two_streams_do_not_interfere(weights_gpu, prompt):
-    """Per-stream device state: two decoders on two streams, interleaved."""
-    ref = _decoder(weights_gpu)
+    """Per-stream device state: two decoders on two streams, interleaved step by step."""
+    ref = decoder(weights_gpu)
     expect = [ref.step(t) for t in prompt[:8]]
     s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
-    d1, d2 = _decoder(weights_gpu), _decoder(weights_gpu)
+    d1, d2 = decoder(weights_gpu), decoder(weights_gpu)
     got1, got2 = [], []
     for t in prompt[:8]:
         with torch.cuda.stream(s1):
@@ -379,13 +200,57 @@ def test_two_streams_do_not_interfere(weights_gpu, prompt):
     assert got1 == expect and got2 == expect
 
 
-def test_c_abi_matches_torch_op(weights_gpu, prompt):
-    """launch_ldg_decode_direct / _persistent through ctypes give the op's token and cache."""
-    from qwen_megakernel_amd.build import load_c_library
+def _c_generate(lib, dec, first, steps, start, out, stream):
+    vp = ctypes.c_void_p
+    st = lib.qmk_generate_model(
+        ctypes.c_int(0), ctypes.c_int(first), ctypes.c_int(steps), vp(dec._embed_weight.data_ptr()),
+        vp(dec._layer_weights_packed.data_ptr()), vp(dec._final_norm_weight.data_ptr()),
+        vp(dec._lm_head_weight.data_ptr()), vp(dec._cos_table.data_ptr()), vp(dec._sin_table.data_ptr()),
+        vp(dec._k_cache.data_ptr()), vp(dec._v_cache.data_ptr()), vp(dec._hidden.data_ptr()),
+        vp(dec._norm_out.data_ptr()), vp(out.data_ptr()), ctypes.c_int(28), ctypes.c_int(start),
+        ctypes.c_int(dec._max_seq_len), ctypes.c_float(dec._attn_scale), vp(stream.cuda_stream))
+    assert st == 0, lib.qmk_status_string(st)
+
+
+def test_concurrent_generate_on_two_streams(shape, weights_gpu, prompt):
+    """Two device-fed generate loops enqueued on two streams with no host synchronisation in
+    between (through the C ABI, which does not synchronise).  Every launch needs all 256 CUs, so
+    the library orders the second loop's launches after the first's; without that the two
+    kernels would share the chip, wait for absent workgroups and latch a time-out.  Both streams
+    give the single-stream tokens and no device error."""
+    from qwen_megakernel.build import load_c_library
 
     lib = load_c_library()
-    a = _decoder(weights_gpu)
-    b = _decoder(weights_gpu)
+    lib.qmk_status_string.restype = ctypes.c_char_p
+    steps = 200
+    ref = decoder(weights_gpu)
+    expect = ref.generate(prompt, steps)
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    d1, d2 = decoder(weights_gpu), decoder(weights_gpu)
+    for d in (d1, d2):
+        d.prefill(prompt[:-1])
+    torch.cuda.synchronize()
+    o1 = torch.empty(steps, dtype=torch.int32, device="cuda")
+    o2 = torch.empty(steps, dtype=torch.int32, device="cuda")
+    start = len(prompt) - 1
+    _c_generate(lib, d1, prompt[-1], steps, start, o1, s1)
+    _c_generate(lib, d2, prompt[-1], steps, start, o2, s2)
+    s1.synchronize()
+    s2.synchronize()
+    ops = torch.ops.qwen_megakernel_C
+    for s in (s1, s2):
+        with torch.cuda.stream(s):
+            assert int(ops.device_error()) == 0
+    assert o1.cpu().tolist() == expect and o2.cpu().tolist() == expect
+
+
+def test_c_abi_matches_torch_op(weights_gpu, prompt):
+    """launch_ldg_decode_direct / _persistent through ctypes give the op's token and cache."""
+    from qwen_megakernel.build import load_c_library
+
+    lib = load_c_library()
+    a = decoder(weights_gpu)
+    b = decoder(weights_gpu)
     vp = ctypes.c_void_p
     stream = vp(torch.cuda.current_stream().cuda_stream)
 
@@ -411,7 +276,7 @@ def test_c_abi_matches_torch_op(weights_gpu, prompt):
 def test_failure_path_is_bounded_and_resettable(weights_gpu, prompt):
     """A forced one-tick wait bound makes the step fail fast; reset() recovers."""
     ops = torch.ops.qwen_megakernel_C
-    dec = _decoder(weights_gpu)
+    dec = decoder(weights_gpu)
     good = dec.step(prompt[0])
     dec.reset()
     ops.set_wait_limit(1)
@@ -428,9 +293,26 @@ def test_failure_path_is_bounded_and_resettable(weights_gpu, prompt):
     assert dec.step(prompt[0]) == good
 
 
-def test_many_steps_stream(weights_gpu, prompt):
-    """1024 consecutive device-fed steps (context 16 -> 1039) without a device error."""
-    dec = _decoder(weights_gpu)
-    out = dec.generate(prompt, 1024)
-    assert len(out) == 1024 and all(0 <= t < 151936 for t in out)
-    assert int(torch.ops.qwen_megakernel_C.device_error()) == 0
+def test_ten_thousand_step_stream(shape, weights_gpu, prompt):
+    """10,000 consecutive device-fed steps (contexts 16..10,015; about 39 wraps of the 16-bit
+    exchange tags, the long-context kernel from context 2049 on) without a device error, twice:
+    on a fresh stream state, and on a second stream whose tags were first advanced by 37 launches,
+    so the two runs meet every tag wrap at different steps.  The two streams are identical."""
+    steps, max_seq = 10000, 10048
+    wg = with_rope(weights_gpu, max_seq, "cuda")
+    ops = torch.ops.qwen_megakernel_C
+    outs = []
+    for i, s in enumerate((torch.cuda.Stream(), torch.cuda.Stream())):
+        with torch.cuda.stream(s):
+            ops.reset()
+            if i == 1:
+                warm = decoder(wg, max_seq_len=max_seq)
+                ops.generate_nosync(7, 37, *warm._scratch(), shape.num_layers, 0, max_seq, warm._attn_scale)
+            dec = decoder(wg, max_seq_len=max_seq)
+            dec.prefill(prompt[:-1])
+            out = ops.generate_nosync(prompt[-1], steps, *dec._scratch(), shape.num_layers, len(prompt) - 1,
+                                      max_seq, dec._attn_scale).cpu().tolist()
+            assert int(ops.device_error()) == 0
+        assert all(0 <= t < shape.vocab for t in out)
+        outs.append(out)
+    assert outs[0] == outs[1], f"first difference at step {next(i for i in range(steps) if outs[0][i] != outs[1][i])}"

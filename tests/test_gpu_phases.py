@@ -7,8 +7,8 @@ pytestmark = pytest.mark.gpu
 
 
 def _setup(pid, n=2, seed=3):
-    from qwen_megakernel_amd.build import get_extension
-    from qwen_megakernel_amd.phases import make_inputs, phases, run
+    from qwen_megakernel.build import get_extension
+    from qwen_megakernel.phases import make_inputs, phases, run
 
     get_extension()
     ph = phases()[pid]
@@ -56,7 +56,7 @@ def test_phase_gate_up_silu_mul():
 
 
 def test_phase_lm_head_argmax():
-    from qwen_megakernel_amd.phases import argmax_from_keys
+    from qwen_megakernel.phases import argmax_from_keys
 
     ph, w, act, norm, out = _setup(4)
     logits = (w.view(151936, 1024).float() @ act.float()).to(torch.bfloat16).float()

@@ -1,4 +1,4 @@
-"""GPU tests of sampling (qwen_megakernel_amd/csrc/qmk_sample.hip) against the
+"""GPU tests of sampling (qwen_megakernel/csrc/qmk_sample.hip) against the
 sampling oracle (oracle/sampling_ref.py, itself pinned against HF's warpers in
 tests/test_sampling.py).
 
@@ -14,13 +14,13 @@ import pytest
 import torch
 
 from oracle import sampling_ref as S
-from test_gpu_decode import _decoder, prompt, shape, weights_cpu, weights_gpu  # noqa: F401
+from parity import decoder as _decoder
 
 pytestmark = pytest.mark.gpu
 
 
 def _ops():
-    from qwen_megakernel_amd.build import get_extension
+    from qwen_megakernel.build import get_extension
 
     return get_extension()
 
@@ -179,8 +179,8 @@ def test_generate_sample_stops_at_eos(weights_gpu, prompt):
 def test_batch_sampled_generate_matches_host_loop(shape, weights_gpu):
     """BatchDecoder with sampling: per-sequence counters (position + sequence << 32), each row the
     oracle's draw from that row's logits."""
-    from qwen_megakernel_amd.model import BatchDecoder
-    from qwen_megakernel_amd.weights import make_prompt
+    from qwen_megakernel.model import BatchDecoder
+    from qwen_megakernel.weights import make_prompt
 
     T, k, p, seed, n = 1.1, 0, 0.9, 21, 8
     prompts = [make_prompt(m, shape.vocab, seed=30 + m) for m in (6, 11)]

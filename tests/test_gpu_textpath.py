@@ -10,13 +10,13 @@ work (single steps, resets) in between.
 import pytest
 import torch
 
-from test_gpu_decode import _decoder, prompt, shape, weights_cpu, weights_gpu  # noqa: F401
+from parity import decoder as _decoder
 
 pytestmark = pytest.mark.gpu
 
 
 def _ops():
-    from qwen_megakernel_amd.build import get_extension
+    from qwen_megakernel.build import get_extension
 
     return get_extension()
 

@@ -10,7 +10,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 
 
 def _tiny():
-    from qwen_megakernel_amd.shapes import Qwen3Shape
+    from qwen_megakernel.shapes import Qwen3Shape
 
     cfg = json.load(open(os.path.join(HERE, "golden", "hf_tiny_keys.json")))
     c = cfg["config"]
@@ -27,8 +27,8 @@ def _state_from_hf_keys(keys, seed=0, tie=True):
 
 
 def test_loader_consumes_hf_key_names_in_reference_order():
-    from qwen_megakernel_amd.shapes import LAYER_TENSOR_NAMES
-    from qwen_megakernel_amd.weights import load_weights_from_state_dict
+    from qwen_megakernel.shapes import LAYER_TENSOR_NAMES
+    from qwen_megakernel.weights import load_weights_from_state_dict
 
     shape, keys = _tiny()
     sd = _state_from_hf_keys(keys)
@@ -51,7 +51,7 @@ def test_loader_consumes_hf_key_names_in_reference_order():
 
 
 def test_loader_untied_head_and_shape_errors():
-    from qwen_megakernel_amd.weights import load_weights_from_state_dict
+    from qwen_megakernel.weights import load_weights_from_state_dict
 
     shape, keys = _tiny()
     sd = _state_from_hf_keys(keys, tie=False)
@@ -69,12 +69,12 @@ def test_loader_untied_head_and_shape_errors():
 
 def test_safetensors_directory_roundtrip_gives_identical_oracle_logits(tmp_path):
     """Save seeded weights as an HF-named safetensors checkpoint, load them back through
-    qwen_megakernel_amd.load_weights, and decode with the oracle: logits are bit-identical."""
+    qwen_megakernel.load_weights, and decode with the oracle: logits are bit-identical."""
     from safetensors.torch import save_file
 
     from oracle.qwen3_ref import OracleDecoder
-    from qwen_megakernel_amd.model import load_weights
-    from qwen_megakernel_amd.weights import make_weights
+    from qwen_megakernel.model import load_weights
+    from qwen_megakernel.weights import make_weights
 
     shape, keys = _tiny()
     w = make_weights(shape, seed=0, norm_std=0.1, max_seq_len=32)

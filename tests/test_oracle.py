@@ -18,8 +18,8 @@ import pytest
 import torch
 
 from oracle.qwen3_ref import OracleDecoder, apply_rope, attention, greedy_stream, rms_norm, rotate_half, top2_gap
-from qwen_megakernel_amd.shapes import QWEN3_0_6B, Qwen3Shape
-from qwen_megakernel_amd.weights import make_kv_prefill, make_prompt, make_weights, rope_tables
+from qwen_megakernel.shapes import QWEN3_0_6B, Qwen3Shape
+from qwen_megakernel.weights import make_kv_prefill, make_prompt, make_weights, rope_tables
 
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
 TINY = Qwen3Shape("tiny", 2, 256, 512, 4, 2, 64, 1000)

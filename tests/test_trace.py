@@ -2,7 +2,7 @@
 
 import numpy as np
 
-from qwen_megakernel_amd import trace
+from qwen_megakernel import trace
 
 
 def test_summarize_synthetic_stamps():
