@@ -76,9 +76,10 @@ struct DevInfo {
   uint32_t ticks_per_s = 100000000u;
   // cross-stream ordering of decode launches on this device
   std::mutex order_mu;
-  hipEvent_t order_evt = nullptr;      // recorded after the last decode launch group
-  hipStream_t order_stream = nullptr;  // the stream it was recorded on
+  hipEvent_t order_evt = nullptr;      // recorded after every group once order_multi is set
+  hipStream_t order_stream = nullptr;  // the stream of the last decode launch group
   bool order_valid = false;
+  bool order_multi = false;            // a second stream has launched on this device
 };
 
 std::mutex g_mu;
@@ -188,35 +189,46 @@ int check_device(int dev, DevInfo** out) {
 }
 
 // Orders one group of decode launches on `stream` after the previous group on
-// the same device, whatever stream that was on: a wait on the event recorded
-// after it (nothing when it was on the same stream), then, once the group is
-// enqueued, an event record on `stream`.  The lock keeps the wait, the
-// launches and the record of one group together against other host threads.
-// A stream under graph capture is left alone (the graph's owner orders its
-// replays).
+// the same device, whatever stream that was on.  While a device sees one
+// stream nothing is added (a marker after every launch costs 4 us between
+// back-to-back kernels, measured).  When a second stream first launches, the
+// device is synchronised once, and from then on an event is recorded after
+// every group, on the stream that group used, and a group on another stream
+// waits on it.  The lock keeps the check, the wait, the launches and the
+// record of one group together against other host threads.  A stream under
+// graph capture is left alone (the graph's owner orders its replays).
 class DeviceOrder {
  public:
   DeviceOrder(DevInfo* di, hipStream_t stream) : di_(di), stream_(stream), lk_(di->order_mu) {
-    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(stream, &cs) != hipSuccess) cs = hipStreamCaptureStatusNone;
-    capturing_ = cs != hipStreamCaptureStatusNone;
-    if (!capturing_ && di_->order_valid && di_->order_stream != stream_)
-      ok_ = hipStreamWaitEvent(stream_, di_->order_evt, 0) == hipSuccess;
+    capturing_ = capturing(stream);
+    if (capturing_) return;
+    if (di_->order_valid && di_->order_stream != stream) {
+      if (!di_->order_multi) {
+        ok_ = hipDeviceSynchronize() == hipSuccess;
+        di_->order_multi = true;
+      } else {
+        ok_ = hipStreamWaitEvent(stream, di_->order_evt, 0) == hipSuccess;
+      }
+    }
+    di_->order_stream = stream;
+    di_->order_valid = true;
   }
   bool ok() const { return ok_; }
-  // call after the group's launches were enqueued
+  // call once the group's launches are enqueued
   int finish() {
-    if (capturing_) return QMK_OK;
-    if (hipEventRecord(di_->order_evt, stream_) != hipSuccess) {
-      di_->order_valid = false;
-      return QMK_ERR_HIP;
-    }
-    di_->order_stream = stream_;
-    di_->order_valid = true;
-    return QMK_OK;
+    if (capturing_ || !di_->order_multi) return QMK_OK;
+    return hipEventRecord(di_->order_evt, stream_) == hipSuccess ? QMK_OK : QMK_ERR_HIP;
   }
 
  private:
+  static bool capturing(hipStream_t s) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &cs) != hipSuccess) {
+      (void)hipGetLastError();
+      return false;
+    }
+    return cs != hipStreamCaptureStatusNone;
+  }
   DevInfo* di_;
   hipStream_t stream_;
   std::lock_guard<std::mutex> lk_;
