@@ -39,14 +39,19 @@ State and layout follow the reference's decode step (csrc/kernel.cu:1210,
 ``[L, NKV, S, D]`` bf16 cache, attention over ``0..p``.  :meth:`forward`
 runs T tokens at consecutive positions at once (causal); because every
 reduction is exact, each row is the same as a one-token step, so a whole
-token stream is checked in one pass.
+token stream is checked in one pass.  With ``given_cache`` it runs them over
+another decoder's cache instead of its own: each row then sees exactly the
+inputs that decoder's step saw (its earlier K/V rows), which is how a kernel's
+steps are compared one by one without the two trajectories drifting apart.
 
 Pinned by tests/test_oracle_exact.py: the single rounding against a brute
 force over the two bf16 neighbours (midpoint cases included), exact dots
 against ``math.fsum``, batched rows against one-token steps (bit for bit), the
-closed forms of attention, HF's golden logits (hf_tiny.npz in full,
-hf_qwen3_0p6b.npz top-16 values and tokens) within a few bf16 ulps, and the
-fp32-accumulating oracle within the same bound.
+closed forms of attention, the given-cache mode against the ordinary one on
+the oracle's own cache (bit for bit) and on a perturbed one, HF's golden
+logits (hf_tiny.npz in full, hf_qwen3_0p6b.npz top-16 values and tokens)
+within a few bf16 ulps, and the fp32-accumulating oracle within the same
+bound.
 """
 
 from __future__ import annotations
@@ -173,8 +178,13 @@ class ExactOracle:
         self.v_cache[:, :, :cache_len] = v[: self.num_layers, :, :cache_len]
         self.position = cache_len
 
-    def _attention(self, li: int, q: torch.Tensor, p0: int, t: int) -> torch.Tensor:
-        """q: bf16 ``[NQ, T, D]`` at positions p0..p0+T-1; returns bf16 ``[T, NQ*D]``."""
+    def _attention(self, li: int, q: torch.Tensor, p0: int, t: int, own=None) -> torch.Tensor:
+        """q: bf16 ``[NQ, T, D]`` at positions p0..p0+T-1; returns bf16 ``[T, NQ*D]``.
+
+        ``own = (k, v)`` (bf16 ``[NKV, T, D]``): row i attends to the cache's rows
+        for positions below p0+i and to ``own``'s row i at p0+i (the cache holds
+        another decoder's rows there); otherwise the cache holds this oracle's rows.
+        """
         s = self.shape
         rep = s.num_q_heads // s.num_kv_heads
         c = p0 + t
@@ -182,24 +192,39 @@ class ExactOracle:
         v64 = self.v_cache[li, :, :c].to(F64)
         qg = q.to(F64).contiguous().view(s.num_kv_heads, rep * t, s.head_dim)  # heads 2g, 2g+1 share kv head g
         sc = round_bf16(qg @ k64.transpose(1, 2))  # [NKV, rep*T, C]
+        rows = torch.arange(rep * t)
+        diag = p0 + rows % t  # the position of row r = r // t * t + i is p0 + i
+        if own is not None:
+            k_own = own[0].to(F64).repeat(1, rep, 1)  # row r -> own row r % t
+            sc[:, rows, diag] = round_bf16((qg * k_own).sum(-1))
         sc = round_bf16(sc.to(F64) * self.scale).to(F64)
         # causal: row i (position p0+i) sees positions 0..p0+i
         pos = torch.arange(c)
-        row_pos = (p0 + torch.arange(t)).repeat(rep)
-        mask = pos[None, :] > row_pos[:, None]
+        mask = pos[None, :] > diag[:, None]
         sc = sc.masked_fill(mask[None], float("-inf"))
         m = sc.max(-1, keepdim=True).values
         e = torch.exp(sc - m)
-        pr = round_bf16(e / e.sum(-1, keepdim=True))
-        out = round_bf16(pr.to(F64) @ v64)  # [NKV, rep*T, D]
+        pr = round_bf16(e / e.sum(-1, keepdim=True)).to(F64)
+        if own is None:
+            out = round_bf16(pr @ v64)  # [NKV, rep*T, D]
+        else:
+            p_diag = pr[:, rows, diag].clone()
+            pr[:, rows, diag] = 0.0
+            out = round_bf16(pr @ v64 + p_diag[..., None] * own[1].to(F64).repeat(1, rep, 1))
         out = out.view(s.num_kv_heads, rep, t, s.head_dim).permute(2, 0, 1, 3)
         return out.reshape(t, s.num_q_heads * s.head_dim)
 
     @torch.no_grad()
-    def hidden(self, tokens: list[int]) -> torch.Tensor:
+    def hidden(self, tokens: list[int], given_cache: bool = False) -> torch.Tensor:
         """Run the decoder layers over ``tokens`` at positions position..position+T-1; bf16 ``[T, H]``.
 
-        Appends their K/V to the cache and advances the position.
+        Appends their K/V to the cache and advances the position.  With
+        ``given_cache`` the cache already holds another decoder's rows for these
+        positions (and all before): row i then attends to those rows below its
+        position and to its own K/V at its position, so every row is computed from
+        exactly the inputs that decoder's step had; the cache is left as it is and
+        this oracle's own K/V rows are kept in ``own_k`` / ``own_v``
+        (``[L, NKV, T, D]``) for comparison with the given ones.
         """
         s = self.shape
         t = len(tokens)
@@ -210,6 +235,9 @@ class ExactOracle:
         sin = self.sin[p0:p0 + t].view(1, t, s.head_dim)
         x = self.embed[torch.tensor(tokens, dtype=torch.long)]  # [T, H] bf16
         eps = s.rms_eps
+        if given_cache:
+            self.own_k = torch.empty(self.num_layers, s.num_kv_heads, t, s.head_dim, dtype=BF16)
+            self.own_v = torch.empty_like(self.own_k)
         for li, L in enumerate(self.layers):
             residual = x
             h = rms_norm(x, L["w_in"], eps)
@@ -218,9 +246,13 @@ class ExactOracle:
             v = exact_linear(h, L["wv"]).view(t, s.num_kv_heads, s.head_dim).transpose(0, 1)
             q = apply_rope(rms_norm(q, L["wqn"], eps), cos, sin)
             k = apply_rope(rms_norm(k, L["wkn"], eps), cos, sin)
-            self.k_cache[li, :, p0:p0 + t] = k
-            self.v_cache[li, :, p0:p0 + t] = v
-            a = self._attention(li, q, p0, t)
+            if given_cache:
+                self.own_k[li], self.own_v[li] = k, v
+                a = self._attention(li, q, p0, t, own=(k, v))
+            else:
+                self.k_cache[li, :, p0:p0 + t] = k
+                self.v_cache[li, :, p0:p0 + t] = v
+                a = self._attention(li, q, p0, t)
             x = residual + exact_linear(a, L["wo"])
             residual = x
             h = rms_norm(x, L["w_post"], eps)
@@ -237,10 +269,11 @@ class ExactOracle:
         rows = [exact_linear(n[i:i + chunk], self.lm_head64).float() for i in range(0, n.shape[0], chunk)]
         return torch.cat(rows, 0)
 
-    def forward(self, tokens: list[int], emit=None) -> torch.Tensor:
+    def forward(self, tokens: list[int], emit=None, given_cache: bool = False) -> torch.Tensor:
         """Logits ``[len(emit), V]`` (fp32 holding bf16 values) of the rows ``emit`` (default: all)
-        after running ``tokens`` at consecutive positions from the current one."""
-        x = self.hidden(list(tokens))
+        after running ``tokens`` at consecutive positions from the current one (``given_cache``:
+        see :meth:`hidden`)."""
+        x = self.hidden(list(tokens), given_cache)
         if emit is not None:
             x = x[torch.as_tensor(emit, dtype=torch.long)]
         return self.logits(x)
@@ -253,17 +286,3 @@ def top2(logits: torch.Tensor):
     """(argmax with first-index ties, top-2 gap, top value) of a logits row."""
     v, i = torch.topk(logits, 2)
     return int(torch.argmax(logits)), float(v[0] - v[1]), float(v[0])
-
-
-def score_stream(orc: ExactOracle, prompt: list[int], generated: list[int], emit_prompt_last: bool = True):
-    """Teacher-forced evaluation of a token stream in one pass.
-
-    ``prompt`` then ``generated`` (the tokens a decoder produced after it) are
-    run from the oracle's current position; returns the oracle's logits for
-    the rows that produced each generated token (the last prompt row and every
-    generated row but the last), so row i is the oracle's distribution for
-    ``generated[i]`` given the same prefix.
-    """
-    seq = list(prompt) + list(generated[:-1])
-    n0 = len(prompt) - 1
-    return orc.forward(seq, emit=list(range(n0, len(seq))))

@@ -1,17 +1,20 @@
 """GPU parity tests of the batched forward (prompt prefill and batched decode).
 
 The batched path (qwen_megakernel/csrc/qmk_batch.hip, MFMA GEMMs) is checked
-against the exact CPU oracle, which runs the same tokens in one pass: each of
-its rows is exactly a decode step at that position (causal, exact reductions),
-so every prefilled row and every batched step has its expected logits.  Same
-bar as the decode kernel (tests/parity.py): cosine >= 0.999 and max abs <= 0.1
-per row, greedy tokens equal to the oracle's argmax except at near-ties.
+against the exact CPU oracle, which runs the same tokens in one pass over the
+batched path's own cache: each of its rows is exactly a decode step at that
+position on the inputs that row had (causal, exact reductions), so every
+prefilled row and every batched step has its expected logits.  Same bar as the
+decode kernel (tests/parity.py): cosine >= 0.999 and max abs <= 0.1 per row,
+greedy tokens equal to the oracle's argmax except at near-ties, K/V rows equal
+up to rounding.
 """
 
 import pytest
 import torch
 
-from parity import Tally, check_row, check_rows, decoder, exact_oracle, stream_rows, with_rope
+from parity import (LAYERS28, LITERAL, Tally, check_kv_rows, check_row, check_rows, decoder, exact_oracle, oracle_steps,
+                    stream_rows, with_rope)
 
 pytestmark = pytest.mark.gpu
 
@@ -48,28 +51,18 @@ def test_mfma_operand_layout():
     assert err <= 1e-4, f"MFMA layout/result mismatch: max abs {err}"
 
 
-def _check_cache(dec_k, dec_v, orc, p0, p1):
-    """K/V rows [p0, p1) the forward wrote: layer 0 within one bf16 ulp at |x| < 8, all layers cos >= 0.999."""
-    for name, got, exp in (("K", dec_k, orc.k_cache), ("V", dec_v, orc.v_cache)):
-        g, e = got[:, :, p0:p1].float().cpu(), exp[:, :, p0:p1].float()
-        d = (g[0] - e[0]).abs().max().item()
-        assert d <= 0.0625, f"layer-0 {name} cache rows differ by {d}"
-        cos = torch.nn.functional.cosine_similarity(g.flatten().double(), e.flatten().double(), dim=0).item()
-        assert cos >= 0.999, f"{name} cache cosine {cos}"
-
-
 @pytest.mark.parametrize("n", [12, 40], ids=["12tok-split-attention", "40tok-rowwise-attention"])
 def test_prefill_all_rows_match_oracle(shape, exact06, weights_gpu, n):
     """Every row of a 28-layer prefill against the oracle's row at that position; K/V written alike."""
     from qwen_megakernel.weights import make_prompt
 
     ids = make_prompt(n, shape.vocab, seed=3)
-    orc = exact_oracle(exact06, shape, 2048)
-    ref = orc.forward(ids)
     dec = decoder(weights_gpu)
     toks, logits = _forward_rows(dec._forward, ids, 0, dec._k_cache, dec._v_cache)
-    print(check_rows(Tally(f"prefill {n} rows"), ref, toks, logits))
-    _check_cache(dec._k_cache, dec._v_cache, orc, 0, n)
+    orc = exact_oracle(exact06, shape, 2048)
+    ref = oracle_steps(orc, dec._k_cache, dec._v_cache, 0, ids)
+    print(check_rows(Tally(f"prefill {n} rows"), ref, toks, logits, bar=LAYERS28))
+    check_kv_rows(f"prefill {n} rows", orc, dec._k_cache, dec._v_cache, 0, n)
 
 
 def test_prefill_then_decode_kernel(shape, exact06, weights_gpu):
@@ -86,8 +79,10 @@ def test_prefill_then_decode_kernel(shape, exact06, weights_gpu):
         tok, lg = dec.step_logits(toks[-1])
         toks.append(tok)
         lgs.append(lg.cpu())
-    ref = stream_rows(exact_oracle(exact06, shape, 2048), prompt, toks)
-    print(check_rows(Tally("prefill + decode"), ref, toks, torch.stack(lgs)))
+    orc = exact_oracle(exact06, shape, 2048)
+    ref = stream_rows(orc, dec._k_cache, dec._v_cache, prompt, toks)
+    print(check_rows(Tally("prefill + decode"), ref, toks, torch.stack(lgs), bar=LAYERS28))
+    check_kv_rows("prefill + decode", orc, dec._k_cache, dec._v_cache, 0, len(prompt) + 11)
 
 
 def test_generate_with_prefill_matches_oracle_stream(shape, exact06, weights_gpu):
@@ -97,9 +92,10 @@ def test_generate_with_prefill_matches_oracle_stream(shape, exact06, weights_gpu
 
     prompt = make_prompt(20, V, seed=6)
     for use_prefill in (True, False):
-        out = decoder(weights_gpu, use_prefill=use_prefill).generate(prompt, 24)
-        ref = stream_rows(exact_oracle(exact06, shape, 2048), prompt, out)
-        print(check_rows(Tally(f"generate use_prefill={use_prefill}"), ref, out))
+        dec = decoder(weights_gpu, use_prefill=use_prefill)
+        out = dec.generate(prompt, 24)
+        ref = stream_rows(exact_oracle(exact06, shape, 2048), dec._k_cache, dec._v_cache, prompt, out)
+        print(check_rows(Tally(f"generate use_prefill={use_prefill}"), ref, out, bar=LAYERS28))
 
 
 @pytest.fixture(scope="module")
@@ -128,8 +124,10 @@ def test_batch_decode_matches_oracle(shape, exact06, weights_gpu, batch_prompts)
             toks[b].append(nxt[b])
             lgs[b].append(logits[b].cpu())
     for b in range(4):
-        ref = stream_rows(exact_oracle(exact06, shape, 2048), prompts[b], toks[b])
-        print(check_rows(Tally(f"batched decode sequence {b}"), ref, toks[b], torch.stack(lgs[b])))
+        orc = exact_oracle(exact06, shape, 2048)
+        ref = stream_rows(orc, bd._k_cache[b], bd._v_cache[b], prompts[b], toks[b])
+        print(check_rows(Tally(f"batched decode sequence {b}"), ref, toks[b], torch.stack(lgs[b]), bar=LAYERS28))
+        check_kv_rows(f"batched decode sequence {b}", orc, bd._k_cache[b], bd._v_cache[b], 0, len(prompts[b]) + 10)
 
 
 def test_batch_generate_matches_oracle_streams(shape, exact06, weights_gpu, batch_prompts):
@@ -140,8 +138,8 @@ def test_batch_generate_matches_oracle_streams(shape, exact06, weights_gpu, batc
     bd = BatchDecoder(weights=weights_gpu, batch_size=4, max_seq_len=2048, verbose=False)
     out = bd.generate_ids(prompts, 11)
     for b in range(4):
-        ref = stream_rows(exact_oracle(exact06, shape, 2048), prompts[b], out[b])
-        check_rows(Tally(f"batched generate sequence {b}"), ref, out[b])
+        ref = stream_rows(exact_oracle(exact06, shape, 2048), bd._k_cache[b], bd._v_cache[b], prompts[b], out[b])
+        check_rows(Tally(f"batched generate sequence {b}"), ref, out[b], bar=LAYERS28)
     assert bd.positions == [len(p) + 10 for p in prompts]
 
 
@@ -155,7 +153,6 @@ def test_long_two_sequence_prefill_mfma_attention(shape, exact06, weights_gpu):
 
     layers, lens = 2, (600, 500)
     prompts = [make_prompt(n, shape.vocab, seed=70 + i) for i, n in enumerate(lens)]
-    refs = [exact_oracle(exact06, shape, 1024, num_layers=layers).forward(p) for p in prompts]
     bd = BatchDecoder(weights=weights_gpu, batch_size=2, max_seq_len=1024, num_layers=layers, verbose=False)
     toks = prompts[0] + prompts[1]
     seqs = [0] * lens[0] + [1] * lens[1]
@@ -171,9 +168,14 @@ def test_long_two_sequence_prefill_mfma_attention(shape, exact06, weights_gpu):
         runs.append((out.cpu().tolist(), logits.cpu()))
     got, lg = runs[0]
     assert runs[1][0] == got and torch.equal(runs[1][1], lg), "second forward differs"
+    refs = []
+    for sq in range(2):
+        orc = exact_oracle(exact06, shape, 1024, num_layers=layers)
+        refs.append(oracle_steps(orc, bd._k_cache[sq], bd._v_cache[sq], 0, prompts[sq]))
+        check_kv_rows(f"two-sequence prefill, sequence {sq}", orc, bd._k_cache[sq], bd._v_cache[sq], 0, lens[sq])
     t = Tally("two-sequence 1100-token prefill")
     for r, (sq, i) in enumerate(rows):
-        check_row(t, (sq, i), refs[sq][i], got[r], lg[r])
+        check_row(t, (sq, i), refs[sq][i], got[r], lg[r], bar=LITERAL)
     print(t)
 
 
@@ -192,12 +194,12 @@ def test_prefill_all_matches_per_sequence_prefill(shape, weights_gpu):
     assert one.positions == each.positions == [5, 17, 33]
     t = Tally("prefill_all vs per-sequence prefill")
     for b in range(3):
-        check_row(t, b, ref[b][1].cpu(), toks[b], lg[b])
+        check_row(t, b, ref[b][1].cpu(), toks[b], lg[b], bar=LAYERS28)
     feed = [ref[b][0] for b in range(3)]  # the same inputs to both
     s1, l1 = one.step_logits(feed)
     s2, l2 = each.step_logits(feed)
     for b in range(3):
-        check_row(t, ("step", b), l2[b].cpu(), s1[b], l1[b])
+        check_row(t, ("step", b), l2[b].cpu(), s1[b], l1[b], bar=LAYERS28)
 
 
 @pytest.mark.parametrize("n", [8, 40], ids=["8tok-split", "40tok-rowwise"])
@@ -209,13 +211,14 @@ def test_long_context_prefill(shape, exact06, weights_gpu, n):
     c0, layers = 2100, 2
     max_seq = c0 + 64
     k, v = make_kv_prefill(shape, c0, seed=2)
-    orc = exact_oracle(exact06, shape, max_seq, num_layers=layers, kv=(k, v), cache_len=c0)
     ids = make_prompt(n, shape.vocab, seed=7)
-    ref = orc.forward(ids)
     dec = decoder(with_rope(weights_gpu, max_seq, "cuda"), num_layers=layers, max_seq_len=max_seq)
     dec.load_kv(k.cuda(), v.cuda(), c0)
     toks, logits = _forward_rows(dec._forward, ids, c0, dec._k_cache, dec._v_cache)
-    print(check_rows(Tally(f"long-context prefill {n} rows after {c0}"), ref, toks, logits))
+    orc = exact_oracle(exact06, shape, max_seq, num_layers=layers)
+    ref = oracle_steps(orc, dec._k_cache, dec._v_cache, c0, ids)
+    print(check_rows(Tally(f"long-context prefill {n} rows after {c0}"), ref, toks, logits, bar=LITERAL))
+    check_kv_rows(f"long-context prefill {n}", orc, dec._k_cache, dec._v_cache, c0, n)
 
 
 def test_random_norm_weights_prefill(shape):
@@ -225,10 +228,12 @@ def test_random_norm_weights_prefill(shape):
 
     w = make_weights(shape, seed=5, norm_std=0.1, num_layers=3, max_seq_len=256)
     ids = make_prompt(36, shape.vocab, seed=8)
-    ref = ExactOracle(w, shape, num_layers=3, max_seq_len=256).forward(ids)
     dec = decoder(to_device(w, "cuda"), num_layers=3, max_seq_len=256)
     toks, logits = _forward_rows(dec._forward, ids, 0, dec._k_cache, dec._v_cache)
-    print(check_rows(Tally("random norm weights prefill"), ref, toks, logits))
+    orc = ExactOracle(w, shape, num_layers=3, max_seq_len=256)
+    ref = oracle_steps(orc, dec._k_cache, dec._v_cache, 0, ids)
+    print(check_rows(Tally("random norm weights prefill"), ref, toks, logits, bar=LITERAL))
+    check_kv_rows("random norm weights prefill", orc, dec._k_cache, dec._v_cache, 0, 36)
 
 
 def test_qwen3_1p7b_prefill_and_batch():
@@ -249,7 +254,8 @@ def test_qwen3_1p7b_prefill_and_batch():
     for b, p in enumerate(prompts):
         toks, logits = _forward_rows(bd._forward, p, 0, bd._k_cache, bd._v_cache, seq=b)
         bd._positions[b] = len(p)
-        check_rows(t, exact_oracle(ew, QWEN3_1_7B, 256).forward(p), toks, logits)
+        check_rows(t, oracle_steps(exact_oracle(ew, QWEN3_1_7B, 256), bd._k_cache[b], bd._v_cache[b], 0, p),
+                   toks, logits, bar=LITERAL)
         gen.append([toks[-1]])
     lgs = [[], []]
     for _ in range(2):
@@ -258,8 +264,10 @@ def test_qwen3_1p7b_prefill_and_batch():
             gen[b].append(nxt[b])
             lgs[b].append(logits[b].cpu())
     for b in range(2):
-        ref = stream_rows(exact_oracle(ew, QWEN3_1_7B, 256), prompts[b], gen[b])
-        check_rows(t, ref[1:], gen[b][1:], torch.stack(lgs[b]))
+        orc = exact_oracle(ew, QWEN3_1_7B, 256)
+        ref = stream_rows(orc, bd._k_cache[b], bd._v_cache[b], prompts[b], gen[b])
+        check_rows(t, ref[1:], gen[b][1:], torch.stack(lgs[b]), bar=LITERAL)
+        check_kv_rows(f"qwen3-1.7b 4 layers sequence {b}", orc, bd._k_cache[b], bd._v_cache[b], 0, len(prompts[b]) + 2)
     print(t)
 
 
@@ -315,8 +323,11 @@ def test_decode_batch_16_sequences(shape, exact06, weights_gpu):
             lgs[b].append(logits[b].cpu())
     t = Tally("16-sequence batched decode")
     for b in range(B):
-        ref = stream_rows(exact_oracle(exact06, shape, 128, num_layers=layers), prompts[b], gen[b])
-        check_rows(t, ref, gen[b], torch.stack(lgs[b]))
+        orc = exact_oracle(exact06, shape, 128, num_layers=layers)
+        ref = stream_rows(orc, bd._k_cache[b], bd._v_cache[b], prompts[b], gen[b])
+        check_rows(t, ref, gen[b], torch.stack(lgs[b]), bar=LITERAL)
+        check_kv_rows(f"16-sequence batched decode, sequence {b}", orc, bd._k_cache[b], bd._v_cache[b], 0,
+                      len(prompts[b]) + 3)
     print(t)
 
 
@@ -329,10 +340,9 @@ def test_decode_batch_long_context_general_path(shape, exact06, weights_gpu):
     layers, max_seq = 2, 5100
     bd = BatchDecoder(weights=with_rope(weights_gpu, max_seq, "cuda"), batch_size=2, max_seq_len=max_seq,
                       num_layers=layers, verbose=False)
-    orcs = []
-    for b, c0 in enumerate((5000, 4200)):
+    c0s = (5000, 4200)
+    for b, c0 in enumerate(c0s):
         k, v = make_kv_prefill(shape, c0, seed=2 + b)
-        orcs.append(exact_oracle(exact06, shape, max_seq, num_layers=layers, kv=(k, v), cache_len=c0))
         bd.load_kv(b, k.cuda(), v.cuda(), c0)
     feed, lgs = [[11], [22]], [[], []]
     for _ in range(3):
@@ -342,8 +352,10 @@ def test_decode_batch_long_context_general_path(shape, exact06, weights_gpu):
             lgs[b].append(logits[b].cpu())
     t = Tally("batched decode, general path, 5000/4200 context")
     for b in range(2):
-        ref = orcs[b].forward(feed[b][:-1])
-        check_rows(t, ref, feed[b][1:], torch.stack(lgs[b]))
+        orc = exact_oracle(exact06, shape, max_seq, num_layers=layers)
+        ref = oracle_steps(orc, bd._k_cache[b], bd._v_cache[b], c0s[b], feed[b][:-1])
+        check_rows(t, ref, feed[b][1:], torch.stack(lgs[b]), bar=LITERAL)
+        check_kv_rows(f"general path sequence {b}", orc, bd._k_cache[b], bd._v_cache[b], c0s[b], 3)
     print(t)
 
 
@@ -370,7 +382,7 @@ def test_decode_batch_equals_general_forward(weights_gpu):
     ar = torch.arange(4, dtype=torch.int32, device="cuda")
     bd._forward(toks, ar, pos, ar, out_b, lg_b, bd._k_cache, bd._v_cache, 64)
     t = Tally("fused decode step vs general forward")
-    check_rows(t, lg_b.cpu(), out_a.cpu().tolist(), lg_a.cpu())
+    check_rows(t, lg_b.cpu(), out_a.cpu().tolist(), lg_a.cpu(), bar=LAYERS28)
     # the appended K rows agree up to rounding: layer 0 within one ulp at |k| < 8, every layer's
     # rows with cosine >= 0.999
     d = (ka[:, 0].float() - bd._k_cache[:, 0].float()).abs().max().item()
@@ -391,7 +403,6 @@ def test_long_prefill_tiled_gemm(shape, exact06, weights_gpu, n):
     layers = 2
     ids = make_prompt(n, shape.vocab, seed=13)
     emit = list(range(0, n, 25)) + [n - 1]
-    ref = exact_oracle(exact06, shape, 512, num_layers=layers).forward(ids, emit=emit)
     dec = decoder(weights_gpu, num_layers=layers, max_seq_len=512)
     runs = []
     for _ in range(2):
@@ -403,4 +414,7 @@ def test_long_prefill_tiled_gemm(shape, exact06, weights_gpu, n):
         runs.append((out.cpu().tolist(), logits.cpu()))
     toks, lg = runs[0]
     assert runs[1][0] == toks and torch.equal(runs[1][1], lg), "second forward differs"
-    print(check_rows(Tally(f"tiled-GEMM prefill {n}"), ref, toks, lg, labels=emit))
+    orc = exact_oracle(exact06, shape, 512, num_layers=layers)
+    ref = oracle_steps(orc, dec._k_cache, dec._v_cache, 0, ids, emit=emit)
+    print(check_rows(Tally(f"tiled-GEMM prefill {n}"), ref, toks, lg, labels=emit, bar=LITERAL))
+    check_kv_rows(f"tiled-GEMM prefill {n}", orc, dec._k_cache, dec._v_cache, 0, n)

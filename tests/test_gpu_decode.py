@@ -1,10 +1,12 @@
 """GPU parity tests: the HIP decode kernel against the exact CPU oracle.
 
-The bar and the near-tie rule are in tests/parity.py: per step, logits cosine
->= 0.999 and max abs <= 0.1 against oracle/qwen3_exact.py (HF Qwen3's bf16
-rounding points, exact arithmetic between them), and the greedy token equal to
-the oracle's argmax given the same prefix except at a near-tie (gap below
-max(1e-2, one bf16 ulp)).  No bound depends on the CPU the test runs on.
+The bar and the near-tie rule are in tests/parity.py: per step, on the inputs
+the kernel's step had (its token and its cache), logits cosine >= 0.999 and
+max abs <= 0.1 against oracle/qwen3_exact.py (HF Qwen3's bf16 rounding points,
+exact arithmetic between them), the greedy token equal to the oracle's argmax
+except at a near-tie (gap below max(1e-2, one bf16 ulp)), and the K/V rows
+the step wrote equal to the oracle's up to rounding.  No bound depends on the
+CPU the test runs on.
 """
 
 import ctypes
@@ -13,16 +15,20 @@ import math
 import pytest
 import torch
 
-from parity import DEEP, LITERAL, Tally, check_rows, decoder, exact_oracle, kernel_stream, stream_rows, with_rope
+from parity import (DEEP, LAYERS28, LITERAL, Tally, check_kv_rows, check_rows, decoder, exact_oracle, kernel_stream,
+                    oracle_steps, stream_rows, with_rope)
 
 pytestmark = pytest.mark.gpu
 
 
 def test_decode_parity_qwen3_0p6b(shape, exact06, weights_gpu, prompt):
     """Config-0 shapes: 16-token prompt fed one step at a time, then 64 greedy steps; every row."""
-    feed, toks, lgs = kernel_stream(decoder(weights_gpu), prompt, 64)
-    ref = exact_oracle(exact06, shape, 2048).forward(feed)
-    print(check_rows(Tally("qwen3-0.6b 16+64"), ref, toks, lgs))
+    dec = decoder(weights_gpu)
+    feed, toks, lgs = kernel_stream(dec, prompt, 64)
+    orc = exact_oracle(exact06, shape, 2048)
+    ref = oracle_steps(orc, dec._k_cache, dec._v_cache, 0, feed)
+    print(check_rows(Tally("qwen3-0.6b 16+64"), ref, toks, lgs, bar=LAYERS28))
+    check_kv_rows("qwen3-0.6b 16+64", orc, dec._k_cache, dec._v_cache, 0, len(feed))
 
 
 def test_decode_parity_random_norm_weights(shape, prompt):
@@ -31,9 +37,12 @@ def test_decode_parity_random_norm_weights(shape, prompt):
     from qwen_megakernel.weights import make_weights, to_device
 
     w = make_weights(shape, seed=5, norm_std=0.1, num_layers=3, max_seq_len=256)
-    feed, toks, lgs = kernel_stream(decoder(to_device(w, "cuda"), num_layers=3, max_seq_len=256), prompt, 16)
-    ref = ExactOracle(w, shape, num_layers=3, max_seq_len=256).forward(feed)
-    print(check_rows(Tally("random norm weights, 3 layers"), ref, toks, lgs))
+    dec = decoder(to_device(w, "cuda"), num_layers=3, max_seq_len=256)
+    feed, toks, lgs = kernel_stream(dec, prompt, 16)
+    orc = ExactOracle(w, shape, num_layers=3, max_seq_len=256)
+    ref = oracle_steps(orc, dec._k_cache, dec._v_cache, 0, feed)
+    print(check_rows(Tally("random norm weights, 3 layers"), ref, toks, lgs, bar=LITERAL))
+    check_kv_rows("random norm weights", orc, dec._k_cache, dec._v_cache, 0, len(feed))
 
 
 def test_generate_nosync_matches_oracle_stream(shape, exact06, weights_gpu, prompt):
@@ -41,8 +50,8 @@ def test_generate_nosync_matches_oracle_stream(shape, exact06, weights_gpu, prom
     dec = decoder(weights_gpu)
     out = dec.generate(prompt, 64)
     assert len(out) == 64 and dec.position == len(prompt) - 1 + 64
-    ref = stream_rows(exact_oracle(exact06, shape, 2048), prompt, out)
-    print(check_rows(Tally("generate 64"), ref, out))
+    ref = stream_rows(exact_oracle(exact06, shape, 2048), dec._k_cache, dec._v_cache, prompt, out)
+    print(check_rows(Tally("generate 64"), ref, out, bar=LAYERS28))
 
 
 @pytest.fixture(scope="module")
@@ -60,19 +69,17 @@ def bench_workload(shape, exact06, weights_gpu):
     orc = exact_oracle(exact06, shape, 2048)
     seq = list(prompt) + out[:-1]
     n0 = len(prompt) - 1
-    ref = orc.forward(seq, emit=list(range(n0 - 1, len(seq))))  # row n0-1: the prefill's last row
+    # over the kernel's cache; row n0-1 is the prefill's last row
+    ref = oracle_steps(orc, dec._k_cache, dec._v_cache, 0, seq, emit=list(range(n0 - 1, len(seq))))
+    check_kv_rows("1024-step stream", orc, dec._k_cache, dec._v_cache, 0, len(seq))
     return prompt, out, ref
 
 
 def test_bench_workload_1024_step_stream(bench_workload):
-    """Every one of the 1024 generated tokens is the oracle's argmax given the same prefix, up to
-    near-ties: the free-running stream equals the oracle's except where a near-tie lets them part.
-    The first 256 steps (the north star's stream length) at the literal bar, the rest at the deep
-    bar (the reference's own fp32 stream departs from the exact centre at 2-ulp gaps there)."""
+    """Every one of the 1024 generated tokens is the oracle's argmax given the same prefix (tokens
+    and cache), up to near-ties: the stream is the greedy stream of its own history."""
     prompt, out, ref = bench_workload
-    t = Tally("1024-step stream")
-    check_rows(t, ref[1:257], out[:256], bar=LITERAL)
-    print(check_rows(t, ref[257:], out[256:], labels=list(range(256, 1024)), bar=DEEP))
+    print(check_rows(Tally("1024-step stream"), ref[1:], out, bar=LAYERS28))
 
 
 def test_bench_workload_256_steps_with_logits(shape, exact06, weights_gpu, bench_workload):
@@ -83,18 +90,17 @@ def test_bench_workload_256_steps_with_logits(shape, exact06, weights_gpu, bench
     dec = decoder(weights_gpu)
     tok, lg = dec.prefill(prompt[:-1], return_logits=True)
     t = Tally("prefill + 256 steps")
-    check_rows(t, ref[:1], [tok], lg[None].cpu(), labels=["prefill"])
+    check_rows(t, ref[:1], [tok], lg[None].cpu(), labels=["prefill"], bar=LAYERS28)
     feed, toks, lgs = [prompt[-1]], [], []
     for i in range(256):
         tk, l = dec.step_logits(feed[-1])
         toks.append(tk)
         lgs.append(l.cpu())
         feed.append(tk)
-    if toks == out[:256]:
-        rows = ref[1:257]
-    else:  # a different stream (it may part from generate's at a near-tie): its own oracle rows
-        rows = stream_rows(exact_oracle(exact06, shape, 2048), prompt, toks)
-    print(check_rows(t, rows, toks, torch.stack(lgs)))
+    assert toks == out[:256], "step-by-step launches and the device-fed loop gave different streams"
+    orc = exact_oracle(exact06, shape, 2048)
+    rows = stream_rows(orc, dec._k_cache, dec._v_cache, prompt, toks)
+    print(check_rows(t, rows, toks, torch.stack(lgs), bar=LAYERS28))
 
 
 @pytest.mark.parametrize(
@@ -106,8 +112,7 @@ def test_long_context_parity(shape, exact06, weights_gpu, c0, layers, steps):
     """Attention over an injected N(0,1) cache of c0 positions (split-K over the 32 workgroups of
     an XCD; above 2048 positions the long-context kernel runs, each wave streaming several K/V
     batches through the LDS ring; at 2100 wave 0 has a second, partial batch).  Every step
-    against the exact oracle, and the K/V rows the kernel appended.  4 layers: the literal bar;
-    28 layers: the deep bar (no fp32 implementation holds the literal one there, tests/parity.py)."""
+    against the exact oracle on the step's own inputs, and the K/V rows the kernel appended."""
     from qwen_megakernel.weights import make_kv_prefill
 
     max_seq = c0 + 64
@@ -115,18 +120,11 @@ def test_long_context_parity(shape, exact06, weights_gpu, c0, layers, steps):
     dec = decoder(with_rope(weights_gpu, max_seq, "cuda"), num_layers=layers, max_seq_len=max_seq)
     dec.load_kv(k.cuda(), v.cuda(), c0)
     feed, toks, lgs = kernel_stream(dec, [11, 22], steps)
-    orc = exact_oracle(exact06, shape, max_seq, num_layers=layers, kv=(k, v), cache_len=c0)
-    ref = orc.forward(feed)
+    assert torch.equal(dec._k_cache[:, :, :c0].cpu(), k[:layers, :, :c0])  # the injected rows are untouched
+    orc = exact_oracle(exact06, shape, max_seq, num_layers=layers)
+    ref = oracle_steps(orc, dec._k_cache, dec._v_cache, c0, feed)
     print(check_rows(Tally(f"context {c0} x {layers} layers"), ref, toks, lgs, bar=DEEP if layers == 28 else LITERAL))
-    # the appended K/V rows: layer 0 within one bf16 ulp of |v| <= 8 (0.0625), every layer's rows
-    # with cosine >= 0.999 (deeper layers carry the accumulated rounding differences)
-    pos = c0 + len(feed)
-    for name, got, exp in (("K", dec._k_cache, orc.k_cache), ("V", dec._v_cache, orc.v_cache)):
-        g, e = got[:, :, c0:pos].float().cpu(), exp[:, :, c0:pos].float()
-        d0 = (g[0] - e[0]).abs().max().item()
-        assert d0 <= 0.0625, f"layer-0 {name} rows differ by {d0}"
-        cos = torch.nn.functional.cosine_similarity(g.flatten().double(), e.flatten().double(), dim=0).item()
-        assert cos >= 0.999, f"{name} rows cosine {cos}"
+    check_kv_rows(f"context {c0} x {layers} layers", orc, dec._k_cache, dec._v_cache, c0, len(feed))
 
 
 def test_generate_across_long_context_boundary(shape, weights_gpu):

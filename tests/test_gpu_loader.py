@@ -15,7 +15,8 @@ import os
 import pytest
 import torch
 
-from parity import Tally, check_rows, decoder, exact_oracle, kernel_stream, stream_rows
+from parity import (LAYERS28, Tally, check_kv_rows, check_rows, decoder, exact_oracle, kernel_stream, oracle_steps,
+                    stream_rows)
 
 pytestmark = pytest.mark.gpu
 
@@ -73,20 +74,24 @@ def test_loaded_checkpoint_untied_head_decode_and_batched(monkeypatch, shape, ch
     prompt = make_prompt(12, shape.vocab, seed=3)
 
     # the decode megakernel: 12 prompt steps, then 16 greedy steps, every row
-    feed, toks, lgs = kernel_stream(decoder(w, max_seq_len=256), prompt, 16)
-    ref = exact_oracle(ew, shape, 256).forward(feed)
-    print(check_rows(Tally("loaded checkpoint, decode kernel"), ref, toks, lgs))
+    kd = decoder(w, max_seq_len=256)
+    feed, toks, lgs = kernel_stream(kd, prompt, 16)
+    orc = exact_oracle(ew, shape, 256)
+    ref = oracle_steps(orc, kd._k_cache, kd._v_cache, 0, feed)
+    print(check_rows(Tally("loaded checkpoint, decode kernel"), ref, toks, lgs, bar=LAYERS28))
+    check_kv_rows("loaded checkpoint", orc, kd._k_cache, kd._v_cache, 0, len(feed))
     # the check has teeth: an oracle with the embedding as its head is far from the kernel
     wrong_head = exact_oracle(ew, shape, 256)
     wrong_head.lm_head64 = w_ref["embed_weight"].double()
-    wrong = wrong_head.forward(feed[:4])
+    wrong = oracle_steps(wrong_head, kd._k_cache, kd._v_cache, 0, feed[:4])
     assert (wrong - lgs[:4]).abs().max().item() > 0.3
 
     # the batched path: every prefill row, then two batched steps of two sequences
     dec = decoder(w, max_seq_len=256)
     tok0, lg0 = dec.prefill(prompt, return_logits=True)
     t = Tally("loaded checkpoint, batched path")
-    check_rows(t, ref[len(prompt) - 1: len(prompt)], [tok0], lg0[None].cpu())
+    pre = oracle_steps(exact_oracle(ew, shape, 256), dec._k_cache, dec._v_cache, 0, prompt, emit=[len(prompt) - 1])
+    check_rows(t, pre, [tok0], lg0[None].cpu(), bar=LAYERS28)
     bd = BatchDecoder(weights=w, batch_size=2, max_seq_len=256, verbose=False)
     prompts = [prompt, make_prompt(7, shape.vocab, seed=4)]
     first = bd.prefill_all(prompts)
@@ -97,6 +102,6 @@ def test_loaded_checkpoint_untied_head_decode_and_batched(monkeypatch, shape, ch
             gen[b].append(nxt[b])
             lgs2[b].append(logits[b].cpu())
     for b in range(2):
-        rows = stream_rows(exact_oracle(ew, shape, 256), prompts[b], gen[b])
-        check_rows(t, rows[1:], gen[b][1:], torch.stack(lgs2[b]))
+        rows = stream_rows(exact_oracle(ew, shape, 256), bd._k_cache[b], bd._v_cache[b], prompts[b], gen[b])
+        check_rows(t, rows[1:], gen[b][1:], torch.stack(lgs2[b]), bar=LAYERS28)
     print(t)

@@ -233,19 +233,32 @@ def test_exact_oracle_near_fp32_oracle():
 
 
 @pytest.mark.slow
-def test_reference_path_itself_misses_the_literal_bar_on_qwen3_1p7b():
+def test_reference_path_itself_misses_the_literal_bar_at_long_context(w06):
     """The reference's PyTorch bf16 path (HF semantics, fp32 accumulation: oracle/qwen3_ref.py)
-    against the exact centre on Qwen3-1.7B, 28 layers, the seeded 8-token prompt and 8 greedy
-    steps: it is more than 0.1 away at some step (0.125 on the CPU that wrote this), so the
-    literal 0.1 bar cannot hold there for any fp32 implementation, and within the deep bar's 0.15
-    (tests/parity.py)."""
-    from qwen_megakernel.shapes import QWEN3_1_7B
+    against the exact centre on identical inputs: Qwen3-0.6B, 28 layers, a seeded N(0, 1) cache
+    of 1500 positions, 12 steps, each run over the exact oracle's own cache.  It is more than
+    0.1 away at some step (0.110 on the CPU that wrote this; Qwen3-1.7B after a 24-token prompt
+    reaches 0.117 the same way), so the literal 0.1 bar cannot hold there for an fp32
+    implementation, and within 0.2 (the GPU tests' bar for these workloads, tests/parity.py)."""
+    from qwen_megakernel.weights import rope_tables
 
-    w = make_weights(QWEN3_1_7B, seed=0, max_seq_len=64)
-    res = greedy_stream(OracleDecoder(w, QWEN3_1_7B, max_seq_len=64), make_prompt(8, QWEN3_1_7B.vocab, seed=1), 8,
-                        record_logits=True)
-    exact = X.ExactOracle(w, QWEN3_1_7B, max_seq_len=64).forward(res["inputs"])
-    d = (res["logits"] - exact).abs().max(-1).values
-    print("HF-semantics fp32 vs exact, per step:", [round(x, 4) for x in d.tolist()])
-    assert d.max().item() > 0.1
-    assert d.max().item() <= 0.15
+    c0 = 1500
+    cos, sin = rope_tables(c0 + 16, 128, 1e6)
+    w = dict(w06)
+    w["cos_table"], w["sin_table"] = cos, sin
+    k, v = make_kv_prefill(QWEN3_0_6B, c0, seed=2)
+    toks = [11, 22, 5, 6, 7, 8, 9, 10, 12, 13, 14, 15]
+    ex = X.ExactOracle(w, QWEN3_0_6B, max_seq_len=c0 + 16)
+    ex.load_kv(k, v, c0)
+    lx = ex.forward(toks)
+    hf = OracleDecoder(w, QWEN3_0_6B, max_seq_len=c0 + 16)
+    d = []
+    for i, t in enumerate(toks):
+        p = c0 + i
+        hf.k_cache[:, :, :p] = ex.k_cache[:, :, :p]
+        hf.v_cache[:, :, :p] = ex.v_cache[:, :, :p]
+        hf.position = p
+        d.append((hf.step_logits(t) - lx[i]).abs().max().item())
+    print("HF-semantics fp32 vs exact on identical inputs, per step:", [round(x, 4) for x in d])
+    assert max(d) > 0.1
+    assert max(d) <= 0.2
