@@ -65,6 +65,8 @@ enum {
   QMK_ERR_DEVICE = 3,     /* device unsuitable (needs 256 CUs, gfx950) */
   QMK_ERR_HIP = 4,        /* a HIP runtime call failed */
   QMK_ERR_POISONED = 5,   /* a previous launch on this stream failed; call qmk_reset */
+  QMK_ERR_INIT = 6,       /* qmk_init() was not called on this device */
+  QMK_ERR_SIZE = 7,       /* input beyond the allocation-free entry point's limits */
 };
 
 /* Device error bits (qmk_device_error). */
@@ -141,6 +143,36 @@ enum {
 /* One decode step of `model` (and the fp32 copy of its bf16 logits when
  * logits_out is not NULL).  Returns a status code.  Asynchronous. */
 int qmk_decode_model(
+    int model, int input_token_id, int *output_token_id, float *logits_out,
+    const void *embed_weight, const LDGLayerWeights *layer_weights,
+    const void *final_norm_weight, const void *lm_head_weight,
+    const void *cos_table, const void *sin_table, void *k_cache, void *v_cache,
+    void *hidden_buffer, void *g_normalized, int num_layers, int position,
+    int max_seq_len, float attn_scale, hipStream_t stream);
+
+/* The library's set-up call for the current device: checks it (gfx950, 256
+ * CUs, one decode workgroup per CU) and takes the device address of its copy
+ * of the allocation-free entry point's scratch.  Call once per device, with
+ * that device current, before qmk_decode_model_noalloc (for example before
+ * capturing a graph).  Allocates no device memory.  Returns a status code.
+ * No counterpart in the reference. */
+int qmk_init(void);
+
+/* qmk_decode_model without any allocation: no hipMalloc, hipFree or other
+ * allocating call, on any call.  For callers that cannot allocate: code under
+ * HIP graph capture, tight serving loops, harnesses that forbid it.  No
+ * counterpart in the reference.
+ *
+ * The kernel's device state and exchange words live in a file-scope device
+ * array of 979,200 bytes per GPU (kept until the process ends) instead of the
+ * per-stream buffers the other entry points allocate on first use.  Every call
+ * on a GPU shares that array: calls are ordered across streams like every
+ * decode launch, but calls replayed from captured graphs on several streams at
+ * once race and must not overlap.  Limits: num_layers <= 28 and max_seq_len <=
+ * 65536 (QMK_ERR_SIZE beyond them); qmk_init() first (QMK_ERR_INIT).  A call
+ * that fails on the device leaves -1 in output_token_id; the next call starts
+ * clean.  Returns a status code.  Asynchronous. */
+int qmk_decode_model_noalloc(
     int model, int input_token_id, int *output_token_id, float *logits_out,
     const void *embed_weight, const LDGLayerWeights *layer_weights,
     const void *final_norm_weight, const void *lm_head_weight,

@@ -36,6 +36,15 @@ constexpr uint32_t kXWords = Dims<Qwen3_0_6B>::X_WORDS > Dims<Qwen3_1_7B>::X_WOR
 
 thread_local int t_status = QMK_OK;
 
+// Scratch of the allocation-free entry point (qmk_decode_model_noalloc): one
+// DecodeState header followed by one exchange area sized for the larger of the
+// two models' layouts, 979,200 bytes.  Each GPU holds its own copy until the
+// process ends.  Host code never uses this name as an address: qmk_init()
+// takes the device address of the current device's copy with
+// hipGetSymbolAddress and keeps it in that device's DevInfo.
+constexpr size_t kScratchBytes = sizeof(DecodeState) + (size_t)kXWords * 4;
+static __device__ __align__(256) uint32_t scratch[kScratchBytes / 4];
+
 // generate: persistent launches recorded once into a HIP graph and replayed
 // in groups of this many steps (the rest launched directly)
 constexpr int kGraphSteps = 32;
@@ -80,6 +89,7 @@ struct DevInfo {
   hipStream_t order_stream = nullptr;  // the stream of the last decode launch group
   bool order_valid = false;
   bool order_multi = false;            // a second stream has launched on this device
+  uint32_t* scratch = nullptr;         // this device's copy of `scratch` (set by qmk_init)
 };
 
 std::mutex g_mu;
@@ -242,6 +252,29 @@ class DeviceOrder {
 __global__ void clear_exchange_kernel(DecodeState* st, uint32_t* x, uint32_t n) {
   for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) x[i] = 0u;
   if (blockIdx.x == 0 && threadIdx.x == 0) st->epoch = 0u;
+}
+
+// Start of every qmk_decode_model_noalloc call, one workgroup: on the first
+// call of a process (zeroed scratch) or when the model differs from the last
+// call's, zero the exchange words and restart the tags; after a failed call
+// (error bits set), move the tags past every tag that call could have written.
+// Then clear the error bits, so one failure does not block later calls.
+__global__ void noalloc_prepare_kernel(DecodeState* st, uint32_t* x, uint32_t n, uint32_t model_tag) {
+  __shared__ int mode;
+  if (threadIdx.x == 0) mode = st->reserved[0] != model_tag ? 2 : (st->err != 0 ? 1 : 0);
+  __syncthreads();
+  if (mode == 2)
+    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) x[i] = 0u;
+  if (threadIdx.x == 0) {
+    if (mode == 2) {
+      st->epoch = 0u;
+      st->reserved[0] = model_tag;
+    } else if (mode == 1) {
+      st->epoch += 2u * 256u;  // a launch advances the tags by at most 9 * 28 + 1
+    }
+    st->err = 0u;
+    st->done = 0u;
+  }
 }
 
 int prepare_model(Ctx* ctx, int model, hipStream_t stream) {
@@ -642,6 +675,64 @@ int qmk_decode_logits(int input_token_id, int* output_token_id, float* logits_ou
   return decode_impl(c, input_token_id, position, output_token_id, logits_out, stream, false);
 }
 
+int qmk_init(void) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess) return fail(QMK_ERR_HIP);
+  std::lock_guard<std::mutex> lk(g_mu);
+  DevInfo* di = nullptr;
+  const int s = check_device(dev, &di);
+  if (s != QMK_OK) return fail(s);
+  if (!di->scratch) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return fail(QMK_ERR_HIP);
+    di->scratch = static_cast<uint32_t*>(p);
+  }
+  return fail(QMK_OK);
+}
+
+int qmk_decode_model_noalloc(int model, int input_token_id, int* output_token_id, float* logits_out,
+                             const void* embed_weight, const LDGLayerWeights* layer_weights,
+                             const void* final_norm_weight, const void* lm_head_weight, const void* cos_table,
+                             const void* sin_table, void* k_cache, void* v_cache, void* hidden_buffer,
+                             void* g_normalized, int num_layers, int position, int max_seq_len, float attn_scale,
+                             hipStream_t stream) {
+  // the scratch holds one exchange area for at most kMaxLayers layers of either model and caches of
+  // at most kMaxSeqLen positions (the kernel's own limits)
+  if (num_layers > kMaxLayers || max_seq_len > kMaxSeqLen) return fail(QMK_ERR_SIZE);
+  Common c{model, embed_weight, layer_weights, final_norm_weight, lm_head_weight, cos_table, sin_table, k_cache, v_cache,
+           hidden_buffer, g_normalized, num_layers, max_seq_len, attn_scale};
+  int s = validate(c);
+  if (s != QMK_OK) return fail(s);
+  if (position < 0 || position >= c.max_seq_len) return fail(QMK_ERR_POSITION);
+  if (input_token_id < 0 || input_token_id >= Dm::V) return fail(QMK_ERR_ARG);
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess) return fail(QMK_ERR_HIP);
+  DevInfo* di = nullptr;
+  {
+    std::lock_guard<std::mutex> lk(g_mu);
+    auto it = g_dev.find(dev);
+    if (it != g_dev.end() && it->second.ok && it->second.scratch) di = &it->second;
+  }
+  if (!di) return fail(QMK_ERR_INIT);
+  Ctx view;  // the kernel arguments' view of the scratch; nothing is allocated
+  view.st = reinterpret_cast<DecodeState*>(di->scratch);
+  view.x = di->scratch + sizeof(DecodeState) / 4;
+  view.timeout = di->ticks_per_s;
+  view.xcd_local = di->xcd_local;
+  KArgs a = make_args(c, &view);
+  a.out_token = output_token_id;
+  a.logits = logits_out;
+  a.position = position;
+  a.token = input_token_id;
+  DeviceOrder order(di, stream);
+  if (!order.ok()) return fail(QMK_ERR_HIP);
+  hipLaunchKernelGGL(noalloc_prepare_kernel, dim3(1), dim3(256), 0, stream, view.st, view.x, kXWords,
+                     (uint32_t)model + 1u);
+  s = hipGetLastError() == hipSuccess ? launch(a, model, position + 1 > kLongContext, stream) : QMK_ERR_HIP;
+  const int so = order.finish();
+  return fail(s != QMK_OK ? s : so);
+}
+
 int qmk_last_status(void) { return t_status; }
 
 const char* qmk_status_string(int status) {
@@ -652,6 +743,9 @@ const char* qmk_status_string(int status) {
     case QMK_ERR_DEVICE: return "device unsuitable: needs a gfx950 GPU with 256 CUs";
     case QMK_ERR_HIP: return "HIP runtime call failed";
     case QMK_ERR_POISONED: return "an earlier launch on this stream failed on the device; call qmk_reset";
+    case QMK_ERR_INIT: return "qmk_init() has not been called on this device";
+    case QMK_ERR_SIZE:
+      return "input beyond the allocation-free entry point's limits (num_layers <= 28, max_seq_len <= 65536)";
     default: return "unknown status";
   }
 }
