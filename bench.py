@@ -470,7 +470,8 @@ def main():
         dec._position = last
 
         stamps = trace.capture(lambda: dec.step(int(toks[-1])), QWEN3_0_6B.num_layers)
-        summ = trace.summarize(stamps, QWEN3_0_6B.num_layers)
+        # positions below 2,048 run the split-K form of the Qwen3-0.6B kernel
+        summ = trace.summarize(stamps, QWEN3_0_6B.num_layers, split=last + 1 <= 2048)
         summ["context"] = last + 1
         result["phase_trace"] = summ
         log(f"phase trace at context {last + 1}:\n" + trace.format_table(summ))

@@ -22,8 +22,9 @@
 //
 //   k  exchange   producers -> consumers                scope
 //   0  qkv        32 WGs of XCD x -> same 32 WGs         XCD-local
-//   1  ml         softmax (max, sum) per WG and head     XCD-local
-//   2  acc        P@V partial sums per WG and head       XCD-local
+//   1  ml         softmax (max, sum) per WG and head     XCD-local (two-pass form only)
+//   2  acc        P@V partial sums per WG and head       XCD-local (split form: with the
+//                 WG's (max, sum), in the ml slots)
 //   3  attn       attention output of heads 2x, 2x+1     XCD-local
 //   4  o          o_proj partials, rows 32r..32r+31      across XCDs (8 -> 8)
 //   5  h2         h' = h + o_proj(attn)                  XCD-local
@@ -36,8 +37,12 @@
 // RoPE products and sum, attention scores and their scaling, softmax
 // probabilities, attention output, residual adds, SiLU and its product,
 // logits); dot products accumulate in fp32.  Attention is split over the 32
-// workgroups of an XCD in two passes so that probabilities are normalised
-// with the global max and sum before they are rounded, as HF does.
+// workgroups of an XCD.  The Qwen3-0.6B kernel below 2,048 positions runs it
+// as a split-K softmax (each wave's terms exp(s - m) against its own maximum,
+// in fp32, rescaled to the global maximum in the combine, as the reference's
+// kernel does); the other forms take two passes so that the probabilities
+// are normalised with the global max and sum and rounded to bf16 before P@V,
+// as HF does.
 //
 // Each workgroup has 9 waves.  Wave 0 ("control") moves activations: it polls
 // exchanges, applies norms / RoPE / residuals / SiLU, publishes results and
@@ -574,7 +579,9 @@ __device__ __forceinline__ uint32_t orderable16(uint32_t h) { return (h & 0x8000
     if (s.abort_flag) return; \
   } while (0)
 
-template <class M>
+// SPLIT: the compute waves run attention as a split-K softmax between barriers c and f and hand
+// over per-wave (max, sum, unnormalised P@V); there is no (max, sum) exchange and no barriers d, e.
+template <class M, bool SPLIT>
 __device__ __forceinline__ void control_path(const KArgs& a, Smem<M>& s, const Step& p, int b, int lane) {
   using Dm = Dims<M>;
   const int xcd = b & (kGroups - 1), r = b >> 3;
@@ -646,49 +653,54 @@ __device__ __forceinline__ void control_path(const KArgs& a, Smem<M>& s, const S
     }
     stamp(tp + 3);
     QMK_SYNC();  // c
-    QMK_SYNC();  // d
-    stamp(tp + 4);
-    // ------------------------------------------------------------ d..e  softmax max and sum
-    {
-      const uint32_t t = tag_of(L, 1);
-      // lanes 0..GQ-1: merge the eight wave (max, sum) pairs of head h = lane
-      float mx = -INFINITY, sm = 0.f;
-      if (lane < Dm::GQ) {
-#pragma unroll
-        for (int c = 0; c < kComputeWaves; c++) mx = fmaxf(mx, s.wml[c][lane][0]);
-#pragma unroll
-        for (int c = 0; c < kComputeWaves; c++) {
-          const float mc = s.wml[c][lane][0];
-          sm += mc == -INFINITY ? 0.f : s.wml[c][lane][1] * exp_acc(mc - mx);
-        }
-      }
-      if (lane < Dm::GQ) ctl.put_f32x2(true, Dm::X_ML + (xcd * kGroupSize + r) * Dm::GQ * 4 + 4 * lane, mx, sm, t);
-      // gather every active workgroup's pairs: chunk i = (rank i / GQ, head i % GQ)
-      float pm[2] = {-INFINITY, -INFINITY}, pl[2] = {0.f, 0.f};
-      const bool ok = ctl.template gather<kGroupSize * Dm::GQ>(
-          t, [&](int i) { return Dm::X_ML + (uint32_t)((xcd * kGroupSize + i / Dm::GQ) * Dm::GQ * 4 + 4 * (i % Dm::GQ)); },
-          [&](int i, u32x4 v) {
-            pm[i / 64] = f32_from_words(v.x, v.y);
-            pl[i / 64] = f32_from_words(v.z, v.w);
-          });
-      if (ok) {
-        // lane l holds chunks l and l+64 (64 chunks: only the first): head = l % GQ
-        static_assert(kGroupSize * Dm::GQ <= 64, "one chunk per lane");
-        const int h = lane % Dm::GQ;
-        const bool act = (lane / Dm::GQ) < p.n_act;
-        float m0 = act ? pm[0] : -INFINITY;
-        float gm = m0;
-        for (int o = Dm::GQ; o < 64; o <<= 1) gm = fmaxf(gm, __shfl_xor(gm, o));
-        float lsum = (act && m0 != -INFINITY) ? pl[0] * exp_acc(m0 - gm) : 0.f;
-        for (int o = Dm::GQ; o < 64; o <<= 1) lsum += __shfl_xor(lsum, o);
+    if constexpr (SPLIT) {
+      stamp(tp + 4);
+      stamp(tp + 5);
+    } else {
+      QMK_SYNC();  // d
+      stamp(tp + 4);
+      // ------------------------------------------------------------ d..e  softmax max and sum
+      {
+        const uint32_t t = tag_of(L, 1);
+        // lanes 0..GQ-1: merge the eight wave (max, sum) pairs of head h = lane
+        float mx = -INFINITY, sm = 0.f;
         if (lane < Dm::GQ) {
-          s.ml[h][0] = gm;
-          s.ml[h][1] = lsum;
+  #pragma unroll
+          for (int c = 0; c < kComputeWaves; c++) mx = fmaxf(mx, s.wml[c][lane][0]);
+  #pragma unroll
+          for (int c = 0; c < kComputeWaves; c++) {
+            const float mc = s.wml[c][lane][0];
+            sm += mc == -INFINITY ? 0.f : s.wml[c][lane][1] * exp_acc(mc - mx);
+          }
+        }
+        if (lane < Dm::GQ) ctl.put_f32x2(true, Dm::X_ML + (xcd * kGroupSize + r) * Dm::GQ * 4 + 4 * lane, mx, sm, t);
+        // gather every active workgroup's pairs: chunk i = (rank i / GQ, head i % GQ)
+        float pm[2] = {-INFINITY, -INFINITY}, pl[2] = {0.f, 0.f};
+        const bool ok = ctl.template gather<kGroupSize * Dm::GQ>(
+            t, [&](int i) { return Dm::X_ML + (uint32_t)((xcd * kGroupSize + i / Dm::GQ) * Dm::GQ * 4 + 4 * (i % Dm::GQ)); },
+            [&](int i, u32x4 v) {
+              pm[i / 64] = f32_from_words(v.x, v.y);
+              pl[i / 64] = f32_from_words(v.z, v.w);
+            });
+        if (ok) {
+          // lane l holds chunks l and l+64 (64 chunks: only the first): head = l % GQ
+          static_assert(kGroupSize * Dm::GQ <= 64, "one chunk per lane");
+          const int h = lane % Dm::GQ;
+          const bool act = (lane / Dm::GQ) < p.n_act;
+          float m0 = act ? pm[0] : -INFINITY;
+          float gm = m0;
+          for (int o = Dm::GQ; o < 64; o <<= 1) gm = fmaxf(gm, __shfl_xor(gm, o));
+          float lsum = (act && m0 != -INFINITY) ? pl[0] * exp_acc(m0 - gm) : 0.f;
+          for (int o = Dm::GQ; o < 64; o <<= 1) lsum += __shfl_xor(lsum, o);
+          if (lane < Dm::GQ) {
+            s.ml[h][0] = gm;
+            s.ml[h][1] = lsum;
+          }
         }
       }
+      stamp(tp + 5);
+      QMK_SYNC();  // e
     }
-    stamp(tp + 5);
-    QMK_SYNC();  // e
     QMK_SYNC();  // f
     stamp(tp + 6);
     // ------------------------------------------------------------ f..g  P@V partials, combine, attn
@@ -698,10 +710,27 @@ __device__ __forceinline__ void control_path(const KArgs& a, Smem<M>& s, const S
 #pragma unroll
       for (int h = 0; h < Dm::GQ; h++) {
         float a0 = 0.f, a1 = 0.f;
+        if constexpr (SPLIT) {
+          // wave c's terms are relative to its own maximum: rescale to the workgroup's, and
+          // publish the workgroup's (max, sum) of head h beside the partial, under the same tag
+          float mh = -INFINITY, lh = 0.f;
 #pragma unroll
-        for (int c = 0; c < kComputeWaves; c++) {
-          a0 += s.wacc[c][h][2 * lane];
-          a1 += s.wacc[c][h][2 * lane + 1];
+          for (int c = 0; c < kComputeWaves; c++) mh = fmaxf(mh, s.wml[c][h][0]);
+#pragma unroll
+          for (int c = 0; c < kComputeWaves; c++) {
+            const float mc = s.wml[c][h][0];
+            const float f = mc == -INFINITY ? 0.f : exp_acc(mc - mh);
+            lh += f * s.wml[c][h][1];
+            a0 += f * s.wacc[c][h][2 * lane];
+            a1 += f * s.wacc[c][h][2 * lane + 1];
+          }
+          if (lane == 0) ctl.put_f32x2(true, Dm::X_ML + (xcd * kGroupSize + r) * Dm::GQ * 4 + 4 * h, mh, lh, t);
+        } else {
+#pragma unroll
+          for (int c = 0; c < kComputeWaves; c++) {
+            a0 += s.wacc[c][h][2 * lane];
+            a1 += s.wacc[c][h][2 * lane + 1];
+          }
         }
         ctl.put_f32x2(true, Dm::X_ACC + (uint32_t)((xcd * kGroupSize + r) * Dm::GQ * Dm::D * 2 + h * Dm::D * 2 + 4 * lane),
                       a0, a1, t);
@@ -710,20 +739,46 @@ __device__ __forceinline__ void control_path(const KArgs& a, Smem<M>& s, const S
       // dims 8kb+2(i%4), +1); lane l receives chunks l and l+64 (ranks l/4 and l/4+16).
       const int hh = r / (Dm::D / 8), kb = r % (Dm::D / 8);
       static_assert(kGroupSize * 4 == 128, "two chunks per lane");
+      // SPLIT: chunks 128 + j carry rank j's (max, sum) of head hh, lane j receives them
+      constexpr int NCHUNK = kGroupSize * 4 + (SPLIT ? kGroupSize : 0);
       float v0[2] = {0.f, 0.f}, v1[2] = {0.f, 0.f};
-      const bool ok2 = ctl.template gather<kGroupSize * 4>(
+      [[maybe_unused]] float mr = -INFINITY, lr = 0.f;
+      const bool ok2 = ctl.template gather<NCHUNK>(
           t,
           [&](int i) {
+            if (SPLIT && i >= kGroupSize * 4)
+              return Dm::X_ML + (uint32_t)((xcd * kGroupSize + (i - kGroupSize * 4)) * Dm::GQ * 4 + 4 * hh);
             return Dm::X_ACC + (uint32_t)((xcd * kGroupSize + i / 4) * Dm::GQ * Dm::D * 2 + hh * Dm::D * 2 +
                                           (8 * kb + 2 * (i % 4)) * 2);
           },
           [&](int i, u32x4 v) {
-            const bool act = (i / 4) < p.n_act;
-            v0[i / 64] = act ? f32_from_words(v.x, v.y) : 0.f;
-            v1[i / 64] = act ? f32_from_words(v.z, v.w) : 0.f;
+            if (SPLIT && i >= kGroupSize * 4) {
+              const bool act = (i - kGroupSize * 4) < p.n_act;
+              mr = act ? f32_from_words(v.x, v.y) : -INFINITY;
+              lr = act ? f32_from_words(v.z, v.w) : 0.f;
+            } else {
+              const bool act = (i / 4) < p.n_act;
+              v0[(i / 64) & 1] = act ? f32_from_words(v.x, v.y) : 0.f;
+              v1[(i / 64) & 1] = act ? f32_from_words(v.z, v.w) : 0.f;
+            }
           });
       if (ok2) {
-        float s0 = v0[0] + v0[1], s1 = v1[0] + v1[1];  // ranks l/4 and l/4 + 16
+        float s0, s1;  // ranks l/4 and l/4 + 16
+        [[maybe_unused]] float gsum = 1.f;  // SPLIT: the softmax denominator
+        if constexpr (SPLIT) {
+          // rescale rank j's partial by exp(m_j - M) (M the maximum over the active ranks) and
+          // normalise by the rescaled sum of the sums
+          const float gm = wave_max(mr);
+          const float f = mr == -INFINITY ? 0.f : exp_acc(mr - gm);
+          const float gl = wave_sum(f * lr);
+          const float fa = __shfl(f, lane >> 2), fb = __shfl(f, (lane >> 2) + 16);
+          s0 = v0[0] * fa + v0[1] * fb;
+          s1 = v1[0] * fa + v1[1] * fb;
+          gsum = gl;
+        } else {
+          s0 = v0[0] + v0[1];
+          s1 = v1[0] + v1[1];
+        }
 #pragma unroll
         for (int o = 4; o < 64; o <<= 1) {
           s0 += __shfl_xor(s0, o);
@@ -731,8 +786,14 @@ __device__ __forceinline__ void control_path(const KArgs& a, Smem<M>& s, const S
         }
         // lanes with equal l%4 now hold the sum over all ranks of dims 8kb+2(l%4), +1;
         // lanes 0 and 1 publish dims 8kb..8kb+3 and 8kb+4..8kb+7
-        const float d2 = __shfl(s0, (lane & 1) * 2 + 0), d3 = __shfl(s1, (lane & 1) * 2 + 0);
-        const float d4 = __shfl(s0, (lane & 1) * 2 + 1), d5 = __shfl(s1, (lane & 1) * 2 + 1);
+        float d2 = __shfl(s0, (lane & 1) * 2 + 0), d3 = __shfl(s1, (lane & 1) * 2 + 0);
+        float d4 = __shfl(s0, (lane & 1) * 2 + 1), d5 = __shfl(s1, (lane & 1) * 2 + 1);
+        if constexpr (SPLIT) {
+          d2 = __fdiv_rn(d2, gsum);
+          d3 = __fdiv_rn(d3, gsum);
+          d4 = __fdiv_rn(d4, gsum);
+          d5 = __fdiv_rn(d5, gsum);
+        }
         if (lane < 2)
           ctl.put_bf16x4(true, Dm::X_ATTN + (uint32_t)(xcd * Dm::OC + hh * Dm::D + 8 * kb + 4 * lane), d2, d3, d4, d5,
                          tag_of(L, 3));
@@ -902,21 +963,21 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
       load_seg_p<Dm::LD>(wd + op * Dm::LD, wd_base + (size_t)rs_row(op) * Dm::I + Dm::MS * xcd, t16);
   };
 
-  // EARLY (short-context form, weights one layer ahead): the weight slices are
-  // requested in the three windows in which the control wave does not poll,
-  // so fewer exchange polls queue behind them (a CU returns vector-memory data
-  // in order): one of the next layer's two QKV rows at barrier c (scores),
-  // this layer's gate/up slice and the other QKV row at e (P@V), the next
-  // layer's o_proj slice and this layer's down slice at i (gate/up).  The K/V
-  // waits in the first two windows leave those newer loads outstanding.
-  // Requested right after each compute phase instead, i.e. just before an
-  // exchange: 1,899 against 1,974 tok/s.
+  // EARLY (short-context form with every slice in its own registers): attention
+  // is a split-K softmax in one compute window, c..f (SPLIT; the control wave
+  // combines in f..g), and the weight slices are requested in the two windows
+  // in which the control wave does not poll, so that no exchange poll queues
+  // behind them (a CU returns vector-memory data in order): this layer's
+  // gate/up and o_proj slices at barrier c, behind the V rows; this layer's
+  // down slice and the next layer's QKV rows at i (gate/up).  Measured against
+  // the other placements of the same split kernel at context 1024 (direct
+  // launches): 1,996-2,005 tok/s; QKV row 0 and gate/up at c, o_proj, down
+  // and QKV row 1 at i 1,974-1,983; gate/up and both QKV rows at c 1,955;
+  // the V rows requested before barrier c with the K rows 1,943.
   constexpr bool EARLY = !ST && !LONG;
-  constexpr int NB_C = EARLY ? Dm::LH : 0;  // loads issued at barrier c
-  constexpr int NB_E = EARLY ? Dm::GU_W * Dm::LH + Dm::LH : 0;  // loads issued at barrier e
-  static_assert(NB_C <= 12 && NB_E <= 12, "wait_vmcnt range");
+  constexpr bool SPLIT = EARLY;
+  static_assert(!EARLY || kLongContext / kGroupSize <= 32 * kKvU, "EARLY: at most one K/V batch per wave");
   prefetch_qkv(0);
-  if (EARLY) prefetch_o(0);
   if (!ST && !EARLY) {
     prefetch_o(0);
     prefetch_gu(0);
@@ -933,11 +994,15 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
   for (int L = 0; L < p.nl; L++) {
     const uint16_t* kc = a.k_cache + L * kv_layer_stride + (size_t)xcd * a.max_seq_len * Dm::D;
     const uint16_t* vc = a.v_cache + L * kv_layer_stride + (size_t)xcd * a.max_seq_len * Dm::D;
+    // the layer whose slices are requested one layer ahead; the last layer requests its own again
+    // (L2-warm, unused), so every path issues the same loads and the compiler's counted waits
+    // hold for all layers
+    [[maybe_unused]] const int L_next = L + 1 < p.nl ? L + 1 : L;
     // K/V batches go straight from HBM into this wave's slots of an LDS ring
     // (kKvStages batches in flight) and are read back with the same lane
     // layout: lane (slot, t16) holds dims 8*t16..+7 of position base + 32u + slot.
     const int nb = base0_of(c) < p.p_end ? (p.p_end - base0_of(c) + 32 * U - 1) / (32 * U) : 0;  // batches of this wave
-    auto kv_issue = [&](const uint16_t* base, int j) {
+    auto kv_issue_at = [&](const uint16_t* base, int j, int stage) {
       const int bpos = base0_of(c) + 32 * U * j;
 #pragma unroll
       for (int u = 0; u < U; u++) {
@@ -946,9 +1011,10 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
         // LDS) load row 0, which every cache has; their values are never used
         const int pl = (pp < p.p_end && pp != p.pos) ? pp : 0;
         __builtin_amdgcn_global_load_lds(as_global<void>(base + (size_t)pl * Dm::D + 8 * t16),
-                                         (__attribute__((address_space(3))) void*)&s.kv[j % kKvStages][c][u][0], 16, 0, 0);
+                                         (__attribute__((address_space(3))) void*)&s.kv[stage][c][u][0], 16, 0, 0);
       }
     };
+    auto kv_issue = [&](const uint16_t* base, int j) { kv_issue_at(base, j, j % kKvStages); };
     // wait until batch j has landed: the batches issued after it may stay in flight
     auto kv_wait = [&](int j, int newer) { wait_vmcnt(U * min(kKvStages - 1, nb - 1 - j) + newer); };
     auto kv_refill = [&](const uint16_t* base, int j) {
@@ -982,286 +1048,365 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
     // right after barrier a instead, batch 0 measured slower: 1,946 against
     // 1,960 tok/s.)
     if (nb > 0) kv_issue(kc, 0);
-    QMK_SYNC();  // c
-    for (int j = 1; j < min(nb, kKvStages); j++) kv_issue(kc, j);
-    if constexpr (EARLY) {
-      static_assert(!EARLY || kLongContext / kGroupSize <= 32 * U, "EARLY: at most one K/V batch per wave");
-      // the last layer reloads its own rows, so the waits below count a static
-      // number of loads (8 MB more reads per token; loading a 2 KB row instead
-      // measured no faster)
-      prefetch_qkv_row(L + 1 < p.nl ? L + 1 : L, 0);
-    }
-    cstamp(L, 2);
-    // ------------------------------------------------ scores and local (max, sum)
-    // position of entry i of this wave's batches (i = 8 batch + 4 u + slot)
-    [[maybe_unused]] auto wave_pos = [&](int i) { return base0 + 32 * U * (i >> 3) + 32 * ((i >> 2) & 1) + (i & 3); };
-    if constexpr (LONG) {
-      // A batch gives each 16-lane row two positions (u = 0, 1) and two heads: four
-      // partial dot products per lane, summed over the row in one transposed
-      // reduction, after which lane t16 < 4 of the row owns the score of
-      // (u = t16 & 1, head = (t16 >> 1) & 1) and alone scales, stores and maxes it.
-      // The softmax terms are then computed once per position, one position per
-      // lane, instead of once per lane of its row.
-      static_assert(Dm::GQ == 2 && U == 2, "four (position, head) scores per lane and batch");
-      const int own_u = t16 & 1, own_h = (t16 >> 1) & 1;
-      const bool owner = t16 < 4;
-      {
+    if constexpr (SPLIT) {
+      QMK_SYNC();  // c
+      cstamp(L, 2);
+      // V rows of this wave's batch into ring stage 1 (its K rows are in stage 0), then this
+      // layer's gate/up and o_proj slices.  The control wave does not poll between barriers c and
+      // f, so nothing queues behind them.  (A wave without positions loads row 0 too: requests
+      // on every path keep the compiler's counted waits exact.)
+      kv_issue_at(vc, 0, 1);
+      prefetch_gu(L);
+      prefetch_o(L);
+      constexpr int kLoadsC = Dm::GU_W * Dm::LH + Dm::OP * Dm::LO;  // weight loads issued after the V rows
+      // ---------------------------------------------- split-K attention over this wave's positions
+      // Lane (slot, t16) holds dims 8*t16..+7 of position base0 + 32u + slot.  Scores as HF
+      // rounds them; the softmax terms are exp(s - m) against the wave's own maximum m, kept in
+      // fp32, and P@V accumulates them unnormalised.  The control wave rescales the waves'
+      // (m, l, acc) to the workgroup's maximum and the combine to the global one.
+      float m_w[Dm::GQ], l_w[Dm::GQ], acc[Dm::GQ][8];
+#pragma unroll
+      for (int h = 0; h < Dm::GQ; h++) {
+        m_w[h] = -INFINITY;
+        l_w[h] = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) acc[h][i] = 0.f;
+      }
+      wait_vmcnt_upto<kLoadsC>();  // the V rows have landed; the weight slices may stay in flight
+      float sc[U][Dm::GQ];  // this lane's row's scores (-inf past the range)
+      if (nb > 0) {
         u32x4 qv[Dm::GQ];
-  #pragma unroll
+#pragma unroll
         for (int h = 0; h < Dm::GQ; h++) qv[h] = *reinterpret_cast<const u32x4*>(s.q + h * Dm::D + 8 * t16);
         const u32x4 k_now = *reinterpret_cast<const u32x4*>(s.k + 8 * t16);
-        // Scores of this wave's positions (to LDS) and their maximum; the keys of
-        // the next batch are requested before the current batch is used.
-        float mloc = -INFINITY;  // owners: the maximum of head own_h over their positions
-        for (int j = 0; j < nb; j++) {
-          const int base = base0 + 32 * U * j;
-          kv_wait(j, 0);
-          const int pp0 = base + slot, pp1 = base + 32 + slot;
-          const u32x4 k0 = pp0 == p.pos ? k_now : s.kv[j % kKvStages][c][0][lane];
-          const u32x4 k1 = pp1 == p.pos ? k_now : s.kv[j % kKvStages][c][1][lane];
-          const float x = row16_sum_t4(dot8(k0, qv[0], 0.f), dot8(k0, qv[1], 0.f), dot8(k1, qv[0], 0.f),
-                                       dot8(k1, qv[1], 0.f), t16);
-          const float sc = bf16r(bf16r(x) * a.attn_scale);
-          const int pp = own_u ? pp1 : pp0;
-          if (owner && pp < p.p_end) {
-            sw[own_h * kHeadStride + 8 * j + 4 * own_u + slot] = sc;
-            mloc = fmaxf(mloc, sc);
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+          const int pp = base0 + 32 * u + slot;
+          // the K rows landed before barrier c (it waits for every LDS write)
+          const u32x4 kx = pp == p.pos ? k_now : s.kv[0][c][u][lane];
+#pragma unroll
+          for (int h = 0; h < Dm::GQ; h++) {
+            const float x = bf16r(bf16r(row16_sum(dot8(kx, qv[h], 0.f))) * a.attn_scale);
+            sc[u][h] = pp < p.p_end ? x : -INFINITY;
+            m_w[h] = fmaxf(m_w[h], sc[u][h]);
           }
-          kv_refill(kc, j);
         }
-        // Every K batch has landed (the last wait was vmcnt(0)); saying so here
-        // lets the compiler drop the vmcnt(0) it would otherwise put before the
-        // next workgroup barriers, which would also wait for weight prefetches.
-        wait_vmcnt(0);
-        // wave maximum per head: lanes 0, 1 of each row hold head 0, lanes 2, 3 head 1
-        {
+#pragma unroll
+        for (int h = 0; h < Dm::GQ; h++) {  // wave maximum over the four 16-lane rows
           float x, y;
-          mloc = fmaxf(mloc, dpp_get<0xB1>(mloc));
-          swap16(mloc, x, y);
-          mloc = fmaxf(x, y);
-          swap32(mloc, x, y);
-          mloc = fmaxf(x, y);
+          swap16(m_w[h], x, y);
+          m_w[h] = fmaxf(x, y);
+          swap32(m_w[h], x, y);
+          m_w[h] = fmaxf(x, y);
         }
-        const float wm[2] = {__int_as_float(__builtin_amdgcn_readlane(__float_as_int(mloc), 0)),
-                             __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mloc), 2))};
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        // sum of exp(s - max), one position per lane
-        float lsum[Dm::GQ] = {0.f, 0.f};
-        for (int i = lane; i < 8 * nb; i += kWave) {
-          const int pp = wave_pos(i);
-          if (pp < p.p_end) {
-  #pragma unroll
-            for (int h = 0; h < Dm::GQ; h++) lsum[h] += exp_acc(sw[h * kHeadStride + i] - wm[h]);
+      }
+      cstamp(L, 3);
+      cstamp(L, 4);
+      if (nb > 0) {
+        const u32x4 v_now = *reinterpret_cast<const u32x4*>(s.v + 8 * t16);
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+          const int pp = base0 + 32 * u + slot;
+          const u32x4 vx = pp == p.pos ? v_now : s.kv[1][c][u][lane];
+          const float vf[8] = {lo_bf16(vx.x), hi_bf16(vx.x), lo_bf16(vx.y), hi_bf16(vx.y),
+                               lo_bf16(vx.z), hi_bf16(vx.z), lo_bf16(vx.w), hi_bf16(vx.w)};
+#pragma unroll
+          for (int h = 0; h < Dm::GQ; h++) {
+            // positions past the range load row 0 (finite) and get weight 0
+            const float e = pp < p.p_end ? exp_acc(sc[u][h] - m_w[h]) : 0.f;
+            l_w[h] += e;
+#pragma unroll
+            for (int i = 0; i < 8; i++) acc[h][i] = __builtin_fmaf(e, vf[i], acc[h][i]);
           }
         }
-  #pragma unroll
-        for (int h = 0; h < Dm::GQ; h++) {
-          lsum[h] = wave_total(lsum[h]);
-          if (lane == 0) {
-            s.wml[c][h][0] = wm[h];
-            s.wml[c][h][1] = lsum[h];
-          }
+      }
+      // sum the wave's four rows; lanes 0..15 then hold dims 8*t16..+7 (a wave without positions
+      // publishes (-inf, 0, 0))
+#pragma unroll
+      for (int h = 0; h < Dm::GQ; h++) {
+        l_w[h] = rows_sum4(l_w[h]);
+#pragma unroll
+        for (int i = 0; i < 8; i++) acc[h][i] = rows_sum4(acc[h][i]);
+        if (lane < 16) {
+#pragma unroll
+          for (int i = 0; i < 8; i++) s.wacc[c][h][8 * t16 + i] = acc[h][i];
+        }
+        if (lane == 0) {
+          s.wml[c][h][0] = m_w[h];
+          s.wml[c][h][1] = l_w[h];
         }
       }
     } else {
-      {
-        u32x4 qv[Dm::GQ];
-  #pragma unroll
-        for (int h = 0; h < Dm::GQ; h++) qv[h] = *reinterpret_cast<const u32x4*>(s.q + h * Dm::D + 8 * t16);
-        const u32x4 k_now = *reinterpret_cast<const u32x4*>(s.k + 8 * t16);
-        // Scores of this wave's positions (to LDS) and their maximum; the keys of
-        // the next batch are requested before the current batch is used.
-        float mloc[Dm::GQ];
-  #pragma unroll
-        for (int h = 0; h < Dm::GQ; h++) mloc[h] = -INFINITY;
-        for (int j = 0; j < nb; j++) {
-          const int base = base0 + 32 * U * j;
-          if constexpr (EARLY) wait_vmcnt(NB_C); else kv_wait(j, 0);
-  #pragma unroll
-          for (int u = 0; u < U; u++) {
-            if (base + 32 * u >= p.p_end) break;  // the rest of the batch is past this workgroup's range
-            const int pp = base + 32 * u + slot;
-            const u32x4 kx = pp == p.pos ? k_now : s.kv[j % kKvStages][c][u][lane];
-  #pragma unroll
-            for (int h = 0; h < Dm::GQ; h++) {
-              float sc = row16_sum(dot8(kx, qv[h], 0.f));
-              sc = bf16r(bf16r(sc) * a.attn_scale);
+      QMK_SYNC();  // c
+      for (int j = 1; j < min(nb, kKvStages); j++) kv_issue(kc, j);
+      cstamp(L, 2);
+      // ------------------------------------------------ scores and local (max, sum)
+      // position of entry i of this wave's batches (i = 8 batch + 4 u + slot)
+      [[maybe_unused]] auto wave_pos = [&](int i) { return base0 + 32 * U * (i >> 3) + 32 * ((i >> 2) & 1) + (i & 3); };
+      if constexpr (LONG) {
+        // A batch gives each 16-lane row two positions (u = 0, 1) and two heads: four
+        // partial dot products per lane, summed over the row in one transposed
+        // reduction, after which lane t16 < 4 of the row owns the score of
+        // (u = t16 & 1, head = (t16 >> 1) & 1) and alone scales, stores and maxes it.
+        // The softmax terms are then computed once per position, one position per
+        // lane, instead of once per lane of its row.
+        static_assert(Dm::GQ == 2 && U == 2, "four (position, head) scores per lane and batch");
+        const int own_u = t16 & 1, own_h = (t16 >> 1) & 1;
+        const bool owner = t16 < 4;
+        {
+          u32x4 qv[Dm::GQ];
+    #pragma unroll
+          for (int h = 0; h < Dm::GQ; h++) qv[h] = *reinterpret_cast<const u32x4*>(s.q + h * Dm::D + 8 * t16);
+          const u32x4 k_now = *reinterpret_cast<const u32x4*>(s.k + 8 * t16);
+          // Scores of this wave's positions (to LDS) and their maximum; the keys of
+          // the next batch are requested before the current batch is used.
+          float mloc = -INFINITY;  // owners: the maximum of head own_h over their positions
+          for (int j = 0; j < nb; j++) {
+            const int base = base0 + 32 * U * j;
+            kv_wait(j, 0);
+            const int pp0 = base + slot, pp1 = base + 32 + slot;
+            const u32x4 k0 = pp0 == p.pos ? k_now : s.kv[j % kKvStages][c][0][lane];
+            const u32x4 k1 = pp1 == p.pos ? k_now : s.kv[j % kKvStages][c][1][lane];
+            const float x = row16_sum_t4(dot8(k0, qv[0], 0.f), dot8(k0, qv[1], 0.f), dot8(k1, qv[0], 0.f),
+                                         dot8(k1, qv[1], 0.f), t16);
+            const float sc = bf16r(bf16r(x) * a.attn_scale);
+            const int pp = own_u ? pp1 : pp0;
+            if (owner && pp < p.p_end) {
+              sw[own_h * kHeadStride + 8 * j + 4 * own_u + slot] = sc;
+              mloc = fmaxf(mloc, sc);
+            }
+            kv_refill(kc, j);
+          }
+          // Every K batch has landed (the last wait was vmcnt(0)); saying so here
+          // lets the compiler drop the vmcnt(0) it would otherwise put before the
+          // next workgroup barriers, which would also wait for weight prefetches.
+          wait_vmcnt(0);
+          // wave maximum per head: lanes 0, 1 of each row hold head 0, lanes 2, 3 head 1
+          {
+            float x, y;
+            mloc = fmaxf(mloc, dpp_get<0xB1>(mloc));
+            swap16(mloc, x, y);
+            mloc = fmaxf(x, y);
+            swap32(mloc, x, y);
+            mloc = fmaxf(x, y);
+          }
+          const float wm[2] = {__int_as_float(__builtin_amdgcn_readlane(__float_as_int(mloc), 0)),
+                               __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mloc), 2))};
+          __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+          __builtin_amdgcn_wave_barrier();
+          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+          // sum of exp(s - max), one position per lane
+          float lsum[Dm::GQ] = {0.f, 0.f};
+          for (int i = lane; i < 8 * nb; i += kWave) {
+            const int pp = wave_pos(i);
+            if (pp < p.p_end) {
+    #pragma unroll
+              for (int h = 0; h < Dm::GQ; h++) lsum[h] += exp_acc(sw[h * kHeadStride + i] - wm[h]);
+            }
+          }
+    #pragma unroll
+          for (int h = 0; h < Dm::GQ; h++) {
+            lsum[h] = wave_total(lsum[h]);
+            if (lane == 0) {
+              s.wml[c][h][0] = wm[h];
+              s.wml[c][h][1] = lsum[h];
+            }
+          }
+        }
+      } else {
+        {
+          u32x4 qv[Dm::GQ];
+    #pragma unroll
+          for (int h = 0; h < Dm::GQ; h++) qv[h] = *reinterpret_cast<const u32x4*>(s.q + h * Dm::D + 8 * t16);
+          const u32x4 k_now = *reinterpret_cast<const u32x4*>(s.k + 8 * t16);
+          // Scores of this wave's positions (to LDS) and their maximum; the keys of
+          // the next batch are requested before the current batch is used.
+          float mloc[Dm::GQ];
+    #pragma unroll
+          for (int h = 0; h < Dm::GQ; h++) mloc[h] = -INFINITY;
+          for (int j = 0; j < nb; j++) {
+            const int base = base0 + 32 * U * j;
+            kv_wait(j, 0);
+    #pragma unroll
+            for (int u = 0; u < U; u++) {
+              if (base + 32 * u >= p.p_end) break;  // the rest of the batch is past this workgroup's range
+              const int pp = base + 32 * u + slot;
+              const u32x4 kx = pp == p.pos ? k_now : s.kv[j % kKvStages][c][u][lane];
+    #pragma unroll
+              for (int h = 0; h < Dm::GQ; h++) {
+                float sc = row16_sum(dot8(kx, qv[h], 0.f));
+                sc = bf16r(bf16r(sc) * a.attn_scale);
+                if (pp < p.p_end) {
+                  if (t16 == 0) s.sc[h][pp - p.p_begin] = sc;
+                  mloc[h] = fmaxf(mloc[h], sc);
+                }
+              }
+            }
+            kv_refill(kc, j);
+          }
+          // Every K batch has landed (the last wait was vmcnt(0)); saying so here
+          // lets the compiler drop the vmcnt(0) it would otherwise put before the
+          // next workgroup barriers, which would also wait for weight prefetches.
+          wait_vmcnt(0);
+          // wave maximum over the four 16-lane rows, then the sum of exp(s - max)
+          // with one exponential per position
+    #pragma unroll
+          for (int h = 0; h < Dm::GQ; h++) {
+            float x, y;
+            swap16(mloc[h], x, y);
+            mloc[h] = fmaxf(x, y);
+            swap32(mloc[h], x, y);
+            mloc[h] = fmaxf(x, y);
+          }
+          __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+          __builtin_amdgcn_wave_barrier();
+          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+          float lsum[Dm::GQ];
+    #pragma unroll
+          for (int h = 0; h < Dm::GQ; h++) lsum[h] = 0.f;
+          for (int j = 0; j < nb; j++) {
+            const int base = base0 + 32 * U * j;
+    #pragma unroll
+            for (int u = 0; u < U; u++) {
+              const int pp = base + 32 * u + slot;
               if (pp < p.p_end) {
-                if (t16 == 0) s.sc[h][pp - p.p_begin] = sc;
-                mloc[h] = fmaxf(mloc[h], sc);
+    #pragma unroll
+                for (int h = 0; h < Dm::GQ; h++) lsum[h] += exp_acc(s.sc[h][pp - p.p_begin] - mloc[h]);
               }
             }
           }
-          if constexpr (!EARLY) kv_refill(kc, j);  // EARLY: one batch per wave, no refill
+    #pragma unroll
+          for (int h = 0; h < Dm::GQ; h++) {
+            lsum[h] = rows_sum4(lsum[h]);  // rows hold different positions; lanes of a row the same one
+            if (lane == 0) {
+              s.wml[c][h][0] = mloc[h];
+              s.wml[c][h][1] = lsum[h];
+            }
+          }
         }
-        // Every K batch has landed (the last wait was vmcnt(0)); saying so here
-        // lets the compiler drop the vmcnt(0) it would otherwise put before the
-        // next workgroup barriers, which would also wait for weight prefetches.
-        wait_vmcnt(NB_C);  // the weight slices requested at c may stay in flight
-        // wave maximum over the four 16-lane rows, then the sum of exp(s - max)
-        // with one exponential per position
+      }
+      cstamp(L, 3);
+      QMK_SYNC();  // d
+      if (nb > 0) kv_issue(vc, 0);
+      QMK_SYNC();  // e
+      for (int j = 1; j < min(nb, kKvStages); j++) kv_issue(vc, j);
+      cstamp(L, 4);
+      // ------------------------------------------------ probabilities and P@V
+      if constexpr (LONG)
+      {
+        const u32x4 v_now = *reinterpret_cast<const u32x4*>(s.v + 8 * t16);
+        float gm[Dm::GQ], ginv[Dm::GQ];
   #pragma unroll
         for (int h = 0; h < Dm::GQ; h++) {
-          float x, y;
-          swap16(mloc[h], x, y);
-          mloc[h] = fmaxf(x, y);
-          swap32(mloc[h], x, y);
-          mloc[h] = fmaxf(x, y);
+          gm[h] = s.ml[h][0];
+          ginv[h] = __fdiv_rn(1.0f, s.ml[h][1]);
+        }
+        // HF: softmax in fp32, probabilities rounded to bf16 before P@V; one
+        // position per lane, both heads' bf16 bits in one word
+        for (int i = lane; i < 8 * nb; i += kWave) {
+          const int pp = wave_pos(i);
+          if (pp < p.p_end) {
+            const uint32_t p0 = f32_to_bf16(exp_acc(sw[i] - gm[0]) * ginv[0]);
+            const uint32_t p1 = f32_to_bf16(exp_acc(sw[kHeadStride + i] - gm[1]) * ginv[1]);
+            pw[i] = p1 << 16 | p0;
+          }
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        float lsum[Dm::GQ];
+        float acc[Dm::GQ][8];
   #pragma unroll
-        for (int h = 0; h < Dm::GQ; h++) lsum[h] = 0.f;
+        for (int h = 0; h < Dm::GQ; h++)
+  #pragma unroll
+          for (int i = 0; i < 8; i++) acc[h][i] = 0.f;
         for (int j = 0; j < nb; j++) {
           const int base = base0 + 32 * U * j;
+          kv_wait(j, 0);
+          // the row's two positions are paired in bf16x2 operands: probabilities
+          // (head h of both) and values (one dimension of both), so one dot2
+          // accumulates two positions; a position past the range has probability 0
+          const int pp0 = base + slot, pp1 = base + 32 + slot;
+          const u32x4 v0 = pp0 == p.pos ? v_now : s.kv[j % kKvStages][c][0][lane];
+          const u32x4 v1 = pp1 == p.pos ? v_now : s.kv[j % kKvStages][c][1][lane];
+          const uint32_t w0 = pp0 < p.p_end ? pw[8 * j + slot] : 0u;
+          const uint32_t w1 = pp1 < p.p_end ? pw[8 * j + 4 + slot] : 0u;
+          const bf16x2 pr[2] = {as_bf2(__builtin_amdgcn_perm(w1, w0, 0x05040100u)),
+                                as_bf2(__builtin_amdgcn_perm(w1, w0, 0x07060302u))};
+          const uint32_t va[4] = {v0.x, v0.y, v0.z, v0.w}, vb[4] = {v1.x, v1.y, v1.z, v1.w};
   #pragma unroll
-          for (int u = 0; u < U; u++) {
-            const int pp = base + 32 * u + slot;
-            if (pp < p.p_end) {
+          for (int k = 0; k < 4; k++) {
+            const bf16x2 lo = as_bf2(__builtin_amdgcn_perm(vb[k], va[k], 0x05040100u));  // dim 2k
+            const bf16x2 hi = as_bf2(__builtin_amdgcn_perm(vb[k], va[k], 0x07060302u));  // dim 2k+1
   #pragma unroll
-              for (int h = 0; h < Dm::GQ; h++) lsum[h] += exp_acc(s.sc[h][pp - p.p_begin] - mloc[h]);
+            for (int h = 0; h < Dm::GQ; h++) {
+              acc[h][2 * k] = __builtin_amdgcn_fdot2_f32_bf16(pr[h], lo, acc[h][2 * k], false);
+              acc[h][2 * k + 1] = __builtin_amdgcn_fdot2_f32_bf16(pr[h], hi, acc[h][2 * k + 1], false);
             }
           }
+          kv_refill(vc, j);
         }
+        wait_vmcnt(0);  // every V batch has landed (see above)
+        // sum the wave's four slots; lanes 0..15 then hold dims 8*t16..+7
   #pragma unroll
         for (int h = 0; h < Dm::GQ; h++) {
-          lsum[h] = rows_sum4(lsum[h]);  // rows hold different positions; lanes of a row the same one
-          if (lane == 0) {
-            s.wml[c][h][0] = mloc[h];
-            s.wml[c][h][1] = lsum[h];
+  #pragma unroll
+          for (int i = 0; i < 8; i++) acc[h][i] = rows_sum4(acc[h][i]);
+          if (lane < 16) {
+  #pragma unroll
+            for (int i = 0; i < 8; i++) s.wacc[c][h][8 * t16 + i] = acc[h][i];
           }
         }
       }
-    }
-    cstamp(L, 3);
-    QMK_SYNC();  // d
-    if (nb > 0) kv_issue(vc, 0);
-    QMK_SYNC();  // e
-    for (int j = 1; j < min(nb, kKvStages); j++) kv_issue(vc, j);
-    if constexpr (EARLY) {
-      prefetch_gu(L);
-      prefetch_qkv_row(L + 1 < p.nl ? L + 1 : L, 1);
-    }
-    cstamp(L, 4);
-    // ------------------------------------------------ probabilities and P@V
-    if constexpr (LONG)
-    {
-      const u32x4 v_now = *reinterpret_cast<const u32x4*>(s.v + 8 * t16);
-      float gm[Dm::GQ], ginv[Dm::GQ];
-#pragma unroll
-      for (int h = 0; h < Dm::GQ; h++) {
-        gm[h] = s.ml[h][0];
-        ginv[h] = __fdiv_rn(1.0f, s.ml[h][1]);
-      }
-      // HF: softmax in fp32, probabilities rounded to bf16 before P@V; one
-      // position per lane, both heads' bf16 bits in one word
-      for (int i = lane; i < 8 * nb; i += kWave) {
-        const int pp = wave_pos(i);
-        if (pp < p.p_end) {
-          const uint32_t p0 = f32_to_bf16(exp_acc(sw[i] - gm[0]) * ginv[0]);
-          const uint32_t p1 = f32_to_bf16(exp_acc(sw[kHeadStride + i] - gm[1]) * ginv[1]);
-          pw[i] = p1 << 16 | p0;
+      else
+      {
+        const u32x4 v_now = *reinterpret_cast<const u32x4*>(s.v + 8 * t16);
+        float gm[Dm::GQ], ginv[Dm::GQ];
+  #pragma unroll
+        for (int h = 0; h < Dm::GQ; h++) {
+          gm[h] = s.ml[h][0];
+          ginv[h] = __fdiv_rn(1.0f, s.ml[h][1]);
         }
-      }
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      float acc[Dm::GQ][8];
-#pragma unroll
-      for (int h = 0; h < Dm::GQ; h++)
-#pragma unroll
-        for (int i = 0; i < 8; i++) acc[h][i] = 0.f;
-      for (int j = 0; j < nb; j++) {
-        const int base = base0 + 32 * U * j;
-        kv_wait(j, 0);
-        // the row's two positions are paired in bf16x2 operands: probabilities
-        // (head h of both) and values (one dimension of both), so one dot2
-        // accumulates two positions; a position past the range has probability 0
-        const int pp0 = base + slot, pp1 = base + 32 + slot;
-        const u32x4 v0 = pp0 == p.pos ? v_now : s.kv[j % kKvStages][c][0][lane];
-        const u32x4 v1 = pp1 == p.pos ? v_now : s.kv[j % kKvStages][c][1][lane];
-        const uint32_t w0 = pp0 < p.p_end ? pw[8 * j + slot] : 0u;
-        const uint32_t w1 = pp1 < p.p_end ? pw[8 * j + 4 + slot] : 0u;
-        const bf16x2 pr[2] = {as_bf2(__builtin_amdgcn_perm(w1, w0, 0x05040100u)),
-                              as_bf2(__builtin_amdgcn_perm(w1, w0, 0x07060302u))};
-        const uint32_t va[4] = {v0.x, v0.y, v0.z, v0.w}, vb[4] = {v1.x, v1.y, v1.z, v1.w};
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-          const bf16x2 lo = as_bf2(__builtin_amdgcn_perm(vb[k], va[k], 0x05040100u));  // dim 2k
-          const bf16x2 hi = as_bf2(__builtin_amdgcn_perm(vb[k], va[k], 0x07060302u));  // dim 2k+1
-#pragma unroll
-          for (int h = 0; h < Dm::GQ; h++) {
-            acc[h][2 * k] = __builtin_amdgcn_fdot2_f32_bf16(pr[h], lo, acc[h][2 * k], false);
-            acc[h][2 * k + 1] = __builtin_amdgcn_fdot2_f32_bf16(pr[h], hi, acc[h][2 * k + 1], false);
-          }
-        }
-        kv_refill(vc, j);
-      }
-      wait_vmcnt(0);  // every V batch has landed (see above)
-      // sum the wave's four slots; lanes 0..15 then hold dims 8*t16..+7
-#pragma unroll
-      for (int h = 0; h < Dm::GQ; h++) {
-#pragma unroll
-        for (int i = 0; i < 8; i++) acc[h][i] = rows_sum4(acc[h][i]);
-        if (lane < 16) {
-#pragma unroll
-          for (int i = 0; i < 8; i++) s.wacc[c][h][8 * t16 + i] = acc[h][i];
-        }
-      }
-    }
-    else
-    {
-      const u32x4 v_now = *reinterpret_cast<const u32x4*>(s.v + 8 * t16);
-      float gm[Dm::GQ], ginv[Dm::GQ];
-#pragma unroll
-      for (int h = 0; h < Dm::GQ; h++) {
-        gm[h] = s.ml[h][0];
-        ginv[h] = __fdiv_rn(1.0f, s.ml[h][1]);
-      }
-      float acc[Dm::GQ][8];
-#pragma unroll
-      for (int h = 0; h < Dm::GQ; h++)
-#pragma unroll
-        for (int i = 0; i < 8; i++) acc[h][i] = 0.f;
-      for (int j = 0; j < nb; j++) {
-        const int base = base0 + 32 * U * j;
-        if constexpr (EARLY) wait_vmcnt(NB_E); else kv_wait(j, 0);
-#pragma unroll
-        for (int u = 0; u < U; u++) {
-          if (base + 32 * u >= p.p_end) break;
-          const int pp = base + 32 * u + slot;
-          if (pp < p.p_end) {
-            const u32x4 vx = pp == p.pos ? v_now : s.kv[j % kKvStages][c][u][lane];
-            const float vf[8] = {lo_bf16(vx.x), hi_bf16(vx.x), lo_bf16(vx.y), hi_bf16(vx.y),
-                                 lo_bf16(vx.z), hi_bf16(vx.z), lo_bf16(vx.w), hi_bf16(vx.w)};
-#pragma unroll
-            for (int h = 0; h < Dm::GQ; h++) {
-              // HF: softmax in fp32, probabilities rounded to bf16 before P@V
-              const float pr = bf16r(exp_acc(s.sc[h][pp - p.p_begin] - gm[h]) * ginv[h]);
-#pragma unroll
-              for (int i = 0; i < 8; i++) acc[h][i] += pr * vf[i];
+        float acc[Dm::GQ][8];
+  #pragma unroll
+        for (int h = 0; h < Dm::GQ; h++)
+  #pragma unroll
+          for (int i = 0; i < 8; i++) acc[h][i] = 0.f;
+        for (int j = 0; j < nb; j++) {
+          const int base = base0 + 32 * U * j;
+          kv_wait(j, 0);
+  #pragma unroll
+          for (int u = 0; u < U; u++) {
+            if (base + 32 * u >= p.p_end) break;
+            const int pp = base + 32 * u + slot;
+            if (pp < p.p_end) {
+              const u32x4 vx = pp == p.pos ? v_now : s.kv[j % kKvStages][c][u][lane];
+              const float vf[8] = {lo_bf16(vx.x), hi_bf16(vx.x), lo_bf16(vx.y), hi_bf16(vx.y),
+                                   lo_bf16(vx.z), hi_bf16(vx.z), lo_bf16(vx.w), hi_bf16(vx.w)};
+  #pragma unroll
+              for (int h = 0; h < Dm::GQ; h++) {
+                // HF: softmax in fp32, probabilities rounded to bf16 before P@V
+                const float pr = bf16r(exp_acc(s.sc[h][pp - p.p_begin] - gm[h]) * ginv[h]);
+  #pragma unroll
+                for (int i = 0; i < 8; i++) acc[h][i] += pr * vf[i];
+              }
             }
           }
+          kv_refill(vc, j);
         }
-        if constexpr (!EARLY) kv_refill(vc, j);  // EARLY: one batch per wave, no refill
-      }
-      wait_vmcnt(NB_E);  // every V batch has landed; the slices requested at e may stay in flight
-      // sum the wave's four slots; lanes 0..15 then hold dims 8*t16..+7
-#pragma unroll
-      for (int h = 0; h < Dm::GQ; h++) {
-#pragma unroll
-        for (int i = 0; i < 8; i++) acc[h][i] = rows_sum4(acc[h][i]);
-        if (lane < 16) {
-#pragma unroll
-          for (int i = 0; i < 8; i++) s.wacc[c][h][8 * t16 + i] = acc[h][i];
+        wait_vmcnt(0);  // every V batch has landed
+        // sum the wave's four slots; lanes 0..15 then hold dims 8*t16..+7
+  #pragma unroll
+        for (int h = 0; h < Dm::GQ; h++) {
+  #pragma unroll
+          for (int i = 0; i < 8; i++) acc[h][i] = rows_sum4(acc[h][i]);
+          if (lane < 16) {
+  #pragma unroll
+            for (int i = 0; i < 8; i++) s.wacc[c][h][8 * t16 + i] = acc[h][i];
+          }
         }
       }
+      if (!ST && !EARLY && L + 1 < p.nl) prefetch_qkv(L + 1);
     }
-    if (!ST && !EARLY && L + 1 < p.nl) prefetch_qkv(L + 1);
     cstamp(L, 5);
     QMK_SYNC();  // f
     QMK_SYNC();  // g
@@ -1282,7 +1427,10 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
     QMK_SYNC();  // i
     cstamp(L, 8);
     if constexpr (EARLY) {
-      if (L + 1 < p.nl) { prefetch_o(L + 1); } prefetch_dn(L);
+      // this layer's down slice and the next layer's QKV rows
+      prefetch_dn(L);
+      prefetch_qkv_row(L_next, 0);
+      prefetch_qkv_row(L_next, 1);
     }
     {
       u32x4 act[Dm::LH];
@@ -1432,7 +1580,7 @@ __global__ void __launch_bounds__(kBlock, 1) decode_kernel(KArgs a) {
   p.p_end = min(p.C, p.p_begin + p.chunk);
   p.n_act = (p.C + p.chunk - 1) / p.chunk;
   if (wave == 0) {
-    control_path<M>(a, s, p, b, lane);
+    control_path<M, !LONG && !Dm::kStream>(a, s, p, b, lane);
   } else if constexpr (LONG) {
     compute_path<M, SAMPLED, true>(a, s, p, b, wave - 1, lane, s.sw[wave - 1], s.pw[wave - 1]);
   } else {

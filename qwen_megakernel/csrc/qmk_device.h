@@ -216,6 +216,14 @@ __device__ __forceinline__ void wait_vmcnt(int n) {
   asm volatile("" ::: "memory");  // LDS written by the completed loads is read only after this point
 }
 
+// The same for a compile-time count up to 63 (the whole vmcnt range).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt_upto() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+  asm volatile("" ::: "memory");
+}
+
 // ------------------------------------------------------- tagged exchange
 
 constexpr uint32_t kTimeoutDefault = 100u * 1000u * 1000u;  // 1 s of the 100 MHz wall clock
