@@ -1100,8 +1100,6 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
           m_w[h] = fmaxf(x, y);
         }
       }
-      cstamp(L, 3);
-      cstamp(L, 4);
       if (nb > 0) {
         const u32x4 v_now = *reinterpret_cast<const u32x4*>(s.v + 8 * t16);
 #pragma unroll
@@ -1120,6 +1118,8 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
           }
         }
       }
+      cstamp(L, 3);
+      cstamp(L, 4);
       // sum the wave's four rows; lanes 0..15 then hold dims 8*t16..+7 (a wave without positions
       // publishes (-inf, 0, 0))
 #pragma unroll
@@ -1464,10 +1464,8 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
     cstamp(L, 11);
   }
 
-  QMK_SYNC();  // final a
   {
-    u32x4 act[Dm::LH];
-    load_act(act, s.n, 0, lane);
+    u32x4 act[Dm::LH];  // the final-normed activation, loaded after barrier final a
     const int row0 = b * Dm::LM_RPW;
     const int nrows = min(Dm::V - row0, Dm::LM_RPW);
     const int nmine = (nrows - c + kComputeWaves - 1) / kComputeWaves;
@@ -1500,7 +1498,11 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
         }
       }
     };
+    // the first batch of rows needs no activation: requested before barrier final a, it streams
+    // while the control wave gathers h and applies the final norm
     load_batch(bufA, 0);
+    QMK_SYNC();  // final a
+    load_act(act, s.n, 0, lane);
     for (int i = 0; i < nmine; i += 2 * Dm::LM_U) {
       load_batch(bufB, i + Dm::LM_U);
       do_batch(bufA, i);
