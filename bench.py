@@ -47,7 +47,8 @@ SiLU*mul, down, LM head + argmax) run alone over >= 1 GiB of rotating seeded
 N(0, 0.02) weight copies with N(0, 1) activations, in GB/s.
 
 Options for profiling runs: ``--phase-trace`` adds the in-kernel phase trace
-of one more step (at the last timed context) to the JSON line;
+of one more step (at the last timed context) to the JSON line, for the
+Qwen3-0.6B run and for Qwen3-1.7B at batch 1;
 ``--copy-calibration`` first runs a plain 1 GiB device-to-device copy five
 times, so that a counter run (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE) sees a
 kernel of known traffic beside the decode kernel.
@@ -73,7 +74,7 @@ PROMPT_LEN = 128
 TRAFFIC_PROFILE = {
     "file": "profiles/decode_kernel_qwen3_0p6b_ctx129-1152_xcd_parallel.md",
     "contexts": "129..1152",
-    "measured_bytes": 1_315_038_787,
+    "measured_bytes": 1_353_526_495,
     "algorithmic_bytes": 1_265_674_240,
 }
 METRIC = "decode tok/s, batch 1, Qwen3-0.6B bf16; achieved HBM GB/s vs ~8 TB/s peak"
@@ -183,7 +184,7 @@ def long_context(w, steps: int, contexts=(8192, 32768)):
     return out
 
 
-def qwen3_1p7b(steps: int = 256, prompt_len: int = 512, batch: int = 4):
+def qwen3_1p7b(steps: int = 256, prompt_len: int = 512, batch: int = 4, phase_trace: bool = False):
     """Qwen3-1.7B at batch 1 and at batch `batch`.
 
     Batch 1: a `prompt_len`-token prompt prefilled, then `steps` device-fed steps of the decode
@@ -212,6 +213,16 @@ def qwen3_1p7b(steps: int = 256, prompt_len: int = 512, batch: int = 4):
     torch.cuda.synchronize()
     assert int(ops.device_error()) == 0
     t = e0.elapsed_time(e1) / 1e3 / steps
+    trace_summary = None
+    if phase_trace:
+        from qwen_megakernel import trace
+
+        # one more step, at the context after the timed ones, with the in-kernel trace on
+        dec._position = prompt_len - 1 + steps
+        stamps = trace.capture(lambda: dec.step(11), S.num_layers)
+        trace_summary = trace.summarize(stamps, S.num_layers)
+        trace_summary["context"] = prompt_len + steps
+        log(f"qwen3-1.7b phase trace at context {prompt_len + steps}:\n" + trace.format_table(trace_summary))
     mean_c = prompt_len + (steps - 1) / 2.0
     byts = S.weight_bytes_per_token() + S.kv_bytes_per_position() * (mean_c + 1)
     del dec
@@ -220,6 +231,8 @@ def qwen3_1p7b(steps: int = 256, prompt_len: int = 512, batch: int = 4):
     out = {"tok_per_s": round(1.0 / t, 2), "ms_per_token": round(t * 1e3, 4), "batch": 1, "steps": steps,
            "context": f"{prompt_len}..{prompt_len + steps - 1}", "bytes_per_token": int(byts),
            "achieved_GBps": round(byts / t / 1e9, 1), "roofline_frac": round(byts / t / 1e9 / PEAK_HBM_GBS, 4)}
+    if trace_summary is not None:
+        out["phase_trace"] = trace_summary
 
     bd = BatchDecoder(weights=w, batch_size=batch, max_seq_len=max_seq, verbose=False)
     prompts = [make_prompt(prompt_len, S.vocab, seed=1 + b) for b in range(batch)]
@@ -487,7 +500,7 @@ def main():
     del w
     torch.cuda.empty_cache()
     if not args.no_1p7b:
-        result["qwen3_1p7b"] = qwen3_1p7b()
+        result["qwen3_1p7b"] = qwen3_1p7b(phase_trace=args.phase_trace)
     if not args.no_phases:
         from qwen_megakernel import phases as P
 
