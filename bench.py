@@ -262,8 +262,8 @@ def qwen3_1p7b(steps: int = 256, prompt_len: int = 512, batch: int = 4, phase_tr
                      "bytes_per_step": int(byts_b), "achieved_GBps": round(byts_b / tb / 1e9, 1),
                      "roofline_frac": round(byts_b / tb / 1e9 / PEAK_HBM_GBS, 4),
                      "prefill_ms": round(prefill_s * 1e3, 2),
-                     "path": "decode_batch: 5 launches per layer (norm-prologue / residual- and SiLU-epilogue "
-                             "K-split MFMA GEMMs, fused attention), streamed LM head"}
+                     "path": "decode_batch: 6 launches per layer (norm-prologue / residual- and SiLU-epilogue "
+                             "K-split MFMA GEMMs, split-K attention over all CUs and its merge), streamed LM head"}
     return out
 
 

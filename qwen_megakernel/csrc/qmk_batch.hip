@@ -1016,10 +1016,11 @@ __global__ void __launch_bounds__(256) keys_reduce(const unsigned long long* __r
 // ---------------------------------------------------------------- decode step, few sequences
 //
 // One token per sequence, at most 16 sequences (one MFMA row tile), contexts
-// up to kFusedCtx: five launches per layer instead of eleven.
+// up to kFusedCtx: six launches per layer instead of eleven.
 //
 //   gemm_rows<NORM>(q,k,v)   input RMSNorm in the prologue, bf16 q|k|v out
-//   attention_fused          q/k head norm + RoPE, K/V append, attention
+//   attention_split          q/k head norm + RoPE, K/V append, split-K attention
+//                            over all CUs; attention_merge combines the splits
 //   gemm_rows(o)             epilogue: residual add into the hidden rows
 //   gemm_rows<NORM>(g|u)     post-attention RMSNorm in the prologue, SiLU(g)*u out
 //   gemm_rows(down)          epilogue: residual add
@@ -1197,49 +1198,101 @@ __global__ void __launch_bounds__(NW * 64) gemm_rows(const uint16_t* __restrict_
   else *dst = (uint16_t)f32_to_bf16(y);
 }
 
-// One workgroup of 16 waves per (sequence's token, KV head g): the q heads 2g,
-// 2g+1 and k head g get their head RMSNorm + RoPE, K/V of the token are
-// appended at its position, then eager attention over positions 0..pos (the
-// token's own K/V taken from LDS).  Valid only when no other token of the
-// launch writes this sequence's cache (one token per sequence).
-__global__ void __launch_bounds__(1024) attention_fused(const uint16_t* __restrict__ QKV, const Tok* __restrict__ tok,
-                                                        int L, const uint16_t* q_norm, const uint16_t* k_norm,
-                                                        const uint16_t* cos_t, const uint16_t* sin_t, Cache c,
-                                                        float eps, float scale, uint16_t* __restrict__ out) {
-  __shared__ float sc[2][kFusedCtx];
+// Decode-step attention, split over positions: S workgroups of kSplitWaves
+// waves per (sequence's token, KV head), S * T * 8 >= 256, so that every CU
+// streams K/V (one workgroup per (token, KV head) left 224 of 256 CUs idle at
+// four sequences).  Each workgroup:
+// - requests the token's q/k/v head values, norm weights and RoPE row, then
+//   every K and V row of its positions [pb, pe) at once (a CU returns loads in
+//   order, so the small loads come first);
+// - forms the q heads 2g, 2g+1 and k head g (head RMSNorm + RoPE, as HF), and
+//   split 0 appends the token's K/V at its position (the token's own K/V are
+//   used from LDS, so no workgroup reads that cache row);
+// - scores its positions as HF rounds them and accumulates exp(s - m) * v in
+//   fp32 against its running maximum m: a split-K softmax whose probabilities
+//   are not rounded to bf16, as in the reference kernel's attention
+//   (csrc/kernel.cu:498-571);
+// - writes its (m, l, acc) to the workspace; attention_merge (the next launch)
+//   rescales the S partials of each (token, KV head) to the global maximum in
+//   split order and writes the bf16 attention output.  (A merge by the last
+//   workgroup to arrive, behind device-scope release/acquire fences, measured
+//   1.77 ms per Qwen3-1.7B batch-4 step against 1.51 for the second launch.)
+// Valid only when no other token of the launch writes this sequence's cache
+// (one token per sequence).
+constexpr int kSplitWaves = 4;    // waves per workgroup
+constexpr int kSplitRounds = 8;   // 16-position rounds of K and V rows in flight per wave
+constexpr int kMaxAttnSplit = 32;
+
+struct AttnPart {
+  float acc[2][kD];  // unnormalised P@V of heads 2g, 2g+1 against m
+  float m[2], l[2];  // maximum score and sum of exp(s - m)
+};
+
+// position splits per (token, KV head) for T tokens
+int attn_splits(int T) { return std::min(kMaxAttnSplit, std::max(1, 256 / (kNKV * T))); }
+
+__global__ void __launch_bounds__(kSplitWaves * 64) attention_split(
+    const uint16_t* __restrict__ QKV, const Tok* __restrict__ tok, int L, const uint16_t* q_norm,
+    const uint16_t* k_norm, const uint16_t* cos_t, const uint16_t* sin_t, Cache c, float eps, float scale,
+    AttnPart* __restrict__ part, uint16_t* __restrict__ out) {
   __shared__ uint16_t qs[2][kD], kn[kD], vn[kD];
-  __shared__ float redm[2][kRowWaves];
-  __shared__ float pv[kRowWaves][2][kD];
-  const int t = blockIdx.x, g = blockIdx.y;
+  __shared__ float wm[kSplitWaves][2], wl[kSplitWaves][2];
+  __shared__ float wacc[kSplitWaves][2][kD];
+  const int t = blockIdx.x, g = blockIdx.y, sp = blockIdx.z, S = gridDim.z;
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, slot = lane >> 4, t16 = lane & 15;
   const Tok tk = tok[t];
   uint16_t* dst = out + (size_t)t * kQS + 2 * g * kD;
   if (!tk.valid) {
-    if (threadIdx.x < 2 * kD) dst[threadIdx.x] = 0;
+    if (sp == 0 && threadIdx.x < 2 * kD) dst[threadIdx.x] = 0;
     return;
   }
   const int pos = tk.pos, C = pos + 1;
+  const int chunk = (C + S - 1) / S;
+  const int pb = min(C, sp * chunk), pe = min(C, pb + chunk);
   const size_t base = cache_base(c, tk, L, g);
-  if (w < 4) {
-    // waves 0,1: q heads 2g, 2g+1; wave 2: k head g; wave 3: v head g
-    const int h = w < 2 ? 2 * g + w : (w == 2 ? kNQ + g : kNQ + kNKV + g);
-    const uint16_t* src = QKV + (size_t)t * kNQKV + h * kD;
-    const float x0 = bf16_to_f32(src[lane]), x1 = bf16_to_f32(src[lane + 64]);
+  const uint16_t* kc = c.k + base;
+  const uint16_t* vc = c.v + base;
+  // waves 0, 1: q heads 2g, 2g+1; wave 2: k head g; wave 3: v head g
+  const int h = w < 2 ? 2 * g + w : (w == 2 ? kNQ + g : kNQ + kNKV + g);
+  const uint16_t* src = QKV + (size_t)t * kNQKV + h * kD;
+  const uint16_t* nw = w < 2 ? q_norm : k_norm;
+  const uint32_t x0b = ldu16(src + lane), x1b = ldu16(src + lane + 64);
+  const uint32_t w0b = ldu16(nw + lane), w1b = ldu16(nw + lane + 64);
+  const uint16_t* cr = cos_t + (size_t)pos * kD;
+  const uint16_t* sr = sin_t + (size_t)pos * kD;
+  const uint32_t c0b = ldu16(cr + lane), c1b = ldu16(cr + lane + 64);
+  const uint32_t s0b = ldu16(sr + lane), s1b = ldu16(sr + lane + 64);
+  // lane (slot, t16) of wave w takes dims 8*t16..+7 of position p0 + 16r + 4w + slot in round r;
+  // positions outside [pb, pe) and pos itself load row 0 (every cache has it) and are masked
+  u32x4 kx[kSplitRounds], vx[kSplitRounds];
+  auto issue = [&](int p0) {
+#pragma unroll
+    for (int r = 0; r < kSplitRounds; r++) {
+      const int p = p0 + 16 * r + 4 * w + slot;
+      kx[r] = ld16(kc + (size_t)((p < pe && p != pos) ? p : 0) * kD + 8 * t16);
+    }
+#pragma unroll
+    for (int r = 0; r < kSplitRounds; r++) {
+      const int p = p0 + 16 * r + 4 * w + slot;
+      vx[r] = ld16(vc + (size_t)((p < pe && p != pos) ? p : 0) * kD + 8 * t16);
+    }
+  };
+  issue(pb);
+  {
+    const float x0 = bf16_to_f32(x0b), x1 = bf16_to_f32(x1b);
     if (w == 3) {
-      vn[lane] = src[lane];
-      vn[lane + 64] = src[lane + 64];
-      c.v[base + (size_t)pos * kD + lane] = src[lane];
-      c.v[base + (size_t)pos * kD + lane + 64] = src[lane + 64];
+      vn[lane] = (uint16_t)x0b;
+      vn[lane + 64] = (uint16_t)x1b;
+      if (sp == 0) {
+        c.v[base + (size_t)pos * kD + lane] = (uint16_t)x0b;
+        c.v[base + (size_t)pos * kD + lane + 64] = (uint16_t)x1b;
+      }
     } else {
-      const uint16_t* nw = w < 2 ? q_norm : k_norm;
       const float ss = wave_sum(x0 * x0 + x1 * x1);
       const float rstd = rcp_sqrt_torch(__fdiv_rn(ss, (float)kD) + eps);
-      const float n0 = bf16r(bf16_to_f32(ldu16(nw + lane)) * bf16r(x0 * rstd));
-      const float n1 = bf16r(bf16_to_f32(ldu16(nw + lane + 64)) * bf16r(x1 * rstd));
-      const uint16_t* cr = cos_t + (size_t)pos * kD;
-      const uint16_t* sr = sin_t + (size_t)pos * kD;
-      const float c0 = bf16_to_f32(ldu16(cr + lane)), c1 = bf16_to_f32(ldu16(cr + lane + 64));
-      const float s0 = bf16_to_f32(ldu16(sr + lane)), s1 = bf16_to_f32(ldu16(sr + lane + 64));
+      const float n0 = bf16r(bf16_to_f32(w0b) * bf16r(x0 * rstd));
+      const float n1 = bf16r(bf16_to_f32(w1b) * bf16r(x1 * rstd));
+      const float c0 = bf16_to_f32(c0b), c1 = bf16_to_f32(c1b), s0 = bf16_to_f32(s0b), s1 = bf16_to_f32(s1b);
       const uint16_t y0 = (uint16_t)f32_to_bf16(bf16r(bf16r(n0 * c0) + bf16r(-n1 * s0)));
       const uint16_t y1 = (uint16_t)f32_to_bf16(bf16r(bf16r(n1 * c1) + bf16r(n0 * s1)));
       if (w < 2) {
@@ -1248,125 +1301,125 @@ __global__ void __launch_bounds__(1024) attention_fused(const uint16_t* __restri
       } else {
         kn[lane] = y0;
         kn[lane + 64] = y1;
-        c.k[base + (size_t)pos * kD + lane] = y0;
-        c.k[base + (size_t)pos * kD + lane + 64] = y1;
+        if (sp == 0) {
+          c.k[base + (size_t)pos * kD + lane] = y0;
+          c.k[base + (size_t)pos * kD + lane + 64] = y1;
+        }
       }
     }
   }
   __syncthreads();
-  const uint16_t* kc = c.k + base;
-  const uint16_t* vc = c.v + base;
   u32x4 qv[2];
 #pragma unroll
-  for (int h = 0; h < 2; h++) qv[h] = *reinterpret_cast<const u32x4*>(&qs[h][8 * t16]);
+  for (int hh = 0; hh < 2; hh++) qv[hh] = *reinterpret_cast<const u32x4*>(&qs[hh][8 * t16]);
   const u32x4 k_now = *reinterpret_cast<const u32x4*>(&kn[8 * t16]);
-  // scores: each 16-lane row one position, 64 per round, kAttnRounds rounds in flight
-  float m0 = -INFINITY, m1 = -INFINITY;
-  for (int p0 = 4 * w + slot; p0 < C; p0 += kAttnRounds * 64) {
-    u32x4 kx[kAttnRounds];
-#pragma unroll
-    for (int u = 0; u < kAttnRounds; u++) {
-      const int p = p0 + 64 * u;
-      kx[u] = (p < C && p != pos) ? ld16(kc + (size_t)p * kD + 8 * t16) : k_now;
-    }
-#pragma unroll
-    for (int u = 0; u < kAttnRounds; u++) {
-      const int p = p0 + 64 * u;
-      if (p < C) {
-        const float s0 = bf16r(bf16r(row16_sum(dot8(kx[u], qv[0], 0.f))) * scale);
-        const float s1 = bf16r(bf16r(row16_sum(dot8(kx[u], qv[1], 0.f))) * scale);
-        if (t16 == 0) {
-          sc[0][p] = s0;
-          sc[1][p] = s1;
-        }
-        m0 = fmaxf(m0, s0);
-        m1 = fmaxf(m1, s1);
-      }
-    }
-  }
-  m0 = wave_max(m0);
-  m1 = wave_max(m1);
-  if (lane == 0) {
-    redm[0][w] = m0;
-    redm[1][w] = m1;
-  }
-  __syncthreads();
-  float M0 = redm[0][0], M1 = redm[1][0];
-  for (int q = 1; q < kRowWaves; q++) {
-    M0 = fmaxf(M0, redm[0][q]);
-    M1 = fmaxf(M1, redm[1][q]);
-  }
-  float l0 = 0.f, l1 = 0.f;
-  for (int i = threadIdx.x; i < C; i += 1024) {
-    l0 += exp_acc(sc[0][i] - M0);
-    l1 += exp_acc(sc[1][i] - M1);
-  }
-  l0 = wave_sum(l0);
-  l1 = wave_sum(l1);
-  __syncthreads();
-  if (lane == 0) {
-    redm[0][w] = l0;
-    redm[1][w] = l1;
-  }
-  __syncthreads();
-  float S0 = 0.f, S1 = 0.f;
-  for (int q = 0; q < kRowWaves; q++) {
-    S0 += redm[0][q];
-    S1 += redm[1][q];
-  }
-  const float inv0 = __fdiv_rn(1.0f, S0), inv1 = __fdiv_rn(1.0f, S1);
-  for (int i = threadIdx.x; i < C; i += 1024) {
-    sc[0][i] = bf16r(exp_acc(sc[0][i] - M0) * inv0);
-    sc[1][i] = bf16r(exp_acc(sc[1][i] - M1) * inv1);
-  }
-  __syncthreads();
-  // P @ V: each 16-lane row takes one position (lane t16: dims 8*t16..+7 of both heads), 64 per
-  // round, kAttnRounds rounds in flight; then the four rows of a wave and the 16 waves are summed in order
   const u32x4 v_now = *reinterpret_cast<const u32x4*>(&vn[8 * t16]);
-  float acc0[8], acc1[8];
+  float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.f, 0.f}, acc[2][8];
 #pragma unroll
-  for (int i = 0; i < 8; i++) acc0[i] = acc1[i] = 0.f;
-  for (int p0 = 4 * w + slot; p0 < C; p0 += kAttnRounds * 64) {
-    u32x4 vx[kAttnRounds];
+  for (int hh = 0; hh < 2; hh++)
 #pragma unroll
-    for (int u = 0; u < kAttnRounds; u++) {
-      const int p = p0 + 64 * u;
-      vx[u] = (p < C && p != pos) ? ld16(vc + (size_t)p * kD + 8 * t16) : v_now;
+    for (int i = 0; i < 8; i++) acc[hh][i] = 0.f;
+  for (int p0 = pb; p0 < pe; p0 += 16 * kSplitRounds) {
+    if (p0 != pb) issue(p0);  // positions beyond the first 16 * kSplitRounds of the split
+    float sc[kSplitRounds][2], bm[2] = {-INFINITY, -INFINITY};
+#pragma unroll
+    for (int r = 0; r < kSplitRounds; r++) {
+      const int p = p0 + 16 * r + 4 * w + slot;
+      const u32x4 kr = p == pos ? k_now : kx[r];
+#pragma unroll
+      for (int hh = 0; hh < 2; hh++) {
+        const float x = bf16r(bf16r(row16_sum(dot8(kr, qv[hh], 0.f))) * scale);
+        sc[r][hh] = p < pe ? x : -INFINITY;
+        bm[hh] = fmaxf(bm[hh], sc[r][hh]);
+      }
     }
 #pragma unroll
-    for (int u = 0; u < kAttnRounds; u++) {
-      const int p = p0 + 64 * u;
-      if (p < C) {
-        const float pa = sc[0][p], pb = sc[1][p];
-        const float vf[8] = {lo_bf16(vx[u].x), hi_bf16(vx[u].x), lo_bf16(vx[u].y), hi_bf16(vx[u].y),
-                             lo_bf16(vx[u].z), hi_bf16(vx[u].z), lo_bf16(vx[u].w), hi_bf16(vx[u].w)};
+    for (int hh = 0; hh < 2; hh++) {
+      float a, b;
+      swap16(bm[hh], a, b);
+      bm[hh] = fmaxf(a, b);
+      swap32(bm[hh], a, b);
+      bm[hh] = fmaxf(a, b);
+      // rescale the running terms to the new maximum
+      const float mn = fmaxf(m[hh], bm[hh]);
+      const float f = m[hh] == -INFINITY ? 0.f : exp_acc(m[hh] - mn);
+      l[hh] *= f;
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-          acc0[i] += pa * vf[i];
-          acc1[i] += pb * vf[i];
-        }
+      for (int i = 0; i < 8; i++) acc[hh][i] *= f;
+      m[hh] = mn;
+    }
+#pragma unroll
+    for (int r = 0; r < kSplitRounds; r++) {
+      const int p = p0 + 16 * r + 4 * w + slot;
+      const u32x4 vr = p == pos ? v_now : vx[r];
+      const float vf[8] = {lo_bf16(vr.x), hi_bf16(vr.x), lo_bf16(vr.y), hi_bf16(vr.y),
+                           lo_bf16(vr.z), hi_bf16(vr.z), lo_bf16(vr.w), hi_bf16(vr.w)};
+#pragma unroll
+      for (int hh = 0; hh < 2; hh++) {
+        const float e = sc[r][hh] == -INFINITY ? 0.f : exp_acc(sc[r][hh] - m[hh]);
+        l[hh] += e;
+#pragma unroll
+        for (int i = 0; i < 8; i++) acc[hh][i] = __builtin_fmaf(e, vf[i], acc[hh][i]);
       }
     }
   }
+  // the wave's four rows summed; lanes 0..15 hold dims 8*t16..+7
 #pragma unroll
-  for (int i = 0; i < 8; i++) {
-    acc0[i] = rows_sum4(acc0[i]);
-    acc1[i] = rows_sum4(acc1[i]);
-  }
-  if (lane < 16) {
+  for (int hh = 0; hh < 2; hh++) {
+    l[hh] = rows_sum4(l[hh]);
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-      pv[w][0][8 * t16 + i] = acc0[i];
-      pv[w][1][8 * t16 + i] = acc1[i];
+    for (int i = 0; i < 8; i++) acc[hh][i] = rows_sum4(acc[hh][i]);
+    if (lane < 16) {
+#pragma unroll
+      for (int i = 0; i < 8; i++) wacc[w][hh][8 * t16 + i] = acc[hh][i];
+    }
+    if (lane == 0) {
+      wm[w][hh] = m[hh];
+      wl[w][hh] = l[hh];
     }
   }
   __syncthreads();
-  if (threadIdx.x < 2 * kD) {
-    const int h = threadIdx.x >> 7, d = threadIdx.x & 127;
-    float y = 0.f;
-    for (int q = 0; q < kRowWaves; q++) y += pv[q][h][d];
-    dst[threadIdx.x] = (uint16_t)f32_to_bf16(y);
+  // this workgroup's partial: the waves rescaled to its maximum, in wave order
+  AttnPart* pt = part + ((size_t)t * kNKV + g) * S;
+  {
+    const int hh = threadIdx.x >> 7, d = threadIdx.x & 127;  // 256 threads: both heads' dims
+    float mx = -INFINITY;
+#pragma unroll
+    for (int q = 0; q < kSplitWaves; q++) mx = fmaxf(mx, wm[q][hh]);
+    float a = 0.f, ls = 0.f;
+#pragma unroll
+    for (int q = 0; q < kSplitWaves; q++) {
+      const float f = wm[q][hh] == -INFINITY ? 0.f : exp_acc(wm[q][hh] - mx);
+      a += f * wacc[q][hh][d];
+      ls += f * wl[q][hh];
+    }
+    pt[sp].acc[hh][d] = a;
+    if (d == 0) {
+      pt[sp].m[hh] = mx;
+      pt[sp].l[hh] = ls;
+    }
   }
+}
+
+// The attention output of (token t, KV head g) from its S partials: each rescaled to the global
+// maximum, in split order.  256 threads: thread i takes head 2g + i / 128, dim i % 128.
+__global__ void __launch_bounds__(256) attention_merge(const Tok* __restrict__ tok, int S,
+                                                       const AttnPart* __restrict__ part, uint16_t* __restrict__ out) {
+  const int t = blockIdx.x, g = blockIdx.y;
+  if (!tok[t].valid) return;  // attention_split wrote the zeros
+  const AttnPart* pt = part + ((size_t)t * kNKV + g) * S;
+  uint16_t* dst = out + (size_t)t * kQS + 2 * g * kD;
+  const int hh = threadIdx.x >> 7, d = threadIdx.x & 127;
+  float mx = -INFINITY;
+  for (int q = 0; q < S; q++) mx = fmaxf(mx, pt[q].m[hh]);
+  float y = 0.f, ls = 0.f;
+  for (int q = 0; q < S; q++) {
+    const float mq = pt[q].m[hh];
+    const float f = mq == -INFINITY ? 0.f : exp_acc(mq - mx);
+    y += f * pt[q].acc[hh][d];
+    ls += f * pt[q].l[hh];
+  }
+  dst[threadIdx.x] = (uint16_t)f32_to_bf16(__fdiv_rn(y, ls));
 }
 
 // ---------------------------------------------------------------- self-test
@@ -1468,7 +1521,7 @@ size_t part_floats(int T, int N, int K) { return (size_t)plan_gemm(T, N, K).kspl
 int split_chunks(int max_context) { return (max_context + kSplitChunk - 1) / kSplitChunk; }
 
 struct Layout {
-  size_t tok, erow, keys, x, n, q, att, m, qkv, part, scores, ml, pv, redo, total;
+  size_t tok, erow, keys, x, n, q, att, m, qkv, apart, part, scores, ml, pv, redo, total;
 };
 
 constexpr int kLmTiles(int V) { return V / 64; }
@@ -1496,6 +1549,7 @@ Layout layout(int T, int R, int max_context, bool one_per_seq = false) {
   take(l.m, (size_t)T * Dm::I * 2);
   if (one_per_seq && fused_decode(T, max_context)) {
     take(l.qkv, (size_t)T * kNQKV * 2);
+    take(l.apart, (size_t)T * kNKV * attn_splits(T) * sizeof(AttnPart));
     l.total = off;
     return l;
   }
@@ -1606,6 +1660,8 @@ int forward_fused(const Args& a, hipStream_t s) {
   static_assert(Dm::H == 1024 || Dm::H == 2048, "K splits of the hidden size");
   static_assert(Dm::I == 3072 || Dm::I == 6144, "K splits of the MLP size");
   static_assert(kQS == 2048 && Dm::H <= kMaxRowsH, "K splits of the attention output");
+  AttnPart* apart = reinterpret_cast<AttnPart*>(a.ws + l.apart);
+  const int nsplit = attn_splits(T);
   hipLaunchKernelGGL(prep_tokens, dim3((std::max(T, R) + 255) / 256), dim3(256), 0, s, a.tokens, a.seqs, a.pos, T,
                      a.emit, R, a.num_seqs, a.max_context, Dm::V, tok, erow);
   hipLaunchKernelGGL(embed_rows, dim3(T), dim3(256), 0, s, a.embed, tok, Dm::H, X);
@@ -1613,8 +1669,10 @@ int forward_fused(const Args& a, hipStream_t s) {
     const LDGLayerWeights& w = a.layers[L];
     const Seg qkv{{u16(w.q_proj_weight), u16(w.k_proj_weight), u16(w.v_proj_weight)}, {kQS, kNKV * kD, kNKV * kD}};
     launch_rows<kEpiStore, true, 16>(kNQKV / 16, X, u16(w.input_layernorm_weight), eps, T, Dm::H, qkv, QKV, kNQKV, s);
-    hipLaunchKernelGGL(attention_fused, dim3(T, kNKV), dim3(1024), 0, s, QKV, tok, L, u16(w.q_norm_weight),
-                       u16(w.k_norm_weight), a.cos_t, a.sin_t, a.cache, eps, a.attn_scale, ATT);
+    hipLaunchKernelGGL(attention_split, dim3(T, kNKV, nsplit), dim3(kSplitWaves * 64), 0, s, QKV, tok, L,
+                       u16(w.q_norm_weight), u16(w.k_norm_weight), a.cos_t, a.sin_t, a.cache, eps, a.attn_scale,
+                       apart, ATT);
+    hipLaunchKernelGGL(attention_merge, dim3(T, kNKV), dim3(256), 0, s, tok, nsplit, apart, ATT);
     const Seg o{{u16(w.o_proj_weight), nullptr, nullptr}, {Dm::H, 0, 0}};
     launch_rows<kEpiResidual, false, 16, true>(Dm::H / 8, ATT, nullptr, eps, T, kQS, o, X, Dm::H, s);
     const Seg gu{{u16(w.gate_proj_weight), u16(w.up_proj_weight), nullptr}, {Dm::I, Dm::I, 0}};
