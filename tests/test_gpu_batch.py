@@ -359,6 +359,37 @@ def test_decode_batch_long_context_general_path(shape, exact06, weights_gpu):
     print(t)
 
 
+@pytest.mark.parametrize("c0s", [(3900,), (3000, 17), (2900, 1, 2500, 40)],
+                         ids=["batch1-32splits", "batch2-16splits", "batch4-8splits"])
+def test_decode_batch_fused_split_attention_contexts(shape, exact06, weights_gpu, c0s):
+    """The fused step's attention splits each (sequence, KV head) over S = 256 / (8 B) workgroups.
+    Injected N(0,1) caches: 2900-3900 positions give a split two or three 128-position batches
+    (its running-maximum rescale), and 1, 17 or 40 positions leave some of the S splits empty.
+    2 layers, three steps, every sequence against the exact oracle on its own cache."""
+    from qwen_megakernel.model import BatchDecoder
+    from qwen_megakernel.weights import make_kv_prefill
+
+    B, layers, max_seq = len(c0s), 2, 4096
+    bd = BatchDecoder(weights=with_rope(weights_gpu, max_seq, "cuda"), batch_size=B, max_seq_len=max_seq,
+                      num_layers=layers, verbose=False)
+    for b, c0 in enumerate(c0s):
+        k, v = make_kv_prefill(shape, c0, seed=5 + b)
+        bd.load_kv(b, k.cuda(), v.cuda(), c0)
+    feed, lgs = [[11 + 7 * b] for b in range(B)], [[] for _ in range(B)]
+    for _ in range(3):
+        nxt, logits = bd.step_logits([f[-1] for f in feed])
+        for b in range(B):
+            feed[b].append(nxt[b])
+            lgs[b].append(logits[b].cpu())
+    t = Tally(f"fused split attention, contexts {c0s}")
+    for b in range(B):
+        orc = exact_oracle(exact06, shape, max_seq, num_layers=layers)
+        ref = oracle_steps(orc, bd._k_cache[b], bd._v_cache[b], c0s[b], feed[b][:-1])
+        check_rows(t, ref, feed[b][1:], torch.stack(lgs[b]), bar=LITERAL)
+        check_kv_rows(f"fused split attention sequence {b}", orc, bd._k_cache[b], bd._v_cache[b], c0s[b], 3)
+    print(t)
+
+
 def test_decode_batch_equals_general_forward(weights_gpu):
     """The fused decode step and forward_tokens (general path) on the same inputs: logits within
     the bar of each other and the same tokens up to near-ties."""
