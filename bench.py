@@ -47,8 +47,8 @@ SiLU*mul, down, LM head + argmax) run alone over >= 1 GiB of rotating seeded
 N(0, 0.02) weight copies with N(0, 1) activations, in GB/s.
 
 Options for profiling runs: ``--phase-trace`` adds the in-kernel phase trace
-of one more step (at the last timed context) to the JSON line, for the
-Qwen3-0.6B run and for Qwen3-1.7B at batch 1;
+of one more step (at the context after the timed ones) to the JSON line, for
+the Qwen3-0.6B run, each long-context run and Qwen3-1.7B at batch 1;
 ``--copy-calibration`` first runs a plain 1 GiB device-to-device copy five
 times, so that a counter run (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE) sees a
 kernel of known traffic beside the decode kernel.
@@ -141,8 +141,10 @@ def cpu_baseline(sample_steps: int = 384):
                           f"timed at context {PROMPT_LEN + 1}..{PROMPT_LEN + sample_steps} ({dt1:.1f} s)"}}
 
 
-def long_context(w, steps: int, contexts=(8192, 32768)):
-    """Decode `steps` device-fed greedy tokens after a KV cache prefilled with N(0, 1) K/V."""
+def long_context(w, steps: int, contexts=(8192, 32768), phase_trace: bool = False):
+    """Decode `steps` device-fed greedy tokens after a KV cache prefilled with N(0, 1) K/V.
+
+    ``phase_trace``: one more step after the timed ones, with the in-kernel trace on."""
     import torch
 
     from qwen_megakernel.model import Decoder
@@ -179,6 +181,15 @@ def long_context(w, steps: int, contexts=(8192, 32768)):
                         "context": f"{c0 + 5}..{c0 + 4 + steps}", "achieved_GBps": round(byts / t / 1e9, 1),
                         "roofline_frac": round(byts / t / 1e9 / PEAK_HBM_GBS, 4)}
         log(f"long context {c0}: {1.0 / t:.1f} tok/s, {byts / t / 1e9:.0f} GB/s algorithmic")
+        if phase_trace:
+            from qwen_megakernel import trace
+
+            dec._position = c0 + 4 + steps  # the cache holds every position before it
+            stamps = trace.capture(lambda: dec.step(11), S.num_layers)
+            summ = trace.summarize(stamps, S.num_layers, split=c0 + 5 + steps <= 2048)
+            summ["context"] = c0 + 5 + steps
+            out[str(c0)]["phase_trace"] = summ
+            log(f"long-context phase trace at context {c0 + 5 + steps}:\n" + trace.format_table(summ))
     del dec, k, v
     torch.cuda.empty_cache()
     return out
@@ -496,7 +507,7 @@ def main():
     result["prefill"] = prefill_rate(w)
     result["prefill_long"] = prefill_rate(w, 2048, iters=5)
     if not args.no_long_context:
-        result["long_context"] = long_context(w, args.long_steps)
+        result["long_context"] = long_context(w, args.long_steps, phase_trace=args.phase_trace)
     del w
     torch.cuda.empty_cache()
     if not args.no_1p7b:

@@ -360,6 +360,33 @@ int qmk_decode_batch(
     int max_seq_len, int max_context, float attn_scale, void *workspace,
     size_t workspace_bytes, hipStream_t stream);
 
+/* The batched decode step of qmk_decode_batch as one persistent kernel
+ * launch: the arguments and results of qmk_decode_batch (no workspace), for
+ * 2 <= batch <= 4 and max_context <= 2048.  The 256 workgroups of the decode
+ * kernel stream each weight slice once and apply it to all `batch` rows;
+ * activations move between workgroups through the per-stream exchange area
+ * (allocated on the stream's first call).  tokens and positions must not
+ * overlap out_tokens, which receives -1 first, so a step that fails on the
+ * device (qmk_device_error) leaves -1.  Returns QMK_ERR_DEVICE where the
+ * kernel does not fit one workgroup per CU; qmk_decode_batch then keeps its
+ * multi-launch path.  No counterpart in the reference, which decodes one
+ * sequence (qwen_megakernel/model.py:111-250).  Asynchronous. */
+int qmk_decode_batch_persistent(
+    int model, int batch, const int *tokens, const int *positions, int *out_tokens,
+    float *logits_out, const void *embed_weight,
+    const LDGLayerWeights *layer_weights_host, const void *final_norm_weight,
+    const void *lm_head_weight, const void *cos_table, const void *sin_table,
+    void *k_cache, void *v_cache, long long seq_stride, int num_layers,
+    int max_seq_len, int max_context, float attn_scale, hipStream_t stream);
+
+/* Process-wide switch (default on): qmk_decode_batch runs the persistent
+ * kernel above for the shapes it covers.  Off: always the multi-launch path
+ * (for comparisons).  Returns QMK_OK. */
+int qmk_set_batch_persistent(int enable);
+
+/* 1 while qmk_decode_batch uses the persistent kernel where it applies. */
+int qmk_batch_persistent_enabled(void);
+
 /* One 16x16x32 bf16 MFMA with the operand layouts the batched GEMM assumes:
  * c[16][16] (f32) = a[16][32] . b[16][32]^T (bf16, row-major).  For tests.
  * Asynchronous; returns a status code. */

@@ -15,12 +15,14 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cstring>
 #include <map>
 #include <mutex>
 #include <utility>
 
 #include "../../include/qwen_megakernel.h"
+#include "qmk_batch_decode.h"
 #include "qmk_decode_kernel.h"
 #include "qmk_phase_bench.h"
 #include "qmk_sample.h"
@@ -33,6 +35,17 @@ using Dm = Dims<Model>;
 // One exchange area per stream serves every model.
 constexpr uint32_t kXWords = Dims<Qwen3_0_6B>::X_WORDS > Dims<Qwen3_1_7B>::X_WORDS ? Dims<Qwen3_0_6B>::X_WORDS
                                                                                     : Dims<Qwen3_1_7B>::X_WORDS;
+
+// The batched persistent kernel's exchange area (one per stream, allocated on
+// its first use) serves every (model, batch size) it runs.
+template <int B>
+constexpr uint32_t bx_words_for() {
+  return BDims<Qwen3_0_6B, B>::X_WORDS > BDims<Qwen3_1_7B, B>::X_WORDS ? BDims<Qwen3_0_6B, B>::X_WORDS
+                                                                       : BDims<Qwen3_1_7B, B>::X_WORDS;
+}
+constexpr uint32_t kBXWords = bx_words_for<4>() > bx_words_for<3>()
+                                  ? (bx_words_for<4>() > bx_words_for<2>() ? bx_words_for<4>() : bx_words_for<2>())
+                                  : (bx_words_for<3>() > bx_words_for<2>() ? bx_words_for<3>() : bx_words_for<2>());
 
 thread_local int t_status = QMK_OK;
 
@@ -76,6 +89,10 @@ struct Ctx {
   } graphs[2];                    // by attention form: [0] contexts <= kLongContext, [1] beyond
   float* logits = nullptr;        // sampled generate: the step's logits (float[vocab])
   SampleWork* swork = nullptr;    // sampled generate: the sampler's work between its launches
+  // batched persistent kernel: its own state header (epoch, error bits) and exchange area
+  DecodeState* bst = nullptr;
+  uint32_t* bx = nullptr;
+  int last_bkind = -1;            // model * 8 + batch of the last batched launch on this stream
 };
 
 struct DevInfo {
@@ -90,6 +107,7 @@ struct DevInfo {
   bool order_valid = false;
   bool order_multi = false;            // a second stream has launched on this device
   uint32_t* scratch = nullptr;         // this device's copy of `scratch` (set by qmk_init)
+  bool batch_ok = false;               // every batched persistent kernel fits one workgroup per CU
 };
 
 std::mutex g_mu;
@@ -171,6 +189,23 @@ int check_device(int dev, DevInfo** out) {
     di.ok = false;
     return QMK_ERR_DEVICE;
   }
+  // the batched persistent kernels: without room for one workgroup per CU, qmk_decode_batch keeps
+  // its multi-launch path
+  bool batch_ok = true;
+  {
+    const std::pair<const void*, int> bk[] = {
+        {reinterpret_cast<const void*>(batch_decode_kernel<Qwen3_0_6B, 2>), batch_block<2>()},
+        {reinterpret_cast<const void*>(batch_decode_kernel<Qwen3_0_6B, 3>), batch_block<3>()},
+        {reinterpret_cast<const void*>(batch_decode_kernel<Qwen3_0_6B, 4>), batch_block<4>()},
+        {reinterpret_cast<const void*>(batch_decode_kernel<Qwen3_1_7B, 2>), batch_block<2>()},
+        {reinterpret_cast<const void*>(batch_decode_kernel<Qwen3_1_7B, 3>), batch_block<3>()},
+        {reinterpret_cast<const void*>(batch_decode_kernel<Qwen3_1_7B, 4>), batch_block<4>()}};
+    for (const auto& k : bk) {
+      int ob = 0;
+      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&ob, k.first, k.second, 0) != hipSuccess) return QMK_ERR_HIP;
+      batch_ok = batch_ok && ob >= 1;
+    }
+  }
   uint32_t ticks = 100000000u;
   int khz = 0;
   if (hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev) == hipSuccess && khz > 0)
@@ -192,6 +227,7 @@ int check_device(int dev, DevInfo** out) {
   int all = 1;
   for (int i = 0; i < kNumWG; i++) all &= h_ok[i];
   di.xcd_local = all;
+  di.batch_ok = batch_ok;
   di.ticks_per_s = ticks;
   di.ok = true;
   di.checked = true;
@@ -541,6 +577,107 @@ int generate_impl(const Common& c, int first_token_id, int num_steps, int eos, i
   return fail(s != QMK_OK ? s : so);
 }
 
+// ---------------------------------------------------------------- batched persistent step
+
+std::atomic<int> g_batch_persistent{1};  // qmk_set_batch_persistent
+
+template <class M>
+int launch_batch(int batch, const BArgs& a, hipStream_t stream) {
+  switch (batch) {
+    case 2: hipLaunchKernelGGL((batch_decode_kernel<M, 2>), dim3(kNumWG), dim3(batch_block<2>()), 0, stream, a); break;
+    case 3: hipLaunchKernelGGL((batch_decode_kernel<M, 3>), dim3(kNumWG), dim3(batch_block<3>()), 0, stream, a); break;
+    default: hipLaunchKernelGGL((batch_decode_kernel<M, 4>), dim3(kNumWG), dim3(batch_block<4>()), 0, stream, a); break;
+  }
+  return hipGetLastError() == hipSuccess ? QMK_OK : QMK_ERR_HIP;
+}
+
+bool ranges_overlap(const void* a, size_t an, const void* b, size_t bn) {
+  const char* pa = static_cast<const char*>(a);
+  const char* pb = static_cast<const char*>(b);
+  return pa < pb + bn && pb < pa + an;
+}
+
+int batch_persistent_impl(int model, int batch, const int* tokens, const int* positions, int* out_tokens,
+                          float* logits_out, const void* embed_weight, const LDGLayerWeights* layer_weights_host,
+                          const void* final_norm_weight, const void* lm_head_weight, const void* cos_table,
+                          const void* sin_table, void* k_cache, void* v_cache, long long seq_stride, int num_layers,
+                          int max_seq_len, int max_context, float attn_scale, hipStream_t stream) {
+  if (model != QMK_MODEL_QWEN3_0_6B && model != QMK_MODEL_QWEN3_1_7B) return QMK_ERR_ARG;
+  if (batch < kBatchMin || batch > kBatchMax || !tokens || !positions || !out_tokens || !embed_weight ||
+      !layer_weights_host || !final_norm_weight || !lm_head_weight || !cos_table || !sin_table || !k_cache ||
+      !v_cache || num_layers < 1 || num_layers > kMaxLayers || max_seq_len < 1 || max_seq_len > kMaxSeqLen ||
+      max_context < 1 || max_context > max_seq_len || max_context > kBatchMaxContext || !(attn_scale > 0.f))
+    return QMK_ERR_ARG;
+  if (seq_stride < (long long)num_layers * Dm::NKV * max_seq_len * Dm::D) return QMK_ERR_ARG;
+  // out_tokens is written (-1) at the start of the step, before every workgroup has read tokens
+  if (ranges_overlap(tokens, batch * sizeof(int), out_tokens, batch * sizeof(int)) ||
+      ranges_overlap(positions, batch * sizeof(int), out_tokens, batch * sizeof(int)))
+    return QMK_ERR_ARG;
+  BArgs a{};
+  for (int L = 0; L < num_layers; L++) {
+    const LDGLayerWeights& w = layer_weights_host[L];
+    const void* p[11] = {w.input_layernorm_weight, w.q_proj_weight, w.k_proj_weight, w.v_proj_weight,
+                         w.q_norm_weight, w.k_norm_weight, w.o_proj_weight, w.post_attn_layernorm_weight,
+                         w.gate_proj_weight, w.up_proj_weight, w.down_proj_weight};
+    for (const void* q : p)
+      if (!q) return QMK_ERR_ARG;
+    static_assert(sizeof(LayerPtrs) == sizeof(LDGLayerWeights), "layer table layout");
+    std::memcpy(&a.layers[L], &w, sizeof(LayerPtrs));
+  }
+  Ctx* ctx = nullptr;
+  int s = get_ctx(stream, &ctx);
+  if (s != QMK_OK) return s;
+  if (!ctx->dev->batch_ok) return QMK_ERR_DEVICE;
+  if ((s = poisoned(ctx)) != QMK_OK) return s;
+  if (!ctx->bx) {
+    const size_t bytes = sizeof(DecodeState) + (size_t)kBXWords * 4;
+    void* mem = nullptr;
+    if (hipMalloc(&mem, bytes) != hipSuccess) return QMK_ERR_HIP;
+    if (hipMemset(mem, 0, bytes) != hipSuccess) {
+      hipFree(mem);
+      return QMK_ERR_HIP;
+    }
+    ctx->bst = reinterpret_cast<DecodeState*>(mem);
+    ctx->bx = reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(mem) + sizeof(DecodeState));
+  }
+  a.embed = static_cast<const uint16_t*>(embed_weight);
+  a.final_norm = static_cast<const uint16_t*>(final_norm_weight);
+  a.lm_head = static_cast<const uint16_t*>(lm_head_weight);
+  a.cos_t = static_cast<const uint16_t*>(cos_table);
+  a.sin_t = static_cast<const uint16_t*>(sin_table);
+  a.k_cache = static_cast<uint16_t*>(k_cache);
+  a.v_cache = static_cast<uint16_t*>(v_cache);
+  a.seq_stride = seq_stride;
+  a.tokens = tokens;
+  a.positions = positions;
+  a.out_tokens = out_tokens;
+  a.logits = logits_out;
+  a.st = ctx->bst;
+  a.x = ctx->bx;
+  a.host_err = ctx->host_err;
+  a.trace = ctx->trace;
+  a.num_layers = num_layers;
+  a.max_seq_len = max_seq_len;
+  a.max_context = max_context;
+  a.attn_scale = attn_scale;
+  a.rms_eps = 1e-6f;
+  a.timeout = ctx->timeout;
+  a.xcd_local = ctx->xcd_local;
+  DeviceOrder order(ctx->dev, stream);
+  if (!order.ok()) return QMK_ERR_HIP;
+  const int kind = model * 8 + batch;
+  if (ctx->last_bkind >= 0 && ctx->last_bkind != kind) {
+    // another layout's words must never be read as current: zero them and restart the tags
+    hipLaunchKernelGGL(clear_exchange_kernel, dim3(kNumWG), dim3(256), 0, stream, ctx->bst, ctx->bx, kBXWords);
+    if (hipGetLastError() != hipSuccess) return QMK_ERR_HIP;
+  }
+  ctx->last_bkind = kind;
+  s = model == QMK_MODEL_QWEN3_1_7B ? launch_batch<Qwen3_1_7B>(batch, a, stream)
+                                    : launch_batch<Qwen3_0_6B>(batch, a, stream);
+  const int so = order.finish();
+  return s != QMK_OK ? s : so;
+}
+
 size_t phase_copy_elems(int phase) {
   switch (phase) {
     case kPhaseQKV: return (size_t)(Dm::QS + 2 * Dm::NKV * Dm::D) * Dm::H;
@@ -754,9 +891,10 @@ uint32_t qmk_device_error(hipStream_t stream) {
   Ctx* ctx = nullptr;
   if (get_ctx(stream, &ctx) != QMK_OK) return 0xffffffffu;
   if (hipStreamSynchronize(stream) != hipSuccess) return 0xffffffffu;
-  uint32_t v = 0;
+  uint32_t v = 0, vb = 0;
   if (hipMemcpy(&v, &ctx->st->err, sizeof(v), hipMemcpyDeviceToHost) != hipSuccess) return 0xffffffffu;
-  return v | *ctx->host_err;
+  if (ctx->bst && hipMemcpy(&vb, &ctx->bst->err, sizeof(vb), hipMemcpyDeviceToHost) != hipSuccess) return 0xffffffffu;
+  return v | vb | *ctx->host_err;
 }
 
 int qmk_reset(hipStream_t stream) {
@@ -766,6 +904,8 @@ int qmk_reset(hipStream_t stream) {
   if (hipStreamSynchronize(stream) != hipSuccess) return fail(QMK_ERR_HIP);
   const size_t bytes = sizeof(DecodeState) + (size_t)kXWords * 4;
   if (hipMemset(ctx->st, 0, bytes) != hipSuccess) return fail(QMK_ERR_HIP);
+  if (ctx->bst && hipMemset(ctx->bst, 0, sizeof(DecodeState) + (size_t)kBXWords * 4) != hipSuccess)
+    return fail(QMK_ERR_HIP);
   *ctx->host_err = 0;
   return fail(QMK_OK);
 }
@@ -828,5 +968,24 @@ void qmk_launch_geometry(int* workgroups, int* threads) {
   if (workgroups) *workgroups = kNumWG;
   if (threads) *threads = kBlock;
 }
+
+int qmk_decode_batch_persistent(int model, int batch, const int* tokens, const int* positions, int* out_tokens,
+                                float* logits_out, const void* embed_weight, const LDGLayerWeights* layer_weights_host,
+                                const void* final_norm_weight, const void* lm_head_weight, const void* cos_table,
+                                const void* sin_table, void* k_cache, void* v_cache, long long seq_stride,
+                                int num_layers, int max_seq_len, int max_context, float attn_scale,
+                                hipStream_t stream) {
+  return fail(batch_persistent_impl(model, batch, tokens, positions, out_tokens, logits_out, embed_weight,
+                                    layer_weights_host, final_norm_weight, lm_head_weight, cos_table, sin_table,
+                                    k_cache, v_cache, seq_stride, num_layers, max_seq_len, max_context, attn_scale,
+                                    stream));
+}
+
+int qmk_set_batch_persistent(int enable) {
+  g_batch_persistent.store(enable != 0);
+  return QMK_OK;
+}
+
+int qmk_batch_persistent_enabled(void) { return g_batch_persistent.load(); }
 
 }  // extern "C"

@@ -28,6 +28,7 @@
 #include <algorithm>
 
 #include "../../include/qwen_megakernel.h"
+#include "qmk_batch_decode.h"
 #include "qmk_decode_kernel.h"
 
 namespace qmk {
@@ -1851,6 +1852,13 @@ int qmk_decode_batch(int model, int batch, const int* tokens, const int* positio
                          w.gate_proj_weight, w.up_proj_weight, w.down_proj_weight};
     for (const void* q : p)
       if (!q) return QMK_ERR_ARG;
+  }
+  if (qmk_batch_persistent_enabled() && batch >= kBatchMin && batch <= kBatchMax && max_context <= kBatchMaxContext) {
+    const int s = qmk_decode_batch_persistent(model, batch, tokens, positions, out_tokens, logits_out, embed_weight,
+                                              layer_weights_host, final_norm_weight, lm_head_weight, cos_table,
+                                              sin_table, k_cache, v_cache, seq_stride, num_layers, max_seq_len,
+                                              max_context, attn_scale, stream);
+    if (s != QMK_ERR_DEVICE) return s;
   }
   if (workspace_bytes < qmk_decode_batch_workspace_bytes(model, batch, max_context)) return QMK_ERR_ARG;
   batch::Args a{};

@@ -478,6 +478,13 @@ void decode_batch(torch::Tensor tokens, torch::Tensor positions, torch::Tensor o
   TORCH_CHECK(B >= 1 && B <= 256, "tokens must hold 1 .. 256 entries");
   TORCH_CHECK(positions.numel() == B && out_tokens.numel() == B, "positions and out_tokens must match tokens");
   TORCH_CHECK(bm.num_seqs == B, "k_cache must hold one sequence per token (", B, "), got ", bm.num_seqs);
+  const auto overlap = [](const torch::Tensor& x, const torch::Tensor& y) {
+    const char* a = static_cast<const char*>(x.data_ptr());
+    const char* b = static_cast<const char*>(y.data_ptr());
+    return a < b + y.nbytes() && b < a + x.nbytes();
+  };
+  TORCH_CHECK(!overlap(tokens, out_tokens) && !overlap(positions, out_tokens),
+              "out_tokens must not overlap tokens or positions");
   float* lg = nullptr;
   if (logits.has_value()) {
     check_cuda(*logits, "logits");
@@ -582,6 +589,14 @@ void forward_tokens(torch::Tensor tokens, torch::Tensor seq_ids, torch::Tensor p
   TORCH_CHECK(s == QMK_OK, "forward_tokens failed: ", qmk_status_string(s));
 }
 
+// decode_batch runs the batched persistent kernel where it applies (default), or always the
+// multi-launch path (qmk_set_batch_persistent); returns the previous setting.
+bool set_batch_persistent(bool enable) {
+  const bool was = qmk_batch_persistent_enabled() != 0;
+  qmk_set_batch_persistent(enable ? 1 : 0);
+  return was;
+}
+
 void selftest_mfma(torch::Tensor a, torch::Tensor b, torch::Tensor c) {
   check_bf16(a, "a", 16 * 32);
   check_bf16(b, "b", 16 * 32);
@@ -677,6 +692,7 @@ TORCH_LIBRARY(qwen_megakernel_C, ops) {
       "Tensor sin_table, Tensor k_cache, Tensor v_cache, Tensor workspace, int num_layers, int max_context, "
       "float attn_scale) -> ()");
   ops.impl("decode_batch", torch::kCUDA, &decode_batch);
+  ops.def("set_batch_persistent(bool enable) -> bool", &set_batch_persistent);
   ops.def("selftest_mfma(Tensor a, Tensor b, Tensor c) -> ()");
   ops.impl("selftest_mfma", torch::kCUDA, &selftest_mfma);
 }
