@@ -44,6 +44,52 @@ constexpr int kBatchMin = 2, kBatchMax = 4;
 constexpr int kBatchMaxContext = kGroupSize * 32 * kKvU;  // 2048: one K/V batch per wave and sequence
 constexpr uint32_t kNoChunk = 0xffffffffu;
 
+// Eight sums over the wave at once: lanes 8k..8k+7 receive the sum over all 64
+// lanes of v[k].  Each step halves the values a lane carries and adds its
+// partner's copy of the ones it keeps: the half-wave swap (lanes l, l ^ 32) and
+// the row-pair swap (l, l ^ 16) on the gfx950 permlane swaps, a rotation by 8
+// inside each 16-lane row (l, l ^ 8) on DPP; three DPP adds then sum each group
+// of eight lanes.  About 20 instructions for eight sums, against about 90 for
+// eight separate wave reductions.
+__device__ __forceinline__ float wave_sum8(const float (&v)[8], int lane) {
+  float w[4];
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[j]), __float_as_uint(v[j + 4]), false, false);
+    w[j] = __uint_as_float(r[0]) + __uint_as_float(r[1]);  // lanes 0-31: v[j], lanes 32-63: v[j + 4]
+  }
+  float z[2];
+#pragma unroll
+  for (int j = 0; j < 2; j++) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(w[j]), __float_as_uint(w[j + 2]), false, false);
+    z[j] = __uint_as_float(r[0]) + __uint_as_float(r[1]);  // even rows: w[j], odd rows: w[j + 2]
+  }
+  const bool hi = (lane & 8) != 0;
+  float x = (hi ? z[1] : z[0]) + dpp_get<0x128>(hi ? z[0] : z[1]);  // row_ror:8, i.e. lane ^ 8
+  x = dpp_add<0xB1>(x);   // quad_perm [1,0,3,2]
+  x = dpp_add<0x4E>(x);   // quad_perm [2,3,0,1]
+  x = dpp_add<0x141>(x);  // row_half_mirror: the other quad of the eight lanes
+  return x;
+}
+
+// This lane's share of a row's dot product (NL 16-byte chunks of weights and activations).
+template <int NL>
+__device__ __forceinline__ float row_part(const u32x4* w, const u32x4 (&x)[NL]) {
+  float acc = 0.f;
+#pragma unroll
+  for (int j = 0; j < NL; j++) acc = dot8(w[j], x[j], acc);
+  return acc;
+}
+
+// One 4-byte word at word index ``w``, same scopes as put4.
+__device__ __forceinline__ void put1(uint32_t* buf, uint32_t w, uint32_t v, bool device) {
+  auto rs = make_rsrc(buf, 0x7fffffffu);
+  if (device)
+    __builtin_amdgcn_raw_buffer_store_b32(v, rs, w * 4u, 0, 0x10 /* sc1 */);
+  else
+    __builtin_amdgcn_raw_buffer_store_b32(v, rs, w * 4u, 0, 0);
+}
+
 template <class M, int B>
 struct BDims {
   using D1 = Dims<M>;
@@ -52,7 +98,7 @@ struct BDims {
   static constexpr int M_WG = D1::M_WG, GU_W = D1::GU_W, ROWS_WG = D1::ROWS_WG, ROWS_W = D1::ROWS_W;
   static constexpr int OP = D1::OP, LO = D1::LO, LD = D1::LD, LM_RPW = D1::LM_RPW, NX = D1::NX;
   static constexpr int NBUF = D1::NBUF;     // the shared weight buffer of the QKV, gate/up and down phases
-  static constexpr int LMU = B * LH > 8 ? 1 : 2;  // LM-head rows per wave per batch (two batches in flight)
+  static constexpr int LMU = 2;  // LM-head rows per wave per batch (two batches in flight)
   static constexpr int CPX = ROWS_WG / 2;   // reduce-scatter: chunks per source XCD and sequence
   // exchange layout (words)
   static constexpr uint32_t X_QKV = 0;
@@ -68,7 +114,7 @@ struct BDims {
   static constexpr uint32_t X_WORDS = X_KEY + kNumWG * B * 4;
 
   static_assert(B >= kBatchMin && B <= kBatchMax, "batch size");
-  static_assert(RQ_W == 2, "one 8-byte store per wave and sequence");
+  static_assert(RQ_W * B <= 8 && LMU * B <= 8, "QKV and LM-head dots reduced eight at a time");
   static_assert((kGroups * CPX * B) % 64 == 0 && kGroups * CPX * B <= 16 * 64 && (kGroups * CPX) % 64 == 0,
                 "reduce-scatter: whole 64-chunk slots per sequence, at most 16 loads per lane");
   static_assert(kGroupSize * 4 == 128, "combine: two acc chunks per lane and sequence");
@@ -722,17 +768,23 @@ __device__ __forceinline__ void batch_compute(const BArgs& a, BSmem<M, B>& s, co
     QMK_BSYNC();  // a
     cstamp(L, 0);
     {
+      // value k = RQ_W b + row; lanes 8k.. receive its sum, lane 8k publishes it
+      float v8[8];
+#pragma unroll
+      for (int k = 0; k < 8; k++) v8[k] = 0.f;
 #pragma unroll
       for (int b = 0; b < B; b++) {
         u32x4 act[Dm::LH];
         load_act(act, s.n[b], 0, lane);
-        const float v0 = row_dot_p<Dm::LH>(w_buf, act);
-        const float v1 = row_dot_p<Dm::LH>(w_buf + Dm::LH, act);
-        if (lane == 0) {
-          const uint32_t t = make_tag(p.epoch, (uint32_t)(L * Dm::NX + 0));
-          put2(a.x, Dm::X_QKV + (xcd * B + b) * Dm::RG + Dm::RQ_WG * r + Dm::RQ_W * c, word(f32_to_bf16(v0), t),
-               word(f32_to_bf16(v1), t), !a.xcd_local);
-        }
+#pragma unroll
+        for (int i = 0; i < Dm::RQ_W; i++) v8[Dm::RQ_W * b + i] = row_part<Dm::LH>(w_buf + i * Dm::LH, act);
+      }
+      const float tot = wave_sum8(v8, lane);
+      const int k = lane >> 3;
+      if ((lane & 7) == 0 && k < Dm::RQ_W * B) {
+        const uint32_t t = make_tag(p.epoch, (uint32_t)(L * Dm::NX + 0));
+        put1(a.x, Dm::X_QKV + (xcd * B + k / Dm::RQ_W) * Dm::RG + Dm::RQ_WG * r + Dm::RQ_W * c + k % Dm::RQ_W,
+             word(f32_to_bf16(tot), t), !a.xcd_local);
       }
     }
     prefetch_o(L);
@@ -860,11 +912,16 @@ __device__ __forceinline__ void batch_compute(const BArgs& a, BSmem<M, B>& s, co
     QMK_BSYNC();  // f
     QMK_BSYNC();  // g
     cstamp(L, 6);
+    // o_proj partials: each sequence's attention chunks are read from LDS once and serve every
+    // row pass
 #pragma unroll
-    for (int op = 0; op < Dm::OP; op++) {
+    for (int b = 0; b < B; b++) {
+      u32x4 xa[Dm::LO];
 #pragma unroll
-      for (int b = 0; b < B; b++) {
-        const float v = seg_dot_p<Dm::LO>(w_o + op * Dm::LO, s.attn[b], t16);
+      for (int j = 0; j < Dm::LO; j++) xa[j] = *reinterpret_cast<const u32x4*>(s.attn[b] + 8 * (t16 + 16 * j));
+#pragma unroll
+      for (int op = 0; op < Dm::OP; op++) {
+        const float v = row16_sum(row_part<Dm::LO>(w_o + op * Dm::LO, xa));
         if (t16 == 0) {
           const uint32_t t = make_tag(p.epoch, (uint32_t)(L * Dm::NX + 4));
           put2(a.x, Dm::X_O + (uint32_t)(((xcd * kGroupSize + r) * B + b) * Dm::ROWS_WG + Dm::ROWS_W * c + 4 * op + slot) * 2,
@@ -876,14 +933,27 @@ __device__ __forceinline__ void batch_compute(const BArgs& a, BSmem<M, B>& s, co
     cstamp(L, 7);
     QMK_BSYNC();  // i
     cstamp(L, 8);
+    {
+      // sums eight at a time: value k of group g is row RPG g + k / B of sequence k % B (each
+      // group reads the activation rows from LDS again, which keeps fewer registers live)
+      constexpr int RPG = 8 / B;                        // rows per group of eight values
+      constexpr int NG = (Dm::GU_W + RPG - 1) / RPG;
 #pragma unroll
-    for (int b = 0; b < B; b++) {
-      u32x4 act[Dm::LH];
-      load_act(act, s.n[b], 0, lane);
+      for (int g = 0; g < NG; g++) {
+        float v8[8];
 #pragma unroll
-      for (int i = 0; i < Dm::GU_W; i++) {
-        const float v = row_dot_p<Dm::LH>(w_buf + i * Dm::LH, act);
-        if (lane == 0) s.out[b][gu_out + i] = bf16r(v);
+        for (int k = 0; k < 8; k++) v8[k] = 0.f;
+#pragma unroll
+        for (int b = 0; b < B; b++) {
+          u32x4 act[Dm::LH];
+          load_act(act, s.n[b], 0, lane);
+#pragma unroll
+          for (int q = 0; q < RPG; q++)
+            if (RPG * g + q < Dm::GU_W) v8[B * q + b] = row_part<Dm::LH>(w_buf + (RPG * g + q) * Dm::LH, act);
+        }
+        const float tot = wave_sum8(v8, lane);
+        const int k = lane >> 3, row = RPG * g + k / B;
+        if ((lane & 7) == 0 && k < RPG * B && row < Dm::GU_W) s.out[k % B][gu_out + row] = bf16r(tot);
       }
     }
     prefetch_dn(L);
@@ -892,10 +962,13 @@ __device__ __forceinline__ void batch_compute(const BArgs& a, BSmem<M, B>& s, co
     QMK_BSYNC();  // k
     cstamp(L, 10);
 #pragma unroll
-    for (int op = 0; op < Dm::OP; op++) {
+    for (int b = 0; b < B; b++) {
+      u32x4 xm[Dm::LD];
 #pragma unroll
-      for (int b = 0; b < B; b++) {
-        const float v = seg_dot_p<Dm::LD>(w_buf + op * Dm::LD, s.m[b], t16);
+      for (int j = 0; j < Dm::LD; j++) xm[j] = *reinterpret_cast<const u32x4*>(s.m[b] + 8 * (t16 + 16 * j));
+#pragma unroll
+      for (int op = 0; op < Dm::OP; op++) {
+        const float v = row16_sum(row_part<Dm::LD>(w_buf + op * Dm::LD, xm));
         if (t16 == 0) {
           const uint32_t t = make_tag(p.epoch, (uint32_t)(L * Dm::NX + 7));
           put2(a.x, Dm::X_D + (uint32_t)(((xcd * kGroupSize + r) * B + b) * Dm::ROWS_WG + Dm::ROWS_W * c + 4 * op + slot) * 2,
@@ -914,9 +987,12 @@ __device__ __forceinline__ void batch_compute(const BArgs& a, BSmem<M, B>& s, co
     const int row0 = wg * Dm::LM_RPW;
     const int nrows = min(Dm::V - row0, Dm::LM_RPW);
     const int nmine = (nrows - c + kComputeWaves - 1) / kComputeWaves;
-    uint64_t best[B];
-#pragma unroll
-    for (int b = 0; b < B; b++) best[b] = 0;
+    // lanes 8k.. hold value k = B u + b of every batch (row u of the batch, sequence b) after the
+    // eight-way reduction; each lane keeps the best key of its value
+    const int kv = lane >> 3;
+    const int kb = kv % B;
+    const bool kval = kv < LMU * B;
+    uint64_t best = 0;
     u32x4 bufA[LMU][Dm::LH], bufB[LMU][Dm::LH];
     auto row_of = [&](int i) { return row0 + c + kComputeWaves * i; };
     auto load_batch = [&](u32x4 (&buf)[LMU][Dm::LH], int i0) {
@@ -927,19 +1003,21 @@ __device__ __forceinline__ void batch_compute(const BArgs& a, BSmem<M, B>& s, co
       }
     };
     auto do_batch = [&](u32x4 (&buf)[LMU][Dm::LH], int i0) {
+      float v8[8];
 #pragma unroll
-      for (int u = 0; u < LMU; u++) {
+      for (int k = 0; k < 8; k++) v8[k] = 0.f;
 #pragma unroll
-        for (int b = 0; b < B; b++) {
-          const float v = row_dot(buf[u], act[b]);
-          if (i0 + u < nmine) {
-            const int row = row_of(i0 + u);
-            const uint32_t hb = f32_to_bf16(v);
-            const uint64_t key = ((uint64_t)(orderable16(hb) << 16) << 32) | (uint64_t)(0xffffffffu - (uint32_t)row);
-            best[b] = key > best[b] ? key : best[b];
-            if (a.logits && lane == 0) a.logits[(size_t)b * Dm::V + row] = bf16_to_f32(hb);
-          }
-        }
+      for (int u = 0; u < LMU; u++)
+#pragma unroll
+        for (int b = 0; b < B; b++) v8[B * u + b] = row_part<Dm::LH>(buf[u], act[b]);
+      const float tot = wave_sum8(v8, lane);
+      const int iu = i0 + kv / B;
+      if (kval && iu < nmine) {
+        const int row = row_of(iu);
+        const uint32_t hb = f32_to_bf16(tot);
+        const uint64_t key = ((uint64_t)(orderable16(hb) << 16) << 32) | (uint64_t)(0xffffffffu - (uint32_t)row);
+        best = key > best ? key : best;
+        if (a.logits && (lane & 7) == 0) a.logits[(size_t)kb * Dm::V + row] = bf16_to_f32(hb);
       }
     };
     load_batch(bufA, 0);
@@ -952,9 +1030,10 @@ __device__ __forceinline__ void batch_compute(const BArgs& a, BSmem<M, B>& s, co
       if (i + 2 * LMU < nmine) load_batch(bufA, i + 2 * LMU);
       do_batch(bufB, i + LMU);
     }
-    if (lane == 0) {
 #pragma unroll
-      for (int b = 0; b < B; b++) s.best[c][b] = best[b];
+    for (int b = 0; b < B; b++) {
+      const uint64_t kb_best = wave_max_u64(kval && kb == b ? best : 0);
+      if (lane == 0) s.best[c][b] = kb_best;
     }
   }
   QMK_BSYNC();  // final b

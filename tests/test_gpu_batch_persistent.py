@@ -47,8 +47,10 @@ def _step(bd, tokens, positions, max_context):
 def test_persistent_batch_matches_oracle_and_launch_path(shape, exact06, weights_gpu, B):
     """B sequences with prompts of different lengths, 4 layers: every persistent step against the
     oracle on the sequence's own cache (literal bar) and the K/V rows it appended; then the same
-    steps replayed through the multi-launch path from the same cache and tokens, whose logits must
-    agree with the persistent kernel's within the same bar."""
+    steps replayed through the multi-launch path from the same cache and tokens, checked against
+    the oracle on its own cache the same way, and its logits within cosine 0.999 / max abs 0.1 of
+    the persistent kernel's (the two round the softmax probabilities differently, so their greedy
+    tokens are each held to the oracle, not to each other)."""
     from qwen_megakernel.model import BatchDecoder
     from qwen_megakernel.weights import make_prompt
 
@@ -77,13 +79,23 @@ def test_persistent_batch_matches_oracle_and_launch_path(shape, exact06, weights
     kp = bd._k_cache.clone()
     bd._k_cache.copy_(k0)
     bd._v_cache.copy_(v0)
-    t2 = Tally(f"persistent vs multi-launch batch {B}")
+    out_l, lg_l = [[] for _ in range(B)], [[] for _ in range(B)]
     with persistent(False):
         for i in range(steps):
             pos = [start[b] + i for b in range(B)]
-            _, lg = _step(bd, [feed[b][i] for b in range(B)], pos, max(pos) + 1)
+            nxt, lg = _step(bd, [feed[b][i] for b in range(B)], pos, max(pos) + 1)
             for b in range(B):
-                check_rows(t2, lg[b:b + 1], [feed[b][i + 1]], lgs[b][i][None], bar=LITERAL)
+                out_l[b].append(nxt[b])
+                lg_l[b].append(lg[b])
+    t2 = Tally(f"multi-launch replay, batch {B}")
+    for b in range(B):
+        orc = exact_oracle(exact06, shape, max_seq, num_layers=layers)
+        ref = oracle_steps(orc, bd._k_cache[b], bd._v_cache[b], start[b], feed[b][:-1])
+        check_rows(t2, ref, out_l[b], torch.stack(lg_l[b]), bar=LITERAL)
+        for i in range(steps):
+            x, y = lgs[b][i].double(), lg_l[b][i].double()
+            assert torch.nn.functional.cosine_similarity(x, y, dim=0).item() >= 0.999
+            assert (x - y).abs().max().item() <= 0.1
     d = (kp[:, 0].float() - bd._k_cache[:, 0].float()).abs().max().item()
     assert d <= 0.0625, d
     print(t2)
