@@ -895,15 +895,26 @@ __device__ __forceinline__ void batch_compute(const BArgs& a, BSmem<M, B>& s, co
           }
         }
       }
+      // the wave's four 16-lane rows summed for all 16 values at once: a half-wave swap halves
+      // the values each lane carries, a row-pair swap halves them again; lane (t16, row) then
+      // holds values 4 (row & 1) + j of head row >> 1, dims 8 t16 + 4 (row & 1) + j
+      static_assert(Dm::GQ == 2, "16 accumulators per lane");
+      float w8[8];
 #pragma unroll
-      for (int h = 0; h < Dm::GQ; h++) {
-#pragma unroll
-        for (int i = 0; i < 8; i++) acc[h][i] = rows_sum4(acc[h][i]);
-        if (lane < 16) {
-#pragma unroll
-          for (int i = 0; i < 8; i++) s.wacc[c][b][h][8 * t16 + i] = acc[h][i];
-        }
+      for (int j = 0; j < 8; j++) {
+        const auto r2 = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[0][j]), __float_as_uint(acc[1][j]),
+                                                         false, false);
+        w8[j] = __uint_as_float(r2[0]) + __uint_as_float(r2[1]);  // lanes 0-31: head 0, 32-63: head 1
       }
+      float4 z;
+      float* zf = reinterpret_cast<float*>(&z);
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const auto r2 = __builtin_amdgcn_permlane16_swap(__float_as_uint(w8[j]), __float_as_uint(w8[j + 4]), false,
+                                                         false);
+        zf[j] = __uint_as_float(r2[0]) + __uint_as_float(r2[1]);  // even rows: dims j, odd rows: dims j + 4
+      }
+      *reinterpret_cast<float4*>(&s.wacc[c][b][lane >> 5][8 * t16 + 4 * ((lane >> 4) & 1)]) = z;
     }
     // every K/V item has landed (the last wait was vmcnt(0)); saying so lets the compiler drop the
     // vmcnt(0) it would otherwise put before the next workgroup barriers
