@@ -200,8 +200,9 @@ def qwen3_1p7b(steps: int = 256, prompt_len: int = 512, batch: int = 4, phase_tr
 
     Batch 1: a `prompt_len`-token prompt prefilled, then `steps` device-fed steps of the decode
     megakernel.  Batch `batch`: `batch` sequences, each with its own `prompt_len`-token prompt
-    (seeds 1..batch), all prefilled together in one batched forward, then `steps` device-fed batched steps
-    (one MFMA forward over `batch` tokens per step; context 513..768 per sequence).
+    (seeds 1..batch), all prefilled together in one batched forward, then `steps` device-fed batched
+    steps (context 513..768 per sequence): one launch of the batched persistent kernel per step,
+    and for comparison the same steps on the multi-launch batched step (``multi_launch``).
     """
     import torch
 
@@ -253,28 +254,56 @@ def qwen3_1p7b(steps: int = 256, prompt_len: int = 512, batch: int = 4, phase_tr
     prefill_s = time.perf_counter() - tp
     first_t = torch.tensor(first, dtype=torch.int32, device="cuda")
     start_pos = bd.positions
-    bd.decode_steps(first_t, 4)  # warm-up (contexts 513..516), then rewind to the prefilled state
-    bd._positions = list(start_pos)
-    torch.cuda.synchronize()
-    e0.record(stream)
-    log_t = bd.decode_steps(first_t, steps)
-    e1.record(stream)
-    torch.cuda.synchronize()
-    assert int(log_t.min()) >= 0
-    tb = e0.elapsed_time(e1) / 1e3 / steps  # seconds per batched step
+
+    def timed_steps():
+        bd.decode_steps(first_t, 4)  # warm-up (contexts 513..516), then rewind to the prefilled state
+        bd._positions = list(start_pos)
+        torch.cuda.synchronize()
+        e0.record(stream)
+        log_t = bd.decode_steps(first_t, steps)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        assert int(log_t.min()) >= 0 and int(ops.device_error()) == 0
+        bd._positions = list(start_pos)
+        return e0.elapsed_time(e1) / 1e3 / steps, log_t  # seconds per batched step
+
+    was = ops.set_batch_persistent(False)
+    try:
+        tm, _ = timed_steps()
+    finally:
+        ops.set_batch_persistent(was)
+    tb, log_p = timed_steps()
+    batch_trace = None
+    if phase_trace:
+        from qwen_megakernel import trace
+
+        bd._positions = [p + steps for p in start_pos]
+        nxt = [int(t) for t in log_p[-1].tolist()]
+        stamps = trace.capture(lambda: bd.step(nxt), S.num_layers)
+        batch_trace = trace.summarize(stamps, S.num_layers)
+        batch_trace["context"] = prompt_len + steps + 1
+        log(f"qwen3-1.7b batch {batch} phase trace (control wave of sequence 0) at context {prompt_len + steps + 1}:\n"
+            + trace.format_table(batch_trace))
     # per step: the weights once, each sequence's KV read over its context plus its new K/V row
     byts_b = S.weight_bytes_per_token() + batch * S.kv_bytes_per_position() * (mean_c + 1)
     del bd, w
     torch.cuda.empty_cache()
-    log(f"qwen3-1.7b batch {batch}: {batch / tb:.1f} tok/s ({tb * 1e3:.3f} ms/step), "
-        f"{byts_b / tb / 1e9:.0f} GB/s algorithmic; prefill {batch} x {prompt_len} tokens in one forward {prefill_s * 1e3:.1f} ms")
+    log(f"qwen3-1.7b batch {batch}: {batch / tb:.1f} tok/s ({tb * 1e3:.3f} ms/step; multi-launch path "
+        f"{tm * 1e3:.3f} ms/step), {byts_b / tb / 1e9:.0f} GB/s algorithmic; prefill {batch} x {prompt_len} tokens "
+        f"in one forward {prefill_s * 1e3:.1f} ms")
     out["batch4"] = {"tok_per_s": round(batch / tb, 2), "ms_per_step": round(tb * 1e3, 4), "batch": batch,
                      "steps": steps, "context": f"{prompt_len + 1}..{prompt_len + steps} per sequence",
                      "bytes_per_step": int(byts_b), "achieved_GBps": round(byts_b / tb / 1e9, 1),
                      "roofline_frac": round(byts_b / tb / 1e9 / PEAK_HBM_GBS, 4),
                      "prefill_ms": round(prefill_s * 1e3, 2),
-                     "path": "decode_batch: 6 launches per layer (norm-prologue / residual- and SiLU-epilogue "
-                             "K-split MFMA GEMMs, split-K attention over all CUs and its merge), streamed LM head"}
+                     "path": "decode_batch: one launch of the batched persistent kernel per step (256 workgroups of "
+                             "one control wave per sequence and 8 compute waves, tagged-word exchanges, HF's "
+                             "two-pass attention per sequence, LM head and argmax in the same launch)",
+                     "multi_launch": {"tok_per_s": round(batch / tm, 2), "ms_per_step": round(tm * 1e3, 4),
+                                      "path": "6 launches per layer (K-split MFMA GEMMs, split-K attention over "
+                                              "all CUs and its merge), streamed LM head"}}
+    if batch_trace is not None:
+        out["batch4"]["phase_trace"] = batch_trace
     return out
 
 
