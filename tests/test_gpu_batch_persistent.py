@@ -245,3 +245,29 @@ def test_persistent_batch_generate_28_layers(shape, exact06, weights_gpu):
         ref = stream_rows(exact_oracle(exact06, shape, 2048), bd._k_cache[b], bd._v_cache[b], prompts[b], out[b])
         check_rows(t, ref, out[b], bar=LAYERS28)
     print(t)
+
+
+def test_persistent_batch_long_stream_across_tag_wraps(weights_gpu):
+    """600 device-fed batched steps on the 28-layer model at batch 2 (the 16-bit exchange tags
+    advance by 253 per step and wrap about twice), on two streams: a fresh one and one whose
+    batched state was first advanced by 37 steps, so the two meet every wrap at different steps.
+    No device error, and the two token streams are identical."""
+    from qwen_megakernel.model import BatchDecoder
+    from qwen_megakernel.weights import make_prompt
+
+    prompts = [make_prompt(9, V, seed=120), make_prompt(4, V, seed=121)]
+    ops = _ops()
+    logs = []
+    for i, st in enumerate((torch.cuda.Stream(), torch.cuda.Stream())):
+        with torch.cuda.stream(st), persistent(True):
+            ops.reset()
+            if i == 1:
+                warm = BatchDecoder(weights=weights_gpu, batch_size=2, max_seq_len=64, verbose=False)
+                warm.decode_steps(_i32([1, 2]), 37)
+            bd = BatchDecoder(weights=weights_gpu, batch_size=2, max_seq_len=1024, verbose=False)
+            first = bd.prefill_all(prompts)
+            log = bd.decode_steps(_i32(first), 600).cpu()
+            assert int(ops.device_error()) == 0
+        assert int(log.min()) >= 0 and int(log.max()) < V
+        logs.append(log)
+    assert torch.equal(logs[0], logs[1])
