@@ -127,6 +127,40 @@ def test_long_context_parity(shape, exact06, weights_gpu, c0, layers, steps):
     check_kv_rows(f"context {c0} x {layers} layers", orc, dec._k_cache, dec._v_cache, c0, len(feed))
 
 
+@pytest.mark.parametrize("c0", [8192, 32768], ids=["8192", "32768"])
+def test_long_context_256_step_stream(shape, exact06, weights_gpu, c0):
+    """The long-context workload's full length: 256 device-fed greedy steps (generate_nosync, the
+    long-form kernel) after an injected N(0,1) cache of c0 positions, 28 layers.  No device error;
+    rows 0, 63, 127, 191 and 255 of the stream are decoded again for their logits (each step
+    rewrites only its own K/V row, with the same values) and checked against the exact oracle on
+    the kernel's own cache and tokens, at the deep bar."""
+    from qwen_megakernel.weights import make_kv_prefill
+
+    steps, max_seq = 256, c0 + 272
+    ops = torch.ops.qwen_megakernel_C
+    k, v = make_kv_prefill(shape, c0, seed=2)
+    dec = decoder(with_rope(weights_gpu, max_seq, "cuda"), max_seq_len=max_seq)
+    dec.load_kv(k.cuda(), v.cuda(), c0)
+    out = ops.generate_nosync(11, steps, *dec._scratch(), shape.num_layers, c0, max_seq, dec._attn_scale).cpu().tolist()
+    assert int(ops.device_error()) == 0
+    assert all(0 <= t < shape.vocab for t in out)
+    feed = [11] + out[:-1]  # the input of step i; out[i] follows it
+    rows = [0, 63, 127, 191, 255]
+    lgs = []
+    for i in rows:
+        dec._position = c0 + i
+        tok, lg = dec.step_logits(feed[i])
+        assert tok == out[i], f"step {i}: the repeated step gave {tok}, the stream {out[i]}"
+        lgs.append(lg.cpu())
+    del k, v
+    orc = exact_oracle(exact06, shape, max_seq)
+    t = Tally(f"context {c0}, 256-step stream, rows {rows}")
+    for j, i in enumerate(rows):
+        ref = oracle_steps(orc, dec._k_cache, dec._v_cache, c0 + i, [feed[i]])
+        check_rows(t, ref, [out[i]], lgs[j][None], labels=[i], bar=DEEP)
+    print(t)
+
+
 def test_generate_across_long_context_boundary(shape, weights_gpu):
     """generate_nosync from position 1990 for 100 steps runs contexts 1991..2090: the loop switches
     from the short-context kernel to the long-context one after context 2048, each form with its

@@ -133,3 +133,60 @@ def test_qwen3_1p7b_generate_matches_steps(w17):
     for _ in range(23):
         toks_b.append(b.step(toks_b[-1]))
     assert toks_a == toks_b
+
+
+def test_qwen3_1p7b_256_step_streams_batch1_and_batch4(w17, exact17):
+    """The Qwen3-1.7B workload's full length: 256 device-fed greedy steps after 512-token prompts,
+    at batch 1 (the decode megakernel, generate_nosync) and at batch 4 (BatchDecoder.decode_steps,
+    the batched persistent kernel), 28 layers.  No device error; rows 0, 85, 170 and 255 of every
+    stream are decoded again for their logits (each step rewrites only its own K/V rows, with the
+    same values) and checked against the exact oracle on the decoder's own cache and tokens, at
+    the deep bar."""
+    from qwen_megakernel.model import BatchDecoder
+    from qwen_megakernel.shapes import QWEN3_1_7B as S
+    from qwen_megakernel.weights import make_prompt
+
+    _, wg = w17
+    ops = torch.ops.qwen_megakernel_C
+    steps, max_seq, rows = 256, 1024, [0, 85, 170, 255]
+    t = Tally("qwen3-1.7b 256-step streams, rows " + str(rows))
+
+    # batch 1
+    prompt = make_prompt(512, S.vocab, seed=1)
+    dec = decoder(wg, max_seq_len=max_seq)
+    dec.prefill(prompt[:-1])
+    p0 = dec.position
+    out = ops.generate_nosync(prompt[-1], steps, *dec._scratch(), S.num_layers, p0, max_seq,
+                              dec._attn_scale).cpu().tolist()
+    assert int(ops.device_error()) == 0
+    feed = [prompt[-1]] + out[:-1]
+    orc = exact_oracle(exact17, S, max_seq)
+    for i in rows:
+        dec._position = p0 + i
+        tok, lg = dec.step_logits(feed[i])
+        assert tok == out[i]
+        ref = oracle_steps(orc, dec._k_cache, dec._v_cache, p0 + i, [feed[i]])
+        check_rows(t, ref, [out[i]], lg.cpu()[None], labels=[f"batch 1 step {i}"], bar=DEEP)
+    del dec
+
+    # batch 4
+    B = 4
+    prompts = [make_prompt(512, S.vocab, seed=1 + b) for b in range(B)]
+    bd = BatchDecoder(weights=wg, batch_size=B, max_seq_len=max_seq, verbose=False)
+    first = bd.prefill_all(prompts)
+    start = bd.positions
+    log = bd.decode_steps(torch.tensor(first, dtype=torch.int32, device="cuda"), steps).cpu()
+    assert int(ops.device_error()) == 0 and int(log.min()) >= 0
+    for i in rows:
+        toks = log[i].tolist()  # the inputs of step i; log[i + 1] follows them
+        out_t = torch.empty(B, dtype=torch.int32, device="cuda")
+        lg = torch.empty(B, S.vocab, dtype=torch.float32, device="cuda")
+        pos = [p + i for p in start]
+        bd._forward.decode(torch.tensor(toks, dtype=torch.int32, device="cuda"),
+                           torch.tensor(pos, dtype=torch.int32, device="cuda"), out_t, lg, bd._k_cache, bd._v_cache,
+                           max(pos) + 1)
+        assert out_t.cpu().tolist() == log[i + 1].tolist()
+        for b in range(B):
+            ref = oracle_steps(orc, bd._k_cache[b], bd._v_cache[b], pos[b], [toks[b]])
+            check_rows(t, ref, [int(log[i + 1][b])], lg[b].cpu()[None], labels=[f"batch 4 seq {b} step {i}"], bar=DEEP)
+    print(t)
