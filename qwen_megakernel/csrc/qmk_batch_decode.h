@@ -818,6 +818,13 @@ __device__ __forceinline__ void batch_compute(const BArgs& a, BSmem<M, B>& s, co
         const u32x4 k_now = *reinterpret_cast<const u32x4*>(s.k[b] + 8 * t16);
 #pragma unroll
         for (int u = 0; u < U; u++) {
+          // a row group past the workgroup's range (u = 1 for every wave at contexts up to 1024)
+          // is skipped with a wave-uniform branch
+          if (base0 + 32 * u >= p.p_end[b]) {
+#pragma unroll
+            for (int h = 0; h < Dm::GQ; h++) sc[b][u][h] = -INFINITY;
+            continue;
+          }
           const int pp = base0 + 32 * u + slot;
           const u32x4 kx = pp == p.pos[b] ? k_now : s.kv[b][c][u][lane];
 #pragma unroll
@@ -881,6 +888,7 @@ __device__ __forceinline__ void batch_compute(const BArgs& a, BSmem<M, B>& s, co
         }
 #pragma unroll
         for (int u = 0; u < U; u++) {
+          if (base0 + 32 * u >= p.p_end[b]) continue;  // wave-uniform, as in pass 1
           const int pp = base0 + 32 * u + slot;
           const u32x4 vx = pp == p.pos[b] ? v_now : s.kv[b][c][u][lane];
           const float vf[8] = {lo_bf16(vx.x), hi_bf16(vx.x), lo_bf16(vx.y), hi_bf16(vx.y),
