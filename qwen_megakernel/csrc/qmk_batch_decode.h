@@ -953,26 +953,33 @@ __device__ __forceinline__ void batch_compute(const BArgs& a, BSmem<M, B>& s, co
     QMK_BSYNC();  // i
     cstamp(L, 8);
     {
-      // sums eight at a time: value k of group g is row RPG g + k / B of sequence k % B (each
-      // group reads the activation rows from LDS again, which keeps fewer registers live)
-      constexpr int RPG = 8 / B;                        // rows per group of eight values
+      // Sequences in passes of SB, their activation rows read from LDS once and held in registers;
+      // the partial dots of a pass are summed eight at a time: value k of group g is row
+      // RPG g + k / SB of sequence b0 + k % SB.
+      constexpr int SB = B > 2 ? 2 : B;
+      constexpr int RPG = 8 / SB;
       constexpr int NG = (Dm::GU_W + RPG - 1) / RPG;
 #pragma unroll
-      for (int g = 0; g < NG; g++) {
-        float v8[8];
+      for (int b0 = 0; b0 < B; b0 += SB) {
+        u32x4 act[SB][Dm::LH];
 #pragma unroll
-        for (int k = 0; k < 8; k++) v8[k] = 0.f;
+        for (int j = 0; j < SB; j++)
+          if (b0 + j < B) load_act(act[j], s.n[b0 + j], 0, lane);
 #pragma unroll
-        for (int b = 0; b < B; b++) {
-          u32x4 act[Dm::LH];
-          load_act(act, s.n[b], 0, lane);
+        for (int g = 0; g < NG; g++) {
+          float v8[8];
+#pragma unroll
+          for (int k = 0; k < 8; k++) v8[k] = 0.f;
 #pragma unroll
           for (int q = 0; q < RPG; q++)
-            if (RPG * g + q < Dm::GU_W) v8[B * q + b] = row_part<Dm::LH>(w_buf + (RPG * g + q) * Dm::LH, act);
+#pragma unroll
+            for (int j = 0; j < SB; j++)
+              if (RPG * g + q < Dm::GU_W && b0 + j < B)
+                v8[SB * q + j] = row_part<Dm::LH>(w_buf + (RPG * g + q) * Dm::LH, act[j]);
+          const float tot = wave_sum8(v8, lane);
+          const int k = lane >> 3, row = RPG * g + k / SB, bj = b0 + k % SB;
+          if ((lane & 7) == 0 && k < RPG * SB && row < Dm::GU_W && bj < B) s.out[bj][gu_out + row] = bf16r(tot);
         }
-        const float tot = wave_sum8(v8, lane);
-        const int k = lane >> 3, row = RPG * g + k / B;
-        if ((lane & 7) == 0 && k < RPG * B && row < Dm::GU_W) s.out[k % B][gu_out + row] = bf16r(tot);
       }
     }
     prefetch_dn(L);
