@@ -169,7 +169,53 @@ struct BSmem {
   uint64_t best[kComputeWaves][B];
   LayerPtrs layers[kMaxLayers];
   int abort_flag;
+  // attention hand-offs inside the workgroup, per sequence, counting up through the launch (so no
+  // reset is needed): compute waves that published their (max, sum) (8 per layer), layers whose
+  // global (max, sum) is in ml (set by the sequence's control wave), compute waves that published
+  // their P@V partial (8 per layer)
+  int sig_scores[B];
+  int sig_ml[B];
+  int sig_pv[B];
 };
+
+// In-workgroup signals between waves through LDS.  A wave's LDS operations complete in order, so
+// waiting for lgkmcnt(0) before the signal makes every LDS write the wave issued before it visible
+// to a wave that has seen the signal.  They are written as inline assembly: as LDS atomics the
+// compiler would put a vmcnt(0) before each of them (it cannot tell them from the K/V ring that
+// the wave's LDS-DMA loads are filling), which would stall the wave on every K/V batch in flight.
+__device__ __forceinline__ uint32_t lds_addr(const int* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) int*)p;
+}
+__device__ __forceinline__ void lds_signal_add(int* p) {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\tds_add_u32 %0, %1" ::"v"(lds_addr(p)), "v"(1) : "memory");
+}
+__device__ __forceinline__ void lds_signal_set(int* p, int v) {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\tds_write_b32 %0, %1" ::"v"(lds_addr(p)), "v"(v) : "memory");
+}
+// A 16-byte LDS store the compiler does not hold back behind the K/V ring's loads (see above); a
+// later lds_signal_add orders it before the signal.
+__device__ __forceinline__ void lds_store16(float* p, float4 v) {
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+  const f32x4 x = {v.x, v.y, v.z, v.w};
+  asm volatile("ds_write_b128 %0, %1" ::"v"((uint32_t)(uintptr_t)(__attribute__((address_space(3))) float*)p), "v"(x)
+               : "memory");
+}
+__device__ __forceinline__ int lds_read_now(const int* p) {
+  int v;
+  asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(lds_addr(p)) : "memory");
+  return __builtin_amdgcn_readfirstlane(v);
+}
+// Waits until *p >= v.  Returns false when the workgroup has aborted or the wait exceeded
+// ``timeout`` ticks of the wall clock (the caller then records the failure).
+__device__ __forceinline__ bool lds_wait_ge(int* p, int v, int* abort_flag, uint32_t timeout) {
+  const uint64_t t0 = wall_clock64();
+  while (lds_read_now(p) < v) {
+    if (lds_read_now(abort_flag)) return false;
+    if (wall_clock64() - t0 > timeout) return false;
+    __builtin_amdgcn_s_sleep(1);
+  }
+  return true;
+}
 
 template <int B>
 struct BStep {
@@ -504,9 +550,11 @@ __device__ __forceinline__ void batch_control(const BArgs& a, BSmem<M, B>& s, co
     }
     stamp(tp + 3);
     QMK_BSYNC();  // c
-    QMK_BSYNC();  // d
+    // the compute waves' (max, sum) of this sequence (they score the sequences in order, so the
+    // exchange of an early sequence overlaps the scores of the later ones)
+    if (!lds_wait_ge(&s.sig_scores[sb], kComputeWaves * (L + 1), &s.abort_flag, a.timeout)) ctl.fail(kErrTimeout);
     stamp(tp + 4);
-    // ------------------------------------------------------------ d..e  softmax max and sum
+    // ------------------------------------------------------------ softmax max and sum
     {
       const uint32_t t = tag_of(L, 1);
       // lanes 0..GQ-1 merge the eight waves' (max, sum) of head h = lane and publish them
@@ -545,10 +593,11 @@ __device__ __forceinline__ void batch_control(const BArgs& a, BSmem<M, B>& s, co
           s.ml[sb][lane][1] = lsum;
         }
       }
+      // set even after a failed exchange, so no compute wave waits for it (the abort flag is set)
+      if (lane == 0) lds_signal_set(&s.sig_ml[sb], L + 1);
     }
     stamp(tp + 5);
-    QMK_BSYNC();  // e
-    QMK_BSYNC();  // f
+    if (!lds_wait_ge(&s.sig_pv[sb], kComputeWaves * (L + 1), &s.abort_flag, a.timeout)) ctl.fail(kErrTimeout);
     stamp(tp + 6);
     // ------------------------------------------------------------ f..g  P@V partials, combine, attn
     {
@@ -699,14 +748,15 @@ __device__ __forceinline__ void batch_compute(const BArgs& a, BSmem<M, B>& s, co
                                               int lane) {
   using Dm = BDims<M, B>;
   const int xcd = wg & (kGroups - 1), r = wg >> 3;
-  const int slot = lane >> 4, t16 = lane & 15;
   const size_t kv_layer_stride = (size_t)Dm::NKV * a.max_seq_len * Dm::D;
   constexpr int U = kKvU;
 
   u32x4 w_buf[Dm::NBUF];         // QKV, gate/up and down slices, one phase ahead
   u32x4 w_o[Dm::OP * Dm::LO];    // o_proj slice, requested after QKV and kept through attention
 
-  auto rs_row = [&](int pass) { return Dm::ROWS_WG * r + Dm::ROWS_W * c + 4 * pass + slot; };
+  // the lambdas read ``lane`` itself, which is laundered per layer, so their lane-derived addresses
+  // are not hoisted out of the layer loop
+  auto rs_row = [&](int pass) { return Dm::ROWS_WG * r + Dm::ROWS_W * c + 4 * pass + (lane >> 4); };
   const bool gu_up = c >= kComputeWaves / 2;
   const int gu_i = (gu_up ? c - kComputeWaves / 2 : c) * Dm::GU_W;
   const int gu_m0 = Dm::MS * xcd + Dm::M_WG * r + gu_i;
@@ -725,7 +775,7 @@ __device__ __forceinline__ void batch_compute(const BArgs& a, BSmem<M, B>& s, co
     const uint16_t* wo_base = uniform_ptr(s.layers[layer].wo);
 #pragma unroll
     for (int op = 0; op < Dm::OP; op++)
-      load_seg_p<Dm::LO>(w_o + op * Dm::LO, wo_base + (size_t)rs_row(op) * Dm::QS + Dm::OC * xcd, t16);
+      load_seg_p<Dm::LO>(w_o + op * Dm::LO, wo_base + (size_t)rs_row(op) * Dm::QS + Dm::OC * xcd, lane & 15);
   };
   auto prefetch_gu = [&](int layer) {
     const uint16_t* base = uniform_ptr(gu_up ? s.layers[layer].wu : s.layers[layer].wg);
@@ -737,7 +787,7 @@ __device__ __forceinline__ void batch_compute(const BArgs& a, BSmem<M, B>& s, co
     const uint16_t* wd_base = uniform_ptr(s.layers[layer].wd);
 #pragma unroll
     for (int op = 0; op < Dm::OP; op++)
-      load_seg_p<Dm::LD>(w_buf + op * Dm::LD, wd_base + (size_t)rs_row(op) * Dm::I + Dm::MS * xcd, t16);
+      load_seg_p<Dm::LD>(w_buf + op * Dm::LD, wd_base + (size_t)rs_row(op) * Dm::I + Dm::MS * xcd, lane & 15);
   };
 
   uint64_t* ctrace = a.trace ? a.trace + (size_t)(a.num_layers * kTracePoints + 3) * kNumWG : nullptr;
@@ -803,7 +853,9 @@ __device__ __forceinline__ void batch_compute(const BArgs& a, BSmem<M, B>& s, co
     float sc[B][U][Dm::GQ];
 #pragma unroll
     for (int b = 0; b < B; b++) {
-      wait_vmcnt(U * (B - b - 1));  // sequence b's keys; the later sequences' may stay in flight
+      // sequence b's keys; the later sequences' keys and the earlier sequences' V rows, issued
+      // after them, may stay in flight
+      wait_vmcnt(U * (B - 1));
       const int base0 = p.p_begin[b] + 4 * c;
       float m_w[Dm::GQ], l_w[Dm::GQ];
 #pragma unroll
@@ -858,20 +910,25 @@ __device__ __forceinline__ void batch_compute(const BArgs& a, BSmem<M, B>& s, co
           s.wml[c][b][h][0] = m_w[h];
           s.wml[c][b][h][1] = l_w[h];
         }
+        lds_signal_add(&s.sig_scores[b]);
       }
+      // sequence b's V rows replace its keys in this wave's slots of ring stage b (this wave's
+      // reads of them are done: the signal waited for them, and lgkmcnt(0) covers every lane)
+      __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+      issue_kv(b, true);
     }
-    // every key batch has landed (the last wait was vmcnt(0))
-    wait_vmcnt(0);
     cstamp(L, 3);
-    QMK_BSYNC();  // d
-    // the V rows replace the keys in the ring (every wave's reads of them are done)
-#pragma unroll
-    for (int b = 0; b < B; b++) issue_kv(b, true);
-    QMK_BSYNC();  // e
-    cstamp(L, 4);
+    auto fail_here = [&]() {
+      atomicOr(&a.st->err, kErrTimeout);
+      if (a.host_err) __hip_atomic_store(a.host_err, kErrTimeout, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+      s.abort_flag = 1;
+    };
 #pragma unroll
     for (int b = 0; b < B; b++) {
-      wait_vmcnt(U * (B - b - 1));  // sequence b's V rows
+      // the sequence's global (max, sum), then its V rows (the later sequences' may stay in flight)
+      if (!lds_wait_ge(&s.sig_ml[b], L + 1, &s.abort_flag, a.timeout) && !lds_read_now(&s.abort_flag)) fail_here();
+      if (b == 0) cstamp(L, 4);
+      wait_vmcnt(U * (B - b - 1));
       const int base0 = p.p_begin[b] + 4 * c;
       float acc[Dm::GQ][8];
 #pragma unroll
@@ -922,13 +979,13 @@ __device__ __forceinline__ void batch_compute(const BArgs& a, BSmem<M, B>& s, co
                                                          false);
         zf[j] = __uint_as_float(r2[0]) + __uint_as_float(r2[1]);  // even rows: dims j, odd rows: dims j + 4
       }
-      *reinterpret_cast<float4*>(&s.wacc[c][b][lane >> 5][8 * t16 + 4 * ((lane >> 4) & 1)]) = z;
+      lds_store16(&s.wacc[c][b][lane >> 5][8 * t16 + 4 * ((lane >> 4) & 1)], z);
+      if (lane == 0) lds_signal_add(&s.sig_pv[b]);
     }
     // every K/V item has landed (the last wait was vmcnt(0)); saying so lets the compiler drop the
-    // vmcnt(0) it would otherwise put before the next workgroup barriers
+    // vmcnt(0) it would otherwise put before the next workgroup barrier
     wait_vmcnt(0);
     cstamp(L, 5);
-    QMK_BSYNC();  // f
     QMK_BSYNC();  // g
     cstamp(L, 6);
     // o_proj partials: each sequence's attention chunks are read from LDS once and serve every
@@ -1084,6 +1141,11 @@ __global__ void __launch_bounds__(batch_block<B>(), 1) batch_decode_kernel(BArgs
     for (int i = threadIdx.x; i < n; i += batch_block<B>()) dst[i] = src[i];
   }
   if (threadIdx.x == 0) s.abort_flag = __hip_atomic_load(&a.st->err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
+  if ((int)threadIdx.x < B) {
+    s.sig_scores[threadIdx.x] = 0;
+    s.sig_ml[threadIdx.x] = 0;
+    s.sig_pv[threadIdx.x] = 0;
+  }
   __syncthreads();
   if (s.abort_flag) return;
   BStep<B> p;
