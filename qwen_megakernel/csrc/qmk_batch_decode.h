@@ -777,10 +777,10 @@ __device__ __forceinline__ void batch_compute(const BArgs& a, BSmem<M, B>& s, co
     for (int op = 0; op < Dm::OP; op++)
       load_seg_p<Dm::LO>(w_o + op * Dm::LO, wo_base + (size_t)rs_row(op) * Dm::QS + Dm::OC * xcd, lane & 15);
   };
-  auto prefetch_gu = [&](int layer) {
+  auto prefetch_gu = [&](int layer, int i0, int i1) {
     const uint16_t* base = uniform_ptr(gu_up ? s.layers[layer].wu : s.layers[layer].wg);
 #pragma unroll
-    for (int i = 0; i < Dm::GU_W; i++)
+    for (int i = i0; i < i1; i++)
       load_row_p<Dm::LH>(w_buf + i * Dm::LH, base + (size_t)(gu_m0 + i) * Dm::H, lane);
   };
   auto prefetch_dn = [&](int layer) {
@@ -985,6 +985,9 @@ __device__ __forceinline__ void batch_compute(const BArgs& a, BSmem<M, B>& s, co
     // every K/V item has landed (the last wait was vmcnt(0)); saying so lets the compiler drop the
     // vmcnt(0) it would otherwise put before the next workgroup barrier
     wait_vmcnt(0);
+    // half of the gate/up slice now, half after o_proj: the first half drains during the
+    // attention-output exchanges, and the polls of the o reduce-scatter queue behind only the second
+    prefetch_gu(L, 0, Dm::GU_W / 2);
     cstamp(L, 5);
     QMK_BSYNC();  // g
     cstamp(L, 6);
@@ -1005,7 +1008,7 @@ __device__ __forceinline__ void batch_compute(const BArgs& a, BSmem<M, B>& s, co
         }
       }
     }
-    prefetch_gu(L);
+    prefetch_gu(L, Dm::GU_W / 2, Dm::GU_W);
     cstamp(L, 7);
     QMK_BSYNC();  // i
     cstamp(L, 8);
