@@ -86,7 +86,7 @@ struct Ctx {
     int model = -1;
     bool sampled = false;
     SampleParams sp{};
-  } graphs[2];                    // by attention form: [0] contexts <= kLongContext, [1] beyond
+  } graphs[3];                    // by attention form (form_of): short, long, deep
   float* logits = nullptr;        // sampled generate: the step's logits (float[vocab])
   SampleWork* swork = nullptr;    // sampled generate: the sampler's work between its launches
   // batched persistent kernel: its own state header (epoch, error bits) and exchange area
@@ -174,7 +174,7 @@ int check_device(int dev, DevInfo** out) {
   hipDeviceProp_t prop;
   if (hipGetDeviceProperties(&prop, dev) != hipSuccess) return QMK_ERR_HIP;
   int occ = 0, occ17 = 0;
-  int occl = 0, occl17 = 0;
+  int occl = 0, occl17 = 0, occd = 0, occd17 = 0;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, reinterpret_cast<const void*>(decode_kernel<Qwen3_0_6B, false>), kBlock,
                                                    0) != hipSuccess ||
       hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ17, reinterpret_cast<const void*>(decode_kernel<Qwen3_1_7B, false>), kBlock,
@@ -182,9 +182,14 @@ int check_device(int dev, DevInfo** out) {
       hipOccupancyMaxActiveBlocksPerMultiprocessor(
           &occl, reinterpret_cast<const void*>(decode_kernel<Qwen3_0_6B, false, true>), kBlock, 0) != hipSuccess ||
       hipOccupancyMaxActiveBlocksPerMultiprocessor(
-          &occl17, reinterpret_cast<const void*>(decode_kernel<Qwen3_1_7B, false, true>), kBlock, 0) != hipSuccess)
+          &occl17, reinterpret_cast<const void*>(decode_kernel<Qwen3_1_7B, false, true>), kBlock, 0) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(
+          &occd, reinterpret_cast<const void*>(decode_kernel_deep<Qwen3_0_6B, false>), kBlock, 0) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(
+          &occd17, reinterpret_cast<const void*>(decode_kernel_deep<Qwen3_1_7B, false>), kBlock, 0) != hipSuccess)
     return QMK_ERR_HIP;
-  if (prop.multiProcessorCount < kNumWG || occ < 1 || occ17 < 1 || occl < 1 || occl17 < 1) {
+  if (prop.multiProcessorCount < kNumWG || occ < 1 || occ17 < 1 || occl < 1 || occl17 < 1 || occd < 1 ||
+      occd17 < 1) {
     di.checked = true;
     di.ok = false;
     return QMK_ERR_DEVICE;
@@ -418,21 +423,30 @@ KArgs make_args(const Common& c, Ctx* ctx) {
   return a;
 }
 
-template <class M, bool LONG>
-void launch_model(const KArgs& a, hipStream_t stream) {
-  if (a.temperature > 0.f) hipLaunchKernelGGL((decode_kernel<M, true, LONG>), dim3(kNumWG), dim3(kBlock), 0, stream, a);
-  else hipLaunchKernelGGL((decode_kernel<M, false, LONG>), dim3(kNumWG), dim3(kBlock), 0, stream, a);
+// The attention form of a step at context `ctx` (positions 0..ctx-1): 0 up to kLongContext,
+// 1 up to kDeepContext, 2 beyond.
+int form_of(long long ctx) { return ctx > kDeepContext ? 2 : ctx > kLongContext ? 1 : 0; }
+
+template <class M>
+void launch_model(const KArgs& a, int form, hipStream_t stream) {
+  const bool t = a.temperature > 0.f;
+  const dim3 g(kNumWG), k(kBlock);
+  if (form == 2) {
+    if (t) hipLaunchKernelGGL((decode_kernel_deep<M, true>), g, k, 0, stream, a);
+    else hipLaunchKernelGGL((decode_kernel_deep<M, false>), g, k, 0, stream, a);
+  } else if (form == 1) {
+    if (t) hipLaunchKernelGGL((decode_kernel<M, true, true>), g, k, 0, stream, a);
+    else hipLaunchKernelGGL((decode_kernel<M, false, true>), g, k, 0, stream, a);
+  } else {
+    if (t) hipLaunchKernelGGL((decode_kernel<M, true, false>), g, k, 0, stream, a);
+    else hipLaunchKernelGGL((decode_kernel<M, false, false>), g, k, 0, stream, a);
+  }
 }
 
-// One decode launch; long_ctx: the step's context exceeds kLongContext.
-int launch(const KArgs& a, int model, bool long_ctx, hipStream_t stream) {
-  if (model == QMK_MODEL_QWEN3_1_7B) {
-    if (long_ctx) launch_model<Qwen3_1_7B, true>(a, stream);
-    else launch_model<Qwen3_1_7B, false>(a, stream);
-  } else {
-    if (long_ctx) launch_model<Qwen3_0_6B, true>(a, stream);
-    else launch_model<Qwen3_0_6B, false>(a, stream);
-  }
+// One decode launch in attention form `form` (form_of the step's context).
+int launch(const KArgs& a, int model, int form, hipStream_t stream) {
+  if (model == QMK_MODEL_QWEN3_1_7B) launch_model<Qwen3_1_7B>(a, form, stream);
+  else launch_model<Qwen3_0_6B>(a, form, stream);
   return hipGetLastError() == hipSuccess ? QMK_OK : QMK_ERR_HIP;
 }
 
@@ -460,16 +474,16 @@ int decode_impl(const Common& c, int token, int position, int* out_token, float*
     a.position = position;
     a.token = token;
   }
-  s = launch(a, c.model, position + 1 > kLongContext, stream);
+  s = launch(a, c.model, form_of(position + 1), stream);
   const int so = order.finish();
   return fail(s != QMK_OK ? s : so);
 }
 
 // One step of the generate loop: the decode launch, and with sampling the
 // sampler that replaces its greedy token.
-int launch_step(const KArgs& a, int model, const SampleParams* sp, SampleWork* sw, bool long_ctx,
+int launch_step(const KArgs& a, int model, const SampleParams* sp, SampleWork* sw, int form,
                 hipStream_t stream) {
-  int s = launch(a, model, long_ctx, stream);
+  int s = launch(a, model, form, stream);
   if (s == QMK_OK && sp) s = launch_sample_state(a.logits, Dims<Qwen3_0_6B>::V, *sp, a.st, a.out_log, sw, stream);
   return s;
 }
@@ -477,9 +491,9 @@ int launch_step(const KArgs& a, int model, const SampleParams* sp, SampleWork* s
 // The instantiated graph of kGraphSteps steps with arguments `a` (and `sp`) in
 // one attention form, recorded again when the arguments, the model or the
 // sampling change.
-int graph_for(Ctx* ctx, const KArgs& a, int model, const SampleParams* sp, bool long_ctx, hipGraphExec_t* out) {
+int graph_for(Ctx* ctx, const KArgs& a, int model, const SampleParams* sp, int form, hipGraphExec_t* out) {
   const bool sampled = sp != nullptr;
-  Ctx::Graph& gr = ctx->graphs[long_ctx ? 1 : 0];
+  Ctx::Graph& gr = ctx->graphs[form];
   if (gr.exec && gr.model == model && std::memcmp(&gr.args, &a, sizeof(KArgs)) == 0 && gr.sampled == sampled &&
       (!sampled || std::memcmp(&gr.sp, sp, sizeof(SampleParams)) == 0)) {
     *out = gr.exec;
@@ -492,7 +506,7 @@ int graph_for(Ctx* ctx, const KArgs& a, int model, const SampleParams* sp, bool 
   if (!ctx->cap && hipStreamCreateWithFlags(&ctx->cap, hipStreamNonBlocking) != hipSuccess) return QMK_ERR_HIP;
   if (hipStreamBeginCapture(ctx->cap, hipStreamCaptureModeThreadLocal) != hipSuccess) return QMK_ERR_HIP;
   int s = QMK_OK;
-  for (int i = 0; i < kGraphSteps && s == QMK_OK; i++) s = launch_step(a, model, sp, ctx->swork, long_ctx, ctx->cap);
+  for (int i = 0; i < kGraphSteps && s == QMK_OK; i++) s = launch_step(a, model, sp, ctx->swork, form, ctx->cap);
   hipGraph_t g = nullptr;
   const hipError_t e = hipStreamEndCapture(ctx->cap, &g);
   if (s != QMK_OK || e != hipSuccess || !g) {
@@ -518,21 +532,22 @@ int generate_steps(Ctx* ctx, const Common& c, const KArgs& a, int first_token_id
   int s = QMK_OK;
   hipLaunchKernelGGL(set_step_kernel, dim3(1), dim3(1), 0, stream, ctx->st, start_position, first_token_id,
                      eos < 0 ? -1 : eos);
-  // Step i runs at context start_position + i + 1.  The steps up to context
-  // kLongContext take the short-context kernel, the rest the long-context one;
-  // each run of steps replays its form's graph, with direct launches for the remainder.
+  // Step i runs at context start_position + i + 1, in the attention form of that context
+  // (form_of); each run of steps in one form replays that form's graph, with direct launches for
+  // the remainder.
   for (int done = 0; done < num_steps;) {
     const long long ctx0 = (long long)start_position + done + 1;
-    const bool lg = ctx0 > kLongContext;
+    const int form = form_of(ctx0);
     int run = num_steps - done;
-    if (!lg) run = (int)std::min<long long>(run, kLongContext - ctx0 + 1);
+    if (form == 0) run = (int)std::min<long long>(run, kLongContext - ctx0 + 1);
+    if (form == 1) run = (int)std::min<long long>(run, kDeepContext - ctx0 + 1);
     hipGraphExec_t g = nullptr;
-    if (ctx->use_graphs && run >= kGraphSteps && graph_for(ctx, a, c.model, sp, lg, &g) == QMK_OK) {
+    if (ctx->use_graphs && run >= kGraphSteps && graph_for(ctx, a, c.model, sp, form, &g) == QMK_OK) {
       for (; run >= kGraphSteps; run -= kGraphSteps, done += kGraphSteps)
         if (hipGraphLaunch(g, stream) != hipSuccess) return QMK_ERR_HIP;
     }
     for (; run > 0; run--, done++)
-      if ((s = launch_step(a, c.model, sp, ctx->swork, lg, stream)) != QMK_OK) return s;
+      if ((s = launch_step(a, c.model, sp, ctx->swork, form, stream)) != QMK_OK) return s;
   }
   if (hipMemcpyAsync(output_log, ctx->log, (size_t)num_steps * sizeof(int), hipMemcpyDeviceToDevice, stream) !=
       hipSuccess)
@@ -865,7 +880,7 @@ int qmk_decode_model_noalloc(int model, int input_token_id, int* output_token_id
   if (!order.ok()) return fail(QMK_ERR_HIP);
   hipLaunchKernelGGL(noalloc_prepare_kernel, dim3(1), dim3(256), 0, stream, view.st, view.x, kXWords,
                      (uint32_t)model + 1u);
-  s = hipGetLastError() == hipSuccess ? launch(a, model, position + 1 > kLongContext, stream) : QMK_ERR_HIP;
+  s = hipGetLastError() == hipSuccess ? launch(a, model, form_of(position + 1), stream) : QMK_ERR_HIP;
   const int so = order.finish();
   return fail(s != QMK_OK ? s : so);
 }

@@ -80,6 +80,7 @@ constexpr int kMaxLayers = 28;
 constexpr int kKvU = 2;        // attention: each wave covers 4 positions (16-lane rows) x kKvU per batch
 constexpr int kKvStages = 4;   // K/V batches in flight per wave (LDS ring)
 constexpr int kLongContext = 2048;  // contexts above this run decode_kernel<M, S, true>
+constexpr int kDeepContext = 12288; // contexts above this run decode_kernel_deep<M, S>
 
 template <class M>
 struct Dims {
@@ -901,8 +902,11 @@ __device__ __forceinline__ void control_path(const KArgs& a, Smem<M>& s, const S
 }
 
 // LONG: the long-context attention form; sw and pw are this wave's rows of
-// SmemLong::sw and SmemLong::pw, unused otherwise.
-template <class M, bool SAMPLED, bool LONG>
+// SmemLong::sw and SmemLong::pw, unused otherwise.  DEEP (with LONG): the ring's
+// first K batches are all requested before barrier c and its first V batches at
+// barrier d, so that a wave streaming many batches starts both passes with the
+// ring full.
+template <class M, bool SAMPLED, bool LONG, bool DEEP = false>
 __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const Step& p, int b, int c, int lane,
                                              [[maybe_unused]] float* sw, [[maybe_unused]] uint32_t* pw) {
   using Dm = Dims<M>;
@@ -1047,7 +1051,11 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
     // fills after the barrier, behind the first batch's compute.  (Requested
     // right after barrier a instead, batch 0 measured slower: 1,946 against
     // 1,960 tok/s.)
-    if (nb > 0) kv_issue(kc, 0);
+    if constexpr (DEEP) {
+      for (int j = 0; j < min(nb, kKvStages); j++) kv_issue(kc, j);
+    } else {
+      if (nb > 0) kv_issue(kc, 0);
+    }
     if constexpr (SPLIT) {
       QMK_SYNC();  // c
       cstamp(L, 2);
@@ -1138,7 +1146,8 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
       }
     } else {
       QMK_SYNC();  // c
-      for (int j = 1; j < min(nb, kKvStages); j++) kv_issue(kc, j);
+      if constexpr (!DEEP)
+        for (int j = 1; j < min(nb, kKvStages); j++) kv_issue(kc, j);
       cstamp(L, 2);
       // ------------------------------------------------ scores and local (max, sum)
       // position of entry i of this wave's batches (i = 8 batch + 4 u + slot)
@@ -1287,9 +1296,15 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
       }
       cstamp(L, 3);
       QMK_SYNC();  // d
-      if (nb > 0) kv_issue(vc, 0);
-      QMK_SYNC();  // e
-      for (int j = 1; j < min(nb, kKvStages); j++) kv_issue(vc, j);
+      if constexpr (DEEP) {
+        // the V batches stream while the control wave exchanges (max, sum)
+        for (int j = 0; j < min(nb, kKvStages); j++) kv_issue(vc, j);
+        QMK_SYNC();  // e
+      } else {
+        if (nb > 0) kv_issue(vc, 0);
+        QMK_SYNC();  // e
+        for (int j = 1; j < min(nb, kKvStages); j++) kv_issue(vc, j);
+      }
       cstamp(L, 4);
       // ------------------------------------------------ probabilities and P@V
       if constexpr (LONG)
@@ -1520,10 +1535,9 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
 // softmax term computed once per position, P@V on bf16 pairs).  Both forms are
 // exact for every context; the host picks by the step's context, because the
 // long form, compiled into the same kernel, slows the short-context exchanges.
-template <class M, bool SAMPLED = false, bool LONG = false>
-__global__ void __launch_bounds__(kBlock, 1) decode_kernel(KArgs a) {
+template <class M, bool SAMPLED, bool LONG, bool DEEP, class S>
+__device__ __forceinline__ void decode_body(const KArgs& a, S& s) {
   using Dm = Dims<M>;
-  __shared__ std::conditional_t<LONG, SmemLong<M>, Smem<M>> s;
   const int b = blockIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar branches on the role
   const int lane = threadIdx.x & 63;
@@ -1584,10 +1598,25 @@ __global__ void __launch_bounds__(kBlock, 1) decode_kernel(KArgs a) {
   if (wave == 0) {
     control_path<M, !LONG && !Dm::kStream>(a, s, p, b, lane);
   } else if constexpr (LONG) {
-    compute_path<M, SAMPLED, true>(a, s, p, b, wave - 1, lane, s.sw[wave - 1], s.pw[wave - 1]);
+    compute_path<M, SAMPLED, true, DEEP>(a, s, p, b, wave - 1, lane, s.sw[wave - 1], s.pw[wave - 1]);
   } else {
     compute_path<M, SAMPLED, false>(a, s, p, b, wave - 1, lane, nullptr, nullptr);
   }
+}
+
+template <class M, bool SAMPLED = false, bool LONG = false>
+__global__ void __launch_bounds__(kBlock, 1) decode_kernel(KArgs a) {
+  __shared__ std::conditional_t<LONG, SmemLong<M>, Smem<M>> s;
+  decode_body<M, SAMPLED, LONG, false>(a, s);
+}
+
+// The long form for contexts beyond kDeepContext, where each wave streams more K/V batches than
+// the ring holds: both passes start with the ring full (DEEP).  Below that context, the ring's
+// extra requests delay the q/k/v and (max, sum) exchanges by more than they save.
+template <class M, bool SAMPLED = false>
+__global__ void __launch_bounds__(kBlock, 1) decode_kernel_deep(KArgs a) {
+  __shared__ SmemLong<M> s;
+  decode_body<M, SAMPLED, true, true>(a, s);
 }
 
 #undef QMK_SYNC

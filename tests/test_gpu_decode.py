@@ -105,14 +105,17 @@ def test_bench_workload_256_steps_with_logits(shape, exact06, weights_gpu, bench
 
 @pytest.mark.parametrize(
     "c0,layers,steps",
-    [(1500, 4, 6), (1500, 28, 8), (2100, 4, 6), (2100, 28, 8), (8192, 4, 4), (8192, 28, 16), (32768, 28, 8)],
+    [(1500, 4, 6), (1500, 28, 8), (2100, 4, 6), (2100, 28, 8), (8192, 4, 4), (8192, 28, 16), (12300, 4, 4),
+     (32768, 28, 8)],
     ids=["1500-4layers", "1500-28layers", "2100-4layers", "2100-28layers", "8192-4layers", "8192-28layers",
-         "32768-28layers"])
+         "12300-4layers", "32768-28layers"])
 def test_long_context_parity(shape, exact06, weights_gpu, c0, layers, steps):
     """Attention over an injected N(0,1) cache of c0 positions (split-K over the 32 workgroups of
     an XCD; above 2048 positions the long-context kernel runs, each wave streaming several K/V
-    batches through the LDS ring; at 2100 wave 0 has a second, partial batch).  Every step
-    against the exact oracle on the step's own inputs, and the K/V rows the kernel appended."""
+    batches through the LDS ring; at 2100 wave 0 has a second, partial batch; above 12288 the
+    deep form, which starts both passes with the ring full; at 12300 the waves have 7 and 6
+    batches).  Every step against the exact oracle on the step's own inputs, and the K/V rows the
+    kernel appended."""
     from qwen_megakernel.weights import make_kv_prefill
 
     max_seq = c0 + 64
@@ -161,15 +164,18 @@ def test_long_context_256_step_stream(shape, exact06, weights_gpu, c0):
     print(t)
 
 
-def test_generate_across_long_context_boundary(shape, weights_gpu):
+@pytest.mark.parametrize("c0", [1990, 12248], ids=["short-long", "long-deep"])
+def test_generate_across_long_context_boundary(shape, weights_gpu, c0):
     """generate_nosync from position 1990 for 100 steps runs contexts 1991..2090: the loop switches
     from the short-context kernel to the long-context one after context 2048, each form with its
-    own recorded graph.  Its tokens equal those of 100 per-step launches, which pick the kernel by
-    the same rule, with graph replay and with direct launches."""
+    own recorded graph (from 12248, contexts 12249..12348: from the long form to the deep one after
+    context 12288).  Its tokens equal those of 100 per-step launches, which pick the kernel by the
+    same rule, with graph replay and with direct launches."""
     from qwen_megakernel.build import get_extension
     from qwen_megakernel.weights import make_kv_prefill
 
-    c0, n, max_seq = 1990, 100, 2200
+    n = 100
+    max_seq = c0 + 210
     wg = with_rope(weights_gpu, max_seq, "cuda")
     k, v = make_kv_prefill(shape, c0, seed=3)
 
