@@ -176,6 +176,7 @@ struct BSmem {
   int sig_scores[B];
   int sig_ml[B];
   int sig_pv[B];
+  int sig_attn[B];  // layers whose attention output is in attn (set by the sequence's control wave)
 };
 
 // In-workgroup signals between waves through LDS.  A wave's LDS operations complete in order, so
@@ -653,8 +654,9 @@ __device__ __forceinline__ void batch_control(const BArgs& a, BSmem<M, B>& s, co
         });
       }
     }
+    // set even after a failed exchange, so no compute wave waits for it (the abort flag is set)
+    if (lane == 0) lds_signal_set(&s.sig_attn[sb], L + 1);
     stamp(tp + 7);
-    QMK_BSYNC();  // g
     stamp(tp + 8);
     // ------------------------------------------------------------ g..i  o reduce-scatter, h', norm
     {
@@ -989,12 +991,12 @@ __device__ __forceinline__ void batch_compute(const BArgs& a, BSmem<M, B>& s, co
     // attention-output exchanges, and the polls of the o reduce-scatter queue behind only the second
     prefetch_gu(L, 0, Dm::GU_W / 2);
     cstamp(L, 5);
-    QMK_BSYNC();  // g
-    cstamp(L, 6);
-    // o_proj partials: each sequence's attention chunks are read from LDS once and serve every
-    // row pass
+    // o_proj partials, each sequence's as soon as its attention output is in LDS: its chunks are
+    // read from LDS once and serve every row pass
 #pragma unroll
     for (int b = 0; b < B; b++) {
+      if (!lds_wait_ge(&s.sig_attn[b], L + 1, &s.abort_flag, a.timeout) && !lds_read_now(&s.abort_flag)) fail_here();
+      if (b == 0) cstamp(L, 6);
       u32x4 xa[Dm::LO];
 #pragma unroll
       for (int j = 0; j < Dm::LO; j++) xa[j] = *reinterpret_cast<const u32x4*>(s.attn[b] + 8 * (t16 + 16 * j));
@@ -1148,6 +1150,7 @@ __global__ void __launch_bounds__(batch_block<B>(), 1) batch_decode_kernel(BArgs
     s.sig_scores[threadIdx.x] = 0;
     s.sig_ml[threadIdx.x] = 0;
     s.sig_pv[threadIdx.x] = 0;
+    s.sig_attn[threadIdx.x] = 0;
   }
   __syncthreads();
   if (s.abort_flag) return;
