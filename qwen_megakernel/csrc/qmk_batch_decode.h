@@ -177,6 +177,8 @@ struct BSmem {
   int sig_ml[B];
   int sig_pv[B];
   int sig_attn[B];  // layers whose attention output is in attn (set by the sequence's control wave)
+  int sig_n2[B];    // layers whose post-attention normed row is in n (set by the control wave)
+  int sig_gu[B];    // compute waves that wrote the sequence's gate/up outputs to out (8 per layer)
 };
 
 // In-workgroup signals between waves through LDS.  A wave's LDS operations complete in order, so
@@ -664,10 +666,12 @@ __device__ __forceinline__ void batch_control(const BArgs& a, BSmem<M, B>& s, co
       if (ctl.reduce_rows(Dm::X_O, tag_of(L, 4), Dm::X_H2, tag_of(L, 5), xcd, r, sb) &&
           ctl.template gather_seq<Dm::H>(Dm::X_H2 + xcd * B * Dm::H, sb, tag_of(L, 5), to_n))
         ctl.rmsnorm_inplace(n, nw_post);
+      // set even after a failed exchange, so no compute wave waits for it (the abort flag is set)
+      if (lane == 0) lds_signal_set(&s.sig_n2[sb], L + 1);
     }
     stamp(tp + 9);
-    QMK_BSYNC();  // i
-    QMK_BSYNC();  // j
+    // the sequence's gate/up outputs (the compute waves take the sequences in pairs)
+    if (!lds_wait_ge(&s.sig_gu[sb], kComputeWaves * (L + 1), &s.abort_flag, a.timeout)) ctl.fail(kErrTimeout);
     stamp(tp + 10);
     // ------------------------------------------------------------ j..k  m
     {
@@ -1012,8 +1016,6 @@ __device__ __forceinline__ void batch_compute(const BArgs& a, BSmem<M, B>& s, co
     }
     prefetch_gu(L, Dm::GU_W / 2, Dm::GU_W);
     cstamp(L, 7);
-    QMK_BSYNC();  // i
-    cstamp(L, 8);
     {
       // Sequences in passes of SB, their activation rows read from LDS once and held in registers;
       // the partial dots of a pass are summed eight at a time: value k of group g is row
@@ -1023,6 +1025,13 @@ __device__ __forceinline__ void batch_compute(const BArgs& a, BSmem<M, B>& s, co
       constexpr int NG = (Dm::GU_W + RPG - 1) / RPG;
 #pragma unroll
       for (int b0 = 0; b0 < B; b0 += SB) {
+        // the pass's post-attention normed rows
+#pragma unroll
+        for (int j = 0; j < SB; j++)
+          if (b0 + j < B && !lds_wait_ge(&s.sig_n2[b0 + j], L + 1, &s.abort_flag, a.timeout) &&
+              !lds_read_now(&s.abort_flag))
+            fail_here();
+        if (b0 == 0) cstamp(L, 8);
         u32x4 act[SB][Dm::LH];
 #pragma unroll
         for (int j = 0; j < SB; j++)
@@ -1042,11 +1051,15 @@ __device__ __forceinline__ void batch_compute(const BArgs& a, BSmem<M, B>& s, co
           const int k = lane >> 3, row = RPG * g + k / SB, bj = b0 + k % SB;
           if ((lane & 7) == 0 && k < RPG * SB && row < Dm::GU_W && bj < B) s.out[bj][gu_out + row] = bf16r(tot);
         }
+        if (lane == 0) {
+#pragma unroll
+          for (int j = 0; j < SB; j++)
+            if (b0 + j < B) lds_signal_add(&s.sig_gu[b0 + j]);
+        }
       }
     }
     prefetch_dn(L);
     cstamp(L, 9);
-    QMK_BSYNC();  // j
     QMK_BSYNC();  // k
     cstamp(L, 10);
 #pragma unroll
@@ -1151,6 +1164,8 @@ __global__ void __launch_bounds__(batch_block<B>(), 1) batch_decode_kernel(BArgs
     s.sig_ml[threadIdx.x] = 0;
     s.sig_pv[threadIdx.x] = 0;
     s.sig_attn[threadIdx.x] = 0;
+    s.sig_n2[threadIdx.x] = 0;
+    s.sig_gu[threadIdx.x] = 0;
   }
   __syncthreads();
   if (s.abort_flag) return;
