@@ -179,6 +179,7 @@ struct BSmem {
   int sig_attn[B];  // layers whose attention output is in attn (set by the sequence's control wave)
   int sig_n2[B];    // layers whose post-attention normed row is in n (set by the control wave)
   int sig_gu[B];    // compute waves that wrote the sequence's gate/up outputs to out (8 per layer)
+  int sig_m[B];     // layers whose SiLU(gate)*up row is in m (set by the control wave)
 };
 
 // In-workgroup signals between waves through LDS.  A wave's LDS operations complete in order, so
@@ -694,9 +695,10 @@ __device__ __forceinline__ void batch_control(const BArgs& a, BSmem<M, B>& s, co
         d[0] = (v.x >> 16) | (v.y & 0xffff0000u);
         d[1] = (v.z >> 16) | (v.w & 0xffff0000u);
       });
+      // set even after a failed exchange, so no compute wave waits for it (the abort flag is set)
+      if (lane == 0) lds_signal_set(&s.sig_m[sb], L + 1);
     }
     stamp(tp + 11);
-    QMK_BSYNC();  // k
     stamp(tp + 12);
     // ------------------------------------------------------------ k..a'  d reduce-scatter, h''
     ctl.reduce_rows(Dm::X_D, tag_of(L, 7), Dm::X_H, tag_of(L, 8), xcd, r, sb);
@@ -1060,10 +1062,11 @@ __device__ __forceinline__ void batch_compute(const BArgs& a, BSmem<M, B>& s, co
     }
     prefetch_dn(L);
     cstamp(L, 9);
-    QMK_BSYNC();  // k
-    cstamp(L, 10);
+    // down_proj partials, each sequence's as soon as its m row is in LDS
 #pragma unroll
     for (int b = 0; b < B; b++) {
+      if (!lds_wait_ge(&s.sig_m[b], L + 1, &s.abort_flag, a.timeout) && !lds_read_now(&s.abort_flag)) fail_here();
+      if (b == 0) cstamp(L, 10);
       u32x4 xm[Dm::LD];
 #pragma unroll
       for (int j = 0; j < Dm::LD; j++) xm[j] = *reinterpret_cast<const u32x4*>(s.m[b] + 8 * (t16 + 16 * j));
@@ -1166,6 +1169,7 @@ __global__ void __launch_bounds__(batch_block<B>(), 1) batch_decode_kernel(BArgs
     s.sig_attn[threadIdx.x] = 0;
     s.sig_n2[threadIdx.x] = 0;
     s.sig_gu[threadIdx.x] = 0;
+    s.sig_m[threadIdx.x] = 0;
   }
   __syncthreads();
   if (s.abort_flag) return;
