@@ -46,8 +46,8 @@ HIP_FLAGS = [
     f"-I{_INCLUDE}",
 ]
 
-_LIB_SOURCES = ["qmk_api.hip", "qmk_batch.hip", "qmk_sample.hip", "qmk_decode_kernel.h", "qmk_device.h",
-                "qmk_state.h", "qmk_phase_bench.h", "qmk_sample.h"]
+_LIB_SOURCES = ["qmk_api.hip", "qmk_batch.hip", "qmk_sample.hip", "qmk_decode_kernel.h", "qmk_batch_decode.h",
+                "qmk_device.h", "qmk_state.h", "qmk_phase_bench.h", "qmk_sample.h"]
 _LIB_UNITS = ["qmk_api.hip", "qmk_batch.hip", "qmk_sample.hip"]
 _OPS_SOURCES = ["torch_bindings.cpp"]
 

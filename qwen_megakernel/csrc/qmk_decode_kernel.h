@@ -377,13 +377,13 @@ struct Ctl {
     }
     ss = wave_sum(ss);
     const float rstd = rcp_sqrt_torch(__fdiv_rn(ss, (float)Dm::H) + a.rms_eps);
+    // two elements per conversion: bf16(x * rstd), then bf16(w * that)
 #pragma unroll
     for (int i = 0; i < P; i++) {
       const int pi = lane + 64 * i;
       const uint32_t wp = nw.w[i];
-      const float n0 = bf16r(lo_bf16(wp) * bf16r(xv[i].x * rstd));
-      const float n1 = bf16r(hi_bf16(wp) * bf16r(xv[i].y * rstd));
-      reinterpret_cast<uint32_t*>(s.n)[pi] = f32_to_bf16(n0) | (f32_to_bf16(n1) << 16);
+      const uint32_t xn = pack_bf16x2(xv[i].x * rstd, xv[i].y * rstd);
+      reinterpret_cast<uint32_t*>(s.n)[pi] = pack_bf16x2(lo_bf16(wp) * lo_bf16(xn), hi_bf16(wp) * hi_bf16(xn));
     }
   }
 
@@ -407,13 +407,16 @@ struct Ctl {
     const float x0 = s.qkv[src_off + lane], x1 = s.qkv[src_off + lane + 64];
     const float ss = wave_sum(x0 * x0 + x1 * x1);
     const float rstd = rcp_sqrt_torch(__fdiv_rn(ss, (float)Dm::D) + a.rms_eps);
-    const float n0 = bf16r(hw.w0 * bf16r(x0 * rstd));
-    const float n1 = bf16r(hw.w1 * bf16r(x1 * rstd));
-    // x*cos + rotate_half(x)*sin with rotate_half(x) = (-x[64:], x[:64])
-    const float y0 = bf16r(bf16r(n0 * hw.c0) + bf16r(-n1 * hw.s0));
-    const float y1 = bf16r(bf16r(n1 * hw.c1) + bf16r(n0 * hw.s1));
-    dst[lane] = (uint16_t)f32_to_bf16(y0);
-    dst[lane + 64] = (uint16_t)f32_to_bf16(y1);
+    // the lane's two elements share each bf16 conversion
+    const uint32_t xn = pack_bf16x2(x0 * rstd, x1 * rstd);
+    const uint32_t nn = pack_bf16x2(hw.w0 * lo_bf16(xn), hw.w1 * hi_bf16(xn));
+    const float n0 = lo_bf16(nn), n1 = hi_bf16(nn);
+    // x*cos + rotate_half(x)*sin with rotate_half(x) = (-x[64:], x[:64]), each product rounded
+    const uint32_t pc = pack_bf16x2(n0 * hw.c0, n1 * hw.c1);
+    const uint32_t ps = pack_bf16x2(-n1 * hw.s0, n0 * hw.s1);
+    const uint32_t y = pack_bf16x2(lo_bf16(pc) + lo_bf16(ps), hi_bf16(pc) + hi_bf16(ps));
+    dst[lane] = (uint16_t)(y & 0xffffu);
+    dst[lane + 64] = (uint16_t)(y >> 16);
   }
 
   // Reduce-scatter across XCDs: sums the eight XCD partials of this rank's
@@ -454,9 +457,9 @@ struct Ctl {
     }
     if (lane < CPX) {
       const int row = R * r + 2 * lane;
-      const float h0 = bf16r(res[row] + bf16r(sum0));
-      const float h1 = bf16r(res[row + 1] + bf16r(sum1));
-      const uint32_t hb0 = f32_to_bf16(h0), hb1 = f32_to_bf16(h1);
+      const uint32_t sb = pack_bf16x2(sum0, sum1);
+      const uint32_t hb = pack_bf16x2(res[row] + lo_bf16(sb), res[row + 1] + hi_bf16(sb));
+      const uint32_t hb0 = hb & 0xffffu, hb1 = hb >> 16;
       // two words per lane: pairs of lanes form one 16-byte store
       const uint32_t ob0 = __shfl_xor(hb0, 1), ob1 = __shfl_xor(hb1, 1);
       if ((lane & 1) == 0) {
@@ -818,18 +821,17 @@ __device__ __forceinline__ void control_path(const KArgs& a, Smem<M>& s, const S
     stamp(tp + 10);
     // ------------------------------------------------------------ j..k  m
     {
-      if (lane < Dm::M_WG / 4) {
-        float mv[4];
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-          const float gt = s.out[4 * lane + q];
-          const float up = s.out[Dm::M_WG + 4 * lane + q];
-          const float sg = bf16r(__fdiv_rn(gt, 1.0f + expf(-gt)));
-          mv[q] = bf16r(sg * up);
-        }
-        ctl.put_bf16x4(true, Dm::X_M + (uint32_t)(xcd * Dm::MS + Dm::M_WG * r + 4 * lane), mv[0], mv[1], mv[2], mv[3],
-                       tag_of(L, 6));
+      // one m value per lane; lane 4j publishes values 4j..4j+3, taken from its quad by DPP
+      static_assert(Dm::M_WG % 4 == 0 && Dm::M_WG <= 64, "m values in whole quads of one wave");
+      float mv = 0.f;
+      if (lane < Dm::M_WG) {
+        const float gt = s.out[lane];
+        const float up = s.out[Dm::M_WG + lane];
+        mv = bf16r(bf16r(__fdiv_rn(gt, 1.0f + expf(-gt))) * up);
       }
+      const float m1 = quad_lane<1>(mv), m2 = quad_lane<2>(mv), m3 = quad_lane<3>(mv);
+      if (lane < Dm::M_WG && (lane & 3) == 0)
+        ctl.put_bf16x4(true, Dm::X_M + (uint32_t)(xcd * Dm::MS + Dm::M_WG * r + lane), mv, m1, m2, m3, tag_of(L, 6));
       ctl.template gather_range<Dm::MS>(Dm::X_M + xcd * Dm::MS, tag_of(L, 6), to_bf16(s.m));
     }
     stamp(tp + 11);

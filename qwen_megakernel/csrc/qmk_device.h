@@ -42,6 +42,14 @@ __device__ __forceinline__ uint32_t f32_to_bf16(float f) {
 // Value of ``f`` rounded to bf16, as fp32.
 __device__ __forceinline__ float bf16r(float f) { return bf16_to_f32(f32_to_bf16(f)); }
 
+// Two fp32 values rounded to bf16 as f32_to_bf16 rounds them, in one v_cvt_pk_bf16_f32 (the
+// scalar form converts one value per instruction): ``lo`` in bits [15:0], ``hi`` in [31:16].
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  const f32x2 v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+}
+
 __device__ __forceinline__ float lo_bf16(uint32_t packed) { return __uint_as_float(packed << 16); }
 __device__ __forceinline__ float hi_bf16(uint32_t packed) { return __uint_as_float(packed & 0xffff0000u); }
 
@@ -102,6 +110,12 @@ template <int CTRL>
 __device__ __forceinline__ float dpp_add(float v) {
   int s = __builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false);
   return v + __int_as_float(s);
+}
+
+// Value of lane 4*(lane/4) + Q (the lane's quad member Q), by DPP quad_perm.
+template <int Q>
+__device__ __forceinline__ float quad_lane(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), Q * 0x55, 0xf, 0xf, false));
 }
 
 // Sum over each row of 16 lanes; every lane of the row receives the row sum.
