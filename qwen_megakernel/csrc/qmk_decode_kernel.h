@@ -440,15 +440,18 @@ struct Ctl {
           part1[slot] = f32_from_words(v.z, v.w);
         });
     if (!ok) return false;
-    // lane l sums row pair rp = l % CPX over the sources in order 0..7, each
-    // fetched from the lane and slot that received it
-    const int rp = lane % CPX;
+    // lane l < CPX sums row pair l over the sources in order 0..7, each fetched
+    // from the lane that received it, (src * CPX) % 64 lanes ahead, by row swaps
     float p0[kGroups], p1[kGroups];
 #pragma unroll
     for (int src = 0; src < kGroups; src++) {
-      const int from = (src * CPX) % 64 + rp;
-      p0[src] = __shfl(part0[(src * CPX) / 64], from);
-      p1[src] = __shfl(part1[(src * CPX) / 64], from);
+      const int sl = (src * CPX) / 64;
+      switch ((src * CPX) % 64) {
+        case 0: p0[src] = part0[sl]; p1[src] = part1[sl]; break;
+        case 16: p0[src] = lane_ahead<16>(part0[sl]); p1[src] = lane_ahead<16>(part1[sl]); break;
+        case 32: p0[src] = lane_ahead<32>(part0[sl]); p1[src] = lane_ahead<32>(part1[sl]); break;
+        default: p0[src] = lane_ahead<48>(part0[sl]); p1[src] = lane_ahead<48>(part1[sl]); break;
+      }
     }
 #pragma unroll
     for (int src = 0; src < kGroups; src++) {
@@ -720,10 +723,12 @@ __device__ __forceinline__ void control_path(const KArgs& a, Smem<M>& s, const S
           float mh = -INFINITY, lh = 0.f;
 #pragma unroll
           for (int c = 0; c < kComputeWaves; c++) mh = fmaxf(mh, s.wml[c][h][0]);
+          // wave c's factor exp(m_c - mh) is computed by lane c and read from it
+          const float ml = s.wml[lane & (kComputeWaves - 1)][h][0];
+          const float fl = ml == -INFINITY ? 0.f : exp_acc(ml - mh);
 #pragma unroll
           for (int c = 0; c < kComputeWaves; c++) {
-            const float mc = s.wml[c][h][0];
-            const float f = mc == -INFINITY ? 0.f : exp_acc(mc - mh);
+            const float f = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(fl), c));
             lh += f * s.wml[c][h][1];
             a0 += f * s.wacc[c][h][2 * lane];
             a1 += f * s.wacc[c][h][2 * lane + 1];
@@ -783,21 +788,22 @@ __device__ __forceinline__ void control_path(const KArgs& a, Smem<M>& s, const S
           s0 = v0[0] + v0[1];
           s1 = v1[0] + v1[1];
         }
-#pragma unroll
-        for (int o = 4; o < 64; o <<= 1) {
-          s0 += __shfl_xor(s0, o);
-          s1 += __shfl_xor(s1, o);
-        }
-        // lanes with equal l%4 now hold the sum over all ranks of dims 8kb+2(l%4), +1;
-        // lanes 0 and 1 publish dims 8kb..8kb+3 and 8kb+4..8kb+7
-        float d2 = __shfl(s0, (lane & 1) * 2 + 0), d3 = __shfl(s1, (lane & 1) * 2 + 0);
-        float d4 = __shfl(s0, (lane & 1) * 2 + 1), d5 = __shfl(s1, (lane & 1) * 2 + 1);
+        // sum over the 16 lanes of each class l % 4: rotations by 4 and 8 inside each 16-lane row,
+        // then the row swaps.  Lane l < 4 then holds the sum over all ranks of dims 8kb+2l, +1,
+        // added as (v_l + v_l+4) + (v_l+8 + v_l+12), then with row 1's, then with rows 2-3's.
+        s0 = dpp_add<0x124>(s0);
+        s1 = dpp_add<0x124>(s1);
+        s0 = dpp_add<0x128>(s0);
+        s1 = dpp_add<0x128>(s1);
+        s0 = rows_sum4(s0);
+        s1 = rows_sum4(s1);
         if constexpr (SPLIT) {
-          d2 = __fdiv_rn(d2, gsum);
-          d3 = __fdiv_rn(d3, gsum);
-          d4 = __fdiv_rn(d4, gsum);
-          d5 = __fdiv_rn(d5, gsum);
+          s0 = __fdiv_rn(s0, gsum);
+          s1 = __fdiv_rn(s1, gsum);
         }
+        // lanes 0 and 1 publish dims 8kb..8kb+3 (from lanes 0, 1) and 8kb+4..8kb+7 (lanes 2, 3)
+        const float d2 = dpp_mov<0x88>(s0), d3 = dpp_mov<0x88>(s1);  // quad_perm [0,2,0,2]
+        const float d4 = dpp_mov<0xDD>(s0), d5 = dpp_mov<0xDD>(s1);  // quad_perm [1,3,1,3]
         if (lane < 2)
           ctl.put_bf16x4(true, Dm::X_ATTN + (uint32_t)(xcd * Dm::OC + hh * Dm::D + 8 * kb + 4 * lane), d2, d3, d4, d5,
                          tag_of(L, 3));

@@ -96,6 +96,20 @@ __device__ __forceinline__ void swap32(float v, float& a, float& b) {
   a = __uint_as_float(r[0]);
   b = __uint_as_float(r[1]);
 }
+// Value of lane l + OFF (OFF = 16, 32 or 48), by the row swaps above.  Valid in the lanes whose
+// source stays in the wave: row 0 for OFF = 48, rows 0 and 1 for OFF = 32, rows 0 and 2 for 16.
+template <int OFF>
+__device__ __forceinline__ float lane_ahead(float v) {
+  static_assert(OFF == 16 || OFF == 32 || OFF == 48, "a whole number of rows");
+  float a, b;
+  if constexpr (OFF == 16) {
+    swap16(v, a, b);  // rows 0 and 2 receive rows 1 and 3 in b
+  } else {
+    swap32(v, a, b);  // rows 0 and 1 receive rows 2 and 3 in b
+    if constexpr (OFF == 48) swap16(b, a, b);  // row 0 receives row 1 of that: row 3
+  }
+  return b;
+}
 __device__ __forceinline__ float rows_sum4(float v) {  // sum over the four 16-lane rows, in every lane
   float a, b;
   swap16(v, a, b);
@@ -116,6 +130,12 @@ __device__ __forceinline__ float dpp_add(float v) {
 template <int Q>
 __device__ __forceinline__ float quad_lane(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), Q * 0x55, 0xf, 0xf, false));
+}
+
+// Any DPP lane move (CTRL: quad_perm 0x00-0xFF, row_ror:n 0x120 + n).
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
 }
 
 // Sum over each row of 16 lanes; every lane of the row receives the row sum.
