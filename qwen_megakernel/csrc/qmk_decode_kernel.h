@@ -376,7 +376,9 @@ struct Ctl {
       ss += xv[i].x * xv[i].x + xv[i].y * xv[i].y;
     }
     ss = wave_sum(ss);
-    const float rstd = rcp_sqrt_torch(__fdiv_rn(ss, (float)Dm::H) + a.rms_eps);
+    // the mean: H is a power of two, so the product with 1/H is the correctly rounded quotient
+    static_assert((Dm::H & (Dm::H - 1)) == 0, "H a power of two");
+    const float rstd = rcp_sqrt_torch(ss * (1.0f / Dm::H) + a.rms_eps);
     // two elements per conversion: bf16(x * rstd), then bf16(w * that)
 #pragma unroll
     for (int i = 0; i < P; i++) {
@@ -406,7 +408,8 @@ struct Ctl {
   __device__ void head_norm_rope(int src_off, const HeadW& hw, uint16_t* dst) {
     const float x0 = s.qkv[src_off + lane], x1 = s.qkv[src_off + lane + 64];
     const float ss = wave_sum(x0 * x0 + x1 * x1);
-    const float rstd = rcp_sqrt_torch(__fdiv_rn(ss, (float)Dm::D) + a.rms_eps);
+    static_assert((Dm::D & (Dm::D - 1)) == 0, "head_dim a power of two");
+    const float rstd = rcp_sqrt_torch(ss * (1.0f / Dm::D) + a.rms_eps);
     // the lane's two elements share each bf16 conversion
     const uint32_t xn = pack_bf16x2(x0 * rstd, x1 * rstd);
     const uint32_t nn = pack_bf16x2(hw.w0 * lo_bf16(xn), hw.w1 * hi_bf16(xn));
@@ -464,7 +467,8 @@ struct Ctl {
       const uint32_t hb = pack_bf16x2(res[row] + lo_bf16(sb), res[row + 1] + hi_bf16(sb));
       const uint32_t hb0 = hb & 0xffffu, hb1 = hb >> 16;
       // two words per lane: pairs of lanes form one 16-byte store
-      const uint32_t ob0 = __shfl_xor(hb0, 1), ob1 = __shfl_xor(hb1, 1);
+      const uint32_t ob0 = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)hb0, 0xB1, 0xf, 0xf, false);  // lane ^ 1
+      const uint32_t ob1 = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)hb1, 0xB1, 0xf, 0xf, false);
       if ((lane & 1) == 0) {
         u32x4 d;
         d.x = word(hb0, dst_tag);
@@ -777,7 +781,7 @@ __device__ __forceinline__ void control_path(const KArgs& a, Smem<M>& s, const S
         if constexpr (SPLIT) {
           // rescale rank j's partial by exp(m_j - M) (M the maximum over the active ranks) and
           // normalise by the rescaled sum of the sums
-          const float gm = wave_max(mr);
+          const float gm = wave_max_all(mr);
           const float f = mr == -INFINITY ? 0.f : exp_acc(mr - gm);
           const float gl = wave_sum(f * lr);
           const float fa = __shfl(f, lane >> 2), fb = __shfl(f, (lane >> 2) + 16);
@@ -890,7 +894,7 @@ __device__ __forceinline__ void control_path(const KArgs& a, Smem<M>& s, const S
     });
     stamp(p.nl * kTracePoints + 2);
     if (ok) {
-      best = wave_max_u64(best);
+      best = wave_max_u64_all(best);
       const int token = (int)(0xffffffffu - (uint32_t)best);
       if (lane == 0) {
         DecodeState* st = a.st;

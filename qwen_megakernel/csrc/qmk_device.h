@@ -15,6 +15,9 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+#include <utility>
+
 namespace qmk {
 
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
@@ -193,6 +196,61 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
   for (int o = 32; o >= 1; o >>= 1) {
     uint64_t w = __shfl_xor(v, o);
     v = w > v ? w : v;
+  }
+  return v;
+}
+
+// The same maxima by DPP (quads, then rotations inside each 16-lane row) and the row swaps, on
+// the VALU instead of the LDS crossbar.  Every lane of the wave must be active.
+__device__ __forceinline__ float wave_max_all(float v) {
+  v = fmaxf(v, dpp_mov<0xB1>(v));   // quad_perm [1,0,3,2]
+  v = fmaxf(v, dpp_mov<0x4E>(v));   // quad_perm [2,3,0,1]
+  v = fmaxf(v, dpp_mov<0x124>(v));  // row_ror:4
+  v = fmaxf(v, dpp_mov<0x128>(v));  // row_ror:8
+  float a, b;
+  swap16(v, a, b);
+  v = fmaxf(a, b);
+  swap32(v, a, b);
+  return fmaxf(a, b);
+}
+
+__device__ __forceinline__ uint64_t wave_max_u64_all(uint64_t v) {
+  auto take = [&v](uint32_t lo, uint32_t hi) {
+    const uint64_t w = ((uint64_t)hi << 32) | lo;
+    v = w > v ? w : v;
+  };
+  auto dpp = [](uint64_t x, auto ctrl) {
+    return std::pair<uint32_t, uint32_t>(
+        (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)x, decltype(ctrl)::value, 0xf, 0xf, false),
+        (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(x >> 32), decltype(ctrl)::value, 0xf, 0xf, false));
+  };
+  {
+    const auto p = dpp(v, std::integral_constant<int, 0xB1>());
+    take(p.first, p.second);
+  }
+  {
+    const auto p = dpp(v, std::integral_constant<int, 0x4E>());
+    take(p.first, p.second);
+  }
+  {
+    const auto p = dpp(v, std::integral_constant<int, 0x124>());
+    take(p.first, p.second);
+  }
+  {
+    const auto p = dpp(v, std::integral_constant<int, 0x128>());
+    take(p.first, p.second);
+  }
+  {
+    const auto lo = __builtin_amdgcn_permlane16_swap((uint32_t)v, (uint32_t)v, false, false);
+    const auto hi = __builtin_amdgcn_permlane16_swap((uint32_t)(v >> 32), (uint32_t)(v >> 32), false, false);
+    take(lo[0], hi[0]);
+    take(lo[1], hi[1]);
+  }
+  {
+    const auto lo = __builtin_amdgcn_permlane32_swap((uint32_t)v, (uint32_t)v, false, false);
+    const auto hi = __builtin_amdgcn_permlane32_swap((uint32_t)(v >> 32), (uint32_t)(v >> 32), false, false);
+    take(lo[0], hi[0]);
+    take(lo[1], hi[1]);
   }
   return v;
 }
