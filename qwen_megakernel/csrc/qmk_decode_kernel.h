@@ -404,12 +404,29 @@ struct Ctl {
     return h;
   }
 
-  // Per-head RMSNorm + rotate-half RoPE of one 128-wide head held in s.qkv.
-  __device__ void head_norm_rope(int src_off, const HeadW& hw, uint16_t* dst) {
-    const float x0 = s.qkv[src_off + lane], x1 = s.qkv[src_off + lane + 64];
-    const float ss = wave_sum(x0 * x0 + x1 * x1);
+  // Per-head RMSNorm + rotate-half RoPE of the GQ q heads and the k head held in s.qkv, into s.q
+  // and s.k.  Each head's sum of squares is reduced on its own; the correctly rounded 1/sqrt of
+  // head h's mean is evaluated in lane h, once for all heads, and read back with readlane.
+  __device__ void qk_norm_rope(const HeadW& hq, const HeadW& hk) {
+    constexpr int NH = Dm::GQ + 1;
     static_assert((Dm::D & (Dm::D - 1)) == 0, "head_dim a power of two");
-    const float rstd = rcp_sqrt_torch(ss * (1.0f / Dm::D) + a.rms_eps);
+    float x0[NH], x1[NH], v = 0.f;
+#pragma unroll
+    for (int h = 0; h < NH; h++) {
+      x0[h] = s.qkv[h * Dm::D + lane];
+      x1[h] = s.qkv[h * Dm::D + lane + 64];
+      const float ss = wave_sum(x0[h] * x0[h] + x1[h] * x1[h]);
+      v = lane == h ? ss : v;
+    }
+    const float rl = rcp_sqrt_torch(v * (1.0f / Dm::D) + a.rms_eps);
+#pragma unroll
+    for (int h = 0; h < NH; h++) {
+      const float rstd = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(rl), h));
+      head_rope(x0[h], x1[h], rstd, h < Dm::GQ ? hq : hk, h < Dm::GQ ? s.q + h * Dm::D : s.k);
+    }
+  }
+
+  __device__ void head_rope(float x0, float x1, float rstd, const HeadW& hw, uint16_t* dst) {
     // the lane's two elements share each bf16 conversion
     const uint32_t xn = pack_bf16x2(x0 * rstd, x1 * rstd);
     const uint32_t nn = pack_bf16x2(hw.w0 * lo_bf16(xn), hw.w1 * hi_bf16(xn));
@@ -647,9 +664,7 @@ __device__ __forceinline__ void control_path(const KArgs& a, Smem<M>& s, const S
       const auto hq = ctl.load_head(w.q_norm, cosr, sinr);
       const auto hk = ctl.load_head(w.k_norm, cosr, sinr);
       if (ctl.template gather_range<Dm::RG>(Dm::X_QKV + xcd * Dm::RG, t, to_f32(s.qkv))) {
-#pragma unroll
-        for (int h = 0; h < Dm::GQ; h++) ctl.head_norm_rope(h * Dm::D, hq, s.q + h * Dm::D);
-        ctl.head_norm_rope(Dm::GQ * Dm::D, hk, s.k);
+        ctl.qk_norm_rope(hq, hk);
         const float v0 = s.qkv[(Dm::GQ + 1) * Dm::D + lane], v1 = s.qkv[(Dm::GQ + 1) * Dm::D + lane + 64];
         s.v[lane] = (uint16_t)f32_to_bf16(v0);
         s.v[lane + 64] = (uint16_t)f32_to_bf16(v1);
