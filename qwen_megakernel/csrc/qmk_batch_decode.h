@@ -342,28 +342,50 @@ struct BCtl {
       ss += xv[i].x * xv[i].x + xv[i].y * xv[i].y;
     }
     ss = wave_sum(ss);
-    const float rstd = rcp_sqrt_torch(__fdiv_rn(ss, (float)Dm::H) + a.rms_eps);
+    // the mean: H is a power of two, so the product with 1/H is the correctly rounded quotient
+    static_assert((Dm::H & (Dm::H - 1)) == 0, "H a power of two");
+    const float rstd = rcp_sqrt_torch(ss * (1.0f / Dm::H) + a.rms_eps);
+    // two elements per conversion: bf16(x * rstd), then bf16(w * that)
 #pragma unroll
     for (int i = 0; i < P; i++) {
       const uint32_t wp = nw.w[i];
-      const float n0 = bf16r(lo_bf16(wp) * bf16r(xv[i].x * rstd));
-      const float n1 = bf16r(hi_bf16(wp) * bf16r(xv[i].y * rstd));
-      r2[lane + 64 * i] = f32_to_bf16(n0) | (f32_to_bf16(n1) << 16);
+      const uint32_t xn = pack_bf16x2(xv[i].x * rstd, xv[i].y * rstd);
+      r2[lane + 64 * i] = pack_bf16x2(lo_bf16(wp) * lo_bf16(xn), hi_bf16(wp) * hi_bf16(xn));
     }
   }
 
-  // per-head RMSNorm + rotate-half RoPE of one 128-wide head (elements lane, lane + 64)
-  __device__ void head_norm_rope(const float* src, float w0, float w1, float c0, float c1, float s0, float s1,
-                                 uint16_t* dst) {
-    const float x0 = src[lane], x1 = src[lane + 64];
-    const float ss = wave_sum(x0 * x0 + x1 * x1);
-    const float rstd = rcp_sqrt_torch(__fdiv_rn(ss, (float)Dm::D) + a.rms_eps);
-    const float n0 = bf16r(w0 * bf16r(x0 * rstd));
-    const float n1 = bf16r(w1 * bf16r(x1 * rstd));
-    const float y0 = bf16r(bf16r(n0 * c0) + bf16r(-n1 * s0));
-    const float y1 = bf16r(bf16r(n1 * c1) + bf16r(n0 * s1));
-    dst[lane] = (uint16_t)f32_to_bf16(y0);
-    dst[lane + 64] = (uint16_t)f32_to_bf16(y1);
+  // Per-head RMSNorm + rotate-half RoPE (elements lane, lane + 64) of the GQ q heads and the k
+  // head at qkv, into q and k.  Each head's sum of squares is reduced on its own; the correctly
+  // rounded 1/sqrt of head h's mean is evaluated in lane h, once for all heads, and read back.
+  __device__ void qk_norm_rope(const float* qkv, float qw0, float qw1, float kw0, float kw1, float c0, float c1,
+                               float s0, float s1, uint16_t* q, uint16_t* k) {
+    constexpr int NH = Dm::GQ + 1;
+    static_assert((Dm::D & (Dm::D - 1)) == 0, "head_dim a power of two");
+    float x0[NH], x1[NH], v = 0.f;
+#pragma unroll
+    for (int h = 0; h < NH; h++) {
+      x0[h] = qkv[h * Dm::D + lane];
+      x1[h] = qkv[h * Dm::D + lane + 64];
+      const float ss = wave_sum(x0[h] * x0[h] + x1[h] * x1[h]);
+      v = lane == h ? ss : v;
+    }
+    const float rl = rcp_sqrt_torch(v * (1.0f / Dm::D) + a.rms_eps);
+#pragma unroll
+    for (int h = 0; h < NH; h++) {
+      const float rstd = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(rl), h));
+      const bool isq = h < Dm::GQ;
+      uint16_t* dst = isq ? q + h * Dm::D : k;
+      // the lane's two elements share each bf16 conversion
+      const uint32_t xn = pack_bf16x2(x0[h] * rstd, x1[h] * rstd);
+      const uint32_t nn = pack_bf16x2((isq ? qw0 : kw0) * lo_bf16(xn), (isq ? qw1 : kw1) * hi_bf16(xn));
+      const float n0 = lo_bf16(nn), n1 = hi_bf16(nn);
+      // x*cos + rotate_half(x)*sin with rotate_half(x) = (-x[64:], x[:64]), each product rounded
+      const uint32_t pc = pack_bf16x2(n0 * c0, n1 * c1);
+      const uint32_t ps = pack_bf16x2(-n1 * s0, n0 * s1);
+      const uint32_t y = pack_bf16x2(lo_bf16(pc) + lo_bf16(ps), hi_bf16(pc) + hi_bf16(ps));
+      dst[lane] = (uint16_t)(y & 0xffffu);
+      dst[lane + 64] = (uint16_t)(y >> 16);
+    }
   }
 
   // Reduce-scatter across XCDs for sequence sb: sums the eight XCD partials of
@@ -387,15 +409,18 @@ struct BCtl {
           part1[j] = f32_from_words(v.z, v.w);
         });
     if (!ok) return false;
-    int ln = lane;
-    asm volatile("" : "+v"(ln));  // computed here, not hoisted (and spilled) across the gather
-    const int rp = ln % CPX;
+    // lane l < CPX sums row pair l over the sources in order 0..7, each fetched from the lane that
+    // received it, (src * CPX) % 64 lanes ahead, by row swaps
     float p0[kGroups], p1[kGroups];
 #pragma unroll
     for (int src = 0; src < kGroups; src++) {
-      const int from = (src * CPX) % 64 + rp;
-      p0[src] = __shfl(part0[(src * CPX) / 64], from);
-      p1[src] = __shfl(part1[(src * CPX) / 64], from);
+      const int sl = (src * CPX) / 64;
+      switch ((src * CPX) % 64) {
+        case 0: p0[src] = part0[sl]; p1[src] = part1[sl]; break;
+        case 16: p0[src] = lane_ahead<16>(part0[sl]); p1[src] = lane_ahead<16>(part1[sl]); break;
+        case 32: p0[src] = lane_ahead<32>(part0[sl]); p1[src] = lane_ahead<32>(part1[sl]); break;
+        default: p0[src] = lane_ahead<48>(part0[sl]); p1[src] = lane_ahead<48>(part1[sl]); break;
+      }
     }
     float sum0 = 0.f, sum1 = 0.f;
 #pragma unroll
@@ -405,14 +430,15 @@ struct BCtl {
     }
     uint32_t hb0 = 0, hb1 = 0;
     if (lane < CPX) {
-      const float h0 = bf16r(s.res[sb][2 * lane] + bf16r(sum0));
-      const float h1 = bf16r(s.res[sb][2 * lane + 1] + bf16r(sum1));
-      s.res[sb][2 * lane] = h0;
-      s.res[sb][2 * lane + 1] = h1;
-      hb0 = f32_to_bf16(h0);
-      hb1 = f32_to_bf16(h1);
+      const uint32_t sbits = pack_bf16x2(sum0, sum1);
+      const uint32_t hb = pack_bf16x2(s.res[sb][2 * lane] + lo_bf16(sbits), s.res[sb][2 * lane + 1] + hi_bf16(sbits));
+      s.res[sb][2 * lane] = lo_bf16(hb);
+      s.res[sb][2 * lane + 1] = hi_bf16(hb);
+      hb0 = hb & 0xffffu;
+      hb1 = hb >> 16;
     }
-    const uint32_t ob0 = __shfl_xor(hb0, 1), ob1 = __shfl_xor(hb1, 1);
+    const uint32_t ob0 = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)hb0, 0xB1, 0xf, 0xf, false);  // lane ^ 1
+    const uint32_t ob1 = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)hb1, 0xB1, 0xf, 0xf, false);
     if (lane < CPX && (lane & 1) == 0) {
       u32x4 d;
       d.x = word(hb0, dst_tag);
@@ -536,10 +562,7 @@ __device__ __forceinline__ void batch_control(const BArgs& a, BSmem<M, B>& s, co
                                                          d[3] = bf16_to_f32(v.w >> 16);
                                                        });
       if (ok) {
-#pragma unroll
-        for (int h = 0; h < Dm::GQ; h++)
-          ctl.head_norm_rope(qkv + h * Dm::D, qw0, qw1, c0, c1, s0, s1, s.q[sb] + h * Dm::D);
-        ctl.head_norm_rope(qkv + Dm::GQ * Dm::D, kw0, kw1, c0, c1, s0, s1, s.k[sb]);
+        ctl.qk_norm_rope(qkv, qw0, qw1, kw0, kw1, c0, c1, s0, s1, s.q[sb], s.k[sb]);
         const float v0 = qkv[(Dm::GQ + 1) * Dm::D + lane], v1 = qkv[(Dm::GQ + 1) * Dm::D + lane + 64];
         s.v[sb][lane] = (uint16_t)f32_to_bf16(v0);
         s.v[sb][lane + 64] = (uint16_t)f32_to_bf16(v1);
@@ -588,10 +611,9 @@ __device__ __forceinline__ void batch_control(const BArgs& a, BSmem<M, B>& s, co
             pl = act ? f32_from_words(v.z, v.w) : 0.f;
           });
       if (ok) {
-        float gm = pm;
-        for (int o = Dm::GQ; o < 64; o <<= 1) gm = fmaxf(gm, __shfl_xor(gm, o));
-        float lsum = pm == -INFINITY ? 0.f : pl * exp_acc(pm - gm);
-        for (int o = Dm::GQ; o < 64; o <<= 1) lsum += __shfl_xor(lsum, o);
+        static_assert(Dm::GQ == 2, "lane classes of two");
+        const float gm = class2_max(pm);
+        const float lsum = class2_sum(pm == -INFINITY ? 0.f : pl * exp_acc(pm - gm));
         if (lane < Dm::GQ) {
           s.ml[sb][lane][0] = gm;
           s.ml[sb][lane][1] = lsum;
@@ -637,15 +659,14 @@ __device__ __forceinline__ void batch_control(const BArgs& a, BSmem<M, B>& s, co
       if (ok2) {
         float x0 = v0[0] + v0[1];
         float x1 = v1[0] + v1[1];
-#pragma unroll
-        for (int o = 4; o < 64; o <<= 1) {
-          x0 += __shfl_xor(x0, o);
-          x1 += __shfl_xor(x1, o);
-        }
-        // lanes with equal lane % 4 hold the sum over all ranks of dims 8kb + 2(lane % 4), +1;
-        // lanes 0 and 1 publish dims 8kb..8kb+3 and 8kb+4..8kb+7
-        const float d2 = __shfl(x0, (lane & 1) * 2 + 0), d3 = __shfl(x1, (lane & 1) * 2 + 0);
-        const float d4 = __shfl(x0, (lane & 1) * 2 + 1), d5 = __shfl(x1, (lane & 1) * 2 + 1);
+        // sum over the 16 lanes of each class lane % 4: row_ror:12 and row_ror:8 inside each 16-lane
+        // row (lanes 0..3 read lanes 4..7, then 8..11), then the row swaps; lane l < 4 then holds the
+        // sum over all ranks of dims 8kb + 2l, +1, in the xor butterfly's order
+        x0 = rows_sum4(dpp_add<0x128>(dpp_add<0x12C>(x0)));
+        x1 = rows_sum4(dpp_add<0x128>(dpp_add<0x12C>(x1)));
+        // lanes 0 and 1 publish dims 8kb..8kb+3 (from lanes 0, 1) and 8kb+4..8kb+7 (lanes 2, 3)
+        const float d2 = dpp_mov<0x88>(x0), d3 = dpp_mov<0x88>(x1);  // quad_perm [0,2,0,2]
+        const float d4 = dpp_mov<0xDD>(x0), d5 = dpp_mov<0xDD>(x1);  // quad_perm [1,3,1,3]
         if (lane < 2)
           ctl.put_bf16x4(true, Dm::X_ATTN + (uint32_t)((xcd * B + sb) * Dm::OC + hh * Dm::D + 8 * kb + 4 * lane), d2,
                          d3, d4, d5, tag_of(L, 3));
@@ -676,19 +697,18 @@ __device__ __forceinline__ void batch_control(const BArgs& a, BSmem<M, B>& s, co
     stamp(tp + 10);
     // ------------------------------------------------------------ j..k  m
     {
-      constexpr int QPB = Dm::M_WG / 4;  // quads of m values per workgroup
-      if (lane < QPB) {
-        float mv[4];
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-          const float gt = s.out[sb][4 * lane + q];
-          const float up = s.out[sb][Dm::M_WG + 4 * lane + q];
-          const float sg = bf16r(__fdiv_rn(gt, 1.0f + expf(-gt)));
-          mv[q] = bf16r(sg * up);
-        }
-        ctl.put_bf16x4(true, Dm::X_M + (uint32_t)((xcd * B + sb) * Dm::MS + Dm::M_WG * r + 4 * lane), mv[0], mv[1],
-                       mv[2], mv[3], tag_of(L, 6));
+      // one m value per lane; lane 4j publishes values 4j..4j+3, taken from its quad by DPP
+      static_assert(Dm::M_WG % 4 == 0 && Dm::M_WG <= 64, "m values in whole quads of one wave");
+      float mv = 0.f;
+      if (lane < Dm::M_WG) {
+        const float gt = s.out[sb][lane];
+        const float up = s.out[sb][Dm::M_WG + lane];
+        mv = bf16r(bf16r(__fdiv_rn(gt, 1.0f + expf(-gt))) * up);
       }
+      const float m1 = quad_lane<1>(mv), m2 = quad_lane<2>(mv), m3 = quad_lane<3>(mv);
+      if (lane < Dm::M_WG && (lane & 3) == 0)
+        ctl.put_bf16x4(true, Dm::X_M + (uint32_t)((xcd * B + sb) * Dm::MS + Dm::M_WG * r + lane), mv, m1, m2, m3,
+                       tag_of(L, 6));
       uint16_t* const mm = s.m[sb];
       ctl.template gather_seq<Dm::MS>(Dm::X_M + xcd * B * Dm::MS, sb, tag_of(L, 6), [&](int ci, u32x4 v) {
         uint32_t* d = reinterpret_cast<uint32_t*>(mm) + 2 * ci;

@@ -714,10 +714,9 @@ __device__ __forceinline__ void control_path(const KArgs& a, Smem<M>& s, const S
           const int h = lane % Dm::GQ;
           const bool act = (lane / Dm::GQ) < p.n_act;
           float m0 = act ? pm[0] : -INFINITY;
-          float gm = m0;
-          for (int o = Dm::GQ; o < 64; o <<= 1) gm = fmaxf(gm, __shfl_xor(gm, o));
-          float lsum = (act && m0 != -INFINITY) ? pl[0] * exp_acc(m0 - gm) : 0.f;
-          for (int o = Dm::GQ; o < 64; o <<= 1) lsum += __shfl_xor(lsum, o);
+          static_assert(Dm::GQ == 2, "lane classes of two");
+          const float gm = class2_max(m0);
+          const float lsum = class2_sum((act && m0 != -INFINITY) ? pl[0] * exp_acc(m0 - gm) : 0.f);
           if (lane < Dm::GQ) {
             s.ml[h][0] = gm;
             s.ml[h][1] = lsum;
@@ -807,11 +806,12 @@ __device__ __forceinline__ void control_path(const KArgs& a, Smem<M>& s, const S
           s0 = v0[0] + v0[1];
           s1 = v1[0] + v1[1];
         }
-        // sum over the 16 lanes of each class l % 4: rotations by 4 and 8 inside each 16-lane row,
-        // then the row swaps.  Lane l < 4 then holds the sum over all ranks of dims 8kb+2l, +1,
-        // added as (v_l + v_l+4) + (v_l+8 + v_l+12), then with row 1's, then with rows 2-3's.
-        s0 = dpp_add<0x124>(s0);
-        s1 = dpp_add<0x124>(s1);
+        // sum over the 16 lanes of each class l % 4: row_ror:12 and row_ror:8 inside each 16-lane row
+        // (lanes 0..3 read lanes 4..7, then 8..11), then the row swaps.  Lane l < 4 then holds the
+        // sum over all ranks of dims 8kb+2l, +1, added as the xor butterfly adds it:
+        // (v_l + v_l+4) + (v_l+8 + v_l+12), then with row 1's, then with rows 2-3's.
+        s0 = dpp_add<0x12C>(s0);
+        s1 = dpp_add<0x12C>(s1);
         s0 = dpp_add<0x128>(s0);
         s1 = dpp_add<0x128>(s1);
         s0 = rows_sum4(s0);

@@ -135,7 +135,8 @@ __device__ __forceinline__ float quad_lane(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), Q * 0x55, 0xf, 0xf, false));
 }
 
-// Any DPP lane move (CTRL: quad_perm 0x00-0xFF, row_ror:n 0x120 + n).
+// Any DPP lane move (CTRL: quad_perm 0x00-0xFF; row_ror:n 0x120 + n, by which lane i of each
+// 16-lane row reads lane (i - n) mod 16, so row_ror:12 reads lane i + 4 for i < 12).
 template <int CTRL>
 __device__ __forceinline__ float dpp_mov(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
@@ -174,6 +175,27 @@ __device__ __forceinline__ float row16_sum_t4(float v00, float v01, float v10, f
   return r;
 }
 
+// Maximum and sum over the lanes of each class lane % 2 (lanes 2 apart), as the xor butterfly over
+// distances 2, 4, .., 32 forms them, in lanes 0..3: DPP quad_perm [2,3,0,1], then row_ror:12 and
+// row_ror:8 (lanes 0..3 read lanes 4..7, then 8..11, as the xor by 4 and by 8 would), then the row
+// swaps.  Every lane of the wave must be active.
+__device__ __forceinline__ float class2_max(float v) {
+  v = fmaxf(v, dpp_mov<0x4E>(v));
+  v = fmaxf(v, dpp_mov<0x12C>(v));
+  v = fmaxf(v, dpp_mov<0x128>(v));
+  float a, b;
+  swap16(v, a, b);
+  v = fmaxf(a, b);
+  swap32(v, a, b);
+  return fmaxf(a, b);
+}
+__device__ __forceinline__ float class2_sum(float v) {
+  v = dpp_add<0x4E>(v);
+  v = dpp_add<0x12C>(v);
+  v = dpp_add<0x128>(v);
+  return rows_sum4(v);
+}
+
 // Sum over the wave, the same value in every lane.
 __device__ __forceinline__ float wave_total(float v) { return rows_sum4(row16_sum(v)); }
 
@@ -205,7 +227,7 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
 __device__ __forceinline__ float wave_max_all(float v) {
   v = fmaxf(v, dpp_mov<0xB1>(v));   // quad_perm [1,0,3,2]
   v = fmaxf(v, dpp_mov<0x4E>(v));   // quad_perm [2,3,0,1]
-  v = fmaxf(v, dpp_mov<0x124>(v));  // row_ror:4
+  v = fmaxf(v, dpp_mov<0x12C>(v));  // row_ror:12
   v = fmaxf(v, dpp_mov<0x128>(v));  // row_ror:8
   float a, b;
   swap16(v, a, b);
