@@ -270,10 +270,16 @@ struct Ctl {
   // chunk as it arrives.  A round is one 16-byte load per lane for every 64
   // chunks (NC loads).  A CU returns vector-memory data in order, so every poll
   // load in flight delays the next one and the compute waves' loads behind it:
-  // rounds of one load keep two rounds in flight (a chunk that lands while one
-  // is out is seen by the next half a round trip later), larger rounds keep
-  // one.  Measured on the decode step: two rounds everywhere 1,866 tok/s, one
-  // everywhere 1,890, this rule 1,899; three or four rounds 1,688 / 1,567.
+  // rounds of one load, and of two loads in the Qwen3-0.6B kernel, keep two
+  // rounds in flight (a chunk that lands while one is out is seen by the next
+  // half a round trip later), larger rounds keep one.  Measured on the decode
+  // step: two rounds everywhere 1,866 tok/s, one everywhere 1,890, two for
+  // one-load rounds only 1,899; three or four rounds 1,688 / 1,567.  With the
+  // control wave's element work cut (same-box A/B, context 1024): two rounds
+  // for rounds of up to two loads 2,118-2,120 against 2,115, up to three
+  // 2,104, up to four 2,056; Qwen3-1.7B (whose one two-load gather is the qkv
+  // exchange, polled behind the o_proj slice requested before it) 1,103
+  // against 1,111 with two rounds for it, so it keeps one.
   template <int NCH, class Off, class F>
   __device__ bool gather(uint32_t tag, Off&& off, F&& sink) {
     constexpr int NC = (NCH + 63) / 64;
@@ -291,7 +297,7 @@ struct Ctl {
     // static vmcnt((R - 1) * NC); chunks already received are pointed past the end of the
     // buffer descriptor, which makes their loads return 0 without memory traffic.
     constexpr uint32_t kOOB = 0xfffffff0u;
-    constexpr int R = NC == 1 ? 2 : 1;  // rounds in flight
+    constexpr int R = (NC == 1 || (NC == 2 && !Dm::kStream)) ? 2 : 1;  // rounds in flight
     u32x4 v[R][NC];
 #pragma unroll
     for (int k = 0; k < R - 1; k++)
