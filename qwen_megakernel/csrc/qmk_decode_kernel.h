@@ -1086,17 +1086,20 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
     // 1,960 tok/s.)
     if constexpr (DEEP) {
       for (int j = 0; j < min(nb, kKvStages); j++) kv_issue(kc, j);
+    } else if constexpr (EARLY) {
+      if (nb > 0 && L == 0) kv_issue(kc, 0);  // later layers' K rows were requested after down_proj
     } else {
       if (nb > 0) kv_issue(kc, 0);
     }
     if constexpr (SPLIT) {
       QMK_SYNC();  // c
       cstamp(L, 2);
-      // V rows of this wave's batch into ring stage 1 (its K rows are in stage 0); this layer's
-      // gate/up and o_proj slices follow the scores.  The control wave does not poll between
-      // barriers c and f, so nothing queues behind them.  (A wave without positions loads row 0
-      // too: requests on every path keep the compiler's counted waits exact.)
-      kv_issue_at(vc, 0, 1);
+      // Layer 0's V rows into ring stage 1 (its K rows are in stage 0); later layers' K and V
+      // rows were requested after the previous layer's down_proj, and barrier a waited for them.
+      // This layer's gate/up and o_proj slices follow the scores.  The control wave does not poll
+      // between barriers c and f, so nothing queues behind them.  (A wave without positions loads
+      // row 0 too: requests on every path keep the compiler's counted waits exact.)
+      if (L == 0) kv_issue_at(vc, 0, 1);
       // The scores need only the K rows (landed before barrier c): they are computed before this
       // layer's gate/up and o_proj slices are requested, so that they do not wait behind those
       // requests' issue (same-box A/B over contexts 129..1152: 2,136 tok/s against 2,118 with the
@@ -1521,6 +1524,16 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
       if (L + 1 < p.nl) prefetch_qkv(L + 1);
     } else if (!EARLY && L + 1 < p.nl) {
       prefetch_dn(L + 1);
+    }
+    if constexpr (EARLY) {
+      // The next layer's K and V rows into ring stages 0 and 1, free since this layer's
+      // attention: they land while the control wave reduces down_proj and gathers h (barrier a
+      // waits for them), so neither the qkv exchange's polls nor the attention window wait behind
+      // them.  Same-box A/B at context 1024: requested in the layer's own windows (K before
+      // barrier c, V after it) 2,125 tok/s; K here 2,140; K and V here 2,151-2,152.  (The last
+      // layer requests its own rows again, so every path issues the same loads.)
+      if (nb > 0) kv_issue(a.k_cache + L_next * kv_layer_stride + (size_t)xcd * a.max_seq_len * Dm::D, 0);
+      kv_issue_at(a.v_cache + L_next * kv_layer_stride + (size_t)xcd * a.max_seq_len * Dm::D, 0, 1);
     }
     cstamp(L, 11);
   }
