@@ -1096,14 +1096,16 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
       cstamp(L, 2);
       // Layer 0's V rows into ring stage 1 (its K rows are in stage 0); later layers' K and V
       // rows were requested after the previous layer's down_proj, and barrier a waited for them.
-      // This layer's gate/up and o_proj slices follow the scores.  The control wave does not poll
-      // between barriers c and f, so nothing queues behind them.  (A wave without positions loads
-      // row 0 too: requests on every path keep the compiler's counted waits exact.)
+      // Then this layer's gate/up and o_proj slices.  The control wave does not poll between
+      // barriers c and f, so nothing queues behind them.  (A wave without positions loads row 0
+      // too: requests on every path keep the compiler's counted waits exact.)  While the V rows
+      // were requested here for every layer, computing the scores before requesting the slices
+      // was faster (2,136 against 2,118 tok/s over contexts 129..1152); with the K and V rows in
+      // LDS at barrier c the two orders measure the same (2,178-2,180 either way; 2,155-2,156
+      // against 2,152 at context 1024 with the slices first).
       if (L == 0) kv_issue_at(vc, 0, 1);
-      // The scores need only the K rows (landed before barrier c): they are computed before this
-      // layer's gate/up and o_proj slices are requested, so that they do not wait behind those
-      // requests' issue (same-box A/B over contexts 129..1152: 2,136 tok/s against 2,118 with the
-      // slices requested first).
+      prefetch_gu(L);
+      prefetch_o(L);
       constexpr int kLoadsC = Dm::GU_W * Dm::LH + Dm::OP * Dm::LO;  // weight loads issued after the V rows
       // ---------------------------------------------- split-K attention over this wave's positions
       // Lane (slot, t16) holds dims 8*t16..+7 of position base0 + 32u + slot.  Scores as HF
@@ -1145,10 +1147,6 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
           m_w[h] = fmaxf(x, y);
         }
       }
-      __builtin_amdgcn_sched_barrier(0);
-      prefetch_gu(L);
-      prefetch_o(L);
-      __builtin_amdgcn_sched_barrier(0);
       wait_vmcnt_upto<kLoadsC>();  // the V rows have landed; the weight slices may stay in flight
       if (nb > 0) {
         const u32x4 v_now = *reinterpret_cast<const u32x4*>(s.v + 8 * t16);
