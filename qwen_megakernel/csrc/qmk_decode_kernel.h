@@ -1002,15 +1002,17 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
 
   // EARLY (short-context form with every slice in its own registers): attention
   // is a split-K softmax in one compute window, c..f (SPLIT; the control wave
-  // combines in f..g), and the weight slices are requested in the two windows
-  // in which the control wave does not poll, so that no exchange poll queues
-  // behind them (a CU returns vector-memory data in order): this layer's
-  // gate/up and o_proj slices at barrier c, behind the V rows; this layer's
-  // down slice and the next layer's QKV rows at i (gate/up).  Measured against
-  // the other placements of the same split kernel at context 1024 (direct
-  // launches): 1,996-2,005 tok/s; QKV row 0 and gate/up at c, o_proj, down
-  // and QKV row 1 at i 1,974-1,983; gate/up and both QKV rows at c 1,955;
-  // the V rows requested before barrier c with the K rows 1,943.
+  // combines in f..g).  A CU returns vector-memory data in order, so every
+  // request is placed where the control wave's polls do not follow it closely:
+  // this layer's gate/up and o_proj slices at barrier c and its down slice at i
+  // (the two windows in which the control wave does not poll), and the next
+  // layer's K, V and QKV rows right after the down_proj partials, where they
+  // land while the control wave reduces down_proj and gathers h.  Measured
+  // placements at context 1024 (direct launches) in earlier forms of this
+  // kernel: with the QKV rows at i, 1,996-2,005 tok/s; QKV row 0 and gate/up
+  // at c, o_proj, down and QKV row 1 at i 1,974-1,983; gate/up and both QKV
+  // rows at c 1,955; the V rows requested before barrier c with the K rows
+  // 1,943.  Those of this form are given where each request is issued.
   constexpr bool EARLY = !ST && !LONG;
   constexpr bool SPLIT = EARLY;
   static_assert(!EARLY || kLongContext / kGroupSize <= 32 * kKvU, "EARLY: at most one K/V batch per wave");
@@ -1481,10 +1483,8 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
     cstamp(L, 7);
     QMK_SYNC();  // i
     cstamp(L, 8);
-    // EARLY: this layer's down slice, then the gate/up rows, the first RQ_W of them each followed
-    // by one of the next layer's QKV rows, so that the dot products do not wait behind the whole
-    // window's requests (same-box A/B at context 1024: 2,124-2,126 tok/s against 2,115-2,116 with
-    // every request before the first dot product)
+    // EARLY: this layer's down slice, then the gate/up rows (the next layer's QKV rows follow the
+    // down_proj partials, with its K and V rows)
     if constexpr (EARLY) prefetch_dn(L);
     {
       u32x4 act[Dm::LH];
@@ -1493,14 +1493,6 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
       for (int i = 0; i < Dm::GU_W; i++) {
         const float v = row_dot_p<Dm::LH>(wgu + i * Dm::LH, act);
         if (lane == 0) s.out[gu_out + i] = bf16r(v);
-        if constexpr (EARLY) {
-          static_assert(Dm::RQ_W <= Dm::GU_W, "one QKV row after each of the first gate/up rows");
-          if (i < Dm::RQ_W) {
-            __builtin_amdgcn_sched_barrier(0);
-            prefetch_qkv_row(L_next, i);
-            __builtin_amdgcn_sched_barrier(0);
-          }
-        }
       }
     }
     if (ST) prefetch_dn(L);
@@ -1525,13 +1517,18 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
     }
     if constexpr (EARLY) {
       // The next layer's K and V rows into ring stages 0 and 1, free since this layer's
-      // attention: they land while the control wave reduces down_proj and gathers h (barrier a
-      // waits for them), so neither the qkv exchange's polls nor the attention window wait behind
-      // them.  Same-box A/B at context 1024: requested in the layer's own windows (K before
-      // barrier c, V after it) 2,125 tok/s; K here 2,140; K and V here 2,151-2,152.  (The last
-      // layer requests its own rows again, so every path issues the same loads.)
+      // attention, then its QKV rows: they land while the control wave reduces down_proj and
+      // gathers h (barrier a waits for them), so neither the qkv exchange's polls nor the
+      // attention window wait behind the K and V rows, and the m exchange's polls no longer wait
+      // behind the QKV rows.  Same-box A/B at context 1024: K and V requested in the layer's own
+      // windows (K before barrier c, V after it) 2,125 tok/s; K here 2,140; K and V here
+      // 2,151-2,152; the QKV rows here too instead of between the gate/up dot products 2,153
+      // (over contexts 129..1152: 2,177 -> 2,184).  (The last layer requests its own rows again,
+      // so every path issues the same loads.)
       if (nb > 0) kv_issue(a.k_cache + L_next * kv_layer_stride + (size_t)xcd * a.max_seq_len * Dm::D, 0);
       kv_issue_at(a.v_cache + L_next * kv_layer_stride + (size_t)xcd * a.max_seq_len * Dm::D, 0, 1);
+      prefetch_qkv_row(L_next, 0);
+      prefetch_qkv_row(L_next, 1);
     }
     cstamp(L, 11);
   }
