@@ -1359,8 +1359,10 @@ __global__ void __launch_bounds__(kSplitWaves * 64) attention_split(
       for (int hh = 0; hh < 2; hh++) {
         const float e = sc[r][hh] == -INFINITY ? 0.f : exp_acc(sc[r][hh] - m[hh]);
         l[hh] += e;
+        // a masked position (it loaded cache row 0, which the caller may not have written) leaves the
+        // sum untouched, so that a NaN there cannot enter it through 0 * NaN
 #pragma unroll
-        for (int i = 0; i < 8; i++) acc[hh][i] = __builtin_fmaf(e, vf[i], acc[hh][i]);
+        for (int i = 0; i < 8; i++) acc[hh][i] = p < pe ? __builtin_fmaf(e, vf[i], acc[hh][i]) : acc[hh][i];
       }
     }
   }

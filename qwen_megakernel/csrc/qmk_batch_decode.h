@@ -983,8 +983,10 @@ __device__ __forceinline__ void batch_compute(const BArgs& a, BSmem<M, B>& s, co
             // HF: softmax in fp32, probabilities rounded to bf16 before P@V; positions past the
             // range (which load row 0) get probability 0
             const float pr = pp < p.p_end[b] ? bf16r(exp_acc(sc[b][u][h] - gm[h]) * ginv[h]) : 0.f;
+            // a position past the range (it loaded cache row 0, which the caller may not have written)
+            // leaves the sum untouched, so that a NaN there cannot enter it through 0 * NaN
 #pragma unroll
-            for (int i = 0; i < 8; i++) acc[h][i] = __builtin_fmaf(pr, vf[i], acc[h][i]);
+            for (int i = 0; i < 8; i++) acc[h][i] = pp < p.p_end[b] ? __builtin_fmaf(pr, vf[i], acc[h][i]) : acc[h][i];
           }
         }
       }

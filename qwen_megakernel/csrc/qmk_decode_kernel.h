@@ -81,6 +81,13 @@ constexpr int kKvU = 2;        // attention: each wave covers 4 positions (16-la
 constexpr int kKvStages = 4;   // K/V batches in flight per wave (LDS ring)
 constexpr int kLongContext = 2048;  // contexts above this run decode_kernel<M, S, true>
 constexpr int kDeepContext = 12288; // contexts above this run decode_kernel_deep<M, S>
+// Short-context Qwen3-0.6B attention: false = HF's two passes (global max and sum exchanged, the
+// probabilities rounded to bf16 before P@V); true = split-K softmax in one window (unrounded
+// probabilities rescaled in the combine).
+constexpr bool kShortSplitK = false;
+// Short-context Qwen3-0.6B, two-pass form: this layer's gate/up and o_proj slices are requested at
+// barrier e (after the (max, sum) exchange) instead of barrier c.
+constexpr bool kWeightsAtE = true;
 
 template <class M>
 struct Dims {
@@ -1014,7 +1021,8 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
   // rows at c 1,955; the V rows requested before barrier c with the K rows
   // 1,943.  Those of this form are given where each request is issued.
   constexpr bool EARLY = !ST && !LONG;
-  constexpr bool SPLIT = EARLY;
+  constexpr bool SPLIT = EARLY && kShortSplitK;
+  constexpr bool W_AT_C = SPLIT || !kWeightsAtE;  // EARLY: this layer's gate/up and o_proj slices at barrier c
   static_assert(!EARLY || kLongContext / kGroupSize <= 32 * kKvU, "EARLY: at most one K/V batch per wave");
   prefetch_qkv(0);
   if (!ST && !EARLY) {
@@ -1093,7 +1101,7 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
     } else {
       if (nb > 0) kv_issue(kc, 0);
     }
-    if constexpr (SPLIT) {
+    if constexpr (EARLY) {
       QMK_SYNC();  // c
       cstamp(L, 2);
       // Layer 0's V rows into ring stage 1 (its K rows are in stage 0); later layers' K and V
@@ -1106,9 +1114,11 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
       // LDS at barrier c the two orders measure the same (2,178-2,180 either way; 2,155-2,156
       // against 2,152 at context 1024 with the slices first).
       if (L == 0) kv_issue_at(vc, 0, 1);
-      prefetch_gu(L);
-      prefetch_o(L);
-      constexpr int kLoadsC = Dm::GU_W * Dm::LH + Dm::OP * Dm::LO;  // weight loads issued after the V rows
+      if constexpr (W_AT_C) {
+        prefetch_gu(L);
+        prefetch_o(L);
+      }
+      constexpr int kLoadsC = W_AT_C ? Dm::GU_W * Dm::LH + Dm::OP * Dm::LO : 0;  // weight loads issued after the V rows
       // ---------------------------------------------- split-K attention over this wave's positions
       // Lane (slot, t16) holds dims 8*t16..+7 of position base0 + 32u + slot.  Scores as HF
       // rounds them; the softmax terms are exp(s - m) against the wave's own maximum m, kept in
@@ -1149,7 +1159,71 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
           m_w[h] = fmaxf(x, y);
         }
       }
-      wait_vmcnt_upto<kLoadsC>();  // the V rows have landed; the weight slices may stay in flight
+      // the V rows have landed (layer 0's were requested at c; the others before barrier a); the
+      // weight slices may stay in flight.  Waiting here, before any barrier, also tells the
+      // compiler that no LDS DMA is outstanding at the barriers that follow.
+      wait_vmcnt_upto<kLoadsC>();
+      if constexpr (!SPLIT) {
+        // HF's two passes: the wave's (max, sum of exp(s - max)) to the control wave, which merges the
+        // workgroups' pairs across the XCD (barriers d..e); then bf16(exp(s - M) / L) times V.
+        if (nb > 0) {
+#pragma unroll
+          for (int u = 0; u < U; u++) {
+            const int pp = base0 + 32 * u + slot;
+#pragma unroll
+            for (int h = 0; h < Dm::GQ; h++) l_w[h] += pp < p.p_end ? exp_acc(sc[u][h] - m_w[h]) : 0.f;
+          }
+        }
+#pragma unroll
+        for (int h = 0; h < Dm::GQ; h++) {
+          l_w[h] = rows_sum4(l_w[h]);  // the rows hold different positions, the lanes of a row the same one
+          if (lane == 0) {
+            s.wml[c][h][0] = m_w[h];
+            s.wml[c][h][1] = l_w[h];
+          }
+        }
+        cstamp(L, 3);
+        QMK_SYNC();  // d
+        QMK_SYNC();  // e
+        if constexpr (!W_AT_C) {
+          prefetch_gu(L);
+          prefetch_o(L);
+        }
+        cstamp(L, 4);
+        if (nb > 0) {
+          float gm[Dm::GQ], ginv[Dm::GQ];
+#pragma unroll
+          for (int h = 0; h < Dm::GQ; h++) {
+            gm[h] = s.ml[h][0];
+            ginv[h] = __fdiv_rn(1.0f, s.ml[h][1]);
+          }
+          const u32x4 v_now = *reinterpret_cast<const u32x4*>(s.v + 8 * t16);
+#pragma unroll
+          for (int u = 0; u < U; u++) {
+            const int pp = base0 + 32 * u + slot;
+            const u32x4 vx = pp == p.pos ? v_now : s.kv[1][c][u][lane];
+            const float vf[8] = {lo_bf16(vx.x), hi_bf16(vx.x), lo_bf16(vx.y), hi_bf16(vx.y),
+                                 lo_bf16(vx.z), hi_bf16(vx.z), lo_bf16(vx.w), hi_bf16(vx.w)};
+#pragma unroll
+            for (int h = 0; h < Dm::GQ; h++) {
+              // HF: softmax in fp32, probabilities rounded to bf16 before P@V; positions past the
+              // range (they load row 0) take probability 0 and their values are not used
+              const float pr = pp < p.p_end ? bf16r(exp_acc(sc[u][h] - gm[h]) * ginv[h]) : 0.f;
+#pragma unroll
+              for (int i = 0; i < 8; i++) acc[h][i] += pp < p.p_end ? pr * vf[i] : 0.f;
+            }
+          }
+        }
+#pragma unroll
+        for (int h = 0; h < Dm::GQ; h++) {
+#pragma unroll
+          for (int i = 0; i < 8; i++) acc[h][i] = rows_sum4(acc[h][i]);
+          if (lane < 16) {
+#pragma unroll
+            for (int i = 0; i < 8; i++) s.wacc[c][h][8 * t16 + i] = acc[h][i];
+          }
+        }
+      } else {
       if (nb > 0) {
         const u32x4 v_now = *reinterpret_cast<const u32x4*>(s.v + 8 * t16);
 #pragma unroll
@@ -1160,11 +1234,11 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
                                lo_bf16(vx.z), hi_bf16(vx.z), lo_bf16(vx.w), hi_bf16(vx.w)};
 #pragma unroll
           for (int h = 0; h < Dm::GQ; h++) {
-            // positions past the range load row 0 (finite) and get weight 0
+            // positions past the range load row 0 and get weight 0; their values are not used
             const float e = pp < p.p_end ? exp_acc(sc[u][h] - m_w[h]) : 0.f;
             l_w[h] += e;
 #pragma unroll
-            for (int i = 0; i < 8; i++) acc[h][i] = __builtin_fmaf(e, vf[i], acc[h][i]);
+            for (int i = 0; i < 8; i++) acc[h][i] = pp < p.p_end ? __builtin_fmaf(e, vf[i], acc[h][i]) : acc[h][i];
           }
         }
       }
@@ -1185,6 +1259,7 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
           s.wml[c][h][0] = m_w[h];
           s.wml[c][h][1] = l_w[h];
         }
+      }
       }
     } else {
       QMK_SYNC();  // c
@@ -1383,8 +1458,11 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
           // (head h of both) and values (one dimension of both), so one dot2
           // accumulates two positions; a position past the range has probability 0
           const int pp0 = base + slot, pp1 = base + 32 + slot;
-          const u32x4 v0 = pp0 == p.pos ? v_now : s.kv[j % kKvStages][c][0][lane];
-          const u32x4 v1 = pp1 == p.pos ? v_now : s.kv[j % kKvStages][c][1][lane];
+          // positions past the range loaded cache row 0, which the caller may not have written: their
+          // values are replaced by 0, so that a NaN there cannot reach the sum through 0 * NaN
+          const u32x4 zero = {0u, 0u, 0u, 0u};
+          const u32x4 v0 = pp0 == p.pos ? v_now : pp0 < p.p_end ? s.kv[j % kKvStages][c][0][lane] : zero;
+          const u32x4 v1 = pp1 == p.pos ? v_now : pp1 < p.p_end ? s.kv[j % kKvStages][c][1][lane] : zero;
           const uint32_t w0 = pp0 < p.p_end ? pw[8 * j + slot] : 0u;
           const uint32_t w1 = pp1 < p.p_end ? pw[8 * j + 4 + slot] : 0u;
           const bf16x2 pr[2] = {as_bf2(__builtin_amdgcn_perm(w1, w0, 0x05040100u)),
@@ -1650,7 +1728,7 @@ __device__ __forceinline__ void decode_body(const KArgs& a, S& s) {
   p.p_end = min(p.C, p.p_begin + p.chunk);
   p.n_act = (p.C + p.chunk - 1) / p.chunk;
   if (wave == 0) {
-    control_path<M, !LONG && !Dm::kStream>(a, s, p, b, lane);
+    control_path<M, !LONG && !Dm::kStream && kShortSplitK>(a, s, p, b, lane);
   } else if constexpr (LONG) {
     compute_path<M, SAMPLED, true, DEEP>(a, s, p, b, wave - 1, lane, s.sw[wave - 1], s.pw[wave - 1]);
   } else {

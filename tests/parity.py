@@ -22,25 +22,31 @@ ulp = 0.0156 apart, so the north star's gap < 1e-2 is an exact tie there):
 
 * ``LITERAL`` (0.999, 0.1, 1 ulp): the north star's bar, on workloads of at
   most four layers.
-* ``LAYERS28`` (0.999, 0.1, 2 ulps): 28-layer Qwen3-0.6B on real prompts
+* ``LAYERS28`` (0.999, 0.1, 1 ulp): 28-layer Qwen3-0.6B on real prompts
   (config 0, the benchmark's workload, prefill rows, batched steps).  The
-  kernel stays within 0.053 of the centre here, and HF's own fp32 path on
-  identical inputs within 0.047; the kernel's greedy token departed from the
-  centre's at 2-ulp gaps (steps 73 and 84 of the benchmark stream), HF's at 0
-  or 1 ulp over 1024 steps (and at 2 ulps on its own cache).
-* ``DEEP`` (0.998, 0.2, 4 ulps): 28 layers over N(0, 1) long-context caches,
-  and Qwen3-1.7B.  HF's own fp32 path, given the exact oracle's cache, is
-  itself this far from the centre on single steps: max abs 0.110 at 1500
-  positions (pinned by tests/test_oracle_exact.py), 0.117 with cosine down to
-  0.99915 at 8192, 0.117 on Qwen3-1.7B after a prompt and 0.172 with cosine
-  down to 0.99913 on Qwen3-1.7B over a 512-position cache.  No fp32
-  implementation holds the literal bar there; the kernel measures the same
-  (0.105-0.173, cosine down to 0.99893).  With logit errors of that size
-  (0.04 standard deviation per logit on Qwen3-1.7B), the top two logits trade
-  places across gaps of several ulps.  Swapping any single op class of the
-  exact oracle into fp32 (only RMSNorm, only the projections, only
-  attention) moves these logits by 0.08-0.13 as well: the excess is carried
-  by every op, through the model's amplification of bf16 rounding flips.
+  kernel stays within 0.05 of the centre here, and HF's own fp32 path on
+  identical inputs within 0.047.  A token may leave the centre's argmax
+  beyond one ulp only where the caller passes the step's fp32 envelope and
+  the gap is within it: the kernel departs at 2-ulp gaps at steps 73 and 84
+  of the benchmark stream (with HF's rounding of the softmax probabilities
+  as well as without), HF's path at 0 or 1 ulp there; both are fp32 orders
+  of the same sums, and the fp32 restatement's orders themselves are
+  0.04-0.05 from the centre on those steps.
+* ``ENVELOPE``, the fp32 envelope (:class:`Env`, :func:`envelope`): 28 layers over N(0, 1)
+  long-context caches, and Qwen3-1.7B.  There no fp32 implementation of the
+  reference path holds the literal 0.1: HF's own, given the exact oracle's
+  cache, is 0.110 away at 1500 positions and 0.117 at 8192; the fp32
+  restatement (oracle/qwen3_fp32.c) 0.10-0.22 on Qwen3-1.7B.  So each such
+  step is held to what fp32 implementations do on that step's inputs: the
+  restatement runs the step in four summation orders (pairwise tree, left to
+  right, eight interleaved sums, right to left), and the envelope is their
+  largest max abs error and smallest cosine against the centre.  The step's
+  logits must have cosine >= min(0.999, envelope - 0.0002) and max abs <=
+  max(0.1, 1.25 x envelope); its token may leave the centre's argmax only
+  where the gap is below 1e-2 or within the envelope's max abs.  HF's own
+  path meets that bound on every step measured (tests/test_oracle_fp32.py);
+  one summation order alone would not bound HF (HF's error is up to 1.5
+  times the pairwise tree's on the same step), which is why it takes four.
 
 A token stream is checked teacher-forced on the decoder's own tokens and
 cache: at every step the decoder's token must be the oracle's argmax given
@@ -57,16 +63,19 @@ import torch
 COS_MIN = 0.999
 ABS_MAX = 0.1
 TIE_GAP = 1e-2
+REL_ABS = 1.25   # relative bar: max abs within 1.25 x the fp32 envelope's (or 0.1)
+REL_COS = 2e-4   # relative bar: cosine within 0.0002 below the envelope's (or 0.999)
 
 
 class Bar:
-    def __init__(self, name: str, cos_min: float, abs_max: float, tie_ulps: int):
+    def __init__(self, name: str, cos_min: float, abs_max: float, tie_ulps: int, relative: bool = False):
         self.name, self.cos_min, self.abs_max, self.tie_ulps = name, cos_min, abs_max, tie_ulps
+        self.relative = relative  # logits and tokens against the step's fp32 envelope (:class:`Env`)
 
 
 LITERAL = Bar("literal", COS_MIN, ABS_MAX, 1)
-LAYERS28 = Bar("28 layers", COS_MIN, ABS_MAX, 2)
-DEEP = Bar("deep", 0.998, 0.2, 4)
+LAYERS28 = Bar("28 layers", COS_MIN, ABS_MAX, 1)
+ENVELOPE = Bar("fp32 envelope", COS_MIN, ABS_MAX, 0, relative=True)
 
 
 def bf16_ulp(x: float) -> float:
@@ -88,39 +97,136 @@ class Tally:
         self.cos = 1.0
         self.mab = 0.0
         self.flips = []
+        self.env = []  # rows checked against an fp32 envelope: (step, max abs / envelope, envelope)
+        self.env_flips = []  # departures beyond the bar's ulps, within the envelope: (step, gap in ulps, envelope)
 
     def __str__(self):
-        return (f"{self.what}: {self.rows} rows, worst cos {self.cos:.6f}, max abs {self.mab:.4f}, "
-                f"near-tie flips (step, gap in ulps) {self.flips}")
+        s = (f"{self.what}: {self.rows} rows, worst cos {self.cos:.6f}, max abs {self.mab:.4f}, "
+             f"near-tie flips (step, gap in ulps) {self.flips}")
+        if self.env:
+            worst = max(self.env, key=lambda e: e[1])
+            s += f", worst max abs / fp32 envelope {worst[1]} (step {worst[0]}, envelope {worst[2]})"
+        if self.env_flips:
+            s += f", departures covered by the fp32 envelope {self.env_flips}"
+        return s
 
 
-def check_row(t: Tally, label, ref: torch.Tensor, tok: int, got: torch.Tensor | None = None, bar: Bar = LITERAL):
-    """One step: ``ref`` the oracle's fp32 logits row, ``tok`` the decoder's token, ``got`` its logits."""
+class Env:
+    """The fp32 error envelope of one step: the fp32 restatement's max abs error and cosine against
+    the exact centre, per summation order, on the step's inputs (:func:`envelope`)."""
+
+    def __init__(self, errs, coss):
+        self.errs, self.coss = list(errs), list(coss)
+        self.abs = max(self.errs)   # the largest error of an fp32 order on this step
+        self.cos = min(self.coss)   # the smallest cosine
+
+    def abs_bound(self) -> float:
+        return max(ABS_MAX, REL_ABS * self.abs)
+
+    def cos_bound(self) -> float:
+        return min(COS_MIN, self.cos - REL_COS)
+
+    def __repr__(self):
+        return f"Env(abs {self.abs:.4f}, cos {self.cos:.6f})"
+
+
+def check_row(t: Tally, label, ref: torch.Tensor, tok: int, got: torch.Tensor | None = None, bar: Bar = LITERAL,
+              env=None):
+    """One step: ``ref`` the oracle's fp32 logits row, ``tok`` the decoder's token, ``got`` its logits.
+
+    ``env``: the step's fp32 envelope (an :class:`Env`, or a callable returning one, evaluated only
+    when needed).  With ``bar = ENVELOPE`` the bar is relative to what fp32 implementations of the
+    reference path do on the same inputs: cosine >= min(0.999, the envelope's cosine - 0.0002), max
+    abs <= max(0.1, 1.25 x the envelope's max abs), and a token may leave the oracle's argmax only
+    where the gap is below 1e-2 or within the envelope's max abs.  With a fixed bar, the logits are
+    held to it, and a token may leave the argmax where the gap is within max(1e-2, ``tie_ulps`` bf16
+    ulps) of the top, or, given ``env``, within the envelope's max abs."""
     ref = ref.float()
     t.rows += 1
+    envv = [env]
+
+    def get_env():
+        if callable(envv[0]):
+            envv[0] = envv[0]()
+        return envv[0]
+
+    if bar.relative and env is None:
+        raise ValueError("the fp32 envelope bar needs the step's envelope")
     if got is not None:
         got = got.float().cpu()
         cos = torch.nn.functional.cosine_similarity(got.double(), ref.double(), dim=0).item()
         mab = (got - ref).abs().max().item()
         t.cos, t.mab = min(t.cos, cos), max(t.mab, mab)
-        assert cos >= bar.cos_min, f"{t.what} {label}: cos {cos} ({bar.name} bar)"
-        assert mab <= bar.abs_max, f"{t.what} {label}: max abs {mab} ({bar.name} bar)"
+        if not bar.relative:
+            assert cos >= bar.cos_min, f"{t.what} {label}: cos {cos} ({bar.name} bar)"
+            assert mab <= bar.abs_max, f"{t.what} {label}: max abs {mab} ({bar.name} bar)"
+        else:
+            e = get_env()
+            t.env.append((label, round(mab / e.abs, 3), round(e.abs, 4)))
+            assert cos >= e.cos_bound(), f"{t.what} {label}: cos {cos} (fp32 envelope {e})"
+            assert mab <= e.abs_bound(), f"{t.what} {label}: max abs {mab} (fp32 envelope {e})"
     want = int(torch.argmax(ref))
     if tok != want:
         top = float(ref[want])
         assert 0 <= tok < ref.numel(), f"{t.what} {label}: token {tok} outside the vocabulary"
         gap = top - float(ref[tok])
-        assert gap <= tie_tolerance(top, bar.tie_ulps), (
+        allowed, why = (TIE_GAP, "") if bar.relative else (tie_tolerance(top, bar.tie_ulps), f"{bar.name} bar")
+        if gap > allowed and env is not None:
+            e = get_env()
+            allowed, why = max(allowed, e.abs), f"{why}, fp32 envelope {e}"
+            t.env_flips.append((label, round(gap / bf16_ulp(top), 2), round(e.abs, 4)))
+        assert gap <= allowed, (
             f"{t.what} {label}: token {tok} (oracle logit {float(ref[tok])}) != oracle argmax {want} "
-            f"(top {top}, gap {gap}, {bar.name} bar)")
+            f"(top {top}, gap {gap}, {why})")
         t.flips.append((label, round(gap / bf16_ulp(top), 2)))
 
 
-def check_rows(t: Tally, ref: torch.Tensor, toks, got: torch.Tensor | None = None, labels=None, bar: Bar = LITERAL):
+def check_rows(t: Tally, ref: torch.Tensor, toks, got: torch.Tensor | None = None, labels=None, bar: Bar = LITERAL,
+               envs=None):
     for i in range(len(toks)):
         check_row(t, labels[i] if labels is not None else i, ref[i], int(toks[i]),
-                  None if got is None else got[i], bar)
+                  None if got is None else got[i], bar, None if envs is None else envs[i])
     return t
+
+
+def fp32_oracle(weights, shape, max_seq_len: int, num_layers: int | None = None):
+    """The fp32 restatement (oracle/qwen3_fp32.py) on CPU ``weights``, with RoPE tables long enough
+    for ``max_seq_len``."""
+    from oracle.qwen3_fp32 import Fp32Oracle
+    from qwen_megakernel.weights import rope_tables
+
+    cos, sin = (None, None)
+    if weights["cos_table"].shape[0] < max_seq_len:
+        cos, sin = rope_tables(max_seq_len, shape.head_dim, shape.rope_theta)
+    return Fp32Oracle(weights, shape, max_seq_len=max_seq_len, num_layers=num_layers, cos=cos, sin=sin)
+
+
+def envelope(forc, k_cache, v_cache, p0: int, tokens, ref_rows: torch.Tensor):
+    """The fp32 envelope (:class:`Env`) of each row of ``tokens`` at positions p0.. over a decoder's
+    cache (``[L, NKV, S, D]``, any device, holding every row below p0 + len(tokens)): the fp32
+    restatement ``forc`` in each of its summation orders, each row over the same inputs as the
+    decoder's step, against ``ref_rows`` (the exact oracle's rows for the same steps)."""
+    from oracle.qwen3_fp32 import ORDERS
+
+    n = p0 + len(tokens)
+    forc.k_cache[:, :, :n] = k_cache[: forc.num_layers, :, :n].cpu()
+    forc.v_cache[:, :, :n] = v_cache[: forc.num_layers, :, :n].cpu()
+    ref = ref_rows.float()
+    errs, coss = [], []
+    for o in ORDERS:
+        forc.position = p0
+        lg = forc.forward(list(tokens), given_cache=True, order=o)
+        errs.append((lg - ref).abs().amax(-1).tolist())
+        coss.append(torch.nn.functional.cosine_similarity(lg.double(), ref.double(), dim=-1).tolist())
+    return [Env([e[i] for e in errs], [c[i] for c in coss]) for i in range(len(tokens))]
+
+
+def stream_envelopes(forc, k_cache, v_cache, p0: int, feed, ref_rows: torch.Tensor):
+    """Lazy envelopes for a stream whose row i is token feed[i] at position p0 + i: entry i, when
+    called, computes the envelope of that row alone (tokens are checked on every row, and the
+    envelope is needed only where a token leaves the oracle's argmax)."""
+    return [(lambda i=i: envelope(forc, k_cache, v_cache, p0 + i, [feed[i]], ref_rows[i:i + 1])[0])
+            for i in range(len(feed))]
 
 
 def exact_oracle(ew, shape, max_seq_len: int, num_layers: int | None = None, kv=None, cache_len: int = 0):

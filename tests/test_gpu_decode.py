@@ -15,19 +15,21 @@ import math
 import pytest
 import torch
 
-from parity import (DEEP, LAYERS28, LITERAL, Tally, check_kv_rows, check_rows, decoder, exact_oracle, kernel_stream,
-                    oracle_steps, stream_rows, with_rope)
+from parity import (ENVELOPE, LAYERS28, LITERAL, Tally, check_kv_rows, check_row, check_rows, decoder, envelope, exact_oracle,
+                    fp32_oracle, kernel_stream, oracle_steps, stream_envelopes, stream_rows, with_rope)
 
 pytestmark = pytest.mark.gpu
 
 
-def test_decode_parity_qwen3_0p6b(shape, exact06, weights_gpu, prompt):
-    """Config-0 shapes: 16-token prompt fed one step at a time, then 64 greedy steps; every row."""
+def test_decode_parity_qwen3_0p6b(shape, exact06, weights_cpu, weights_gpu, prompt):
+    """Config-0 shapes: 16-token prompt fed one step at a time, then 64 greedy steps; every row
+    (a token departure beyond one ulp only within the step's fp32 envelope)."""
     dec = decoder(weights_gpu)
     feed, toks, lgs = kernel_stream(dec, prompt, 64)
     orc = exact_oracle(exact06, shape, 2048)
     ref = oracle_steps(orc, dec._k_cache, dec._v_cache, 0, feed)
-    print(check_rows(Tally("qwen3-0.6b 16+64"), ref, toks, lgs, bar=LAYERS28))
+    envs = stream_envelopes(fp32_oracle(weights_cpu, shape, 2048), dec._k_cache, dec._v_cache, 0, feed, ref)
+    print(check_rows(Tally("qwen3-0.6b 16+64"), ref, toks, lgs, bar=LAYERS28, envs=envs))
     check_kv_rows("qwen3-0.6b 16+64", orc, dec._k_cache, dec._v_cache, 0, len(feed))
 
 
@@ -45,20 +47,23 @@ def test_decode_parity_random_norm_weights(shape, prompt):
     check_kv_rows("random norm weights", orc, dec._k_cache, dec._v_cache, 0, len(feed))
 
 
-def test_generate_nosync_matches_oracle_stream(shape, exact06, weights_gpu, prompt):
+def test_generate_nosync_matches_oracle_stream(shape, exact06, weights_cpu, weights_gpu, prompt):
     """The device-fed greedy stream (generate_nosync) is the oracle's, up to near-ties."""
     dec = decoder(weights_gpu)
     out = dec.generate(prompt, 64)
     assert len(out) == 64 and dec.position == len(prompt) - 1 + 64
     ref = stream_rows(exact_oracle(exact06, shape, 2048), dec._k_cache, dec._v_cache, prompt, out)
-    print(check_rows(Tally("generate 64"), ref, out, bar=LAYERS28))
+    n0 = len(prompt) - 1
+    envs = stream_envelopes(fp32_oracle(weights_cpu, shape, 2048), dec._k_cache, dec._v_cache, n0,
+                            [prompt[-1]] + out[:-1], ref)
+    print(check_rows(Tally("generate 64"), ref, out, bar=LAYERS28, envs=envs))
 
 
 @pytest.fixture(scope="module")
-def bench_workload(shape, exact06, weights_gpu):
+def bench_workload(shape, exact06, weights_cpu, weights_gpu):
     """The decode benchmark's workload: the seeded 128-token prompt (seed 1) through the batched
-    prefill, then 1024 device-fed greedy steps (contexts 129..1152), and the exact oracle's
-    logits for every row that produced a generated token."""
+    prefill, then 1024 device-fed greedy steps (contexts 129..1152), the exact oracle's logits for
+    every row that produced a generated token, and (lazily) the fp32 envelopes of those rows."""
     from qwen_megakernel.weights import make_prompt
 
     prompt = make_prompt(128, shape.vocab, seed=1)
@@ -72,20 +77,22 @@ def bench_workload(shape, exact06, weights_gpu):
     # over the kernel's cache; row n0-1 is the prefill's last row
     ref = oracle_steps(orc, dec._k_cache, dec._v_cache, 0, seq, emit=list(range(n0 - 1, len(seq))))
     check_kv_rows("1024-step stream", orc, dec._k_cache, dec._v_cache, 0, len(seq))
-    return prompt, out, ref
+    kc, vc = dec._k_cache.cpu(), dec._v_cache.cpu()
+    envs = stream_envelopes(fp32_oracle(weights_cpu, shape, 2048), kc, vc, n0, seq[n0:], ref[1:])
+    return prompt, out, ref, envs
 
 
 def test_bench_workload_1024_step_stream(bench_workload):
     """Every one of the 1024 generated tokens is the oracle's argmax given the same prefix (tokens
     and cache), up to near-ties: the stream is the greedy stream of its own history."""
-    prompt, out, ref = bench_workload
-    print(check_rows(Tally("1024-step stream"), ref[1:], out, bar=LAYERS28))
+    prompt, out, ref, envs = bench_workload
+    print(check_rows(Tally("1024-step stream"), ref[1:], out, bar=LAYERS28, envs=envs))
 
 
-def test_bench_workload_256_steps_with_logits(shape, exact06, weights_gpu, bench_workload):
+def test_bench_workload_256_steps_with_logits(shape, exact06, weights_cpu, weights_gpu, bench_workload):
     """The same prompt prefilled, then 256 decode steps (one launch each, logits out) on the
     decoder's own tokens: every row's logits within the bar, the prefill's last row too."""
-    prompt, out, ref = bench_workload
+    prompt, out, ref, _ = bench_workload
     n0 = len(prompt) - 1
     dec = decoder(weights_gpu)
     tok, lg = dec.prefill(prompt[:-1], return_logits=True)
@@ -100,7 +107,9 @@ def test_bench_workload_256_steps_with_logits(shape, exact06, weights_gpu, bench
     assert toks == out[:256], "step-by-step launches and the device-fed loop gave different streams"
     orc = exact_oracle(exact06, shape, 2048)
     rows = stream_rows(orc, dec._k_cache, dec._v_cache, prompt, toks)
-    print(check_rows(t, rows, toks, torch.stack(lgs), bar=LAYERS28))
+    envs = stream_envelopes(fp32_oracle(weights_cpu, shape, 2048), dec._k_cache, dec._v_cache, n0,
+                            [prompt[-1]] + toks[:-1], rows)
+    print(check_rows(t, rows, toks, torch.stack(lgs), bar=LAYERS28, envs=envs))
 
 
 @pytest.mark.parametrize(
@@ -109,13 +118,15 @@ def test_bench_workload_256_steps_with_logits(shape, exact06, weights_gpu, bench
      (32768, 28, 8)],
     ids=["1500-4layers", "1500-28layers", "2100-4layers", "2100-28layers", "8192-4layers", "8192-28layers",
          "12300-4layers", "32768-28layers"])
-def test_long_context_parity(shape, exact06, weights_gpu, c0, layers, steps):
+def test_long_context_parity(shape, exact06, weights_cpu, weights_gpu, c0, layers, steps):
     """Attention over an injected N(0,1) cache of c0 positions (split-K over the 32 workgroups of
     an XCD; above 2048 positions the long-context kernel runs, each wave streaming several K/V
     batches through the LDS ring; at 2100 wave 0 has a second, partial batch; above 12288 the
     deep form, which starts both passes with the ring full; at 12300 the waves have 7 and 6
     batches).  Every step against the exact oracle on the step's own inputs, and the K/V rows the
-    kernel appended."""
+    kernel appended.  Four layers: the literal bar.  28 layers, where no fp32 implementation holds
+    the literal 0.1 (tests/test_oracle_fp32.py): every step within the fp32 envelope of the same
+    step (tests/parity.py)."""
     from qwen_megakernel.weights import make_kv_prefill
 
     max_seq = c0 + 64
@@ -126,17 +137,21 @@ def test_long_context_parity(shape, exact06, weights_gpu, c0, layers, steps):
     assert torch.equal(dec._k_cache[:, :, :c0].cpu(), k[:layers, :, :c0])  # the injected rows are untouched
     orc = exact_oracle(exact06, shape, max_seq, num_layers=layers)
     ref = oracle_steps(orc, dec._k_cache, dec._v_cache, c0, feed)
-    print(check_rows(Tally(f"context {c0} x {layers} layers"), ref, toks, lgs, bar=DEEP if layers == 28 else LITERAL))
+    envs = None
+    if layers == 28:
+        envs = envelope(fp32_oracle(weights_cpu, shape, max_seq), dec._k_cache, dec._v_cache, c0, feed, ref)
+    print(check_rows(Tally(f"context {c0} x {layers} layers"), ref, toks, lgs, bar=ENVELOPE if envs else LITERAL, envs=envs))
     check_kv_rows(f"context {c0} x {layers} layers", orc, dec._k_cache, dec._v_cache, c0, len(feed))
 
 
 @pytest.mark.parametrize("c0", [8192, 32768], ids=["8192", "32768"])
-def test_long_context_256_step_stream(shape, exact06, weights_gpu, c0):
+def test_long_context_256_step_stream(shape, exact06, weights_cpu, weights_gpu, c0):
     """The long-context workload's full length: 256 device-fed greedy steps (generate_nosync, the
     long-form kernel) after an injected N(0,1) cache of c0 positions, 28 layers.  No device error;
-    rows 0, 63, 127, 191 and 255 of the stream are decoded again for their logits (each step
-    rewrites only its own K/V row, with the same values) and checked against the exact oracle on
-    the kernel's own cache and tokens, at the deep bar."""
+    every one of the 256 tokens is the exact oracle's argmax given the same prefix (one causal pass
+    of the oracle over the kernel's own cache and tokens), up to the fp32 envelope of that step;
+    rows 0, 63, 127, 191 and 255 are decoded again for their logits (each step rewrites only its own
+    K/V row, with the same values) and checked within the fp32 envelope of the same step."""
     from qwen_megakernel.weights import make_kv_prefill
 
     steps, max_seq = 256, c0 + 272
@@ -156,11 +171,16 @@ def test_long_context_256_step_stream(shape, exact06, weights_gpu, c0):
         assert tok == out[i], f"step {i}: the repeated step gave {tok}, the stream {out[i]}"
         lgs.append(lg.cpu())
     del k, v
+    kc, vc = dec._k_cache.cpu(), dec._v_cache.cpu()
+    del dec
     orc = exact_oracle(exact06, shape, max_seq)
-    t = Tally(f"context {c0}, 256-step stream, rows {rows}")
+    ref = oracle_steps(orc, kc, vc, c0, feed)  # every row of the stream
+    forc = fp32_oracle(weights_cpu, shape, max_seq)
+    t = Tally(f"context {c0}, 256-step stream")
+    check_rows(t, ref, out, bar=ENVELOPE, envs=stream_envelopes(forc, kc, vc, c0, feed, ref))
     for j, i in enumerate(rows):
-        ref = oracle_steps(orc, dec._k_cache, dec._v_cache, c0 + i, [feed[i]])
-        check_rows(t, ref, [out[i]], lgs[j][None], labels=[i], bar=DEEP)
+        env = envelope(forc, kc, vc, c0 + i, [feed[i]], ref[i:i + 1])[0]
+        check_row(t, ("logits", i), ref[i], out[i], lgs[j], bar=ENVELOPE, env=env)
     print(t)
 
 

@@ -1,18 +1,23 @@
 """Qwen3-1.7B shape (hidden 2048, MLP 6144) on the same kernels: parity with the exact CPU oracle.
 
-Same bar as tests/test_gpu_decode.py (tests/parity.py): every step on the
-inputs the kernel's step had, cosine >= 0.999 and max abs <= 0.1, tokens equal
-to the oracle's argmax except at near-ties, K/V rows equal up to rounding.
-Covers the 1.7B workload of the benchmark: one sequence after a 512-token
-prompt, and four sequences with their own 512-token prompts decoded together
-by the batched step.
+Every step on the inputs the kernel's step had, against the exact oracle
+(tests/parity.py).  Over 28 layers of this shape no fp32 implementation of
+the reference path holds the literal 0.1 (the fp32 restatement is 0.10-0.22
+from the centre on identical inputs), so 28-layer rows are held to the fp32
+envelope of the same step: cosine >= min(0.999, envelope - 0.0002), max abs
+<= max(0.1, 1.25 x the envelope), tokens equal to the oracle's argmax except
+where the gap is within 1e-2 or the envelope.  Four-layer rows: the literal
+bar.  K/V rows equal up to rounding.  Covers the 1.7B workload of the
+benchmark: one sequence after a 512-token prompt, and four sequences with
+their own 512-token prompts decoded together by the batched step, each
+256-step stream checked token by token.
 """
 
 import pytest
 import torch
 
-from parity import (DEEP, LITERAL, Tally, check_kv_rows, check_rows, decoder, exact_oracle, kernel_stream,
-                    oracle_steps, stream_rows, with_rope)
+from parity import (ENVELOPE, LITERAL, Tally, check_kv_rows, check_row, check_rows, decoder, envelope, exact_oracle, fp32_oracle,
+                    kernel_stream, oracle_steps, stream_envelopes, stream_rows, with_rope)
 
 pytestmark = pytest.mark.gpu
 
@@ -44,7 +49,8 @@ def test_qwen3_1p7b_decode_parity(w17, exact17):
     feed, toks, lgs = kernel_stream(dec, make_prompt(8, QWEN3_1_7B.vocab, seed=1), 32)
     orc = exact_oracle(exact17, QWEN3_1_7B, 1024)
     ref = oracle_steps(orc, dec._k_cache, dec._v_cache, 0, feed)
-    print(check_rows(Tally("qwen3-1.7b 8+32"), ref, toks, lgs, bar=DEEP))
+    envs = envelope(fp32_oracle(w17[0], QWEN3_1_7B, 1024), dec._k_cache, dec._v_cache, 0, feed, ref)
+    print(check_rows(Tally("qwen3-1.7b 8+32"), ref, toks, lgs, bar=ENVELOPE, envs=envs))
     check_kv_rows("qwen3-1.7b 8+32", orc, dec._k_cache, dec._v_cache, 0, len(feed))
 
 
@@ -63,9 +69,14 @@ def test_qwen3_1p7b_512_token_prompt(w17, exact17):
     gen = toks + rest
     orc = exact_oracle(exact17, QWEN3_1_7B, 1024)
     ref = stream_rows(orc, dec._k_cache, dec._v_cache, prompt, gen)
+    p0 = len(prompt) - 1  # the position of the row that produced gen[0]
+    envs = envelope(fp32_oracle(w17[0], QWEN3_1_7B, 1024), dec._k_cache, dec._v_cache, p0, feed, ref[:32])
     t = Tally("qwen3-1.7b 512-token prompt")
-    check_rows(t, ref[:32], toks, lgs, bar=DEEP)
-    print(check_rows(t, ref[32:], rest, labels=list(range(32, 64)), bar=DEEP))
+    check_rows(t, ref[:32], toks, lgs, bar=ENVELOPE, envs=envs)
+    forc = fp32_oracle(w17[0], QWEN3_1_7B, 1024)
+    seq = [prompt[-1]] + gen[:-1]
+    print(check_rows(t, ref[32:], rest, labels=list(range(32, 64)), bar=ENVELOPE,
+                     envs=stream_envelopes(forc, dec._k_cache, dec._v_cache, p0, seq, ref)[32:]))
     check_kv_rows("qwen3-1.7b 512-token prompt", orc, dec._k_cache, dec._v_cache, 0, len(prompt) + 63)
 
 
@@ -83,7 +94,10 @@ def test_qwen3_1p7b_context(w17, exact17, c0, layers):
     feed, toks, lgs = kernel_stream(dec, [11, 22], 8)
     orc = exact_oracle(exact17, QWEN3_1_7B, max_seq, num_layers=layers)
     ref = oracle_steps(orc, dec._k_cache, dec._v_cache, c0, feed)
-    print(check_rows(Tally(f"qwen3-1.7b context {c0} x {layers} layers"), ref, toks, lgs, bar=DEEP if layers == 28 else LITERAL))
+    envs = None
+    if layers == 28:
+        envs = envelope(fp32_oracle(w17[0], QWEN3_1_7B, max_seq), dec._k_cache, dec._v_cache, c0, feed, ref)
+    print(check_rows(Tally(f"qwen3-1.7b context {c0} x {layers} layers"), ref, toks, lgs, bar=ENVELOPE if envs else LITERAL, envs=envs))
     check_kv_rows(f"qwen3-1.7b context {c0}", orc, dec._k_cache, dec._v_cache, c0, len(feed))
 
 
@@ -108,10 +122,13 @@ def test_qwen3_1p7b_batch4_512_token_prompts(w17, exact17):
             toks[b].append(nxt[b])
             lgs[b].append(logits[b].cpu())
     assert bd.positions == [512 + steps] * B
+    forc = fp32_oracle(w17[0], QWEN3_1_7B, 1024)
     for b in range(B):
         orc = exact_oracle(exact17, QWEN3_1_7B, 1024)
         ref = stream_rows(orc, bd._k_cache[b], bd._v_cache[b], prompts[b], toks[b])
-        print(check_rows(Tally(f"qwen3-1.7b batch-4 sequence {b}"), ref, toks[b], torch.stack(lgs[b]), bar=DEEP))
+        seq = [prompts[b][-1]] + toks[b][:-1]  # the rows at positions 511.. (the prefill's last, then the steps)
+        envs = envelope(forc, bd._k_cache[b], bd._v_cache[b], 511, seq, ref)
+        print(check_rows(Tally(f"qwen3-1.7b batch-4 sequence {b}"), ref, toks[b], torch.stack(lgs[b]), bar=ENVELOPE, envs=envs))
         check_kv_rows(f"qwen3-1.7b batch-4 sequence {b}", orc, bd._k_cache[b], bd._v_cache[b], 0, 512 + steps)
 
 
@@ -138,18 +155,30 @@ def test_qwen3_1p7b_generate_matches_steps(w17):
 def test_qwen3_1p7b_256_step_streams_batch1_and_batch4(w17, exact17):
     """The Qwen3-1.7B workload's full length: 256 device-fed greedy steps after 512-token prompts,
     at batch 1 (the decode megakernel, generate_nosync) and at batch 4 (BatchDecoder.decode_steps,
-    the batched persistent kernel), 28 layers.  No device error; rows 0, 85, 170 and 255 of every
-    stream are decoded again for their logits (each step rewrites only its own K/V rows, with the
-    same values) and checked against the exact oracle on the decoder's own cache and tokens, at
-    the deep bar."""
+    the batched persistent kernel), 28 layers.  No device error; every token of every stream is the
+    exact oracle's argmax given the same prefix (one causal pass of the oracle over the decoder's
+    own cache and tokens per stream), up to the fp32 envelope of that step; rows 0, 85, 170 and 255
+    of every stream are decoded again for their logits (each step rewrites only its own K/V rows,
+    with the same values) and checked within the fp32 envelope of the same step."""
     from qwen_megakernel.model import BatchDecoder
     from qwen_megakernel.shapes import QWEN3_1_7B as S
     from qwen_megakernel.weights import make_prompt
 
-    _, wg = w17
+    w, wg = w17
     ops = torch.ops.qwen_megakernel_C
     steps, max_seq, rows = 256, 1024, [0, 85, 170, 255]
-    t = Tally("qwen3-1.7b 256-step streams, rows " + str(rows))
+    t = Tally("qwen3-1.7b 256-step streams")
+    orc = exact_oracle(exact17, S, max_seq)
+    forc = fp32_oracle(w, S, max_seq)
+
+    def check_stream(label, kc, vc, p0, feed, out, logit_rows):
+        """Every token of the stream (feed[i] at p0 + i gave out[i]); logit_rows: {i: logits}."""
+        ref = oracle_steps(orc, kc, vc, p0, feed)
+        check_rows(t, ref, out, labels=[(label, i) for i in range(len(out))], bar=ENVELOPE,
+                   envs=stream_envelopes(forc, kc, vc, p0, feed, ref))
+        for i, lg in logit_rows.items():
+            env = envelope(forc, kc, vc, p0 + i, [feed[i]], ref[i:i + 1])[0]
+            check_row(t, (label, "logits", i), ref[i], out[i], lg, bar=ENVELOPE, env=env)
 
     # batch 1
     prompt = make_prompt(512, S.vocab, seed=1)
@@ -160,13 +189,13 @@ def test_qwen3_1p7b_256_step_streams_batch1_and_batch4(w17, exact17):
                               dec._attn_scale).cpu().tolist()
     assert int(ops.device_error()) == 0
     feed = [prompt[-1]] + out[:-1]
-    orc = exact_oracle(exact17, S, max_seq)
+    lgs = {}
     for i in rows:
         dec._position = p0 + i
         tok, lg = dec.step_logits(feed[i])
         assert tok == out[i]
-        ref = oracle_steps(orc, dec._k_cache, dec._v_cache, p0 + i, [feed[i]])
-        check_rows(t, ref, [out[i]], lg.cpu()[None], labels=[f"batch 1 step {i}"], bar=DEEP)
+        lgs[i] = lg.cpu()
+    check_stream("batch 1", dec._k_cache.cpu(), dec._v_cache.cpu(), p0, feed, out, lgs)
     del dec
 
     # batch 4
@@ -177,6 +206,7 @@ def test_qwen3_1p7b_256_step_streams_batch1_and_batch4(w17, exact17):
     start = bd.positions
     log = bd.decode_steps(torch.tensor(first, dtype=torch.int32, device="cuda"), steps).cpu()
     assert int(ops.device_error()) == 0 and int(log.min()) >= 0
+    lgs = [dict() for _ in range(B)]
     for i in rows:
         toks = log[i].tolist()  # the inputs of step i; log[i + 1] follows them
         out_t = torch.empty(B, dtype=torch.int32, device="cuda")
@@ -187,6 +217,8 @@ def test_qwen3_1p7b_256_step_streams_batch1_and_batch4(w17, exact17):
                            max(pos) + 1)
         assert out_t.cpu().tolist() == log[i + 1].tolist()
         for b in range(B):
-            ref = oracle_steps(orc, bd._k_cache[b], bd._v_cache[b], pos[b], [toks[b]])
-            check_rows(t, ref, [int(log[i + 1][b])], lg[b].cpu()[None], labels=[f"batch 4 seq {b} step {i}"], bar=DEEP)
+            lgs[b][i] = lg[b].cpu()
+    for b in range(B):
+        check_stream(f"batch 4 seq {b}", bd._k_cache[b].cpu(), bd._v_cache[b].cpu(), start[b],
+                     log[:steps, b].tolist(), log[1:, b].tolist(), lgs[b])
     print(t)
