@@ -350,6 +350,8 @@ size_t qmk_decode_batch_workspace_bytes(int model, int batch, int max_context);
  * max_context <= 4096 run five fused launches per layer (RMSNorm in the GEMM
  * prologues, q/k norm + RoPE + K/V append inside attention, residual and
  * SiLU*up in the GEMM epilogues).  Invalid ids or positions emit -1.
+ * tokens and positions may share memory with out_tokens (an in-place step):
+ * such calls take the multi-launch path, which reads them before writing.
  * Asynchronous; returns a status code. */
 int qmk_decode_batch(
     int model, int batch, const int *tokens, const int *positions, int *out_tokens,
@@ -365,12 +367,16 @@ int qmk_decode_batch(
  * 2 <= batch <= 4 and max_context <= 2048.  The 256 workgroups of the decode
  * kernel stream each weight slice once and apply it to all `batch` rows;
  * activations move between workgroups through the per-stream exchange area
- * (allocated on the stream's first call).  tokens and positions must not
- * overlap out_tokens, which receives -1 first, so a step that fails on the
- * device (qmk_device_error) leaves -1.  Returns QMK_ERR_DEVICE where the
- * kernel does not fit one workgroup per CU; qmk_decode_batch then keeps its
- * multi-launch path.  No counterpart in the reference, which decodes one
- * sequence (qwen_megakernel/model.py:111-250).  Asynchronous. */
+ * (allocated on the stream's first call).  The layer table is copied to
+ * device memory once per distinct table (up to 64 per device, kept until the
+ * process ends).  tokens and positions must not overlap out_tokens, which
+ * receives -1 first, so a step that fails on the device (qmk_device_error)
+ * leaves -1 (QMK_ERR_ARG otherwise).  Returns QMK_ERR_DEVICE where the kernel
+ * does not fit one workgroup per CU, or where a new table cannot be copied
+ * now (the stream is being captured, or 64 tables are kept);
+ * qmk_decode_batch then keeps its multi-launch path.  No counterpart in the
+ * reference, which decodes one sequence (qwen_megakernel/model.py:111-250).
+ * Asynchronous. */
 int qmk_decode_batch_persistent(
     int model, int batch, const int *tokens, const int *positions, int *out_tokens,
     float *logits_out, const void *embed_weight,

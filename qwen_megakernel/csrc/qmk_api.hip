@@ -20,6 +20,7 @@
 #include <map>
 #include <mutex>
 #include <utility>
+#include <vector>
 
 #include "../../include/qwen_megakernel.h"
 #include "qmk_batch_decode.h"
@@ -108,7 +109,16 @@ struct DevInfo {
   bool order_multi = false;            // a second stream has launched on this device
   uint32_t* scratch = nullptr;         // this device's copy of `scratch` (set by qmk_init)
   bool batch_ok = false;               // every batched persistent kernel fits one workgroup per CU
+  // device copies of the layer tables the batched persistent kernel was called with (device_table)
+  struct Table {
+    std::vector<LayerPtrs> host;
+    LayerPtrs* dev = nullptr;
+  };
+  std::mutex table_mu;
+  std::vector<Table> tables;
 };
+
+constexpr size_t kMaxTables = 64;  // distinct batched layer tables kept per device
 
 std::mutex g_mu;
 std::map<std::pair<int, hipStream_t>, Ctx*> g_ctx;
@@ -606,6 +616,37 @@ int launch_batch(int batch, const BArgs& a, hipStream_t stream) {
   return hipGetLastError() == hipSuccess ? QMK_OK : QMK_ERR_HIP;
 }
 
+// The device copy of a batched step's layer table (num_layers entries): uploaded once per distinct
+// table with a synchronous copy into a new buffer, which no kernel reads yet, and kept until the
+// process ends.  QMK_ERR_DEVICE (the caller takes the multi-launch path) where no copy can be made
+// now: on a stream under capture, or with kMaxTables tables already kept.
+int device_table(DevInfo* di, const LDGLayerWeights* host, int num_layers, hipStream_t stream,
+                 const LayerPtrs** out) {
+  static_assert(sizeof(LayerPtrs) == sizeof(LDGLayerWeights), "layer table layout");
+  const size_t bytes = (size_t)num_layers * sizeof(LayerPtrs);
+  std::lock_guard<std::mutex> lk(di->table_mu);
+  for (const DevInfo::Table& t : di->tables)
+    if ((int)t.host.size() == num_layers && std::memcmp(t.host.data(), host, bytes) == 0) {
+      *out = t.dev;
+      return QMK_OK;
+    }
+  if (di->tables.size() >= kMaxTables) return QMK_ERR_DEVICE;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(stream, &cs) != hipSuccess) return QMK_ERR_HIP;
+  if (cs != hipStreamCaptureStatusNone) return QMK_ERR_DEVICE;
+  DevInfo::Table t;
+  t.host.resize((size_t)num_layers);
+  std::memcpy(t.host.data(), host, bytes);
+  if (hipMalloc(&t.dev, bytes) != hipSuccess) return QMK_ERR_HIP;
+  if (hipMemcpy(t.dev, t.host.data(), bytes, hipMemcpyHostToDevice) != hipSuccess) {
+    hipFree(t.dev);
+    return QMK_ERR_HIP;
+  }
+  *out = t.dev;
+  di->tables.push_back(std::move(t));
+  return QMK_OK;
+}
+
 bool ranges_overlap(const void* a, size_t an, const void* b, size_t bn) {
   const char* pa = static_cast<const char*>(a);
   const char* pb = static_cast<const char*>(b);
@@ -636,14 +677,13 @@ int batch_persistent_impl(int model, int batch, const int* tokens, const int* po
                          w.gate_proj_weight, w.up_proj_weight, w.down_proj_weight};
     for (const void* q : p)
       if (!q) return QMK_ERR_ARG;
-    static_assert(sizeof(LayerPtrs) == sizeof(LDGLayerWeights), "layer table layout");
-    std::memcpy(&a.layers[L], &w, sizeof(LayerPtrs));
   }
   Ctx* ctx = nullptr;
   int s = get_ctx(stream, &ctx);
   if (s != QMK_OK) return s;
   if (!ctx->dev->batch_ok) return QMK_ERR_DEVICE;
   if ((s = poisoned(ctx)) != QMK_OK) return s;
+  if ((s = device_table(ctx->dev, layer_weights_host, num_layers, stream, &a.layers)) != QMK_OK) return s;
   if (!ctx->bx) {
     const size_t bytes = sizeof(DecodeState) + (size_t)kBXWords * 4;
     void* mem = nullptr;

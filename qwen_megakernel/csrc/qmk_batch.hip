@@ -1855,7 +1855,16 @@ int qmk_decode_batch(int model, int batch, const int* tokens, const int* positio
     for (const void* q : p)
       if (!q) return QMK_ERR_ARG;
   }
-  if (qmk_batch_persistent_enabled() && batch >= kBatchMin && batch <= kBatchMax && max_context <= kBatchMaxContext) {
+  // The persistent kernel writes out_tokens (-1) before every workgroup has read tokens and
+  // positions, so a call whose out_tokens overlaps them takes the multi-launch path, which reads
+  // them first.
+  const auto overlaps = [&](const void* p) {
+    const char* a = static_cast<const char*>(p);
+    const char* o = reinterpret_cast<const char*>(out_tokens);
+    return a < o + batch * sizeof(int) && o < a + batch * sizeof(int);
+  };
+  if (qmk_batch_persistent_enabled() && batch >= kBatchMin && batch <= kBatchMax && max_context <= kBatchMaxContext &&
+      !overlaps(tokens) && !overlaps(positions)) {
     const int s = qmk_decode_batch_persistent(model, batch, tokens, positions, out_tokens, logits_out, embed_weight,
                                               layer_weights_host, final_norm_weight, lm_head_weight, cos_table,
                                               sin_table, k_cache, v_cache, seq_stride, num_layers, max_seq_len,

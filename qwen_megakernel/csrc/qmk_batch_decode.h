@@ -44,52 +44,6 @@ constexpr int kBatchMin = 2, kBatchMax = 4;
 constexpr int kBatchMaxContext = kGroupSize * 32 * kKvU;  // 2048: one K/V batch per wave and sequence
 constexpr uint32_t kNoChunk = 0xffffffffu;
 
-// Eight sums over the wave at once: lanes 8k..8k+7 receive the sum over all 64
-// lanes of v[k].  Each step halves the values a lane carries and adds its
-// partner's copy of the ones it keeps: the half-wave swap (lanes l, l ^ 32) and
-// the row-pair swap (l, l ^ 16) on the gfx950 permlane swaps, a rotation by 8
-// inside each 16-lane row (l, l ^ 8) on DPP; three DPP adds then sum each group
-// of eight lanes.  About 20 instructions for eight sums, against about 90 for
-// eight separate wave reductions.
-__device__ __forceinline__ float wave_sum8(const float (&v)[8], int lane) {
-  float w[4];
-#pragma unroll
-  for (int j = 0; j < 4; j++) {
-    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[j]), __float_as_uint(v[j + 4]), false, false);
-    w[j] = __uint_as_float(r[0]) + __uint_as_float(r[1]);  // lanes 0-31: v[j], lanes 32-63: v[j + 4]
-  }
-  float z[2];
-#pragma unroll
-  for (int j = 0; j < 2; j++) {
-    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(w[j]), __float_as_uint(w[j + 2]), false, false);
-    z[j] = __uint_as_float(r[0]) + __uint_as_float(r[1]);  // even rows: w[j], odd rows: w[j + 2]
-  }
-  const bool hi = (lane & 8) != 0;
-  float x = (hi ? z[1] : z[0]) + dpp_get<0x128>(hi ? z[0] : z[1]);  // row_ror:8, i.e. lane ^ 8
-  x = dpp_add<0xB1>(x);   // quad_perm [1,0,3,2]
-  x = dpp_add<0x4E>(x);   // quad_perm [2,3,0,1]
-  x = dpp_add<0x141>(x);  // row_half_mirror: the other quad of the eight lanes
-  return x;
-}
-
-// This lane's share of a row's dot product (NL 16-byte chunks of weights and activations).
-template <int NL>
-__device__ __forceinline__ float row_part(const u32x4* w, const u32x4 (&x)[NL]) {
-  float acc = 0.f;
-#pragma unroll
-  for (int j = 0; j < NL; j++) acc = dot8(w[j], x[j], acc);
-  return acc;
-}
-
-// One 4-byte word at word index ``w``, same scopes as put4.
-__device__ __forceinline__ void put1(uint32_t* buf, uint32_t w, uint32_t v, bool device) {
-  auto rs = make_rsrc(buf, 0x7fffffffu);
-  if (device)
-    __builtin_amdgcn_raw_buffer_store_b32(v, rs, w * 4u, 0, 0x10 /* sc1 */);
-  else
-    __builtin_amdgcn_raw_buffer_store_b32(v, rs, w * 4u, 0, 0);
-}
-
 template <class M, int B>
 struct BDims {
   using D1 = Dims<M>;
@@ -121,10 +75,10 @@ struct BDims {
   static_assert(X_WORDS % 4 == 0, "alignment");
 };
 
-// Kernel arguments.  The layer table travels by value (28 x 88 bytes), so the
-// launch needs no device copy of it.
+// Kernel arguments.  The layer table is a device copy (num_layers x 88 bytes) that the host library
+// uploads once per distinct table, as the decode kernel's is; the kernel copies it into LDS.
 struct BArgs {
-  LayerPtrs layers[kMaxLayers];
+  const LayerPtrs* layers;
   const uint16_t* embed;
   const uint16_t* final_norm;
   const uint16_t* lm_head;

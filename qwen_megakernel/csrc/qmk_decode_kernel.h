@@ -85,9 +85,12 @@ constexpr int kDeepContext = 12288; // contexts above this run decode_kernel_dee
 // probabilities rounded to bf16 before P@V); true = split-K softmax in one window (unrounded
 // probabilities rescaled in the combine).
 constexpr bool kShortSplitK = false;
-// Short-context Qwen3-0.6B, two-pass form: this layer's gate/up and o_proj slices are requested at
-// barrier e (after the (max, sum) exchange) instead of barrier c.
-constexpr bool kWeightsAtE = true;
+// Short-context Qwen3-0.6B, two-pass form: this layer's gate/up slice is requested at barrier c
+// (it drains during the scores and the (max, sum) exchange) and its o_proj slice at barrier e
+// (during P@V).  Same-box A/B at context 1024: both at c 1,999 tok/s, both at e 2,010, gate/up at c
+// and o_proj at e 2,062.  A pause of 0.25-1 us between the down_proj partials' publish and the next
+// layer's K/V and QKV-row requests measured 2,064 / 2,065 / 2,044 against 2,061.
+constexpr bool kGateUpAtC = true, kOprojAtC = false;
 
 template <class M>
 struct Dims {
@@ -110,7 +113,7 @@ struct Dims {
   static constexpr int LM_RPW = (V + kNumWG - 1) / kNumWG;
   static constexpr int LM_U = 8 / LH;           // LM-head rows per wave per batch (two batches in flight)
   static constexpr int NX = 9;                  // exchanges per layer
-  static constexpr int OUT = 2 * M_WG > 32 ? 2 * M_WG : 32;  // per-workgroup results handed to the control wave
+  static constexpr int OUT = 2 * M_WG > 64 ? 2 * M_WG : 64;  // per-workgroup results handed to the control wave
   // Weight prefetch.  When a workgroup's share of a layer fits the compute
   // waves' registers (Qwen3-0.6B: 120 KB per workgroup), every phase's slice is
   // requested one layer ahead into its own registers.  Otherwise (Qwen3-1.7B:
@@ -291,6 +294,7 @@ struct Ctl {
   __device__ bool gather(uint32_t tag, Off&& off, F&& sink) {
     constexpr int NC = (NCH + 63) / 64;
     static_assert(NC <= 16, "gather size");
+    if (s.abort_flag) return false;  // an earlier wait of this workgroup expired: go to the next barrier
     auto rs = make_rsrc(a.x, 0x7fffffffu);
     uint32_t o[NC];
     uint32_t pend = 0;
@@ -338,6 +342,22 @@ struct Ctl {
   __device__ bool gather_range(uint32_t base, uint32_t tag, F&& sink) {
     static_assert(NW % 4 == 0, "whole chunks");
     return gather<NW / 4>(tag, [&](int i) { return base + 4u * (uint32_t)i; }, sink);
+  }
+
+  // gather sinks: chunk ci (four bf16 payloads) to fp32 dst[4ci..4ci+3], or to bf16 dst[4ci..]
+  static __device__ auto to_f32(float* dst) {
+    return [dst](int ci, u32x4 v) {
+      float* d = dst + 4 * ci;
+      d[0] = bf16_to_f32(v.x >> 16); d[1] = bf16_to_f32(v.y >> 16);
+      d[2] = bf16_to_f32(v.z >> 16); d[3] = bf16_to_f32(v.w >> 16);
+    };
+  }
+  static __device__ auto to_bf16(uint16_t* dst) {
+    return [dst](int ci, u32x4 v) {
+      uint32_t* d = reinterpret_cast<uint32_t*>(dst) + 2 * ci;
+      d[0] = (v.x >> 16) | (v.y & 0xffff0000u);
+      d[1] = (v.z >> 16) | (v.w & 0xffff0000u);
+    };
   }
 
   __device__ void put(bool local, uint32_t w, u32x4 d) {
@@ -620,6 +640,79 @@ __device__ __forceinline__ uint32_t orderable16(uint32_t h) { return (h & 0x8000
     if (s.abort_flag) return; \
   } while (0)
 
+// The step's end, control wave: gather the last layer's output h (exchange words at x_h, this XCD's
+// copy), final RMSNorm into LDS for the compute waves' LM-head rows (barrier final a), then (after
+// barrier final b) publish this workgroup's best (logit, row) key at x_key; workgroup 0 gathers the
+// 256 keys, writes the token and advances the stream state.
+template <class M>
+__device__ __forceinline__ void final_control(Ctl<M>& ctl, const KArgs& a, Smem<M>& s, const Step& p, int b, int lane,
+                                              uint32_t x_h, uint32_t x_key) {
+  using Dm = Dims<M>;
+  const int xcd = b & (kGroups - 1);
+  auto stamp = [&](int point) {
+    if (a.trace && lane == 0) a.trace[(size_t)point * kNumWG + b] = wall_clock64();
+  };
+  const auto nw_final = ctl.load_norm(a.final_norm);
+  if (ctl.template gather_range<Dm::H>(x_h + xcd * Dm::H, make_tag(p.epoch, (uint32_t)((p.nl - 1) * Dm::NX + 8)),
+                                              Ctl<M>::to_f32(s.x))) {
+    ctl.rmsnorm(s.x, nw_final);
+    if (b == 0) {
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      for (int i = lane; i < Dm::H; i += 64) {
+        if (a.hidden_out) a.hidden_out[i] = (uint16_t)f32_to_bf16(s.x[i]);
+        if (a.normalized_out) a.normalized_out[i] = bf16_to_f32(s.n[i]);
+      }
+    }
+  }
+  stamp(p.nl * kTracePoints + 0);
+  QMK_SYNC();  // final a
+  QMK_SYNC();  // final b
+  stamp(p.nl * kTracePoints + 1);
+  const uint32_t tk = make_tag(p.epoch, (uint32_t)(p.nl * Dm::NX));
+  if (lane == 0) {
+    uint64_t best = 0;
+#pragma unroll
+    for (int cc = 0; cc < kComputeWaves; cc++) best = s.best[cc] > best ? s.best[cc] : best;
+    const uint32_t idx = 0xffffffffu - (uint32_t)best;
+    const uint32_t score32 = (uint32_t)(best >> 32);
+    u32x4 d;
+    d.x = word(score32 >> 16, tk);
+    d.y = word(idx & 0xffffu, tk);
+    d.z = word(idx >> 16, tk);
+    d.w = word(score32 & 0xffffu, tk);
+    put4<true>(a.x, x_key + 4 * b, d);
+  }
+  if (b == 0) {
+    uint64_t best = 0;
+    const bool ok = ctl.template gather_range<kNumWG * 4>(x_key, tk, [&](int ci, u32x4 v) {
+      const uint32_t idx = (v.y >> 16) | (v.z & 0xffff0000u);
+      const uint32_t score32 = (v.x & 0xffff0000u) | (v.w >> 16);
+      const uint64_t key = ((uint64_t)score32 << 32) | (uint64_t)(0xffffffffu - idx);
+      best = key > best ? key : best;
+    });
+    stamp(p.nl * kTracePoints + 2);
+    if (ok) {
+      best = wave_max_u64_all(best);
+      const int token = (int)(0xffffffffu - (uint32_t)best);
+      if (lane == 0) {
+        DecodeState* st = a.st;
+        if (a.out_token) *a.out_token = token;
+        if (p.persistent) {
+          if (a.out_log) a.out_log[p.step] = token;
+          st->tok = token;
+          st->pos = p.pos + 1;
+          st->step = p.step + 1;
+          st->ran = 1;
+          if (token == st->eos) st->done = 1;
+        }
+        st->epoch = p.epoch + (uint32_t)(p.nl * Dm::NX + 1);
+      }
+    }
+  }
+}
+
 // SPLIT: the compute waves run attention as a split-K softmax between barriers c and f and hand
 // over per-wave (max, sum, unnormalised P@V); there is no (max, sum) exchange and no barriers d, e.
 template <class M, bool SPLIT>
@@ -632,20 +725,8 @@ __device__ __forceinline__ void control_path(const KArgs& a, Smem<M>& s, const S
     if (a.trace && lane == 0) a.trace[(size_t)point * kNumWG + b] = wall_clock64();
   };
   const size_t kv_layer_stride = (size_t)Dm::NKV * a.max_seq_len * Dm::D;
-  auto to_f32 = [&](float* dst) {
-    return [dst](int ci, u32x4 v) {
-      float* d = dst + 4 * ci;
-      d[0] = bf16_to_f32(v.x >> 16); d[1] = bf16_to_f32(v.y >> 16);
-      d[2] = bf16_to_f32(v.z >> 16); d[3] = bf16_to_f32(v.w >> 16);
-    };
-  };
-  auto to_bf16 = [&](uint16_t* dst) {
-    return [dst](int ci, u32x4 v) {
-      uint32_t* d = reinterpret_cast<uint32_t*>(dst) + 2 * ci;
-      d[0] = (v.x >> 16) | (v.y & 0xffff0000u);
-      d[1] = (v.z >> 16) | (v.w & 0xffff0000u);
-    };
-  };
+  auto to_f32 = [](float* dst) { return Ctl<M>::to_f32(dst); };
+  auto to_bf16 = [](uint16_t* dst) { return Ctl<M>::to_bf16(dst); };
 
   for (int L = 0; L < p.nl; L++) {
     const LayerPtrs& w = s.layers[L];
@@ -881,64 +962,63 @@ __device__ __forceinline__ void control_path(const KArgs& a, Smem<M>& s, const S
   }
 
   // ------------------------------------------------------------------ final
-  const auto nw_final = ctl.load_norm(a.final_norm);
-  if (ctl.template gather_range<Dm::H>(Dm::X_H + xcd * Dm::H, tag_of(p.nl - 1, 8), to_f32(s.x))) {
-    ctl.rmsnorm(s.x, nw_final);
-    if (b == 0) {
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      for (int i = lane; i < Dm::H; i += 64) {
-        if (a.hidden_out) a.hidden_out[i] = (uint16_t)f32_to_bf16(s.x[i]);
-        if (a.normalized_out) a.normalized_out[i] = bf16_to_f32(s.n[i]);
-      }
-    }
-  }
-  stamp(p.nl * kTracePoints + 0);
-  QMK_SYNC();  // final a
-  QMK_SYNC();  // final b
-  stamp(p.nl * kTracePoints + 1);
-  const uint32_t tk = make_tag(p.epoch, (uint32_t)(p.nl * Dm::NX));
-  if (lane == 0) {
+  final_control<M>(ctl, a, s, p, b, lane, Dm::X_H, Dm::X_KEY);
+}
+
+// The step's end, compute waves: LM-head rows of this workgroup (594 per workgroup, every eighth to
+// each wave) against the final-normed activation, keeping the best 64-bit key (barriers final a
+// and final b, matching final_control).
+template <class M, bool SAMPLED>
+__device__ __forceinline__ void final_compute(const KArgs& a, Smem<M>& s, const Step& p, int b, int c, int lane) {
+  using Dm = Dims<M>;
+  {
+    u32x4 act[Dm::LH];  // the final-normed activation, loaded after barrier final a
+    const int row0 = b * Dm::LM_RPW;
+    const int nrows = min(Dm::V - row0, Dm::LM_RPW);
+    const int nmine = (nrows - c + kComputeWaves - 1) / kComputeWaves;
     uint64_t best = 0;
+    u32x4 bufA[Dm::LM_U][Dm::LH], bufB[Dm::LM_U][Dm::LH];
+    auto row_of = [&](int i) { return row0 + c + kComputeWaves * i; };
+    auto load_batch = [&](u32x4 (&buf)[Dm::LM_U][Dm::LH], int i0) {
 #pragma unroll
-    for (int cc = 0; cc < kComputeWaves; cc++) best = s.best[cc] > best ? s.best[cc] : best;
-    const uint32_t idx = 0xffffffffu - (uint32_t)best;
-    const uint32_t score32 = (uint32_t)(best >> 32);
-    u32x4 d;
-    d.x = word(score32 >> 16, tk);
-    d.y = word(idx & 0xffffu, tk);
-    d.z = word(idx >> 16, tk);
-    d.w = word(score32 & 0xffffu, tk);
-    put4<true>(a.x, Dm::X_KEY + 4 * b, d);
-  }
-  if (b == 0) {
-    uint64_t best = 0;
-    const bool ok = ctl.template gather_range<kNumWG * 4>(Dm::X_KEY, tk, [&](int ci, u32x4 v) {
-      const uint32_t idx = (v.y >> 16) | (v.z & 0xffff0000u);
-      const uint32_t score32 = (v.x & 0xffff0000u) | (v.w >> 16);
-      const uint64_t key = ((uint64_t)score32 << 32) | (uint64_t)(0xffffffffu - idx);
-      best = key > best ? key : best;
-    });
-    stamp(p.nl * kTracePoints + 2);
-    if (ok) {
-      best = wave_max_u64_all(best);
-      const int token = (int)(0xffffffffu - (uint32_t)best);
-      if (lane == 0) {
-        DecodeState* st = a.st;
-        if (a.out_token) *a.out_token = token;
-        if (p.persistent) {
-          if (a.out_log) a.out_log[p.step] = token;
-          st->tok = token;
-          st->pos = p.pos + 1;
-          st->step = p.step + 1;
-          st->ran = 1;
-          if (token == st->eos) st->done = 1;
-        }
-        st->epoch = p.epoch + (uint32_t)(p.nl * Dm::NX + 1);
+      for (int u = 0; u < Dm::LM_U; u++) {
+        const int i = min(i0 + u, nmine - 1);
+        load_row(buf[u], a.lm_head + (size_t)row_of(i) * Dm::H, 0, lane);
       }
+    };
+    // key = score32 << 32 | ~row: score32 = orderable bf16 logit << 16 (greedy, the first index of
+    // the maximum) or the order-preserving key of logit / T + Gumbel noise (a draw)
+    const uint64_t base = SAMPLED ? draw_base(a.seed, (uint64_t)p.pos) : 0;
+    auto do_batch = [&](u32x4 (&buf)[Dm::LM_U][Dm::LH], int i0) {
+#pragma unroll
+      for (int u = 0; u < Dm::LM_U; u++) {
+        const float v = row_dot(buf[u], act);
+        if (i0 + u < nmine) {
+          const int row = row_of(i0 + u);
+          const uint32_t hb = f32_to_bf16(v);
+          uint32_t score32;
+          if constexpr (SAMPLED) score32 = gumbel_key(bf16_to_f32(hb), a.temperature, base, row);
+          else score32 = orderable16(hb) << 16;
+          const uint64_t key = ((uint64_t)score32 << 32) | (uint64_t)(0xffffffffu - (uint32_t)row);
+          best = key > best ? key : best;
+          if (a.logits && lane == 0) a.logits[row] = bf16_to_f32(hb);
+        }
+      }
+    };
+    // the first batch of rows needs no activation: requested before barrier final a, it streams
+    // while the control wave gathers h and applies the final norm
+    load_batch(bufA, 0);
+    QMK_SYNC();  // final a
+    load_act(act, s.n, 0, lane);
+    for (int i = 0; i < nmine; i += 2 * Dm::LM_U) {
+      load_batch(bufB, i + Dm::LM_U);
+      do_batch(bufA, i);
+      if (i + 2 * Dm::LM_U < nmine) load_batch(bufA, i + 2 * Dm::LM_U);
+      do_batch(bufB, i + Dm::LM_U);
     }
+    if (lane == 0) s.best[c] = best;
   }
+  QMK_SYNC();  // final b
 }
 
 // LONG: the long-context attention form; sw and pw are this wave's rows of
@@ -1022,7 +1102,9 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
   // 1,943.  Those of this form are given where each request is issued.
   constexpr bool EARLY = !ST && !LONG;
   constexpr bool SPLIT = EARLY && kShortSplitK;
-  constexpr bool W_AT_C = SPLIT || !kWeightsAtE;  // EARLY: this layer's gate/up and o_proj slices at barrier c
+  // EARLY: this layer's gate/up (GU_C) and o_proj (O_C) slices requested at barrier c, else at e
+  constexpr bool GU_C = SPLIT || kGateUpAtC;
+  constexpr bool O_C = SPLIT || kOprojAtC;
   static_assert(!EARLY || kLongContext / kGroupSize <= 32 * kKvU, "EARLY: at most one K/V batch per wave");
   prefetch_qkv(0);
   if (!ST && !EARLY) {
@@ -1114,11 +1196,10 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
       // LDS at barrier c the two orders measure the same (2,178-2,180 either way; 2,155-2,156
       // against 2,152 at context 1024 with the slices first).
       if (L == 0) kv_issue_at(vc, 0, 1);
-      if constexpr (W_AT_C) {
-        prefetch_gu(L);
-        prefetch_o(L);
-      }
-      constexpr int kLoadsC = W_AT_C ? Dm::GU_W * Dm::LH + Dm::OP * Dm::LO : 0;  // weight loads issued after the V rows
+      if constexpr (GU_C) prefetch_gu(L);
+      if constexpr (O_C) prefetch_o(L);
+      // weight loads issued after the V rows
+      constexpr int kLoadsC = (GU_C ? Dm::GU_W * Dm::LH : 0) + (O_C ? Dm::OP * Dm::LO : 0);
       // ---------------------------------------------- split-K attention over this wave's positions
       // Lane (slot, t16) holds dims 8*t16..+7 of position base0 + 32u + slot.  Scores as HF
       // rounds them; the softmax terms are exp(s - m) against the wave's own maximum m, kept in
@@ -1185,10 +1266,8 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
         cstamp(L, 3);
         QMK_SYNC();  // d
         QMK_SYNC();  // e
-        if constexpr (!W_AT_C) {
-          prefetch_gu(L);
-          prefetch_o(L);
-        }
+        if constexpr (!GU_C) prefetch_gu(L);
+        if constexpr (!O_C) prefetch_o(L);
         cstamp(L, 4);
         if (nb > 0) {
           float gm[Dm::GQ], ginv[Dm::GQ];
@@ -1611,54 +1690,7 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
     cstamp(L, 11);
   }
 
-  {
-    u32x4 act[Dm::LH];  // the final-normed activation, loaded after barrier final a
-    const int row0 = b * Dm::LM_RPW;
-    const int nrows = min(Dm::V - row0, Dm::LM_RPW);
-    const int nmine = (nrows - c + kComputeWaves - 1) / kComputeWaves;
-    uint64_t best = 0;
-    u32x4 bufA[Dm::LM_U][Dm::LH], bufB[Dm::LM_U][Dm::LH];
-    auto row_of = [&](int i) { return row0 + c + kComputeWaves * i; };
-    auto load_batch = [&](u32x4 (&buf)[Dm::LM_U][Dm::LH], int i0) {
-#pragma unroll
-      for (int u = 0; u < Dm::LM_U; u++) {
-        const int i = min(i0 + u, nmine - 1);
-        load_row(buf[u], a.lm_head + (size_t)row_of(i) * Dm::H, 0, lane);
-      }
-    };
-    // key = score32 << 32 | ~row: score32 = orderable bf16 logit << 16 (greedy, the first index of
-    // the maximum) or the order-preserving key of logit / T + Gumbel noise (a draw)
-    const uint64_t base = SAMPLED ? draw_base(a.seed, (uint64_t)p.pos) : 0;
-    auto do_batch = [&](u32x4 (&buf)[Dm::LM_U][Dm::LH], int i0) {
-#pragma unroll
-      for (int u = 0; u < Dm::LM_U; u++) {
-        const float v = row_dot(buf[u], act);
-        if (i0 + u < nmine) {
-          const int row = row_of(i0 + u);
-          const uint32_t hb = f32_to_bf16(v);
-          uint32_t score32;
-          if constexpr (SAMPLED) score32 = gumbel_key(bf16_to_f32(hb), a.temperature, base, row);
-          else score32 = orderable16(hb) << 16;
-          const uint64_t key = ((uint64_t)score32 << 32) | (uint64_t)(0xffffffffu - (uint32_t)row);
-          best = key > best ? key : best;
-          if (a.logits && lane == 0) a.logits[row] = bf16_to_f32(hb);
-        }
-      }
-    };
-    // the first batch of rows needs no activation: requested before barrier final a, it streams
-    // while the control wave gathers h and applies the final norm
-    load_batch(bufA, 0);
-    QMK_SYNC();  // final a
-    load_act(act, s.n, 0, lane);
-    for (int i = 0; i < nmine; i += 2 * Dm::LM_U) {
-      load_batch(bufB, i + Dm::LM_U);
-      do_batch(bufA, i);
-      if (i + 2 * Dm::LM_U < nmine) load_batch(bufA, i + 2 * Dm::LM_U);
-      do_batch(bufB, i + Dm::LM_U);
-    }
-    if (lane == 0) s.best[c] = best;
-  }
-  QMK_SYNC();  // final b
+  final_compute<M, SAMPLED>(a, s, p, b, c, lane);
 }
 
 // SAMPLED: the LM-head keys are Gumbel-perturbed (temperature sampling, KArgs::temperature > 0);

@@ -478,13 +478,8 @@ void decode_batch(torch::Tensor tokens, torch::Tensor positions, torch::Tensor o
   TORCH_CHECK(B >= 1 && B <= 256, "tokens must hold 1 .. 256 entries");
   TORCH_CHECK(positions.numel() == B && out_tokens.numel() == B, "positions and out_tokens must match tokens");
   TORCH_CHECK(bm.num_seqs == B, "k_cache must hold one sequence per token (", B, "), got ", bm.num_seqs);
-  const auto overlap = [](const torch::Tensor& x, const torch::Tensor& y) {
-    const char* a = static_cast<const char*>(x.data_ptr());
-    const char* b = static_cast<const char*>(y.data_ptr());
-    return a < b + y.nbytes() && b < a + x.nbytes();
-  };
-  TORCH_CHECK(!overlap(tokens, out_tokens) && !overlap(positions, out_tokens),
-              "out_tokens must not overlap tokens or positions");
+  // out_tokens may share memory with tokens or positions (an in-place step): qmk_decode_batch then
+  // takes its multi-launch path, which reads them before writing
   float* lg = nullptr;
   if (logits.has_value()) {
     check_cuda(*logits, "logits");

@@ -271,3 +271,32 @@ def test_persistent_batch_long_stream_across_tag_wraps(weights_gpu):
         assert int(log.min()) >= 0 and int(log.max()) < V
         logs.append(log)
     assert torch.equal(logs[0], logs[1])
+
+
+def test_in_place_batched_step_takes_the_multi_launch_path(shape, weights_gpu):
+    """decode_batch with out_tokens sharing memory with tokens (an in-place step, batch 4 at a
+    context the persistent kernel serves) succeeds and gives, bit for bit, the tokens of the same
+    step with separate buffers on the multi-launch path, which reads its inputs before writing."""
+    from qwen_megakernel.model import BatchDecoder
+    from qwen_megakernel.weights import make_prompt
+
+    B, layers, max_seq = 4, 4, 256
+    prompts = [make_prompt(n, shape.vocab, seed=90 + b) for b, n in enumerate([5, 9, 3, 12])]
+    bd = BatchDecoder(weights=weights_gpu, batch_size=B, max_seq_len=max_seq, num_layers=layers, verbose=False)
+    first = bd.prefill_all(prompts)
+    pos = bd.positions
+    k0, v0 = bd._k_cache.clone(), bd._v_cache.clone()
+    results = {}
+    for name, persistent_on, in_place in (("launches", False, False), ("persistent", True, False),
+                                          ("in place", True, True)):
+        bd._k_cache.copy_(k0)
+        bd._v_cache.copy_(v0)
+        toks = _i32(first)
+        out = toks if in_place else torch.empty(B, dtype=torch.int32, device="cuda")
+        with persistent(persistent_on):
+            bd._forward.decode(toks, _i32(pos), out, None, bd._k_cache, bd._v_cache, max(pos) + 1)
+        results[name] = out.cpu().tolist()
+    assert int(_ops().device_error()) == 0
+    assert min(results["launches"]) >= 0
+    assert results["in place"] == results["launches"], results
+    assert min(results["persistent"]) >= 0

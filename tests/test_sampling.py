@@ -4,14 +4,16 @@
   of the generator seeded with 0: 0xE220A8397B1DCDAF, 0x6E789E6AA1B965F4).
 * The kept sets against HF transformers' own warpers (TemperatureLogitsWarper,
   TopKLogitsWarper, TopPLogitsWarper, applied in HF's order) on random rows and
-  on rows with ties at the k-th value.
+  on rows with ties at the k-th value: the fixtures tests/golden/
+  hf_sampling_kept.npz, written by tests/golden/make_sampling_golden.py.
 * The Gumbel-max draw against the softmax of the kept scores: frequencies over
   many counters within 5 standard deviations, and never a removed token.
 """
 
+import os
+
 import numpy as np
 import pytest
-import torch
 
 from oracle import sampling_ref as S
 
@@ -30,41 +32,33 @@ def test_uniforms_in_open_interval_and_flat():
     assert not np.array_equal(u[:100], S.uniforms(seed=7, counter=4, n=100))
 
 
-def _hf_kept(logits, temperature, top_k, top_p):
-    from transformers.generation.logits_process import (TemperatureLogitsWarper, TopKLogitsWarper,
-                                                        TopPLogitsWarper)
-
-    scores = torch.from_numpy(np.asarray(logits, dtype=np.float32))[None, :].clone()
-    scores = TemperatureLogitsWarper(temperature)(None, scores)
-    if 0 < top_k < scores.shape[-1]:
-        scores = TopKLogitsWarper(top_k)(None, scores)
-    if 0.0 < top_p < 1.0:
-        scores = TopPLogitsWarper(top_p)(None, scores)
-    return torch.isfinite(scores[0]).numpy()
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "hf_sampling_kept.npz")
 
 
-@pytest.mark.parametrize("seed", range(6))
-@pytest.mark.parametrize("temperature,top_k,top_p", [(0.7, 0, 0.9), (1.0, 50, 1.0), (1.3, 40, 0.8),
-                                                     (0.5, 0, 0.5), (1.0, 7, 0.95)])
-def test_kept_sets_match_hf_warpers(seed, temperature, top_k, top_p):
-    rng = np.random.default_rng(seed)
-    logits = (rng.standard_normal(2000) * 3.0).astype(np.float32)
-    _, keep = S.kept_mask(logits, temperature, top_k, top_p)
-    hf = _hf_kept(logits, temperature, top_k, top_p)
-    assert np.array_equal(keep, hf), f"kept {keep.sum()} vs HF {hf.sum()}"
+@pytest.fixture(scope="module")
+def hf_golden():
+    return np.load(GOLDEN)
 
 
-def test_top_k_keeps_ties_like_hf():
-    logits = np.array([5, 4, 4, 4, 3, 2, 1, 4, 0], dtype=np.float32)
-    _, keep = S.kept_mask(logits, 1.0, 3, 1.0)
-    assert keep.tolist() == _hf_kept(logits, 1.0, 3, 1.0).tolist()
+def test_kept_sets_match_hf_warpers(hf_golden):
+    """30 random rows (default_rng(seed), N(0, 3^2), 2000 entries) x (T, top-k, top-p) settings."""
+    cases = hf_golden["random_cases"]
+    kept = np.unpackbits(hf_golden["random_kept"], axis=1)[:, :2000].astype(bool)
+    for (seed, t, k, p), want in zip(cases, kept):
+        logits = (np.random.default_rng(int(seed)).standard_normal(2000) * 3.0).astype(np.float32)
+        _, keep = S.kept_mask(logits, float(t), int(k), float(p))
+        assert np.array_equal(keep, want), f"seed {seed} T {t} k {k} p {p}: kept {keep.sum()} vs HF {want.sum()}"
+
+
+def test_top_k_keeps_ties_like_hf(hf_golden):
+    _, keep = S.kept_mask(hf_golden["tie_row"], 1.0, 3, 1.0)
+    assert keep.tolist() == hf_golden["tie_kept"].tolist()
     assert keep.sum() == 5  # the three 4s tied at the 3rd value are all kept, as HF does
 
 
-def test_top_p_keeps_the_top_token_at_tiny_p():
-    logits = np.array([1.0, 3.0, 2.0, 3.5], dtype=np.float32)
-    _, keep = S.kept_mask(logits, 1.0, 0, 1e-9)
-    assert keep.tolist() == [False, False, False, True] == _hf_kept(logits, 1.0, 0, 1e-9).tolist()
+def test_top_p_keeps_the_top_token_at_tiny_p(hf_golden):
+    _, keep = S.kept_mask(hf_golden["tiny_p_row"], 1.0, 0, 1e-9)
+    assert keep.tolist() == [False, False, False, True] == hf_golden["tiny_p_kept"].tolist()
 
 
 def test_greedy_at_zero_temperature():
