@@ -74,7 +74,7 @@ PROMPT_LEN = 128
 TRAFFIC_PROFILE = {
     "file": "profiles/decode_kernel_qwen3_0p6b_ctx129-1152_xcd_parallel.md",
     "contexts": "129..1152",
-    "measured_bytes": 1_353_651_577,
+    "measured_bytes": 1_353_604_847,
     "algorithmic_bytes": 1_265_674_240,
 }
 METRIC = "decode tok/s, batch 1, Qwen3-0.6B bf16; achieved HBM GB/s vs ~8 TB/s peak"
@@ -186,7 +186,7 @@ def long_context(w, steps: int, contexts=(8192, 32768), phase_trace: bool = Fals
 
             dec._position = c0 + 4 + steps  # the cache holds every position before it
             stamps = trace.capture(lambda: dec.step(11), S.num_layers)
-            summ = trace.summarize(stamps, S.num_layers, split=c0 + 5 + steps <= 2048)
+            summ = trace.summarize(stamps, S.num_layers)
             summ["context"] = c0 + 5 + steps
             out[str(c0)]["phase_trace"] = summ
             log(f"long-context phase trace at context {c0 + 5 + steps}:\n" + trace.format_table(summ))
@@ -523,8 +523,7 @@ def main():
         dec._position = last
 
         stamps = trace.capture(lambda: dec.step(int(toks[-1])), QWEN3_0_6B.num_layers)
-        # positions below 2,048 run the split-K form of the Qwen3-0.6B kernel
-        summ = trace.summarize(stamps, QWEN3_0_6B.num_layers, split=last + 1 <= 2048)
+        summ = trace.summarize(stamps, QWEN3_0_6B.num_layers)
         summ["context"] = last + 1
         result["phase_trace"] = summ
         log(f"phase trace at context {last + 1}:\n" + trace.format_table(summ))

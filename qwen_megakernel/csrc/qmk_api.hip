@@ -236,7 +236,7 @@ int check_device(int dev, DevInfo** out) {
            hipMemcpyAsync(h_ok, d_ok, sizeof(h_ok), hipMemcpyDeviceToHost, ps) == hipSuccess &&
            hipStreamSynchronize(ps) == hipSuccess;
   }
-  hipStreamDestroy(ps);
+  (void)hipStreamDestroy(ps);
   if (!good) return QMK_ERR_HIP;
   if (!di.order_evt && hipEventCreateWithFlags(&di.order_evt, hipEventDisableTiming) != hipSuccess) return QMK_ERR_HIP;
   int all = 1;
@@ -364,14 +364,14 @@ int get_ctx(hipStream_t stream, Ctx** out) {
     return QMK_ERR_HIP;
   }
   if (hipMemset(mem, 0, bytes) != hipSuccess || hipHostMalloc(&c->host_err, sizeof(uint32_t), hipHostMallocDefault) != hipSuccess) {
-    hipFree(mem);
+    (void)hipFree(mem);
     delete c;
     return QMK_ERR_HIP;
   }
   *c->host_err = 0;
   if (hipMalloc(&c->log, (size_t)kMaxSeqLen * sizeof(int)) != hipSuccess) {
-    hipFree(mem);
-    hipHostFree(c->host_err);
+    (void)hipFree(mem);
+    (void)hipHostFree(c->host_err);
     delete c;
     return QMK_ERR_HIP;
   }
@@ -510,7 +510,7 @@ int graph_for(Ctx* ctx, const KArgs& a, int model, const SampleParams* sp, int f
     return QMK_OK;
   }
   if (gr.exec) {
-    hipGraphExecDestroy(gr.exec);
+    (void)hipGraphExecDestroy(gr.exec);
     gr.exec = nullptr;
   }
   if (!ctx->cap && hipStreamCreateWithFlags(&ctx->cap, hipStreamNonBlocking) != hipSuccess) return QMK_ERR_HIP;
@@ -520,12 +520,12 @@ int graph_for(Ctx* ctx, const KArgs& a, int model, const SampleParams* sp, int f
   hipGraph_t g = nullptr;
   const hipError_t e = hipStreamEndCapture(ctx->cap, &g);
   if (s != QMK_OK || e != hipSuccess || !g) {
-    if (g) hipGraphDestroy(g);
+    if (g) (void)hipGraphDestroy(g);
     return QMK_ERR_HIP;
   }
   hipGraphExec_t ex = nullptr;
   const hipError_t ie = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
-  hipGraphDestroy(g);
+  (void)hipGraphDestroy(g);
   if (ie != hipSuccess) return QMK_ERR_HIP;
   gr.exec = ex;
   gr.args = a;
@@ -639,7 +639,7 @@ int device_table(DevInfo* di, const LDGLayerWeights* host, int num_layers, hipSt
   std::memcpy(t.host.data(), host, bytes);
   if (hipMalloc(&t.dev, bytes) != hipSuccess) return QMK_ERR_HIP;
   if (hipMemcpy(t.dev, t.host.data(), bytes, hipMemcpyHostToDevice) != hipSuccess) {
-    hipFree(t.dev);
+    (void)hipFree(t.dev);
     return QMK_ERR_HIP;
   }
   *out = t.dev;
@@ -689,7 +689,7 @@ int batch_persistent_impl(int model, int batch, const int* tokens, const int* po
     void* mem = nullptr;
     if (hipMalloc(&mem, bytes) != hipSuccess) return QMK_ERR_HIP;
     if (hipMemset(mem, 0, bytes) != hipSuccess) {
-      hipFree(mem);
+      (void)hipFree(mem);
       return QMK_ERR_HIP;
     }
     ctx->bst = reinterpret_cast<DecodeState*>(mem);

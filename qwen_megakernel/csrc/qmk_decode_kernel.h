@@ -22,9 +22,8 @@
 //
 //   k  exchange   producers -> consumers                scope
 //   0  qkv        32 WGs of XCD x -> same 32 WGs         XCD-local
-//   1  ml         softmax (max, sum) per WG and head     XCD-local (two-pass form only)
-//   2  acc        P@V partial sums per WG and head       XCD-local (split form: with the
-//                 WG's (max, sum), in the ml slots)
+//   1  ml         softmax (max, sum) per WG and head     XCD-local
+//   2  acc        P@V partial sums per WG and head       XCD-local
 //   3  attn       attention output of heads 2x, 2x+1     XCD-local
 //   4  o          o_proj partials, rows 32r..32r+31      across XCDs (8 -> 8)
 //   5  h2         h' = h + o_proj(attn)                  XCD-local
@@ -37,12 +36,9 @@
 // RoPE products and sum, attention scores and their scaling, softmax
 // probabilities, attention output, residual adds, SiLU and its product,
 // logits); dot products accumulate in fp32.  Attention is split over the 32
-// workgroups of an XCD.  The Qwen3-0.6B kernel below 2,048 positions runs it
-// as a split-K softmax (each wave's terms exp(s - m) against its own maximum,
-// in fp32, rescaled to the global maximum in the combine, as the reference's
-// kernel does); the other forms take two passes so that the probabilities
-// are normalised with the global max and sum and rounded to bf16 before P@V,
-// as HF does.
+// workgroups of an XCD and takes HF's two passes in every form: the
+// workgroups' (max, sum) pairs are merged first, so that the probabilities
+// are normalised with the global max and sum and rounded to bf16 before P@V.
 //
 // Each workgroup has 9 waves.  Wave 0 ("control") moves activations: it polls
 // exchanges, applies norms / RoPE / residuals / SiLU, publishes results and
@@ -81,10 +77,6 @@ constexpr int kKvU = 2;        // attention: each wave covers 4 positions (16-la
 constexpr int kKvStages = 4;   // K/V batches in flight per wave (LDS ring)
 constexpr int kLongContext = 2048;  // contexts above this run decode_kernel<M, S, true>
 constexpr int kDeepContext = 12288; // contexts above this run decode_kernel_deep<M, S>
-// Short-context Qwen3-0.6B attention: false = HF's two passes (global max and sum exchanged, the
-// probabilities rounded to bf16 before P@V); true = split-K softmax in one window (unrounded
-// probabilities rescaled in the combine).
-constexpr bool kShortSplitK = false;
 // Short-context Qwen3-0.6B, two-pass form: this layer's gate/up slice is requested at barrier c
 // (it drains during the scores and the (max, sum) exchange) and its o_proj slice at barrier e
 // (during P@V).  Same-box A/B at context 1024: both at c 1,999 tok/s, both at e 2,010, gate/up at c
@@ -713,9 +705,7 @@ __device__ __forceinline__ void final_control(Ctl<M>& ctl, const KArgs& a, Smem<
   }
 }
 
-// SPLIT: the compute waves run attention as a split-K softmax between barriers c and f and hand
-// over per-wave (max, sum, unnormalised P@V); there is no (max, sum) exchange and no barriers d, e.
-template <class M, bool SPLIT>
+template <class M>
 __device__ __forceinline__ void control_path(const KArgs& a, Smem<M>& s, const Step& p, int b, int lane) {
   using Dm = Dims<M>;
   const int xcd = b & (kGroups - 1), r = b >> 3;
@@ -773,53 +763,48 @@ __device__ __forceinline__ void control_path(const KArgs& a, Smem<M>& s, const S
     }
     stamp(tp + 3);
     QMK_SYNC();  // c
-    if constexpr (SPLIT) {
-      stamp(tp + 4);
-      stamp(tp + 5);
-    } else {
-      QMK_SYNC();  // d
-      stamp(tp + 4);
-      // ------------------------------------------------------------ d..e  softmax max and sum
-      {
-        const uint32_t t = tag_of(L, 1);
-        // lanes 0..GQ-1: merge the eight wave (max, sum) pairs of head h = lane
-        float mx = -INFINITY, sm = 0.f;
-        if (lane < Dm::GQ) {
-  #pragma unroll
-          for (int c = 0; c < kComputeWaves; c++) mx = fmaxf(mx, s.wml[c][lane][0]);
-  #pragma unroll
-          for (int c = 0; c < kComputeWaves; c++) {
-            const float mc = s.wml[c][lane][0];
-            sm += mc == -INFINITY ? 0.f : s.wml[c][lane][1] * exp_acc(mc - mx);
-          }
-        }
-        if (lane < Dm::GQ) ctl.put_f32x2(true, Dm::X_ML + (xcd * kGroupSize + r) * Dm::GQ * 4 + 4 * lane, mx, sm, t);
-        // gather every active workgroup's pairs: chunk i = (rank i / GQ, head i % GQ)
-        float pm[2] = {-INFINITY, -INFINITY}, pl[2] = {0.f, 0.f};
-        const bool ok = ctl.template gather<kGroupSize * Dm::GQ>(
-            t, [&](int i) { return Dm::X_ML + (uint32_t)((xcd * kGroupSize + i / Dm::GQ) * Dm::GQ * 4 + 4 * (i % Dm::GQ)); },
-            [&](int i, u32x4 v) {
-              pm[i / 64] = f32_from_words(v.x, v.y);
-              pl[i / 64] = f32_from_words(v.z, v.w);
-            });
-        if (ok) {
-          // lane l holds chunks l and l+64 (64 chunks: only the first): head = l % GQ
-          static_assert(kGroupSize * Dm::GQ <= 64, "one chunk per lane");
-          const int h = lane % Dm::GQ;
-          const bool act = (lane / Dm::GQ) < p.n_act;
-          float m0 = act ? pm[0] : -INFINITY;
-          static_assert(Dm::GQ == 2, "lane classes of two");
-          const float gm = class2_max(m0);
-          const float lsum = class2_sum((act && m0 != -INFINITY) ? pl[0] * exp_acc(m0 - gm) : 0.f);
-          if (lane < Dm::GQ) {
-            s.ml[h][0] = gm;
-            s.ml[h][1] = lsum;
-          }
+    QMK_SYNC();  // d
+    stamp(tp + 4);
+    // ------------------------------------------------------------ d..e  softmax max and sum
+    {
+      const uint32_t t = tag_of(L, 1);
+      // lanes 0..GQ-1: merge the eight wave (max, sum) pairs of head h = lane
+      float mx = -INFINITY, sm = 0.f;
+      if (lane < Dm::GQ) {
+#pragma unroll
+        for (int c = 0; c < kComputeWaves; c++) mx = fmaxf(mx, s.wml[c][lane][0]);
+#pragma unroll
+        for (int c = 0; c < kComputeWaves; c++) {
+          const float mc = s.wml[c][lane][0];
+          sm += mc == -INFINITY ? 0.f : s.wml[c][lane][1] * exp_acc(mc - mx);
         }
       }
-      stamp(tp + 5);
-      QMK_SYNC();  // e
+      if (lane < Dm::GQ) ctl.put_f32x2(true, Dm::X_ML + (xcd * kGroupSize + r) * Dm::GQ * 4 + 4 * lane, mx, sm, t);
+      // gather every active workgroup's pairs: chunk i = (rank i / GQ, head i % GQ)
+      float pm[2] = {-INFINITY, -INFINITY}, pl[2] = {0.f, 0.f};
+      const bool ok = ctl.template gather<kGroupSize * Dm::GQ>(
+          t, [&](int i) { return Dm::X_ML + (uint32_t)((xcd * kGroupSize + i / Dm::GQ) * Dm::GQ * 4 + 4 * (i % Dm::GQ)); },
+          [&](int i, u32x4 v) {
+            pm[i / 64] = f32_from_words(v.x, v.y);
+            pl[i / 64] = f32_from_words(v.z, v.w);
+          });
+      if (ok) {
+        // lane l holds chunks l and l+64 (64 chunks: only the first): head = l % GQ
+        static_assert(kGroupSize * Dm::GQ <= 64, "one chunk per lane");
+        const int h = lane % Dm::GQ;
+        const bool act = (lane / Dm::GQ) < p.n_act;
+        float m0 = act ? pm[0] : -INFINITY;
+        static_assert(Dm::GQ == 2, "lane classes of two");
+        const float gm = class2_max(m0);
+        const float lsum = class2_sum((act && m0 != -INFINITY) ? pl[0] * exp_acc(m0 - gm) : 0.f);
+        if (lane < Dm::GQ) {
+          s.ml[h][0] = gm;
+          s.ml[h][1] = lsum;
+        }
+      }
     }
+    stamp(tp + 5);
+    QMK_SYNC();  // e
     QMK_SYNC();  // f
     stamp(tp + 6);
     // ------------------------------------------------------------ f..g  P@V partials, combine, attn
@@ -829,29 +814,10 @@ __device__ __forceinline__ void control_path(const KArgs& a, Smem<M>& s, const S
 #pragma unroll
       for (int h = 0; h < Dm::GQ; h++) {
         float a0 = 0.f, a1 = 0.f;
-        if constexpr (SPLIT) {
-          // wave c's terms are relative to its own maximum: rescale to the workgroup's, and
-          // publish the workgroup's (max, sum) of head h beside the partial, under the same tag
-          float mh = -INFINITY, lh = 0.f;
 #pragma unroll
-          for (int c = 0; c < kComputeWaves; c++) mh = fmaxf(mh, s.wml[c][h][0]);
-          // wave c's factor exp(m_c - mh) is computed by lane c and read from it
-          const float ml = s.wml[lane & (kComputeWaves - 1)][h][0];
-          const float fl = ml == -INFINITY ? 0.f : exp_acc(ml - mh);
-#pragma unroll
-          for (int c = 0; c < kComputeWaves; c++) {
-            const float f = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(fl), c));
-            lh += f * s.wml[c][h][1];
-            a0 += f * s.wacc[c][h][2 * lane];
-            a1 += f * s.wacc[c][h][2 * lane + 1];
-          }
-          if (lane == 0) ctl.put_f32x2(true, Dm::X_ML + (xcd * kGroupSize + r) * Dm::GQ * 4 + 4 * h, mh, lh, t);
-        } else {
-#pragma unroll
-          for (int c = 0; c < kComputeWaves; c++) {
-            a0 += s.wacc[c][h][2 * lane];
-            a1 += s.wacc[c][h][2 * lane + 1];
-          }
+        for (int c = 0; c < kComputeWaves; c++) {
+          a0 += s.wacc[c][h][2 * lane];
+          a1 += s.wacc[c][h][2 * lane + 1];
         }
         ctl.put_f32x2(true, Dm::X_ACC + (uint32_t)((xcd * kGroupSize + r) * Dm::GQ * Dm::D * 2 + h * Dm::D * 2 + 4 * lane),
                       a0, a1, t);
@@ -860,46 +826,20 @@ __device__ __forceinline__ void control_path(const KArgs& a, Smem<M>& s, const S
       // dims 8kb+2(i%4), +1); lane l receives chunks l and l+64 (ranks l/4 and l/4+16).
       const int hh = r / (Dm::D / 8), kb = r % (Dm::D / 8);
       static_assert(kGroupSize * 4 == 128, "two chunks per lane");
-      // SPLIT: chunks 128 + j carry rank j's (max, sum) of head hh, lane j receives them
-      constexpr int NCHUNK = kGroupSize * 4 + (SPLIT ? kGroupSize : 0);
       float v0[2] = {0.f, 0.f}, v1[2] = {0.f, 0.f};
-      [[maybe_unused]] float mr = -INFINITY, lr = 0.f;
-      const bool ok2 = ctl.template gather<NCHUNK>(
+      const bool ok2 = ctl.template gather<kGroupSize * 4>(
           t,
           [&](int i) {
-            if (SPLIT && i >= kGroupSize * 4)
-              return Dm::X_ML + (uint32_t)((xcd * kGroupSize + (i - kGroupSize * 4)) * Dm::GQ * 4 + 4 * hh);
             return Dm::X_ACC + (uint32_t)((xcd * kGroupSize + i / 4) * Dm::GQ * Dm::D * 2 + hh * Dm::D * 2 +
                                           (8 * kb + 2 * (i % 4)) * 2);
           },
           [&](int i, u32x4 v) {
-            if (SPLIT && i >= kGroupSize * 4) {
-              const bool act = (i - kGroupSize * 4) < p.n_act;
-              mr = act ? f32_from_words(v.x, v.y) : -INFINITY;
-              lr = act ? f32_from_words(v.z, v.w) : 0.f;
-            } else {
-              const bool act = (i / 4) < p.n_act;
-              v0[(i / 64) & 1] = act ? f32_from_words(v.x, v.y) : 0.f;
-              v1[(i / 64) & 1] = act ? f32_from_words(v.z, v.w) : 0.f;
-            }
+            const bool act = (i / 4) < p.n_act;
+            v0[(i / 64) & 1] = act ? f32_from_words(v.x, v.y) : 0.f;
+            v1[(i / 64) & 1] = act ? f32_from_words(v.z, v.w) : 0.f;
           });
       if (ok2) {
-        float s0, s1;  // ranks l/4 and l/4 + 16
-        [[maybe_unused]] float gsum = 1.f;  // SPLIT: the softmax denominator
-        if constexpr (SPLIT) {
-          // rescale rank j's partial by exp(m_j - M) (M the maximum over the active ranks) and
-          // normalise by the rescaled sum of the sums
-          const float gm = wave_max_all(mr);
-          const float f = mr == -INFINITY ? 0.f : exp_acc(mr - gm);
-          const float gl = wave_sum(f * lr);
-          const float fa = __shfl(f, lane >> 2), fb = __shfl(f, (lane >> 2) + 16);
-          s0 = v0[0] * fa + v0[1] * fb;
-          s1 = v1[0] * fa + v1[1] * fb;
-          gsum = gl;
-        } else {
-          s0 = v0[0] + v0[1];
-          s1 = v1[0] + v1[1];
-        }
+        float s0 = v0[0] + v0[1], s1 = v1[0] + v1[1];  // ranks l/4 and l/4 + 16
         // sum over the 16 lanes of each class l % 4: row_ror:12 and row_ror:8 inside each 16-lane row
         // (lanes 0..3 read lanes 4..7, then 8..11), then the row swaps.  Lane l < 4 then holds the
         // sum over all ranks of dims 8kb+2l, +1, added as the xor butterfly adds it:
@@ -910,10 +850,6 @@ __device__ __forceinline__ void control_path(const KArgs& a, Smem<M>& s, const S
         s1 = dpp_add<0x128>(s1);
         s0 = rows_sum4(s0);
         s1 = rows_sum4(s1);
-        if constexpr (SPLIT) {
-          s0 = __fdiv_rn(s0, gsum);
-          s1 = __fdiv_rn(s1, gsum);
-        }
         // lanes 0 and 1 publish dims 8kb..8kb+3 (from lanes 0, 1) and 8kb+4..8kb+7 (lanes 2, 3)
         const float d2 = dpp_mov<0x88>(s0), d3 = dpp_mov<0x88>(s1);  // quad_perm [0,2,0,2]
         const float d4 = dpp_mov<0xDD>(s0), d5 = dpp_mov<0xDD>(s1);  // quad_perm [1,3,1,3]
@@ -1088,8 +1024,9 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
   };
 
   // EARLY (short-context form with every slice in its own registers): attention
-  // is a split-K softmax in one compute window, c..f (SPLIT; the control wave
-  // combines in f..g).  A CU returns vector-memory data in order, so every
+  // runs HF's two passes, scores and the wave's (max, sum) in c..d, P@V in e..f
+  // (the control wave merges the (max, sum) pairs in d..e and combines the P@V
+  // partials in f..g).  A CU returns vector-memory data in order, so every
   // request is placed where the control wave's polls do not follow it closely:
   // this layer's gate/up and o_proj slices at barrier c and its down slice at i
   // (the two windows in which the control wave does not poll), and the next
@@ -1101,10 +1038,9 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
   // rows at c 1,955; the V rows requested before barrier c with the K rows
   // 1,943.  Those of this form are given where each request is issued.
   constexpr bool EARLY = !ST && !LONG;
-  constexpr bool SPLIT = EARLY && kShortSplitK;
   // EARLY: this layer's gate/up (GU_C) and o_proj (O_C) slices requested at barrier c, else at e
-  constexpr bool GU_C = SPLIT || kGateUpAtC;
-  constexpr bool O_C = SPLIT || kOprojAtC;
+  constexpr bool GU_C = kGateUpAtC;
+  constexpr bool O_C = kOprojAtC;
   static_assert(!EARLY || kLongContext / kGroupSize <= 32 * kKvU, "EARLY: at most one K/V batch per wave");
   prefetch_qkv(0);
   if (!ST && !EARLY) {
@@ -1200,11 +1136,9 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
       if constexpr (O_C) prefetch_o(L);
       // weight loads issued after the V rows
       constexpr int kLoadsC = (GU_C ? Dm::GU_W * Dm::LH : 0) + (O_C ? Dm::OP * Dm::LO : 0);
-      // ---------------------------------------------- split-K attention over this wave's positions
+      // ---------------------------------------------- attention over this wave's positions
       // Lane (slot, t16) holds dims 8*t16..+7 of position base0 + 32u + slot.  Scores as HF
-      // rounds them; the softmax terms are exp(s - m) against the wave's own maximum m, kept in
-      // fp32, and P@V accumulates them unnormalised.  The control wave rescales the waves'
-      // (m, l, acc) to the workgroup's maximum and the combine to the global one.
+      // rounds them, kept in registers between the two passes.
       float m_w[Dm::GQ], l_w[Dm::GQ], acc[Dm::GQ][8];
 #pragma unroll
       for (int h = 0; h < Dm::GQ; h++) {
@@ -1244,66 +1178,37 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
       // weight slices may stay in flight.  Waiting here, before any barrier, also tells the
       // compiler that no LDS DMA is outstanding at the barriers that follow.
       wait_vmcnt_upto<kLoadsC>();
-      if constexpr (!SPLIT) {
-        // HF's two passes: the wave's (max, sum of exp(s - max)) to the control wave, which merges the
-        // workgroups' pairs across the XCD (barriers d..e); then bf16(exp(s - M) / L) times V.
-        if (nb > 0) {
-#pragma unroll
-          for (int u = 0; u < U; u++) {
-            const int pp = base0 + 32 * u + slot;
-#pragma unroll
-            for (int h = 0; h < Dm::GQ; h++) l_w[h] += pp < p.p_end ? exp_acc(sc[u][h] - m_w[h]) : 0.f;
-          }
-        }
-#pragma unroll
-        for (int h = 0; h < Dm::GQ; h++) {
-          l_w[h] = rows_sum4(l_w[h]);  // the rows hold different positions, the lanes of a row the same one
-          if (lane == 0) {
-            s.wml[c][h][0] = m_w[h];
-            s.wml[c][h][1] = l_w[h];
-          }
-        }
-        cstamp(L, 3);
-        QMK_SYNC();  // d
-        QMK_SYNC();  // e
-        if constexpr (!GU_C) prefetch_gu(L);
-        if constexpr (!O_C) prefetch_o(L);
-        cstamp(L, 4);
-        if (nb > 0) {
-          float gm[Dm::GQ], ginv[Dm::GQ];
-#pragma unroll
-          for (int h = 0; h < Dm::GQ; h++) {
-            gm[h] = s.ml[h][0];
-            ginv[h] = __fdiv_rn(1.0f, s.ml[h][1]);
-          }
-          const u32x4 v_now = *reinterpret_cast<const u32x4*>(s.v + 8 * t16);
-#pragma unroll
-          for (int u = 0; u < U; u++) {
-            const int pp = base0 + 32 * u + slot;
-            const u32x4 vx = pp == p.pos ? v_now : s.kv[1][c][u][lane];
-            const float vf[8] = {lo_bf16(vx.x), hi_bf16(vx.x), lo_bf16(vx.y), hi_bf16(vx.y),
-                                 lo_bf16(vx.z), hi_bf16(vx.z), lo_bf16(vx.w), hi_bf16(vx.w)};
-#pragma unroll
-            for (int h = 0; h < Dm::GQ; h++) {
-              // HF: softmax in fp32, probabilities rounded to bf16 before P@V; positions past the
-              // range (they load row 0) take probability 0 and their values are not used
-              const float pr = pp < p.p_end ? bf16r(exp_acc(sc[u][h] - gm[h]) * ginv[h]) : 0.f;
-#pragma unroll
-              for (int i = 0; i < 8; i++) acc[h][i] += pp < p.p_end ? pr * vf[i] : 0.f;
-            }
-          }
-        }
-#pragma unroll
-        for (int h = 0; h < Dm::GQ; h++) {
-#pragma unroll
-          for (int i = 0; i < 8; i++) acc[h][i] = rows_sum4(acc[h][i]);
-          if (lane < 16) {
-#pragma unroll
-            for (int i = 0; i < 8; i++) s.wacc[c][h][8 * t16 + i] = acc[h][i];
-          }
-        }
-      } else {
+      // HF's two passes: the wave's (max, sum of exp(s - max)) to the control wave, which merges the
+      // workgroups' pairs across the XCD (barriers d..e); then bf16(exp(s - M) / L) times V.
       if (nb > 0) {
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+          const int pp = base0 + 32 * u + slot;
+#pragma unroll
+          for (int h = 0; h < Dm::GQ; h++) l_w[h] += pp < p.p_end ? exp_acc(sc[u][h] - m_w[h]) : 0.f;
+        }
+      }
+#pragma unroll
+      for (int h = 0; h < Dm::GQ; h++) {
+        l_w[h] = rows_sum4(l_w[h]);  // the rows hold different positions, the lanes of a row the same one
+        if (lane == 0) {
+          s.wml[c][h][0] = m_w[h];
+          s.wml[c][h][1] = l_w[h];
+        }
+      }
+      cstamp(L, 3);
+      QMK_SYNC();  // d
+      QMK_SYNC();  // e
+      if constexpr (!GU_C) prefetch_gu(L);
+      if constexpr (!O_C) prefetch_o(L);
+      cstamp(L, 4);
+      if (nb > 0) {
+        float gm[Dm::GQ], ginv[Dm::GQ];
+#pragma unroll
+        for (int h = 0; h < Dm::GQ; h++) {
+          gm[h] = s.ml[h][0];
+          ginv[h] = __fdiv_rn(1.0f, s.ml[h][1]);
+        }
         const u32x4 v_now = *reinterpret_cast<const u32x4*>(s.v + 8 * t16);
 #pragma unroll
         for (int u = 0; u < U; u++) {
@@ -1313,32 +1218,22 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
                                lo_bf16(vx.z), hi_bf16(vx.z), lo_bf16(vx.w), hi_bf16(vx.w)};
 #pragma unroll
           for (int h = 0; h < Dm::GQ; h++) {
-            // positions past the range load row 0 and get weight 0; their values are not used
-            const float e = pp < p.p_end ? exp_acc(sc[u][h] - m_w[h]) : 0.f;
-            l_w[h] += e;
+            // HF: softmax in fp32, probabilities rounded to bf16 before P@V; positions past the
+            // range (they load row 0) take probability 0 and their values are not used
+            const float pr = pp < p.p_end ? bf16r(exp_acc(sc[u][h] - gm[h]) * ginv[h]) : 0.f;
 #pragma unroll
-            for (int i = 0; i < 8; i++) acc[h][i] = pp < p.p_end ? __builtin_fmaf(e, vf[i], acc[h][i]) : acc[h][i];
+            for (int i = 0; i < 8; i++) acc[h][i] += pp < p.p_end ? pr * vf[i] : 0.f;
           }
         }
       }
-      cstamp(L, 3);
-      cstamp(L, 4);
-      // sum the wave's four rows; lanes 0..15 then hold dims 8*t16..+7 (a wave without positions
-      // publishes (-inf, 0, 0))
 #pragma unroll
       for (int h = 0; h < Dm::GQ; h++) {
-        l_w[h] = rows_sum4(l_w[h]);
 #pragma unroll
         for (int i = 0; i < 8; i++) acc[h][i] = rows_sum4(acc[h][i]);
         if (lane < 16) {
 #pragma unroll
           for (int i = 0; i < 8; i++) s.wacc[c][h][8 * t16 + i] = acc[h][i];
         }
-        if (lane == 0) {
-          s.wml[c][h][0] = m_w[h];
-          s.wml[c][h][1] = l_w[h];
-        }
-      }
       }
     } else {
       QMK_SYNC();  // c
@@ -1760,7 +1655,7 @@ __device__ __forceinline__ void decode_body(const KArgs& a, S& s) {
   p.p_end = min(p.C, p.p_begin + p.chunk);
   p.n_act = (p.C + p.chunk - 1) / p.chunk;
   if (wave == 0) {
-    control_path<M, !LONG && !Dm::kStream && kShortSplitK>(a, s, p, b, lane);
+    control_path<M>(a, s, p, b, lane);
   } else if constexpr (LONG) {
     compute_path<M, SAMPLED, true, DEEP>(a, s, p, b, wave - 1, lane, s.sw[wave - 1], s.pw[wave - 1]);
   } else {

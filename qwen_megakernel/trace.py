@@ -38,15 +38,6 @@ CTL_SEGMENTS = [
     "barrier k (wake-up)",
     "down_proj rows + d reduce-scatter across XCDs + publish h''",
 ]
-# The split-K form (Qwen3-0.6B below 2,048 positions) has no (max, sum) exchange: its control
-# wave stamps points 4 and 5 right after barrier c, and the compute waves run scores, softmax
-# and P@V in one window up to barrier f.
-CTL_SEGMENTS_SPLIT = CTL_SEGMENTS[:3] + [
-    "barrier c (wake-up)",
-    "(no softmax exchange)",
-    "scores + softmax + P@V (compute waves)",
-    "P@V partials + (max, sum) + combine + attention-output exchange",
-] + CTL_SEGMENTS[7:]
 COMPUTE_PHASES = ["QKV", "scores", "P@V", "O", "gate/up", "down"]
 CTL_READY = [1, 3, 5, 7, 9, 11]  # control stamp after which each compute phase may start
 
@@ -70,12 +61,9 @@ def capture(step_fn, num_layers: int, device="cuda") -> np.ndarray:
     return buf.cpu().numpy().reshape(-1, NUM_WG)
 
 
-def summarize(stamps: np.ndarray, num_layers: int, split: bool = False) -> dict:
-    """Per-segment times (us; mean/min/max over layers 1.. and workgroups).
-
-    ``split``: the stamps come from the split-K form (segment names follow it; its P@V phase
-    starts after the scores, not after a barrier, so it has no barrier wake-up)."""
-    names = CTL_SEGMENTS_SPLIT if split else CTL_SEGMENTS
+def summarize(stamps: np.ndarray, num_layers: int) -> dict:
+    """Per-segment times (us; mean/min/max over layers 1.. and workgroups)."""
+    names = CTL_SEGMENTS
     nl = num_layers
     t = (stamps - stamps[0].min()).astype(np.float64) * TICK_US
     ctl = t[: nl * CTL_POINTS].reshape(nl, CTL_POINTS, NUM_WG)
@@ -104,8 +92,7 @@ def summarize(stamps: np.ndarray, num_layers: int, split: bool = False) -> dict:
         b = (comp[first:, 2 * k + 1] - comp[first:, 2 * k]).ravel()
         w = (comp[first:, 2 * k] - ctl[first:, CTL_READY[k]]).ravel()
         busy[name] = round(float(b.mean()), 3)
-        if not (split and name == "P@V"):
-            wake[name] = round(float(w.mean()), 3)
+        wake[name] = round(float(w.mean()), 3)
     out["compute_busy_us"] = busy
     # time from the control wave's last stamp before a barrier to compute wave 0 starting after it
     out["barrier_wake_us"] = wake

@@ -33,15 +33,3 @@ def test_summarize_synthetic_stamps():
     assert all(abs(v - 0.07) < 1e-9 for v in s["barrier_wake_us"].values())
     assert "per layer" in trace.format_table(s)
     assert trace.entries(28) == (28 * 25 + 3) * 256
-
-
-def test_summarize_split_form_names():
-    nl = 2
-    n_pts = nl * (trace.CTL_POINTS + trace.COMPUTE_POINTS) + trace.FINAL_POINTS
-    st = np.arange(n_pts, dtype=np.int64)[:, None].repeat(trace.NUM_WG, 1)
-    s = trace.summarize(st, nl, split=True)
-    names = list(s["segments_us"])
-    assert names[3] == "barrier c (wake-up)" and names[4] == "(no softmax exchange)"
-    assert names[5].startswith("scores + softmax + P@V")
-    assert len(names) == trace.CTL_POINTS
-    assert "P@V" not in s["barrier_wake_us"] and "P@V" in s["compute_busy_us"]
