@@ -998,12 +998,15 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
     for (int i = 0; i < Dm::RQ_W; i++)
       load_row_p<Dm::LH>(wq + i * Dm::LH, qkv_row<M>(w, xcd, Dm::RQ_WG * r + Dm::RQ_W * c + i), lane);
   };
-  auto prefetch_qkv_row = [&](int layer, int i) {
+  // hot: read the final-norm weights (one H-wide row that every workgroup reads anyway) in place
+  // of the row, for a request that only keeps the load count of every path equal
+  auto prefetch_qkv_row = [&](int layer, int i, bool hot = false) {
     LayerPtrs w;
     w.wq = uniform_ptr(s.layers[layer].wq);
     w.wk = uniform_ptr(s.layers[layer].wk);
     w.wv = uniform_ptr(s.layers[layer].wv);
-    load_row_p<Dm::LH>(wq + i * Dm::LH, qkv_row<M>(w, xcd, Dm::RQ_WG * r + Dm::RQ_W * c + i), lane);
+    const uint16_t* row = qkv_row<M>(w, xcd, Dm::RQ_WG * r + Dm::RQ_W * c + i);
+    load_row_p<Dm::LH>(wq + i * Dm::LH, hot ? a.final_norm : row, lane);
   };
   auto prefetch_o = [&](int layer) {
     const uint16_t* wo_base = uniform_ptr(s.layers[layer].wo);
@@ -1067,14 +1070,15 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
     // (kKvStages batches in flight) and are read back with the same lane
     // layout: lane (slot, t16) holds dims 8*t16..+7 of position base + 32u + slot.
     const int nb = base0_of(c) < p.p_end ? (p.p_end - base0_of(c) + 32 * U - 1) / (32 * U) : 0;  // batches of this wave
-    auto kv_issue_at = [&](const uint16_t* base, int j, int stage) {
+    // row0: every position loads row 0 (a request that only keeps the load count of every path equal)
+    auto kv_issue_at = [&](const uint16_t* base, int j, int stage, bool row0 = false) {
       const int bpos = base0_of(c) + 32 * U * j;
 #pragma unroll
       for (int u = 0; u < U; u++) {
         const int pp = bpos + 32 * u + slot;
         // positions outside this workgroup's range (and pos, whose K/V come from
         // LDS) load row 0, which every cache has; their values are never used
-        const int pl = (pp < p.p_end && pp != p.pos) ? pp : 0;
+        const int pl = (!row0 && pp < p.p_end && pp != p.pos) ? pp : 0;
         __builtin_amdgcn_global_load_lds(as_global<void>(base + (size_t)pl * Dm::D + 8 * t16),
                                          (__attribute__((address_space(3))) void*)&s.kv[stage][c][u][0], 16, 0, 0);
       }
@@ -1575,12 +1579,16 @@ __device__ __forceinline__ void compute_path(const KArgs& a, Smem<M>& s, const S
       // behind the QKV rows.  Same-box A/B at context 1024: K and V requested in the layer's own
       // windows (K before barrier c, V after it) 2,125 tok/s; K here 2,140; K and V here
       // 2,151-2,152; the QKV rows here too instead of between the gate/up dot products 2,153
-      // (over contexts 129..1152: 2,177 -> 2,184).  (The last layer requests its own rows again,
-      // so every path issues the same loads.)
-      if (nb > 0) kv_issue(a.k_cache + L_next * kv_layer_stride + (size_t)xcd * a.max_seq_len * Dm::D, 0);
-      kv_issue_at(a.v_cache + L_next * kv_layer_stride + (size_t)xcd * a.max_seq_len * Dm::D, 0, 1);
-      prefetch_qkv_row(L_next, 0);
-      prefetch_qkv_row(L_next, 1);
+      // (over contexts 129..1152: 2,177 -> 2,184).  The last layer issues the same requests, so
+      // that every path issues the same loads and the compiler's counted waits stay exact, but
+      // they read one row that every workgroup of the XCD shares (row 0 of this layer's K and V
+      // rows of the XCD's head, the final-norm weights): L2 hits instead of a second HBM read of
+      // its own rows.
+      const bool last = L + 1 == p.nl;
+      if (nb > 0) kv_issue_at(a.k_cache + L_next * kv_layer_stride + (size_t)xcd * a.max_seq_len * Dm::D, 0, 0, last);
+      kv_issue_at(a.v_cache + L_next * kv_layer_stride + (size_t)xcd * a.max_seq_len * Dm::D, 0, 1, last);
+      prefetch_qkv_row(L_next, 0, last);
+      prefetch_qkv_row(L_next, 1, last);
     }
     cstamp(L, 11);
   }
