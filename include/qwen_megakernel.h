@@ -180,6 +180,21 @@ int qmk_decode_model_noalloc(
     void *hidden_buffer, void *g_normalized, int num_layers, int position,
     int max_seq_len, float attn_scale, hipStream_t stream);
 
+/* The allocation-free entry point's status, read without allocating: waits
+ * for `stream` and returns the error bits the last qmk_decode_model_noalloc
+ * call on the current device left in the scratch array (0 = ok;
+ * 0xffffffff if qmk_init() has not run on this device or a HIP call failed).
+ * The next qmk_decode_model_noalloc call clears them.  No counterpart in the
+ * reference; for the callers that cannot allocate. */
+uint32_t qmk_noalloc_device_error(hipStream_t stream);
+
+/* Sets the bound of every device-side wait of qmk_decode_model_noalloc on the
+ * current device, in wall-clock ticks (0 restores the default of one second).
+ * qmk_init() first (QMK_ERR_INIT).  Tests use a tiny bound to drive its
+ * failure path without any risk of a hang.  No counterpart in the reference;
+ * for the callers that cannot allocate.  Returns a status code. */
+int qmk_noalloc_set_wait_limit(uint32_t ticks);
+
 /* launch_ldg_generate_nosync for `model`.  Returns a status code. */
 int qmk_generate_model(
     int model, int first_token_id, int num_steps, const void *embed_weight,

@@ -108,6 +108,7 @@ struct DevInfo {
   bool order_valid = false;
   bool order_multi = false;            // a second stream has launched on this device
   uint32_t* scratch = nullptr;         // this device's copy of `scratch` (set by qmk_init)
+  uint32_t noalloc_timeout = 0;        // wait bound of qmk_decode_model_noalloc (0: one second)
   bool batch_ok = false;               // every batched persistent kernel fits one workgroup per CU
   // device copies of the layer tables the batched persistent kernel was called with (device_table)
   struct Table {
@@ -900,16 +901,20 @@ int qmk_decode_model_noalloc(int model, int input_token_id, int* output_token_id
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess) return fail(QMK_ERR_HIP);
   DevInfo* di = nullptr;
+  uint32_t timeout = 0;
   {
     std::lock_guard<std::mutex> lk(g_mu);
     auto it = g_dev.find(dev);
-    if (it != g_dev.end() && it->second.ok && it->second.scratch) di = &it->second;
+    if (it != g_dev.end() && it->second.ok && it->second.scratch) {
+      di = &it->second;
+      timeout = di->noalloc_timeout ? di->noalloc_timeout : di->ticks_per_s;
+    }
   }
   if (!di) return fail(QMK_ERR_INIT);
   Ctx view;  // the kernel arguments' view of the scratch; nothing is allocated
   view.st = reinterpret_cast<DecodeState*>(di->scratch);
   view.x = di->scratch + sizeof(DecodeState) / 4;
-  view.timeout = di->ticks_per_s;
+  view.timeout = timeout;
   view.xcd_local = di->xcd_local;
   KArgs a = make_args(c, &view);
   a.out_token = output_token_id;
@@ -923,6 +928,37 @@ int qmk_decode_model_noalloc(int model, int input_token_id, int* output_token_id
   s = hipGetLastError() == hipSuccess ? launch(a, model, form_of(position + 1), stream) : QMK_ERR_HIP;
   const int so = order.finish();
   return fail(s != QMK_OK ? s : so);
+}
+
+namespace {
+// the current device's entry once qmk_init has set its scratch up, else null
+DevInfo* noalloc_device() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+  std::lock_guard<std::mutex> lk(g_mu);
+  auto it = g_dev.find(dev);
+  return (it != g_dev.end() && it->second.ok && it->second.scratch) ? &it->second : nullptr;
+}
+}  // namespace
+
+int qmk_noalloc_set_wait_limit(uint32_t ticks) {
+  DevInfo* di = noalloc_device();
+  if (!di) return fail(QMK_ERR_INIT);
+  std::lock_guard<std::mutex> lk(g_mu);
+  di->noalloc_timeout = ticks;
+  return fail(QMK_OK);
+}
+
+uint32_t qmk_noalloc_device_error(hipStream_t stream) {
+  DevInfo* di = noalloc_device();
+  if (!di) return 0xffffffffu;
+  if (hipStreamSynchronize(stream) != hipSuccess) return 0xffffffffu;
+  // the state header sits at the start of the scratch; one word straight into a local
+  uint32_t v = 0;
+  if (hipMemcpy(&v, &reinterpret_cast<DecodeState*>(di->scratch)->err, sizeof(v), hipMemcpyDeviceToHost) !=
+      hipSuccess)
+    return 0xffffffffu;
+  return v;
 }
 
 int qmk_last_status(void) { return t_status; }

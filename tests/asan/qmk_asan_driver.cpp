@@ -67,6 +67,8 @@ void host_argument_checks() {
   expect(qmk_forward_workspace_bytes(5, 16, 1, 64) == 0, "forward workspace: unknown model");
   expect(qmk_decode_batch_workspace_bytes(0, 0, 64) == 0, "batch workspace: batch 0");
   expect(qmk_trace_entries(28) > qmk_trace_entries(2) && qmk_trace_entries(2) > 0, "trace entries");
+  expect(qmk_noalloc_set_wait_limit(1) == QMK_ERR_INIT, "noalloc wait limit before qmk_init");
+  expect(qmk_noalloc_device_error(nullptr) == 0xffffffffu, "noalloc error before qmk_init");
   for (int s = 0; s <= 8; s++) expect(qmk_status_string(s) != nullptr, "status string");
   int wg = 0, th = 0;
   qmk_launch_geometry(&wg, &th);
@@ -141,6 +143,8 @@ void gpu_paths() {
   expect(qmk_decode_model_noalloc(QMK_MODEL_QWEN3_0_6B, 11, tok, logits, embed, dtable, fnorm, embed, cos_t, sin_t, kc,
                                   vc, hidden, normed, kLayers, 3, kSeq, scale, s1) == QMK_OK,
          "noalloc");
+  expect(qmk_noalloc_device_error(s1) == 0u, "noalloc error bits");
+  expect(qmk_noalloc_set_wait_limit(0) == QMK_OK, "noalloc wait limit");
   expect(qmk_decode_model_noalloc(QMK_MODEL_QWEN3_0_6B, 11, tok, logits, embed, dtable, fnorm, embed, cos_t, sin_t, kc,
                                   vc, hidden, normed, 29, 3, kSeq, scale, s1) == QMK_ERR_SIZE,
          "noalloc: too many layers");

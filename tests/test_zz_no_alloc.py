@@ -77,3 +77,44 @@ def test_noalloc_rejects_sizes_beyond_its_limits(weights_gpu):
     lg = torch.empty(151936, dtype=torch.float32, device="cuda")
     st = _call(lib.qmk_decode_model_noalloc, dec, 5, out, lg, 29, 0, torch.cuda.current_stream())
     assert st == 7 and b"limits" in lib.qmk_status_string(st)
+
+
+def test_noalloc_failure_is_read_without_allocating_and_the_next_call_recovers(weights_gpu, prompt):
+    """A call whose waits are bounded to one tick fails on the device: it leaves -1 in the output
+    token and error bits in the scratch array, which qmk_noalloc_device_error reads without
+    allocating.  The next call, with the default bound, starts clean and gives qmk_decode_model's
+    token, logits and cache bit for bit."""
+    lib = _lib()
+    lib.qmk_noalloc_device_error.restype = ctypes.c_uint32
+    lib.qmk_noalloc_device_error.argtypes = [ctypes.c_void_p]
+    lib.qmk_noalloc_set_wait_limit.argtypes = [ctypes.c_uint32]
+    assert lib.qmk_init() == 0
+    stream = torch.cuda.current_stream()
+    layers, max_seq, ctx_ids, tok = 4, 64, prompt[:3], 21
+    a = decoder(weights_gpu, num_layers=layers, max_seq_len=max_seq)
+    b = decoder(weights_gpu, num_layers=layers, max_seq_len=max_seq)
+    for d in (a, b):
+        d.prefill(ctx_ids)
+    torch.cuda.synchronize()
+    pos = len(ctx_ids)
+    outs = [torch.full((1,), -7, dtype=torch.int32, device="cuda") for _ in range(2)]
+    lgs = [torch.zeros(151936, dtype=torch.float32, device="cuda") for _ in range(2)]
+    assert _call(lib.qmk_decode_model, a, tok, outs[0], lgs[0], layers, pos, stream) == 0
+    torch.cuda.synchronize()
+    free_before = torch.cuda.mem_get_info()[0]
+    try:
+        assert lib.qmk_noalloc_set_wait_limit(1) == 0
+        assert _call(lib.qmk_decode_model_noalloc, b, tok, outs[1], lgs[1], layers, pos, stream) == 0
+        err = lib.qmk_noalloc_device_error(ctypes.c_void_p(stream.cuda_stream))
+        assert err not in (0, 0xFFFFFFFF), hex(err)
+        assert int(outs[1].item()) == -1
+    finally:
+        assert lib.qmk_noalloc_set_wait_limit(0) == 0
+    outs[1].fill_(-7)
+    assert _call(lib.qmk_decode_model_noalloc, b, tok, outs[1], lgs[1], layers, pos, stream) == 0
+    assert lib.qmk_noalloc_device_error(ctypes.c_void_p(stream.cuda_stream)) == 0
+    assert torch.cuda.mem_get_info()[0] == free_before, "the allocation-free calls changed free memory"
+    ta, tb = int(outs[0].item()), int(outs[1].item())
+    assert ta >= 0 and ta == tb, (ta, tb)
+    assert torch.equal(lgs[0], lgs[1]), f"logits differ by {(lgs[0] - lgs[1]).abs().max().item()}"
+    assert torch.equal(a._k_cache, b._k_cache) and torch.equal(a._v_cache, b._v_cache), "caches differ"
