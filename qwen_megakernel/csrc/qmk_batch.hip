@@ -543,204 +543,256 @@ __global__ void __launch_bounds__(256) attention_rows(const uint16_t* __restrict
   dst[threadIdx.x] = (uint16_t)f32_to_bf16(pv_merge_waves(acc, pv));
 }
 
-// Prompt prefill attention on MFMA.  One workgroup of 8 waves per (tile of kQT
-// consecutive tokens, KV head g): when the tile's tokens are one sequence at
-// consecutive positions (every prompt prefill), the tile's query rows of heads
-// 2g and 2g+1 share each block of kKB cached keys and values, staged through
-// LDS, instead of every row reading its whole context.  Two passes over the
-// keys, as HF's eager softmax: pass 1 gives each row's max M and sum L of
-// exp(s - M) (per lane online over the blocks, then across the lanes); pass 2
-// recomputes the scores, rounds the probabilities bf16(exp(s - M) / L) and
-// multiplies them with V on MFMA.  Scores are bf16(bf16(q.k) * scale), as in
-// attention_rows.  A tile that is not one such run (several sequences, an
-// invalid token) is marked in redo[tile] and left to attention_rows.
+// Prompt prefill attention on MFMA.  Tiles of kQT consecutive tokens; one
+// workgroup of 8 waves per (pair of tiles, query head h): tiles i and nt-1-i
+// (the middle tile alone when nt is odd), one after the other, so that every
+// workgroup's causal work is about the same (the last tile alone has twice
+// the average).  For a tile whose tokens are one sequence at consecutive
+// positions (every prompt prefill) the tile's 64 query rows share each block
+// of kKB cached keys and values, staged through LDS.  Two passes over the keys,
+// as HF's eager softmax: pass 1 gives each row's max M and sum L of exp(s - M)
+// (online per lane over the blocks, then across lanes and the two waves of a
+// row group); pass 2 recomputes the scores, rounds the probabilities
+// bf16(exp(s - M) / L) and multiplies them with V on MFMA.  Scores are
+// bf16(bf16(q.k) * scale), as in attention_rows.  A tile that is not one such
+// run (several sequences, an invalid token) is marked in redo[tile] and left to
+// attention_rows.
 //
 // MFMA 16x16x32 bf16 layout: lane l supplies A[l%16][8(l/16)..+7] and
 // B[8(l/16)..+7][l%16] and receives C[4(l/16)+i][l%16].  Wave w owns query rows
-// 16(w/2)..+15 of the tile for q head 2g + w%2 (the two heads of a row group in
-// two waves: half the serial work per wave, two waves per SIMD).  Scores: A =
-// the rows' q (dims as k), B = K rows of the block (its positions as columns).
-// P@V: A = the wave's probabilities (positions as k, through LDS), B = V
-// transposed in LDS (dims as columns).
+// 16(w/2)..+15 of the tile and keys 32(w%2)..+31 of every block (two waves per
+// row group, each with half of the keys).  Scores are computed transposed (A =
+// 16 keys' K rows, B = the rows' q), so lane (l16, lg) holds row l16's scores of
+// keys 16n + 4lg + i, i = 0..3: every lane carries one query row.  P@V takes A =
+// those probabilities straight from the registers: the 8 k-slots 8lg..8lg+7 of
+// a 32-key step are keys 4lg..4lg+3 and 16+4lg..16+4lg+3 of the wave's half
+// block, and V is stored transposed in LDS in that slot order (B = V^T rows,
+// 16 contiguous bytes per lane).  The two waves of a row group add their P@V
+// partials through LDS at the end (in a fixed order).
 constexpr int kAttnWaves = 8;
+
+// LDS slot of key q (0..kKB-1) of a block in the transposed V: the order in
+// which a wave's P@V k-slots take its keys (see above)
+__device__ __forceinline__ int attn_v_slot(int q) {
+  const int half = q >> 5, r = q & 31;
+  return 32 * half + 8 * ((r & 15) >> 2) + 4 * (r >> 4) + (r & 3);
+}
 
 __global__ void __launch_bounds__(kAttnWaves * 64) attention_mfma(const uint16_t* __restrict__ Q,
                                                                  const Tok* __restrict__ tok, int T, int L, Cache c,
                                                                  float scale, uint16_t* __restrict__ out,
                                                                  int* __restrict__ redo) {
   constexpr int NT = kAttnWaves * 64;
-  __shared__ __align__(16) uint16_t Ks[kKB][kKPad];
-  __shared__ __align__(16) uint16_t Vt[kD][kVPad];
-  __shared__ __align__(16) uint16_t Ps[kAttnWaves][16][kVPad];
-  __shared__ int s_ok;
-  const int tile = blockIdx.x, g = blockIdx.y;
-  const int t0 = tile * kQT, nrows = min(kQT, T - t0);
+  static_assert(kQT == 64 && kKB == 64 && kAttnWaves == 8, "4 row groups of 16 x 2 key halves of 32");
+  // K block [kKB][kKPad] and transposed V [kD][kVPad]; after the passes the same bytes hold the
+  // odd waves' P@V partials [4 row groups][16 rows][kD] fp32 for the even waves to add
+  constexpr int kKBytes = kKB * kKPad * 2, kVBytes = kD * kVPad * 2, kRedBytes = 4 * 16 * kD * 4;
+  static_assert(kKBytes + kVBytes >= kRedBytes, "the partials fit in the K/V buffers");
+  __shared__ __align__(16) unsigned char smem[kKBytes + kVBytes];
+  __shared__ int s_ok[2];
+  auto Ks = reinterpret_cast<uint16_t(*)[kKPad]>(smem);
+  auto Vt = reinterpret_cast<uint16_t(*)[kVPad]>(smem + kKBytes);
+  auto Vw = reinterpret_cast<uint32_t(*)[kVPad / 2]>(smem + kKBytes);  // the same rows as 32-bit words
+  auto red = reinterpret_cast<float(*)[16][kD]>(smem);
+  __shared__ float s_ml[4][2][16][2];  // (max, sum) per row group, key half and row
+  const int nt = (T + kQT - 1) / kQT;
+  const int h = blockIdx.y, g = h >> 1;
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, l16 = lane & 15, lg = lane >> 4;
-  const int hq = w & 1, rg = w >> 1;  // q head 2g + hq, rows 16rg..16rg+15
-  const Tok first = tok[t0];
-  if (threadIdx.x == 0) s_ok = 1;
+  const int rg = w >> 1, kh = w & 1;  // rows 16rg..16rg+15, keys 32kh..32kh+31 of each block
+  const int tiles[2] = {(int)blockIdx.x, nt - 1 - (int)blockIdx.x};
+  const int ntile = tiles[1] == tiles[0] ? 1 : 2;
+  // which of the pair's tiles are one sequence at consecutive positions
+  if (threadIdx.x < 2) s_ok[threadIdx.x] = 1;
   __syncthreads();
-  if ((int)threadIdx.x < nrows) {
-    const Tok tk = tok[t0 + threadIdx.x];
-    if (!tk.valid || tk.seq != first.seq || tk.pos != first.pos + (int)threadIdx.x) s_ok = 0;
+  for (int u = 0; u < ntile; u++) {
+    const int t0 = tiles[u] * kQT, nrows = min(kQT, T - t0);
+    if ((int)threadIdx.x < nrows) {
+      const Tok first = tok[t0], tk = tok[t0 + threadIdx.x];
+      if (!tk.valid || tk.seq != first.seq || tk.pos != first.pos + (int)threadIdx.x) s_ok[u] = 0;
+    }
   }
   __syncthreads();
-  const bool ok = s_ok != 0;
-  if (g == 0 && threadIdx.x == 0) redo[tile] = ok ? 0 : 1;
-  if (!ok) return;
-  const int pos0 = first.pos, pmax = pos0 + nrows - 1;
-  const size_t base = cache_base(c, first, L, g);
-  const uint16_t* kc = c.k + base;
-  const uint16_t* vc = c.v + base;
-  // A operands of this lane's query row (rows past the tile's tokens repeat its last one)
-  const int tq = t0 + min(16 * rg + l16, nrows - 1);
-  bf16x8 qa[4];
+  if (h == 0 && threadIdx.x < (unsigned)ntile) redo[tiles[threadIdx.x]] = s_ok[threadIdx.x] ? 0 : 1;
+
+  for (int u = 0; u < ntile; u++) {
+    if (!s_ok[u]) continue;  // uniform over the workgroup
+    const int t0 = tiles[u] * kQT, nrows = min(kQT, T - t0);
+    const Tok first = tok[t0];
+    const int pos0 = first.pos, pmax = pos0 + nrows - 1;
+    const size_t base = cache_base(c, first, L, g);
+    const uint16_t* kc = c.k + base;
+    const uint16_t* vc = c.v + base;
+    // B operands: this lane's query row (rows past the tile's tokens repeat its last one)
+    const int tq = t0 + min(16 * rg + l16, nrows - 1);
+    bf16x8 qb[4];
 #pragma unroll
-  for (int kk = 0; kk < 4; kk++) qa[kk] = ld_bf16x8(Q + (size_t)tq * kQS + (2 * g + hq) * kD + 32 * kk + 8 * lg);
-  // positions of the rows this lane's accumulators hold: rows 16rg + 4lg + i
-  int rpos[4];
+    for (int kk = 0; kk < 4; kk++) qb[kk] = ld_bf16x8(Q + (size_t)tq * kQS + h * kD + 32 * kk + 8 * lg);
+    const int rpos = pos0 + 16 * rg + l16;      // this lane's row position
+    const int wave_last = pos0 + 16 * rg + 15;  // the wave's largest row position
+    const int nkb = (pmax + kKB) / kKB;         // blocks covering positions 0..pmax
+    // Block kb: positions kb*kKB + pr; rows past pmax load row pmax (masked below).  Each
+    // thread carries kCh 16-byte chunks of K (and of V): block kb+1 is requested into registers
+    // before block kb's MFMAs, so its memory latency overlaps them, and written to LDS after
+    // the next barrier.
+    constexpr int kCh = kKB * (kD / 8) / NT;
+    u32x4 rk[kCh], rv[kCh];
+    auto load_k = [&](int kb) {
 #pragma unroll
-  for (int i = 0; i < 4; i++) rpos[i] = pos0 + 16 * rg + 4 * lg + i;
-  const int wave_last = pos0 + 16 * rg + 15;  // the wave's largest row position
-  const int nkb = (pmax + kKB) / kKB;         // blocks covering positions 0..pmax
-  // Block kb: positions kb*kKB + pr; rows past pmax load row pmax (masked
-  // below).  Each thread carries kCh 16-byte chunks of K (and of V): block kb+1
-  // is requested into registers before block kb's MFMAs, so its memory latency
-  // overlaps them, and written to LDS after the next barrier.
-  constexpr int kCh = kKB * (kD / 8) / NT;
-  u32x4 rk[kCh], rv[kCh];
-  auto load_k = [&](int kb) {
+      for (int j = 0; j < kCh; j++) {
+        const int ci = threadIdx.x + NT * j, pr = ci >> 4, col = (ci & 15) * 8;
+        rk[j] = ld16(kc + (size_t)min(kb * kKB + pr, pmax) * kD + col);
+      }
+    };
+    // V: this thread carries keys 2va and 2va+1 of the block, dims 8vc..8vc+7 (a wave's lanes
+    // cover four dim chunks of 16 key pairs), so each transposed LDS word takes both keys' values
+    static_assert(kCh == 2, "one key pair per thread");
+    const int va = (lane >> 2) + 16 * (w & 1), vcol = 8 * ((lane & 3) + 4 * (w >> 1));
+    auto load_v = [&](int kb) {
 #pragma unroll
-    for (int j = 0; j < kCh; j++) {
-      const int ci = threadIdx.x + NT * j, pr = ci >> 4, col = (ci & 15) * 8;
-      rk[j] = ld16(kc + (size_t)min(kb * kKB + pr, pmax) * kD + col);
-    }
-  };
-  auto load_v = [&](int kb) {
+      for (int j = 0; j < 2; j++) rv[j] = ld16(vc + (size_t)min(kb * kKB + 2 * va + j, pmax) * kD + vcol);
+    };
+    auto put_k = [&]() {
 #pragma unroll
-    for (int j = 0; j < kCh; j++) {
-      const int ci = threadIdx.x + NT * j, pr = ci >> 4, col = (ci & 15) * 8;
-      rv[j] = ld16(vc + (size_t)min(kb * kKB + pr, pmax) * kD + col);
-    }
-  };
-  auto put_k = [&]() {
-#pragma unroll
-    for (int j = 0; j < kCh; j++) {
-      const int ci = threadIdx.x + NT * j, pr = ci >> 4, col = (ci & 15) * 8;
-      *reinterpret_cast<u32x4*>(&Ks[pr][col]) = rk[j];
-    }
-  };
-  auto put_v = [&]() {  // transposed: Vt[dim][position]
-#pragma unroll
-    for (int j = 0; j < kCh; j++) {
-      const int ci = threadIdx.x + NT * j, pr = ci >> 4, col = (ci & 15) * 8;
-      const uint32_t u[4] = {rv[j].x, rv[j].y, rv[j].z, rv[j].w};
+      for (int j = 0; j < kCh; j++) {
+        const int ci = threadIdx.x + NT * j, pr = ci >> 4, col = (ci & 15) * 8;
+        *reinterpret_cast<u32x4*>(&Ks[pr][col]) = rk[j];
+      }
+    };
+    auto put_v = [&]() {  // transposed, keys in P@V slot order: Vt[dim][slot]; keys 2va, 2va+1
+                          // take adjacent slots, so each dim is one 32-bit word
+      const int sw = attn_v_slot(2 * va) >> 1;
+      const uint32_t k0[4] = {rv[0].x, rv[0].y, rv[0].z, rv[0].w}, k1[4] = {rv[1].x, rv[1].y, rv[1].z, rv[1].w};
 #pragma unroll
       for (int e = 0; e < 4; e++) {
-        Vt[col + 2 * e][pr] = (uint16_t)(u[e] & 0xffffu);
-        Vt[col + 2 * e + 1][pr] = (uint16_t)(u[e] >> 16);
+        Vw[vcol + 2 * e][sw] = (k0[e] & 0xffffu) | (k1[e] << 16);
+        Vw[vcol + 2 * e + 1][sw] = (k0[e] >> 16) | (k1[e] & 0xffff0000u);
       }
-    }
-  };
-  // raw q.k of the block's positions kb*kKB + 16n + l16 for rows 4lg + i
-  auto tile_scores = [&](int n) {
-    f32x4 sc = f32x4{0.f, 0.f, 0.f, 0.f};
+    };
+    // raw q.k of row l16 with keys kb*kKB + 32kh + 16n + 4lg + i
+    auto tile_scores = [&](int n) {
+      f32x4 sc = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int kk = 0; kk < 4; kk++)
-      sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-          qa[kk], *reinterpret_cast<const bf16x8*>(&Ks[16 * n + l16][32 * kk + 8 * lg]), sc, 0, 0, 0);
-    return sc;
-  };
-  // ---- pass 1: per lane, online max and sum of exp over its positions
-  float m[4], ls[4];
+      for (int kk = 0; kk < 4; kk++)
+        sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+            *reinterpret_cast<const bf16x8*>(&Ks[32 * kh + 16 * n + l16][32 * kk + 8 * lg]), qb[kk], sc, 0, 0, 0);
+      return sc;
+    };
+    // ---- pass 1: per lane, online max and sum of exp over its positions (one exp per score,
+    // one rescale per block)
+    float m = -INFINITY, ls = 0.f;
+    load_k(0);
+    for (int kb = 0; kb < nkb; kb++) {
+      __syncthreads();  // the previous block's reads are done
+      put_k();
+      __syncthreads();
+      if (kb + 1 < nkb) load_k(kb + 1);
+      const int kbase = kb * kKB + 32 * kh;
+      if (kbase > wave_last) continue;  // every key of the wave's half block follows its rows
+      float x[2][4];
+      float mb = -INFINITY;
 #pragma unroll
-  for (int i = 0; i < 4; i++) {
-    m[i] = -INFINITY;
-    ls[i] = 0.f;
-  }
-  load_k(0);
-  for (int kb = 0; kb < nkb; kb++) {
-    __syncthreads();  // the previous block's reads are done
-    put_k();
-    __syncthreads();
-    if (kb + 1 < nkb) load_k(kb + 1);
-    if (kb * kKB > wave_last) continue;  // every position of the block follows the wave's rows
+      for (int n = 0; n < 2; n++) {
+        const f32x4 sc = kbase + 16 * n <= wave_last ? tile_scores(n) : f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int n = 0; n < kKB / 16; n++) {
-      if (kb * kKB + 16 * n > wave_last) break;
-      const f32x4 sc = tile_scores(n);
-      const int p = kb * kKB + 16 * n + l16;
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        if (p <= rpos[i]) {
-          const float x = bf16r(bf16r(sc[i]) * scale);
-          const float mn = fmaxf(m[i], x);
-          ls[i] = ls[i] * exp_acc(m[i] - mn) + exp_acc(x - mn);
-          m[i] = mn;
+        for (int i = 0; i < 4; i++) {
+          const int p = kbase + 16 * n + 4 * lg + i;
+          x[n][i] = p <= rpos ? bf16r(bf16r(sc[i]) * scale) : -INFINITY;
+          mb = fmaxf(mb, x[n][i]);
         }
       }
-    }
-  }
-  // each row's M and 1/L over its 16 lanes (lanes with equal lg hold the same rows)
-  float gm[4], ginv[4];
+      const float mn = fmaxf(m, mb);
+      if (mn != -INFINITY) {
+        float e = 0.f;
 #pragma unroll
-  for (int i = 0; i < 4; i++) {
-    float mx = m[i];
+        for (int n = 0; n < 2; n++)
 #pragma unroll
-    for (int o = 1; o < 16; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
-    float sm = m[i] == -INFINITY ? 0.f : ls[i] * exp_acc(m[i] - mx);
-#pragma unroll
-    for (int o = 1; o < 16; o <<= 1) sm += __shfl_xor(sm, o);
-    gm[i] = mx;
-    ginv[i] = __fdiv_rn(1.0f, sm);
-  }
-  // ---- pass 2: probabilities (bf16, as HF rounds them) times V
-  f32x4 acc[8];
-#pragma unroll
-  for (int j = 0; j < 8; j++) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-  load_k(0);
-  load_v(0);
-  for (int kb = 0; kb < nkb; kb++) {
-    __syncthreads();
-    put_k();
-    put_v();
-    __syncthreads();
-    if (kb + 1 < nkb) {
-      load_k(kb + 1);
-      load_v(kb + 1);
-    }
-    if (kb * kKB > wave_last) continue;
-#pragma unroll
-    for (int n = 0; n < kKB / 16; n++) {
-      // a tile wholly past the wave's rows is masked for every row: no MFMA for it
-      const f32x4 sc = kb * kKB + 16 * n <= wave_last ? tile_scores(n) : f32x4{0.f, 0.f, 0.f, 0.f};
-      const int p = kb * kKB + 16 * n + l16;
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const float pr = p <= rpos[i] ? bf16r(exp_acc(bf16r(bf16r(sc[i]) * scale) - gm[i]) * ginv[i]) : 0.f;
-        Ps[w][4 * lg + i][16 * n + l16] = (uint16_t)f32_to_bf16(pr);
+          for (int i = 0; i < 4; i++) e += exp_acc(x[n][i] - mn);
+        ls = (m == -INFINITY ? 0.f : ls * exp_acc(m - mn)) + e;
+        m = mn;
       }
     }
-    // the wave's own probabilities, written by its lanes, read back in the A layout
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // row l16's (max, sum): over the 4 lanes of equal l16, then the row group's two waves (the
+    // even wave's pair first in every wave, so both waves hold the same M and 1/L)
+    {
+      float mx = m;
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      float sm = m == -INFINITY ? 0.f : ls * exp_acc(m - mx);
+      sm += __shfl_xor(sm, 16);
+      sm += __shfl_xor(sm, 32);
+      if (lg == 0) {
+        s_ml[rg][kh][l16][0] = mx;
+        s_ml[rg][kh][l16][1] = sm;
+      }
+    }
+    __syncthreads();
+    float gm, ginv;
+    {
+      const float m0 = s_ml[rg][0][l16][0], l0 = s_ml[rg][0][l16][1];
+      const float m1 = s_ml[rg][1][l16][0], l1 = s_ml[rg][1][l16][1];
+      gm = fmaxf(m0, m1);
+      const float sm = (m0 == -INFINITY ? 0.f : l0 * exp_acc(m0 - gm)) + (m1 == -INFINITY ? 0.f : l1 * exp_acc(m1 - gm));
+      ginv = __fdiv_rn(1.0f, sm);
+    }
+    // ---- pass 2: probabilities (bf16, as HF rounds them) times V
+    f32x4 acc[8];
 #pragma unroll
-    for (int ks = 0; ks < kKB / 32; ks++) {
-      const bf16x8 pa = *reinterpret_cast<const bf16x8*>(&Ps[w][l16][32 * ks + 8 * lg]);
+    for (int j = 0; j < 8; j++) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    load_k(0);
+    load_v(0);
+    for (int kb = 0; kb < nkb; kb++) {
+      __syncthreads();
+      put_k();
+      put_v();
+      __syncthreads();
+      if (kb + 1 < nkb) {
+        load_k(kb + 1);
+        load_v(kb + 1);
+      }
+      const int kbase = kb * kKB + 32 * kh;
+      if (kbase > wave_last) continue;
+      // A operand: k-slot 4n + i of this lane is key kbase + 16n + 4lg + i of row l16
+      uint32_t pw[4];
+#pragma unroll
+      for (int n = 0; n < 2; n++) {
+        // a 16-key tile wholly past the wave's rows is masked for every row: no MFMA for it
+        const f32x4 sc = kbase + 16 * n <= wave_last ? tile_scores(n) : f32x4{0.f, 0.f, 0.f, 0.f};
+        float pr[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const int p = kbase + 16 * n + 4 * lg + i;
+          pr[i] = p <= rpos ? bf16r(exp_acc(bf16r(bf16r(sc[i]) * scale) - gm) * ginv) : 0.f;
+        }
+        pw[2 * n] = f32_to_bf16(pr[0]) | (f32_to_bf16(pr[1]) << 16);
+        pw[2 * n + 1] = f32_to_bf16(pr[2]) | (f32_to_bf16(pr[3]) << 16);
+      }
+      const bf16x8 pa = __builtin_bit_cast(bf16x8, u32x4{pw[0], pw[1], pw[2], pw[3]});
 #pragma unroll
       for (int j = 0; j < 8; j++)
         acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-            pa, *reinterpret_cast<const bf16x8*>(&Vt[16 * j + l16][32 * ks + 8 * lg]), acc[j], 0, 0, 0);
+            pa, *reinterpret_cast<const bf16x8*>(&Vt[16 * j + l16][32 * kh + 8 * lg]), acc[j], 0, 0, 0);
     }
-  }
+    // the row group's two partials: the odd wave's through LDS (over the K/V buffers), added to
+    // the even wave's
+    __syncthreads();
+    if (kh == 1) {
 #pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const int r = 16 * rg + 4 * lg + i;
-    if (r < nrows) {
-      uint16_t* dst = out + (size_t)(t0 + r) * kQS + (2 * g + hq) * kD;
+      for (int j = 0; j < 8; j++)
 #pragma unroll
-      for (int j = 0; j < 8; j++) dst[16 * j + l16] = (uint16_t)f32_to_bf16(acc[j][i]);
+        for (int i = 0; i < 4; i++) red[rg][4 * lg + i][16 * j + l16] = acc[j][i];
+    }
+    __syncthreads();
+    if (kh == 0) {
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int r = 16 * rg + 4 * lg + i;
+        if (r < nrows) {
+          uint16_t* dst = out + (size_t)(t0 + r) * kQS + h * kD;
+#pragma unroll
+          for (int j = 0; j < 8; j++)
+            dst[16 * j + l16] = (uint16_t)f32_to_bf16(acc[j][i] + red[rg][4 * lg + i][16 * j + l16]);
+        }
+      }
     }
   }
 }
@@ -1737,8 +1789,9 @@ int forward(const Args& a, hipStream_t s) {
       if (mfma_attn) {
         // tiles of one sequence's consecutive tokens on MFMA; any other tile row by row
         int* redo = reinterpret_cast<int*>(a.ws + l.redo);
-        hipLaunchKernelGGL(attention_mfma, dim3((T + kQT - 1) / kQT, kNKV), dim3(kAttnWaves * 64), 0, s, Qb, tok, T,
-                           L, a.cache, a.attn_scale, ATT, redo);
+        const int ntiles = (T + kQT - 1) / kQT;
+        hipLaunchKernelGGL(attention_mfma, dim3((ntiles + 1) / 2, kNQ), dim3(kAttnWaves * 64), 0, s, Qb, tok, T, L,
+                           a.cache, a.attn_scale, ATT, redo);
         hipLaunchKernelGGL(attention_rows, dim3(T, kNKV), dim3(256), 0, s, Qb, tok, L, a.cache, a.attn_scale, ATT,
                            redo);
       } else {

@@ -179,6 +179,35 @@ def test_long_two_sequence_prefill_mfma_attention(shape, exact06, weights_gpu):
     print(t)
 
 
+def test_long_single_sequence_prefill_mfma_attention(shape, exact06, weights_gpu):
+    """A 2048-token prompt of one sequence, 2 layers: the MFMA attention's 32 tiles in 16 pairs
+    (tiles i and 31 - i in one workgroup per query head), rows 0..2047 in every tile; every 97th
+    row and the last against the oracle, and a repeat bit-exact."""
+    from qwen_megakernel.model import BatchDecoder
+    from qwen_megakernel.weights import make_prompt
+
+    layers, n = 2, 2048
+    prompt = make_prompt(n, shape.vocab, seed=91)
+    bd = BatchDecoder(weights=weights_gpu, batch_size=1, max_seq_len=n, num_layers=layers, verbose=False)
+    rows = list(range(0, n, 97)) + [n - 1]
+    runs = []
+    for _ in range(2):
+        out = torch.empty(len(rows), dtype=torch.int32, device="cuda")
+        logits = torch.empty(len(rows), V, dtype=torch.float32, device="cuda")
+        bd._forward(_i32(prompt), _i32([0] * n), _i32(list(range(n))), _i32(rows), out, logits, bd._k_cache,
+                    bd._v_cache, n)
+        runs.append((out.cpu().tolist(), logits.cpu()))
+    got, lg = runs[0]
+    assert runs[1][0] == got and torch.equal(runs[1][1], lg), "second forward differs"
+    orc = exact_oracle(exact06, shape, n, num_layers=layers)
+    ref = oracle_steps(orc, bd._k_cache[0], bd._v_cache[0], 0, prompt, emit=rows)
+    check_kv_rows("2048-token prefill", orc, bd._k_cache[0], bd._v_cache[0], 0, n)
+    t = Tally("2048-token prefill")
+    for r, i in enumerate(rows):
+        check_row(t, i, ref[r], got[r], lg[r], bar=LITERAL)
+    print(t)
+
+
 def test_prefill_all_matches_per_sequence_prefill(shape, weights_gpu):
     """Three prompts of different lengths in one forward (tokens of three sequences interleaved in
     one batch, each attending only to its own cache) against one prefill per sequence: the same
