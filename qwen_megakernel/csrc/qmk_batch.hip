@@ -13,11 +13,13 @@
 // and decodes one sequence; the batched forward is an addition.
 //
 // Per layer (kernels in launch order):
-//   gemm_partial(qkv)  -> qkv_finish (split-K sum, q/k RMSNorm + RoPE, K/V append)
+//   gemm_partial(qkv)  -> qkv_finish (split-K sum, q/k RMSNorm + RoPE, K/V append;
+//                         in the GEMM's epilogue when K is not split)
 //   attention          (one kernel per (token, KV head) for many tokens; a
 //                       context-split pair + merge for few tokens)
 //   gemm_partial(o)    -> residual_norm (residual add, post-attention RMSNorm)
-//   gemm_partial(g|u)  -> gate_up_finish (SiLU(g) * u)
+//   gemm_partial(g|u)  -> gate_up_finish (SiLU(g) * u; in the GEMM's epilogue when K
+//                         is not split)
 //   gemm_partial(down) -> residual_norm (residual add, next layer's input RMSNorm
 //                                        or the final norm)
 // then lm_head_gemm over the emitted rows (bf16 logits, per-tile argmax keys)
@@ -218,6 +220,70 @@ __global__ void __launch_bounds__(256) gemm_partial(const uint16_t* __restrict__
   }
 }
 
+// The work after the q/k/v projection for one (token, head) of the 32 q/k/v heads, one wave,
+// lane l holding the head's bf16-rounded projections x0 = column l, x1 = column l + 64: q:
+// RMSNorm over head_dim + RoPE -> Q;  k: the same -> K cache at the token's position;  v: -> V
+// cache.  (modeling_qwen3.py:252-253, 168)
+struct QkvOut {
+  const Tok* tok;
+  int L;
+  const uint16_t* q_norm;
+  const uint16_t* k_norm;
+  const uint16_t* cos_t;
+  const uint16_t* sin_t;
+  Cache c;
+  float eps;
+  uint16_t* Q;
+};
+
+__device__ __forceinline__ void qkv_head(const QkvOut& o, int t, int h, int lane, float x0, float x1) {
+  const Tok tk = o.tok[t];
+  if (h >= kNQ + kNKV) {
+    if (tk.valid) {
+      uint16_t* dst = o.c.v + cache_base(o.c, tk, o.L, h - kNQ - kNKV) + (size_t)tk.pos * kD;
+      dst[lane] = (uint16_t)f32_to_bf16(x0);
+      dst[lane + 64] = (uint16_t)f32_to_bf16(x1);
+    }
+    return;
+  }
+  const bool is_q = h < kNQ;
+  if (!is_q && !tk.valid) return;
+  const uint16_t* nw = is_q ? o.q_norm : o.k_norm;
+  const uint16_t* cr = o.cos_t + (size_t)tk.pos * kD;
+  const uint16_t* sr = o.sin_t + (size_t)tk.pos * kD;
+  const float ss = wave_sum(x0 * x0 + x1 * x1);
+  const float rstd = rcp_sqrt_torch(__fdiv_rn(ss, (float)kD) + o.eps);
+  const float n0 = bf16r(bf16_to_f32(ldu16(nw + lane)) * bf16r(x0 * rstd));
+  const float n1 = bf16r(bf16_to_f32(ldu16(nw + lane + 64)) * bf16r(x1 * rstd));
+  const float c0 = bf16_to_f32(ldu16(cr + lane)), c1 = bf16_to_f32(ldu16(cr + lane + 64));
+  const float s0 = bf16_to_f32(ldu16(sr + lane)), s1 = bf16_to_f32(ldu16(sr + lane + 64));
+  // x*cos + rotate_half(x)*sin, rotate_half(x) = (-x[64:], x[:64])
+  const float y0 = bf16r(bf16r(n0 * c0) + bf16r(-n1 * s0));
+  const float y1 = bf16r(bf16r(n1 * c1) + bf16r(n0 * s1));
+  uint16_t* dst =
+      is_q ? o.Q + (size_t)t * kQS + h * kD : o.c.k + cache_base(o.c, tk, o.L, h - kNQ) + (size_t)tk.pos * kD;
+  dst[lane] = (uint16_t)f32_to_bf16(y0);
+  dst[lane + 64] = (uint16_t)f32_to_bf16(y1);
+}
+
+// SiLU(g) * u as HF rounds it: bf16(bf16(silu(g)) * u), g and u bf16 (modeling_qwen3.py:82)
+__device__ __forceinline__ float silu_mul(float g, float u) {
+  const float sg = bf16r(__fdiv_rn(g, 1.0f + expf(-g)));
+  return bf16r(sg * u);
+}
+
+// What gemm_tiled does with its sums: kEpiPart writes them to part (any K split); with the K
+// range unsplit, kEpiQkv (128-column tiles = one q/k/v head each) runs the head's norm, RoPE and
+// K/V append (qkv_head) and kEpiGateUp (tile columns 0..63 the gate rows m0..m0+63, 64..127
+// the up rows of the same m) writes bf16(bf16(silu(g)) * u) to M, so neither the fp32 sums nor
+// a finishing kernel touch memory.
+enum { kEpiPart = 0, kEpiQkv = 1, kEpiGateUp = 2 };
+
+struct GateUpOut {
+  uint16_t* M;
+  int I;
+};
+
 // Large T (prompt prefill): an LDS-tiled MFMA GEMM, part[z][t][n] = the sum
 // over K split z of X[t][k] W[n][k].  Workgroup tile 128 rows x TN columns
 // (TN = 128, or 64 for narrow N so that more workgroups run), BK = 64; wave w
@@ -228,10 +294,11 @@ __global__ void __launch_bounds__(256) gemm_partial(const uint16_t* __restrict__
 // spread over the LDS banks.
 constexpr int kTM = 128, kTK = 64, kTPad = kTK + 8;
 
-template <int TN>
+template <int TN, int EPI = kEpiPart>
 __global__ void __launch_bounds__(256) gemm_tiled(const uint16_t* __restrict__ X, int T, int K, Seg seg, int N,
-                                                  int ksplit, float* __restrict__ part) {
+                                                  int ksplit, float* __restrict__ part, QkvOut qo, GateUpOut go) {
   static_assert(TN == 64 || TN == 128, "tile width");
+  static_assert(EPI == kEpiPart || TN == 128, "fused epilogues take 128-column tiles");
   constexpr int BQ = TN / 32;  // 16-byte B chunks per thread per step (TN rows x 8 chunks over 256 threads)
   constexpr int WJ = TN / 32;  // 16-column MFMA tiles per wave (a wave covers TN / 2 columns)
   __shared__ __align__(16) uint16_t As[2][kTM][kTPad];
@@ -258,7 +325,10 @@ __global__ void __launch_bounds__(256) gemm_tiled(const uint16_t* __restrict__ X
     const int c = threadIdx.x + 256 * i;
     brow[i] = c >> 3;
     bcol[i] = (c & 7) * 8;
-    bsrc[i] = seg_row(seg, n0 + brow[i], K) + kz + bcol[i];
+    if constexpr (EPI == kEpiGateUp)  // tile columns 0..63: gate rows m0.., 64..127: up rows m0..
+      bsrc[i] = seg.w[brow[i] >> 6] + (size_t)(n0 / 2 + (brow[i] & 63)) * K + kz + bcol[i];
+    else
+      bsrc[i] = seg_row(seg, n0 + brow[i], K) + kz + bcol[i];
   }
   u32x4 ra[4], rb[BQ];
   auto gload = [&](int k) {
@@ -304,17 +374,67 @@ __global__ void __launch_bounds__(256) gemm_tiled(const uint16_t* __restrict__ X
       __syncthreads();
     }
   }
+  if constexpr (EPI == kEpiPart) {
 #pragma unroll
-  for (int i = 0; i < 4; i++)
+    for (int i = 0; i < 4; i++)
 #pragma unroll
-    for (int j = 0; j < WJ; j++) {
-      const int n = n0 + (TN / 2) * wn + 16 * j + l16;
+      for (int j = 0; j < WJ; j++) {
+        const int n = n0 + (TN / 2) * wn + 16 * j + l16;
 #pragma unroll
-      for (int r = 0; r < 4; r++) {
-        const int t = t0 + 64 * wm + 16 * i + 4 * (lane >> 4) + r;
-        if (t < T) part[(size_t)t * N + n] = acc[i][j][r];
+        for (int r = 0; r < 4; r++) {
+          const int t = t0 + 64 * wm + 16 * i + 4 * (lane >> 4) + r;
+          if (t < T) part[(size_t)t * N + n] = acc[i][j][r];
+        }
       }
+  } else if constexpr (EPI == kEpiQkv) {
+    // the tile's 128 rows x 128 columns (one head), bf16-rounded, through LDS: then wave w takes
+    // rows 32w..32w+31 one at a time, lane l columns l and l + 64
+    static_assert(sizeof(As) >= kTM * 128 * 2, "the head tile fits the A operand buffers");
+    auto Xh = reinterpret_cast<uint16_t(*)[128]>(&As[0][0][0]);
+    __syncthreads();  // every wave's last operand reads are done
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+      for (int j = 0; j < WJ; j++)
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+          Xh[64 * wm + 16 * i + 4 * (lane >> 4) + r][64 * wn + 16 * j + l16] = (uint16_t)f32_to_bf16(acc[i][j][r]);
+    __syncthreads();
+    const int h = blockIdx.x;
+    for (int rr = 0; rr < 32; rr++) {
+      const int row = 32 * w + rr, t = t0 + row;
+      if (t >= T) break;
+      qkv_head(qo, t, h, lane, bf16_to_f32(Xh[row][lane]), bf16_to_f32(Xh[row][lane + 64]));
     }
+  } else {
+    // the up waves (wn = 1) hand their sums to the gate waves (wn = 0) of the same rows through LDS
+    static_assert(sizeof(As) >= kTM * 64 * 4, "the up sums fit the A operand buffers");
+    auto U = reinterpret_cast<float(*)[64]>(&As[0][0][0]);
+    __syncthreads();  // every wave's last operand reads are done
+    if (wn == 1) {
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < WJ; j++)
+#pragma unroll
+          for (int r = 0; r < 4; r++) U[64 * wm + 16 * i + 4 * (lane >> 4) + r][16 * j + l16] = acc[i][j][r];
+    }
+    __syncthreads();
+    if (wn == 0) {
+      const int m0 = n0 / 2;
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < WJ; j++)
+#pragma unroll
+          for (int r = 0; r < 4; r++) {
+            const int row = 64 * wm + 16 * i + 4 * (lane >> 4) + r, t = t0 + row;
+            if (t < T)
+              go.M[(size_t)t * go.I + m0 + 16 * j + l16] =
+                  (uint16_t)f32_to_bf16(silu_mul(bf16r(acc[i][j][r]), bf16r(U[row][16 * j + l16])));
+          }
+    }
+  }
 }
 
 // Sum of the K-split partials of element (t, n), in split order.  All loads
@@ -375,40 +495,11 @@ __global__ void __launch_bounds__(1024) residual_norm(const float* __restrict__ 
 // and rounds (the bf16 projections), then q: RMSNorm over head_dim + RoPE ->
 // Q;  k: the same -> K cache at the token's position;  v: -> V cache.
 // (modeling_qwen3.py:252-253, 168)
-__global__ void __launch_bounds__(64) qkv_finish(const float* __restrict__ part, int ksplit, int T,
-                                                 const Tok* __restrict__ tok, int L, const uint16_t* q_norm,
-                                                 const uint16_t* k_norm, const uint16_t* cos_t,
-                                                 const uint16_t* sin_t, Cache c, float eps,
-                                                 uint16_t* __restrict__ Q) {
+__global__ void __launch_bounds__(64) qkv_finish(const float* __restrict__ part, int ksplit, int T, QkvOut o) {
   const int t = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
-  const Tok tk = tok[t];
   const float x0 = bf16r(sum_splits(part, ksplit, T, kNQKV, t, h * kD + lane));
   const float x1 = bf16r(sum_splits(part, ksplit, T, kNQKV, t, h * kD + lane + 64));
-  if (h >= kNQ + kNKV) {
-    if (tk.valid) {
-      uint16_t* dst = c.v + cache_base(c, tk, L, h - kNQ - kNKV) + (size_t)tk.pos * kD;
-      dst[lane] = (uint16_t)f32_to_bf16(x0);
-      dst[lane + 64] = (uint16_t)f32_to_bf16(x1);
-    }
-    return;
-  }
-  const bool is_q = h < kNQ;
-  if (!is_q && !tk.valid) return;
-  const uint16_t* nw = is_q ? q_norm : k_norm;
-  const uint16_t* cr = cos_t + (size_t)tk.pos * kD;
-  const uint16_t* sr = sin_t + (size_t)tk.pos * kD;
-  const float ss = wave_sum(x0 * x0 + x1 * x1);
-  const float rstd = rcp_sqrt_torch(__fdiv_rn(ss, (float)kD) + eps);
-  const float n0 = bf16r(bf16_to_f32(ldu16(nw + lane)) * bf16r(x0 * rstd));
-  const float n1 = bf16r(bf16_to_f32(ldu16(nw + lane + 64)) * bf16r(x1 * rstd));
-  const float c0 = bf16_to_f32(ldu16(cr + lane)), c1 = bf16_to_f32(ldu16(cr + lane + 64));
-  const float s0 = bf16_to_f32(ldu16(sr + lane)), s1 = bf16_to_f32(ldu16(sr + lane + 64));
-  // x*cos + rotate_half(x)*sin, rotate_half(x) = (-x[64:], x[:64])
-  const float y0 = bf16r(bf16r(n0 * c0) + bf16r(-n1 * s0));
-  const float y1 = bf16r(bf16r(n1 * c1) + bf16r(n0 * s1));
-  uint16_t* dst = is_q ? Q + (size_t)t * kQS + h * kD : c.k + cache_base(c, tk, L, h - kNQ) + (size_t)tk.pos * kD;
-  dst[lane] = (uint16_t)f32_to_bf16(y0);
-  dst[lane + 64] = (uint16_t)f32_to_bf16(y1);
+  qkv_head(o, t, h, lane, x0, x1);
 }
 
 // M[t][n] = bf16(bf16(silu(g)) * u); g and u are columns n and I + n of the
@@ -420,8 +511,7 @@ __global__ void __launch_bounds__(256) gate_up_finish(const float* __restrict__ 
   const int t = (int)(i / I), n = (int)(i % I);
   const float g = bf16r(sum_splits(part, ksplit, T, 2 * I, t, n));
   const float u = bf16r(sum_splits(part, ksplit, T, 2 * I, t, I + n));
-  const float sg = bf16r(__fdiv_rn(g, 1.0f + expf(-g)));
-  M[i] = (uint16_t)f32_to_bf16(bf16r(sg * u));
+  M[i] = (uint16_t)f32_to_bf16(silu_mul(g, u));
 }
 
 // ---------------------------------------------------------------- attention
@@ -1541,15 +1631,30 @@ Gemm plan_gemm(int T, int N, int K) {
   return {nb, ks, 0};
 }
 
+// The q/k/v and gate/up GEMMs with their finishing work in the epilogue (kEpiQkv, kEpiGateUp)
+// when the LDS-tiled plan can leave K unsplit: 128-column tiles filling at least one workgroup
+// per CU.  Then no fp32 sums go to memory and no finishing kernel runs; *ks_out = 0 says so.
+// Otherwise the sums go to part and *ks_out is the split count for the finishing kernel.
 void launch_gemm(const uint16_t* X, const int* rows, int T, int K, const Seg& seg, int N, float* part, hipStream_t s,
-                 int* ks_out) {
+                 int* ks_out, int epi = kEpiPart, const QkvOut* qo = nullptr, const GateUpOut* go = nullptr) {
+  const QkvOut q0 = qo ? *qo : QkvOut{};
+  const GateUpOut g0 = go ? *go : GateUpOut{};
+  if (epi != kEpiPart && !rows && use_tiled(T, N, K) && (long long)((T + kTM - 1) / kTM) * (N / 128) >= kNumWG) {
+    const dim3 grid(N / 128, (T + kTM - 1) / kTM, 1);
+    if (epi == kEpiQkv)
+      hipLaunchKernelGGL((gemm_tiled<128, kEpiQkv>), grid, dim3(256), 0, s, X, T, K, seg, N, 1, part, q0, g0);
+    else
+      hipLaunchKernelGGL((gemm_tiled<128, kEpiGateUp>), grid, dim3(256), 0, s, X, T, K, seg, N, 1, part, q0, g0);
+    *ks_out = 0;
+    return;
+  }
   const Gemm g = plan_gemm(T, N, K);
   if (g.nb == 0) {  // LDS-tiled
     const dim3 grid(N / g.tn, (T + kTM - 1) / kTM, g.ksplit);
     if (g.tn == 128)
-      hipLaunchKernelGGL(gemm_tiled<128>, grid, dim3(256), 0, s, X, T, K, seg, N, g.ksplit, part);
+      hipLaunchKernelGGL((gemm_tiled<128, kEpiPart>), grid, dim3(256), 0, s, X, T, K, seg, N, g.ksplit, part, q0, g0);
     else
-      hipLaunchKernelGGL(gemm_tiled<64>, grid, dim3(256), 0, s, X, T, K, seg, N, g.ksplit, part);
+      hipLaunchKernelGGL((gemm_tiled<64, kEpiPart>), grid, dim3(256), 0, s, X, T, K, seg, N, g.ksplit, part, q0, g0);
     *ks_out = g.ksplit;
     return;
   }
@@ -1774,9 +1879,9 @@ int forward(const Args& a, hipStream_t s) {
   for (int L = 0; L < a.num_layers; L++) {
     const LDGLayerWeights& w = a.layers[L];
     const Seg qkv{{u16(w.q_proj_weight), u16(w.k_proj_weight), u16(w.v_proj_weight)}, {kQS, kNKV * kD, kNKV * kD}};
-    launch_gemm(N, nullptr, T, Dm::H, qkv, kNQKV, part, s, &ks);
-    hipLaunchKernelGGL(qkv_finish, dim3(T, kNQ + 2 * kNKV), dim3(64), 0, s, part, ks, T, tok, L, u16(w.q_norm_weight),
-                       u16(w.k_norm_weight), a.cos_t, a.sin_t, a.cache, eps, Qb);
+    const QkvOut qo{tok, L, u16(w.q_norm_weight), u16(w.k_norm_weight), a.cos_t, a.sin_t, a.cache, eps, Qb};
+    launch_gemm(N, nullptr, T, Dm::H, qkv, kNQKV, part, s, &ks, kEpiQkv, &qo);
+    if (ks) hipLaunchKernelGGL(qkv_finish, dim3(T, kNQ + 2 * kNKV), dim3(64), 0, s, part, ks, T, qo);
     if (split) {
       float* scores = reinterpret_cast<float*>(a.ws + l.scores);
       float2* ml = reinterpret_cast<float2*>(a.ws + l.ml);
@@ -1804,8 +1909,9 @@ int forward(const Args& a, hipStream_t s) {
     hipLaunchKernelGGL((residual_norm<Dm::H>), dim3(T), dim3(1024), 0, s, part, ks, T, X,
                        u16(w.post_attn_layernorm_weight), eps, N);
     const Seg gu{{u16(w.gate_proj_weight), u16(w.up_proj_weight), nullptr}, {Dm::I, Dm::I, 0}};
-    launch_gemm(N, nullptr, T, Dm::H, gu, 2 * Dm::I, part, s, &ks);
-    hipLaunchKernelGGL(gate_up_finish, blocks((size_t)T * Dm::I), dim3(256), 0, s, part, ks, T, Dm::I, MM);
+    const GateUpOut go{MM, Dm::I};
+    launch_gemm(N, nullptr, T, Dm::H, gu, 2 * Dm::I, part, s, &ks, kEpiGateUp, nullptr, &go);
+    if (ks) hipLaunchKernelGGL(gate_up_finish, blocks((size_t)T * Dm::I), dim3(256), 0, s, part, ks, T, Dm::I, MM);
     const Seg dn{{u16(w.down_proj_weight), nullptr, nullptr}, {Dm::H, 0, 0}};
     launch_gemm(MM, nullptr, T, Dm::I, dn, Dm::H, part, s, &ks);
     const uint16_t* next_norm = L + 1 < a.num_layers ? u16(a.layers[L + 1].input_layernorm_weight) : a.final_norm;
