@@ -42,7 +42,8 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 constexpr int kD = 128, kNQ = 16, kNKV = 8, kQS = kNQ * kD, kNQKV = (kNQ + 2 * kNKV) * kD;
 constexpr int kAttnChunk = 2048;  // one-kernel attention: scores of this many positions per LDS pass
 constexpr int kQT = 64, kKB = 64, kKPad = kD + 8, kVPad = kKB + 8;  // MFMA prefill attention tiles
-constexpr int kMfmaAttnFrom = 1024;  // tokens or context positions from which attention_mfma runs
+constexpr int kMfmaAttnTokens = 320;   // prompts of this many tokens run attention_mfma
+constexpr int kMfmaAttnContext = 1024; // so do fewer tokens over this many positions of context
 constexpr int kSplitChunk = 64;   // split attention: positions per workgroup
 constexpr int kSplitBelow = 32;   // fewer tokens than this use the split attention
 constexpr int kTargetWaves = 2048;
@@ -266,6 +267,72 @@ __device__ __forceinline__ void qkv_head(const QkvOut& o, int t, int h, int lane
   dst[lane + 64] = (uint16_t)f32_to_bf16(y1);
 }
 
+// qkv_head for the 128 rows x 128 columns of one head held in LDS (bf16), rows t0.. (those
+// below T): wave w takes rows 32w..32w+31, four at a time, 16 lanes per row; lane c of a row
+// holds columns 4c..4c+3 and their RoPE partners 64+4c..64+4c+3.  The head-norm weights are
+// loaded once; the sum of squares runs over the row's 16 lanes.
+__device__ __forceinline__ void qkv_tile_rows(const QkvOut& o, const uint16_t (*Xh)[128], int t0, int T, int h, int w,
+                                              int lane) {
+  const int c = lane & 15, sub = lane >> 4;
+  const bool is_v = h >= kNQ + kNKV, is_q = h < kNQ;
+  float nw[8];
+  if (!is_v) {
+    const uint16_t* wp = is_q ? o.q_norm : o.k_norm;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      nw[e] = bf16_to_f32(ldu16(wp + 4 * c + e));
+      nw[4 + e] = bf16_to_f32(ldu16(wp + 64 + 4 * c + e));
+    }
+  }
+  for (int it = 0; it < 8; it++) {
+    const int row = 32 * w + 4 * it + sub, t = t0 + row;
+    if (t0 + 32 * w + 4 * it >= T) break;  // uniform: no row of this group is below T
+    const bool live = t < T;
+    const Tok tk = o.tok[live ? t : t0];
+    const uint2 lo = *reinterpret_cast<const uint2*>(&Xh[row][4 * c]);
+    const uint2 hi = *reinterpret_cast<const uint2*>(&Xh[row][64 + 4 * c]);
+    float x[8] = {lo_bf16(lo.x), hi_bf16(lo.x), lo_bf16(lo.y), hi_bf16(lo.y),
+                  lo_bf16(hi.x), hi_bf16(hi.x), lo_bf16(hi.y), hi_bf16(hi.y)};
+    if (is_v) {
+      if (live && tk.valid) {
+        uint16_t* dst = o.c.v + cache_base(o.c, tk, o.L, h - kNQ - kNKV) + (size_t)tk.pos * kD;
+        *reinterpret_cast<uint2*>(dst + 4 * c) = lo;
+        *reinterpret_cast<uint2*>(dst + 64 + 4 * c) = hi;
+      }
+      continue;
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; e++) ss += x[e] * x[e];
+#pragma unroll
+    for (int m = 1; m < 16; m <<= 1) ss += __shfl_xor(ss, m);  // within the row's 16 lanes
+    const float rstd = rcp_sqrt_torch(__fdiv_rn(ss, (float)kD) + o.eps);
+    float n[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) n[e] = bf16r(nw[e] * bf16r(x[e] * rstd));
+    const uint2 cl = *reinterpret_cast<const uint2*>(o.cos_t + (size_t)tk.pos * kD + 4 * c);
+    const uint2 ch = *reinterpret_cast<const uint2*>(o.cos_t + (size_t)tk.pos * kD + 64 + 4 * c);
+    const uint2 sl = *reinterpret_cast<const uint2*>(o.sin_t + (size_t)tk.pos * kD + 4 * c);
+    const uint2 sh = *reinterpret_cast<const uint2*>(o.sin_t + (size_t)tk.pos * kD + 64 + 4 * c);
+    const float cs[8] = {lo_bf16(cl.x), hi_bf16(cl.x), lo_bf16(cl.y), hi_bf16(cl.y),
+                         lo_bf16(ch.x), hi_bf16(ch.x), lo_bf16(ch.y), hi_bf16(ch.y)};
+    const float sn[8] = {lo_bf16(sl.x), hi_bf16(sl.x), lo_bf16(sl.y), hi_bf16(sl.y),
+                         lo_bf16(sh.x), hi_bf16(sh.x), lo_bf16(sh.y), hi_bf16(sh.y)};
+    // x*cos + rotate_half(x)*sin, rotate_half(x) = (-x[64:], x[:64])
+    float y[8];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      y[e] = bf16r(bf16r(n[e] * cs[e]) + bf16r(-n[4 + e] * sn[e]));
+      y[4 + e] = bf16r(bf16r(n[4 + e] * cs[4 + e]) + bf16r(n[e] * sn[4 + e]));
+    }
+    if (!live || (!is_q && !tk.valid)) continue;
+    uint16_t* dst =
+        is_q ? o.Q + (size_t)t * kQS + h * kD : o.c.k + cache_base(o.c, tk, o.L, h - kNQ) + (size_t)tk.pos * kD;
+    *reinterpret_cast<uint2*>(dst + 4 * c) = make_uint2(pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3]));
+    *reinterpret_cast<uint2*>(dst + 64 + 4 * c) = make_uint2(pack_bf16x2(y[4], y[5]), pack_bf16x2(y[6], y[7]));
+  }
+}
+
 // SiLU(g) * u as HF rounds it: bf16(bf16(silu(g)) * u), g and u bf16 (modeling_qwen3.py:82)
 __device__ __forceinline__ float silu_mul(float g, float u) {
   const float sg = bf16r(__fdiv_rn(g, 1.0f + expf(-g)));
@@ -400,39 +467,38 @@ __global__ void __launch_bounds__(256) gemm_tiled(const uint16_t* __restrict__ X
         for (int r = 0; r < 4; r++)
           Xh[64 * wm + 16 * i + 4 * (lane >> 4) + r][64 * wn + 16 * j + l16] = (uint16_t)f32_to_bf16(acc[i][j][r]);
     __syncthreads();
-    const int h = blockIdx.x;
-    for (int rr = 0; rr < 32; rr++) {
-      const int row = 32 * w + rr, t = t0 + row;
-      if (t >= T) break;
-      qkv_head(qo, t, h, lane, bf16_to_f32(Xh[row][lane]), bf16_to_f32(Xh[row][lane + 64]));
-    }
+    qkv_tile_rows(qo, Xh, t0, T, blockIdx.x, w, lane);
   } else {
-    // the up waves (wn = 1) hand their sums to the gate waves (wn = 0) of the same rows through LDS
-    static_assert(sizeof(As) >= kTM * 64 * 4, "the up sums fit the A operand buffers");
-    auto U = reinterpret_cast<float(*)[64]>(&As[0][0][0]);
+    // the tile's gate and up projections, bf16-rounded, through LDS: G[row][c], U[row][c] for
+    // m = m0 + c; then each thread takes 8 consecutive m of one row at a time and stores them
+    // as one 16-byte chunk
+    static_assert(sizeof(As) >= 2 * kTM * 64 * 2, "the gate and up tiles fit the A operand buffers");
+    auto G = reinterpret_cast<uint16_t(*)[64]>(&As[0][0][0]);
+    auto U = G + kTM;
     __syncthreads();  // every wave's last operand reads are done
-    if (wn == 1) {
+    auto GU = wn == 0 ? G : U;
 #pragma unroll
-      for (int i = 0; i < 4; i++)
+    for (int i = 0; i < 4; i++)
 #pragma unroll
-        for (int j = 0; j < WJ; j++)
+      for (int j = 0; j < WJ; j++)
 #pragma unroll
-          for (int r = 0; r < 4; r++) U[64 * wm + 16 * i + 4 * (lane >> 4) + r][16 * j + l16] = acc[i][j][r];
-    }
+        for (int r = 0; r < 4; r++)
+          GU[64 * wm + 16 * i + 4 * (lane >> 4) + r][16 * j + l16] = (uint16_t)f32_to_bf16(acc[i][j][r]);
     __syncthreads();
-    if (wn == 0) {
-      const int m0 = n0 / 2;
+    const int m0 = n0 / 2, row = threadIdx.x >> 1, t = t0 + row;
+    if (t < T) {
 #pragma unroll
-      for (int i = 0; i < 4; i++)
+      for (int q = 0; q < 4; q++) {
+        const int c0 = 32 * (threadIdx.x & 1) + 8 * q;
+        const u32x4 g8 = *reinterpret_cast<const u32x4*>(&G[row][c0]);
+        const u32x4 u8 = *reinterpret_cast<const u32x4*>(&U[row][c0]);
+        const uint32_t gw[4] = {g8.x, g8.y, g8.z, g8.w}, uw[4] = {u8.x, u8.y, u8.z, u8.w};
+        uint32_t mw[4];
 #pragma unroll
-        for (int j = 0; j < WJ; j++)
-#pragma unroll
-          for (int r = 0; r < 4; r++) {
-            const int row = 64 * wm + 16 * i + 4 * (lane >> 4) + r, t = t0 + row;
-            if (t < T)
-              go.M[(size_t)t * go.I + m0 + 16 * j + l16] =
-                  (uint16_t)f32_to_bf16(silu_mul(bf16r(acc[i][j][r]), bf16r(U[row][16 * j + l16])));
-          }
+        for (int e = 0; e < 4; e++)
+          mw[e] = pack_bf16x2(silu_mul(lo_bf16(gw[e]), lo_bf16(uw[e])), silu_mul(hi_bf16(gw[e]), hi_bf16(uw[e])));
+        *reinterpret_cast<u32x4*>(go.M + (size_t)t * go.I + m0 + c0) = u32x4{mw[0], mw[1], mw[2], mw[3]};
+      }
     }
   }
 }
@@ -1864,9 +1930,11 @@ int forward(const Args& a, hipStream_t s) {
   const float eps = 1e-6f;
   const bool split = T < kSplitBelow;
   const int nch = split ? split_chunks(a.max_context) : 0;
-  // attention_mfma pays off from about 1024 tokens or 1024 positions of context
-  // (below that the row kernel's per-token reads are cheaper than its passes)
-  const bool mfma_attn = !split && (T >= kMfmaAttnFrom || a.max_context >= kMfmaAttnFrom);
+  // attention_mfma pays off from about 320 tokens or 1024 positions of context (below that the
+  // row kernel's per-token reads are cheaper than its passes).  Measured 0.6B prefills, row
+  // kernel against attention_mfma: 256 tokens 2.55 / 2.62 ms, 384 tokens 3.37 / 3.18, 512 tokens
+  // 4.23 / 3.67, 768 tokens 5.85 / 4.45.
+  const bool mfma_attn = !split && (T >= kMfmaAttnTokens || a.max_context >= kMfmaAttnContext);
   auto blocks = [](size_t n) { return dim3((unsigned)((n + 255) / 256)); };
   auto u16 = [](const void* p) { return static_cast<const uint16_t*>(p); };
   int ks = 1;

@@ -452,12 +452,14 @@ def test_decode_batch_equals_general_forward(weights_gpu):
     assert cos >= 0.999, cos
 
 
-@pytest.mark.parametrize("n", [128, 200, 300], ids=["128tok-64col-tiles", "200tok-128col-tiles", "300tok-mixed-tiles"])
+@pytest.mark.parametrize("n", [128, 200, 300, 450],
+                         ids=["128tok-64col-tiles", "200tok-128col-tiles", "300tok-mixed-tiles", "450tok-mfma-attention"])
 def test_long_prefill_tiled_gemm(shape, exact06, weights_gpu, n):
     """Prefills of 96+ tokens take the LDS-tiled MFMA GEMM: every 25th row and the last against
     the oracle, 2 layers, and a second identical forward bit-exact.  128 tokens: 64-column tiles
     for all four projections, o and down split 16 ways over K; 200 tokens: 128-column tiles with
-    a partial last row tile; 300 tokens: 128-column tiles and 64-column tiles for down."""
+    a partial last row tile; 300 tokens: 128-column tiles and 64-column tiles for down; 450 tokens:
+    the MFMA attention (8 tiles in 4 pairs, a partial last tile)."""
     from qwen_megakernel.weights import make_prompt
 
     layers = 2
