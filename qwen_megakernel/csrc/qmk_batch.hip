@@ -753,7 +753,9 @@ __global__ void __launch_bounds__(kAttnWaves * 64) attention_mfma(const uint16_t
   __shared__ float s_ml[4][2][16][2];  // (max, sum) per row group, key half and row
   const int nt = (T + kQT - 1) / kQT;
   const int h = blockIdx.y, g = h >> 1;
-  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, l16 = lane & 15, lg = lane >> 4;
+  // the wave index made uniform, so that branches on the wave's rows and keys are scalar
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63, l16 = lane & 15,
+            lg = lane >> 4;
   const int rg = w >> 1, kh = w & 1;  // rows 16rg..16rg+15, keys 32kh..32kh+31 of each block
   const int tiles[2] = {(int)blockIdx.x, nt - 1 - (int)blockIdx.x};
   const int ntile = tiles[1] == tiles[0] ? 1 : 2;
@@ -833,6 +835,17 @@ __global__ void __launch_bounds__(kAttnWaves * 64) attention_mfma(const uint16_t
             *reinterpret_cast<const bf16x8*>(&Ks[32 * kh + 16 * n + l16][32 * kk + 8 * lg]), qb[kk], sc, 0, 0, 0);
       return sc;
     };
+    // the four scores bf16(bf16(q.k) * scale), two roundings per conversion; no branch per
+    // element (the callers mask by select), so the four chains interleave
+    auto scaled = [&](const f32x4& sc, float (&x)[4]) {
+      const uint32_t r01 = pack_bf16x2(sc[0], sc[1]), r23 = pack_bf16x2(sc[2], sc[3]);
+      const uint32_t s01 = pack_bf16x2(lo_bf16(r01) * scale, hi_bf16(r01) * scale);
+      const uint32_t s23 = pack_bf16x2(lo_bf16(r23) * scale, hi_bf16(r23) * scale);
+      x[0] = lo_bf16(s01);
+      x[1] = hi_bf16(s01);
+      x[2] = lo_bf16(s23);
+      x[3] = hi_bf16(s23);
+    };
     // ---- pass 1: per lane, online max and sum of exp over its positions (one exp per score,
     // one rescale per block)
     float m = -INFINITY, ls = 0.f;
@@ -849,23 +862,24 @@ __global__ void __launch_bounds__(kAttnWaves * 64) attention_mfma(const uint16_t
 #pragma unroll
       for (int n = 0; n < 2; n++) {
         const f32x4 sc = kbase + 16 * n <= wave_last ? tile_scores(n) : f32x4{0.f, 0.f, 0.f, 0.f};
+        scaled(sc, x[n]);
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-          const int p = kbase + 16 * n + 4 * lg + i;
-          x[n][i] = p <= rpos ? bf16r(bf16r(sc[i]) * scale) : -INFINITY;
+          x[n][i] = kbase + 16 * n + 4 * lg + i <= rpos ? x[n][i] : -INFINITY;
           mb = fmaxf(mb, x[n][i]);
         }
       }
+      // no branch: while every key so far is masked for this lane's row (mn = -inf) the terms are
+      // taken against 0, and exp_acc turns -inf into 0, so ls stays 0
       const float mn = fmaxf(m, mb);
-      if (mn != -INFINITY) {
-        float e = 0.f;
+      const float ref = mn == -INFINITY ? 0.f : mn;
+      float e = 0.f;
 #pragma unroll
-        for (int n = 0; n < 2; n++)
+      for (int n = 0; n < 2; n++)
 #pragma unroll
-          for (int i = 0; i < 4; i++) e += exp_acc(x[n][i] - mn);
-        ls = (m == -INFINITY ? 0.f : ls * exp_acc(m - mn)) + e;
-        m = mn;
-      }
+        for (int i = 0; i < 4; i++) e += exp_acc(x[n][i] - ref);
+      ls = ls * exp_acc(m - ref) + e;
+      m = mn;
     }
     // row l16's (max, sum): over the 4 lanes of equal l16, then the row group's two waves (the
     // even wave's pair first in every wave, so both waves hold the same M and 1/L)
@@ -913,14 +927,17 @@ __global__ void __launch_bounds__(kAttnWaves * 64) attention_mfma(const uint16_t
       for (int n = 0; n < 2; n++) {
         // a 16-key tile wholly past the wave's rows is masked for every row: no MFMA for it
         const f32x4 sc = kbase + 16 * n <= wave_last ? tile_scores(n) : f32x4{0.f, 0.f, 0.f, 0.f};
-        float pr[4];
+        float x[4], pr[4];
+        scaled(sc, x);
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-          const int p = kbase + 16 * n + 4 * lg + i;
-          pr[i] = p <= rpos ? bf16r(exp_acc(bf16r(bf16r(sc[i]) * scale) - gm) * ginv) : 0.f;
+          // the probability bf16(exp(s - M) / L) (rounded once, by the packing below); masked
+          // keys, whose terms may be anything, take 0
+          const float e = exp_acc(x[i] - gm) * ginv;
+          pr[i] = kbase + 16 * n + 4 * lg + i <= rpos ? e : 0.f;
         }
-        pw[2 * n] = f32_to_bf16(pr[0]) | (f32_to_bf16(pr[1]) << 16);
-        pw[2 * n + 1] = f32_to_bf16(pr[2]) | (f32_to_bf16(pr[3]) << 16);
+        pw[2 * n] = pack_bf16x2(pr[0], pr[1]);
+        pw[2 * n + 1] = pack_bf16x2(pr[2], pr[3]);
       }
       const bf16x8 pa = __builtin_bit_cast(bf16x8, u32x4{pw[0], pw[1], pw[2], pw[3]});
 #pragma unroll
