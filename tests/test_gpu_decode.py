@@ -119,8 +119,8 @@ def test_bench_workload_256_steps_with_logits(shape, exact06, weights_cpu, weigh
     ids=["1500-4layers", "1500-28layers", "2100-4layers", "2100-28layers", "8192-4layers", "8192-28layers",
          "12300-4layers", "32768-28layers"])
 def test_long_context_parity(shape, exact06, weights_cpu, weights_gpu, c0, layers, steps):
-    """Attention over an injected N(0,1) cache of c0 positions (split-K over the 32 workgroups of
-    an XCD; above 2048 positions the long-context kernel runs, each wave streaming several K/V
+    """Attention over an injected N(0,1) cache of c0 positions (split over the 32 workgroups of
+    an XCD, two passes; above 2048 positions the long-context kernel runs, each wave streaming several K/V
     batches through the LDS ring; at 2100 wave 0 has a second, partial batch; above 12288 the
     deep form, which starts both passes with the ring full; at 12300 the waves have 7 and 6
     batches).  Every step against the exact oracle on the step's own inputs, and the K/V rows the
