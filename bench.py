@@ -300,8 +300,9 @@ def qwen3_1p7b(steps: int = 256, prompt_len: int = 512, batch: int = 4, phase_tr
                              "one control wave per sequence and 8 compute waves, tagged-word exchanges, HF's "
                              "two-pass attention per sequence, LM head and argmax in the same launch)",
                      "multi_launch": {"tok_per_s": round(batch / tm, 2), "ms_per_step": round(tm * 1e3, 4),
-                                      "path": "6 launches per layer (K-split MFMA GEMMs, split-K attention over "
-                                              "all CUs and its merge), streamed LM head"}}
+                                      "path": "7 launches per layer (K-split MFMA GEMMs; HF's two-pass attention "
+                                              "split over all CUs: scores, probabilities times V, sum), streamed "
+                                              "LM head"}}
     if batch_trace is not None:
         out["batch4"]["phase_trace"] = batch_trace
     return out

@@ -1242,11 +1242,13 @@ __global__ void __launch_bounds__(256) keys_reduce(const unsigned long long* __r
 // ---------------------------------------------------------------- decode step, few sequences
 //
 // One token per sequence, at most 16 sequences (one MFMA row tile), contexts
-// up to kFusedCtx: six launches per layer instead of eleven.
+// up to kFusedCtx: seven launches per layer instead of eleven.
 //
 //   gemm_rows<NORM>(q,k,v)   input RMSNorm in the prologue, bf16 q|k|v out
-//   attention_split          q/k head norm + RoPE, K/V append, split-K attention
-//                            over all CUs; attention_merge combines the splits
+//   attention_split          q/k head norm + RoPE, K/V append, scores and each
+//                            position split's (max, sum) over all CUs;
+//                            attention_pv the probabilities (HF's rounding) times
+//                            V per split; attention_merge adds the splits
 //   gemm_rows(o)             epilogue: residual add into the hidden rows
 //   gemm_rows<NORM>(g|u)     post-attention RMSNorm in the prologue, SiLU(g)*u out
 //   gemm_rows(down)          epilogue: residual add
@@ -1427,49 +1429,46 @@ __global__ void __launch_bounds__(NW * 64) gemm_rows(const uint16_t* __restrict_
 // Decode-step attention, split over positions: S workgroups of kSplitWaves
 // waves per (sequence's token, KV head), S * T * 8 >= 256, so that every CU
 // streams K/V (one workgroup per (token, KV head) left 224 of 256 CUs idle at
-// four sequences).  Each workgroup:
-// - requests the token's q/k/v head values, norm weights and RoPE row, then
-//   every K and V row of its positions [pb, pe) at once (a CU returns loads in
-//   order, so the small loads come first);
-// - forms the q heads 2g, 2g+1 and k head g (head RMSNorm + RoPE, as HF), and
-//   split 0 appends the token's K/V at its position (the token's own K/V are
-//   used from LDS, so no workgroup reads that cache row);
-// - scores its positions as HF rounds them and accumulates exp(s - m) * v in
-//   fp32 against its running maximum m: a split-K softmax whose probabilities
-//   are not rounded to bf16, as in the reference kernel's attention
-//   (csrc/kernel.cu:498-571);
-// - writes its (m, l, acc) to the workspace; attention_merge (the next launch)
-//   rescales the S partials of each (token, KV head) to the global maximum in
-//   split order and writes the bf16 attention output.  (A merge by the last
-//   workgroup to arrive, behind device-scope release/acquire fences, measured
-//   1.77 ms per Qwen3-1.7B batch-4 step against 1.51 for the second launch.)
+// four sequences), in HF's two passes over three launches:
+// - attention_split requests the token's q/k/v head values, norm weights and
+//   RoPE row, then every K row of its positions [pb, pe) (a CU returns loads in
+//   order, so the small loads come first); forms the q heads 2g, 2g+1 and k head
+//   g (head RMSNorm + RoPE, as HF), and split 0 appends the token's K/V at its
+//   position (the token's own K is used from LDS, so no workgroup of this launch
+//   reads that cache row); scores its positions as HF rounds them, stores them
+//   (fp32) and writes the split's (max m, sum l of exp(s - m)) per head;
+// - attention_pv merges the S (m, l) pairs into the global (M, L) in split order
+//   (the same in every workgroup of the token), forms the probabilities
+//   bf16(exp(s - M) * (1 / L)) as HF rounds them, and multiplies them with the V
+//   rows of its positions: a partial P@V per split;
+// - attention_merge adds the S partials in split order and rounds to bf16.
 // Valid only when no other token of the launch writes this sequence's cache
 // (one token per sequence).
 constexpr int kSplitWaves = 4;    // waves per workgroup
-constexpr int kSplitRounds = 8;   // 16-position rounds of K and V rows in flight per wave
+constexpr int kSplitRounds = 8;   // 16-position rounds of K (or V) rows in flight per wave
 constexpr int kMaxAttnSplit = 32;
 
 struct AttnPart {
-  float acc[2][kD];  // unnormalised P@V of heads 2g, 2g+1 against m
-  float m[2], l[2];  // maximum score and sum of exp(s - m)
+  float acc[2][kD];  // P@V of heads 2g, 2g+1 over the split's positions (probabilities normalised)
+  float m[2], l[2];  // the split's maximum score and sum of exp(s - m)
 };
 
 // position splits per (token, KV head) for T tokens
 int attn_splits(int T) { return std::min(kMaxAttnSplit, std::max(1, 256 / (kNKV * T))); }
 
+// scores[(t * kNQ + head) * cap + p] of token t's positions p: written by attention_split, read
+// by attention_pv
 __global__ void __launch_bounds__(kSplitWaves * 64) attention_split(
     const uint16_t* __restrict__ QKV, const Tok* __restrict__ tok, int L, const uint16_t* q_norm,
     const uint16_t* k_norm, const uint16_t* cos_t, const uint16_t* sin_t, Cache c, float eps, float scale,
-    AttnPart* __restrict__ part, uint16_t* __restrict__ out) {
-  __shared__ uint16_t qs[2][kD], kn[kD], vn[kD];
+    AttnPart* __restrict__ part, float* __restrict__ scores, int cap, uint16_t* __restrict__ out) {
+  __shared__ uint16_t qs[2][kD], kn[kD];
   __shared__ float wm[kSplitWaves][2], wl[kSplitWaves][2];
-  __shared__ float wacc[kSplitWaves][2][kD];
   const int t = blockIdx.x, g = blockIdx.y, sp = blockIdx.z, S = gridDim.z;
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, slot = lane >> 4, t16 = lane & 15;
   const Tok tk = tok[t];
-  uint16_t* dst = out + (size_t)t * kQS + 2 * g * kD;
   if (!tk.valid) {
-    if (sp == 0 && threadIdx.x < 2 * kD) dst[threadIdx.x] = 0;
+    if (sp == 0 && threadIdx.x < 2 * kD) out[(size_t)t * kQS + 2 * g * kD + threadIdx.x] = 0;
     return;
   }
   const int pos = tk.pos, C = pos + 1;
@@ -1477,7 +1476,6 @@ __global__ void __launch_bounds__(kSplitWaves * 64) attention_split(
   const int pb = min(C, sp * chunk), pe = min(C, pb + chunk);
   const size_t base = cache_base(c, tk, L, g);
   const uint16_t* kc = c.k + base;
-  const uint16_t* vc = c.v + base;
   // waves 0, 1: q heads 2g, 2g+1; wave 2: k head g; wave 3: v head g
   const int h = w < 2 ? 2 * g + w : (w == 2 ? kNQ + g : kNQ + kNKV + g);
   const uint16_t* src = QKV + (size_t)t * kNQKV + h * kD;
@@ -1490,25 +1488,18 @@ __global__ void __launch_bounds__(kSplitWaves * 64) attention_split(
   const uint32_t s0b = ldu16(sr + lane), s1b = ldu16(sr + lane + 64);
   // lane (slot, t16) of wave w takes dims 8*t16..+7 of position p0 + 16r + 4w + slot in round r;
   // positions outside [pb, pe) and pos itself load row 0 (every cache has it) and are masked
-  u32x4 kx[kSplitRounds], vx[kSplitRounds];
+  u32x4 kx[kSplitRounds];
   auto issue = [&](int p0) {
 #pragma unroll
     for (int r = 0; r < kSplitRounds; r++) {
       const int p = p0 + 16 * r + 4 * w + slot;
       kx[r] = ld16(kc + (size_t)((p < pe && p != pos) ? p : 0) * kD + 8 * t16);
     }
-#pragma unroll
-    for (int r = 0; r < kSplitRounds; r++) {
-      const int p = p0 + 16 * r + 4 * w + slot;
-      vx[r] = ld16(vc + (size_t)((p < pe && p != pos) ? p : 0) * kD + 8 * t16);
-    }
   };
   issue(pb);
   {
     const float x0 = bf16_to_f32(x0b), x1 = bf16_to_f32(x1b);
     if (w == 3) {
-      vn[lane] = (uint16_t)x0b;
-      vn[lane + 64] = (uint16_t)x1b;
       if (sp == 0) {
         c.v[base + (size_t)pos * kD + lane] = (uint16_t)x0b;
         c.v[base + (size_t)pos * kD + lane + 64] = (uint16_t)x1b;
@@ -1539,12 +1530,8 @@ __global__ void __launch_bounds__(kSplitWaves * 64) attention_split(
 #pragma unroll
   for (int hh = 0; hh < 2; hh++) qv[hh] = *reinterpret_cast<const u32x4*>(&qs[hh][8 * t16]);
   const u32x4 k_now = *reinterpret_cast<const u32x4*>(&kn[8 * t16]);
-  const u32x4 v_now = *reinterpret_cast<const u32x4*>(&vn[8 * t16]);
-  float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.f, 0.f}, acc[2][8];
-#pragma unroll
-  for (int hh = 0; hh < 2; hh++)
-#pragma unroll
-    for (int i = 0; i < 8; i++) acc[hh][i] = 0.f;
+  float* const sc_out = scores + ((size_t)t * kNQ + 2 * g) * cap;
+  float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.f, 0.f};
   for (int p0 = pb; p0 < pe; p0 += 16 * kSplitRounds) {
     if (p0 != pb) issue(p0);  // positions beyond the first 16 * kSplitRounds of the split
     float sc[kSplitRounds][2], bm[2] = {-INFINITY, -INFINITY};
@@ -1557,6 +1544,7 @@ __global__ void __launch_bounds__(kSplitWaves * 64) attention_split(
         const float x = bf16r(bf16r(row16_sum(dot8(kr, qv[hh], 0.f))) * scale);
         sc[r][hh] = p < pe ? x : -INFINITY;
         bm[hh] = fmaxf(bm[hh], sc[r][hh]);
+        if (t16 == 0 && p < pe) sc_out[(size_t)hh * cap + p] = x;
       }
     }
 #pragma unroll
@@ -1566,71 +1554,128 @@ __global__ void __launch_bounds__(kSplitWaves * 64) attention_split(
       bm[hh] = fmaxf(a, b);
       swap32(bm[hh], a, b);
       bm[hh] = fmaxf(a, b);
-      // rescale the running terms to the new maximum
+      // rescale the running sum to the new maximum
       const float mn = fmaxf(m[hh], bm[hh]);
-      const float f = m[hh] == -INFINITY ? 0.f : exp_acc(m[hh] - mn);
-      l[hh] *= f;
-#pragma unroll
-      for (int i = 0; i < 8; i++) acc[hh][i] *= f;
+      l[hh] *= m[hh] == -INFINITY ? 0.f : exp_acc(m[hh] - mn);
       m[hh] = mn;
     }
 #pragma unroll
-    for (int r = 0; r < kSplitRounds; r++) {
-      const int p = p0 + 16 * r + 4 * w + slot;
-      const u32x4 vr = p == pos ? v_now : vx[r];
-      const float vf[8] = {lo_bf16(vr.x), hi_bf16(vr.x), lo_bf16(vr.y), hi_bf16(vr.y),
-                           lo_bf16(vr.z), hi_bf16(vr.z), lo_bf16(vr.w), hi_bf16(vr.w)};
+    for (int r = 0; r < kSplitRounds; r++)
 #pragma unroll
-      for (int hh = 0; hh < 2; hh++) {
-        const float e = sc[r][hh] == -INFINITY ? 0.f : exp_acc(sc[r][hh] - m[hh]);
-        l[hh] += e;
-        // a masked position (it loaded cache row 0, which the caller may not have written) leaves the
-        // sum untouched, so that a NaN there cannot enter it through 0 * NaN
-#pragma unroll
-        for (int i = 0; i < 8; i++) acc[hh][i] = p < pe ? __builtin_fmaf(e, vf[i], acc[hh][i]) : acc[hh][i];
-      }
-    }
+      for (int hh = 0; hh < 2; hh++) l[hh] += sc[r][hh] == -INFINITY ? 0.f : exp_acc(sc[r][hh] - m[hh]);
   }
-  // the wave's four rows summed; lanes 0..15 hold dims 8*t16..+7
+  // the wave's four rows summed (every lane of a row holds the same terms; lane 0 speaks for them)
 #pragma unroll
   for (int hh = 0; hh < 2; hh++) {
     l[hh] = rows_sum4(l[hh]);
-#pragma unroll
-    for (int i = 0; i < 8; i++) acc[hh][i] = rows_sum4(acc[hh][i]);
-    if (lane < 16) {
-#pragma unroll
-      for (int i = 0; i < 8; i++) wacc[w][hh][8 * t16 + i] = acc[hh][i];
-    }
     if (lane == 0) {
       wm[w][hh] = m[hh];
       wl[w][hh] = l[hh];
     }
   }
   __syncthreads();
-  // this workgroup's partial: the waves rescaled to its maximum, in wave order
+  // this workgroup's (max, sum): the waves rescaled to its maximum, in wave order
   AttnPart* pt = part + ((size_t)t * kNKV + g) * S;
-  {
-    const int hh = threadIdx.x >> 7, d = threadIdx.x & 127;  // 256 threads: both heads' dims
+  if (threadIdx.x < 2) {
+    const int hh = threadIdx.x;
     float mx = -INFINITY;
 #pragma unroll
     for (int q = 0; q < kSplitWaves; q++) mx = fmaxf(mx, wm[q][hh]);
-    float a = 0.f, ls = 0.f;
+    float ls = 0.f;
 #pragma unroll
-    for (int q = 0; q < kSplitWaves; q++) {
-      const float f = wm[q][hh] == -INFINITY ? 0.f : exp_acc(wm[q][hh] - mx);
-      a += f * wacc[q][hh][d];
-      ls += f * wl[q][hh];
-    }
-    pt[sp].acc[hh][d] = a;
-    if (d == 0) {
-      pt[sp].m[hh] = mx;
-      pt[sp].l[hh] = ls;
-    }
+    for (int q = 0; q < kSplitWaves; q++) ls += wm[q][hh] == -INFINITY ? 0.f : wl[q][hh] * exp_acc(wm[q][hh] - mx);
+    pt[sp].m[hh] = mx;
+    pt[sp].l[hh] = ls;
   }
 }
 
-// The attention output of (token t, KV head g) from its S partials: each rescaled to the global
-// maximum, in split order.  256 threads: thread i takes head 2g + i / 128, dim i % 128.
+// The second pass of a split: the global (max, sum) of (token t, KV head g) from its S splits' pairs
+// in split order, the probabilities bf16(exp(s - M) * (1 / L)) of the split's positions (HF rounds
+// them to bf16), and their product with V: AttnPart::acc of this split.
+__global__ void __launch_bounds__(kSplitWaves * 64) attention_pv(const Tok* __restrict__ tok, int L, Cache c,
+                                                                 AttnPart* __restrict__ part,
+                                                                 const float* __restrict__ scores, int cap) {
+  __shared__ float wacc[kSplitWaves][2][kD];
+  const int t = blockIdx.x, g = blockIdx.y, sp = blockIdx.z, S = gridDim.z;
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, slot = lane >> 4, t16 = lane & 15;
+  const Tok tk = tok[t];
+  if (!tk.valid) return;  // attention_split wrote the zeros
+  const int C = tk.pos + 1;
+  const int chunk = (C + S - 1) / S;
+  const int pb = min(C, sp * chunk), pe = min(C, pb + chunk);
+  const uint16_t* vc = c.v + cache_base(c, tk, L, g);
+  // lane (slot, t16) of wave w takes dims 8*t16..+7 of position p0 + 16r + 4w + slot in round r;
+  // positions outside [pb, pe) load row 0 and are masked
+  u32x4 vx[kSplitRounds];
+  auto issue = [&](int p0) {
+#pragma unroll
+    for (int r = 0; r < kSplitRounds; r++) {
+      const int p = p0 + 16 * r + 4 * w + slot;
+      vx[r] = ld16(vc + (size_t)(p < pe ? p : 0) * kD + 8 * t16);
+    }
+  };
+  issue(pb);
+  AttnPart* pt = part + ((size_t)t * kNKV + g) * S;
+  float M[2], inv[2];
+#pragma unroll
+  for (int hh = 0; hh < 2; hh++) {
+    float mx = -INFINITY;
+    for (int q = 0; q < S; q++) mx = fmaxf(mx, pt[q].m[hh]);
+    float ls = 0.f;
+    for (int q = 0; q < S; q++) {
+      const float mq = pt[q].m[hh];
+      ls += mq == -INFINITY ? 0.f : pt[q].l[hh] * exp_acc(mq - mx);
+    }
+    M[hh] = mx;
+    inv[hh] = __fdiv_rn(1.0f, ls);
+  }
+  const float* sc_in = scores + ((size_t)t * kNQ + 2 * g) * cap;
+  float acc[2][8];
+#pragma unroll
+  for (int hh = 0; hh < 2; hh++)
+#pragma unroll
+    for (int i = 0; i < 8; i++) acc[hh][i] = 0.f;
+  for (int p0 = pb; p0 < pe; p0 += 16 * kSplitRounds) {
+    if (p0 != pb) issue(p0);
+#pragma unroll
+    for (int r = 0; r < kSplitRounds; r++) {
+      const int p = p0 + 16 * r + 4 * w + slot;
+      const u32x4 vr = vx[r];
+      const float vf[8] = {lo_bf16(vr.x), hi_bf16(vr.x), lo_bf16(vr.y), hi_bf16(vr.y),
+                           lo_bf16(vr.z), hi_bf16(vr.z), lo_bf16(vr.w), hi_bf16(vr.w)};
+#pragma unroll
+      for (int hh = 0; hh < 2; hh++) {
+        const float pr = p < pe ? bf16r(exp_acc(sc_in[(size_t)hh * cap + p] - M[hh]) * inv[hh]) : 0.f;
+        // a masked position (it loaded cache row 0, which the caller may not have written) leaves the
+        // sum untouched, so that a NaN there cannot enter it through 0 * NaN
+#pragma unroll
+        for (int i = 0; i < 8; i++) acc[hh][i] = p < pe ? __builtin_fmaf(pr, vf[i], acc[hh][i]) : acc[hh][i];
+      }
+    }
+  }
+  // the wave's four rows summed; lanes 0..15 hold dims 8*t16..+7
+#pragma unroll
+  for (int hh = 0; hh < 2; hh++) {
+#pragma unroll
+    for (int i = 0; i < 8; i++) acc[hh][i] = rows_sum4(acc[hh][i]);
+    if (lane < 16) {
+#pragma unroll
+      for (int i = 0; i < 8; i++) wacc[w][hh][8 * t16 + i] = acc[hh][i];
+    }
+  }
+  __syncthreads();
+  // this split's partial: the waves' in wave order
+  {
+    const int hh = threadIdx.x >> 7, d = threadIdx.x & 127;  // 256 threads: both heads' dims
+    float a = 0.f;
+#pragma unroll
+    for (int q = 0; q < kSplitWaves; q++) a += wacc[q][hh][d];
+    pt[sp].acc[hh][d] = a;
+  }
+}
+
+// The attention output of (token t, KV head g): its S partials added in split order.  256 threads:
+// thread i takes head 2g + i / 128, dim i % 128.
 __global__ void __launch_bounds__(256) attention_merge(const Tok* __restrict__ tok, int S,
                                                        const AttnPart* __restrict__ part, uint16_t* __restrict__ out) {
   const int t = blockIdx.x, g = blockIdx.y;
@@ -1638,16 +1683,9 @@ __global__ void __launch_bounds__(256) attention_merge(const Tok* __restrict__ t
   const AttnPart* pt = part + ((size_t)t * kNKV + g) * S;
   uint16_t* dst = out + (size_t)t * kQS + 2 * g * kD;
   const int hh = threadIdx.x >> 7, d = threadIdx.x & 127;
-  float mx = -INFINITY;
-  for (int q = 0; q < S; q++) mx = fmaxf(mx, pt[q].m[hh]);
-  float y = 0.f, ls = 0.f;
-  for (int q = 0; q < S; q++) {
-    const float mq = pt[q].m[hh];
-    const float f = mq == -INFINITY ? 0.f : exp_acc(mq - mx);
-    y += f * pt[q].acc[hh][d];
-    ls += f * pt[q].l[hh];
-  }
-  dst[threadIdx.x] = (uint16_t)f32_to_bf16(__fdiv_rn(y, ls));
+  float y = 0.f;
+  for (int q = 0; q < S; q++) y += pt[q].acc[hh][d];
+  dst[threadIdx.x] = (uint16_t)f32_to_bf16(y);
 }
 
 // ---------------------------------------------------------------- self-test
@@ -1793,6 +1831,7 @@ Layout layout(int T, int R, int max_context, bool one_per_seq = false) {
   if (one_per_seq && fused_decode(T, max_context)) {
     take(l.qkv, (size_t)T * kNQKV * 2);
     take(l.apart, (size_t)T * kNKV * attn_splits(T) * sizeof(AttnPart));
+    take(l.scores, (size_t)T * kNQ * max_context * 4);
     l.total = off;
     return l;
   }
@@ -1904,6 +1943,7 @@ int forward_fused(const Args& a, hipStream_t s) {
   static_assert(Dm::I == 3072 || Dm::I == 6144, "K splits of the MLP size");
   static_assert(kQS == 2048 && Dm::H <= kMaxRowsH, "K splits of the attention output");
   AttnPart* apart = reinterpret_cast<AttnPart*>(a.ws + l.apart);
+  float* ascores = reinterpret_cast<float*>(a.ws + l.scores);
   const int nsplit = attn_splits(T);
   hipLaunchKernelGGL(prep_tokens, dim3((std::max(T, R) + 255) / 256), dim3(256), 0, s, a.tokens, a.seqs, a.pos, T,
                      a.emit, R, a.num_seqs, a.max_context, Dm::V, tok, erow);
@@ -1914,7 +1954,9 @@ int forward_fused(const Args& a, hipStream_t s) {
     launch_rows<kEpiStore, true, 16>(kNQKV / 16, X, u16(w.input_layernorm_weight), eps, T, Dm::H, qkv, QKV, kNQKV, s);
     hipLaunchKernelGGL(attention_split, dim3(T, kNKV, nsplit), dim3(kSplitWaves * 64), 0, s, QKV, tok, L,
                        u16(w.q_norm_weight), u16(w.k_norm_weight), a.cos_t, a.sin_t, a.cache, eps, a.attn_scale,
-                       apart, ATT);
+                       apart, ascores, a.max_context, ATT);
+    hipLaunchKernelGGL(attention_pv, dim3(T, kNKV, nsplit), dim3(kSplitWaves * 64), 0, s, tok, L, a.cache, apart,
+                       ascores, a.max_context);
     hipLaunchKernelGGL(attention_merge, dim3(T, kNKV), dim3(256), 0, s, tok, nsplit, apart, ATT);
     const Seg o{{u16(w.o_proj_weight), nullptr, nullptr}, {Dm::H, 0, 0}};
     launch_rows<kEpiResidual, false, 16, true>(Dm::H / 8, ATT, nullptr, eps, T, kQS, o, X, Dm::H, s);

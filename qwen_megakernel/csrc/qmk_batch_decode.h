@@ -18,7 +18,7 @@
 // batch per sequence.  Each sequence has its own control wave, so the
 // per-sequence exchanges, norms and merges of a step run side by side.
 //
-// It replaces the six launches per layer of the fused batched step
+// It replaces the seven launches per layer of the fused batched step
 // (qmk_batch.hip) for these shapes; the reference decodes one sequence
 // (qwen_megakernel/model.py:111-250), so there is no reference counterpart.
 //

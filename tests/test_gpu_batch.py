@@ -13,8 +13,8 @@ up to rounding.
 import pytest
 import torch
 
-from parity import (LAYERS28, LITERAL, Tally, check_kv_rows, check_row, check_rows, decoder, exact_oracle, oracle_steps,
-                    stream_rows, with_rope)
+from parity import (LAYERS28, LITERAL, Tally, check_kv_rows, check_row, check_rows, decoder, exact_oracle, fp32_oracle,
+                    oracle_steps, stream_envelopes, stream_rows, with_rope)
 
 pytestmark = pytest.mark.gpu
 
@@ -128,6 +128,40 @@ def test_batch_decode_matches_oracle(shape, exact06, weights_gpu, batch_prompts)
         ref = stream_rows(orc, bd._k_cache[b], bd._v_cache[b], prompts[b], toks[b])
         print(check_rows(Tally(f"batched decode sequence {b}"), ref, toks[b], torch.stack(lgs[b]), bar=LAYERS28))
         check_kv_rows(f"batched decode sequence {b}", orc, bd._k_cache[b], bd._v_cache[b], 0, len(prompts[b]) + 10)
+
+
+def test_decode_batch_multi_launch_28_layers_long_prompts(shape, exact06, weights_cpu, weights_gpu):
+    """Three sequences after prompts of 1300, 2100 and 3000 tokens, 28 layers, 4 batched steps:
+    contexts above 2,048 positions take the multi-launch step (HF's two softmax passes split over
+    every CU, the probabilities rounded to bf16).  Each sequence's prefill row and steps against
+    its own oracle on the step's inputs, to the 28-layer bar (a token may leave the oracle's argmax
+    beyond one ulp only within the step's fp32 envelope)."""
+    from qwen_megakernel.model import BatchDecoder
+    from qwen_megakernel.weights import make_prompt
+
+    lens, max_seq = (1300, 2100, 3000), 4096
+    prompts = [make_prompt(n, V, seed=80 + i) for i, n in enumerate(lens)]
+    bd = BatchDecoder(weights=with_rope(weights_gpu, max_seq, "cuda"), batch_size=3, max_seq_len=max_seq,
+                      verbose=False)
+    toks, lgs = [], []
+    for b, p in enumerate(prompts):
+        tok, lg = bd.prefill(b, p, return_logits=True)
+        toks.append([tok])
+        lgs.append([lg.cpu()])
+    for _ in range(4):
+        nxt, logits = bd.step_logits([t[-1] for t in toks])
+        for b in range(3):
+            toks[b].append(nxt[b])
+            lgs[b].append(logits[b].cpu())
+    forc = fp32_oracle(weights_cpu, shape, max_seq)
+    for b in range(3):
+        n0 = len(prompts[b]) - 1
+        feed = [prompts[b][-1]] + toks[b][:-1]  # the rows at positions n0.. that produced toks[b]
+        orc = exact_oracle(exact06, shape, max_seq)
+        ref = oracle_steps(orc, bd._k_cache[b], bd._v_cache[b], n0, feed)
+        envs = stream_envelopes(forc, bd._k_cache[b], bd._v_cache[b], n0, feed, ref)
+        print(check_rows(Tally(f"multi-launch batched decode, 28 layers, sequence {b} after {lens[b]}"), ref,
+                         toks[b], torch.stack(lgs[b]), bar=LAYERS28, envs=envs))
 
 
 def test_batch_generate_matches_oracle_streams(shape, exact06, weights_gpu, batch_prompts):
