@@ -74,7 +74,7 @@ PROMPT_LEN = 128
 TRAFFIC_PROFILE = {
     "file": "profiles/decode_kernel_qwen3_0p6b_ctx129-1152_xcd_parallel.md",
     "contexts": "129..1152",
-    "measured_bytes": 1_344_351_773,
+    "measured_bytes": 1_344_236_094,
     "algorithmic_bytes": 1_265_674_240,
 }
 METRIC = "decode tok/s, batch 1, Qwen3-0.6B bf16; achieved HBM GB/s vs ~8 TB/s peak"
