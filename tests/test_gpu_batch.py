@@ -353,6 +353,40 @@ def test_invalid_entries_emit_minus_one(weights_gpu):
         fwd(tokens, _i32([0, 0, 0, 0]), positions, _i32([0]), out[:1], None, dec._k_cache, dec._v_cache, 65)
 
 
+def test_invalid_entries_in_a_long_prompt(weights_gpu):
+    """A 1024-token prompt (the fused q/k/v and gate/up epilogues, the MFMA attention) with a token
+    id outside the vocabulary at row 300 and a position outside max_context at row 700: those rows
+    emit -1 and write no cache row, the tiles holding them are redone row by row, the other rows
+    emit tokens, and a second identical forward gives the same tokens and logits."""
+    from qwen_megakernel.weights import make_prompt
+
+    n = 1024
+    dec = decoder(weights_gpu, num_layers=2, max_seq_len=n)
+    fwd = dec._forward
+    ids = make_prompt(n, V, seed=33)
+    ids[300] = V
+    pos = list(range(n))
+    pos[700] = 5000
+    emit = [0, 299, 300, 301, 700, 1023]
+    runs = []
+    for _ in range(2):
+        dec._k_cache.zero_()
+        dec._v_cache.zero_()
+        out = torch.empty(len(emit), dtype=torch.int32, device="cuda")
+        logits = torch.empty(len(emit), V, dtype=torch.float32, device="cuda")
+        fwd(_i32(ids), _i32([0] * n), _i32(pos), _i32(emit), out, logits, dec._k_cache, dec._v_cache, n)
+        runs.append((out.cpu().tolist(), logits.cpu()))
+    res, lg = runs[0]
+    assert runs[1][0] == res and torch.equal(runs[1][1], lg), "second forward differs"
+    assert res[2] == -1 and res[4] == -1, res
+    assert all(res[i] >= 0 for i in (0, 1, 3, 5)), res
+    kc, vc = dec._k_cache.float().cpu(), dec._v_cache.float().cpu()
+    for p in (300, 700):
+        assert kc[:, :, p].abs().sum() == 0 and vc[:, :, p].abs().sum() == 0, p
+    for p in (0, 299, 301, 1023):
+        assert kc[:, :, p].abs().sum() > 0 and vc[:, :, p].abs().sum() > 0, p
+
+
 def test_batched_forward_deterministic(weights_gpu):
     """Fixed-order reductions: two identical forwards give bit-identical logits."""
     from qwen_megakernel.weights import make_prompt
