@@ -403,6 +403,9 @@ struct Common {
 int validate(const Common& c) {
   if (!c.embed || !c.layers || !c.final_norm || !c.lm_head || !c.cos_t || !c.sin_t || !c.k_cache || !c.v_cache)
     return QMK_ERR_ARG;
+  for (const void* p : {c.embed, (const void*)c.layers, c.final_norm, c.lm_head, c.cos_t, c.sin_t,
+                        (const void*)c.k_cache, (const void*)c.v_cache})
+    if (!aligned16(p)) return QMK_ERR_ARG;
   if (c.model != QMK_MODEL_QWEN3_0_6B && c.model != QMK_MODEL_QWEN3_1_7B) return QMK_ERR_ARG;
   if (c.num_layers < 1 || c.num_layers > 28 || c.max_seq_len < 1 || c.max_seq_len > kMaxSeqLen) return QMK_ERR_ARG;
   if (!(c.attn_scale > 0.f)) return QMK_ERR_ARG;
@@ -665,7 +668,10 @@ int batch_persistent_impl(int model, int batch, const int* tokens, const int* po
       !v_cache || num_layers < 1 || num_layers > kMaxLayers || max_seq_len < 1 || max_seq_len > kMaxSeqLen ||
       max_context < 1 || max_context > max_seq_len || max_context > kBatchMaxContext || !(attn_scale > 0.f))
     return QMK_ERR_ARG;
-  if (seq_stride < (long long)num_layers * Dm::NKV * max_seq_len * Dm::D) return QMK_ERR_ARG;
+  if (seq_stride < (long long)num_layers * Dm::NKV * max_seq_len * Dm::D || seq_stride % 8 != 0) return QMK_ERR_ARG;
+  for (const void* q : {embed_weight, final_norm_weight, lm_head_weight, cos_table, sin_table, (const void*)k_cache,
+                        (const void*)v_cache})
+    if (!aligned16(q)) return QMK_ERR_ARG;
   // out_tokens is written (-1) at the start of the step, before every workgroup has read tokens
   if (ranges_overlap(tokens, batch * sizeof(int), out_tokens, batch * sizeof(int)) ||
       ranges_overlap(positions, batch * sizeof(int), out_tokens, batch * sizeof(int)))
@@ -677,7 +683,7 @@ int batch_persistent_impl(int model, int batch, const int* tokens, const int* po
                          w.q_norm_weight, w.k_norm_weight, w.o_proj_weight, w.post_attn_layernorm_weight,
                          w.gate_proj_weight, w.up_proj_weight, w.down_proj_weight};
     for (const void* q : p)
-      if (!q) return QMK_ERR_ARG;
+      if (!q || !aligned16(q)) return QMK_ERR_ARG;
   }
   Ctx* ctx = nullptr;
   int s = get_ctx(stream, &ctx);

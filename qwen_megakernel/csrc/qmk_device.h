@@ -30,6 +30,10 @@ constexpr int kBlock = (kComputeWaves + 1) * kWave;
 constexpr int kGroups = 8;        // workgroup b runs on XCD b % 8
 constexpr int kGroupSize = kNumWG / kGroups;
 
+// The kernels read weights, tables, caches and activations with 16-byte vector loads (and LDS DMA),
+// so every such pointer must be 16-byte aligned (torch allocations are); the entry points check it.
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
 // ---------------------------------------------------------------- bf16
 
 __device__ __forceinline__ float bf16_to_f32(uint32_t h) { return __uint_as_float(h << 16); }

@@ -87,6 +87,11 @@ def test_host_validation_rejects_bad_arguments_before_launch(lib):
     # persistent form: cache_len must be position + 1
     lib.launch_ldg_decode_persistent(*_decode_args(position=3, cache_len=7))
     assert lib.qmk_last_status() == QMK_ERR_ARG
+    # a weight pointer that is not 16-byte aligned (the kernels read with 16-byte vector loads)
+    args = _decode_args()
+    args[2] = V(4096 + 2)  # embed
+    lib.launch_ldg_decode_direct(*args)
+    assert lib.qmk_last_status() == QMK_ERR_ARG
     assert b"position" in lib.qmk_status_string(QMK_ERR_POSITION)
 
 
@@ -193,9 +198,9 @@ def test_forward_tokens_host_validation(lib):
     p = V(4096)
 
     def call(model=0, T=4, R=4, table_ptr=table, num_seqs=4, stride=2 * 8 * 64 * 128, layers=2, max_seq=64,
-             max_ctx=64, ws=need, null_tokens=False):
+             max_ctx=64, ws=need, null_tokens=False, embed=p, k_cache=p):
         return f(ctypes.c_int(model), ctypes.c_int(T), V(0) if null_tokens else p, p, p, ctypes.c_int(R), p, p,
-                 V(0), p, table_ptr, p, p, p, p, p, p, ctypes.c_int(num_seqs), ctypes.c_longlong(stride),
+                 V(0), embed, table_ptr, p, p, p, p, k_cache, p, ctypes.c_int(num_seqs), ctypes.c_longlong(stride),
                  ctypes.c_int(layers), ctypes.c_int(max_seq), ctypes.c_int(max_ctx), ctypes.c_float(0.088), p,
                  ctypes.c_size_t(ws), V(0))
 
@@ -206,6 +211,14 @@ def test_forward_tokens_host_validation(lib):
     assert call(stride=100) == QMK_ERR_ARG            # sequences would overlap
     assert call(R=257) == QMK_ERR_ARG
     assert call(layers=29) == QMK_ERR_ARG
+    # the kernels read with 16-byte vector loads: every operand pointer 16-byte aligned, and the
+    # per-sequence cache stride a multiple of 8 elements
+    assert call(embed=V(4096 + 2)) == QMK_ERR_ARG
+    assert call(k_cache=V(4096 + 8)) == QMK_ERR_ARG
+    assert call(stride=2 * 8 * 64 * 128 + 4) == QMK_ERR_ARG
+    table[0].q_norm = 4096 + 2
+    assert call() == QMK_ERR_ARG
+    table[0].q_norm = 4096
     table[1].o_proj = None
     assert call() == QMK_ERR_ARG                      # a null weight pointer in the host table
 
