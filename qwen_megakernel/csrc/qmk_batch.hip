@@ -829,7 +829,7 @@ __global__ void __launch_bounds__(kAttnWaves * 64) attention_mfma(const uint16_t
     if (!s_ok[u]) continue;  // uniform over the workgroup
     const int t0 = tiles[u] * kQT, nrows = min(kQT, T - t0);
     const Tok first = tok[t0];
-    const int pos0 = first.pos, pmax = pos0 + nrows - 1;
+    const int pos0 = __builtin_amdgcn_readfirstlane(first.pos), pmax = pos0 + nrows - 1;
     const size_t base = cache_base(c, first, L, g);
     const uint16_t* kc = c.k + base;
     const uint16_t* vc = c.v + base;
@@ -839,6 +839,7 @@ __global__ void __launch_bounds__(kAttnWaves * 64) attention_mfma(const uint16_t
 #pragma unroll
     for (int kk = 0; kk < 4; kk++) qb[kk] = ld_bf16x8(Q + (size_t)tq * kQS + h * kD + 32 * kk + 8 * lg);
     const int rpos = pos0 + 16 * rg + l16;      // this lane's row position
+    const int wave_first = pos0 + 16 * rg;      // the wave's smallest row position
     const int wave_last = pos0 + 16 * rg + 15;  // the wave's largest row position
     const int nkb = (pmax + kKB) / kKB;         // blocks covering positions 0..pmax
     // Block kb: positions kb*kKB + pr; rows past pmax load row pmax (masked below).  Each
@@ -910,29 +911,37 @@ __global__ void __launch_bounds__(kAttnWaves * 64) attention_mfma(const uint16_t
       if (kb + 1 < nkb) load_k(kb + 1);
       const int kbase = kb * kKB + 32 * kh;
       if (kbase > wave_last) continue;  // every key of the wave's half block follows its rows
-      float x[2][4];
-      float mb = -INFINITY;
+      // MASKED: the half block reaches the causal diagonal of the wave's rows (the last one or two
+      // blocks of a tile); every earlier key precedes every row, so neither the mask nor the
+      // clamp of exp_acc is needed (exp_finite gives the same values for finite arguments)
+      auto block = [&](auto masked) {
+        constexpr bool MASKED = decltype(masked)::value;
+        float x[2][4];
+        float mb = -INFINITY;
 #pragma unroll
-      for (int n = 0; n < 2; n++) {
-        const f32x4 sc = kbase + 16 * n <= wave_last ? tile_scores(n) : f32x4{0.f, 0.f, 0.f, 0.f};
-        scaled(sc, x[n]);
+        for (int n = 0; n < 2; n++) {
+          const f32x4 sc = !MASKED || kbase + 16 * n <= wave_last ? tile_scores(n) : f32x4{0.f, 0.f, 0.f, 0.f};
+          scaled(sc, x[n]);
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-          x[n][i] = kbase + 16 * n + 4 * lg + i <= rpos ? x[n][i] : -INFINITY;
-          mb = fmaxf(mb, x[n][i]);
+          for (int i = 0; i < 4; i++) {
+            if constexpr (MASKED) x[n][i] = kbase + 16 * n + 4 * lg + i <= rpos ? x[n][i] : -INFINITY;
+            mb = fmaxf(mb, x[n][i]);
+          }
         }
-      }
-      // no branch: while every key so far is masked for this lane's row (mn = -inf) the terms are
-      // taken against 0, and exp_acc turns -inf into 0, so ls stays 0
-      const float mn = fmaxf(m, mb);
-      const float ref = mn == -INFINITY ? 0.f : mn;
-      float e = 0.f;
+        // no branch: while every key so far is masked for this lane's row (mn = -inf) the terms
+        // are taken against 0, and exp_acc turns -inf into 0, so ls stays 0
+        const float mn = fmaxf(m, mb);
+        const float ref = MASKED && mn == -INFINITY ? 0.f : mn;
+        float e = 0.f;
 #pragma unroll
-      for (int n = 0; n < 2; n++)
+        for (int n = 0; n < 2; n++)
 #pragma unroll
-        for (int i = 0; i < 4; i++) e += exp_acc(x[n][i] - ref);
-      ls = ls * exp_acc(m - ref) + e;
-      m = mn;
+          for (int i = 0; i < 4; i++) e += MASKED ? exp_acc(x[n][i] - ref) : exp_finite(x[n][i] - ref);
+        ls = ls * exp_acc(m - ref) + e;
+        m = mn;
+      };
+      if (kbase + 31 <= wave_first) block(std::false_type{});
+      else block(std::true_type{});
     }
     // row l16's (max, sum): over the 4 lanes of equal l16, then the row group's two waves (the
     // even wave's pair first in every wave, so both waves hold the same M and 1/L)
@@ -976,22 +985,27 @@ __global__ void __launch_bounds__(kAttnWaves * 64) attention_mfma(const uint16_t
       if (kbase > wave_last) continue;
       // A operand: k-slot 4n + i of this lane is key kbase + 16n + 4lg + i of row l16
       uint32_t pw[4];
+      auto probs = [&](auto masked) {  // MASKED as in pass 1
+        constexpr bool MASKED = decltype(masked)::value;
 #pragma unroll
-      for (int n = 0; n < 2; n++) {
-        // a 16-key tile wholly past the wave's rows is masked for every row: no MFMA for it
-        const f32x4 sc = kbase + 16 * n <= wave_last ? tile_scores(n) : f32x4{0.f, 0.f, 0.f, 0.f};
-        float x[4], pr[4];
-        scaled(sc, x);
+        for (int n = 0; n < 2; n++) {
+          // a 16-key tile wholly past the wave's rows is masked for every row: no MFMA for it
+          const f32x4 sc = !MASKED || kbase + 16 * n <= wave_last ? tile_scores(n) : f32x4{0.f, 0.f, 0.f, 0.f};
+          float x[4], pr[4];
+          scaled(sc, x);
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-          // the probability bf16(exp(s - M) / L) (rounded once, by the packing below); masked
-          // keys, whose terms may be anything, take 0
-          const float e = exp_acc(x[i] - gm) * ginv;
-          pr[i] = kbase + 16 * n + 4 * lg + i <= rpos ? e : 0.f;
+          for (int i = 0; i < 4; i++) {
+            // the probability bf16(exp(s - M) / L) (rounded once, by the packing below); masked
+            // keys, whose terms may be anything, take 0
+            if constexpr (MASKED) pr[i] = kbase + 16 * n + 4 * lg + i <= rpos ? exp_acc(x[i] - gm) * ginv : 0.f;
+            else pr[i] = exp_finite(x[i] - gm) * ginv;
+          }
+          pw[2 * n] = pack_bf16x2(pr[0], pr[1]);
+          pw[2 * n + 1] = pack_bf16x2(pr[2], pr[3]);
         }
-        pw[2 * n] = pack_bf16x2(pr[0], pr[1]);
-        pw[2 * n + 1] = pack_bf16x2(pr[2], pr[3]);
-      }
+      };
+      if (kbase + 31 <= wave_first) probs(std::false_type{});
+      else probs(std::true_type{});
       const bf16x8 pa = __builtin_bit_cast(bf16x8, u32x4{pw[0], pw[1], pw[2], pw[3]});
 #pragma unroll
       for (int j = 0; j < 8; j++)

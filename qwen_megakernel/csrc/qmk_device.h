@@ -76,18 +76,21 @@ __device__ __forceinline__ float dot8(u32x4 w, u32x4 x, float acc) {
 // exp(x) for the softmax: 2^(x*log2(e)) with the product split into a rounded
 // high part and its exact low remainder (Cody-Waite style), so that the
 // argument error stays within an ulp for any |x|; the hardware exp2 covers the
-// rest.  The argument is clamped at -128, whose exp underflows to 0, so -inf
-// (an empty softmax row) gives 0 instead of the NaN of inf - inf.
-__device__ __forceinline__ float exp_acc(float x) {
+// rest.  exp_finite takes finite x (it gives NaN for -inf); exp_acc clamps the
+// argument at -128 first, whose exp underflows to 0, so -inf (an empty softmax
+// row, a masked score) gives 0.  For every finite x the two give the same value
+// (below -128 both give 0).
+__device__ __forceinline__ float exp_finite(float x) {
   constexpr float kL2eHi = 1.44269502162933349609375f;   // log2(e) rounded to fp32
   constexpr float kL2eLo = 1.925963033500011e-08f;        // log2(e) - kL2eHi
   constexpr float kLn2 = 0.693147180559945309f;
-  x = fmaxf(x, -128.0f);
   const float hi = x * kL2eHi;
   const float lo = __builtin_fmaf(x, kL2eHi, -hi) + x * kL2eLo;  // |lo| < 2^-16: 2^lo = 1 + lo*ln2
   const float e = __builtin_amdgcn_exp2f(hi);
   return __builtin_fmaf(e * lo, kLn2, e);
 }
+
+__device__ __forceinline__ float exp_acc(float x) { return exp_finite(fmaxf(x, -128.0f)); }
 
 // Exchange a value with the lane 16 (sum over rows 2k, 2k+1) or 32 lanes away
 // (sum over the two wave halves) through the gfx950 permlane swaps, which run
