@@ -847,33 +847,36 @@ __global__ void __launch_bounds__(kAttnWaves * 64) attention_mfma(const uint16_t
     // before block kb's MFMAs, so its memory latency overlaps them, and written to LDS after
     // the next barrier.
     constexpr int kCh = kKB * (kD / 8) / NT;
-    u32x4 rk[kCh], rv[kCh];
-    auto load_k = [&](int kb) {
+    // two register sets: block kb + 2 is requested right after block kb is written to LDS, so a
+    // request has two blocks of compute to land
+    u32x4 rk[2][kCh], rv[2][kCh];
+    auto load_k = [&](int set, int kb) {
 #pragma unroll
       for (int j = 0; j < kCh; j++) {
         const int ci = threadIdx.x + NT * j, pr = ci >> 4, col = (ci & 15) * 8;
-        rk[j] = ld16(kc + (size_t)min(kb * kKB + pr, pmax) * kD + col);
+        rk[set][j] = ld16(kc + (size_t)min(kb * kKB + pr, pmax) * kD + col);
       }
     };
     // V: this thread carries keys 2va and 2va+1 of the block, dims 8vc..8vc+7 (a wave's lanes
     // cover four dim chunks of 16 key pairs), so each transposed LDS word takes both keys' values
     static_assert(kCh == 2, "one key pair per thread");
     const int va = (lane >> 2) + 16 * (w & 1), vcol = 8 * ((lane & 3) + 4 * (w >> 1));
-    auto load_v = [&](int kb) {
+    auto load_v = [&](int set, int kb) {
 #pragma unroll
-      for (int j = 0; j < 2; j++) rv[j] = ld16(vc + (size_t)min(kb * kKB + 2 * va + j, pmax) * kD + vcol);
+      for (int j = 0; j < 2; j++) rv[set][j] = ld16(vc + (size_t)min(kb * kKB + 2 * va + j, pmax) * kD + vcol);
     };
-    auto put_k = [&]() {
+    auto put_k = [&](int set) {
 #pragma unroll
       for (int j = 0; j < kCh; j++) {
         const int ci = threadIdx.x + NT * j, pr = ci >> 4, col = (ci & 15) * 8;
-        *reinterpret_cast<u32x4*>(&Ks[pr][col]) = rk[j];
+        *reinterpret_cast<u32x4*>(&Ks[pr][col]) = rk[set][j];
       }
     };
-    auto put_v = [&]() {  // transposed, keys in P@V slot order: Vt[dim][slot]; keys 2va, 2va+1
-                          // take adjacent slots, so each dim is one 32-bit word
+    auto put_v = [&](int set) {  // transposed, keys in P@V slot order: Vt[dim][slot]; keys 2va, 2va+1
+                                 // take adjacent slots, so each dim is one 32-bit word
       const int sw = attn_v_slot(2 * va) >> 1;
-      const uint32_t k0[4] = {rv[0].x, rv[0].y, rv[0].z, rv[0].w}, k1[4] = {rv[1].x, rv[1].y, rv[1].z, rv[1].w};
+      const u32x4 a0 = rv[set][0], a1 = rv[set][1];
+      const uint32_t k0[4] = {a0.x, a0.y, a0.z, a0.w}, k1[4] = {a1.x, a1.y, a1.z, a1.w};
 #pragma unroll
       for (int e = 0; e < 4; e++) {
         Vw[vcol + 2 * e][sw] = (k0[e] & 0xffffu) | (k1[e] << 16);
@@ -903,14 +906,9 @@ __global__ void __launch_bounds__(kAttnWaves * 64) attention_mfma(const uint16_t
     // ---- pass 1: per lane, online max and sum of exp over its positions (one exp per score,
     // one rescale per block)
     float m = -INFINITY, ls = 0.f;
-    load_k(0);
-    for (int kb = 0; kb < nkb; kb++) {
-      __syncthreads();  // the previous block's reads are done
-      put_k();
-      __syncthreads();
-      if (kb + 1 < nkb) load_k(kb + 1);
+    auto pass1 = [&](int kb) {
       const int kbase = kb * kKB + 32 * kh;
-      if (kbase > wave_last) continue;  // every key of the wave's half block follows its rows
+      if (kbase > wave_last) return;  // every key of the wave's half block follows its rows
       // MASKED: the half block reaches the causal diagonal of the wave's rows (the last one or two
       // blocks of a tile); every earlier key precedes every row, so neither the mask nor the
       // clamp of exp_acc is needed (exp_finite gives the same values for finite arguments)
@@ -942,6 +940,23 @@ __global__ void __launch_bounds__(kAttnWaves * 64) attention_mfma(const uint16_t
       };
       if (kbase + 31 <= wave_first) block(std::false_type{});
       else block(std::true_type{});
+    };
+    // blocks past the last one are requested too (clamped rows, never used), so that every path
+    // issues the same loads and the compiler's counted waits stay exact
+    load_k(0, 0);
+    load_k(1, 1);
+    for (int kb = 0; kb < nkb; kb += 2) {
+      __syncthreads();  // the previous block's reads are done
+      put_k(0);
+      __syncthreads();
+      load_k(0, kb + 2);
+      pass1(kb);
+      if (kb + 1 >= nkb) break;
+      __syncthreads();
+      put_k(1);
+      __syncthreads();
+      load_k(1, kb + 3);
+      pass1(kb + 1);
     }
     // row l16's (max, sum): over the 4 lanes of equal l16, then the row group's two waves (the
     // even wave's pair first in every wave, so both waves hold the same M and 1/L)
@@ -970,19 +985,9 @@ __global__ void __launch_bounds__(kAttnWaves * 64) attention_mfma(const uint16_t
     f32x4 acc[8];
 #pragma unroll
     for (int j = 0; j < 8; j++) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-    load_k(0);
-    load_v(0);
-    for (int kb = 0; kb < nkb; kb++) {
-      __syncthreads();
-      put_k();
-      put_v();
-      __syncthreads();
-      if (kb + 1 < nkb) {
-        load_k(kb + 1);
-        load_v(kb + 1);
-      }
+    auto pass2 = [&](int kb) {
       const int kbase = kb * kKB + 32 * kh;
-      if (kbase > wave_last) continue;
+      if (kbase > wave_last) return;
       // A operand: k-slot 4n + i of this lane is key kbase + 16n + 4lg + i of row l16
       uint32_t pw[4];
       auto probs = [&](auto masked) {  // MASKED as in pass 1
@@ -1011,6 +1016,27 @@ __global__ void __launch_bounds__(kAttnWaves * 64) attention_mfma(const uint16_t
       for (int j = 0; j < 8; j++)
         acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
             pa, *reinterpret_cast<const bf16x8*>(&Vt[16 * j + l16][32 * kh + 8 * lg]), acc[j], 0, 0, 0);
+    };
+    load_k(0, 0);
+    load_v(0, 0);
+    load_k(1, 1);
+    load_v(1, 1);
+    for (int kb = 0; kb < nkb; kb += 2) {
+      __syncthreads();
+      put_k(0);
+      put_v(0);
+      __syncthreads();
+      load_k(0, kb + 2);
+      load_v(0, kb + 2);
+      pass2(kb);
+      if (kb + 1 >= nkb) break;
+      __syncthreads();
+      put_k(1);
+      put_v(1);
+      __syncthreads();
+      load_k(1, kb + 3);
+      load_v(1, kb + 3);
+      pass2(kb + 1);
     }
     // the row group's two partials: the odd wave's through LDS (over the K/V buffers), added to
     // the even wave's
