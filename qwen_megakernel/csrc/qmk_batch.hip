@@ -269,26 +269,52 @@ __device__ __forceinline__ void qkv_head(const QkvOut& o, int t, int h, int lane
 
 // qkv_head for the 128 rows x 128 columns of one head held in LDS (bf16), rows t0.. (those
 // below T): wave w takes rows 32w..32w+31, four at a time, 16 lanes per row; lane c of a row
-// holds columns 4c..4c+3 and their RoPE partners 64+4c..64+4c+3.  The head-norm weights are
-// loaded once; the sum of squares runs over the row's 16 lanes.
-__device__ __forceinline__ void qkv_tile_rows(const QkvOut& o, const uint16_t (*Xh)[128], int t0, int T, int h, int w,
-                                              int lane) {
+// holds columns 4c..4c+3 and their RoPE partners 64+4c..64+4c+3.  The sum of squares runs over
+// the row's 16 lanes.  Everything the rows read from global memory besides the tile (their token
+// records, then their cos/sin entries, and the head-norm weights) is requested up front by
+// qkv_rows_fetch, before the tile goes through LDS, so the eight row groups do not each wait for
+// two dependent loads.
+struct QkvRowsIn {
+  Tok tk[8];
+  uint2 cl[8], ch[8], sl[8], sh[8];
+  float nw[8];
+};
+
+__device__ __forceinline__ void qkv_rows_fetch(const QkvOut& o, int t0, int T, int h, int w, int lane, QkvRowsIn& in) {
   const int c = lane & 15, sub = lane >> 4;
   const bool is_v = h >= kNQ + kNKV, is_q = h < kNQ;
-  float nw[8];
-  if (!is_v) {
-    const uint16_t* wp = is_q ? o.q_norm : o.k_norm;
 #pragma unroll
-    for (int e = 0; e < 4; e++) {
-      nw[e] = bf16_to_f32(ldu16(wp + 4 * c + e));
-      nw[4 + e] = bf16_to_f32(ldu16(wp + 64 + 4 * c + e));
-    }
+  for (int it = 0; it < 8; it++) {
+    const int t = t0 + 32 * w + 4 * it + sub;
+    in.tk[it] = o.tok[t < T ? t : t0];
   }
+  if (is_v) return;
+  const uint16_t* wp = is_q ? o.q_norm : o.k_norm;
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    in.nw[e] = bf16_to_f32(ldu16(wp + 4 * c + e));
+    in.nw[4 + e] = bf16_to_f32(ldu16(wp + 64 + 4 * c + e));
+  }
+#pragma unroll
+  for (int it = 0; it < 8; it++) {
+    const size_t pb = (size_t)in.tk[it].pos * kD;
+    in.cl[it] = *reinterpret_cast<const uint2*>(o.cos_t + pb + 4 * c);
+    in.ch[it] = *reinterpret_cast<const uint2*>(o.cos_t + pb + 64 + 4 * c);
+    in.sl[it] = *reinterpret_cast<const uint2*>(o.sin_t + pb + 4 * c);
+    in.sh[it] = *reinterpret_cast<const uint2*>(o.sin_t + pb + 64 + 4 * c);
+  }
+}
+
+__device__ __forceinline__ void qkv_tile_rows(const QkvOut& o, const uint16_t (*Xh)[128], int t0, int T, int h, int w,
+                                              int lane, const QkvRowsIn& in) {
+  const int c = lane & 15, sub = lane >> 4;
+  const bool is_v = h >= kNQ + kNKV, is_q = h < kNQ;
+#pragma unroll
   for (int it = 0; it < 8; it++) {
     const int row = 32 * w + 4 * it + sub, t = t0 + row;
     if (t0 + 32 * w + 4 * it >= T) break;  // uniform: no row of this group is below T
     const bool live = t < T;
-    const Tok tk = o.tok[live ? t : t0];
+    const Tok tk = in.tk[it];
     const uint2 lo = *reinterpret_cast<const uint2*>(&Xh[row][4 * c]);
     const uint2 hi = *reinterpret_cast<const uint2*>(&Xh[row][64 + 4 * c]);
     float x[8] = {lo_bf16(lo.x), hi_bf16(lo.x), lo_bf16(lo.y), hi_bf16(lo.y),
@@ -309,11 +335,8 @@ __device__ __forceinline__ void qkv_tile_rows(const QkvOut& o, const uint16_t (*
     const float rstd = rcp_sqrt_torch(__fdiv_rn(ss, (float)kD) + o.eps);
     float n[8];
 #pragma unroll
-    for (int e = 0; e < 8; e++) n[e] = bf16r(nw[e] * bf16r(x[e] * rstd));
-    const uint2 cl = *reinterpret_cast<const uint2*>(o.cos_t + (size_t)tk.pos * kD + 4 * c);
-    const uint2 ch = *reinterpret_cast<const uint2*>(o.cos_t + (size_t)tk.pos * kD + 64 + 4 * c);
-    const uint2 sl = *reinterpret_cast<const uint2*>(o.sin_t + (size_t)tk.pos * kD + 4 * c);
-    const uint2 sh = *reinterpret_cast<const uint2*>(o.sin_t + (size_t)tk.pos * kD + 64 + 4 * c);
+    for (int e = 0; e < 8; e++) n[e] = bf16r(in.nw[e] * bf16r(x[e] * rstd));
+    const uint2 cl = in.cl[it], ch = in.ch[it], sl = in.sl[it], sh = in.sh[it];
     const float cs[8] = {lo_bf16(cl.x), hi_bf16(cl.x), lo_bf16(cl.y), hi_bf16(cl.y),
                          lo_bf16(ch.x), hi_bf16(ch.x), lo_bf16(ch.y), hi_bf16(ch.y)};
     const float sn[8] = {lo_bf16(sl.x), hi_bf16(sl.x), lo_bf16(sl.y), hi_bf16(sl.y),
@@ -461,6 +484,8 @@ __global__ void __launch_bounds__(256, 2) gemm_tiled(const uint16_t* __restrict_
     // rows 32w..32w+31 one at a time, lane l columns l and l + 64
     static_assert(sizeof(sm) >= kTM * 128 * 2, "the head tile fits the operand stages");
     auto Xh = reinterpret_cast<uint16_t(*)[128]>(sm);
+    QkvRowsIn in;
+    qkv_rows_fetch(qo, t0, T, blockIdx.x, w, lane, in);
     __syncthreads();  // every wave's last operand reads are done
 #pragma unroll
     for (int i = 0; i < 4; i++)
@@ -470,7 +495,7 @@ __global__ void __launch_bounds__(256, 2) gemm_tiled(const uint16_t* __restrict_
         for (int r = 0; r < 4; r++)
           Xh[64 * wm + 16 * i + 4 * (lane >> 4) + r][64 * wn + 16 * j + l16] = (uint16_t)f32_to_bf16(acc[i][j][r]);
     __syncthreads();
-    qkv_tile_rows(qo, Xh, t0, T, blockIdx.x, w, lane);
+    qkv_tile_rows(qo, Xh, t0, T, blockIdx.x, w, lane, in);
   } else {
     // the tile's gate and up projections, bf16-rounded, through LDS: G[row][c], U[row][c] for
     // m = m0 + c; then each thread takes 8 consecutive m of one row at a time and stores them
