@@ -36,8 +36,6 @@
 namespace qmk {
 namespace batch {
 
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kD = 128, kNQ = 16, kNKV = 8, kQS = kNQ * kD, kNQKV = (kNQ + 2 * kNKV) * kD;
 constexpr int kAttnChunk = 2048;  // one-kernel attention: scores of this many positions per LDS pass

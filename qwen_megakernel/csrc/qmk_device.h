@@ -22,6 +22,8 @@ namespace qmk {
 
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));  // MFMA 16x16x32 bf16 operand
+typedef float f32x4 __attribute__((ext_vector_type(4)));    // MFMA 16x16 accumulator
 
 constexpr int kWave = 64;
 constexpr int kNumWG = 256;       // one workgroup per CU of an MI355X
