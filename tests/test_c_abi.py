@@ -84,6 +84,8 @@ def test_host_validation_rejects_bad_arguments_before_launch(lib):
     assert lib.qmk_last_status() == QMK_ERR_ARG
     lib.launch_ldg_decode_direct(*_decode_args(token=151936))
     assert lib.qmk_last_status() == QMK_ERR_ARG
+    lib.launch_ldg_decode_direct(*_decode_args(max_seq_len=65537))  # 65536 is the largest
+    assert lib.qmk_last_status() == QMK_ERR_ARG
     # persistent form: cache_len must be position + 1
     lib.launch_ldg_decode_persistent(*_decode_args(position=3, cache_len=7))
     assert lib.qmk_last_status() == QMK_ERR_ARG

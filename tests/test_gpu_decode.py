@@ -144,6 +144,32 @@ def test_long_context_parity(shape, exact06, weights_cpu, weights_gpu, c0, layer
     check_kv_rows(f"context {c0} x {layers} layers", orc, dec._k_cache, dec._v_cache, c0, len(feed))
 
 
+def test_decode_at_the_maximum_sequence_length(shape, exact06, weights_gpu):
+    """max_seq_len = 65536, the largest the entry points accept (the deep form, 2048 positions per
+    workgroup): an injected N(0,1) cache of 65532 positions, 4 layers, and 4 steps up to position
+    65535, the last one.  Every step against the exact oracle on the step's own inputs at the literal
+    bar, and the K/V rows the kernel appended; a further step is refused."""
+    from dataclasses import replace
+
+    from qwen_megakernel.weights import make_kv_prefill
+
+    layers, max_seq = 4, 65536
+    c0 = max_seq - 4
+    k, v = make_kv_prefill(replace(shape, num_layers=layers), c0, seed=5)
+    dec = decoder(with_rope(weights_gpu, max_seq, "cuda"), num_layers=layers, max_seq_len=max_seq)
+    dec.load_kv(k.cuda(), v.cuda(), c0)
+    del k, v
+    feed, toks, lgs = kernel_stream(dec, [11, 22], 3)
+    assert dec.position == max_seq
+    assert int(torch.ops.qwen_megakernel_C.device_error()) == 0
+    with pytest.raises(ValueError):
+        dec.step(5)
+    orc = exact_oracle(exact06, shape, max_seq, num_layers=layers)
+    ref = oracle_steps(orc, dec._k_cache, dec._v_cache, c0, feed)
+    print(check_rows(Tally(f"context {c0}..{max_seq - 1} x {layers} layers"), ref, toks, lgs, bar=LITERAL))
+    check_kv_rows(f"context {c0} x {layers} layers", orc, dec._k_cache, dec._v_cache, c0, len(feed))
+
+
 @pytest.mark.parametrize("c0", [8192, 32768], ids=["8192", "32768"])
 def test_long_context_256_step_stream(shape, exact06, weights_cpu, weights_gpu, c0):
     """The long-context workload's full length: 256 device-fed greedy steps (generate_nosync, the
