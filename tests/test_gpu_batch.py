@@ -548,3 +548,27 @@ def test_long_prefill_tiled_gemm(shape, exact06, weights_gpu, n):
     ref = oracle_steps(orc, dec._k_cache, dec._v_cache, 0, ids, emit=emit)
     print(check_rows(Tally(f"tiled-GEMM prefill {n}"), ref, toks, lg, labels=emit, bar=LITERAL))
     check_kv_rows(f"tiled-GEMM prefill {n}", orc, dec._k_cache, dec._v_cache, 0, n)
+
+
+def test_prefill_emits_the_maximum_rows(shape, exact06, weights_gpu):
+    """A 256-token prefill that emits every row: num_emit = 256, the most one forward takes (the
+    LM-head GEMM over 16 row tiles), 2 layers; every row's token and logits against the exact
+    oracle at the literal bar, and the rows in any order (emit reversed) give the same rows."""
+    from qwen_megakernel.weights import make_prompt
+
+    layers, n = 2, 256
+    ids = make_prompt(n, shape.vocab, seed=29)
+    dec = decoder(weights_gpu, num_layers=layers, max_seq_len=512)
+    outs = []
+    for emit in (list(range(n)), list(range(n - 1, -1, -1))):
+        out = torch.empty(n, dtype=torch.int32, device="cuda")
+        logits = torch.empty(n, V, dtype=torch.float32, device="cuda")
+        dec._forward(_i32(ids), torch.zeros(n, dtype=torch.int32, device="cuda"),
+                     torch.arange(n, dtype=torch.int32, device="cuda"), _i32(emit), out, logits, dec._k_cache,
+                     dec._v_cache, n)
+        outs.append((emit, out.cpu().tolist(), logits.cpu()))
+    (e0, t0, l0), (e1, t1, l1) = outs
+    assert t1[::-1] == t0 and torch.equal(l1.flip(0), l0), "the reversed emit list gave other rows"
+    orc = exact_oracle(exact06, shape, 512, num_layers=layers)
+    ref = oracle_steps(orc, dec._k_cache, dec._v_cache, 0, ids)
+    print(check_rows(Tally("256 emitted rows"), ref, t0, l0, bar=LITERAL))
