@@ -17,7 +17,9 @@
  *   layer_weights                  device array of num_layers LDGLayerWeights
  *   cos_table / sin_table          bf16 [max_seq_len][head_dim]
  *   k_cache / v_cache              bf16 [num_layers][num_kv_heads][max_seq_len][head_dim]
- *   hidden_buffer                  bf16 [hidden]   receives the final hidden state
+ *                                  (need not be zeroed: rows at or past a step's
+ *                                  position never reach its output, NaN included)
+ *   hidden_buffer                 bf16 [hidden]   receives the final hidden state
  *   g_normalized                   f32  [hidden]   receives the final-norm output
  * The other scratch pointers of the reference signature (g_activations,
  * g_residual, g_q, g_k, g_v, g_attn_out, g_mlp_intermediate, block_max_vals,
