@@ -13,14 +13,14 @@
 // and decodes one sequence; the batched forward is an addition.
 //
 // Per layer (kernels in launch order):
-//   gemm_partial(qkv)  -> qkv_finish (split-K sum, q/k RMSNorm + RoPE, K/V append;
+//   gemm_tiled(qkv)    -> qkv_finish (split-K sum, q/k RMSNorm + RoPE, K/V append;
 //                         in the GEMM's epilogue when K is not split)
 //   attention          (one kernel per (token, KV head) for many tokens; a
 //                       context-split pair + merge for few tokens)
-//   gemm_partial(o)    -> residual_norm (residual add, post-attention RMSNorm)
-//   gemm_partial(g|u)  -> gate_up_finish (SiLU(g) * u; in the GEMM's epilogue when K
+//   gemm_tiled(o)      -> residual_norm (residual add, post-attention RMSNorm)
+//   gemm_tiled(g|u)    -> gate_up_finish (SiLU(g) * u; in the GEMM's epilogue when K
 //                         is not split)
-//   gemm_partial(down) -> residual_norm (residual add, next layer's input RMSNorm
+//   gemm_tiled(down)   -> residual_norm (residual add, next layer's input RMSNorm
 //                                        or the final norm)
 // then lm_head_gemm over the emitted rows (bf16 logits, per-tile argmax keys)
 // -> keys_reduce (per-row argmax).
@@ -44,8 +44,7 @@ constexpr int kMfmaAttnTokens = 320;   // prompts of this many tokens run attent
 constexpr int kMfmaAttnContext = 1024; // so do fewer tokens over this many positions of context
 constexpr int kSplitChunk = 64;   // split attention: positions per workgroup
 constexpr int kSplitBelow = 32;   // fewer tokens than this use the split attention
-constexpr int kTargetWaves = 2048;
-constexpr int kMaxSplit = 32;     // K splits of one GEMM (their partials are summed in a fixed order)
+constexpr int kMaxSplit = 16;     // K splits of one GEMM (their partials are summed in a fixed order)
 constexpr int kMaxEmit = 256;
 
 static_assert(Qwen3_0_6B::D == kD && Qwen3_0_6B::NQ == kNQ && Qwen3_0_6B::NKV == kNKV, "head layout");
@@ -131,16 +130,11 @@ __global__ void __launch_bounds__(256) embed_rows(const uint16_t* __restrict__ e
 
 // ---------------------------------------------------------------- GEMM
 //
-// part[s][t][n] = sum over k in split s of X[row(t)][k] * W[n][k]   (fp32)
 // W rows come from up to three row-major [rows][K] matrices laid end to end
-// (q, k, v; or gate, up).  One wave computes a 16-row x 16*NB-column tile of
-// one K split with 16x16x32 bf16 MFMAs.  Operand layouts (checked by
-// qmk_selftest_mfma): lane l supplies A[l%16][8*(l/16) .. +7] and
-// B[8*(l/16) .. +7][l%16], i.e. 16 contiguous bytes of an X row and of a W
-// row; it receives C[4*(l/16) + i][l%16], i = 0..3.  Waves are numbered with
-// the row tile fastest, then the column tile, then the split, and workgroups
-// are renumbered so that consecutive numbers share an XCD: the row tiles that
-// read one weight tile run on one XCD and share its L2.
+// (q, k, v; or gate, up).  The GEMMs run on 16x16x32 bf16 MFMAs, whose
+// operand layouts (checked by qmk_selftest_mfma) are: lane l supplies
+// A[l%16][8*(l/16) .. +7] and B[8*(l/16) .. +7][l%16], i.e. 16 contiguous bytes
+// of an X row and of a W row; it receives C[4*(l/16) + i][l%16], i = 0..3.
 struct Seg {
   const uint16_t* w[3];
   int rows[3];
@@ -152,71 +146,6 @@ __device__ __forceinline__ const uint16_t* seg_row(const Seg& s, int n, int K) {
   if (n < s.rows[1]) return s.w[1] + (size_t)n * K;
   n -= s.rows[1];
   return s.w[2] + (size_t)n * K;
-}
-
-template <int NB, bool STREAM>
-__global__ void __launch_bounds__(256) gemm_partial(const uint16_t* __restrict__ X, const int* __restrict__ rows,
-                                                    int T, int K, Seg seg, int N, int ksplit,
-                                                    float* __restrict__ part) {
-  const int nblk = gridDim.x;
-  const int b = blockIdx.x;
-  const int lb = (nblk % kGroups == 0) ? (b % kGroups) * (nblk / kGroups) + b / kGroups : b;
-  const int wave = lb * 4 + (threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  const int mtiles = (T + 15) / 16, ntiles = N / (16 * NB);
-  const int mt = wave % mtiles;
-  const int nt = (wave / mtiles) % ntiles;
-  const int sp = wave / (mtiles * ntiles);
-  if (sp >= ksplit) return;
-  const int kchunk = K / ksplit, k0 = sp * kchunk, k1 = k0 + kchunk;
-  const int kq = 8 * (lane >> 4);
-  int xr = min(mt * 16 + (lane & 15), T - 1);
-  if (rows) xr = max(rows[xr], 0);
-  const uint16_t* xa = X + (size_t)xr * K + kq;
-  const uint16_t* wb[NB];
-#pragma unroll
-  for (int j = 0; j < NB; j++) wb[j] = seg_row(seg, nt * 16 * NB + 16 * j + (lane & 15), K) + kq;
-  f32x4 acc[NB];
-#pragma unroll
-  for (int j = 0; j < NB; j++) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-  bf16x8 a0, a1, b0[NB], b1[NB];
-  auto load = [&](int k, bf16x8& x0, bf16x8& x1, bf16x8 (&y0)[NB], bf16x8 (&y1)[NB]) {
-    x0 = ld_bf16x8(xa + k);
-    x1 = ld_bf16x8(xa + k + 32);
-#pragma unroll
-    for (int j = 0; j < NB; j++) {
-      y0[j] = STREAM ? ld_bf16x8_stream(wb[j] + k) : ld_bf16x8(wb[j] + k);
-      y1[j] = STREAM ? ld_bf16x8_stream(wb[j] + k + 32) : ld_bf16x8(wb[j] + k + 32);
-    }
-  };
-  load(k0, a0, a1, b0, b1);
-  for (int k = k0; k < k1; k += 64) {
-    bf16x8 na0, na1, nb0[NB], nb1[NB];
-    if (k + 64 < k1) load(k + 64, na0, na1, nb0, nb1);
-#pragma unroll
-    for (int j = 0; j < NB; j++) {
-      acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b0[j], acc[j], 0, 0, 0);
-      acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b1[j], acc[j], 0, 0, 0);
-    }
-    if (k + 64 < k1) {
-      a0 = na0;
-      a1 = na1;
-#pragma unroll
-      for (int j = 0; j < NB; j++) {
-        b0[j] = nb0[j];
-        b1[j] = nb1[j];
-      }
-    }
-  }
-#pragma unroll
-  for (int j = 0; j < NB; j++) {
-    const int n = nt * 16 * NB + 16 * j + (lane & 15);
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const int t = mt * 16 + 4 * (lane >> 4) + i;
-      if (t < T) part[((size_t)sp * T + t) * N + n] = acc[j][i];
-    }
-  }
 }
 
 // The work after the q/k/v projection for one (token, head) of the 32 q/k/v heads, one wave,
@@ -1370,7 +1299,7 @@ __global__ void __launch_bounds__(256) keys_reduce(const unsigned long long* __r
 //   gemm_rows(down)          epilogue: residual add
 //
 // gemm_rows: one workgroup of 16 waves per 16*NB-column tile; wave w takes
-// K/16 of the K range (the same MFMA operand layout as gemm_partial) and the
+// K/16 of the K range (the MFMA operand layout above) and the
 // 16 partial tiles are summed in LDS in wave order, so every column is one
 // fp32 sum rounded once, with no partials in memory and no finish kernel.
 
@@ -1807,7 +1736,7 @@ __global__ void __launch_bounds__(256) attention_merge(const Tok* __restrict__ t
 // ---------------------------------------------------------------- self-test
 
 // C[16][16] = A[16][32] . B[16][32]^T through one MFMA with the operand
-// layouts gemm_partial assumes.
+// layouts the GEMMs assume.
 __global__ void mfma_selftest(const uint16_t* A, const uint16_t* B, float* C) {
   const int lane = threadIdx.x, kq = 8 * (lane >> 4);
   const bf16x8 a = ld_bf16x8(A + (lane & 15) * 32 + kq);
@@ -1821,16 +1750,25 @@ __global__ void mfma_selftest(const uint16_t* A, const uint16_t* B, float* C) {
 // ---------------------------------------------------------------- host side
 
 struct Gemm {
-  int nb, ksplit, tn;  // nb = 0: LDS-tiled with tile width tn
+  int ksplit, tn;  // K splits, tile width (128 or 64 columns)
 };
 
-// 64-column tiles (16 for N not a multiple of 64); the K range is split
-// (up to kMaxSplit ways, >= 64 K per wave) until about kTargetWaves waves
-// stream the weights.
-bool use_tiled(int T, int N, int K) { return T >= 96 && N % 128 == 0 && K % (4 * kTK) == 0; }
+// Every projection of both models takes the LDS-tiled GEMM at any token count: N a multiple of the
+// 128-column tile and K a multiple of four 64-wide steps.  (A register-staged MFMA GEMM, one wave
+// per 16-row tile, ran below 96 tokens before; the tiled kernel on a 128-row tile whose rows past
+// T repeat the last one was faster at every count measured: 4 tokens 1.55 -> 1.34 ms per 0.6B
+// prefill, 64 tokens 2.09 -> 1.55, 80 tokens 2.43 -> 1.65.)
+template <class M>
+constexpr bool tiled_shapes() {
+  using Dm = Dims<M>;
+  constexpr int kStep4 = 4 * kTK;
+  return kNQKV % 128 == 0 && Dm::H % 128 == 0 && (2 * Dm::I) % 128 == 0 && Dm::H % kStep4 == 0 &&
+         kQS % kStep4 == 0 && Dm::I % kStep4 == 0;
+}
+static_assert(tiled_shapes<Qwen3_0_6B>() && tiled_shapes<Qwen3_1_7B>(), "projection shapes of the tiled GEMM");
 
-// Tiled, 128-column tiles: K split (at most 8 ways, >= 4 steps of 64 each)
-// until about 512 workgroups run, two per CU.
+// 128-column tiles: K split (at most 8 ways, >= 4 steps of 64 each) until about 512 workgroups
+// run, two per CU.
 int tiled_splits(int T, int N, int K) {
   const long long tiles = (long long)((T + kTM - 1) / kTM) * (N / 128);
   int ks = 1;
@@ -1838,45 +1776,36 @@ int tiled_splits(int T, int N, int K) {
   return ks;
 }
 
-// Tiled, 64-column tiles, for problems whose 128-column plan leaves CUs idle
-// (narrow N at a few hundred rows): K split (at most 16 ways, >= 2 steps of
-// 64 each) until 256 workgroups run, while the fp32 partials
-// (ksplit * T * N * 4 bytes) stay within twice the weight bytes (N * K * 2).
+// 64-column tiles, for problems whose 128-column plan leaves CUs idle (narrow N at a few hundred
+// rows or fewer): K split (at most 16 ways, >= 2 steps of 64 each) until 256 workgroups run,
+// while the fp32 partials (ksplit * T * N * 4 bytes) stay within twice the weight bytes (N * K * 2).
 int narrow_splits(int T, int N, int K) {
   const long long tiles = (long long)((T + kTM - 1) / kTM) * (N / 64);
   int ks = 1;
-  while (tiles * ks < 256 && ks * 2 <= 16 && K % (ks * 2 * kTK) == 0 && K / (ks * 2) >= 2 * kTK &&
+  while (tiles * ks < 256 && ks * 2 <= kMaxSplit && K % (ks * 2 * kTK) == 0 && K / (ks * 2) >= 2 * kTK &&
          (long long)ks * 2 * T * 4 <= 2LL * K * 2)
     ks *= 2;
   return ks;
 }
 
 Gemm plan_gemm(int T, int N, int K) {
-  if (use_tiled(T, N, K)) {
-    const int ks = tiled_splits(T, N, K);
-    const long long wgs = (long long)((T + kTM - 1) / kTM) * (N / 128) * ks;
-    if (wgs >= 256) return {0, ks, 128};
-    const int ks64 = narrow_splits(T, N, K);
-    if ((long long)((T + kTM - 1) / kTM) * (N / 64) * ks64 > wgs) return {0, ks64, 64};
-    return {0, ks, 128};
-  }
-  const int mt = (T + 15) / 16;
-  const int nb = N % 64 == 0 ? 4 : 1;
-  int ks = 1;
-  while ((long long)mt * (N / (16 * nb)) * ks < kTargetWaves && ks * 2 <= kMaxSplit && K % (ks * 2 * 64) == 0)
-    ks *= 2;
-  return {nb, ks, 0};
+  const int ks = tiled_splits(T, N, K);
+  const long long wgs = (long long)((T + kTM - 1) / kTM) * (N / 128) * ks;
+  if (wgs >= 256) return {ks, 128};
+  const int ks64 = narrow_splits(T, N, K);
+  if ((long long)((T + kTM - 1) / kTM) * (N / 64) * ks64 > wgs) return {ks64, 64};
+  return {ks, 128};
 }
 
 // The q/k/v and gate/up GEMMs with their finishing work in the epilogue (kEpiQkv, kEpiGateUp)
-// when the LDS-tiled plan can leave K unsplit: 128-column tiles filling at least one workgroup
-// per CU.  Then no fp32 sums go to memory and no finishing kernel runs; *ks_out = 0 says so.
-// Otherwise the sums go to part and *ks_out is the split count for the finishing kernel.
-void launch_gemm(const uint16_t* X, const int* rows, int T, int K, const Seg& seg, int N, float* part, hipStream_t s,
-                 int* ks_out, int epi = kEpiPart, const QkvOut* qo = nullptr, const GateUpOut* go = nullptr) {
+// when the plan can leave K unsplit: 128-column tiles filling at least one workgroup per CU.
+// Then no fp32 sums go to memory and no finishing kernel runs; *ks_out = 0 says so.  Otherwise
+// the sums go to part and *ks_out is the split count for the finishing kernel.
+void launch_gemm(const uint16_t* X, int T, int K, const Seg& seg, int N, float* part, hipStream_t s, int* ks_out,
+                 int epi = kEpiPart, const QkvOut* qo = nullptr, const GateUpOut* go = nullptr) {
   const QkvOut q0 = qo ? *qo : QkvOut{};
   const GateUpOut g0 = go ? *go : GateUpOut{};
-  if (epi != kEpiPart && !rows && use_tiled(T, N, K) && (long long)((T + kTM - 1) / kTM) * (N / 128) >= kNumWG) {
+  if (epi != kEpiPart && (long long)((T + kTM - 1) / kTM) * (N / 128) >= kNumWG) {
     const dim3 grid(N / 128, (T + kTM - 1) / kTM, 1);
     if (epi == kEpiQkv)
       hipLaunchKernelGGL((gemm_tiled<128, kEpiQkv>), grid, dim3(256), 0, s, X, T, K, seg, N, 1, part, q0, g0);
@@ -1886,30 +1815,11 @@ void launch_gemm(const uint16_t* X, const int* rows, int T, int K, const Seg& se
     return;
   }
   const Gemm g = plan_gemm(T, N, K);
-  if (g.nb == 0) {  // LDS-tiled
-    const dim3 grid(N / g.tn, (T + kTM - 1) / kTM, g.ksplit);
-    if (g.tn == 128)
-      hipLaunchKernelGGL((gemm_tiled<128, kEpiPart>), grid, dim3(256), 0, s, X, T, K, seg, N, g.ksplit, part, q0, g0);
-    else
-      hipLaunchKernelGGL((gemm_tiled<64, kEpiPart>), grid, dim3(256), 0, s, X, T, K, seg, N, g.ksplit, part, q0, g0);
-    *ks_out = g.ksplit;
-    return;
-  }
-  const int mt = (T + 15) / 16;
-  const long long waves = (long long)mt * (N / (16 * g.nb)) * g.ksplit;
-  const dim3 grid((unsigned)((waves + 3) / 4));
-  const bool stream = mt == 1;  // each weight tile is read once: bypass the caches
-  if (g.nb == 4) {
-    if (stream)
-      hipLaunchKernelGGL((gemm_partial<4, true>), grid, dim3(256), 0, s, X, rows, T, K, seg, N, g.ksplit, part);
-    else
-      hipLaunchKernelGGL((gemm_partial<4, false>), grid, dim3(256), 0, s, X, rows, T, K, seg, N, g.ksplit, part);
-  } else {
-    if (stream)
-      hipLaunchKernelGGL((gemm_partial<1, true>), grid, dim3(256), 0, s, X, rows, T, K, seg, N, g.ksplit, part);
-    else
-      hipLaunchKernelGGL((gemm_partial<1, false>), grid, dim3(256), 0, s, X, rows, T, K, seg, N, g.ksplit, part);
-  }
+  const dim3 grid(N / g.tn, (T + kTM - 1) / kTM, g.ksplit);
+  if (g.tn == 128)
+    hipLaunchKernelGGL((gemm_tiled<128, kEpiPart>), grid, dim3(256), 0, s, X, T, K, seg, N, g.ksplit, part, q0, g0);
+  else
+    hipLaunchKernelGGL((gemm_tiled<64, kEpiPart>), grid, dim3(256), 0, s, X, T, K, seg, N, g.ksplit, part, q0, g0);
   *ks_out = g.ksplit;
 }
 
@@ -2123,7 +2033,7 @@ int forward(const Args& a, hipStream_t s) {
     const LDGLayerWeights& w = a.layers[L];
     const Seg qkv{{u16(w.q_proj_weight), u16(w.k_proj_weight), u16(w.v_proj_weight)}, {kQS, kNKV * kD, kNKV * kD}};
     const QkvOut qo{tok, L, u16(w.q_norm_weight), u16(w.k_norm_weight), a.cos_t, a.sin_t, a.cache, eps, Qb};
-    launch_gemm(N, nullptr, T, Dm::H, qkv, kNQKV, part, s, &ks, kEpiQkv, &qo);
+    launch_gemm(N, T, Dm::H, qkv, kNQKV, part, s, &ks, kEpiQkv, &qo);
     if (ks) hipLaunchKernelGGL(qkv_finish, dim3(T, kNQ + 2 * kNKV), dim3(64), 0, s, part, ks, T, qo);
     if (split) {
       float* scores = reinterpret_cast<float*>(a.ws + l.scores);
@@ -2149,15 +2059,15 @@ int forward(const Args& a, hipStream_t s) {
       }
     }
     const Seg o{{u16(w.o_proj_weight), nullptr, nullptr}, {Dm::H, 0, 0}};
-    launch_gemm(ATT, nullptr, T, kQS, o, Dm::H, part, s, &ks);
+    launch_gemm(ATT, T, kQS, o, Dm::H, part, s, &ks);
     hipLaunchKernelGGL((residual_norm<Dm::H>), dim3(T), dim3(256), 0, s, part, ks, T, X,
                        u16(w.post_attn_layernorm_weight), eps, N);
     const Seg gu{{u16(w.gate_proj_weight), u16(w.up_proj_weight), nullptr}, {Dm::I, Dm::I, 0}};
     const GateUpOut go{MM, Dm::I};
-    launch_gemm(N, nullptr, T, Dm::H, gu, 2 * Dm::I, part, s, &ks, kEpiGateUp, nullptr, &go);
+    launch_gemm(N, T, Dm::H, gu, 2 * Dm::I, part, s, &ks, kEpiGateUp, nullptr, &go);
     if (ks) hipLaunchKernelGGL(gate_up_finish, blocks((size_t)T * Dm::I), dim3(256), 0, s, part, ks, T, Dm::I, MM);
     const Seg dn{{u16(w.down_proj_weight), nullptr, nullptr}, {Dm::H, 0, 0}};
-    launch_gemm(MM, nullptr, T, Dm::I, dn, Dm::H, part, s, &ks);
+    launch_gemm(MM, T, Dm::I, dn, Dm::H, part, s, &ks);
     const uint16_t* next_norm = L + 1 < a.num_layers ? u16(a.layers[L + 1].input_layernorm_weight) : a.final_norm;
     hipLaunchKernelGGL((residual_norm<Dm::H>), dim3(T), dim3(256), 0, s, part, ks, T, X, next_norm, eps, N);
   }

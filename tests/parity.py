@@ -229,6 +229,28 @@ def stream_envelopes(forc, k_cache, v_cache, p0: int, feed, ref_rows: torch.Tens
             for i in range(len(feed))]
 
 
+def lazy_envelopes(weights, shape, max_seq_len: int, k_cache, v_cache, p0: int, feed, ref_rows: torch.Tensor,
+                   num_layers: int | None = None):
+    """``stream_envelopes`` with the fp32 restatement on CPU ``weights`` built on first use (most
+    streams leave the oracle's argmax nowhere, and then no envelope is computed)."""
+    box = []
+
+    def forc():
+        if not box:
+            box.append(fp32_oracle(weights, shape, max_seq_len, num_layers=num_layers))
+        return box[0]
+
+    return [(lambda i=i: envelope(forc(), k_cache, v_cache, p0 + i, [feed[i]], ref_rows[i:i + 1])[0])
+            for i in range(len(feed))]
+
+
+def history_envelopes(weights, shape, max_seq_len: int, k_cache, v_cache, prompt, generated, ref_rows: torch.Tensor):
+    """Lazy envelopes of the rows ``stream_rows`` gives for ``generated`` after ``prompt``."""
+    seq = list(prompt) + list(generated[:-1])
+    n0 = len(prompt) - 1
+    return lazy_envelopes(weights, shape, max_seq_len, k_cache, v_cache, n0, seq[n0:], ref_rows)
+
+
 def exact_oracle(ew, shape, max_seq_len: int, num_layers: int | None = None, kv=None, cache_len: int = 0):
     """A fresh exact oracle on shared float64 weights ``ew``, RoPE tables long enough for
     ``max_seq_len``, optionally with injected cache contents ``kv = (k, v)`` of ``cache_len``."""

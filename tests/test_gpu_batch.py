@@ -14,7 +14,7 @@ import pytest
 import torch
 
 from parity import (LAYERS28, LITERAL, Tally, check_kv_rows, check_row, check_rows, decoder, exact_oracle, fp32_oracle,
-                    oracle_steps, stream_envelopes, stream_rows, with_rope)
+                    history_envelopes, lazy_envelopes, oracle_steps, stream_envelopes, stream_rows, with_rope)
 
 pytestmark = pytest.mark.gpu
 
@@ -52,8 +52,9 @@ def test_mfma_operand_layout():
 
 
 @pytest.mark.parametrize("n", [12, 40], ids=["12tok-split-attention", "40tok-rowwise-attention"])
-def test_prefill_all_rows_match_oracle(shape, exact06, weights_gpu, n):
-    """Every row of a 28-layer prefill against the oracle's row at that position; K/V written alike."""
+def test_prefill_all_rows_match_oracle(shape, exact06, weights_cpu, weights_gpu, n):
+    """Every row of a 28-layer prefill against the oracle's row at that position (a token departure
+    beyond one ulp only within the row's fp32 envelope); K/V written alike."""
     from qwen_megakernel.weights import make_prompt
 
     ids = make_prompt(n, shape.vocab, seed=3)
@@ -61,13 +62,15 @@ def test_prefill_all_rows_match_oracle(shape, exact06, weights_gpu, n):
     toks, logits = _forward_rows(dec._forward, ids, 0, dec._k_cache, dec._v_cache)
     orc = exact_oracle(exact06, shape, 2048)
     ref = oracle_steps(orc, dec._k_cache, dec._v_cache, 0, ids)
-    print(check_rows(Tally(f"prefill {n} rows"), ref, toks, logits, bar=LAYERS28))
+    envs = lazy_envelopes(weights_cpu, shape, 2048, dec._k_cache, dec._v_cache, 0, ids, ref)
+    print(check_rows(Tally(f"prefill {n} rows"), ref, toks, logits, bar=LAYERS28, envs=envs))
     check_kv_rows(f"prefill {n} rows", orc, dec._k_cache, dec._v_cache, 0, n)
 
 
-def test_prefill_then_decode_kernel(shape, exact06, weights_gpu):
+def test_prefill_then_decode_kernel(shape, exact06, weights_cpu, weights_gpu):
     """Decoder.prefill writes a cache the decode megakernel continues from: the prefill's last row
-    and 12 decode steps on the decoder's own tokens against the oracle."""
+    and 12 decode steps on the decoder's own tokens against the oracle (a token departure beyond
+    one ulp only within the step's fp32 envelope)."""
     from qwen_megakernel.weights import make_prompt
 
     prompt = make_prompt(24, shape.vocab, seed=5)
@@ -81,11 +84,12 @@ def test_prefill_then_decode_kernel(shape, exact06, weights_gpu):
         lgs.append(lg.cpu())
     orc = exact_oracle(exact06, shape, 2048)
     ref = stream_rows(orc, dec._k_cache, dec._v_cache, prompt, toks)
-    print(check_rows(Tally("prefill + decode"), ref, toks, torch.stack(lgs), bar=LAYERS28))
+    envs = history_envelopes(weights_cpu, shape, 2048, dec._k_cache, dec._v_cache, prompt, toks, ref)
+    print(check_rows(Tally("prefill + decode"), ref, toks, torch.stack(lgs), bar=LAYERS28, envs=envs))
     check_kv_rows("prefill + decode", orc, dec._k_cache, dec._v_cache, 0, len(prompt) + 11)
 
 
-def test_generate_with_prefill_matches_oracle_stream(shape, exact06, weights_gpu):
+def test_generate_with_prefill_matches_oracle_stream(shape, exact06, weights_cpu, weights_gpu):
     """generate() feeds the prompt through prefill by default (use_prefill=False: one decode step per
     prompt token, as the reference); both streams are the oracle's up to near-ties."""
     from qwen_megakernel.weights import make_prompt
@@ -95,7 +99,8 @@ def test_generate_with_prefill_matches_oracle_stream(shape, exact06, weights_gpu
         dec = decoder(weights_gpu, use_prefill=use_prefill)
         out = dec.generate(prompt, 24)
         ref = stream_rows(exact_oracle(exact06, shape, 2048), dec._k_cache, dec._v_cache, prompt, out)
-        print(check_rows(Tally(f"generate use_prefill={use_prefill}"), ref, out, bar=LAYERS28))
+        envs = history_envelopes(weights_cpu, shape, 2048, dec._k_cache, dec._v_cache, prompt, out, ref)
+        print(check_rows(Tally(f"generate use_prefill={use_prefill}"), ref, out, bar=LAYERS28, envs=envs))
 
 
 @pytest.fixture(scope="module")
@@ -105,9 +110,10 @@ def batch_prompts(shape):
     return [make_prompt(n, shape.vocab, seed=10 + b) for b, n in enumerate([5, 17, 33, 9])]
 
 
-def test_batch_decode_matches_oracle(shape, exact06, weights_gpu, batch_prompts):
+def test_batch_decode_matches_oracle(shape, exact06, weights_cpu, weights_gpu, batch_prompts):
     """BatchDecoder: per-sequence prefill, then 10 batched steps, each sequence on its own tokens at
-    its own position; every sequence's rows against its own oracle."""
+    its own position; every sequence's rows against its own oracle (a token departure beyond one
+    ulp only within the step's fp32 envelope)."""
     from qwen_megakernel.model import BatchDecoder
 
     prompts = batch_prompts
@@ -126,7 +132,9 @@ def test_batch_decode_matches_oracle(shape, exact06, weights_gpu, batch_prompts)
     for b in range(4):
         orc = exact_oracle(exact06, shape, 2048)
         ref = stream_rows(orc, bd._k_cache[b], bd._v_cache[b], prompts[b], toks[b])
-        print(check_rows(Tally(f"batched decode sequence {b}"), ref, toks[b], torch.stack(lgs[b]), bar=LAYERS28))
+        envs = history_envelopes(weights_cpu, shape, 2048, bd._k_cache[b], bd._v_cache[b], prompts[b], toks[b], ref)
+        print(check_rows(Tally(f"batched decode sequence {b}"), ref, toks[b], torch.stack(lgs[b]), bar=LAYERS28,
+                         envs=envs))
         check_kv_rows(f"batched decode sequence {b}", orc, bd._k_cache[b], bd._v_cache[b], 0, len(prompts[b]) + 10)
 
 
@@ -164,8 +172,9 @@ def test_decode_batch_multi_launch_28_layers_long_prompts(shape, exact06, weight
                          toks[b], torch.stack(lgs[b]), bar=LAYERS28, envs=envs))
 
 
-def test_batch_generate_matches_oracle_streams(shape, exact06, weights_gpu, batch_prompts):
-    """Device-fed batched generation: every sequence's stream is its oracle's up to near-ties."""
+def test_batch_generate_matches_oracle_streams(shape, exact06, weights_cpu, weights_gpu, batch_prompts):
+    """Device-fed batched generation: every sequence's stream is its oracle's up to near-ties (a
+    token departure beyond one ulp only within the step's fp32 envelope)."""
     from qwen_megakernel.model import BatchDecoder
 
     prompts = batch_prompts
@@ -173,7 +182,8 @@ def test_batch_generate_matches_oracle_streams(shape, exact06, weights_gpu, batc
     out = bd.generate_ids(prompts, 11)
     for b in range(4):
         ref = stream_rows(exact_oracle(exact06, shape, 2048), bd._k_cache[b], bd._v_cache[b], prompts[b], out[b])
-        check_rows(Tally(f"batched generate sequence {b}"), ref, out[b], bar=LAYERS28)
+        envs = history_envelopes(weights_cpu, shape, 2048, bd._k_cache[b], bd._v_cache[b], prompts[b], out[b], ref)
+        check_rows(Tally(f"batched generate sequence {b}"), ref, out[b], bar=LAYERS28, envs=envs)
     assert bd.positions == [len(p) + 10 for p in prompts]
 
 

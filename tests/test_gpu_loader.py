@@ -15,8 +15,8 @@ import os
 import pytest
 import torch
 
-from parity import (LAYERS28, Tally, check_kv_rows, check_rows, decoder, exact_oracle, kernel_stream, oracle_steps,
-                    stream_rows)
+from parity import (LAYERS28, Tally, check_kv_rows, check_rows, decoder, exact_oracle, history_envelopes, kernel_stream,
+                    lazy_envelopes, oracle_steps, stream_rows)
 
 pytestmark = pytest.mark.gpu
 
@@ -78,7 +78,8 @@ def test_loaded_checkpoint_untied_head_decode_and_batched(monkeypatch, shape, ch
     feed, toks, lgs = kernel_stream(kd, prompt, 16)
     orc = exact_oracle(ew, shape, 256)
     ref = oracle_steps(orc, kd._k_cache, kd._v_cache, 0, feed)
-    print(check_rows(Tally("loaded checkpoint, decode kernel"), ref, toks, lgs, bar=LAYERS28))
+    envs = lazy_envelopes(w_ref, shape, 256, kd._k_cache, kd._v_cache, 0, feed, ref)
+    print(check_rows(Tally("loaded checkpoint, decode kernel"), ref, toks, lgs, bar=LAYERS28, envs=envs))
     check_kv_rows("loaded checkpoint", orc, kd._k_cache, kd._v_cache, 0, len(feed))
     # the check has teeth: an oracle with the embedding as its head is far from the kernel
     wrong_head = exact_oracle(ew, shape, 256)
@@ -91,7 +92,8 @@ def test_loaded_checkpoint_untied_head_decode_and_batched(monkeypatch, shape, ch
     tok0, lg0 = dec.prefill(prompt, return_logits=True)
     t = Tally("loaded checkpoint, batched path")
     pre = oracle_steps(exact_oracle(ew, shape, 256), dec._k_cache, dec._v_cache, 0, prompt, emit=[len(prompt) - 1])
-    check_rows(t, pre, [tok0], lg0[None].cpu(), bar=LAYERS28)
+    envs = lazy_envelopes(w_ref, shape, 256, dec._k_cache, dec._v_cache, len(prompt) - 1, prompt[-1:], pre)
+    check_rows(t, pre, [tok0], lg0[None].cpu(), bar=LAYERS28, envs=envs)
     bd = BatchDecoder(weights=w, batch_size=2, max_seq_len=256, verbose=False)
     prompts = [prompt, make_prompt(7, shape.vocab, seed=4)]
     first = bd.prefill_all(prompts)
@@ -103,5 +105,6 @@ def test_loaded_checkpoint_untied_head_decode_and_batched(monkeypatch, shape, ch
             lgs2[b].append(logits[b].cpu())
     for b in range(2):
         rows = stream_rows(exact_oracle(ew, shape, 256), bd._k_cache[b], bd._v_cache[b], prompts[b], gen[b])
-        check_rows(t, rows[1:], gen[b][1:], torch.stack(lgs2[b]), bar=LAYERS28)
+        envs = history_envelopes(w_ref, shape, 256, bd._k_cache[b], bd._v_cache[b], prompts[b], gen[b], rows)[1:]
+        check_rows(t, rows[1:], gen[b][1:], torch.stack(lgs2[b]), bar=LAYERS28, envs=envs)
     print(t)
