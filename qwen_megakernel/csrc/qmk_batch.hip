@@ -43,7 +43,8 @@ constexpr int kQT = 64, kKB = 64, kKPad = kD + 8, kVPad = kKB + 8;  // MFMA pref
 constexpr int kMfmaAttnTokens = 320;   // prompts of this many tokens run attention_mfma
 constexpr int kMfmaAttnContext = 1024; // so do fewer tokens over this many positions of context
 constexpr int kSplitChunk = 64;   // split attention: positions per workgroup
-constexpr int kSplitBelow = 32;   // fewer tokens than this use the split attention
+constexpr int kSplitBelow = 32;   // fewer tokens than this use the split attention ...
+constexpr int kSplitContext = 128;  // ... over more than this many positions of context
 constexpr int kMaxSplit = 16;     // K splits of one GEMM (their partials are summed in a fixed order)
 constexpr int kMaxEmit = 256;
 
@@ -1827,6 +1828,12 @@ size_t part_floats(int T, int N, int K) { return (size_t)plan_gemm(T, N, K).kspl
 
 int split_chunks(int max_context) { return (max_context + kSplitChunk - 1) / kSplitChunk; }
 
+// The context-split attention (three launches) for few tokens over a long context; the row kernel
+// (one launch) for few tokens over a short one.  Qwen3-0.6B prefills, split against rows, same box:
+// from position 0, 1 token 1.31 / 1.21 ms and 31 tokens 1.45 / 1.35; from 96, 1.41 / 1.39; from
+// 192, 1.46 / 1.56; from 500, 1.45 / 2.14.
+bool split_attention(int T, int max_context) { return T < kSplitBelow && max_context > kSplitContext; }
+
 struct Layout {
   size_t tok, erow, keys, x, n, q, att, m, qkv, apart, part, scores, ml, pv, redo, total;
 };
@@ -1866,7 +1873,7 @@ Layout layout(int T, int R, int max_context, bool one_per_seq = false) {
   pf = std::max(pf, part_floats(T, 2 * Dm::I, Dm::H));
   pf = std::max(pf, part_floats(T, Dm::H, Dm::I));
   take(l.part, pf * 4);
-  if (T < kSplitBelow) {
+  if (split_attention(T, max_context)) {
     const int nch = split_chunks(max_context);
     take(l.scores, (size_t)T * kNQ * nch * kSplitChunk * 4);
     take(l.ml, (size_t)T * kNQ * nch * 8);
@@ -2013,7 +2020,7 @@ int forward(const Args& a, hipStream_t s) {
   uint16_t* MM = reinterpret_cast<uint16_t*>(a.ws + l.m);
   float* part = reinterpret_cast<float*>(a.ws + l.part);
   const float eps = 1e-6f;
-  const bool split = T < kSplitBelow;
+  const bool split = split_attention(T, a.max_context);
   const int nch = split ? split_chunks(a.max_context) : 0;
   // attention_mfma pays off from about 320 tokens or 1024 positions of context (below that the
   // row kernel's per-token reads are cheaper than its passes).  Measured 0.6B prefills, row

@@ -51,20 +51,25 @@ def test_mfma_operand_layout():
     assert err <= 1e-4, f"MFMA layout/result mismatch: max abs {err}"
 
 
-@pytest.mark.parametrize("n", [12, 40], ids=["12tok-split-attention", "40tok-rowwise-attention"])
-def test_prefill_all_rows_match_oracle(shape, exact06, weights_cpu, weights_gpu, n):
-    """Every row of a 28-layer prefill against the oracle's row at that position (a token departure
-    beyond one ulp only within the row's fp32 envelope); K/V written alike."""
+@pytest.mark.parametrize("n,start", [(12, 0), (40, 0), (12, 200)],
+                         ids=["12tok-rowwise-attention", "40tok-rowwise-attention", "12tok-after-200-split-attention"])
+def test_prefill_all_rows_match_oracle(shape, exact06, weights_cpu, weights_gpu, n, start):
+    """Every row of a 28-layer prefill at positions start.. against the oracle's row at that
+    position (a token departure beyond one ulp only within the row's fp32 envelope); K/V written
+    alike.  Fewer than 32 tokens take the row attention over at most 128 positions of context and
+    the context-split attention beyond; the first `start` positions come from an earlier prefill."""
     from qwen_megakernel.weights import make_prompt
 
     ids = make_prompt(n, shape.vocab, seed=3)
     dec = decoder(weights_gpu)
-    toks, logits = _forward_rows(dec._forward, ids, 0, dec._k_cache, dec._v_cache)
+    if start:
+        dec.prefill(make_prompt(start, shape.vocab, seed=4))
+    toks, logits = _forward_rows(dec._forward, ids, start, dec._k_cache, dec._v_cache)
     orc = exact_oracle(exact06, shape, 2048)
-    ref = oracle_steps(orc, dec._k_cache, dec._v_cache, 0, ids)
-    envs = lazy_envelopes(weights_cpu, shape, 2048, dec._k_cache, dec._v_cache, 0, ids, ref)
-    print(check_rows(Tally(f"prefill {n} rows"), ref, toks, logits, bar=LAYERS28, envs=envs))
-    check_kv_rows(f"prefill {n} rows", orc, dec._k_cache, dec._v_cache, 0, n)
+    ref = oracle_steps(orc, dec._k_cache, dec._v_cache, start, ids)
+    envs = lazy_envelopes(weights_cpu, shape, 2048, dec._k_cache, dec._v_cache, start, ids, ref)
+    print(check_rows(Tally(f"prefill {n} rows at {start}"), ref, toks, logits, bar=LAYERS28, envs=envs))
+    check_kv_rows(f"prefill {n} rows at {start}", orc, dec._k_cache, dec._v_cache, start, n)
 
 
 def test_prefill_then_decode_kernel(shape, exact06, weights_cpu, weights_gpu):
@@ -275,10 +280,10 @@ def test_prefill_all_matches_per_sequence_prefill(shape, weights_gpu):
         check_row(t, ("step", b), l2[b].cpu(), s1[b], l1[b], bar=LAYERS28)
 
 
-@pytest.mark.parametrize("n", [8, 40], ids=["8tok-split", "40tok-rowwise"])
+@pytest.mark.parametrize("n", [8, 40], ids=["8tok-split", "40tok-mfma"])
 def test_long_context_prefill(shape, exact06, weights_gpu, n):
-    """Prefill after an injected N(0,1) cache of 2100 positions: the row-wise attention takes two
-    2048-position chunks (scores recomputed per pass), the split attention 34 workgroups per head."""
+    """Prefill after an injected N(0,1) cache of 2100 positions: 8 tokens take the split attention
+    (34 workgroups per head), 40 tokens the MFMA attention (more than 1024 positions of context)."""
     from qwen_megakernel.weights import make_kv_prefill, make_prompt
 
     c0, layers = 2100, 2
@@ -292,6 +297,42 @@ def test_long_context_prefill(shape, exact06, weights_gpu, n):
     ref = oracle_steps(orc, dec._k_cache, dec._v_cache, c0, ids)
     print(check_rows(Tally(f"long-context prefill {n} rows after {c0}"), ref, toks, logits, bar=LITERAL))
     check_kv_rows(f"long-context prefill {n}", orc, dec._k_cache, dec._v_cache, c0, n)
+
+
+def test_long_context_prefill_rows_two_sequences(shape, exact06, weights_gpu):
+    """Two sequences of 20 tokens each after injected N(0,1) caches of 2100 and 2060 positions, in
+    one forward with their tokens interleaved: no 64-token tile is one sequence, so every row takes
+    the row attention, which covers the contexts in two 2048-position chunks (scores recomputed per
+    pass).  Every row against its sequence's oracle."""
+    from dataclasses import replace
+
+    from qwen_megakernel.model import BatchDecoder
+    from qwen_megakernel.weights import make_kv_prefill, make_prompt
+
+    c0s, layers, n = (2100, 2060), 2, 20
+    max_seq = max(c0s) + 64
+    bd = BatchDecoder(weights=with_rope(weights_gpu, max_seq, "cuda"), batch_size=2, max_seq_len=max_seq,
+                      num_layers=layers, verbose=False)
+    kvs = [make_kv_prefill(replace(shape, num_layers=layers), c, seed=20 + b) for b, c in enumerate(c0s)]
+    for b, (k, v) in enumerate(kvs):
+        bd.load_kv(b, k.cuda(), v.cuda(), c0s[b])
+    ids = [make_prompt(n, shape.vocab, seed=30 + b) for b in range(2)]
+    toks = [ids[i % 2][i // 2] for i in range(2 * n)]
+    seqs = [i % 2 for i in range(2 * n)]
+    pos = [c0s[i % 2] + i // 2 for i in range(2 * n)]
+    out = torch.empty(2 * n, dtype=torch.int32, device="cuda")
+    logits = torch.empty(2 * n, V, dtype=torch.float32, device="cuda")
+    bd._forward(_i32(toks), _i32(seqs), _i32(pos), _i32(range(2 * n)), out, logits, bd._k_cache, bd._v_cache,
+                max(c0s) + n)
+    got, lg = out.cpu().tolist(), logits.cpu()
+    t = Tally(f"two sequences x {n} rows after {c0s}")
+    for b in range(2):
+        orc = exact_oracle(exact06, shape, max_seq, num_layers=layers)
+        ref = oracle_steps(orc, bd._k_cache[b], bd._v_cache[b], c0s[b], ids[b])
+        rows = list(range(b, 2 * n, 2))
+        check_rows(t, ref, [got[r] for r in rows], lg[rows], bar=LITERAL)
+        check_kv_rows(f"two sequences, sequence {b}", orc, bd._k_cache[b], bd._v_cache[b], c0s[b], n)
+    print(t)
 
 
 def test_random_norm_weights_prefill(shape):
