@@ -32,7 +32,8 @@ device-fed greedy steps at batch 1 on the decode megakernel (context
 four and algorithmic GB/s per step (weights once + each sequence's KV).
 
 ``prefill``: the 128-token prompt through the batched forward, ms and tok/s;
-``prefill_long``: a 2048-token prompt the same way (its attention on MFMA).
+``prefill_long``: a 2048-token prompt the same way (its attention on MFMA);
+``prefill_lens`` (only with ``--prefill-lens 4,32,...``): prompts of those lengths.
 ``context_1024``: the decode rate at exactly 1024 positions of context (a
 1023-token prompt prefilled, then 512 decode launches at position 1023).
 
@@ -425,6 +426,7 @@ def main():
     ap.add_argument("--copy-calibration", action="store_true")
     ap.add_argument("--no-sampling", action="store_true")
     ap.add_argument("--sample-steps", type=int, default=512)
+    ap.add_argument("--prefill-lens", default="", help="comma-separated prompt lengths to time prefill at as well")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (this path does not shard "
@@ -537,6 +539,8 @@ def main():
     result["context_1024"] = context_1024_rate(w)
     result["prefill"] = prefill_rate(w)
     result["prefill_long"] = prefill_rate(w, 2048, iters=5)
+    if args.prefill_lens:
+        result["prefill_lens"] = [prefill_rate(w, int(n)) for n in args.prefill_lens.split(",")]
     if not args.no_long_context:
         result["long_context"] = long_context(w, args.long_steps, phase_trace=args.phase_trace)
     del w
