@@ -335,6 +335,26 @@ def test_long_context_prefill_rows_two_sequences(shape, exact06, weights_gpu):
     print(t)
 
 
+@pytest.mark.parametrize("n,start", [(1, 0), (2, 0), (3, 0), (1, 150), (3, 150)],
+                         ids=["1tok", "2tok", "3tok", "1tok-after-150", "3tok-after-150"])
+def test_prefill_few_tokens(shape, exact06, weights_gpu, n, start):
+    """Prompts of 1-3 tokens, 4 layers: the tiled GEMM's 128-row tile almost all repeats of the last
+    row (rows past T), the row attention from position 0 and the split attention after a
+    150-token prefix; every row against the oracle at the literal bar, and the K/V rows."""
+    from qwen_megakernel.weights import make_prompt
+
+    layers = 4
+    dec = decoder(weights_gpu, num_layers=layers)
+    if start:
+        dec.prefill(make_prompt(start, shape.vocab, seed=12))
+    ids = make_prompt(n, shape.vocab, seed=13 + n)
+    toks, logits = _forward_rows(dec._forward, ids, start, dec._k_cache, dec._v_cache)
+    orc = exact_oracle(exact06, shape, 2048, num_layers=layers)
+    ref = oracle_steps(orc, dec._k_cache, dec._v_cache, start, ids)
+    print(check_rows(Tally(f"{n}-token prefill at {start}"), ref, toks, logits, bar=LITERAL))
+    check_kv_rows(f"{n}-token prefill at {start}", orc, dec._k_cache, dec._v_cache, start, n)
+
+
 def test_random_norm_weights_prefill(shape):
     """Non-unit norm weights (q/k/input/post/final) so an ignored or misplaced norm fails."""
     from oracle.qwen3_exact import ExactOracle
