@@ -41,7 +41,7 @@ constexpr int kD = 128, kNQ = 16, kNKV = 8, kQS = kNQ * kD, kNQKV = (kNQ + 2 * k
 constexpr int kAttnChunk = 2048;  // one-kernel attention: scores of this many positions per LDS pass
 constexpr int kQT = 64, kKB = 64, kKPad = kD + 8, kVPad = kKB + 8;  // MFMA prefill attention tiles
 constexpr int kMfmaAttnTokens = 320;   // prompts of this many tokens run attention_mfma
-constexpr int kMfmaAttnContext = 1024; // so do fewer tokens over this many positions of context
+constexpr int kMfmaAttnContext = 256;  // so do fewer tokens over this many positions of context
 constexpr int kSplitChunk = 64;   // split attention: positions per workgroup
 constexpr int kSplitBelow = 32;   // fewer tokens than this use the split attention ...
 constexpr int kSplitContext = 128;  // ... over more than this many positions of context
@@ -740,10 +740,25 @@ __device__ __forceinline__ int attn_v_slot(int q) {
   return 32 * half + 8 * ((r & 15) >> 2) + 4 * (r >> 4) + (r & 3);
 }
 
+// Modes: kAttnFull runs both passes over a tile's whole context (pairs of tiles per workgroup, as
+// above).  For few tiles over a long context the keys are split into chunks of ck blocks, one
+// workgroup per (tile, chunk, query head): kAttnPass1 writes each row's (max, sum) of its chunk to
+// ml; kAttnPass2 takes every chunk's (max, sum) of its rows (in chunk order) for the global max M
+// and sum L, and writes its chunk's P@V partial (fp32) to part; attention_mfma_merge adds the
+// partials in chunk order.  Workgroups of chunks past a tile's last key do nothing.
+enum AttnMode : int { kAttnFull = 0, kAttnPass1 = 1, kAttnPass2 = 2 };
+
+// Index of (tile, head, chunk)'s row block in the split passes' ml and part buffers
+__device__ __forceinline__ size_t attn_chunk_row(int tile, int h, int nch, int chunk, int row) {
+  return (((size_t)tile * kNQ + h) * nch + chunk) * kQT + row;
+}
+
+template <int MODE>
 __global__ void __launch_bounds__(kAttnWaves * 64) attention_mfma(const uint16_t* __restrict__ Q,
                                                                  const Tok* __restrict__ tok, int T, int L, Cache c,
                                                                  float scale, uint16_t* __restrict__ out,
-                                                                 int* __restrict__ redo) {
+                                                                 int* __restrict__ redo, int nch, int ck,
+                                                                 float2* __restrict__ ml, float* __restrict__ part) {
   constexpr int NT = kAttnWaves * 64;
   static_assert(kQT == 64 && kKB == 64 && kAttnWaves == 8, "4 row groups of 16 x 2 key halves of 32");
   // K block [kKB][kKPad] and transposed V [kD][kVPad]; after the passes the same bytes hold the
@@ -763,7 +778,10 @@ __global__ void __launch_bounds__(kAttnWaves * 64) attention_mfma(const uint16_t
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63, l16 = lane & 15,
             lg = lane >> 4;
   const int rg = w >> 1, kh = w & 1;  // rows 16rg..16rg+15, keys 32kh..32kh+31 of each block
-  const int tiles[2] = {(int)blockIdx.x, nt - 1 - (int)blockIdx.x};
+  // kAttnFull: the pair (i, nt - 1 - i); the split passes: tile blockIdx.x / nch, chunk blockIdx.x % nch
+  const int tiles[2] = {MODE == kAttnFull ? (int)blockIdx.x : (int)blockIdx.x / nch,
+                        MODE == kAttnFull ? nt - 1 - (int)blockIdx.x : (int)blockIdx.x / nch};
+  const int chunk = MODE == kAttnFull ? 0 : (int)blockIdx.x % nch;
   const int ntile = tiles[1] == tiles[0] ? 1 : 2;
   // which of the pair's tiles are one sequence at consecutive positions
   if (threadIdx.x < 2) s_ok[threadIdx.x] = 1;
@@ -776,7 +794,8 @@ __global__ void __launch_bounds__(kAttnWaves * 64) attention_mfma(const uint16_t
     }
   }
   __syncthreads();
-  if (h == 0 && threadIdx.x < (unsigned)ntile) redo[tiles[threadIdx.x]] = s_ok[threadIdx.x] ? 0 : 1;
+  if (MODE != kAttnPass2 && h == 0 && chunk == 0 && threadIdx.x < (unsigned)ntile)
+    redo[tiles[threadIdx.x]] = s_ok[threadIdx.x] ? 0 : 1;
 
   for (int u = 0; u < ntile; u++) {
     if (!s_ok[u]) continue;  // uniform over the workgroup
@@ -795,6 +814,9 @@ __global__ void __launch_bounds__(kAttnWaves * 64) attention_mfma(const uint16_t
     const int wave_first = pos0 + 16 * rg;      // the wave's smallest row position
     const int wave_last = pos0 + 16 * rg + 15;  // the wave's largest row position
     const int nkb = (pmax + kKB) / kKB;         // blocks covering positions 0..pmax
+    // this workgroup's blocks: all of them, or its chunk's (none past the tile's last key)
+    const int kb0 = MODE == kAttnFull ? 0 : chunk * ck, kb1 = MODE == kAttnFull ? nkb : min(kb0 + ck, nkb);
+    if (kb0 >= kb1) continue;  // uniform over the workgroup
     // Block kb: positions kb*kKB + pr; rows past pmax load row pmax (masked below).  Each
     // thread carries kCh 16-byte chunks of K (and of V): block kb+1 is requested into registers
     // before block kb's MFMAs, so its memory latency overlaps them, and written to LDS after
@@ -894,44 +916,62 @@ __global__ void __launch_bounds__(kAttnWaves * 64) attention_mfma(const uint16_t
       if (kbase + 31 <= wave_first) block(std::false_type{});
       else block(std::true_type{});
     };
-    // blocks past the last one are requested too (clamped rows, never used), so that every path
-    // issues the same loads and the compiler's counted waits stay exact
-    load_k(0, 0);
-    load_k(1, 1);
-    for (int kb = 0; kb < nkb; kb += 2) {
-      __syncthreads();  // the previous block's reads are done
-      put_k(0);
-      __syncthreads();
-      load_k(0, kb + 2);
-      pass1(kb);
-      if (kb + 1 >= nkb) break;
-      __syncthreads();
-      put_k(1);
-      __syncthreads();
-      load_k(1, kb + 3);
-      pass1(kb + 1);
-    }
-    // row l16's (max, sum): over the 4 lanes of equal l16, then the row group's two waves (the
-    // even wave's pair first in every wave, so both waves hold the same M and 1/L)
-    {
-      float mx = m;
-      mx = fmaxf(mx, __shfl_xor(mx, 16));
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      float sm = m == -INFINITY ? 0.f : ls * exp_acc(m - mx);
-      sm += __shfl_xor(sm, 16);
-      sm += __shfl_xor(sm, 32);
-      if (lg == 0) {
-        s_ml[rg][kh][l16][0] = mx;
-        s_ml[rg][kh][l16][1] = sm;
-      }
-    }
-    __syncthreads();
     float gm, ginv;
-    {
+    if constexpr (MODE != kAttnPass2) {
+      // blocks past the last one are requested too (clamped rows, never used), so that every path
+      // issues the same loads and the compiler's counted waits stay exact
+      load_k(0, kb0);
+      load_k(1, kb0 + 1);
+      for (int kb = kb0; kb < kb1; kb += 2) {
+        __syncthreads();  // the previous block's reads are done
+        put_k(0);
+        __syncthreads();
+        load_k(0, kb + 2);
+        pass1(kb);
+        if (kb + 1 >= kb1) break;
+        __syncthreads();
+        put_k(1);
+        __syncthreads();
+        load_k(1, kb + 3);
+        pass1(kb + 1);
+      }
+      // row l16's (max, sum): over the 4 lanes of equal l16, then the row group's two waves (the
+      // even wave's pair first in every wave, so both waves hold the same M and 1/L)
+      {
+        float mx = m;
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        float sm = m == -INFINITY ? 0.f : ls * exp_acc(m - mx);
+        sm += __shfl_xor(sm, 16);
+        sm += __shfl_xor(sm, 32);
+        if (lg == 0) {
+          s_ml[rg][kh][l16][0] = mx;
+          s_ml[rg][kh][l16][1] = sm;
+        }
+      }
+      __syncthreads();
       const float m0 = s_ml[rg][0][l16][0], l0 = s_ml[rg][0][l16][1];
       const float m1 = s_ml[rg][1][l16][0], l1 = s_ml[rg][1][l16][1];
       gm = fmaxf(m0, m1);
       const float sm = (m0 == -INFINITY ? 0.f : l0 * exp_acc(m0 - gm)) + (m1 == -INFINITY ? 0.f : l1 * exp_acc(m1 - gm));
+      if constexpr (MODE == kAttnPass1) {
+        // the chunk's (max, sum) of row 16rg + l16 (-inf, 0 when every key of the chunk follows it)
+        if (kh == 0 && lg == 0) ml[attn_chunk_row(tiles[u], h, nch, chunk, 16 * rg + l16)] = make_float2(gm, sm);
+        continue;
+      }
+      ginv = __fdiv_rn(1.0f, sm);
+    } else {
+      // the row's global (max, sum) from its chunks' (chunk 0 holds key 0, so the sum is > 0), the
+      // sum in chunk order
+      const int nc = (nkb + ck - 1) / ck, row = 16 * rg + l16;
+      float mx = -INFINITY;
+      for (int q = 0; q < nc; q++) mx = fmaxf(mx, ml[attn_chunk_row(tiles[u], h, nch, q, row)].x);
+      float sm = 0.f;
+      for (int q = 0; q < nc; q++) {
+        const float2 e = ml[attn_chunk_row(tiles[u], h, nch, q, row)];
+        sm += e.x == -INFINITY ? 0.f : e.y * exp_acc(e.x - mx);
+      }
+      gm = mx;
       ginv = __fdiv_rn(1.0f, sm);
     }
     // ---- pass 2: probabilities (bf16, as HF rounds them) times V
@@ -970,11 +1010,11 @@ __global__ void __launch_bounds__(kAttnWaves * 64) attention_mfma(const uint16_t
         acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
             pa, *reinterpret_cast<const bf16x8*>(&Vt[16 * j + l16][32 * kh + 8 * lg]), acc[j], 0, 0, 0);
     };
-    load_k(0, 0);
-    load_v(0, 0);
-    load_k(1, 1);
-    load_v(1, 1);
-    for (int kb = 0; kb < nkb; kb += 2) {
+    load_k(0, kb0);
+    load_v(0, kb0);
+    load_k(1, kb0 + 1);
+    load_v(1, kb0 + 1);
+    for (int kb = kb0; kb < kb1; kb += 2) {
       __syncthreads();
       put_k(0);
       put_v(0);
@@ -982,7 +1022,7 @@ __global__ void __launch_bounds__(kAttnWaves * 64) attention_mfma(const uint16_t
       load_k(0, kb + 2);
       load_v(0, kb + 2);
       pass2(kb);
-      if (kb + 1 >= nkb) break;
+      if (kb + 1 >= kb1) break;
       __syncthreads();
       put_k(1);
       put_v(1);
@@ -1006,14 +1046,36 @@ __global__ void __launch_bounds__(kAttnWaves * 64) attention_mfma(const uint16_t
       for (int i = 0; i < 4; i++) {
         const int r = 16 * rg + 4 * lg + i;
         if (r < nrows) {
-          uint16_t* dst = out + (size_t)(t0 + r) * kQS + h * kD;
+          if constexpr (MODE == kAttnFull) {
+            uint16_t* dst = out + (size_t)(t0 + r) * kQS + h * kD;
 #pragma unroll
-          for (int j = 0; j < 8; j++)
-            dst[16 * j + l16] = (uint16_t)f32_to_bf16(acc[j][i] + red[rg][4 * lg + i][16 * j + l16]);
+            for (int j = 0; j < 8; j++)
+              dst[16 * j + l16] = (uint16_t)f32_to_bf16(acc[j][i] + red[rg][4 * lg + i][16 * j + l16]);
+          } else {  // this chunk's fp32 partial of the row
+            float* dst = part + attn_chunk_row(tiles[u], h, nch, chunk, r) * kD;
+#pragma unroll
+            for (int j = 0; j < 8; j++) dst[16 * j + l16] = acc[j][i] + red[rg][4 * lg + i][16 * j + l16];
+          }
         }
       }
     }
   }
+}
+
+// The split passes' output: each row of a tile attention_mfma covered (redo 0) is the sum of its
+// chunks' partials in chunk order, rounded to bf16.  One workgroup of kD threads per (token, query
+// head).
+__global__ void __launch_bounds__(kD) attention_mfma_merge(const Tok* __restrict__ tok, int T, int nch, int ck,
+                                                          const float* __restrict__ part,
+                                                          const int* __restrict__ redo, uint16_t* __restrict__ out) {
+  const int t = blockIdx.x, h = blockIdx.y, d = threadIdx.x;
+  const int tile = t / kQT, t0 = tile * kQT, nrows = min(kQT, T - t0);
+  if (redo[tile]) return;
+  const int pmax = tok[t0].pos + nrows - 1;
+  const int nc = ((pmax + kKB) / kKB + ck - 1) / ck;
+  float y = 0.f;
+  for (int q = 0; q < nc; q++) y += part[attn_chunk_row(tile, h, nch, q, t - t0) * kD + d];
+  out[(size_t)t * kQS + h * kD + d] = (uint16_t)f32_to_bf16(y);
 }
 
 // Few tokens: the context of each (token, KV head) is split over workgroups of
@@ -1828,14 +1890,53 @@ size_t part_floats(int T, int N, int K) { return (size_t)plan_gemm(T, N, K).kspl
 
 int split_chunks(int max_context) { return (max_context + kSplitChunk - 1) / kSplitChunk; }
 
-// The context-split attention (three launches) for few tokens over a long context; the row kernel
-// (one launch) for few tokens over a short one.  Qwen3-0.6B prefills, split against rows, same box:
-// from position 0, 1 token 1.31 / 1.21 ms and 31 tokens 1.45 / 1.35; from 96, 1.41 / 1.39; from
-// 192, 1.46 / 1.56; from 500, 1.45 / 2.14.
-bool split_attention(int T, int max_context) { return T < kSplitBelow && max_context > kSplitContext; }
+// The context-split attention (three launches, each token's context over workgroups of 64
+// positions) for few tokens over a longer context; the row kernel (one launch) for few tokens over
+// a short one.  Qwen3-0.6B prefills, split against rows, same box: from position 0, 1 token 1.31 /
+// 1.21 ms and 31 tokens 1.45 / 1.35; from 96, 1.41 / 1.39; from 192, 1.46 / 1.56; from 500, 1.45 /
+// 2.14.  Its work grows with tokens x context, attention_mfma's with the context alone (a 64-token
+// tile costs the same for 1 token as for 64), so a prompt of one sequence takes attention_mfma
+// from about 12288 tokens x positions (split against attention_mfma: 8 tokens after 1100 positions
+// 1.69 / 1.77 ms, 16 tokens 1.92 / 1.80; 4 tokens after 4000 2.59 / 2.48, 31 tokens 7.57 / 2.60;
+// 31 tokens after 7000 17.96 / 2.94).  A batched decode step (one token per sequence, whose tiles
+// hold several sequences and would fall back to the row kernel) keeps the split form.
+constexpr int kSplitWork = 12288;
+bool split_attention(int T, int max_context, bool one_per_seq) {
+  return T < kSplitBelow && max_context > kSplitContext && (one_per_seq || (long long)T * max_context < kSplitWork);
+}
+
+// attention_mfma pays off from about 320 tokens or 256 positions of context (below that the row
+// kernel's per-token reads are cheaper than its passes).  Measured 0.6B prefills, row kernel
+// against attention_mfma: 256 tokens 2.55 / 2.62 ms, 384 tokens 3.37 / 3.18, 512 tokens 4.23 /
+// 3.67, 768 tokens 5.85 / 4.45; with its keys in chunks (below), after 400 positions: 32 tokens
+// 2.01 / 1.78, 256 tokens 3.57 / 2.45; after 950: 64 tokens 3.06 / 1.99.
+bool mfma_attention(int T, int max_context, bool one_per_seq) {
+  return !split_attention(T, max_context, one_per_seq) && (T >= kMfmaAttnTokens || max_context >= kMfmaAttnContext);
+}
+
+// attention_mfma's keys in chunks of ck blocks (nch > 1: the split passes) when its tile pairs would
+// leave CUs idle and the context before the prompt is at least as long as the prompt: a prompt of
+// few tiles over a long context, e.g. a new turn appended to a long conversation, where each
+// pair's workgroup would walk the whole context alone (Qwen3-0.6B, pairs against chunks: 128
+// tokens after 7000 positions 13.9 / 3.3 ms, 32 tokens after 4000 4.82 / 2.61).  From position 0
+// the pairs already balance the causal work and chunks only add passes (1024 tokens 4.01 / 4.27).
+// At most kMaxAttnChunks tile chunks (their fp32 partials, 32 KB per tile chunk and head, stay
+// within 16 MB), at least two blocks each.
+constexpr int kMaxAttnChunks = 32;
+struct AttnSplit {
+  int nch, ck;
+};
+AttnSplit attn_mfma_split(int T, int max_context) {
+  const int nt = (T + kQT - 1) / kQT, nkb = (max_context + kKB - 1) / kKB;
+  if ((nt + 1) / 2 * kNQ >= kNumWG || max_context < 2 * T) return {1, nkb};
+  const int nch = std::min(kMaxAttnChunks / nt, nkb / 2);
+  if (nch < 2) return {1, nkb};
+  const int ck = (nkb + nch - 1) / nch;
+  return {(nkb + ck - 1) / ck, ck};
+}
 
 struct Layout {
-  size_t tok, erow, keys, x, n, q, att, m, qkv, apart, part, scores, ml, pv, redo, total;
+  size_t tok, erow, keys, x, n, q, att, m, qkv, apart, part, scores, ml, pv, redo, mml, mpart, total;
 };
 
 constexpr int kLmTiles(int V) { return V / 64; }
@@ -1873,13 +1974,20 @@ Layout layout(int T, int R, int max_context, bool one_per_seq = false) {
   pf = std::max(pf, part_floats(T, 2 * Dm::I, Dm::H));
   pf = std::max(pf, part_floats(T, Dm::H, Dm::I));
   take(l.part, pf * 4);
-  if (split_attention(T, max_context)) {
+  // the buffers of every attention form the forward may pick for these sizes (one token per
+  // sequence or not: the workspace size query does not say)
+  if (split_attention(T, max_context, true)) {
     const int nch = split_chunks(max_context);
     take(l.scores, (size_t)T * kNQ * nch * kSplitChunk * 4);
     take(l.ml, (size_t)T * kNQ * nch * 8);
     take(l.pv, (size_t)T * nch * kQS * 4);
-  } else {
-    take(l.redo, (size_t)((T + kQT - 1) / kQT) * 4);
+  }
+  take(l.redo, (size_t)((T + kQT - 1) / kQT) * 4);
+  const AttnSplit sp = attn_mfma_split(T, max_context);
+  if (mfma_attention(T, max_context, false) && sp.nch > 1) {  // attention_mfma's chunks: (max, sum), partials
+    const size_t rows = (size_t)((T + kQT - 1) / kQT) * kNQ * sp.nch * kQT;
+    take(l.mml, rows * sizeof(float2));
+    take(l.mpart, rows * kD * 4);
   }
   l.total = off;
   return l;
@@ -2020,13 +2128,10 @@ int forward(const Args& a, hipStream_t s) {
   uint16_t* MM = reinterpret_cast<uint16_t*>(a.ws + l.m);
   float* part = reinterpret_cast<float*>(a.ws + l.part);
   const float eps = 1e-6f;
-  const bool split = split_attention(T, a.max_context);
+  const bool split = split_attention(T, a.max_context, a.one_per_seq);
   const int nch = split ? split_chunks(a.max_context) : 0;
-  // attention_mfma pays off from about 320 tokens or 1024 positions of context (below that the
-  // row kernel's per-token reads are cheaper than its passes).  Measured 0.6B prefills, row
-  // kernel against attention_mfma: 256 tokens 2.55 / 2.62 ms, 384 tokens 3.37 / 3.18, 512 tokens
-  // 4.23 / 3.67, 768 tokens 5.85 / 4.45.
-  const bool mfma_attn = !split && (T >= kMfmaAttnTokens || a.max_context >= kMfmaAttnContext);
+  const bool mfma_attn = mfma_attention(T, a.max_context, a.one_per_seq);
+  const AttnSplit asp = attn_mfma_split(T, a.max_context);
   auto blocks = [](size_t n) { return dim3((unsigned)((n + 255) / 256)); };
   auto u16 = [](const void* p) { return static_cast<const uint16_t*>(p); };
   int ks = 1;
@@ -2055,8 +2160,20 @@ int forward(const Args& a, hipStream_t s) {
         // tiles of one sequence's consecutive tokens on MFMA; any other tile row by row
         int* redo = reinterpret_cast<int*>(a.ws + l.redo);
         const int ntiles = (T + kQT - 1) / kQT;
-        hipLaunchKernelGGL(attention_mfma, dim3((ntiles + 1) / 2, kNQ), dim3(kAttnWaves * 64), 0, s, Qb, tok, T, L,
-                           a.cache, a.attn_scale, ATT, redo);
+        if (asp.nch > 1) {
+          float2* aml = reinterpret_cast<float2*>(a.ws + l.mml);
+          float* apart = reinterpret_cast<float*>(a.ws + l.mpart);
+          const dim3 grid(ntiles * asp.nch, kNQ);
+          hipLaunchKernelGGL(attention_mfma<kAttnPass1>, grid, dim3(kAttnWaves * 64), 0, s, Qb, tok, T, L, a.cache,
+                             a.attn_scale, ATT, redo, asp.nch, asp.ck, aml, apart);
+          hipLaunchKernelGGL(attention_mfma<kAttnPass2>, grid, dim3(kAttnWaves * 64), 0, s, Qb, tok, T, L, a.cache,
+                             a.attn_scale, ATT, redo, asp.nch, asp.ck, aml, apart);
+          hipLaunchKernelGGL(attention_mfma_merge, dim3(T, kNQ), dim3(kD), 0, s, tok, T, asp.nch, asp.ck, apart, redo,
+                             ATT);
+        } else {
+          hipLaunchKernelGGL(attention_mfma<kAttnFull>, dim3((ntiles + 1) / 2, kNQ), dim3(kAttnWaves * 64), 0, s, Qb,
+                             tok, T, L, a.cache, a.attn_scale, ATT, redo, 1, 0, nullptr, nullptr);
+        }
         // the tiles attention_mfma left (redo) row by row: 256 x 8 workgroups loop over the tokens
         hipLaunchKernelGGL(attention_rows, dim3(std::min(T, 256), kNKV), dim3(256), 0, s, Qb, tok, T, L, a.cache,
                            a.attn_scale, ATT, redo);

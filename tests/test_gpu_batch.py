@@ -280,14 +280,17 @@ def test_prefill_all_matches_per_sequence_prefill(shape, weights_gpu):
         check_row(t, ("step", b), l2[b].cpu(), s1[b], l1[b], bar=LAYERS28)
 
 
-@pytest.mark.parametrize("n", [8, 40], ids=["8tok-split", "40tok-mfma"])
+@pytest.mark.parametrize("n", [4, 8, 40, 150],
+                         ids=["4tok-split", "8tok-mfma-chunks", "40tok-mfma-chunks", "150tok-mfma-chunks"])
 def test_long_context_prefill(shape, exact06, weights_gpu, n):
-    """Prefill after an injected N(0,1) cache of 2100 positions: 8 tokens take the split attention
-    (34 workgroups per head), 40 tokens the MFMA attention (more than 1024 positions of context)."""
+    """Prefill after an injected N(0,1) cache of 2100 positions: 4 tokens take the split attention
+    (34 workgroups per head and token); 8, 40 and 150 tokens (one, one and three 64-token tiles,
+    the last partial) the MFMA attention with its keys in chunks over the context (too few tiles
+    to fill the chip)."""
     from qwen_megakernel.weights import make_kv_prefill, make_prompt
 
     c0, layers = 2100, 2
-    max_seq = c0 + 64
+    max_seq = c0 + 192
     k, v = make_kv_prefill(shape, c0, seed=2)
     ids = make_prompt(n, shape.vocab, seed=7)
     dec = decoder(with_rope(weights_gpu, max_seq, "cuda"), num_layers=layers, max_seq_len=max_seq)

@@ -58,11 +58,12 @@ def test_decode_ignores_unwritten_rows(shape, weights_gpu, prompt, c0):
     _same(f"decode from context {c0}", *runs)
 
 
-@pytest.mark.parametrize("n", [100, 333], ids=["rows-100", "mfma-333"])
-def test_prefill_ignores_unwritten_rows(shape, weights_gpu, n):
-    """The batched forward from position 0 (100 tokens: the row attention; 333: the MFMA attention,
-    whose last 64-position tile is ragged), then a second prompt of 21 tokens at position n and two
-    decode steps, on a NaN-filled cache."""
+@pytest.mark.parametrize("first,n", [(0, 100), (0, 333), (400, 150)], ids=["rows-100", "mfma-333", "mfma-chunks-150"])
+def test_prefill_ignores_unwritten_rows(shape, weights_gpu, first, n):
+    """The batched forward of n tokens after `first` prefilled ones (100 from position 0: the row
+    attention; 333: the MFMA attention, whose last 64-position tile is ragged; 150 after 400: the
+    MFMA attention with its keys in chunks), then a second prompt of 21 tokens and two decode
+    steps, on a NaN-filled cache."""
     from qwen_megakernel.weights import make_prompt
 
     ids = make_prompt(n, shape.vocab, seed=31)
@@ -72,12 +73,14 @@ def test_prefill_ignores_unwritten_rows(shape, weights_gpu, n):
         dec = decoder(weights_gpu, num_layers=4)
         if poison:
             _poison(dec._k_cache, dec._v_cache)
+        if first:
+            dec.prefill(make_prompt(first, shape.vocab, seed=30))
         t0, l0 = dec.prefill(ids, return_logits=True)
         t1, l1 = dec.prefill(more, return_logits=True)
         t2, l2 = dec.step_logits(t1)
         t3, l3 = dec.step_logits(t2)
         runs.append(([t0, t1, t2, t3], torch.stack([l0, l1, l2, l3]).cpu()))
-    _same(f"prefill {n} + 21 + 2 steps", *runs)
+    _same(f"prefill {first} + {n} + 21 + 2 steps", *runs)
 
 
 @contextlib.contextmanager
