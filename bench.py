@@ -33,7 +33,8 @@ four and algorithmic GB/s per step (weights once + each sequence's KV).
 
 ``prefill``: the 128-token prompt through the batched forward, ms and tok/s;
 ``prefill_long``: a 2048-token prompt the same way (its attention on MFMA);
-``prefill_lens`` (only with ``--prefill-lens 4,32,...``): prompts of those lengths.
+``prefill_lens`` (only with ``--prefill-lens 4,32,...``): prompts of those lengths, from position 0 or
+``--prefill-start`` (a new turn appended to a conversation).
 ``context_1024``: the decode rate at exactly 1024 positions of context (a
 1023-token prompt prefilled, then 512 decode launches at position 1023).
 
@@ -346,32 +347,44 @@ def context_1024_rate(w, launches: int = 512):
     return {"context": 1024, "launches": launches, "us_per_step": round(us, 2), "tok_per_s": round(1e6 / us, 1)}
 
 
-def prefill_rate(w, prompt_len: int = PROMPT_LEN, iters: int = 10):
-    """Qwen3-0.6B prompt prefill through the batched forward: ms and tokens/s for `prompt_len` tokens."""
+def prefill_rate(w, prompt_len: int = PROMPT_LEN, iters: int = 10, start: int = 0):
+    """Qwen3-0.6B prompt prefill through the batched forward: ms and tokens/s for `prompt_len` tokens
+    at positions start.. (the cache rows before `start` are zero: the work does not depend on their
+    values)."""
     import torch
 
     from qwen_megakernel.model import Decoder
     from qwen_megakernel.shapes import QWEN3_0_6B as S
-    from qwen_megakernel.weights import make_prompt
+    from qwen_megakernel.weights import make_prompt, rope_tables
 
-    dec = Decoder(weights=w, verbose=False, max_seq_len=2048)
+    max_seq = max(2048, start + prompt_len)
+    if w["cos_table"].shape[0] < max_seq:
+        w = dict(w)
+        cos, sin = rope_tables(max_seq, S.head_dim, 1e6)
+        w["cos_table"], w["sin_table"] = cos.cuda(), sin.cuda()
+    dec = Decoder(weights=w, verbose=False, max_seq_len=max_seq)
     prompt = make_prompt(prompt_len, S.vocab, seed=1)
+    dec._position = start
     dec.prefill(prompt)
     stream = torch.cuda.current_stream()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     e0.record(stream)
     for _ in range(iters):
-        dec._position = 0
+        dec._position = start
         dec.prefill(prompt)
     e1.record(stream)
     torch.cuda.synchronize()
     t = e0.elapsed_time(e1) / 1e3 / iters
     del dec
     torch.cuda.empty_cache()
-    log(f"prefill {prompt_len} tokens: {t * 1e3:.3f} ms ({prompt_len / t:.0f} tok/s); one decode step per "
+    at = f" after {start} positions" if start else ""
+    log(f"prefill {prompt_len} tokens{at}: {t * 1e3:.3f} ms ({prompt_len / t:.0f} tok/s); one decode step per "
         f"token would take {prompt_len} launches")
-    return {"prompt_len": prompt_len, "ms": round(t * 1e3, 3), "tok_per_s": round(prompt_len / t, 1)}
+    out = {"prompt_len": prompt_len, "ms": round(t * 1e3, 3), "tok_per_s": round(prompt_len / t, 1)}
+    if start:
+        out["start"] = start
+    return out
 
 
 def sampling(dec, prompt, max_seq: int, steps: int):
@@ -427,6 +440,7 @@ def main():
     ap.add_argument("--no-sampling", action="store_true")
     ap.add_argument("--sample-steps", type=int, default=512)
     ap.add_argument("--prefill-lens", default="", help="comma-separated prompt lengths to time prefill at as well")
+    ap.add_argument("--prefill-start", type=int, default=0, help="position the --prefill-lens prompts start at")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (this path does not shard "
@@ -540,7 +554,7 @@ def main():
     result["prefill"] = prefill_rate(w)
     result["prefill_long"] = prefill_rate(w, 2048, iters=5)
     if args.prefill_lens:
-        result["prefill_lens"] = [prefill_rate(w, int(n)) for n in args.prefill_lens.split(",")]
+        result["prefill_lens"] = [prefill_rate(w, int(n), start=args.prefill_start) for n in args.prefill_lens.split(",")]
     if not args.no_long_context:
         result["long_context"] = long_context(w, args.long_steps, phase_trace=args.phase_trace)
     del w

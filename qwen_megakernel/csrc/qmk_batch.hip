@@ -42,6 +42,7 @@ constexpr int kAttnChunk = 2048;  // one-kernel attention: scores of this many p
 constexpr int kQT = 64, kKB = 64, kKPad = kD + 8, kVPad = kKB + 8;  // MFMA prefill attention tiles
 constexpr int kMfmaAttnTokens = 320;   // prompts of this many tokens run attention_mfma
 constexpr int kMfmaAttnContext = 256;  // so do fewer tokens over this many positions of context
+constexpr int kMaxAttnChunks = 32;    // attention_mfma over key chunks: tiles x chunks at most
 constexpr int kSplitChunk = 64;   // split attention: positions per workgroup
 constexpr int kSplitBelow = 32;   // fewer tokens than this use the split attention ...
 constexpr int kSplitContext = 128;  // ... over more than this many positions of context
@@ -962,13 +963,18 @@ __global__ void __launch_bounds__(kAttnWaves * 64) attention_mfma(const uint16_t
       ginv = __fdiv_rn(1.0f, sm);
     } else {
       // the row's global (max, sum) from its chunks' (chunk 0 holds key 0, so the sum is > 0), the
-      // sum in chunk order
+      // sum in chunk order.  Every chunk's pairs of the tile's rows go to LDS first (over the K/V
+      // buffers, unused until the barrier that opens pass 2's first block), in one round of loads.
       const int nc = (nkb + ck - 1) / ck, row = 16 * rg + l16;
+      float2* const s_cml = reinterpret_cast<float2*>(smem);  // [nc][kQT]
+      static_assert(kMaxAttnChunks * kQT * sizeof(float2) <= kKBytes + kVBytes, "the chunks' pairs fit in LDS");
+      for (int i = threadIdx.x; i < nc * kQT; i += NT) s_cml[i] = ml[attn_chunk_row(tiles[u], h, nch, i / kQT, i % kQT)];
+      __syncthreads();
       float mx = -INFINITY;
-      for (int q = 0; q < nc; q++) mx = fmaxf(mx, ml[attn_chunk_row(tiles[u], h, nch, q, row)].x);
+      for (int q = 0; q < nc; q++) mx = fmaxf(mx, s_cml[q * kQT + row].x);
       float sm = 0.f;
       for (int q = 0; q < nc; q++) {
-        const float2 e = ml[attn_chunk_row(tiles[u], h, nch, q, row)];
+        const float2 e = s_cml[q * kQT + row];
         sm += e.x == -INFINITY ? 0.f : e.y * exp_acc(e.x - mx);
       }
       gm = mx;
@@ -1073,8 +1079,16 @@ __global__ void __launch_bounds__(kD) attention_mfma_merge(const Tok* __restrict
   if (redo[tile]) return;
   const int pmax = tok[t0].pos + nrows - 1;
   const int nc = ((pmax + kKB) / kKB + ck - 1) / ck;
+  // eight chunks' loads in flight at a time, added in chunk order
   float y = 0.f;
-  for (int q = 0; q < nc; q++) y += part[attn_chunk_row(tile, h, nch, q, t - t0) * kD + d];
+  for (int q0 = 0; q0 < nc; q0 += 8) {
+    float v[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) v[j] = q0 + j < nc ? part[attn_chunk_row(tile, h, nch, q0 + j, t - t0) * kD + d] : 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; j++)
+      if (q0 + j < nc) y += v[j];
+  }
   out[(size_t)t * kQS + h * kD + d] = (uint16_t)f32_to_bf16(y);
 }
 
@@ -1896,11 +1910,12 @@ int split_chunks(int max_context) { return (max_context + kSplitChunk - 1) / kSp
 // 1.21 ms and 31 tokens 1.45 / 1.35; from 96, 1.41 / 1.39; from 192, 1.46 / 1.56; from 500, 1.45 /
 // 2.14.  Its work grows with tokens x context, attention_mfma's with the context alone (a 64-token
 // tile costs the same for 1 token as for 64), so a prompt of one sequence takes attention_mfma
-// from about 12288 tokens x positions (split against attention_mfma: 8 tokens after 1100 positions
-// 1.69 / 1.77 ms, 16 tokens 1.92 / 1.80; 4 tokens after 4000 2.59 / 2.48, 31 tokens 7.57 / 2.60;
-// 31 tokens after 7000 17.96 / 2.94).  A batched decode step (one token per sequence, whose tiles
-// hold several sequences and would fall back to the row kernel) keeps the split form.
-constexpr int kSplitWork = 12288;
+// from about 6144 tokens x positions (split against attention_mfma with its keys in chunks: 8
+// tokens after 600 positions 1.55 / 1.62 ms; 2 after 1500 1.61 / 1.64, 8 after 1500 1.83 / 1.68;
+// 1 after 4000 2.01 / 2.07, 2 after 4000 2.12 / 2.08; 1 after 7000 2.60 / 2.38; 31 after 7000
+// 17.96 / 2.42).  A batched decode step (one token per sequence, whose tiles hold several
+// sequences and would fall back to the row kernel) keeps the split form.
+constexpr int kSplitWork = 6144;
 bool split_attention(int T, int max_context, bool one_per_seq) {
   return T < kSplitBelow && max_context > kSplitContext && (one_per_seq || (long long)T * max_context < kSplitWork);
 }
@@ -1922,7 +1937,6 @@ bool mfma_attention(int T, int max_context, bool one_per_seq) {
 // the pairs already balance the causal work and chunks only add passes (1024 tokens 4.01 / 4.27).
 // At most kMaxAttnChunks tile chunks (their fp32 partials, 32 KB per tile chunk and head, stay
 // within 16 MB), at least two blocks each.
-constexpr int kMaxAttnChunks = 32;
 struct AttnSplit {
   int nch, ck;
 };
