@@ -302,6 +302,25 @@ def test_long_context_prefill(shape, exact06, weights_gpu, n):
     check_kv_rows(f"long-context prefill {n}", orc, dec._k_cache, dec._v_cache, c0, n)
 
 
+def test_prompt_after_long_context_28_layers(shape, exact06, weights_cpu, weights_gpu):
+    """A new turn: 100 tokens after a 1200-token prefill, 28 layers (the MFMA attention over key
+    chunks: two tiles, seven chunks of three 64-key blocks); every row against the exact oracle on
+    the kernel's cache (a token departure beyond one ulp only within the row's fp32 envelope), and
+    the K/V rows written."""
+    from qwen_megakernel.weights import make_prompt
+
+    c0, n = 1200, 100
+    dec = decoder(weights_gpu)
+    dec.prefill(make_prompt(c0, shape.vocab, seed=21))
+    ids = make_prompt(n, shape.vocab, seed=22)
+    toks, logits = _forward_rows(dec._forward, ids, c0, dec._k_cache, dec._v_cache)
+    orc = exact_oracle(exact06, shape, 2048)
+    ref = oracle_steps(orc, dec._k_cache, dec._v_cache, c0, ids)
+    envs = lazy_envelopes(weights_cpu, shape, 2048, dec._k_cache, dec._v_cache, c0, ids, ref)
+    print(check_rows(Tally(f"{n} rows after {c0}"), ref, toks, logits, bar=LAYERS28, envs=envs))
+    check_kv_rows(f"{n} rows after {c0}", orc, dec._k_cache, dec._v_cache, c0, n)
+
+
 def test_long_context_prefill_rows_two_sequences(shape, exact06, weights_gpu):
     """Two sequences of 20 tokens each after injected N(0,1) caches of 2100 and 2060 positions, in
     one forward with their tokens interleaved: no 64-token tile is one sequence, so every row takes
