@@ -741,12 +741,13 @@ __device__ __forceinline__ int attn_v_slot(int q) {
   return 32 * half + 8 * ((r & 15) >> 2) + 4 * (r >> 4) + (r & 3);
 }
 
-// Modes: kAttnFull runs both passes over a tile's whole context (pairs of tiles per workgroup, as
-// above).  For few tiles over a long context the keys are split into chunks of ck blocks, one
-// workgroup per (tile, chunk, query head): kAttnPass1 writes each row's (max, sum) of its chunk to
-// ml; kAttnPass2 takes every chunk's (max, sum) of its rows (in chunk order) for the global max M
-// and sum L, and writes its chunk's P@V partial (fp32) to part; attention_mfma_merge adds the
-// partials in chunk order.  Workgroups of chunks past a tile's last key do nothing.
+// Modes: kAttnFull (kernel attention_mfma) runs both passes over a tile's whole context (pairs of
+// tiles per workgroup, as above).  For few tiles over a long context the keys are split into chunks
+// of ck blocks, one workgroup per (tile, chunk, query head): kAttnPass1 (attention_mfma_pass1)
+// writes each row's (max, sum) of its chunk to ml; kAttnPass2 (attention_mfma_pass2) takes every
+// chunk's (max, sum) of its rows (in chunk order) for the global max M and sum L, and writes its
+// chunk's P@V partial (fp32) to part; attention_mfma_merge adds the partials in chunk order.
+// Workgroups of chunks past a tile's last key do nothing.
 enum AttnMode : int { kAttnFull = 0, kAttnPass1 = 1, kAttnPass2 = 2 };
 
 // Index of (tile, head, chunk)'s row block in the split passes' ml and part buffers
@@ -755,11 +756,10 @@ __device__ __forceinline__ size_t attn_chunk_row(int tile, int h, int nch, int c
 }
 
 template <int MODE>
-__global__ void __launch_bounds__(kAttnWaves * 64) attention_mfma(const uint16_t* __restrict__ Q,
-                                                                 const Tok* __restrict__ tok, int T, int L, Cache c,
-                                                                 float scale, uint16_t* __restrict__ out,
-                                                                 int* __restrict__ redo, int nch, int ck,
-                                                                 float2* __restrict__ ml, float* __restrict__ part) {
+__device__ __forceinline__ void attention_mfma_body(const uint16_t* __restrict__ Q, const Tok* __restrict__ tok, int T,
+                                                    int L, Cache c, float scale, uint16_t* __restrict__ out,
+                                                    int* __restrict__ redo, int nch, int ck, float2* __restrict__ ml,
+                                                    float* __restrict__ part) {
   constexpr int NT = kAttnWaves * 64;
   static_assert(kQT == 64 && kKB == 64 && kAttnWaves == 8, "4 row groups of 16 x 2 key halves of 32");
   // K block [kKB][kKPad] and transposed V [kD][kVPad]; after the passes the same bytes hold the
@@ -1067,6 +1067,24 @@ __global__ void __launch_bounds__(kAttnWaves * 64) attention_mfma(const uint16_t
     }
   }
 }
+
+#define QMK_ATTN_ARGS                                                                                      \
+  const uint16_t *__restrict__ Q, const Tok *__restrict__ tok, int T, int L, Cache c, float scale,                 \
+      uint16_t *__restrict__ out, int *__restrict__ redo, int nch, int ck, float2 *__restrict__ ml,                 \
+      float *__restrict__ part
+// The pairs, the first pass over key chunks and the second.  (Held to 128 registers, for two
+// workgroups of the second pass per CU, it spilled 18 and ran slower: 32 tokens after 7,000
+// positions 2.57-2.63 against 2.39-2.44 ms per prefill.)
+__global__ void __launch_bounds__(kAttnWaves * 64) attention_mfma(QMK_ATTN_ARGS) {
+  attention_mfma_body<kAttnFull>(Q, tok, T, L, c, scale, out, redo, nch, ck, ml, part);
+}
+__global__ void __launch_bounds__(kAttnWaves * 64) attention_mfma_pass1(QMK_ATTN_ARGS) {
+  attention_mfma_body<kAttnPass1>(Q, tok, T, L, c, scale, out, redo, nch, ck, ml, part);
+}
+__global__ void __launch_bounds__(kAttnWaves * 64) attention_mfma_pass2(QMK_ATTN_ARGS) {
+  attention_mfma_body<kAttnPass2>(Q, tok, T, L, c, scale, out, redo, nch, ck, ml, part);
+}
+#undef QMK_ATTN_ARGS
 
 // The split passes' output: each row of a tile attention_mfma covered (redo 0) is the sum of its
 // chunks' partials in chunk order, rounded to bf16.  One workgroup of kD threads per (token, query
@@ -2178,14 +2196,14 @@ int forward(const Args& a, hipStream_t s) {
           float2* aml = reinterpret_cast<float2*>(a.ws + l.mml);
           float* apart = reinterpret_cast<float*>(a.ws + l.mpart);
           const dim3 grid(ntiles * asp.nch, kNQ);
-          hipLaunchKernelGGL(attention_mfma<kAttnPass1>, grid, dim3(kAttnWaves * 64), 0, s, Qb, tok, T, L, a.cache,
+          hipLaunchKernelGGL(attention_mfma_pass1, grid, dim3(kAttnWaves * 64), 0, s, Qb, tok, T, L, a.cache,
                              a.attn_scale, ATT, redo, asp.nch, asp.ck, aml, apart);
-          hipLaunchKernelGGL(attention_mfma<kAttnPass2>, grid, dim3(kAttnWaves * 64), 0, s, Qb, tok, T, L, a.cache,
+          hipLaunchKernelGGL(attention_mfma_pass2, grid, dim3(kAttnWaves * 64), 0, s, Qb, tok, T, L, a.cache,
                              a.attn_scale, ATT, redo, asp.nch, asp.ck, aml, apart);
           hipLaunchKernelGGL(attention_mfma_merge, dim3(T, kNQ), dim3(kD), 0, s, tok, T, asp.nch, asp.ck, apart, redo,
                              ATT);
         } else {
-          hipLaunchKernelGGL(attention_mfma<kAttnFull>, dim3((ntiles + 1) / 2, kNQ), dim3(kAttnWaves * 64), 0, s, Qb,
+          hipLaunchKernelGGL(attention_mfma, dim3((ntiles + 1) / 2, kNQ), dim3(kAttnWaves * 64), 0, s, Qb,
                              tok, T, L, a.cache, a.attn_scale, ATT, redo, 1, 0, nullptr, nullptr);
         }
         // the tiles attention_mfma left (redo) row by row: 256 x 8 workgroups loop over the tokens
