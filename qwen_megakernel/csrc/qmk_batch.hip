@@ -42,7 +42,7 @@ constexpr int kAttnChunk = 2048;  // one-kernel attention: scores of this many p
 constexpr int kQT = 64, kKB = 64, kKPad = kD + 8, kVPad = kKB + 8;  // MFMA prefill attention tiles
 constexpr int kMfmaAttnTokens = 320;   // prompts of this many tokens run attention_mfma
 constexpr int kMfmaAttnContext = 256;  // so do fewer tokens over this many positions of context
-constexpr int kMaxAttnChunks = 32;    // attention_mfma over key chunks: tiles x chunks at most
+constexpr int kMaxAttnChunks = 16;    // attention_mfma over key chunks: tiles x chunks at most
 constexpr int kSplitChunk = 64;   // split attention: positions per workgroup
 constexpr int kSplitBelow = 32;   // fewer tokens than this use the split attention ...
 constexpr int kSplitContext = 128;  // ... over more than this many positions of context
@@ -1953,8 +1953,10 @@ bool mfma_attention(int T, int max_context, bool one_per_seq) {
 // pair's workgroup would walk the whole context alone (Qwen3-0.6B, pairs against chunks: 128
 // tokens after 7000 positions 13.9 / 3.3 ms, 32 tokens after 4000 4.82 / 2.61).  From position 0
 // the pairs already balance the causal work and chunks only add passes (1024 tokens 4.01 / 4.27).
-// At most kMaxAttnChunks tile chunks (their fp32 partials, 32 KB per tile chunk and head, stay
-// within 16 MB), at least two blocks each.
+// At most kMaxAttnChunks tile chunks, at least two blocks each: 256 workgroups, so the second pass
+// (one workgroup per CU) runs in one round (at most 32: 32 tokens after 7,000 positions 2.39-2.44
+// against 2.02-2.07 ms per prefill; at most 8: 2.34-2.38), and the fp32 partials (32 KB per tile
+// chunk and head) stay within 8 MB.
 struct AttnSplit {
   int nch, ck;
 };
