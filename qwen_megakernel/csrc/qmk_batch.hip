@@ -1948,11 +1948,13 @@ bool mfma_attention(int T, int max_context, bool one_per_seq) {
 }
 
 // attention_mfma's keys in chunks of ck blocks (nch > 1: the split passes) when its tile pairs would
-// leave CUs idle and the context before the prompt is at least as long as the prompt: a prompt of
-// few tiles over a long context, e.g. a new turn appended to a long conversation, where each
-// pair's workgroup would walk the whole context alone (Qwen3-0.6B, pairs against chunks: 128
-// tokens after 7000 positions 13.9 / 3.3 ms, 32 tokens after 4000 4.82 / 2.61).  From position 0
-// the pairs already balance the causal work and chunks only add passes (1024 tokens 4.01 / 4.27).
+// leave CUs idle and either the context before the prompt is at least as long as the prompt (a
+// prompt of few tiles over a long context, e.g. a new turn appended to a long conversation, where
+// each pair's workgroup would walk the whole context alone: Qwen3-0.6B, pairs against chunks, 128
+// tokens after 7000 positions 13.9 / 2.8 ms, 32 tokens after 4000 4.82 / 1.90) or the prompt has
+// at most 8 tiles (from position 0: 384 tokens 2.87-2.90 / 2.82-2.83, 512 tokens 3.32-3.36 /
+// 3.24; with more tiles from position 0 the pairs balance the causal work as well: 768 tokens
+// 3.70-3.74 / 3.75-3.76, 1024 tokens 3.97-4.00 / 3.99).
 // At most kMaxAttnChunks tile chunks, at least two blocks each: 256 workgroups, so the second pass
 // (one workgroup per CU) runs in one round (at most 32: 32 tokens after 7,000 positions 2.39-2.44
 // against 2.02-2.07 ms per prefill; at most 8: 2.34-2.38), and the fp32 partials (32 KB per tile
@@ -1962,7 +1964,7 @@ struct AttnSplit {
 };
 AttnSplit attn_mfma_split(int T, int max_context) {
   const int nt = (T + kQT - 1) / kQT, nkb = (max_context + kKB - 1) / kKB;
-  if ((nt + 1) / 2 * kNQ >= kNumWG || max_context < 2 * T) return {1, nkb};
+  if ((nt + 1) / 2 * kNQ >= kNumWG || (max_context < 2 * T && nt > 8)) return {1, nkb};
   const int nch = std::min(kMaxAttnChunks / nt, nkb / 2);
   if (nch < 2) return {1, nkb};
   const int ck = (nkb + nch - 1) / nch;
