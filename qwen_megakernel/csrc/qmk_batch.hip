@@ -1955,17 +1955,19 @@ bool mfma_attention(int T, int max_context, bool one_per_seq) {
 // at most 8 tiles (from position 0: 384 tokens 2.87-2.90 / 2.82-2.83, 512 tokens 3.32-3.36 /
 // 3.24; with more tiles from position 0 the pairs balance the causal work as well: 768 tokens
 // 3.70-3.74 / 3.75-3.76, 1024 tokens 3.97-4.00 / 3.99).
-// At most kMaxAttnChunks tile chunks, at least two blocks each: 256 workgroups, so the second pass
-// (one workgroup per CU) runs in one round (at most 32: 32 tokens after 7,000 positions 2.39-2.44
-// against 2.02-2.07 ms per prefill; at most 8: 2.34-2.38), and the fp32 partials (32 KB per tile
-// chunk and head) stay within 8 MB.
+// Up to 8 tiles, at most kMaxAttnChunks tile chunks, at least two blocks each: 256 workgroups, so
+// the second pass (one workgroup per CU) runs in one round (at most 32: 32 tokens after 7,000
+// positions 2.39-2.44 against 2.02-2.07 ms per prefill; at most 8: 2.34-2.38).  More tiles take up
+// to 4 x kMaxAttnChunks tile chunks, two or more rounds, rather than one chunk each (1024 tokens
+// after 4000 positions 10.76 -> 7.56 ms, after 6000 14.05 -> 9.17).  The fp32 partials (32 KB per
+// tile chunk and head) stay within 32 MB.
 struct AttnSplit {
   int nch, ck;
 };
 AttnSplit attn_mfma_split(int T, int max_context) {
   const int nt = (T + kQT - 1) / kQT, nkb = (max_context + kKB - 1) / kKB;
   if ((nt + 1) / 2 * kNQ >= kNumWG || (max_context < 2 * T && nt > 8)) return {1, nkb};
-  const int nch = std::min(kMaxAttnChunks / nt, nkb / 2);
+  const int nch = std::min((nt <= 8 ? kMaxAttnChunks : 4 * kMaxAttnChunks) / nt, nkb / 2);
   if (nch < 2) return {1, nkb};
   const int ck = (nkb + nch - 1) / nch;
   return {(nkb + ck - 1) / ck, ck};

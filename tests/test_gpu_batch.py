@@ -321,6 +321,28 @@ def test_prompt_after_long_context_28_layers(shape, exact06, weights_cpu, weight
     check_kv_rows(f"{n} rows after {c0}", orc, dec._k_cache, dec._v_cache, c0, n)
 
 
+def test_long_prompt_after_long_context(shape, exact06, weights_gpu):
+    """600 tokens (ten 64-token tiles, the last partial) after a 1300-token prefill, 4 layers: the
+    MFMA attention over six key chunks per tile (more than 8 tiles take up to 64 tile chunks);
+    every 50th row and the last against the exact oracle at the literal bar, and the K/V rows."""
+    from qwen_megakernel.weights import make_prompt
+
+    layers, c0, n = 4, 1300, 600
+    dec = decoder(weights_gpu, num_layers=layers)
+    dec.prefill(make_prompt(c0, shape.vocab, seed=23))
+    ids = make_prompt(n, shape.vocab, seed=24)
+    rows = list(range(0, n, 50)) + [n - 1]
+    out = torch.empty(len(rows), dtype=torch.int32, device="cuda")
+    logits = torch.empty(len(rows), V, dtype=torch.float32, device="cuda")
+    dec._forward(_i32(ids), torch.zeros(n, dtype=torch.int32, device="cuda"),
+                 torch.arange(c0, c0 + n, dtype=torch.int32, device="cuda"), _i32(rows), out, logits, dec._k_cache,
+                 dec._v_cache, c0 + n)
+    orc = exact_oracle(exact06, shape, 2048, num_layers=layers)
+    ref = oracle_steps(orc, dec._k_cache, dec._v_cache, c0, ids, emit=rows)
+    print(check_rows(Tally(f"{n} rows after {c0}"), ref, out.cpu().tolist(), logits.cpu(), bar=LITERAL))
+    check_kv_rows(f"{n} rows after {c0}", orc, dec._k_cache, dec._v_cache, c0, n)
+
+
 def test_long_context_prefill_rows_two_sequences(shape, exact06, weights_gpu):
     """Two sequences of 20 tokens each after injected N(0,1) caches of 2100 and 2060 positions, in
     one forward with their tokens interleaved: no 64-token tile is one sequence, so every row takes
