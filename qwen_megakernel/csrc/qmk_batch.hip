@@ -1379,6 +1379,82 @@ __global__ void __launch_bounds__(256) keys_reduce(const unsigned long long* __r
   }
 }
 
+// LM head for at most 4 emitted rows with each vocabulary row read whole: one wave instruction
+// loads 1 KB of one row (lm_head_stream's MFMA operands take 64 bytes of each of 16 rows per
+// instruction, which streams the head at about 5.3 TB/s against about 7 for whole rows).  The same
+// persistent grid: wave gw takes vocabulary rows gw, gw + 2048, ..., four rows of weights in
+// flight; each lane holds the emitted rows' matching 16-byte chunks in registers and adds its share
+// of every dot product with v_dot2; wave_sum8 then finishes eight (vocabulary row, emitted row)
+// sums at once, and the lanes that receive them round the logits and keep the best keys.  Keys
+// per (emitted row, wave) as lm_head_stream's, for keys_reduce.
+template <int R, int K>
+__global__ void __launch_bounds__(kLmWaves * 64) lm_head_rows(const uint16_t* __restrict__ X,
+                                                              const int* __restrict__ rows, int nrow,
+                                                              const uint16_t* __restrict__ W, int V,
+                                                              unsigned long long* __restrict__ keys_part,
+                                                              float* __restrict__ logits) {
+  static_assert(R >= 1 && R <= 4 && K % 512 == 0, "up to four rows, whole 512-element segments");
+  constexpr int NS = K / 512;        // 16-byte chunks per lane of one vocabulary row
+  constexpr int G = R == 3 ? 2 : 8 / R;  // vocabulary rows per eight-sum reduction
+  constexpr int D = 4;               // vocabulary rows in flight (eight: 52.0 against 49.6 us, one 1024-wide row)
+  const int lane = threadIdx.x & 63;
+  const int nw = gridDim.x * kLmWaves, gw = blockIdx.x * kLmWaves + (threadIdx.x >> 6);
+  const int mine = gw < V ? (V - gw + nw - 1) / nw : 0;  // this wave's vocabulary rows
+  // the emitted rows' chunks (row r: elements 512 s + 8 lane .. +7 of segment s); rows past nrow
+  // repeat the last one and are never written
+  u32x4 x[R][NS];
+#pragma unroll
+  for (int r = 0; r < R; r++) {
+    const uint16_t* xr = X + (size_t)max(rows[min(r, nrow - 1)], 0) * K;
+#pragma unroll
+    for (int sg = 0; sg < NS; sg++) x[r][sg] = ld16(xr + 512 * sg + 8 * lane);
+  }
+  auto wrow = [&](int i) { return W + (size_t)(gw + nw * min(i, mine - 1)) * K + 8 * lane; };
+  u32x4 buf[D][NS];
+#pragma unroll
+  for (int u = 0; u < D; u++)
+#pragma unroll
+    for (int sg = 0; sg < NS; sg++) buf[u][sg] = ld_stream(wrow(u) + 512 * sg);
+  unsigned long long best = 0;  // lanes 8k: the best key of emitted row k % R
+  float v[8];
+#pragma unroll
+  for (int k = 0; k < 8; k++) v[k] = 0.f;
+  // rows past `mine` read the wave's last row again (every path issues the same loads) and are
+  // left out of the keys
+  for (int i0 = 0; i0 < mine; i0 += 8) {
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+      const int i = i0 + u, g = u % G;
+#pragma unroll
+      for (int r = 0; r < R; r++) {
+        float acc = 0.f;
+#pragma unroll
+        for (int sg = 0; sg < NS; sg++) acc = dot8(buf[u % D][sg], x[r][sg], acc);
+        v[g * R + r] = acc;
+      }
+#pragma unroll
+      for (int sg = 0; sg < NS; sg++) buf[u % D][sg] = ld_stream(wrow(i + D) + 512 * sg);
+      if (g == G - 1) {
+        const float sum = wave_sum8(v, lane);  // lanes 8k..8k+7: slot k = (row g', emitted row r)
+        const int k = lane >> 3, gk = k / R, rk = k % R;
+        const int n = gw + nw * (i - (G - 1) + gk);
+        if ((lane & 7) == 0 && k < G * R && i - (G - 1) + gk < mine && rk < nrow) {
+          const uint32_t hb = f32_to_bf16(sum);
+          if (logits) logits[(size_t)rk * V + n] = bf16_to_f32(hb);
+          best = key_max(best, ((unsigned long long)orderable16(hb) << 32) | (unsigned long long)(0xffffffffu - (uint32_t)n));
+        }
+      }
+    }
+  }
+  // each emitted row's best over its lanes (8k with k % R = r)
+#pragma unroll
+  for (int r = 0; r < R; r++) {
+    unsigned long long b = ((lane & 7) == 0 && (lane >> 3) % R == r && (lane >> 3) < G * R) ? best : 0ull;
+    b = wave_max_u64(b);
+    if (lane == 0 && r < nrow) keys_part[(size_t)r * nw + gw] = b;
+  }
+}
+
 // ---------------------------------------------------------------- decode step, few sequences
 //
 // One token per sequence, at most 16 sequences (one MFMA row tile), contexts
@@ -2051,6 +2127,17 @@ template <class M>
 void launch_lm_head(const uint16_t* N, const int* erow, int R, const uint16_t* W, unsigned long long* keys,
                     float* logits, const Tok* tok, int* out, hipStream_t s) {
   using Dm = Dims<M>;
+  if (R <= 4) {
+    const dim3 grid(kLmBlocks), block(kLmWaves * 64);
+    switch (R) {
+      case 1: hipLaunchKernelGGL((lm_head_rows<1, Dm::H>), grid, block, 0, s, N, erow, R, W, Dm::V, keys, logits); break;
+      case 2: hipLaunchKernelGGL((lm_head_rows<2, Dm::H>), grid, block, 0, s, N, erow, R, W, Dm::V, keys, logits); break;
+      case 3: hipLaunchKernelGGL((lm_head_rows<3, Dm::H>), grid, block, 0, s, N, erow, R, W, Dm::V, keys, logits); break;
+      default: hipLaunchKernelGGL((lm_head_rows<4, Dm::H>), grid, block, 0, s, N, erow, R, W, Dm::V, keys, logits); break;
+    }
+    hipLaunchKernelGGL(keys_reduce, dim3(R), dim3(256), 0, s, keys, kLmBlocks * kLmWaves, erow, tok, out);
+    return;
+  }
   if (R <= 16) {
     const size_t lds = (size_t)R * Dm::H * 2;
     hipLaunchKernelGGL(lm_head_stream, dim3(kLmBlocks), dim3(kLmWaves * 64), lds, s, N, erow, R, W, Dm::H, Dm::V,
