@@ -1948,12 +1948,14 @@ int tiled_splits(int T, int N, int K) {
 }
 
 // 64-column tiles, for problems whose 128-column plan leaves CUs idle (narrow N at a few hundred
-// rows or fewer): K split (at most 16 ways, >= 2 steps of 64 each) until 256 workgroups run,
-// while the fp32 partials (ksplit * T * N * 4 bytes) stay within twice the weight bytes (N * K * 2).
+// rows or fewer): K split (at most 16 ways, >= 2 steps of 64 each) until 256 workgroups run (512
+// for at most 16 rows, whose partials are small: 4-token prefill 1.245 -> 1.20 ms, 16 tokens 1.266
+// -> 1.245; at 64 tokens 512 was slower, 1.535 -> 1.585), while the fp32 partials
+// (ksplit * T * N * 4 bytes) stay within twice the weight bytes (N * K * 2).
 int narrow_splits(int T, int N, int K) {
-  const long long tiles = (long long)((T + kTM - 1) / kTM) * (N / 64);
+  const long long tiles = (long long)((T + kTM - 1) / kTM) * (N / 64), target = T <= 16 ? 512 : 256;
   int ks = 1;
-  while (tiles * ks < 256 && ks * 2 <= kMaxSplit && K % (ks * 2 * kTK) == 0 && K / (ks * 2) >= 2 * kTK &&
+  while (tiles * ks < target && ks * 2 <= kMaxSplit && K % (ks * 2 * kTK) == 0 && K / (ks * 2) >= 2 * kTK &&
          (long long)ks * 2 * T * 4 <= 2LL * K * 2)
     ks *= 2;
   return ks;
