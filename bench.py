@@ -33,6 +33,8 @@ four and algorithmic GB/s per step (weights once + each sequence's KV).
 
 ``prefill``: the 128-token prompt through the batched forward, ms and tok/s;
 ``prefill_long``: a 2048-token prompt the same way (its attention on MFMA);
+``prefill_after_context``: the 128-token prompt appended after 4000 positions (a new turn of a
+conversation: the MFMA attention over key chunks);
 ``prefill_lens`` (only with ``--prefill-lens 4,32,...``): prompts of those lengths, from position 0 or
 ``--prefill-start`` (a new turn appended to a conversation).
 ``context_1024``: the decode rate at exactly 1024 positions of context (a
@@ -553,6 +555,7 @@ def main():
     result["context_1024"] = context_1024_rate(w)
     result["prefill"] = prefill_rate(w)
     result["prefill_long"] = prefill_rate(w, 2048, iters=5)
+    result["prefill_after_context"] = prefill_rate(w, PROMPT_LEN, start=4000)
     if args.prefill_lens:
         result["prefill_lens"] = [prefill_rate(w, int(n), start=args.prefill_start) for n in args.prefill_lens.split(",")]
     if not args.no_long_context:
