@@ -343,6 +343,37 @@ def test_long_prompt_after_long_context(shape, exact06, weights_gpu):
     check_kv_rows(f"{n} rows after {c0}", orc, dec._k_cache, dec._v_cache, c0, n)
 
 
+@pytest.mark.parametrize(
+    "n,start",
+    [(31, 190), (32, 100), (33, 300), (320, 0), (700, 0), (64, 2000), (1, 3000), (3, 3000)],
+    ids=["split-31@190", "rows-32@100", "mfma-chunks-33@300", "mfma-chunks-320@0", "mfma-pairs-700@0",
+         "mfma-chunks-64@2000", "split-1@3000", "mfma-chunks-3@3000"])
+def test_attention_form_matrix(shape, exact06, weights_gpu, n, start):
+    """One prompt of n tokens after `start` prefilled positions, 2 layers, for each attention form
+    the forward picks (the row kernel, the per-token context split, the MFMA attention in tile pairs
+    or over key chunks) around the thresholds between them: the first, middle and last rows and
+    every 100th against the exact oracle at the literal bar, and the K/V rows."""
+    from qwen_megakernel.weights import make_prompt
+
+    layers = 2
+    max_seq = max(2048, start + n)
+    w = with_rope(weights_gpu, max_seq, "cuda") if max_seq > 2048 else weights_gpu
+    dec = decoder(w, num_layers=layers, max_seq_len=max_seq)
+    if start:
+        dec.prefill(make_prompt(start, shape.vocab, seed=25))
+    ids = make_prompt(n, shape.vocab, seed=26)
+    rows = sorted(set([0, n // 2, n - 1] + list(range(0, n, 100))))
+    out = torch.empty(len(rows), dtype=torch.int32, device="cuda")
+    logits = torch.empty(len(rows), V, dtype=torch.float32, device="cuda")
+    dec._forward(_i32(ids), torch.zeros(n, dtype=torch.int32, device="cuda"),
+                 torch.arange(start, start + n, dtype=torch.int32, device="cuda"), _i32(rows), out, logits,
+                 dec._k_cache, dec._v_cache, start + n)
+    orc = exact_oracle(exact06, shape, max_seq, num_layers=layers)
+    ref = oracle_steps(orc, dec._k_cache, dec._v_cache, start, ids, emit=rows)
+    print(check_rows(Tally(f"{n} tokens at {start}"), ref, out.cpu().tolist(), logits.cpu(), bar=LITERAL))
+    check_kv_rows(f"{n} tokens at {start}", orc, dec._k_cache, dec._v_cache, start, n)
+
+
 def test_long_context_prefill_rows_two_sequences(shape, exact06, weights_gpu):
     """Two sequences of 20 tokens each after injected N(0,1) caches of 2100 and 2060 positions, in
     one forward with their tokens interleaved: no 64-token tile is one sequence, so every row takes
