@@ -1971,14 +1971,24 @@ Gemm plan_gemm(int T, int N, int K) {
 }
 
 // The q/k/v and gate/up GEMMs with their finishing work in the epilogue (kEpiQkv, kEpiGateUp)
-// when the plan can leave K unsplit: 128-column tiles filling at least one workgroup per CU.
-// Then no fp32 sums go to memory and no finishing kernel runs; *ks_out = 0 says so.  Otherwise
-// the sums go to part and *ks_out is the split count for the finishing kernel.
+// when the plan can leave K unsplit: at least kFuseMinWG 128-column tiles (q/k/v: that many per
+// 1024 of K).  Then no fp32 sums go to memory and no finishing kernel runs; *ks_out = 0 says so.
+// Otherwise the sums go to part and *ks_out is the split count for the finishing kernel.  With
+// half the CUs given a tile, the unsplit GEMM plus its epilogue still beats the split one plus the
+// finishing kernel (prefill ms, against a bound of one tile per CU: 0.6B 384 tokens 2.84-2.90 ->
+// 2.67-2.74, 512 3.25-3.34 -> 3.01-3.10, 640 3.80-3.88 -> 3.30-3.36, 896 4.08-4.19 -> 3.79-3.88;
+// 1.7B 256 tokens 3.47-3.57 -> 3.31-3.38, gate/up on 192 tiles); with a quarter it loses (0.6B
+// 256 tokens 2.39-2.45 -> 2.62-2.65, q/k/v on 64 tiles and gate/up on 96), and so does the 1.7B
+// q/k/v, whose K of 2048 doubles each tile's work, on 128 and 160 tiles (512 tokens 4.06-4.15
+// -> 4.38-4.49, 640 5.10-5.20 -> 5.27-5.37).
+constexpr int kFuseMinWG = 128;
+
 void launch_gemm(const uint16_t* X, int T, int K, const Seg& seg, int N, float* part, hipStream_t s, int* ks_out,
                  int epi = kEpiPart, const QkvOut* qo = nullptr, const GateUpOut* go = nullptr) {
   const QkvOut q0 = qo ? *qo : QkvOut{};
   const GateUpOut g0 = go ? *go : GateUpOut{};
-  if (epi != kEpiPart && (long long)((T + kTM - 1) / kTM) * (N / 128) >= kNumWG) {
+  const long long fuse_min = epi == kEpiQkv ? (long long)kFuseMinWG * std::max(1, K / 1024) : kFuseMinWG;
+  if (epi != kEpiPart && (long long)((T + kTM - 1) / kTM) * (N / 128) >= fuse_min) {
     const dim3 grid(N / 128, (T + kTM - 1) / kTM, 1);
     if (epi == kEpiQkv)
       hipLaunchKernelGGL((gemm_tiled<128, kEpiQkv>), grid, dim3(256), 0, s, X, T, K, seg, N, 1, part, q0, g0);
