@@ -699,14 +699,6 @@ __global__ void __launch_bounds__(256) attention_rows(const uint16_t* __restrict
   __shared__ float red[2][4];
   __shared__ float pv[4][2][kD];
   const int g = blockIdx.y, t16 = threadIdx.x & 15;
-  if (redo) {
-    // thread i reads the flag of the workgroup's i-th token, all in one round of loads (one
-    // after another they cost a memory round trip per token: 4.7 us per launch at 640 tokens);
-    // a workgroup none of whose tokens attention_mfma left exits here
-    const long long t = blockIdx.x + (long long)gridDim.x * threadIdx.x;
-    const bool beyond = threadIdx.x == blockDim.x - 1 && t + gridDim.x < T;  // more tokens than threads
-    if (!__syncthreads_or(beyond || (t < T && redo[t / kQT] != 0))) return;
-  }
   for (int t = blockIdx.x; t < T; t += gridDim.x) {
     if (redo && redo[t / kQT] == 0) continue;  // attention_mfma covered this token's tile
     __syncthreads();  // the previous token's reads of the shared arrays are done
